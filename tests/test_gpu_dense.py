@@ -1,0 +1,145 @@
+"""Dense forward on the GPU against the oracle.
+
+Parity reference: the oracle quantizes W with the same rules, dequantizes to
+f32 and runs the reference Dense contract (f64 serial accumulation, bias in
+f64, activation; src/cuda/kernels.cu:130-161). Tolerances, stated per test:
+  * contract: relative L2 error <= 1e-3;
+  * GEMV path (fp32 FMA of exactly-decoded codes): <= 1e-5, because the only
+    difference from the oracle is fp32 accumulation order;
+  * integer-exact cases: bit-exact (every partial sum is an exact f32).
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+TOL_CONTRACT = 1e-3
+TOL_GEMV = 1e-5
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-300))
+
+
+def oracle_dense(oracle, dt, scheme, W, x, act=-1, bias=None):
+    rows, cols = W.shape
+    native, rs, blk = oracle.quantize(dt, scheme, rows, cols, W)
+    Wd = oracle.dequant(dt, scheme, rows, cols, native, rs, blk)
+    return oracle.dense(Wd, x, act, bias)
+
+
+def run(gpu, dt, scheme, W, x, act=-1, bias=None):
+    s = gpu.DenseSession(x.shape[0], W.shape[1], W.shape[0], act, dt, scheme, W, bias)
+    pre, post = s.execute(x)
+    s.close()
+    return pre, post
+
+
+def test_release_smoke_known_answer(gpu):
+    W = np.eye(2, dtype=np.float32).ravel()
+    x = np.array([0.5, -0.25], np.float32)
+    pre, post = gpu.dense_forward(1, 2, 2, -1, 4, 0, W, x)
+    assert pre.tolist() == [[0.5, -0.25]] and post.tolist() == [[0.5, -0.25]]
+
+
+@pytest.mark.parametrize("dt,values", [
+    (4, [-8, -6, -3, -1, 0, 1, 2, 5, 7, 8]),
+    (5, [-8, -4, -3, -1.5, 0, 1, 2, 3, 6, 8]),
+    (16, [-6, -4, -3, -1.5, -0.5, 0, 0.5, 1, 2, 6]),
+])
+def test_integer_exact_bit_for_bit(gpu, oracle, dt, values):
+    rng = np.random.default_rng(dt)
+    for rows, cols, batch in [(129, 1000, 1), (64, 4096, 1), (5, 77, 3)]:
+        W = rng.choice(np.array(values, np.float32), (rows, cols))
+        x = rng.integers(-4, 5, (batch, cols)).astype(np.float32)
+        pre, post = run(gpu, dt, 0, W, x)
+        o_pre, _ = oracle_dense(oracle, dt, 0, W, x)
+        assert np.array_equal(pre, o_pre), (rows, cols, batch)
+        assert np.array_equal(post, o_pre)
+
+
+@pytest.mark.parametrize("dt", [4, 5, 16])
+@pytest.mark.parametrize("scheme", [0, 1, 2, 3])
+@pytest.mark.parametrize("rows,cols,batch", [(33, 70, 1), (300, 1024, 2), (7, 33, 3), (1, 1, 1)])
+def test_dense_matches_oracle(gpu, oracle, dt, scheme, rows, cols, batch):
+    rng = np.random.default_rng(rows + cols + batch + dt + scheme)
+    W = (rng.standard_normal((rows, cols)) / np.sqrt(cols)).astype(np.float32)
+    if scheme == 0:
+        W *= 8.0  # keep unscaled codes mostly in the normal range
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    pre, post = run(gpu, dt, scheme, W, x)
+    o_pre, o_post = oracle_dense(oracle, dt, scheme, W, x)
+    e = rel_l2(pre, o_pre)
+    assert e <= TOL_GEMV and e <= TOL_CONTRACT, e
+    assert np.array_equal(pre, post)
+
+
+@pytest.mark.parametrize("act", [-1, 0, 1, 2, 3, 4, 5, 6])
+def test_bias_and_activation_epilogue(gpu, oracle, act):
+    rng = np.random.default_rng(40 + act)
+    rows, cols = 45, 96
+    W = (rng.standard_normal((rows, cols)) / 10).astype(np.float32)
+    x = rng.standard_normal((2, cols)).astype(np.float32)
+    bias = rng.standard_normal(30)  # shorter than out: rows >= 30 get no bias
+    pre, post = run(gpu, 4, 2, W, x, act, bias)
+    o_pre, o_post = oracle_dense(oracle, 4, 2, W, x, act, bias)
+    assert rel_l2(pre, o_pre) <= TOL_GEMV
+    assert rel_l2(post, o_post) <= TOL_GEMV
+
+
+def test_c1_dense_512_e4m3_per_tensor(gpu, oracle):
+    """Single Dense 512->512, E4M3 + one fp32 per-tensor scale, batch 1."""
+    import pywelvet as pw
+    W = pw.normal(pw.seed_for(1), 512 * 512, 1 / np.sqrt(512)).reshape(512, 512)
+    x = pw.normal(pw.seed_for(1) + 500, 512).reshape(1, 512)
+    pre, _ = run(gpu, 4, 1, W, x)
+    o_pre, _ = oracle_dense(oracle, 4, 1, W, x)
+    assert rel_l2(pre, o_pre) <= TOL_GEMV
+
+
+def test_c2_gemv_4096_e4m3_per_row(gpu, oracle):
+    """Dense GEMV 4096->4096, E4M3 + per-row fp32 scales, batch 1."""
+    import pywelvet as pw
+    W = pw.normal(pw.seed_for(2), 4096 * 4096, 1 / 64.0).reshape(4096, 4096)
+    x = pw.normal(pw.seed_for(2) + 500, 4096).reshape(1, 4096)
+    pre, _ = run(gpu, 4, 2, W, x)
+    o_pre, _ = oracle_dense(oracle, 4, 2, W, x)
+    e = rel_l2(pre, o_pre)
+    assert e <= TOL_GEMV, e
+    # the quantized layer itself against the unquantized fp32 layer (what the
+    # scale scheme costs): E4M3 with per-row scales keeps ~3-4% error
+    full, _ = oracle.dense(W, x)
+    assert rel_l2(pre, full) < 0.05
+
+
+def test_device_resident_execute_matches_host(gpu):
+    import pywelvet as pw
+    hip = pw.Hip()
+    rng = np.random.default_rng(9)
+    W = (rng.standard_normal((256, 512)) / 20).astype(np.float32)
+    x = rng.standard_normal((2, 512)).astype(np.float32)
+    s = pw.DenseSession(2, 512, 256, 1, 16, 3, W, rng.standard_normal(256))
+    pre_h, post_h = s.execute(x)
+    dx = hip.upload(x)
+    dp = hip.malloc(2 * 256 * 4)
+    dq = hip.malloc(2 * 256 * 4)
+    s.execute_device(dx, dp, dq)
+    hip.sync()
+    assert np.array_equal(hip.download(dp, (2, 256)), pre_h)
+    assert np.array_equal(hip.download(dq, (2, 256)), post_h)
+    for p in (dx, dp, dq):
+        hip.free(p)
+    s.close()
+
+
+def test_unsupported_dtype_and_scheme(gpu):
+    import pywelvet as pw
+    W = np.ones((4, 4), np.float32)
+    with pytest.raises(pw.WelvetError) as e:
+        pw.DenseSession(1, 4, 4, -1, 1, 0, W)  # Float32 storage: not this path
+    assert e.value.code == 2
+    with pytest.raises(pw.WelvetError) as e:
+        pw.DenseSession(1, 4, 4, -1, 4, 7, W)
+    assert e.value.code == 1

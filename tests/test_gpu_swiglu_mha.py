@@ -1,0 +1,104 @@
+"""SwiGLU and MHA layers on the GPU against the oracle chain.
+
+SwiGLU (swiglu.cpp:87-136, kernels.cu:296-304): pre = h = SiLU(Gate x) * Up x
+with the reference's f32/f64 rounding; post = Down h.
+MHA (mha.cpp:123-183, kernels.cu:470-631): Q/K/V projections, attention core
+with the reference's global positions and KV ring, O projection.
+Tolerance: relative L2 <= 1e-5 where the GPU keeps fp32 and the oracle f64
+(GEMV path); the attention core uses fp32 exp/sin/cos against f64 libm, so
+<= 1e-4 there. The layer contract bound is 1e-3.
+"""
+import numpy as np
+import pytest
+
+from test_gpu_dense import rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+def oracle_dequant(oracle, dt, scheme, W):
+    rows, cols = W.shape
+    native, rs, blk = oracle.quantize(dt, scheme, rows, cols, W)
+    return oracle.dequant(dt, scheme, rows, cols, native, rs, blk)
+
+
+def oracle_swiglu(oracle, dt, scheme, G, U, D, x):
+    g, _ = oracle.dense(oracle_dequant(oracle, dt, scheme, G), x)
+    u, _ = oracle.dense(oracle_dequant(oracle, dt, scheme, U), x)
+    h = oracle.swiglu_product(g, u)
+    y, _ = oracle.dense(oracle_dequant(oracle, dt, scheme, D), h)
+    return h, y
+
+
+@pytest.mark.parametrize("dt,scheme", [(16, 3), (4, 2), (5, 1), (16, 0)])
+@pytest.mark.parametrize("batch,seq,d,inter", [(1, 1, 64, 160), (2, 3, 96, 200), (16, 1, 128, 352)])
+def test_swiglu_matches_oracle(gpu, oracle, dt, scheme, batch, seq, d, inter):
+    rng = np.random.default_rng(d + inter + dt + batch)
+    G = (rng.standard_normal((inter, d)) / np.sqrt(d)).astype(np.float32)
+    U = (rng.standard_normal((inter, d)) / np.sqrt(d)).astype(np.float32)
+    D = (rng.standard_normal((d, inter)) / np.sqrt(inter)).astype(np.float32)
+    x = rng.standard_normal((batch * seq, d)).astype(np.float32)
+    s = gpu.SwiGLUSession(batch, seq, d, inter, dt, scheme, G, U, D)
+    h, y = s.execute(x)
+    s.close()
+    oh, oy = oracle_swiglu(oracle, dt, scheme, G, U, D, x)
+    assert rel_l2(h, oh) <= 1e-5
+    assert rel_l2(y, oy) <= 1e-5
+
+
+def test_c3_swiglu_fp4_block32_batch1(gpu, oracle):
+    """SwiGLU d_model 4096, d_ff 11008, FP4 E2M1 + E8M0 per 32 along K, batch 1."""
+    import pywelvet as pw
+    d, f = 4096, 11008
+    seed = pw.seed_for(3)
+    G = pw.normal(seed, f * d, 1 / np.sqrt(d)).reshape(f, d)
+    U = pw.normal(seed + 1, f * d, 1 / np.sqrt(d)).reshape(f, d)
+    D = pw.normal(seed + 2, d * f, 1 / np.sqrt(f)).reshape(d, f)
+    x = pw.normal(seed + 500, d).reshape(1, d)
+    s = gpu.SwiGLUSession(1, 1, d, f, 16, 3, G, U, D)
+    h, y = s.execute(x)
+    s.close()
+    oh, oy = oracle_swiglu(oracle, 16, 3, G, U, D, x)
+    assert rel_l2(h, oh) <= 1e-5
+    assert rel_l2(y, oy) <= 1e-5
+
+
+def oracle_mha(oracle, dt, scheme, Q, K, V, O, x, B, S, H, KVH, hd, msl, mask, pos):
+    q, _ = oracle.dense(oracle_dequant(oracle, dt, scheme, Q), x)
+    k, _ = oracle.dense(oracle_dequant(oracle, dt, scheme, K), x)
+    v, _ = oracle.dense(oracle_dequant(oracle, dt, scheme, V), x)
+    attn = oracle.mha_attention(q, k, v, B, S, H, KVH, hd, msl, mask, pos)
+    y, _ = oracle.dense(oracle_dequant(oracle, dt, scheme, O), attn)
+    return attn, y
+
+
+@pytest.mark.parametrize("B,S,d,H,KVH,msl,mask,pos", [
+    (2, 8, 64, 4, 4, 8, 1, 0),     # ring = one sequence: batch 1 re-reads batch 1 keys
+    (3, 5, 32, 4, 2, 7, 1, 0),     # ring wraps mid-sequence, GQA
+    (2, 6, 32, 2, 2, 16, 2, 1),    # bidirectional, no positions
+    (2, 6, 48, 3, 3, 6, 3, 2),     # sliding window (msl), ALiBi
+    (1, 9, 64, 4, 1, 9, 4, 3),     # prefix LM (prefix 0), RoPE + ALiBi, MQA
+])
+def test_mha_matches_oracle(gpu, oracle, B, S, d, H, KVH, msl, mask, pos):
+    dt, scheme = 5, 2
+    hd = d // H
+    rng = np.random.default_rng(B * 100 + S + d + mask)
+    Q = (rng.standard_normal((H * hd, d)) / np.sqrt(d)).astype(np.float32)
+    K = (rng.standard_normal((KVH * hd, d)) / np.sqrt(d)).astype(np.float32)
+    V = (rng.standard_normal((KVH * hd, d)) / np.sqrt(d)).astype(np.float32)
+    O = (rng.standard_normal((d, H * hd)) / np.sqrt(H * hd)).astype(np.float32)
+    x = rng.standard_normal((B * S, d)).astype(np.float32)
+    s = gpu.MHASession(B, S, d, H, KVH, 0, msl, mask, pos, dt, scheme, Q, K, V, O)
+    attn, y = s.execute(x)
+    s.close()
+    oattn, oy = oracle_mha(oracle, dt, scheme, Q, K, V, O, x, B, S, H, KVH, hd, msl, mask, pos)
+    assert rel_l2(attn, oattn) <= 1e-4
+    assert rel_l2(y, oy) <= 1e-4
+
+
+def test_mha_seq_above_max_is_invalid(gpu):
+    import pywelvet as pw
+    W = np.zeros((16, 16), np.float32)
+    with pytest.raises(pw.WelvetError) as e:
+        pw.MHASession(1, 9, 16, 2, 2, 0, 8, 1, 0, 5, 0, W, W, W, W)
+    assert e.value.code == 1

@@ -1,0 +1,678 @@
+// C ABI of the quantized Dense path (declarations in include/welvet_c.h).
+// Status conversion and truncation follow src/interop/c_abi.cpp:41-47; no C++
+// exception crosses the boundary.
+#include "welvet_c.h"
+
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <memory>
+#include <mutex>
+#include <new>
+#include <string>
+
+#include "codec.h"
+#include "layers.h"
+#include "model.h"
+#include "runtime.h"
+
+using wv::Status;
+
+namespace {
+
+welvet_status to_c(const Status& st) {
+  welvet_status out{};
+  out.code = st.code;
+  std::strncpy(out.message, st.message.c_str(), sizeof(out.message) - 1);
+  out.message[sizeof(out.message) - 1] = '\0';
+  return out;
+}
+
+welvet_status invalid(const char* msg) { return to_c(Status::err(wv::kInvalid, msg)); }
+
+template <class F>
+welvet_status guarded(F&& fn) {
+  try {
+    return to_c(fn());
+  } catch (const std::bad_alloc&) {
+    return to_c(Status::err(wv::kInternal, "out of host memory"));
+  } catch (const std::exception& e) {
+    return to_c(Status::err(wv::kInternal, e.what()));
+  } catch (...) {
+    return to_c(Status::err(wv::kInternal, "unknown native failure"));
+  }
+}
+
+welvet_status gap(const char* what) {
+  return to_c(Status::err(wv::kGap, std::string("gap? ") + what +
+                                        " is outside the quantized Dense path of this build"));
+}
+
+hipStream_t pick(void* stream, hipStream_t own) {
+  return stream ? static_cast<hipStream_t>(stream) : own;
+}
+
+}  // namespace
+
+struct welvet_dense_session {
+  wv::Stream stream;
+  wv::DenseLayer layer;
+  wv::Workspace ws;
+  int batch = 0;
+  wv::DevBuf x, pre, post;
+};
+
+struct welvet_swiglu_session {
+  wv::Stream stream;
+  wv::SwiGLULayer layer;
+  wv::Workspace ws;
+  int rows = 0;
+  wv::DevBuf x, pre, post;
+};
+
+struct welvet_mha_session {
+  wv::Stream stream;
+  wv::MHALayer layer;
+  wv::Workspace ws;
+  int batch = 0, seq = 0;
+  wv::DevBuf x, pre, post;
+};
+
+extern "C" {
+
+const char* welvet_version(void) { return "0.79"; }
+
+const char* welvet_runtime_identity(void) {
+  static thread_local std::string id;
+  id = wv::identity();
+  return id.c_str();
+}
+
+welvet_status welvet_cuda_init(void) { return to_c(wv::init_device()); }
+
+int32_t welvet_cuda_available(void) { return wv::device_available() ? 1 : 0; }
+
+// Ledger of this build: reference C entry points served on the GPU vs those
+// returning code 3.
+int32_t welvet_gaps_count(void) { return 41; }
+int32_t welvet_gaps_done(void) { return 18; }
+
+// ---------------------------------------------------------------- Dense ----
+static welvet_status dense_mount(int32_t batch, int32_t in, int32_t out, int32_t act,
+                                 int32_t dtype, int32_t backend, const float* W_init,
+                                 const double* bias, size_t bias_len,
+                                 welvet_dense_session** sess_out) {
+  if (!sess_out) return invalid("null mount args");
+  *sess_out = nullptr;
+  if (!W_init) return invalid("null mount args");
+  if (batch <= 0 || in <= 0 || out <= 0) return invalid("bad dims");
+  return guarded([&]() -> Status {
+    WV_TRY(wv::init_device());
+    auto* s = new welvet_dense_session();
+    auto fail = [&](Status st) {
+      delete s;
+      return st;
+    };
+    Status st = s->stream.create();
+    if (st) st = wv::dense_build(in, out, act, dtype, backend, W_init, bias, bias_len, &s->layer,
+                                 s->stream.s);
+    if (st) st = s->x.alloc((size_t)batch * in * sizeof(float));
+    if (st) st = s->pre.alloc((size_t)batch * out * sizeof(float));
+    if (st) st = s->post.alloc((size_t)batch * out * sizeof(float));
+    if (!st) return fail(st);
+    s->batch = batch;
+    *sess_out = s;
+    return Status::ok();
+  });
+}
+
+welvet_status welvet_dense_mount(int32_t batch, int32_t in, int32_t out, int32_t act,
+                                 int32_t dtype, const float* W_init, const double* bias,
+                                 size_t bias_len, welvet_dense_session** sess_out) {
+  return dense_mount(batch, in, out, act, dtype, 0, W_init, bias, bias_len, sess_out);
+}
+
+welvet_status welvet_dense_mount_q(int32_t batch, int32_t in, int32_t out, int32_t act,
+                                   int32_t dtype, int32_t backend, const float* W_init,
+                                   const double* bias, size_t bias_len,
+                                   welvet_dense_session** sess_out) {
+  return dense_mount(batch, in, out, act, dtype, backend, W_init, bias, bias_len, sess_out);
+}
+
+welvet_status welvet_dense_execute(welvet_dense_session* s, const float* x, float* pre,
+                                   float* post) {
+  if (!s || !x || !pre || !post) return invalid("null execute args");
+  return guarded([&]() -> Status {
+    const size_t xb = (size_t)s->batch * s->layer.in * sizeof(float);
+    const size_t yb = (size_t)s->batch * s->layer.out * sizeof(float);
+    hipStream_t st = s->stream.s;
+    WV_HIP(hipMemcpyAsync(s->x.p, x, xb, hipMemcpyHostToDevice, st));
+    WV_TRY(wv::dense_forward(s->layer, s->batch, s->x.as<float>(), s->pre.as<float>(),
+                             s->post.as<float>(), &s->ws, st));
+    WV_HIP(hipMemcpyAsync(pre, s->pre.p, yb, hipMemcpyDeviceToHost, st));
+    WV_HIP(hipMemcpyAsync(post, s->post.p, yb, hipMemcpyDeviceToHost, st));
+    WV_HIP(hipStreamSynchronize(st));
+    return Status::ok();
+  });
+}
+
+welvet_status welvet_dense_execute_device(welvet_dense_session* s, const float* x, float* pre,
+                                          float* post, void* stream) {
+  if (!s || !x || !pre || !post) return invalid("null execute args");
+  if (pre == post && s->layer.need_epi()) return invalid("pre and post must differ");
+  return guarded([&]() -> Status {
+    return wv::dense_forward(s->layer, s->batch, x, pre, post, &s->ws, pick(stream, s->stream.s));
+  });
+}
+
+welvet_status welvet_dense_export_store(welvet_dense_session* s, uint8_t* native,
+                                        size_t native_cap, size_t* native_len, float* row_scale,
+                                        uint8_t* blk_exp, float* tensor_scale) {
+  if (!s) return invalid("null session");
+  const wv::WeightStore& w = s->layer.store;
+  if (native_len) *native_len = w.native.size();
+  if (native) {
+    if (native_cap < w.native.size()) return invalid("native buffer too small");
+    std::memcpy(native, w.native.data(), w.native.size());
+  }
+  if (row_scale) std::memcpy(row_scale, w.row_scale.data(), w.row_scale.size() * sizeof(float));
+  if (blk_exp && !w.blk_exp.empty()) std::memcpy(blk_exp, w.blk_exp.data(), w.blk_exp.size());
+  if (tensor_scale) *tensor_scale = w.scale;
+  return to_c(Status::ok());
+}
+
+void welvet_dense_release(welvet_dense_session* s) { delete s; }
+
+welvet_status welvet_dense_forward_f32(int32_t batch, int32_t in, int32_t out, int32_t act,
+                                       int32_t dtype, int32_t backend, const float* W_init,
+                                       const double* bias, size_t bias_len, const float* x,
+                                       float* pre, float* post) {
+  if (batch <= 0 || in <= 0 || out <= 0 || !x || !pre || !post) return invalid("bad dims");
+  welvet_dense_session* s = nullptr;
+  std::vector<float> zeros;
+  if (!W_init) {
+    zeros.assign((size_t)in * out, 0.0f);
+    W_init = zeros.data();
+  }
+  welvet_status st = dense_mount(batch, in, out, act, dtype, backend, W_init, bias, bias_len, &s);
+  if (st.code != 0) return st;
+  st = welvet_dense_execute(s, x, pre, post);
+  welvet_dense_release(s);
+  return st;
+}
+
+// --------------------------------------------------------------- SwiGLU ----
+welvet_status welvet_swiglu_mount(int32_t batch, int32_t seq, int32_t input_dim,
+                                  int32_t intermediate_dim, int32_t dtype, int32_t backend,
+                                  const float* Gate, const float* Up, const float* Down,
+                                  welvet_swiglu_session** out) {
+  if (!out) return invalid("swiglu: invalid argument");
+  *out = nullptr;
+  if (batch <= 0 || seq <= 0 || input_dim <= 0 || intermediate_dim <= 0 || !Gate || !Up || !Down)
+    return invalid("swiglu: invalid argument");
+  return guarded([&]() -> Status {
+    WV_TRY(wv::init_device());
+    auto* s = new welvet_swiglu_session();
+    const int rows = batch * seq;
+    Status st = s->stream.create();
+    if (st) st = wv::swiglu_build(input_dim, intermediate_dim, dtype, backend, Gate, Up, Down,
+                                  &s->layer, s->stream.s);
+    if (st) st = s->x.alloc((size_t)rows * input_dim * sizeof(float));
+    if (st) st = s->pre.alloc((size_t)rows * intermediate_dim * sizeof(float));
+    if (st) st = s->post.alloc((size_t)rows * input_dim * sizeof(float));
+    if (!st) {
+      delete s;
+      return st;
+    }
+    s->rows = rows;
+    *out = s;
+    return Status::ok();
+  });
+}
+
+welvet_status welvet_swiglu_execute(welvet_swiglu_session* s, const float* x, float* pre,
+                                    float* post) {
+  if (!s || !x || !pre || !post) return invalid("swiglu: invalid argument");
+  return guarded([&]() -> Status {
+    const size_t xb = (size_t)s->rows * s->layer.in * sizeof(float);
+    const size_t hb = (size_t)s->rows * s->layer.inter * sizeof(float);
+    hipStream_t st = s->stream.s;
+    WV_HIP(hipMemcpyAsync(s->x.p, x, xb, hipMemcpyHostToDevice, st));
+    WV_TRY(wv::swiglu_forward(s->layer, s->rows, s->x.as<float>(), s->pre.as<float>(),
+                              s->post.as<float>(), &s->ws, st));
+    WV_HIP(hipMemcpyAsync(pre, s->pre.p, hb, hipMemcpyDeviceToHost, st));
+    WV_HIP(hipMemcpyAsync(post, s->post.p, xb, hipMemcpyDeviceToHost, st));
+    WV_HIP(hipStreamSynchronize(st));
+    return Status::ok();
+  });
+}
+
+welvet_status welvet_swiglu_execute_device(welvet_swiglu_session* s, const float* x, float* pre,
+                                           float* post, void* stream) {
+  if (!s || !x || !pre || !post) return invalid("swiglu: invalid argument");
+  return guarded([&]() -> Status {
+    return wv::swiglu_forward(s->layer, s->rows, x, pre, post, &s->ws, pick(stream, s->stream.s));
+  });
+}
+
+void welvet_swiglu_release(welvet_swiglu_session* s) { delete s; }
+
+welvet_status welvet_swiglu_forward_f32(int32_t batch, int32_t seq, int32_t input_dim,
+                                        int32_t intermediate_dim, int32_t dtype, int32_t backend,
+                                        const float* Gate, const float* Up, const float* Down,
+                                        const float* x, float* pre, float* post) {
+  if (batch <= 0 || seq <= 0 || input_dim <= 0 || intermediate_dim <= 0 || !Gate || !Up || !Down ||
+      !x || !pre || !post)
+    return invalid("swiglu: invalid argument");
+  welvet_swiglu_session* s = nullptr;
+  welvet_status st = welvet_swiglu_mount(batch, seq, input_dim, intermediate_dim, dtype, backend,
+                                         Gate, Up, Down, &s);
+  if (st.code != 0) return st;
+  st = welvet_swiglu_execute(s, x, pre, post);
+  welvet_swiglu_release(s);
+  return st;
+}
+
+// ------------------------------------------------------------------ MHA ----
+welvet_status welvet_mha_mount(int32_t batch, int32_t seq, int32_t d_model, int32_t num_heads,
+                               int32_t num_kv_heads, int32_t head_dim, int32_t max_seq_len,
+                               int32_t mask, int32_t pos, int32_t dtype, int32_t backend,
+                               const float* Q, const float* K, const float* V, const float* O,
+                               welvet_mha_session** out) {
+  if (!out) return invalid("mha: invalid argument");
+  *out = nullptr;
+  if (batch <= 0 || seq <= 0 || d_model <= 0 || num_heads <= 0 || !Q || !K || !V || !O)
+    return invalid("mha: invalid argument");
+  if (mask < 0 || mask > 5 || pos < 0 || pos > 3) return invalid("mha: bad mask/pos kind");
+  if (mask == 5) return to_c(Status::err(wv::kGap, "gap? mha custom mask"));
+  return guarded([&]() -> Status {
+    WV_TRY(wv::init_device());
+    wv::MHAConfig cfg;
+    cfg.d_model = d_model;
+    cfg.num_heads = num_heads;
+    cfg.num_kv_heads = num_kv_heads;
+    cfg.head_dim = head_dim;
+    cfg.max_seq_len = max_seq_len;
+    cfg.mask = mask;
+    cfg.pos = pos;
+    WV_TRY(wv::mha_validate(&cfg));
+    if (seq > cfg.max_seq_len) return Status::err(wv::kInvalid, "mha: seq > MaxSeqLen");
+    auto* s = new welvet_mha_session();
+    const size_t T = (size_t)batch * seq;
+    Status st = s->stream.create();
+    if (st) st = wv::mha_build(cfg, dtype, backend, Q, K, V, O, &s->layer, s->stream.s);
+    if (st) st = s->x.alloc(T * d_model * sizeof(float));
+    if (st) st = s->pre.alloc(T * cfg.q_dim() * sizeof(float));
+    if (st) st = s->post.alloc(T * d_model * sizeof(float));
+    if (!st) {
+      delete s;
+      return st;
+    }
+    s->batch = batch;
+    s->seq = seq;
+    *out = s;
+    return Status::ok();
+  });
+}
+
+welvet_status welvet_mha_execute(welvet_mha_session* s, const float* x, float* pre, float* post) {
+  if (!s || !x || !pre || !post) return invalid("mha: invalid argument");
+  return guarded([&]() -> Status {
+    const size_t T = (size_t)s->batch * s->seq;
+    const size_t xb = T * s->layer.cfg.d_model * sizeof(float);
+    const size_t ab = T * s->layer.cfg.q_dim() * sizeof(float);
+    hipStream_t st = s->stream.s;
+    WV_HIP(hipMemcpyAsync(s->x.p, x, xb, hipMemcpyHostToDevice, st));
+    WV_TRY(wv::mha_forward(s->layer, s->batch, s->seq, s->x.as<float>(), s->pre.as<float>(),
+                           s->post.as<float>(), &s->ws, st));
+    WV_HIP(hipMemcpyAsync(pre, s->pre.p, ab, hipMemcpyDeviceToHost, st));
+    WV_HIP(hipMemcpyAsync(post, s->post.p, xb, hipMemcpyDeviceToHost, st));
+    WV_HIP(hipStreamSynchronize(st));
+    return Status::ok();
+  });
+}
+
+welvet_status welvet_mha_execute_device(welvet_mha_session* s, const float* x, float* pre,
+                                        float* post, void* stream) {
+  if (!s || !x || !pre || !post) return invalid("mha: invalid argument");
+  return guarded([&]() -> Status {
+    return wv::mha_forward(s->layer, s->batch, s->seq, x, pre, post, &s->ws,
+                           pick(stream, s->stream.s));
+  });
+}
+
+void welvet_mha_release(welvet_mha_session* s) { delete s; }
+
+welvet_status welvet_mha_forward_f32(int32_t batch, int32_t seq, int32_t d_model,
+                                     int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                                     int32_t max_seq_len, int32_t mask, int32_t pos, int32_t dtype,
+                                     int32_t backend, const float* Q, const float* K,
+                                     const float* V, const float* O, const float* x, float* pre,
+                                     float* post) {
+  if (!x || !pre || !post) return invalid("mha: invalid argument");
+  welvet_mha_session* s = nullptr;
+  welvet_status st = welvet_mha_mount(batch, seq, d_model, num_heads, num_kv_heads, head_dim,
+                                      max_seq_len, mask, pos, dtype, backend, Q, K, V, O, &s);
+  if (st.code != 0) return st;
+  st = welvet_mha_execute(s, x, pre, post);
+  welvet_mha_release(s);
+  return st;
+}
+
+// ---------------------------------------------------------------- model ----
+struct welvet_model_session {
+  std::mutex mu;
+  wv::Stream stream;
+  wv::Model model;
+};
+
+int32_t welvet_model_abi_version(void) { return 1; }
+
+static welvet_status model_mount(const uint8_t* descriptor, size_t size, int32_t backend,
+                                 welvet_model_session** out) {
+  if (out) *out = nullptr;
+  if (!out || !descriptor) return invalid("invalid mount arguments");
+  return guarded([&]() -> Status {
+    auto s = std::make_unique<welvet_model_session>();
+    WV_TRY(wv::model_parse(descriptor, size, backend, &s->model));
+    WV_TRY(wv::init_device());
+    WV_TRY(s->stream.create());
+    WV_TRY(wv::model_build(&s->model, s->stream.s));
+    *out = s.release();
+    return Status::ok();
+  });
+}
+
+welvet_status welvet_model_mount(const uint8_t* descriptor, size_t size,
+                                 welvet_model_session** out) {
+  return model_mount(descriptor, size, 0, out);
+}
+
+welvet_status welvet_model_mount_q(const uint8_t* descriptor, size_t size, int32_t backend,
+                                   welvet_model_session** out) {
+  return model_mount(descriptor, size, backend, out);
+}
+
+// Input tensor wire (model_session.cpp:101-116): i32 rank (1..5), i32 dims,
+// then the f32 data without a count. Output (:117-122): rank, dims, i32 count,
+// data.
+welvet_status welvet_model_forward(welvet_model_session* s, const uint8_t* input, size_t size,
+                                   welvet_cuda_blob* out) {
+  if (!s || !input || !out) return invalid("invalid forward arguments");
+  out->data = nullptr;
+  out->size = 0;
+  return guarded([&]() -> Status {
+    std::lock_guard<std::mutex> lock(s->mu);
+    size_t off = 0;
+    auto rd = [&](void* dst, size_t n) {
+      if (size - off < n) return false;
+      std::memcpy(dst, input + off, n);
+      off += n;
+      return true;
+    };
+    int32_t rank = 0;
+    if (!rd(&rank, 4) || rank <= 0 || rank > 5) return Status::err(wv::kInvalid, "tensor rank must be 1..5");
+    std::vector<int> shape((size_t)rank);
+    size_t n = 1;
+    for (auto& d : shape) {
+      int32_t v = 0;
+      if (!rd(&v, 4) || v <= 0 || n > (size_t(1) << 26) / (size_t)v)
+        return Status::err(wv::kInvalid, "invalid tensor shape");
+      d = v;
+      n *= (size_t)v;
+    }
+    if ((size - off) / 4 < n) return Status::err(wv::kInvalid, "short tensor data");
+    if (size - off != n * 4) return Status::err(wv::kInvalid, "trailing descriptor bytes");
+    hipStream_t st = s->stream.s;
+    wv::DevBuf dx, dy;
+    WV_TRY(dx.alloc(n * 4));
+    WV_HIP(hipMemcpyAsync(dx.p, input + off, n * 4, hipMemcpyHostToDevice, st));
+    const size_t cap = size_t(1) << 26;
+    WV_TRY(dy.alloc(cap * 4));
+    std::vector<int> oshape;
+    WV_TRY(wv::model_forward(s->model, shape, dx.as<float>(), &oshape, dy.as<float>(), cap, st));
+    size_t on = 1;
+    for (int d : oshape) on *= (size_t)d;
+    std::vector<uint8_t> blob;
+    auto put = [&](const void* p, size_t k) {
+      const uint8_t* b = static_cast<const uint8_t*>(p);
+      blob.insert(blob.end(), b, b + k);
+    };
+    const int32_t orank = (int32_t)oshape.size();
+    put(&orank, 4);
+    for (int d : oshape) {
+      const int32_t v = d;
+      put(&v, 4);
+    }
+    const int32_t cnt = (int32_t)on;
+    put(&cnt, 4);
+    const size_t hdr = blob.size();
+    blob.resize(hdr + on * 4);
+    WV_HIP(hipMemcpyAsync(blob.data() + hdr, dy.p, on * 4, hipMemcpyDeviceToHost, st));
+    WV_HIP(hipStreamSynchronize(st));
+    out->data = static_cast<uint8_t*>(std::malloc(blob.size()));
+    if (!out->data) return Status::err(wv::kInternal, "out of host memory");
+    std::memcpy(out->data, blob.data(), blob.size());
+    out->size = blob.size();
+    return Status::ok();
+  });
+}
+
+welvet_status welvet_model_forward_device(welvet_model_session* s, const float* x, int32_t batch,
+                                          int32_t width, float* y, int32_t y_cap, void* stream) {
+  if (!s || !x || !y || batch <= 0 || width <= 0 || y_cap <= 0)
+    return invalid("invalid forward arguments");
+  return guarded([&]() -> Status {
+    std::lock_guard<std::mutex> lock(s->mu);
+    std::vector<int> oshape;
+    return wv::model_forward(s->model, {batch, width}, x, &oshape, y, (size_t)y_cap,
+                             pick(stream, s->stream.s));
+  });
+}
+
+welvet_status welvet_model_export_weights(welvet_model_session* s, welvet_cuda_blob* out) {
+  if (!s || !out) return invalid("invalid export arguments");
+  out->data = nullptr;
+  out->size = 0;
+  return guarded([&]() -> Status {
+    std::lock_guard<std::mutex> lock(s->mu);
+    std::vector<uint8_t> blob;
+    WV_TRY(wv::model_export(s->model, &blob));
+    out->data = static_cast<uint8_t*>(std::malloc(blob.size()));
+    if (!out->data) return Status::err(wv::kInternal, "out of host memory");
+    std::memcpy(out->data, blob.data(), blob.size());
+    out->size = blob.size();
+    return Status::ok();
+  });
+}
+
+void welvet_model_release(welvet_model_session* s) { delete s; }
+
+void welvet_cuda_blob_free(welvet_cuda_blob* b) {
+  if (b) {
+    std::free(b->data);
+    b->data = nullptr;
+    b->size = 0;
+  }
+}
+
+// ---------------------------------------------------------- codec check ----
+welvet_status welvet_codec_sweep(int32_t dtype, uint32_t first_chunk, uint32_t n_chunks,
+                                 int64_t* out) {
+  if (!out || n_chunks == 0 || (uint64_t)first_chunk + n_chunks > 4096u)
+    return invalid("codec sweep: chunk range must lie in [0, 4096)");
+  if (dtype != wv::kE4M3 && dtype != wv::kE5M2 && dtype != wv::kFP4)
+    return to_c(Status::err(wv::kUnsupported, "codec sweep: dtype"));
+  return guarded([&]() -> Status {
+    WV_TRY(wv::init_device());
+    wv::Stream s;
+    WV_TRY(s.create());
+    return wv::codec_sweep(dtype, first_chunk, n_chunks, out, s.s);
+  });
+}
+
+// ------------------------------------------------------------- seqmix ----
+// Metadata only (reference include/welvet/seqmix.hpp): kind tags.
+welvet_status welvet_seqmix_kind_name(int32_t kind, char* buf, int32_t buf_len) {
+  if (!buf || buf_len <= 0) return invalid("seqmix: bad buf");
+  static const char* names[] = {"attention", "ssm", "linear_attn", "conv_mix"};
+  if (kind < 0 || kind > 3) {
+    welvet_status st{};
+    st.code = wv::kInvalid;
+    std::snprintf(st.message, sizeof(st.message), "seqmix: unknown kind %d", (int)kind);
+    return st;
+  }
+  std::snprintf(buf, (size_t)buf_len, "%s", names[kind]);
+  return to_c(Status::ok());
+}
+int32_t welvet_seqmix_mha_kind(void) { return 0; }
+int32_t welvet_seqmix_mamba_kind(void) { return 1; }
+int32_t welvet_seqmix_gdn_kind(void) { return 2; }
+
+// ------------------------------------------------- outside this path ----
+welvet_status welvet_model_train_credit(welvet_model_session*, int32_t, double, const uint8_t*,
+                                        size_t) {
+  return gap("model train credit");
+}
+welvet_status welvet_model_dense_proxy(welvet_model_session*, int32_t, const uint8_t*, size_t,
+                                       welvet_cuda_blob*) {
+  return gap("model dense proxy");
+}
+welvet_status welvet_model_forward_pair(welvet_model_session*, const uint8_t*, size_t,
+                                        welvet_cuda_blob*) {
+  return gap("model forward pair");
+}
+welvet_status welvet_model_backward(welvet_model_session*, const uint8_t*, size_t,
+                                    welvet_cuda_blob*) {
+  return gap("model backward");
+}
+welvet_status welvet_model_apply_sgd(welvet_model_session*, double, const uint8_t*, size_t) {
+  return gap("model SGD");
+}
+welvet_status welvet_model_train_mse(welvet_model_session*, int32_t, double, int32_t,
+                                     const uint8_t*, size_t, double*) {
+  return gap("model training");
+}
+welvet_status welvet_model_sync(welvet_model_session*, int32_t) { return gap("model sync"); }
+
+#define WV_GAP_NBP(name, ...) \
+  welvet_status name(__VA_ARGS__) { return gap(#name); }
+
+WV_GAP_NBP(welvet_dense_normalbp_f32, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t,
+           const float*, const double*, size_t, const float*, const float*, int32_t, double, float*,
+           float*, float*, float*, float*, double*)
+WV_GAP_NBP(welvet_rmsnorm_forward_f32, int32_t, int32_t, int32_t, double, int32_t, int32_t,
+           const float*, const float*, float*, float*)
+WV_GAP_NBP(welvet_rmsnorm_normalbp_f32, int32_t, int32_t, int32_t, double, int32_t, int32_t,
+           const float*, const float*, const float*, int32_t, double, float*, float*, float*,
+           float*, float*, double*)
+WV_GAP_NBP(welvet_layernorm_forward_f32, int32_t, int32_t, int32_t, double, int32_t, int32_t,
+           const float*, const float*, const float*, float*, float*)
+WV_GAP_NBP(welvet_layernorm_normalbp_f32, int32_t, int32_t, int32_t, double, int32_t, int32_t,
+           const float*, const float*, const float*, const float*, int32_t, double, float*, float*,
+           float*, float*, float*, float*, double*)
+WV_GAP_NBP(welvet_softmax_forward_f32, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t,
+           double, double, int32_t, int32_t, int32_t, int32_t, const int32_t*, const uint8_t*,
+           int32_t, const int32_t*, int32_t, const float*, float*, float*)
+WV_GAP_NBP(welvet_softmax_normalbp_f32, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t,
+           double, double, int32_t, int32_t, int32_t, int32_t, const int32_t*, const uint8_t*,
+           int32_t, const int32_t*, int32_t, const float*, const float*, int32_t, double, float*,
+           float*, float*, double*)
+WV_GAP_NBP(welvet_swiglu_normalbp_f32, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t,
+           const float*, const float*, const float*, const float*, const float*, int32_t, double,
+           float*, float*, float*, float*, float*, double*)
+WV_GAP_NBP(welvet_embedding_forward_f32, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t,
+           int32_t, int32_t, int32_t, const float*, const float*, float*, float*)
+WV_GAP_NBP(welvet_embedding_normalbp_f32, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t,
+           int32_t, int32_t, int32_t, const float*, const float*, const float*, int32_t, double,
+           float*, float*, float*, float*, float*, double*)
+WV_GAP_NBP(welvet_mha_normalbp_f32, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t,
+           int32_t, int32_t, int32_t, int32_t, const float*, const float*, const float*,
+           const float*, const float*, const float*, int32_t, double, float*, float*, float*,
+           float*, float*, double*)
+WV_GAP_NBP(welvet_cnn1_forward_f32, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t,
+           int32_t, int32_t, int32_t, const float*, const double*, size_t, const float*, float*,
+           float*)
+WV_GAP_NBP(welvet_cnn1_normalbp_f32, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t,
+           int32_t, int32_t, int32_t, const float*, const double*, size_t, const float*,
+           const float*, int32_t, double, float*, float*, float*, float*, float*, double*)
+WV_GAP_NBP(welvet_cnn2_forward_f32, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t,
+           int32_t, int32_t, int32_t, int32_t, const float*, const double*, size_t, const float*,
+           float*, float*)
+WV_GAP_NBP(welvet_cnn2_normalbp_f32, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t,
+           int32_t, int32_t, int32_t, int32_t, const float*, const double*, size_t, const float*,
+           const float*, int32_t, double, float*, float*, float*, float*, float*, double*)
+WV_GAP_NBP(welvet_cnn3_forward_f32, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t,
+           int32_t, int32_t, int32_t, int32_t, int32_t, const float*, const double*, size_t,
+           const float*, float*, float*)
+WV_GAP_NBP(welvet_cnn3_normalbp_f32, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t,
+           int32_t, int32_t, int32_t, int32_t, int32_t, const float*, const double*, size_t,
+           const float*, const float*, int32_t, double, float*, float*, float*, float*, float*,
+           double*)
+WV_GAP_NBP(welvet_convt1_forward_f32, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t,
+           int32_t, int32_t, int32_t, int32_t, const float*, const float*, float*, float*)
+WV_GAP_NBP(welvet_convt1_normalbp_f32, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t,
+           int32_t, int32_t, int32_t, int32_t, int32_t, const float*, const float*, const float*,
+           int32_t, double, float*, float*, float*, float*, float*, double*)
+WV_GAP_NBP(welvet_convt2_forward_f32, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t,
+           int32_t, int32_t, int32_t, int32_t, int32_t, const float*, const float*, float*, float*)
+WV_GAP_NBP(welvet_convt2_normalbp_f32, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t,
+           int32_t, int32_t, int32_t, int32_t, int32_t, int32_t, const float*, const float*,
+           const float*, int32_t, double, float*, float*, float*, float*, float*, double*)
+WV_GAP_NBP(welvet_convt3_forward_f32, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t,
+           int32_t, int32_t, int32_t, int32_t, int32_t, int32_t, const float*, const float*, float*,
+           float*)
+WV_GAP_NBP(welvet_convt3_normalbp_f32, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t,
+           int32_t, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t, const float*,
+           const float*, const float*, int32_t, double, float*, float*, float*, float*, float*,
+           double*)
+WV_GAP_NBP(welvet_rnn_forward_f32, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t,
+           const float*, const float*, float*, float*)
+WV_GAP_NBP(welvet_rnn_normalbp_f32, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t,
+           const float*, const float*, const float*, int32_t, double, float*, float*, float*,
+           float*, float*, double*)
+WV_GAP_NBP(welvet_lstm_forward_f32, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t,
+           const float*, const float*, float*, float*)
+WV_GAP_NBP(welvet_lstm_normalbp_f32, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t,
+           const float*, const float*, const float*, int32_t, double, float*, float*, float*,
+           float*, float*, double*)
+WV_GAP_NBP(welvet_sequential_forward_f32, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t,
+           int32_t, const float*, const float*, float*, float*)
+WV_GAP_NBP(welvet_sequential_normalbp_f32, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t,
+           int32_t, const float*, const float*, const float*, int32_t, double, float*, float*,
+           float*, float*, float*, double*)
+WV_GAP_NBP(welvet_residual_forward_f32, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t,
+           int32_t, const float*, const float*, float*, float*)
+WV_GAP_NBP(welvet_residual_normalbp_f32, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t,
+           int32_t, const float*, const float*, const float*, int32_t, double, float*, float*,
+           float*, float*, float*, double*)
+WV_GAP_NBP(welvet_stack_normalbp_f32, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t,
+           int32_t, const float*, const float*, const float*, int32_t, double, float*, float*,
+           float*, float*, float*, double*)
+WV_GAP_NBP(welvet_mamba_normalbp_f32, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t,
+           int32_t, const float*, const float*, const float*, int32_t, double, float*, float*,
+           float*, float*, float*, double*)
+WV_GAP_NBP(welvet_metacognition_normalbp_f32, int32_t, int32_t, int32_t, int32_t, int32_t,
+           const float*, const float*, const float*, int32_t, double, float*, float*, float*,
+           float*, float*, double*)
+WV_GAP_NBP(welvet_gdn_normalbp_f32, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t,
+           int32_t, int32_t, int32_t, const float*, const float*, const float*, int32_t, double,
+           float*, float*, float*, float*, float*, double*)
+WV_GAP_NBP(welvet_kmeans_normalbp_f32, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t,
+           double, int32_t, int32_t, const float*, const float*, const float*, int32_t, double,
+           float*, float*, float*, float*, float*, double*)
+WV_GAP_NBP(welvet_parallel_normalbp_f32, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t,
+           int32_t, int32_t, int32_t, double, const float*, const float*, const float*, int32_t,
+           double, float*, float*, float*, float*, float*, double*)
+WV_GAP_NBP(welvet_mamba_forward_f32, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t,
+           const float*, const float*, float*, float*)
+WV_GAP_NBP(welvet_metacognition_forward_f32, int32_t, int32_t, int32_t, int32_t, int32_t,
+           const float*, const float*, float*, float*)
+WV_GAP_NBP(welvet_gdn_forward_f32, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t,
+           int32_t, int32_t, int32_t, const float*, const float*, float*, float*)
+WV_GAP_NBP(welvet_kmeans_forward_f32, int32_t, int32_t, int32_t, int32_t, int32_t, double, int32_t,
+           int32_t, int32_t, const int32_t*, const float*, const float*, float*, float*)
+WV_GAP_NBP(welvet_parallel_forward_f32, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t,
+           int32_t, int32_t, int32_t, double, const float*, const float*, float*, float*)
+
+}  // extern "C"

@@ -1,0 +1,55 @@
+// Host-side launchers of the device kernels.
+#pragma once
+
+#include "common.h"
+
+namespace wv {
+
+// ---- mount-time quantization (quant.hip) ----
+// Quantizes the device fp32 matrix dW [rows x cols] into dw (allocates it) and,
+// if d_raw is set, writes the reference FormatNone payload there.
+Status quantize_to_device(const float* dW, int dtype, int scheme, int rows, int cols,
+                          DeviceWeights* dw, uint8_t* d_raw, hipStream_t st);
+// Builds dw from a reference payload already on the device plus optional
+// scales (row scales [rows]; E8M0 bytes [rows][ceil(cols/32)]).
+Status relayout_to_device(const uint8_t* d_raw, int dtype, int scheme, int rows, int cols,
+                          const float* d_row_scale, const uint8_t* d_blk_rows,
+                          DeviceWeights* dw, hipStream_t st);
+// Encoder digests over all f32 patterns of the given 2^20-pattern chunks.
+Status codec_sweep(int dtype, uint32_t first_chunk, uint32_t n_chunks, int64_t* host_out,
+                   hipStream_t st);
+
+// ---- small-batch GEMV (gemv.hip) ----
+struct GemvArgs {
+  const uint8_t* codes[2] = {nullptr, nullptr};
+  const float* scale[2] = {nullptr, nullptr};
+  const uint8_t* blk[2] = {nullptr, nullptr};
+  int mats = 1;
+  int pitch = 0, nblk = 0, kpad = 0, cols = 0, rows = 0;
+  const float* x = nullptr;
+  int x_stride = 0;
+  float* pre = nullptr;
+  float* post = nullptr;
+  int out_stride = 0;
+  int act = kLinear;
+  int need_epi = 0;
+  const double* bias = nullptr;
+  int bias_len = 0;
+};
+Status launch_gemv(const GemvArgs& a, int dtype, bool blk, int batch, int rows_per_group,
+                   hipStream_t st);
+
+// ---- attention core (attention.hip) ----
+struct AttnArgs {
+  const float* q = nullptr;  // [tokens][heads*hd], rotated in place when rope
+  const float* k = nullptr;  // [tokens][kv_heads*hd], rotated in place when rope
+  const float* v = nullptr;  // [tokens][kv_heads*hd]
+  float* out = nullptr;      // [tokens][heads*hd]
+  int tokens = 0, seq = 0, heads = 0, kv_heads = 0, hd = 0, msl = 0;
+  int mask = 1, window = 0, prefix_len = 0, window_causal = 1;
+  int rope = 0, alibi = 0, sigmoid = 0;
+  double rope_theta = 10000.0, scale = 0.125;
+};
+Status launch_attention(const AttnArgs& a, hipStream_t st);
+
+}  // namespace wv

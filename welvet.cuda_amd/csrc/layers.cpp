@@ -1,0 +1,267 @@
+// Dense / SwiGLU / MHA layers over device-resident quantized weights.
+//
+// Reference call structure kept: Dense is the hub (src/layers/dense/dense.cpp:
+// 10-86); SwiGLU = Gate, Up (Linear, no bias), SiLU product, Down
+// (src/layers/swiglu/swiglu.cpp:87-136); MHA = Q/K/V projections on
+// [batch*seq, d], attention core, O projection (src/layers/mha/mha.cpp:123-183).
+// Unlike the reference, weights are quantized once on the device and stay
+// there; activations stay on the device between the layer's kernels.
+#include "layers.h"
+
+#include <cmath>
+#include <cstring>
+
+#include "codec.h"
+
+namespace wv {
+
+Status check_dtype_scheme(int dtype, int scheme) {
+  if (dtype != kE4M3 && dtype != kE5M2 && dtype != kFP4) {
+    return Status::err(kUnsupported, "dtype " + std::to_string(dtype) +
+                                         " is outside the FP8/FP4 path (supported: 4, 5, 16)");
+  }
+  if (scheme < kSchemeRef || scheme > kSchemeBlock32)
+    return Status::err(kInvalid, "backend (scale scheme) must be 0..3");
+  return Status::ok();
+}
+
+static Status download_store(DenseLayer* L, const uint8_t* d_raw, hipStream_t st) {
+  WeightStore& s = L->store;
+  const DeviceWeights& d = L->dev;
+  const int64_t n = (int64_t)d.rows * d.cols;
+  s.native.resize(d.dtype == kFP4 ? (size_t)((n + 1) / 2) : (size_t)n);
+  if (d_raw) {
+    WV_HIP(hipMemcpyAsync(s.native.data(), d_raw, s.native.size(), hipMemcpyDeviceToHost, st));
+  }
+  s.row_scale.resize((size_t)d.rows);
+  WV_HIP(hipMemcpyAsync(s.row_scale.data(), d.d_scale(), (size_t)d.rows * sizeof(float),
+                        hipMemcpyDeviceToHost, st));
+  if (d.scheme == kSchemeBlock32) {
+    const int nb = (d.cols + 31) / 32;
+    s.blk_exp.resize((size_t)d.rows * nb);
+    WV_HIP(hipMemcpy2DAsync(s.blk_exp.data(), nb, d.d_blk(), d.nblk, nb, d.rows,
+                            hipMemcpyDeviceToHost, st));
+  } else {
+    s.blk_exp.clear();
+  }
+  WV_HIP(hipStreamSynchronize(st));
+  s.scale = (d.scheme == kSchemeTensor && !s.row_scale.empty()) ? s.row_scale[0] : 1.0f;
+  return Status::ok();
+}
+
+static Status upload_bias(DenseLayer* L, const double* bias, size_t bias_len, hipStream_t st) {
+  L->store.bias.assign(bias ? bias : nullptr, bias ? bias + bias_len : nullptr);
+  L->bias_len = (bias && bias_len > 0) ? (int)bias_len : 0;
+  L->bias_dev.reset();
+  if (L->bias_len > 0) {
+    WV_TRY(L->bias_dev.alloc(bias_len * sizeof(double)));
+    WV_HIP(hipMemcpyAsync(L->bias_dev.p, bias, bias_len * sizeof(double), hipMemcpyHostToDevice,
+                          st));
+    WV_HIP(hipStreamSynchronize(st));
+  }
+  return Status::ok();
+}
+
+Status dense_build(int in, int out, int act, int dtype, int scheme, const float* W_host,
+                   const double* bias, size_t bias_len, DenseLayer* L, hipStream_t st) {
+  if (!L) return Status::err(kInvalid, "dense: null layer");
+  if (in <= 0 || out <= 0) return Status::err(kInvalid, "dense: bad dims");
+  if (!act_valid(act)) return Status::err(kInvalid, "dense: bad activation");
+  WV_TRY(check_dtype_scheme(dtype, scheme));
+  L->in = in, L->out = out, L->act = act;
+  L->store.dtype = dtype, L->store.scheme = scheme, L->store.rows = out, L->store.cols = in;
+  const int64_t n = (int64_t)in * out;
+  DevBuf dW, raw;
+  WV_TRY(dW.alloc((size_t)n * sizeof(float)));
+  if (W_host) {
+    WV_HIP(hipMemcpyAsync(dW.p, W_host, (size_t)n * sizeof(float), hipMemcpyHostToDevice, st));
+  } else {
+    WV_HIP(hipMemsetAsync(dW.p, 0, (size_t)n * sizeof(float), st));
+  }
+  WV_TRY(raw.alloc(dtype == kFP4 ? (size_t)((n + 1) / 2) : (size_t)n));
+  WV_TRY(quantize_to_device(dW.as<float>(), dtype, scheme, out, in, &L->dev, raw.as<uint8_t>(), st));
+  WV_TRY(download_store(L, raw.as<uint8_t>(), st));
+  return upload_bias(L, bias, bias_len, st);
+}
+
+Status dense_build_from_store(int in, int out, int act, const WeightStore& store, DenseLayer* L,
+                              hipStream_t st) {
+  if (!L) return Status::err(kInvalid, "dense: null layer");
+  if (in <= 0 || out <= 0 || store.rows != out || store.cols != in)
+    return Status::err(kInvalid, "dense: store shape mismatch");
+  if (!act_valid(act)) return Status::err(kInvalid, "dense: bad activation");
+  WV_TRY(check_dtype_scheme(store.dtype, store.scheme));
+  const int64_t n = (int64_t)in * out;
+  const size_t nbytes = store.dtype == kFP4 ? (size_t)((n + 1) / 2) : (size_t)n;
+  if (store.native.size() != nbytes) return Status::err(kInvalid, "dense: native payload length");
+  const int nb = (in + 31) / 32;
+  if (store.scheme == kSchemeBlock32 && store.blk_exp.size() != (size_t)out * nb)
+    return Status::err(kInvalid, "dense: block scale length");
+  if ((store.scheme == kSchemeRow || store.scheme == kSchemeTensor) &&
+      store.row_scale.size() != (size_t)out)
+    return Status::err(kInvalid, "dense: row scale length");
+  L->in = in, L->out = out, L->act = act;
+  L->store = store;
+  DevBuf raw, sc, blk;
+  WV_TRY(raw.alloc(nbytes));
+  WV_HIP(hipMemcpyAsync(raw.p, store.native.data(), nbytes, hipMemcpyHostToDevice, st));
+  const float* d_sc = nullptr;
+  if (!store.row_scale.empty()) {
+    WV_TRY(sc.alloc(store.row_scale.size() * sizeof(float)));
+    WV_HIP(hipMemcpyAsync(sc.p, store.row_scale.data(), store.row_scale.size() * sizeof(float),
+                          hipMemcpyHostToDevice, st));
+    d_sc = sc.as<float>();
+  }
+  const uint8_t* d_blk = nullptr;
+  if (store.scheme == kSchemeBlock32) {
+    WV_TRY(blk.alloc(store.blk_exp.size()));
+    WV_HIP(hipMemcpyAsync(blk.p, store.blk_exp.data(), store.blk_exp.size(), hipMemcpyHostToDevice,
+                          st));
+    d_blk = blk.as<uint8_t>();
+  }
+  WV_TRY(relayout_to_device(raw.as<uint8_t>(), store.dtype, store.scheme, out, in, d_sc, d_blk,
+                            &L->dev, st));
+  if (store.row_scale.empty()) L->store.row_scale.assign((size_t)out, 1.0f);
+  return upload_bias(L, store.bias.data(), store.bias.size(), st);
+}
+
+int gemv_batch_limit() { return 1 << 30; }
+
+static int rows_per_group(int rows) {
+  const int cu = cu_count() > 0 ? cu_count() : 256;
+  if (rows >= 16 * 2 * cu) return 16;
+  if (rows >= 8 * 2 * cu) return 8;
+  return 4;
+}
+
+static GemvArgs gemv_args(const DenseLayer& L, const float* x, int x_stride) {
+  GemvArgs a;
+  a.codes[0] = L.dev.d_codes();
+  a.scale[0] = L.dev.d_scale();
+  a.blk[0] = L.dev.d_blk();
+  a.pitch = L.dev.pitch;
+  a.nblk = L.dev.nblk;
+  a.kpad = L.dev.kpad;
+  a.cols = L.in;
+  a.rows = L.out;
+  a.x = x;
+  a.x_stride = x_stride;
+  a.out_stride = L.out;
+  a.act = L.act;
+  a.need_epi = L.need_epi() ? 1 : 0;
+  a.bias = L.bias_dev.as<const double>();
+  a.bias_len = L.bias_len;
+  return a;
+}
+
+size_t dense_workspace_bytes(const DenseLayer&, int) { return 0; }
+
+Status dense_forward(const DenseLayer& L, int batch, const float* x, float* pre, float* post,
+                     Workspace*, hipStream_t st) {
+  if (batch <= 0 || !x || !pre) return Status::err(kInvalid, "dense forward: bad args");
+  if (L.need_epi() && !post) return Status::err(kInvalid, "dense forward: post needed");
+  GemvArgs a = gemv_args(L, x, L.in);
+  a.pre = pre;
+  a.post = post;
+  return launch_gemv(a, L.dev.dtype, L.dev.scheme == kSchemeBlock32, batch,
+                     rows_per_group(L.out), st);
+}
+
+// ---------------------------------------------------------------------------
+Status swiglu_build(int in, int inter, int dtype, int scheme, const float* G, const float* U,
+                    const float* D, SwiGLULayer* L, hipStream_t st) {
+  if (in <= 0 || inter <= 0)
+    return Status::err(kInvalid, "swiglu: need InputDim>0 and IntermediateDim>0");
+  L->in = in, L->inter = inter;
+  WV_TRY(dense_build(in, inter, kLinear, dtype, scheme, G, nullptr, 0, &L->gate, st));
+  WV_TRY(dense_build(in, inter, kLinear, dtype, scheme, U, nullptr, 0, &L->up, st));
+  WV_TRY(dense_build(inter, in, kLinear, dtype, scheme, D, nullptr, 0, &L->down, st));
+  return Status::ok();
+}
+
+size_t swiglu_workspace_bytes(const SwiGLULayer&, int) { return 0; }
+
+Status swiglu_forward(const SwiGLULayer& L, int rows, const float* x, float* h, float* y,
+                      Workspace* ws, hipStream_t st) {
+  if (rows <= 0 || !x || !h || !y) return Status::err(kInvalid, "swiglu forward: bad args");
+  GemvArgs a = gemv_args(L.gate, x, L.in);
+  a.mats = 2;
+  a.codes[1] = L.up.dev.d_codes();
+  a.scale[1] = L.up.dev.d_scale();
+  a.blk[1] = L.up.dev.d_blk();
+  a.pre = h;
+  a.post = nullptr;
+  a.need_epi = 0;
+  WV_TRY(launch_gemv(a, L.gate.dev.dtype, L.gate.dev.scheme == kSchemeBlock32, rows,
+                     rows_per_group(L.inter), st));
+  return dense_forward(L.down, rows, h, y, nullptr, ws, st);
+}
+
+// ---------------------------------------------------------------------------
+Status mha_validate(MHAConfig* c) {
+  if (c->d_model <= 0 || c->num_heads <= 0)
+    return Status::err(kInvalid, "mha: need DModel>0 and NumHeads>0");
+  if (c->head_dim <= 0) {
+    if (c->d_model % c->num_heads != 0)
+      return Status::err(kInvalid, "mha: HeadDim unset and DModel%NumHeads!=0");
+    c->head_dim = c->d_model / c->num_heads;
+  }
+  if (c->num_kv_heads <= 0) c->num_kv_heads = c->num_heads;
+  if (c->num_heads % c->num_kv_heads != 0)
+    return Status::err(kInvalid, "mha: NumHeads not divisible by NumKVHeads");
+  if (c->max_seq_len <= 0) c->max_seq_len = 512;
+  if (c->mask == 0) c->mask = 1;
+  if (c->rope_theta <= 0) c->rope_theta = 10000.0;
+  if (c->softmax != 0 && c->softmax != 1) return Status::err(kInvalid, "mha: unknown Softmax");
+  return Status::ok();
+}
+
+Status mha_build(const MHAConfig& cfg_in, int dtype, int scheme, const float* Q, const float* K,
+                 const float* V, const float* O, MHALayer* L, hipStream_t st) {
+  MHAConfig cfg = cfg_in;
+  WV_TRY(mha_validate(&cfg));
+  L->cfg = cfg;
+  const int d = cfg.d_model, qd = cfg.q_dim(), kvd = cfg.kv_dim();
+  WV_TRY(dense_build(d, qd, kLinear, dtype, scheme, Q, nullptr, 0, &L->q, st));
+  WV_TRY(dense_build(d, kvd, kLinear, dtype, scheme, K, nullptr, 0, &L->k, st));
+  WV_TRY(dense_build(d, kvd, kLinear, dtype, scheme, V, nullptr, 0, &L->v, st));
+  WV_TRY(dense_build(qd, d, kLinear, dtype, scheme, O, nullptr, 0, &L->o, st));
+  return Status::ok();
+}
+
+size_t mha_workspace_bytes(const MHALayer& L, int batch, int seq) {
+  const size_t t = (size_t)batch * seq;
+  return t * ((size_t)L.cfg.q_dim() + 2 * (size_t)L.cfg.kv_dim()) * sizeof(float);
+}
+
+Status mha_forward(const MHALayer& L, int batch, int seq, const float* x, float* attn, float* y,
+                   Workspace* ws, hipStream_t st) {
+  const MHAConfig& c = L.cfg;
+  if (batch <= 0 || seq <= 0 || !x || !attn || !y || !ws)
+    return Status::err(kInvalid, "mha forward: bad args");
+  if (seq > c.max_seq_len) return Status::err(kInvalid, "mha: seq > MaxSeqLen");
+  const size_t need = mha_workspace_bytes(L, batch, seq);
+  if (ws->a.bytes < need) WV_TRY(ws->a.alloc(need));
+  const int T = batch * seq;
+  float* qb = ws->a.as<float>();
+  float* kb = qb + (size_t)T * c.q_dim();
+  float* vb = kb + (size_t)T * c.kv_dim();
+  WV_TRY(dense_forward(L.q, T, x, qb, nullptr, ws, st));
+  WV_TRY(dense_forward(L.k, T, x, kb, nullptr, ws, st));
+  WV_TRY(dense_forward(L.v, T, x, vb, nullptr, ws, st));
+  AttnArgs a;
+  a.q = qb, a.k = kb, a.v = vb, a.out = attn;
+  a.tokens = T, a.seq = seq, a.heads = c.num_heads, a.kv_heads = c.num_kv_heads;
+  a.hd = c.head_dim, a.msl = c.max_seq_len;
+  a.mask = c.mask, a.window = c.window, a.prefix_len = c.prefix_len;
+  a.window_causal = (c.window_causal || c.mask == 1) ? 1 : 0;
+  a.rope = (c.pos == 0 || c.pos == 3) && c.head_dim / 2 > 0 ? 1 : 0;
+  a.alibi = (c.pos == 2 || c.pos == 3) ? 1 : 0;
+  a.sigmoid = c.softmax == 1 ? 1 : 0;
+  a.rope_theta = c.rope_theta;
+  a.scale = c.scale_override > 0 ? c.scale_override : 1.0 / std::sqrt((double)c.head_dim);
+  WV_TRY(launch_attention(a, st));
+  return dense_forward(L.o, T, attn, y, nullptr, ws, st);
+}
+
+}  // namespace wv

@@ -1,0 +1,93 @@
+// Layer objects of the quantized Dense path: the host weight store, Dense,
+// SwiGLU and MHA layers over device-resident quantized weights.
+#pragma once
+
+#include <vector>
+
+#include "common.h"
+#include "kernels.h"
+#include "runtime.h"
+
+namespace wv {
+
+// Host mirror of the reference WeightStore (include/welvet/weights.hpp:18-51)
+// for FP8/FP4, plus the scale extension. `native` is the reference FormatNone
+// payload; `scale` is the reference's single float (the tensor scale under
+// scheme 1, else 1).
+struct WeightStore {
+  int dtype = 0, scheme = 0, rows = 0, cols = 0;
+  std::vector<uint8_t> native;
+  float scale = 1.0f;
+  std::vector<float> row_scale;   // [rows]
+  std::vector<uint8_t> blk_exp;   // [rows][ceil(cols/32)], scheme 3
+  std::vector<double> bias;
+};
+
+Status check_dtype_scheme(int dtype, int scheme);
+
+// Scratch owned by a session and reused across calls (grown at mount).
+struct Workspace {
+  DevBuf a;  // quantized activations / intermediates
+  DevBuf b;
+  DevBuf c;
+  DevBuf d;
+};
+
+struct DenseLayer {
+  int in = 0, out = 0, act = kLinear;
+  WeightStore store;
+  DeviceWeights dev;
+  DevBuf bias_dev;
+  int bias_len = 0;
+  bool need_epi() const { return act != kLinear || bias_len > 0; }
+};
+
+// Quantizes the host fp32 matrix W_host [out][in] on the device into L.
+Status dense_build(int in, int out, int act, int dtype, int scheme, const float* W_host,
+                   const double* bias, size_t bias_len, DenseLayer* L, hipStream_t st);
+// Builds L from a stored payload (reference FormatNone bytes + scales).
+Status dense_build_from_store(int in, int out, int act, const WeightStore& store, DenseLayer* L,
+                              hipStream_t st);
+
+// Batch rows at or below this go to the GEMV kernels.
+int gemv_batch_limit();
+
+// Device forward: x [batch][in] -> pre/post [batch][out]; queued on st.
+// post may be null when the caller only wants pre (Linear, no bias).
+Status dense_forward(const DenseLayer& L, int batch, const float* x, float* pre, float* post,
+                     Workspace* ws, hipStream_t st);
+// Workspace bytes dense_forward needs for this batch.
+size_t dense_workspace_bytes(const DenseLayer& L, int batch);
+
+struct SwiGLULayer {
+  int in = 0, inter = 0;
+  DenseLayer gate, up, down;
+};
+Status swiglu_build(int in, int inter, int dtype, int scheme, const float* G, const float* U,
+                    const float* D, SwiGLULayer* L, hipStream_t st);
+// x [rows][in] -> h [rows][inter] (pre), y [rows][in] (post).
+Status swiglu_forward(const SwiGLULayer& L, int rows, const float* x, float* h, float* y,
+                      Workspace* ws, hipStream_t st);
+size_t swiglu_workspace_bytes(const SwiGLULayer& L, int rows);
+
+struct MHAConfig {
+  int d_model = 0, num_heads = 0, num_kv_heads = 0, head_dim = 0, max_seq_len = 0;
+  int mask = 1, pos = 0, softmax = 0, window = 0, prefix_len = 0, window_causal = 1;
+  double rope_theta = 10000.0, scale_override = 0.0;
+  int q_dim() const { return num_heads * head_dim; }
+  int kv_dim() const { return num_kv_heads * head_dim; }
+};
+// Fills defaults and validates as src/layers/mha/mha.cpp:55-81.
+Status mha_validate(MHAConfig* c);
+struct MHALayer {
+  MHAConfig cfg;
+  DenseLayer q, k, v, o;
+};
+Status mha_build(const MHAConfig& cfg, int dtype, int scheme, const float* Q, const float* K,
+                 const float* V, const float* O, MHALayer* L, hipStream_t st);
+// x [batch*seq][d] -> attn [batch*seq][q_dim] (pre), y [batch*seq][d] (post).
+Status mha_forward(const MHALayer& L, int batch, int seq, const float* x, float* attn, float* y,
+                   Workspace* ws, hipStream_t st);
+size_t mha_workspace_bytes(const MHALayer& L, int batch, int seq);
+
+}  // namespace wv

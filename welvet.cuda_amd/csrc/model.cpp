@@ -1,0 +1,535 @@
+// WMN1 model sessions: descriptor parsing, device mount and forward.
+//
+// Descriptor layout (reference src/interop/model_session.cpp:319-404,
+// include/welvet/interop/child_wire.hpp:21-55/:95-118/:153-192/:409-421,
+// include/welvet/interop/model_wire.hpp:195-262): little-endian
+//   u32 'WMN1', i32 root, i32 count, i32 dims[4], count children,
+//   root controls, per-child control trees, i32 store count, stores,
+//   and for Grid roots per cell: i32 enabled, remote, tz, ty, tx, tl.
+// Store payload (model_session.cpp:135-153): i32 dtype, rows, cols, f32 scale,
+//   vec<f32> f32, vec<u8> native, vec<f64> bias (vec = i32 count + items).
+// Only the quantized Dense path is served: Dense, NestedStack, SwiGLU and MHA
+// children with FP8/FP4 stores; anything else is reported as code 2/3.
+#include "model.h"
+
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <stdexcept>
+#include <tuple>
+
+#include "codec.h"
+
+namespace wv {
+namespace {
+
+struct Reader {
+  const uint8_t* p;
+  size_t left;
+  int depth = 0;
+  template <class T>
+  bool read(T* out, size_t n) {
+    if (n > left / sizeof(T)) return false;
+    const size_t bytes = n * sizeof(T);
+    if (bytes) std::memcpy(out, p, bytes);
+    p += bytes;
+    left -= bytes;
+    return true;
+  }
+  template <class T>
+  T one() {
+    T v{};
+    if (!read(&v, 1)) throw std::invalid_argument("truncated descriptor");
+    return v;
+  }
+  template <class T>
+  std::vector<T> vec() {
+    const int32_t n = one<int32_t>();
+    if (n < 0 || (size_t)n > left / sizeof(T)) throw std::invalid_argument("invalid vector length");
+    std::vector<T> v((size_t)n);
+    if (!read(v.data(), v.size())) throw std::invalid_argument("short vector");
+    return v;
+  }
+};
+
+void require(bool ok, const char* why) {
+  if (!ok) throw std::invalid_argument(why);
+}
+
+struct StatusError : std::runtime_error {
+  int code;
+  explicit StatusError(const Status& s) : std::runtime_error(s.message), code(s.code) {}
+};
+void good(const Status& s) {
+  if (!s) throw StatusError(s);
+}
+
+size_t count_of(Reader& r, int64_t n, bool allow_empty) {
+  require(n >= 0 && (allow_empty || n > 0) && n <= (int64_t(1) << 26) &&
+              (size_t)n <= r.left / 4,
+          "invalid model payload size");
+  return (size_t)n;
+}
+
+std::vector<float> floats(Reader& r, int64_t n) {
+  std::vector<float> v(count_of(r, n, false));
+  require(r.read(v.data(), v.size()), "short weights");
+  return v;
+}
+
+void read_child(Reader& r, ModelNode* c) {
+  require(++r.depth <= 64, "model nesting exceeds 64");
+  c->kind = r.one<int32_t>();
+  switch (c->kind) {
+  case 0: break;
+  case 1: {  // Dense: child_wire.hpp:29-55
+    c->in = r.one<int32_t>();
+    c->out = r.one<int32_t>();
+    c->act = r.one<int32_t>();
+    c->dtype = r.one<int32_t>();
+    require(c->in > 0 && c->out > 0, "invalid Dense dims");
+    c->W = floats(r, (int64_t)c->out * c->in);
+    const uint32_t bl = r.one<uint32_t>();
+    std::vector<double> bias(count_of(r, bl, true));
+    require(r.read(bias.data(), bias.size()), "short bias");
+    WeightStore s;
+    s.rows = c->out, s.cols = c->in, s.bias = std::move(bias);
+    c->stores.push_back(std::move(s));
+    break;
+  }
+  case 4: {  // SwiGLU: child_wire.hpp:95-118
+    c->in = r.one<int32_t>();
+    c->inter = r.one<int32_t>();
+    c->dtype = r.one<int32_t>();
+    require(c->in > 0 && c->inter > 0, "invalid SwiGLU dims");
+    const int64_t n = (int64_t)c->in * c->inter;
+    std::vector<float> packed = floats(r, 3 * n);
+    c->W.assign(packed.begin(), packed.begin() + n);
+    c->W2.assign(packed.begin() + n, packed.begin() + 2 * n);
+    c->W3.assign(packed.begin() + 2 * n, packed.end());
+    for (int i = 0; i < 3; ++i) {
+      WeightStore s;
+      s.rows = i < 2 ? c->inter : c->in;
+      s.cols = i < 2 ? c->in : c->inter;
+      c->stores.push_back(std::move(s));
+    }
+    break;
+  }
+  case 7: {  // MHA: child_wire.hpp:153-192
+    const int seq = r.one<int32_t>();
+    MHAConfig& g = c->mha_cfg;
+    g.d_model = r.one<int32_t>();
+    g.num_heads = r.one<int32_t>();
+    g.num_kv_heads = r.one<int32_t>();
+    g.head_dim = r.one<int32_t>();
+    const int msl = r.one<int32_t>();
+    g.mask = r.one<int32_t>();
+    g.pos = r.one<int32_t>();
+    c->dtype = r.one<int32_t>();
+    require(g.num_heads > 0 && g.d_model > 0 && g.num_kv_heads >= 0 && g.head_dim >= 0,
+            "invalid MHA dims");
+    const int hd = g.head_dim > 0 ? g.head_dim : g.d_model / g.num_heads;
+    const int kvh = g.num_kv_heads > 0 ? g.num_kv_heads : g.num_heads;
+    g.max_seq_len = msl > 0 ? msl : seq;
+    const int qd = g.num_heads * hd, kvd = kvh * hd;
+    c->W = floats(r, (int64_t)qd * g.d_model);
+    c->W2 = floats(r, (int64_t)kvd * g.d_model);
+    c->W3 = floats(r, (int64_t)kvd * g.d_model);
+    c->W4 = floats(r, (int64_t)g.d_model * qd);
+    good(mha_validate(&g));
+    const int rows[4] = {qd, kvd, kvd, g.d_model}, cols[4] = {g.d_model, g.d_model, g.d_model, qd};
+    for (int i = 0; i < 4; ++i) {
+      WeightStore s;
+      s.rows = rows[i], s.cols = cols[i];
+      c->stores.push_back(std::move(s));
+    }
+    break;
+  }
+  case 19: {  // NestedStack: child_wire.hpp:409-421
+    const int32_t n = r.one<int32_t>();
+    require(n > 0 && n <= 4096, "invalid nested count");
+    c->nested.resize((size_t)n);
+    for (auto& ch : c->nested) read_child(r, &ch);
+    break;
+  }
+  default:
+    --r.depth;
+    throw StatusError(Status::err(kGap, "gap? model child kind " + std::to_string(c->kind) +
+                                            " is outside the quantized Dense path"));
+  }
+  --r.depth;
+}
+
+// Cameral training controls (model_wire.hpp:195-253): parsed for framing and
+// validation; they carry no forward semantics.
+void skip_controls(Reader& r) {
+  int32_t n = r.one<int32_t>();
+  require(n >= 0 && n <= 4096, "invalid controls");
+  for (int i = 0; i < n; ++i) {
+    const int32_t m = r.one<int32_t>();
+    require(m >= 0 && m <= 33, "invalid train mode");
+  }
+  n = r.one<int32_t>();
+  require(n >= 0 && n <= 4096, "invalid controls");
+  for (int i = 0; i < n; ++i) (void)r.one<double>();
+  (void)r.one<double>(), (void)r.one<double>(), (void)r.one<double>();
+  const int32_t present = r.one<int32_t>();
+  if (!present) return;
+  (void)r.one<int32_t>();
+  (void)r.one<double>();
+  const int32_t when = r.one<int32_t>();
+  require(when >= 0 && when <= 3, "invalid sync timing");
+  n = r.one<int32_t>();
+  require(n >= 0 && n <= 4096, "invalid controls");
+  for (int i = 0; i < n; ++i) (void)r.one<double>();
+  n = r.one<int32_t>();
+  require(n >= 0 && n <= 4096, "invalid controls");
+  for (int g = 0; g < n; ++g) {
+    const int32_t cnt = r.one<int32_t>();
+    require(cnt >= 0 && cnt <= 4096, "invalid controls");
+    for (int i = 0; i < cnt; ++i) (void)r.one<int32_t>();
+  }
+  n = r.one<int32_t>();
+  require(n >= 0 && n <= 4096, "invalid controls");
+  for (int i = 0; i < 6 * n; ++i) (void)r.one<int32_t>();
+}
+
+void skip_control_tree(Reader& r, const ModelNode& c) {
+  skip_controls(r);
+  for (const auto& ch : c.nested) skip_control_tree(r, ch);
+}
+
+void collect(ModelNode& c, std::vector<WeightStore*>* out) {
+  for (auto& s : c.stores) out->push_back(&s);
+  for (auto& ch : c.nested) collect(ch, out);
+}
+
+void read_store(Reader& r, WeightStore* s) {
+  const int dt = r.one<int32_t>(), rows = r.one<int32_t>(), cols = r.one<int32_t>();
+  const float scale = r.one<float>();
+  require(dt >= 0 && dt <= 33 && rows == s->rows && cols == s->cols && std::isfinite(scale),
+          "native store metadata mismatch");
+  auto f = r.vec<float>();
+  auto raw = r.vec<uint8_t>();
+  auto bias = r.vec<double>();
+  if (dt != kE4M3 && dt != kE5M2 && dt != kFP4)
+    throw StatusError(Status::err(kUnsupported, "model store dtype " + std::to_string(dt) +
+                                                    " is outside the FP8/FP4 path"));
+  const int64_t n = (int64_t)rows * cols;
+  require(f.empty() && raw.size() == (dt == kFP4 ? (size_t)((n + 1) / 2) : (size_t)n),
+          "native store payload length mismatch");
+  s->dtype = dt;
+  s->scheme = kSchemeRef;
+  s->scale = scale;
+  s->native = std::move(raw);
+  s->row_scale.assign((size_t)rows, 1.0f);
+  s->blk_exp.clear();
+  s->bias = std::move(bias);
+}
+
+void build(ModelNode& c, int scheme, hipStream_t st) {
+  switch (c.kind) {
+  case 1: {
+    c.dense = std::make_unique<DenseLayer>();
+    const WeightStore& s = c.stores[0];
+    if (scheme == kSchemeRef) {
+      good(dense_build_from_store(c.in, c.out, c.act, s, c.dense.get(), st));
+    } else {
+      good(dense_build(c.in, c.out, c.act, s.dtype, scheme, c.W.data(), s.bias.data(),
+                       s.bias.size(), c.dense.get(), st));
+    }
+    break;
+  }
+  case 4: {
+    c.swiglu = std::make_unique<SwiGLULayer>();
+    c.swiglu->in = c.in, c.swiglu->inter = c.inter;
+    DenseLayer* parts[3] = {&c.swiglu->gate, &c.swiglu->up, &c.swiglu->down};
+    const std::vector<float>* ws[3] = {&c.W, &c.W2, &c.W3};
+    for (int i = 0; i < 3; ++i) {
+      const WeightStore& s = c.stores[(size_t)i];
+      if (scheme == kSchemeRef) good(dense_build_from_store(s.cols, s.rows, kLinear, s, parts[i], st));
+      else good(dense_build(s.cols, s.rows, kLinear, s.dtype, scheme, ws[i]->data(), s.bias.data(),
+                            s.bias.size(), parts[i], st));
+    }
+    break;
+  }
+  case 7: {
+    c.mha = std::make_unique<MHALayer>();
+    c.mha->cfg = c.mha_cfg;
+    DenseLayer* parts[4] = {&c.mha->q, &c.mha->k, &c.mha->v, &c.mha->o};
+    const std::vector<float>* ws[4] = {&c.W, &c.W2, &c.W3, &c.W4};
+    for (int i = 0; i < 4; ++i) {
+      const WeightStore& s = c.stores[(size_t)i];
+      if (scheme == kSchemeRef) good(dense_build_from_store(s.cols, s.rows, kLinear, s, parts[i], st));
+      else good(dense_build(s.cols, s.rows, kLinear, s.dtype, scheme, ws[i]->data(), s.bias.data(),
+                            s.bias.size(), parts[i], st));
+    }
+    break;
+  }
+  case 19:
+    for (auto& ch : c.nested) build(ch, scheme, st);
+    break;
+  default: break;
+  }
+  // fp32 copies are no longer needed once the device holds the codes
+  c.W.clear(), c.W2.clear(), c.W3.clear(), c.W4.clear();
+  c.W.shrink_to_fit(), c.W2.shrink_to_fit(), c.W3.shrink_to_fit(), c.W4.shrink_to_fit();
+}
+
+// Flattens NestedStack children into the op sequence (stack.cpp:38-57).
+void flatten(ModelNode& c, std::vector<ModelNode*>* ops) {
+  if (c.kind == 19) {
+    for (auto& ch : c.nested) flatten(ch, ops);
+  } else if (c.kind != 0) {
+    ops->push_back(&c);
+  }
+}
+
+struct Tensor {
+  std::vector<int> shape;
+  float* data = nullptr;  // device
+  size_t numel() const {
+    size_t n = 1;
+    for (int d : shape) n *= (size_t)d;
+    return n;
+  }
+};
+
+// Device arena for a forward pass.
+struct Arena {
+  std::vector<DevBuf> bufs;
+  float* get(size_t n) {
+    bufs.emplace_back();
+    good(bufs.back().alloc(n * sizeof(float)));
+    return bufs.back().as<float>();
+  }
+};
+
+// One op (stack.cpp:58ff child_forward) on device tensors; returns post.
+Tensor op_forward(ModelNode& c, const Tensor& in, Arena& ar, Workspace* ws, hipStream_t st) {
+  Tensor out;
+  switch (c.kind) {
+  case 1: {
+    require(in.shape.size() == 2, "dense: input shape need [batch,in]");
+    require(in.shape[1] == c.in, "dense: input width mismatch");
+    const int b = in.shape[0];
+    out.shape = {b, c.out};
+    out.data = ar.get(out.numel());
+    float* pre = c.dense->need_epi() ? ar.get(out.numel()) : nullptr;
+    if (pre) good(dense_forward(*c.dense, b, in.data, pre, out.data, ws, st));
+    else good(dense_forward(*c.dense, b, in.data, out.data, nullptr, ws, st));
+    break;
+  }
+  case 4: {
+    int rows = 0;
+    if (in.shape.size() == 2) rows = in.shape[0], require(in.shape[1] == c.in, "swiglu: width != InputDim");
+    else if (in.shape.size() == 3) rows = in.shape[0] * in.shape[1], require(in.shape[2] == c.in, "swiglu: last dim != InputDim");
+    else require(false, "swiglu: need [batch,in] or [batch,seq,in]");
+    out.shape = in.shape;
+    out.data = ar.get(out.numel());
+    float* h = ar.get((size_t)rows * c.inter);
+    good(swiglu_forward(*c.swiglu, rows, in.data, h, out.data, ws, st));
+    break;
+  }
+  case 7: {
+    const MHAConfig& g = c.mha->cfg;
+    int b = 1, s = 0;
+    if (in.shape.size() == 3) b = in.shape[0], s = in.shape[1], require(in.shape[2] == g.d_model, "mha: last dim != d_model");
+    else if (in.shape.size() == 2) s = in.shape[0], require(in.shape[1] == g.d_model, "mha: width != d_model");
+    else require(false, "mha: need [batch,seq,d] or [seq,d]");
+    out.shape = {b, s, g.d_model};
+    out.data = ar.get(out.numel());
+    float* attn = ar.get((size_t)b * s * g.q_dim());
+    good(mha_forward(*c.mha, b, s, in.data, attn, out.data, ws, st));
+    break;
+  }
+  default: require(false, "unsupported op");
+  }
+  return out;
+}
+
+Tensor stack_forward(std::vector<ModelNode>& children, const Tensor& in, Arena& ar, Workspace* ws,
+                     hipStream_t st) {
+  std::vector<ModelNode*> ops;
+  for (auto& c : children) flatten(c, &ops);
+  Tensor cur = in;
+  for (ModelNode* op : ops) cur = op_forward(*op, cur, ar, ws, st);
+  return cur;
+}
+
+}  // namespace
+
+Status model_parse(const uint8_t* data, size_t size, int scheme, Model* m) {
+  try {
+    require(data && size >= 28 && size <= (1u << 28), "invalid mount arguments");
+    if (scheme < 0 || scheme > 3) return Status::err(kInvalid, "backend (scale scheme) must be 0..3");
+    Reader r{data, size};
+    require(r.one<uint32_t>() == 0x314e4d57u, "unsupported model descriptor version");
+    m->root = r.one<int32_t>();
+    const int count = r.one<int32_t>();
+    require(m->root >= 0 && m->root <= 2 && count > 0 && count <= 4096, "invalid model root/count");
+    if (m->root == 1) return Status::err(kGap, "gap? Parallel model root is outside the quantized Dense path");
+    for (int& d : m->dims) d = r.one<int32_t>();
+    m->children.resize((size_t)count);
+    for (auto& c : m->children) read_child(r, &c);
+    skip_controls(r);
+    for (auto& c : m->children) skip_control_tree(r, c);
+    std::vector<WeightStore*> stores;
+    for (auto& c : m->children) collect(c, &stores);
+    require(r.one<int32_t>() == (int)stores.size(), "store count mismatch");
+    for (WeightStore* s : stores) read_store(r, s);
+    if (m->root == 2) {
+      int64_t n = 1;
+      for (int d : m->dims) {
+        require(d > 0 && d <= 4096 && n <= 4096 / d, "invalid grid dimensions");
+        n *= d;
+      }
+      require(n == count, "grid cell count mismatch");
+      m->cells.resize((size_t)count);
+      for (int i = 0; i < count; ++i) {
+        GridCell& g = m->cells[(size_t)i];
+        g.enabled = r.one<int32_t>();
+        require(!g.enabled || m->children[(size_t)i].kind != 0, "enabled grid cell has no operation");
+        g.remote = r.one<int32_t>() != 0;
+        g.tz = r.one<int32_t>(), g.ty = r.one<int32_t>(), g.tx = r.one<int32_t>(), g.tl = r.one<int32_t>();
+        if (g.remote)
+          require(g.tz >= 0 && g.tz < m->dims[0] && g.ty >= 0 && g.ty < m->dims[1] && g.tx >= 0 &&
+                      g.tx < m->dims[2] && g.tl >= 0 && g.tl < m->dims[3],
+                  "invalid remote link");
+      }
+    }
+    require(r.left == 0, "trailing descriptor bytes");
+    m->scheme = scheme;
+    return Status::ok();
+  } catch (const StatusError& e) {
+    return Status::err(e.code, e.what());
+  } catch (const std::invalid_argument& e) {
+    return Status::err(kInvalid, e.what());
+  } catch (const std::exception& e) {
+    return Status::err(kInternal, e.what());
+  }
+}
+
+Status model_build(Model* m, hipStream_t st) {
+  try {
+    for (auto& c : m->children) build(c, m->scheme, st);
+    return Status::ok();
+  } catch (const StatusError& e) {
+    return Status::err(e.code, e.what());
+  } catch (const std::invalid_argument& e) {
+    return Status::err(kInvalid, e.what());
+  } catch (const std::exception& e) {
+    return Status::err(kInternal, e.what());
+  }
+}
+
+Status model_forward(Model& m, const std::vector<int>& in_shape, const float* x,
+                     std::vector<int>* out_shape, float* y, size_t y_cap, hipStream_t st) {
+  try {
+    Arena ar;
+    Workspace ws;
+    Tensor in;
+    in.shape = in_shape;
+    in.data = const_cast<float*>(x);
+    Tensor out;
+    if (m.root == 0) {
+      out = stack_forward(m.children, in, ar, &ws, st);
+    } else {
+      // volume_dense (runtime/forward.cpp:98-156): cells in hop order
+      // (z, y, x, l), disabled cells skipped, a remote link reads the post of
+      // its target cell recorded earlier in this pass.
+      const int L = m.dims[3], C = m.dims[2], R = m.dims[1];
+      std::map<int, Tensor> posts;
+      Tensor cur = in;
+      bool any = false;
+      for (size_t i = 0; i < m.children.size(); ++i) {
+        const GridCell& g = m.cells[i];
+        if (!g.enabled) continue;
+        Tensor src = cur;
+        if (g.remote) {
+          const int t = ((g.tz * R + g.ty) * C + g.tx) * L + g.tl;
+          auto it = posts.find(t);
+          require(it != posts.end(), "runtime.forward: remote hop has no recorded activation");
+          src = it->second;
+        }
+        std::vector<ModelNode> one;
+        Tensor post;
+        ModelNode& c = m.children[i];
+        if (c.kind == 19) post = stack_forward(c.nested, src, ar, &ws, st);
+        else post = op_forward(c, src, ar, &ws, st);
+        posts[(int)i] = post;
+        cur = post;
+        any = true;
+      }
+      require(any, "runtime.forward: grid has no enabled cells with ops");
+      out = cur;
+    }
+    *out_shape = out.shape;
+    const size_t n = out.numel();
+    if (n > y_cap) return Status::err(kInvalid, "model forward: output buffer too small");
+    WV_HIP(hipMemcpyAsync(y, out.data, n * sizeof(float), hipMemcpyDeviceToDevice, st));
+    WV_HIP(hipStreamSynchronize(st));
+    return Status::ok();
+  } catch (const StatusError& e) {
+    return Status::err(e.code, e.what());
+  } catch (const std::invalid_argument& e) {
+    return Status::err(kInvalid, e.what());
+  } catch (const std::exception& e) {
+    return Status::err(kInternal, e.what());
+  }
+}
+
+namespace {
+void write_store(std::vector<uint8_t>* w, const WeightStore& s) {
+  auto put = [&](const void* p, size_t n) {
+    const uint8_t* b = static_cast<const uint8_t*>(p);
+    w->insert(w->end(), b, b + n);
+  };
+  const int32_t hdr[3] = {s.dtype, s.rows, s.cols};
+  put(hdr, sizeof hdr);
+  put(&s.scale, 4);
+  const int32_t nf = 0;
+  put(&nf, 4);
+  const int32_t nn = (int32_t)s.native.size();
+  put(&nn, 4);
+  put(s.native.data(), s.native.size());
+  const int32_t nb = (int32_t)s.bias.size();
+  put(&nb, 4);
+  put(s.bias.data(), s.bias.size() * sizeof(double));
+}
+void collect_layers(const ModelNode& c, std::vector<const WeightStore*>* out) {
+  switch (c.kind) {
+  case 1: out->push_back(&c.dense->store); break;
+  case 4:
+    out->push_back(&c.swiglu->gate.store), out->push_back(&c.swiglu->up.store),
+        out->push_back(&c.swiglu->down.store);
+    break;
+  case 7:
+    out->push_back(&c.mha->q.store), out->push_back(&c.mha->k.store),
+        out->push_back(&c.mha->v.store), out->push_back(&c.mha->o.store);
+    break;
+  case 19:
+    for (const auto& ch : c.nested) collect_layers(ch, out);
+    break;
+  default: break;
+  }
+}
+}  // namespace
+
+Status model_export(const Model& m, std::vector<uint8_t>* out) {
+  std::vector<const WeightStore*> stores;
+  for (const auto& c : m.children) collect_layers(c, &stores);
+  out->clear();
+  const uint32_t magic = 0x3153574eu;
+  out->insert(out->end(), reinterpret_cast<const uint8_t*>(&magic),
+              reinterpret_cast<const uint8_t*>(&magic) + 4);
+  const int32_t n = (int32_t)stores.size();
+  out->insert(out->end(), reinterpret_cast<const uint8_t*>(&n), reinterpret_cast<const uint8_t*>(&n) + 4);
+  for (const WeightStore* s : stores) write_store(out, *s);
+  const int32_t extras = 0;
+  out->insert(out->end(), reinterpret_cast<const uint8_t*>(&extras),
+              reinterpret_cast<const uint8_t*>(&extras) + 4);
+  return Status::ok();
+}
+
+}  // namespace wv

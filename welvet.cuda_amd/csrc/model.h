@@ -1,0 +1,62 @@
+// Persistent model sessions over the WMN1 descriptor (Stack and Grid roots).
+#pragma once
+
+#include <memory>
+#include <vector>
+
+#include "layers.h"
+
+namespace wv {
+
+// One child of a Stack / one Grid cell (reference stack::Kind values,
+// include/welvet/stack.hpp:50-77): 0 None, 1 Dense, 4 SwiGLU, 7 MHA,
+// 19 NestedStack.
+struct ModelNode {
+  int kind = 0;
+  // Dense
+  int in = 0, out = 0, act = kLinear, dtype = 0;
+  std::vector<float> W;  // child fp32 weights (the store payload overrides)
+  // SwiGLU
+  int inter = 0;
+  // MHA
+  MHAConfig mha_cfg;
+  std::vector<float> W2, W3, W4;  // Up/Down or K/V/O
+  std::vector<ModelNode> nested;
+  // stores in collect order (Dense: 1, SwiGLU: 3, MHA: 4)
+  std::vector<WeightStore> stores;
+  // built layers
+  std::unique_ptr<DenseLayer> dense;
+  std::unique_ptr<SwiGLULayer> swiglu;
+  std::unique_ptr<MHALayer> mha;
+};
+
+struct GridCell {
+  int enabled = 0, remote = 0, tz = 0, ty = 0, tx = 0, tl = 0;
+};
+
+struct Model {
+  int root = 0;  // 0 Stack, 2 Grid
+  int dims[4] = {1, 1, 1, 1};
+  std::vector<ModelNode> children;  // Stack children or Grid cells in hop order
+  std::vector<GridCell> cells;
+  int scheme = 0;
+};
+
+// Parses and validates a WMN1 descriptor (src/interop/model_session.cpp:
+// 319-404) without touching the device.
+Status model_parse(const uint8_t* data, size_t size, int scheme, Model* m);
+// Mounts the parsed weights on the device. scheme 0 uses the stored payloads
+// as they are (reference behaviour); schemes 1-3 re-quantize each child's
+// fp32 weights.
+Status model_build(Model* m, hipStream_t st);
+
+// Forward over device buffers. x: [rows][width]; y: output; returns the
+// output shape in out_shape. (runtime/forward.cpp:98-156 for Grid,
+// stack/stack.cpp:470-494 for Stack.)
+Status model_forward(Model& m, const std::vector<int>& in_shape, const float* x,
+                     std::vector<int>* out_shape, float* y, size_t y_cap, hipStream_t st);
+
+// NWS1 snapshot of all stores (model_session.cpp:523-550).
+Status model_export(const Model& m, std::vector<uint8_t>* out);
+
+}  // namespace wv

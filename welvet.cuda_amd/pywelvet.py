@@ -1,0 +1,525 @@
+"""Python binding of libwelvet.so (the C ABI in include/welvet_c.h).
+
+Thin ctypes layer used by the tests, the smoke check and the benchmark:
+  * `lib()` loads the in-tree libwelvet.so (built by welvet.cuda_amd/Makefile)
+    and declares every entry point's signature;
+  * `Hip` reaches the HIP runtime that libwelvet.so itself links, for device
+    buffers, streams and events (no second runtime is loaded);
+  * `normal()` is the seeded synthetic-data generator (splitmix64 +
+    Box-Muller in f64), so inputs are identical across runs and machines.
+No computation happens here: every numeric result comes from the library.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libwelvet.so")
+
+E4M3, E5M2, FP4 = 4, 5, 16
+SCHEME_REF, SCHEME_TENSOR, SCHEME_ROW, SCHEME_BLOCK32 = 0, 1, 2, 3
+LINEAR, RELU, SILU, GELU, TANH, SIGMOID, LEAKY, RELU2 = -1, 0, 1, 2, 3, 4, 5, 6
+
+
+class Status(ctypes.Structure):
+    _fields_ = [("code", ctypes.c_int32), ("message", ctypes.c_char * 256)]
+
+
+class Blob(ctypes.Structure):
+    _fields_ = [("data", ctypes.POINTER(ctypes.c_uint8)), ("size", ctypes.c_size_t)]
+
+
+class WelvetError(RuntimeError):
+    def __init__(self, status):
+        self.code = status.code
+        super().__init__(f"welvet status {status.code}: {status.message.decode(errors='replace')}")
+
+
+_LIB = None
+OUT_OF_PATH = (
+    "welvet_model_train_credit", "welvet_model_dense_proxy", "welvet_model_forward_pair",
+    "welvet_model_backward", "welvet_model_apply_sgd", "welvet_model_train_mse", "welvet_model_sync",
+    "welvet_dense_normalbp_f32", "welvet_rmsnorm_forward_f32", "welvet_rmsnorm_normalbp_f32",
+    "welvet_layernorm_forward_f32", "welvet_layernorm_normalbp_f32", "welvet_softmax_forward_f32",
+    "welvet_softmax_normalbp_f32", "welvet_swiglu_normalbp_f32", "welvet_embedding_forward_f32",
+    "welvet_embedding_normalbp_f32", "welvet_mha_normalbp_f32", "welvet_cnn1_forward_f32",
+    "welvet_cnn1_normalbp_f32", "welvet_cnn2_forward_f32", "welvet_cnn2_normalbp_f32",
+    "welvet_cnn3_forward_f32", "welvet_cnn3_normalbp_f32", "welvet_convt1_forward_f32",
+    "welvet_convt1_normalbp_f32", "welvet_convt2_forward_f32", "welvet_convt2_normalbp_f32",
+    "welvet_convt3_forward_f32", "welvet_convt3_normalbp_f32", "welvet_rnn_forward_f32",
+    "welvet_rnn_normalbp_f32", "welvet_lstm_forward_f32", "welvet_lstm_normalbp_f32",
+    "welvet_sequential_forward_f32", "welvet_sequential_normalbp_f32",
+    "welvet_residual_forward_f32", "welvet_residual_normalbp_f32", "welvet_stack_normalbp_f32",
+    "welvet_mamba_normalbp_f32", "welvet_metacognition_normalbp_f32", "welvet_gdn_normalbp_f32",
+    "welvet_kmeans_normalbp_f32", "welvet_parallel_normalbp_f32", "welvet_mamba_forward_f32",
+    "welvet_metacognition_forward_f32", "welvet_gdn_forward_f32", "welvet_kmeans_forward_f32",
+    "welvet_parallel_forward_f32",
+)
+_i32, _u32, _sz, _f64 = ctypes.c_int32, ctypes.c_uint32, ctypes.c_size_t, ctypes.c_double
+_vp = ctypes.c_void_p
+_fp = ctypes.POINTER(ctypes.c_float)
+_dp = ctypes.POINTER(ctypes.c_double)
+_u8p = ctypes.POINTER(ctypes.c_uint8)
+_i64p = ctypes.POINTER(ctypes.c_int64)
+
+
+def _sig(lib, name, res, args):
+    f = getattr(lib, name)
+    f.restype = res
+    f.argtypes = args
+
+
+def lib():
+    """Loads the in-tree library (raises if it was not built)."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is missing: build it with `make -f welvet.cuda_amd/Makefile`")
+    L = ctypes.CDLL(LIB_PATH, mode=ctypes.RTLD_GLOBAL)
+    _sig(L, "welvet_version", ctypes.c_char_p, [])
+    _sig(L, "welvet_runtime_identity", ctypes.c_char_p, [])
+    _sig(L, "welvet_cuda_init", Status, [])
+    _sig(L, "welvet_cuda_available", _i32, [])
+    _sig(L, "welvet_gaps_count", _i32, [])
+    _sig(L, "welvet_gaps_done", _i32, [])
+    _sig(L, "welvet_dense_forward_f32", Status,
+         [_i32, _i32, _i32, _i32, _i32, _i32, _fp, _dp, _sz, _fp, _fp, _fp])
+    _sig(L, "welvet_dense_mount", Status,
+         [_i32, _i32, _i32, _i32, _i32, _fp, _dp, _sz, ctypes.POINTER(_vp)])
+    _sig(L, "welvet_dense_mount_q", Status,
+         [_i32, _i32, _i32, _i32, _i32, _i32, _fp, _dp, _sz, ctypes.POINTER(_vp)])
+    _sig(L, "welvet_dense_execute", Status, [_vp, _fp, _fp, _fp])
+    _sig(L, "welvet_dense_execute_device", Status, [_vp, _vp, _vp, _vp, _vp])
+    _sig(L, "welvet_dense_export_store", Status,
+         [_vp, _u8p, _sz, ctypes.POINTER(_sz), _fp, _u8p, _fp])
+    _sig(L, "welvet_dense_release", None, [_vp])
+    _sig(L, "welvet_swiglu_forward_f32", Status,
+         [_i32, _i32, _i32, _i32, _i32, _i32, _fp, _fp, _fp, _fp, _fp, _fp])
+    _sig(L, "welvet_swiglu_mount", Status,
+         [_i32, _i32, _i32, _i32, _i32, _i32, _fp, _fp, _fp, ctypes.POINTER(_vp)])
+    _sig(L, "welvet_swiglu_execute", Status, [_vp, _fp, _fp, _fp])
+    _sig(L, "welvet_swiglu_execute_device", Status, [_vp, _vp, _vp, _vp, _vp])
+    _sig(L, "welvet_swiglu_release", None, [_vp])
+    _sig(L, "welvet_mha_forward_f32", Status,
+         [_i32] * 11 + [_fp, _fp, _fp, _fp, _fp, _fp, _fp])
+    _sig(L, "welvet_mha_mount", Status, [_i32] * 11 + [_fp, _fp, _fp, _fp, ctypes.POINTER(_vp)])
+    _sig(L, "welvet_mha_execute", Status, [_vp, _fp, _fp, _fp])
+    _sig(L, "welvet_mha_execute_device", Status, [_vp, _vp, _vp, _vp, _vp])
+    _sig(L, "welvet_mha_release", None, [_vp])
+    _sig(L, "welvet_model_abi_version", _i32, [])
+    _sig(L, "welvet_model_mount", Status, [_u8p, _sz, ctypes.POINTER(_vp)])
+    _sig(L, "welvet_model_mount_q", Status, [_u8p, _sz, _i32, ctypes.POINTER(_vp)])
+    _sig(L, "welvet_model_forward", Status, [_vp, _u8p, _sz, ctypes.POINTER(Blob)])
+    _sig(L, "welvet_model_forward_device", Status, [_vp, _vp, _i32, _i32, _vp, _i32, _vp])
+    _sig(L, "welvet_model_export_weights", Status, [_vp, ctypes.POINTER(Blob)])
+    _sig(L, "welvet_model_release", None, [_vp])
+    _sig(L, "welvet_cuda_blob_free", None, [ctypes.POINTER(Blob)])
+    _sig(L, "welvet_codec_sweep", Status, [_i32, _u32, _u32, _i64p])
+    _sig(L, "welvet_seqmix_kind_name", Status, [_i32, ctypes.c_char_p, _i32])
+    for n in ("welvet_seqmix_mha_kind", "welvet_seqmix_mamba_kind", "welvet_seqmix_gdn_kind"):
+        _sig(L, n, _i32, [])
+    # Entry points outside the quantized Dense path return welvet_status by
+    # value (code 3); ctypes must know the struct return to pass its slot.
+    for n in OUT_OF_PATH:
+        getattr(L, n).restype = Status
+    _LIB = L
+    return L
+
+
+def check(st):
+    if st.code != 0:
+        raise WelvetError(st)
+    return st
+
+
+def fptr(a):
+    return a.ctypes.data_as(_fp) if a is not None else None
+
+
+def dptr(a):
+    return a.ctypes.data_as(_dp) if a is not None else None
+
+
+# --------------------------------------------------------------------------
+def normal(seed, n, std=1.0):
+    """n samples of N(0, std^2) as float32: splitmix64 stream from `seed`,
+    uniforms ((z >> 11) + 0.5) * 2^-53, Box-Muller pairs (cos, sin)."""
+    m = (n + 1) // 2
+    with np.errstate(over="ignore"):
+        k = np.arange(1, 2 * m + 1, dtype=np.uint64)
+        z = np.uint64(seed) + k * np.uint64(0x9E3779B97F4A7C15)
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+        z = z ^ (z >> np.uint64(31))
+    u = ((z >> np.uint64(11)).astype(np.float64) + 0.5) * (2.0 ** -53)
+    u1, u2 = u[0::2], u[1::2]
+    r = np.sqrt(-2.0 * np.log(u1))
+    t = 2.0 * np.pi * u2
+    out = np.empty(2 * m, dtype=np.float64)
+    out[0::2] = r * np.cos(t)
+    out[1::2] = r * np.sin(t)
+    return (out[:n] * std).astype(np.float32)
+
+
+def seed_for(config, cell=0):
+    return 0x5EED0000 + config * 1000 + cell
+
+
+# --------------------------------------------------------------------------
+class Hip:
+    """Device buffers, streams and events from the HIP runtime libwelvet links."""
+
+    H2D, D2H, D2D = 1, 2, 3
+
+    def __init__(self):
+        lib()
+        h = ctypes.CDLL("libamdhip64.so.7")
+        _sig(h, "hipMalloc", ctypes.c_int, [ctypes.POINTER(_vp), _sz])
+        _sig(h, "hipFree", ctypes.c_int, [_vp])
+        _sig(h, "hipMemcpy", ctypes.c_int, [_vp, _vp, _sz, ctypes.c_int])
+        _sig(h, "hipMemset", ctypes.c_int, [_vp, ctypes.c_int, _sz])
+        _sig(h, "hipDeviceSynchronize", ctypes.c_int, [])
+        _sig(h, "hipStreamCreate", ctypes.c_int, [ctypes.POINTER(_vp)])
+        _sig(h, "hipStreamDestroy", ctypes.c_int, [_vp])
+        _sig(h, "hipStreamSynchronize", ctypes.c_int, [_vp])
+        _sig(h, "hipEventCreate", ctypes.c_int, [ctypes.POINTER(_vp)])
+        _sig(h, "hipEventDestroy", ctypes.c_int, [_vp])
+        _sig(h, "hipEventRecord", ctypes.c_int, [_vp, _vp])
+        _sig(h, "hipEventSynchronize", ctypes.c_int, [_vp])
+        _sig(h, "hipEventElapsedTime", ctypes.c_int, [_fp, _vp, _vp])
+        _sig(h, "hipGetErrorString", ctypes.c_char_p, [ctypes.c_int])
+        _sig(h, "hipStreamBeginCapture", ctypes.c_int, [_vp, ctypes.c_int])
+        _sig(h, "hipStreamEndCapture", ctypes.c_int, [_vp, ctypes.POINTER(_vp)])
+        _sig(h, "hipGraphInstantiate", ctypes.c_int,
+             [ctypes.POINTER(_vp), _vp, _vp, ctypes.c_char_p, _sz])
+        _sig(h, "hipGraphLaunch", ctypes.c_int, [_vp, _vp])
+        _sig(h, "hipGraphExecDestroy", ctypes.c_int, [_vp])
+        _sig(h, "hipGraphDestroy", ctypes.c_int, [_vp])
+        self.h = h
+
+    def _ok(self, rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what}: {self.h.hipGetErrorString(rc).decode()}")
+
+    def malloc(self, nbytes):
+        p = _vp()
+        self._ok(self.h.hipMalloc(ctypes.byref(p), max(int(nbytes), 16)), "hipMalloc")
+        return p.value
+
+    def free(self, p):
+        if p:
+            self._ok(self.h.hipFree(_vp(p)), "hipFree")
+
+    def upload(self, arr):
+        arr = np.ascontiguousarray(arr)
+        p = self.malloc(arr.nbytes)
+        self._ok(self.h.hipMemcpy(_vp(p), arr.ctypes.data_as(_vp), arr.nbytes, self.H2D), "H2D")
+        return p
+
+    def download(self, p, shape, dtype=np.float32):
+        out = np.empty(shape, dtype=dtype)
+        self._ok(self.h.hipMemcpy(out.ctypes.data_as(_vp), _vp(p), out.nbytes, self.D2H), "D2H")
+        return out
+
+    def memset(self, p, value, nbytes):
+        self._ok(self.h.hipMemset(_vp(p), value, nbytes), "hipMemset")
+
+    def sync(self):
+        self._ok(self.h.hipDeviceSynchronize(), "hipDeviceSynchronize")
+
+    def stream(self):
+        s = _vp()
+        self._ok(self.h.hipStreamCreate(ctypes.byref(s)), "hipStreamCreate")
+        return s.value
+
+    def stream_sync(self, s):
+        self._ok(self.h.hipStreamSynchronize(_vp(s)), "hipStreamSynchronize")
+
+    def event(self):
+        e = _vp()
+        self._ok(self.h.hipEventCreate(ctypes.byref(e)), "hipEventCreate")
+        return e.value
+
+    def record(self, e, s):
+        self._ok(self.h.hipEventRecord(_vp(e), _vp(s)), "hipEventRecord")
+
+    def capture(self, stream, enqueue):
+        """Records what enqueue() queues on `stream` into an instantiated graph."""
+        self._ok(self.h.hipStreamBeginCapture(_vp(stream), 2), "hipStreamBeginCapture")
+        try:
+            enqueue()
+        finally:
+            g = _vp()
+            rc = self.h.hipStreamEndCapture(_vp(stream), ctypes.byref(g))
+        self._ok(rc, "hipStreamEndCapture")
+        ex = _vp()
+        self._ok(self.h.hipGraphInstantiate(ctypes.byref(ex), g, None, None, 0), "hipGraphInstantiate")
+        self._ok(self.h.hipGraphDestroy(g), "hipGraphDestroy")
+        return ex.value
+
+    def launch(self, graph_exec, stream):
+        self._ok(self.h.hipGraphLaunch(_vp(graph_exec), _vp(stream)), "hipGraphLaunch")
+
+    def graph_free(self, graph_exec):
+        self._ok(self.h.hipGraphExecDestroy(_vp(graph_exec)), "hipGraphExecDestroy")
+
+    def elapsed_ms(self, a, b):
+        self._ok(self.h.hipEventSynchronize(_vp(b)), "hipEventSynchronize")
+        t = ctypes.c_float()
+        self._ok(self.h.hipEventElapsedTime(ctypes.byref(t), _vp(a), _vp(b)), "hipEventElapsedTime")
+        return t.value
+
+
+# --------------------------------------------------------------------------
+class DenseSession:
+    """welvet_dense_mount_q / execute / execute_device / export_store / release."""
+
+    def __init__(self, batch, in_dim, out_dim, act, dtype, scheme, W, bias=None):
+        L = lib()
+        self.batch, self.in_dim, self.out_dim = batch, in_dim, out_dim
+        W = np.ascontiguousarray(W, dtype=np.float32)
+        b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float64)
+        h = _vp()
+        check(L.welvet_dense_mount_q(batch, in_dim, out_dim, act, dtype, scheme, fptr(W), dptr(b),
+                                     0 if b is None else b.size, ctypes.byref(h)))
+        self.h = h
+
+    def execute(self, x):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        pre = np.empty((self.batch, self.out_dim), np.float32)
+        post = np.empty_like(pre)
+        check(lib().welvet_dense_execute(self.h, fptr(x), fptr(pre), fptr(post)))
+        return pre, post
+
+    def execute_device(self, x, pre, post, stream=None):
+        check(lib().welvet_dense_execute_device(self.h, _vp(x), _vp(pre), _vp(post),
+                                                _vp(stream) if stream else None))
+
+    def export_store(self, dtype):
+        n = self.in_dim * self.out_dim
+        cap = n if dtype != FP4 else (n + 1) // 2
+        native = np.zeros(cap, np.uint8)
+        nlen = _sz()
+        rs = np.zeros(self.out_dim, np.float32)
+        blk = np.zeros(self.out_dim * ((self.in_dim + 31) // 32), np.uint8)
+        ts = ctypes.c_float()
+        check(lib().welvet_dense_export_store(self.h, native.ctypes.data_as(_u8p), cap,
+                                              ctypes.byref(nlen), fptr(rs),
+                                              blk.ctypes.data_as(_u8p), ctypes.byref(ts)))
+        return native[: nlen.value], rs, blk, ts.value
+
+    def close(self):
+        if self.h:
+            lib().welvet_dense_release(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class SwiGLUSession:
+    def __init__(self, batch, seq, in_dim, inter, dtype, scheme, G, U, D):
+        L = lib()
+        self.rows, self.in_dim, self.inter = batch * seq, in_dim, inter
+        self._keep = [np.ascontiguousarray(a, dtype=np.float32) for a in (G, U, D)]
+        h = _vp()
+        check(L.welvet_swiglu_mount(batch, seq, in_dim, inter, dtype, scheme,
+                                    *[fptr(a) for a in self._keep], ctypes.byref(h)))
+        self._keep = None
+        self.h = h
+
+    def execute(self, x):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        pre = np.empty((self.rows, self.inter), np.float32)
+        post = np.empty((self.rows, self.in_dim), np.float32)
+        check(lib().welvet_swiglu_execute(self.h, fptr(x), fptr(pre), fptr(post)))
+        return pre, post
+
+    def execute_device(self, x, pre, post, stream=None):
+        check(lib().welvet_swiglu_execute_device(self.h, _vp(x), _vp(pre), _vp(post),
+                                                 _vp(stream) if stream else None))
+
+    def close(self):
+        if self.h:
+            lib().welvet_swiglu_release(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class MHASession:
+    def __init__(self, batch, seq, d_model, heads, kv_heads, head_dim, msl, mask, pos, dtype,
+                 scheme, Q, K, V, O):
+        L = lib()
+        self.batch, self.seq, self.d = batch, seq, d_model
+        hd = head_dim if head_dim > 0 else d_model // heads
+        self.q_dim = heads * hd
+        keep = [np.ascontiguousarray(a, dtype=np.float32) for a in (Q, K, V, O)]
+        h = _vp()
+        check(L.welvet_mha_mount(batch, seq, d_model, heads, kv_heads, head_dim, msl, mask, pos,
+                                 dtype, scheme, *[fptr(a) for a in keep], ctypes.byref(h)))
+        self.h = h
+
+    def execute(self, x):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        T = self.batch * self.seq
+        pre = np.empty((T, self.q_dim), np.float32)
+        post = np.empty((T, self.d), np.float32)
+        check(lib().welvet_mha_execute(self.h, fptr(x), fptr(pre), fptr(post)))
+        return pre, post
+
+    def execute_device(self, x, pre, post, stream=None):
+        check(lib().welvet_mha_execute_device(self.h, _vp(x), _vp(pre), _vp(post),
+                                              _vp(stream) if stream else None))
+
+    def close(self):
+        if self.h:
+            lib().welvet_mha_release(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def dense_forward(batch, in_dim, out_dim, act, dtype, scheme, W, x, bias=None):
+    """welvet_dense_forward_f32 (one shot)."""
+    W = np.ascontiguousarray(W, dtype=np.float32)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float64)
+    pre = np.empty((batch, out_dim), np.float32)
+    post = np.empty_like(pre)
+    check(lib().welvet_dense_forward_f32(batch, in_dim, out_dim, act, dtype, scheme, fptr(W),
+                                         dptr(b), 0 if b is None else b.size, fptr(x), fptr(pre),
+                                         fptr(post)))
+    return pre, post
+
+
+def codec_sweep(dtype, first_chunk=0, n_chunks=4096):
+    out = np.zeros(2 * n_chunks, np.int64)
+    check(lib().welvet_codec_sweep(dtype, first_chunk, n_chunks, out.ctypes.data_as(_i64p)))
+    return out.reshape(n_chunks, 2)
+
+
+# --------------------------------------------------------------- WMN1 -----
+class Wire:
+    """Little-endian writer for WMN1 descriptors and tensors
+    (src/interop/model_session.cpp:101-162 layouts)."""
+
+    def __init__(self):
+        self.parts = []
+
+    def i32(self, *v):
+        self.parts.append(np.asarray(v, dtype="<i4").tobytes())
+
+    def u32(self, *v):
+        self.parts.append(np.asarray(v, dtype="<u4").tobytes())
+
+    def f32(self, arr):
+        self.parts.append(np.ascontiguousarray(arr, dtype="<f4").tobytes())
+
+    def f64(self, arr):
+        self.parts.append(np.ascontiguousarray(arr, dtype="<f8").tobytes())
+
+    def u8(self, arr):
+        self.parts.append(np.ascontiguousarray(arr, dtype=np.uint8).tobytes())
+
+    def bytes(self):
+        return b"".join(self.parts)
+
+
+def dense_child(w, in_dim, out_dim, act, dtype, W, bias=None):
+    w.i32(1, in_dim, out_dim, act, dtype)
+    w.f32(W)
+    b = np.zeros(0) if bias is None else np.asarray(bias, np.float64)
+    w.u32(b.size)
+    if b.size:
+        w.f64(b)
+
+
+def empty_controls(w):
+    # modes, branch_lrs, shadow_coef, surprise_thresh, last_loss, sync present
+    w.i32(0, 0)
+    w.f64([0.0, 0.0, 0.0])
+    w.i32(0)
+
+
+def store_payload(w, dtype, rows, cols, native, scale=1.0, bias=None):
+    w.i32(dtype, rows, cols)
+    w.f32([scale])
+    w.i32(0)  # f32 payload (FP8/FP4 stores have none)
+    w.i32(len(native))
+    w.u8(native)
+    b = np.zeros(0) if bias is None else np.asarray(bias, np.float64)
+    w.i32(b.size)
+    if b.size:
+        w.f64(b)
+
+
+def tensor_bytes(x):
+    w = Wire()
+    w.i32(x.ndim, *x.shape)
+    w.f32(x)
+    return w.bytes()
+
+
+class ModelSession:
+    def __init__(self, descriptor, scheme=0):
+        L = lib()
+        buf = np.frombuffer(descriptor, dtype=np.uint8).copy()
+        h = _vp()
+        if scheme:
+            check(L.welvet_model_mount_q(buf.ctypes.data_as(_u8p), buf.size, scheme, ctypes.byref(h)))
+        else:
+            check(L.welvet_model_mount(buf.ctypes.data_as(_u8p), buf.size, ctypes.byref(h)))
+        self.h = h
+
+    def forward(self, x):
+        data = np.frombuffer(tensor_bytes(np.ascontiguousarray(x, np.float32)), np.uint8).copy()
+        blob = Blob()
+        check(lib().welvet_model_forward(self.h, data.ctypes.data_as(_u8p), data.size,
+                                         ctypes.byref(blob)))
+        try:
+            raw = bytes(ctypes.cast(blob.data, ctypes.POINTER(ctypes.c_uint8 * blob.size)).contents)
+        finally:
+            lib().welvet_cuda_blob_free(ctypes.byref(blob))
+        rank = int(np.frombuffer(raw[:4], "<i4")[0])
+        shape = tuple(np.frombuffer(raw[4:4 + 4 * rank], "<i4").tolist())
+        count = int(np.frombuffer(raw[4 + 4 * rank:8 + 4 * rank], "<i4")[0])
+        data = np.frombuffer(raw[8 + 4 * rank:], "<f4")
+        assert data.size == count
+        return data.reshape(shape)
+
+    def forward_device(self, x, batch, width, y, y_cap, stream=None):
+        check(lib().welvet_model_forward_device(self.h, _vp(x), batch, width, _vp(y), y_cap,
+                                                _vp(stream) if stream else None))
+
+    def export(self):
+        blob = Blob()
+        check(lib().welvet_model_export_weights(self.h, ctypes.byref(blob)))
+        try:
+            return bytes(ctypes.cast(blob.data, ctypes.POINTER(ctypes.c_uint8 * blob.size)).contents)
+        finally:
+            lib().welvet_cuda_blob_free(ctypes.byref(blob))
+
+    def close(self):
+        if self.h:
+            lib().welvet_model_release(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
