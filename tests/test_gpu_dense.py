@@ -4,9 +4,14 @@ Parity reference: the oracle quantizes W with the same rules, dequantizes to
 f32 and runs the reference Dense contract (f64 serial accumulation, bias in
 f64, activation; src/cuda/kernels.cu:130-161). Tolerances, stated per test:
   * contract: relative L2 error <= 1e-3;
-  * GEMV path (fp32 FMA of exactly-decoded codes): <= 1e-5, because the only
-    difference from the oracle is fp32 accumulation order;
-  * integer-exact cases: bit-exact (every partial sum is an exact f32).
+  * batch 1, VALU GEMV (fp32 FMA of exactly-decoded codes): <= 1e-5, the only
+    difference from the oracle being fp32 accumulation order;
+  * batches on the scaled matrix cores: <= 5e-5. The activations are split
+    into E4M3 terms (residual ~4e-7) and the f8f6f4 MFMA accumulates with
+    about 2^-16.5 relative precision (measured ~1.1e-5 at K=4096 even when the
+    activations are exact in one term);
+  * integer-exact cases: bit-exact (every partial sum is exact in f32 and in
+    the matrix core).
 """
 import numpy as np
 import pytest
@@ -15,6 +20,11 @@ pytestmark = pytest.mark.gpu
 
 TOL_CONTRACT = 1e-3
 TOL_GEMV = 1e-5
+TOL_MFMA = 5e-5
+
+
+def tol(batch):
+    return TOL_GEMV if batch == 1 else TOL_MFMA
 
 
 def rel_l2(a, b):
@@ -72,7 +82,7 @@ def test_dense_matches_oracle(gpu, oracle, dt, scheme, rows, cols, batch):
     pre, post = run(gpu, dt, scheme, W, x)
     o_pre, o_post = oracle_dense(oracle, dt, scheme, W, x)
     e = rel_l2(pre, o_pre)
-    assert e <= TOL_GEMV and e <= TOL_CONTRACT, e
+    assert e <= tol(batch) and e <= TOL_CONTRACT, e
     assert np.array_equal(pre, post)
 
 
@@ -85,8 +95,8 @@ def test_bias_and_activation_epilogue(gpu, oracle, act):
     bias = rng.standard_normal(30)  # shorter than out: rows >= 30 get no bias
     pre, post = run(gpu, 4, 2, W, x, act, bias)
     o_pre, o_post = oracle_dense(oracle, 4, 2, W, x, act, bias)
-    assert rel_l2(pre, o_pre) <= TOL_GEMV
-    assert rel_l2(post, o_post) <= TOL_GEMV
+    assert rel_l2(pre, o_pre) <= TOL_MFMA
+    assert rel_l2(post, o_post) <= TOL_MFMA
 
 
 def test_c1_dense_512_e4m3_per_tensor(gpu, oracle):

@@ -4,14 +4,15 @@ SwiGLU (swiglu.cpp:87-136, kernels.cu:296-304): pre = h = SiLU(Gate x) * Up x
 with the reference's f32/f64 rounding; post = Down h.
 MHA (mha.cpp:123-183, kernels.cu:470-631): Q/K/V projections, attention core
 with the reference's global positions and KV ring, O projection.
-Tolerance: relative L2 <= 1e-5 where the GPU keeps fp32 and the oracle f64
-(GEMV path); the attention core uses fp32 exp/sin/cos against f64 libm, so
-<= 1e-4 there. The layer contract bound is 1e-3.
+Tolerance: relative L2 <= 1e-5 for one row (VALU GEMV, fp32), <= 5e-5 where
+rows go through the scaled matrix cores (see test_gpu_dense), <= 1e-4 after
+the attention core (fp32 exp/sin/cos against f64 libm). The layer contract
+bound is 1e-3.
 """
 import numpy as np
 import pytest
 
-from test_gpu_dense import rel_l2
+from test_gpu_dense import rel_l2, tol
 
 pytestmark = pytest.mark.gpu
 
@@ -42,8 +43,8 @@ def test_swiglu_matches_oracle(gpu, oracle, dt, scheme, batch, seq, d, inter):
     h, y = s.execute(x)
     s.close()
     oh, oy = oracle_swiglu(oracle, dt, scheme, G, U, D, x)
-    assert rel_l2(h, oh) <= 1e-5
-    assert rel_l2(y, oy) <= 1e-5
+    assert rel_l2(h, oh) <= tol(batch * seq)
+    assert rel_l2(y, oy) <= tol(batch * seq)
 
 
 def test_c3_swiglu_fp4_block32_batch1(gpu, oracle):

@@ -19,8 +19,14 @@
 namespace wv {
 namespace {
 
-constexpr int kWaves = 4;
-constexpr int kThreads = 64 * kWaves;
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// Streaming weight load: non-temporal, so the 16-byte lines do not displace
+// x and other reused data from the caches.
+__device__ __forceinline__ uint4 load_stream(const uint8_t* p) {
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
 
 typedef float v2f __attribute__((ext_vector_type(2)));
 
@@ -119,8 +125,8 @@ constexpr int log2c() {
 
 // MATS = 1: y = W x with the Dense epilogue into pre/post.
 // MATS = 2: g = Wg x, u = Wu x, pre = h = f32(f64(f32(SiLU(g))) * f64(u)).
-template <int DT, bool BLK, int R, int MATS, bool VECX>
-__global__ __launch_bounds__(kThreads) void k_gemv(GemvArgs a) {
+template <int DT, bool BLK, int R, int MATS, bool VECX, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void k_gemv(GemvArgs a) {
   constexpr int KS = Codec<DT>::KS;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -135,7 +141,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv(GemvArgs a) {
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
 
-  for (int c = wave; c < nchunks; c += kWaves) {
+  for (int c = wave; c < nchunks; c += WAVES) {
     const int k0 = c * 64 * KS + lane * KS;
     if (k0 >= a.kpad) continue;
     float xv[KS];
@@ -156,7 +162,9 @@ __global__ __launch_bounds__(kThreads) void k_gemv(GemvArgs a) {
     for (int m = 0; m < MATS; ++m)
 #pragma unroll
       for (int r = 0; r < R; ++r)
-        q[m][r] = *reinterpret_cast<const uint4*>(a.codes[m] + (size_t)(r0 + r) * a.pitch + boff);
+        q[m][r] = load_stream(a.codes[m] + (size_t)(r0 + r) * a.pitch + boff);
+    // every weight load of this chunk is in flight before any decode starts
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int m = 0; m < MATS; ++m) {
 #pragma unroll
@@ -172,7 +180,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv(GemvArgs a) {
     }
   }
 
-  __shared__ float part[MATS][kWaves][R];
+  __shared__ float part[MATS][WAVES][R];
 #pragma unroll
   for (int m = 0; m < MATS; ++m) {
     wave_reduce_rows<R>(acc[m], lane);
@@ -188,7 +196,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv(GemvArgs a) {
   for (int m = 0; m < MATS; ++m) {
     float t = part[m][0][threadIdx.x];
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w) t += part[m][w][threadIdx.x];
+    for (int w = 1; w < WAVES; ++w) t += part[m][w][threadIdx.x];
     tot[m] = t * a.scale[m][o];
   }
   const size_t oi = (size_t)b * a.out_stride + o;
@@ -212,42 +220,66 @@ __global__ __launch_bounds__(kThreads) void k_gemv(GemvArgs a) {
   }
 }
 
-template <int DT, bool BLK, int R, int MATS>
+template <int DT, bool BLK, int R, int MATS, int WAVES>
 Status launch_t(const GemvArgs& a, int batch, hipStream_t st) {
   const bool vecx = (a.cols % 4 == 0) && (a.x_stride % 4 == 0) &&
                     ((reinterpret_cast<uintptr_t>(a.x) & 15u) == 0);
   dim3 grid((a.rows + R - 1) / R, batch);
-  if (vecx) k_gemv<DT, BLK, R, MATS, true><<<grid, kThreads, 0, st>>>(a);
-  else k_gemv<DT, BLK, R, MATS, false><<<grid, kThreads, 0, st>>>(a);
+  if (vecx) k_gemv<DT, BLK, R, MATS, true, WAVES><<<grid, 64 * WAVES, 0, st>>>(a);
+  else k_gemv<DT, BLK, R, MATS, false, WAVES><<<grid, 64 * WAVES, 0, st>>>(a);
   return hip_status(hipGetLastError(), "gemv launch");
 }
 
-template <int R, int MATS>
+template <int R, int MATS, int WAVES>
 Status launch_r(const GemvArgs& a, int dtype, bool blk, int batch, hipStream_t st) {
   switch (dtype) {
-  case kE4M3: return blk ? launch_t<kE4M3, true, R, MATS>(a, batch, st) : launch_t<kE4M3, false, R, MATS>(a, batch, st);
-  case kE5M2: return blk ? launch_t<kE5M2, true, R, MATS>(a, batch, st) : launch_t<kE5M2, false, R, MATS>(a, batch, st);
-  case kFP4: return blk ? launch_t<kFP4, true, R, MATS>(a, batch, st) : launch_t<kFP4, false, R, MATS>(a, batch, st);
+  case kE4M3: return blk ? launch_t<kE4M3, true, R, MATS, WAVES>(a, batch, st) : launch_t<kE4M3, false, R, MATS, WAVES>(a, batch, st);
+  case kE5M2: return blk ? launch_t<kE5M2, true, R, MATS, WAVES>(a, batch, st) : launch_t<kE5M2, false, R, MATS, WAVES>(a, batch, st);
+  case kFP4: return blk ? launch_t<kFP4, true, R, MATS, WAVES>(a, batch, st) : launch_t<kFP4, false, R, MATS, WAVES>(a, batch, st);
   }
   return Status::err(kUnsupported, "gemv: dtype");
 }
 
+template <int MATS, int WAVES>
+Status launch_w(const GemvArgs& a, int dtype, bool blk, int batch, int rows, hipStream_t st) {
+  switch (rows) {
+  case 2: return launch_r<2, MATS, WAVES>(a, dtype, blk, batch, st);
+  case 4: return launch_r<4, MATS, WAVES>(a, dtype, blk, batch, st);
+  case 16: return launch_r<16, MATS, WAVES>(a, dtype, blk, batch, st);
+  default: return launch_r<8, MATS, WAVES>(a, dtype, blk, batch, st);
+  }
+}
+
+template <int MATS>
+Status launch_m(const GemvArgs& a, int dtype, bool blk, int batch, GemvTile t, hipStream_t st) {
+  switch (t.waves) {
+  case 1: return launch_w<MATS, 1>(a, dtype, blk, batch, t.rows, st);
+  case 2: return launch_w<MATS, 2>(a, dtype, blk, batch, t.rows, st);
+  default: return launch_w<MATS, 4>(a, dtype, blk, batch, t.rows, st);
+  }
+}
+
 }  // namespace
 
-Status launch_gemv(const GemvArgs& a, int dtype, bool blk, int batch, int rows_per_group,
-                   hipStream_t st) {
-  if (a.mats == 2) {
-    switch (rows_per_group) {
-    case 4: return launch_r<4, 2>(a, dtype, blk, batch, st);
-    case 16: return launch_r<16, 2>(a, dtype, blk, batch, st);
-    default: return launch_r<8, 2>(a, dtype, blk, batch, st);
-    }
-  }
-  switch (rows_per_group) {
-  case 4: return launch_r<4, 1>(a, dtype, blk, batch, st);
-  case 16: return launch_r<16, 1>(a, dtype, blk, batch, st);
-  default: return launch_r<8, 1>(a, dtype, blk, batch, st);
-  }
+GemvTile gemv_tile(int dtype, int kpad, int rows, int mats, int cus) {
+  // K chunks of 1 KiB per wave: waves per group = chunks (at most 4), then
+  // rows per group so that the grid has >= 8 waves per CU when it can.
+  const int ks = dtype == kFP4 ? 32 : 16;
+  const int chunks = (kpad + 64 * ks - 1) / (64 * ks);
+  GemvTile t;
+  t.waves = chunks >= 4 ? 4 : chunks >= 2 ? 2 : 1;
+  const long want = 8L * (cus > 0 ? cus : 256);
+  t.rows = 16;
+  while (t.rows > 2 && ((long)rows + t.rows - 1) / t.rows * t.waves < want) t.rows /= 2;
+  if (mats == 2 && t.rows > 8) t.rows = 8;
+  return t;
+}
+
+Status launch_gemv(const GemvArgs& a, int dtype, bool blk, int batch, GemvTile t, hipStream_t st) {
+  if (t.rows != 2 && t.rows != 4 && t.rows != 8 && t.rows != 16)
+    return Status::err(kInvalid, "gemv: rows per group must be 2, 4, 8 or 16");
+  return a.mats == 2 ? launch_m<2>(a, dtype, blk, batch, t, st)
+                     : launch_m<1>(a, dtype, blk, batch, t, st);
 }
 
 }  // namespace wv

@@ -36,8 +36,35 @@ struct GemvArgs {
   const double* bias = nullptr;
   int bias_len = 0;
 };
-Status launch_gemv(const GemvArgs& a, int dtype, bool blk, int batch, int rows_per_group,
+// Rows per workgroup (2, 4, 8, 16) and waves per workgroup (1, 2, 4; they split K).
+struct GemvTile {
+  int rows = 8;
+  int waves = 4;
+};
+GemvTile gemv_tile(int dtype, int kpad, int rows, int mats, int cus);
+Status launch_gemv(const GemvArgs& a, int dtype, bool blk, int batch, GemvTile tile,
                    hipStream_t st);
+
+// ---- small-batch GEMV on the scaled MFMA (mxv.hip) ----
+constexpr int kMxvMaxBatch = 4;
+struct MxvArgs {
+  const uint8_t* codes[2] = {nullptr, nullptr};
+  const float* scale[2] = {nullptr, nullptr};
+  const uint8_t* blk[2] = {nullptr, nullptr};
+  int mats = 1;
+  int pitch = 0, nblk = 0, kpad = 0, cols = 0, rows = 0;
+  const float* x = nullptr;
+  int x_stride = 0;
+  int batch = 1;
+  float* pre = nullptr;
+  float* post = nullptr;
+  int out_stride = 0;
+  int act = kLinear;
+  int need_epi = 0;
+  const double* bias = nullptr;
+  int bias_len = 0;
+};
+Status launch_mxv(const MxvArgs& a, int dtype, bool blk, hipStream_t st);
 
 // ---- attention core (attention.hip) ----
 struct AttnArgs {

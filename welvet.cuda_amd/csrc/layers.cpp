@@ -127,11 +127,8 @@ Status dense_build_from_store(int in, int out, int act, const WeightStore& store
 
 int gemv_batch_limit() { return 1 << 30; }
 
-static int rows_per_group(int rows) {
-  const int cu = cu_count() > 0 ? cu_count() : 256;
-  if (rows >= 16 * 2 * cu) return 16;
-  if (rows >= 8 * 2 * cu) return 8;
-  return 4;
+static GemvTile tile_for(const DeviceWeights& d, int mats) {
+  return gemv_tile(d.dtype, d.kpad, d.rows, mats, cu_count());
 }
 
 static GemvArgs gemv_args(const DenseLayer& L, const float* x, int x_stride) {
@@ -154,17 +151,44 @@ static GemvArgs gemv_args(const DenseLayer& L, const float* x, int x_stride) {
   return a;
 }
 
+static MxvArgs mxv_args(const DenseLayer& L, const float* x, int x_stride, int batch) {
+  MxvArgs a;
+  a.codes[0] = L.dev.d_codes();
+  a.scale[0] = L.dev.d_scale();
+  a.blk[0] = L.dev.d_blk();
+  a.pitch = L.dev.pitch;
+  a.nblk = L.dev.nblk;
+  a.kpad = L.dev.kpad;
+  a.cols = L.in;
+  a.rows = L.out;
+  a.x = x;
+  a.x_stride = x_stride;
+  a.batch = batch;
+  a.out_stride = L.out;
+  a.act = L.act;
+  a.need_epi = L.need_epi() ? 1 : 0;
+  a.bias = L.bias_dev.as<const double>();
+  a.bias_len = L.bias_len;
+  return a;
+}
+
 size_t dense_workspace_bytes(const DenseLayer&, int) { return 0; }
 
 Status dense_forward(const DenseLayer& L, int batch, const float* x, float* pre, float* post,
                      Workspace*, hipStream_t st) {
   if (batch <= 0 || !x || !pre) return Status::err(kInvalid, "dense forward: bad args");
   if (L.need_epi() && !post) return Status::err(kInvalid, "dense forward: post needed");
+  if (batch >= 2 && batch <= kMxvMaxBatch) {
+    MxvArgs m = mxv_args(L, x, L.in, batch);
+    m.pre = pre;
+    m.post = post;
+    return launch_mxv(m, L.dev.dtype, L.dev.scheme == kSchemeBlock32, st);
+  }
   GemvArgs a = gemv_args(L, x, L.in);
   a.pre = pre;
   a.post = post;
-  return launch_gemv(a, L.dev.dtype, L.dev.scheme == kSchemeBlock32, batch,
-                     rows_per_group(L.out), st);
+  return launch_gemv(a, L.dev.dtype, L.dev.scheme == kSchemeBlock32, batch, tile_for(L.dev, 1),
+                     st);
 }
 
 // ---------------------------------------------------------------------------
@@ -184,6 +208,17 @@ size_t swiglu_workspace_bytes(const SwiGLULayer&, int) { return 0; }
 Status swiglu_forward(const SwiGLULayer& L, int rows, const float* x, float* h, float* y,
                       Workspace* ws, hipStream_t st) {
   if (rows <= 0 || !x || !h || !y) return Status::err(kInvalid, "swiglu forward: bad args");
+  if (rows >= 2 && rows <= kMxvMaxBatch) {
+    MxvArgs m = mxv_args(L.gate, x, L.in, rows);
+    m.mats = 2;
+    m.codes[1] = L.up.dev.d_codes();
+    m.scale[1] = L.up.dev.d_scale();
+    m.blk[1] = L.up.dev.d_blk();
+    m.pre = h;
+    m.need_epi = 0;
+    WV_TRY(launch_mxv(m, L.gate.dev.dtype, L.gate.dev.scheme == kSchemeBlock32, st));
+    return dense_forward(L.down, rows, h, y, nullptr, ws, st);
+  }
   GemvArgs a = gemv_args(L.gate, x, L.in);
   a.mats = 2;
   a.codes[1] = L.up.dev.d_codes();
@@ -193,7 +228,7 @@ Status swiglu_forward(const SwiGLULayer& L, int rows, const float* x, float* h, 
   a.post = nullptr;
   a.need_epi = 0;
   WV_TRY(launch_gemv(a, L.gate.dev.dtype, L.gate.dev.scheme == kSchemeBlock32, rows,
-                     rows_per_group(L.inter), st));
+                     tile_for(L.gate.dev, 2), st));
   return dense_forward(L.down, rows, h, y, nullptr, ws, st);
 }
 
