@@ -10,6 +10,8 @@ f64, activation; src/cuda/kernels.cu:130-161). Tolerances, stated per test:
     into E4M3 terms (residual ~4e-7) and the f8f6f4 MFMA accumulates with
     about 2^-16.5 relative precision (measured ~1.1e-5 at K=4096 even when the
     activations are exact in one term);
+  * products chained in sequence (SwiGLU down after gate/up, stacks) add
+    their errors: the bound scales with the chain length;
   * integer-exact cases: bit-exact (every partial sum is exact in f32 and in
     the matrix core).
 """
@@ -23,8 +25,9 @@ TOL_GEMV = 1e-5
 TOL_MFMA = 5e-5
 
 
-def tol(batch):
-    return TOL_GEMV if batch == 1 else TOL_MFMA
+def tol(batch, chain=1):
+    """Bound for `chain` quantized products applied in sequence to `batch` rows."""
+    return (TOL_GEMV if batch == 1 else TOL_MFMA) * chain
 
 
 def rel_l2(a, b):
@@ -33,11 +36,11 @@ def rel_l2(a, b):
     return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-300))
 
 
-def oracle_dense(oracle, dt, scheme, W, x, act=-1, bias=None):
+def oracle_dense(oracle, dt, scheme, W, x, act=-1, bias=None, threads=8):
     rows, cols = W.shape
     native, rs, blk = oracle.quantize(dt, scheme, rows, cols, W)
     Wd = oracle.dequant(dt, scheme, rows, cols, native, rs, blk)
-    return oracle.dense(Wd, x, act, bias)
+    return oracle.dense(Wd, x, act, bias, threads=threads)
 
 
 def run(gpu, dt, scheme, W, x, act=-1, bias=None):
@@ -153,3 +156,51 @@ def test_unsupported_dtype_and_scheme(gpu):
     with pytest.raises(pw.WelvetError) as e:
         pw.DenseSession(1, 4, 4, -1, 4, 7, W)
     assert e.value.code == 1
+
+
+@pytest.mark.parametrize("dt,scheme", [(4, 2), (5, 2), (16, 3), (4, 3), (16, 1), (5, 0)])
+@pytest.mark.parametrize("rows,cols,batch", [(70, 300, 5), (64, 256, 16), (130, 512, 17),
+                                              (257, 1024, 64), (96, 160, 257)])
+def test_batched_mfma_matches_oracle(gpu, oracle, dt, scheme, rows, cols, batch):
+    rng = np.random.default_rng(rows * 7 + cols + batch + dt + scheme)
+    W = (rng.standard_normal((rows, cols)) / np.sqrt(cols)).astype(np.float32)
+    if scheme == 0:
+        W *= 8.0
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    pre, post = run(gpu, dt, scheme, W, x)
+    o_pre, _ = oracle_dense(oracle, dt, scheme, W, x)
+    e = rel_l2(pre, o_pre)
+    assert e <= TOL_MFMA, e
+    assert np.array_equal(pre, post)
+
+
+def test_batched_epilogue_bias_act(gpu, oracle):
+    rng = np.random.default_rng(77)
+    W = (rng.standard_normal((100, 256)) / 16).astype(np.float32)
+    x = rng.standard_normal((33, 256)).astype(np.float32)
+    bias = rng.standard_normal(64)
+    for act in (0, 1, 2):
+        pre, post = run(gpu, 16, 3, W, x, act, bias)
+        o_pre, o_post = oracle_dense(oracle, 16, 3, W, x, act, bias)
+        assert rel_l2(pre, o_pre) <= TOL_MFMA and rel_l2(post, o_post) <= TOL_MFMA
+
+
+def test_c4_projection_gemm_e5m2(gpu, oracle):
+    """MHA projection GEMM 4096 x 1024 -> 1024, E5M2 weights with per-row scales."""
+    import pywelvet as pw
+    W = pw.normal(pw.seed_for(4), 1024 * 1024, 1 / 32.0).reshape(1024, 1024)
+    x = pw.normal(pw.seed_for(4) + 500, 4096 * 1024).reshape(4096, 1024)
+    pre, _ = run(gpu, 5, 2, W, x)
+    o_pre, _ = oracle_dense(oracle, 5, 2, W, x, threads=16)
+    assert rel_l2(pre, o_pre) <= TOL_MFMA
+
+
+@pytest.mark.parametrize("dt,scheme", [(4, 2), (16, 3)])
+def test_c5_cell_layer_batch256(gpu, oracle, dt, scheme):
+    """Volume cell layer: Dense 1024 -> 1024, batch 256 (E4M3 per-row / FP4 block-32)."""
+    import pywelvet as pw
+    W = pw.normal(pw.seed_for(5), 1024 * 1024, 1 / 32.0).reshape(1024, 1024)
+    x = pw.normal(pw.seed_for(5) + 500, 256 * 1024).reshape(256, 1024)
+    pre, _ = run(gpu, dt, scheme, W, x)
+    o_pre, _ = oracle_dense(oracle, dt, scheme, W, x)
+    assert rel_l2(pre, o_pre) <= TOL_MFMA

@@ -44,7 +44,7 @@ def test_swiglu_matches_oracle(gpu, oracle, dt, scheme, batch, seq, d, inter):
     s.close()
     oh, oy = oracle_swiglu(oracle, dt, scheme, G, U, D, x)
     assert rel_l2(h, oh) <= tol(batch * seq)
-    assert rel_l2(y, oy) <= tol(batch * seq)
+    assert rel_l2(y, oy) <= tol(batch * seq, chain=2)
 
 
 def test_c3_swiglu_fp4_block32_batch1(gpu, oracle):

@@ -66,6 +66,34 @@ struct MxvArgs {
 };
 Status launch_mxv(const MxvArgs& a, int dtype, bool blk, hipStream_t st);
 
+// ---- batched GEMM on the scaled MFMA (mxg.hip) ----
+// Activations are split into kTerms E4M3 terms with per-32 E8M0 scales.
+constexpr int kTerms = 3;
+struct MxgArgs {
+  const uint8_t* a = nullptr;   // [kTerms][mpad][kpad] term codes
+  const uint8_t* as = nullptr;  // [kTerms][mpad][kpad/32] term scales
+  int M = 0, mpad = 0;
+  const uint8_t* codes[2] = {nullptr, nullptr};
+  const float* scale[2] = {nullptr, nullptr};
+  const uint8_t* blk[2] = {nullptr, nullptr};
+  int mats = 1;
+  int pitch = 0, nblk = 0, kpad = 0, N = 0;
+  float* pre = nullptr;
+  float* post = nullptr;
+  int out_stride = 0;
+  int act = kLinear;
+  int need_epi = 0;
+  const double* bias = nullptr;
+  int bias_len = 0;
+};
+int mxg_block_m(int M);
+// Bytes of the split buffer for M rows of kpad columns.
+size_t split_bytes(int M, int kpad);
+// x [M][cols] (row stride x_stride) -> split terms in buf.
+Status launch_split(const float* x, int x_stride, int M, int cols, int kpad, uint8_t* buf,
+                    hipStream_t st);
+Status launch_mxg(const MxgArgs& p, int dtype, bool blk, hipStream_t st);
+
 // ---- attention core (attention.hip) ----
 struct AttnArgs {
   const float* q = nullptr;  // [tokens][heads*hd], rotated in place when rope

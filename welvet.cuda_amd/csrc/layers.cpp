@@ -172,12 +172,56 @@ static MxvArgs mxv_args(const DenseLayer& L, const float* x, int x_stride, int b
   return a;
 }
 
-size_t dense_workspace_bytes(const DenseLayer&, int) { return 0; }
+bool uses_split(int batch) { return batch > kMxvMaxBatch; }
+
+size_t dense_workspace_bytes(const DenseLayer& L, int batch) {
+  return uses_split(batch) ? split_bytes(batch, L.dev.kpad) : 0;
+}
+
+Status ensure_split(Workspace* ws, size_t n) {
+  if (!ws) return Status::err(kInvalid, "workspace: null");
+  if (ws->b.bytes < n) WV_TRY(ws->b.alloc(n));
+  return Status::ok();
+}
+
+static MxgArgs mxg_args(const DenseLayer& L, int batch, const uint8_t* split) {
+  MxgArgs p;
+  p.M = batch;
+  p.mpad = (int)round_up(batch, mxg_block_m(batch));
+  p.a = split;
+  p.as = split + (size_t)kTerms * p.mpad * L.dev.kpad;
+  p.codes[0] = L.dev.d_codes();
+  p.scale[0] = L.dev.d_scale();
+  p.blk[0] = L.dev.d_blk();
+  p.pitch = L.dev.pitch;
+  p.nblk = L.dev.nblk;
+  p.kpad = L.dev.kpad;
+  p.N = L.out;
+  p.out_stride = L.out;
+  p.act = L.act;
+  p.need_epi = L.need_epi() ? 1 : 0;
+  p.bias = L.bias_dev.as<const double>();
+  p.bias_len = L.bias_len;
+  return p;
+}
+
+Status dense_forward_split(const DenseLayer& L, int batch, const uint8_t* split, float* pre,
+                           float* post, hipStream_t st) {
+  MxgArgs p = mxg_args(L, batch, split);
+  p.pre = pre;
+  p.post = post;
+  return launch_mxg(p, L.dev.dtype, L.dev.scheme == kSchemeBlock32, st);
+}
 
 Status dense_forward(const DenseLayer& L, int batch, const float* x, float* pre, float* post,
-                     Workspace*, hipStream_t st) {
+                     Workspace* ws, hipStream_t st) {
   if (batch <= 0 || !x || !pre) return Status::err(kInvalid, "dense forward: bad args");
   if (L.need_epi() && !post) return Status::err(kInvalid, "dense forward: post needed");
+  if (uses_split(batch)) {
+    WV_TRY(ensure_split(ws, split_bytes(batch, L.dev.kpad)));
+    WV_TRY(launch_split(x, L.in, batch, L.in, L.dev.kpad, ws->b.as<uint8_t>(), st));
+    return dense_forward_split(L, batch, ws->b.as<uint8_t>(), pre, post, st);
+  }
   if (batch >= 2 && batch <= kMxvMaxBatch) {
     MxvArgs m = mxv_args(L, x, L.in, batch);
     m.pre = pre;
@@ -203,7 +247,11 @@ Status swiglu_build(int in, int inter, int dtype, int scheme, const float* G, co
   return Status::ok();
 }
 
-size_t swiglu_workspace_bytes(const SwiGLULayer&, int) { return 0; }
+size_t swiglu_workspace_bytes(const SwiGLULayer& L, int rows) {
+  if (!uses_split(rows)) return 0;
+  const size_t a = split_bytes(rows, L.gate.dev.kpad), b = split_bytes(rows, L.down.dev.kpad);
+  return a > b ? a : b;
+}
 
 Status swiglu_forward(const SwiGLULayer& L, int rows, const float* x, float* h, float* y,
                       Workspace* ws, hipStream_t st) {
@@ -218,6 +266,21 @@ Status swiglu_forward(const SwiGLULayer& L, int rows, const float* x, float* h, 
     m.need_epi = 0;
     WV_TRY(launch_mxv(m, L.gate.dev.dtype, L.gate.dev.scheme == kSchemeBlock32, st));
     return dense_forward(L.down, rows, h, y, nullptr, ws, st);
+  }
+  if (uses_split(rows)) {
+    WV_TRY(ensure_split(ws, swiglu_workspace_bytes(L, rows)));
+    uint8_t* buf = ws->b.as<uint8_t>();
+    WV_TRY(launch_split(x, L.in, rows, L.in, L.gate.dev.kpad, buf, st));
+    MxgArgs p = mxg_args(L.gate, rows, buf);
+    p.mats = 2;
+    p.codes[1] = L.up.dev.d_codes();
+    p.scale[1] = L.up.dev.d_scale();
+    p.blk[1] = L.up.dev.d_blk();
+    p.pre = h;
+    p.need_epi = 0;
+    WV_TRY(launch_mxg(p, L.gate.dev.dtype, L.gate.dev.scheme == kSchemeBlock32, st));
+    WV_TRY(launch_split(h, L.inter, rows, L.inter, L.down.dev.kpad, buf, st));
+    return dense_forward_split(L.down, rows, buf, y, nullptr, st);
   }
   GemvArgs a = gemv_args(L.gate, x, L.in);
   a.mats = 2;
@@ -269,6 +332,18 @@ size_t mha_workspace_bytes(const MHALayer& L, int batch, int seq) {
   return t * ((size_t)L.cfg.q_dim() + 2 * (size_t)L.cfg.kv_dim()) * sizeof(float);
 }
 
+static size_t mha_split_bytes(const MHALayer& L, int T) {
+  if (!uses_split(T)) return 0;
+  const size_t a = split_bytes(T, L.q.dev.kpad), b = split_bytes(T, L.o.dev.kpad);
+  return a > b ? a : b;
+}
+
+Status mha_prepare(const MHALayer& L, int batch, int seq, Workspace* ws) {
+  const size_t need = mha_workspace_bytes(L, batch, seq);
+  if (ws->a.bytes < need) WV_TRY(ws->a.alloc(need));
+  return ensure_split(ws, mha_split_bytes(L, batch * seq));
+}
+
 Status mha_forward(const MHALayer& L, int batch, int seq, const float* x, float* attn, float* y,
                    Workspace* ws, hipStream_t st) {
   const MHAConfig& c = L.cfg;
@@ -281,9 +356,18 @@ Status mha_forward(const MHALayer& L, int batch, int seq, const float* x, float*
   float* qb = ws->a.as<float>();
   float* kb = qb + (size_t)T * c.q_dim();
   float* vb = kb + (size_t)T * c.kv_dim();
-  WV_TRY(dense_forward(L.q, T, x, qb, nullptr, ws, st));
-  WV_TRY(dense_forward(L.k, T, x, kb, nullptr, ws, st));
-  WV_TRY(dense_forward(L.v, T, x, vb, nullptr, ws, st));
+  if (uses_split(T)) {
+    // Q, K and V read the same activations: split them once
+    WV_TRY(ensure_split(ws, mha_split_bytes(L, T)));
+    WV_TRY(launch_split(x, c.d_model, T, c.d_model, L.q.dev.kpad, ws->b.as<uint8_t>(), st));
+    WV_TRY(dense_forward_split(L.q, T, ws->b.as<uint8_t>(), qb, nullptr, st));
+    WV_TRY(dense_forward_split(L.k, T, ws->b.as<uint8_t>(), kb, nullptr, st));
+    WV_TRY(dense_forward_split(L.v, T, ws->b.as<uint8_t>(), vb, nullptr, st));
+  } else {
+    WV_TRY(dense_forward(L.q, T, x, qb, nullptr, ws, st));
+    WV_TRY(dense_forward(L.k, T, x, kb, nullptr, ws, st));
+    WV_TRY(dense_forward(L.v, T, x, vb, nullptr, ws, st));
+  }
   AttnArgs a;
   a.q = qb, a.k = kb, a.v = vb, a.out = attn;
   a.tokens = T, a.seq = seq, a.heads = c.num_heads, a.kv_heads = c.num_kv_heads;

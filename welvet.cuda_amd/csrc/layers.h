@@ -58,6 +58,14 @@ Status dense_forward(const DenseLayer& L, int batch, const float* x, float* pre,
                      Workspace* ws, hipStream_t st);
 // Workspace bytes dense_forward needs for this batch.
 size_t dense_workspace_bytes(const DenseLayer& L, int batch);
+// True when `batch` rows take the split + batched-MFMA path.
+bool uses_split(int batch);
+// Batched path with activations already split (launch_split with L.dev.kpad).
+Status dense_forward_split(const DenseLayer& L, int batch, const uint8_t* split, float* pre,
+                           float* post, hipStream_t st);
+// Grows ws->b to at least n bytes (mount time; a forward that finds it too
+// small allocates, which a captured graph cannot do).
+Status ensure_split(Workspace* ws, size_t n);
 
 struct SwiGLULayer {
   int in = 0, inter = 0;
@@ -89,5 +97,7 @@ Status mha_build(const MHAConfig& cfg, int dtype, int scheme, const float* Q, co
 Status mha_forward(const MHALayer& L, int batch, int seq, const float* x, float* attn, float* y,
                    Workspace* ws, hipStream_t st);
 size_t mha_workspace_bytes(const MHALayer& L, int batch, int seq);
+// Sizes the workspace for (batch, seq) ahead of forward calls.
+Status mha_prepare(const MHALayer& L, int batch, int seq, Workspace* ws);
 
 }  // namespace wv

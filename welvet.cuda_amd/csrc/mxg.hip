@@ -1,0 +1,279 @@
+// Batched quantized GEMM on the CDNA4 scaled matrix cores.
+//
+//   C[m][n] = rowscale[n] * sum_k x[m][k] * dec(W[n][k]) * blockscale[n][k/32]
+//
+// x (fp32) is first split into kTerms E4M3 terms with per-32 E8M0 scales
+// (k_split: each term quantizes the residual of the previous ones, so
+// x ~ sum_t a_t 2^e_t with a relative residual of ~2^-12 for three terms).
+// The terms act as extra K: every term is multiplied by the same weight tile
+// and accumulated into the same fp32 accumulator by
+// v_mfma_scale_f32_16x16x128_f8f6f4, which takes the stored FP8/FP4 weight
+// codes and their E8M0 block scales directly.
+//
+// Tiling: a 256-thread workgroup computes a BM x 64 tile of C; per 128-wide K
+// step it stages the A terms, the weight codes and both scale sets in LDS
+// (rows padded by 16 bytes so 16-byte fragment reads are bank-conflict free),
+// then each wave runs its MFMAs. Operand layout of the instruction (lane l,
+// group g = l/16): FP8 bytes 0-15 -> k = 16g + j, bytes 16-31 -> k = 64 + 16g
+// + j; FP4 nibble j -> k = 32g + j; scale of lane l: row l%16, block g;
+// D: col l%16, rows 4g + r.
+#include "codec.h"
+#include "common.h"
+#include "kernels.h"
+
+namespace wv {
+namespace {
+
+constexpr int kBN = 64;
+constexpr int kThreads = 256;
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v2f __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ double act_f64(int act, double x) {
+  switch (act) {
+  case kReLU: return x < 0.0 ? 0.0 : x;
+  case kSilu: return x / (1.0 + exp(-x));
+  case kGELU: {
+    const double k = 0.7978845608028654;
+    return 0.5 * x * (1.0 + tanh(k * (x + 0.044715 * x * x * x)));
+  }
+  case kTanh: return tanh(x);
+  case kSigmoid: return 1.0 / (1.0 + exp(-x));
+  case kLeaky: return x < 0.0 ? 0.01 * x : x;
+  case kReLU2: return x < 0.0 ? 0.0 : x * x;
+  default: return x;
+  }
+}
+
+__device__ __forceinline__ float quad_max(float v) {
+  int o = __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false);
+  v = fmaxf(v, __builtin_bit_cast(float, o));
+  o = __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false);
+  return fmaxf(v, __builtin_bit_cast(float, o));
+}
+
+// One thread per 8 consecutive elements of a row; the 4 lanes of a quad hold
+// one 32-element block. Rows >= M (padding up to mpad) get zero codes.
+__global__ __launch_bounds__(kThreads) void k_split(const float* __restrict__ x, int x_stride,
+                                                    int M, int cols, int mpad, int kpad,
+                                                    uint8_t* __restrict__ a,
+                                                    uint8_t* __restrict__ as) {
+  const int per_row = kpad / 8;
+  const int64_t item = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (item >= (int64_t)mpad * per_row) return;  // whole quads exit together
+  const int m = (int)(item / per_row), k = (int)(item % per_row) * 8;
+  float r[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r[i] = (m < M && k + i < cols) ? x[(size_t)m * x_stride + k + i] : 0.0f;
+  const int nblk = kpad / 32;
+#pragma unroll
+  for (int t = 0; t < kTerms; ++t) {
+    float am = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) am = fmaxf(am, fabsf(r[i]));
+    am = quad_max(am);
+    const int e = e8m0_exponent(am, 448.0f);
+    const float inv = pow2f(-e), sc = pow2f(e);
+    int w0 = __builtin_amdgcn_cvt_pk_fp8_f32(r[0] * inv, r[1] * inv, 0, false);
+    w0 = __builtin_amdgcn_cvt_pk_fp8_f32(r[2] * inv, r[3] * inv, w0, true);
+    int w1 = __builtin_amdgcn_cvt_pk_fp8_f32(r[4] * inv, r[5] * inv, 0, false);
+    w1 = __builtin_amdgcn_cvt_pk_fp8_f32(r[6] * inv, r[7] * inv, w1, true);
+    *reinterpret_cast<int2*>(a + ((size_t)t * mpad + m) * kpad + k) = make_int2(w0, w1);
+    if ((threadIdx.x & 3) == 0) as[((size_t)t * mpad + m) * nblk + k / 32] = (uint8_t)(e + 127);
+    if (t + 1 < kTerms) {
+      const v2f q0 = __builtin_amdgcn_cvt_pk_f32_fp8(w0, false);
+      const v2f q1 = __builtin_amdgcn_cvt_pk_f32_fp8(w0, true);
+      const v2f q2 = __builtin_amdgcn_cvt_pk_f32_fp8(w1, false);
+      const v2f q3 = __builtin_amdgcn_cvt_pk_f32_fp8(w1, true);
+      r[0] -= q0.x * sc, r[1] -= q0.y * sc, r[2] -= q1.x * sc, r[3] -= q1.y * sc;
+      r[4] -= q2.x * sc, r[5] -= q2.y * sc, r[6] -= q3.x * sc, r[7] -= q3.y * sc;
+    }
+  }
+}
+
+template <int DT>
+constexpr int wfmt() {
+  return DT == kE4M3 ? 0 : DT == kE5M2 ? 1 : 4;
+}
+
+// BM x 64 tile; waves WAVES_M x WAVES_N; each wave SM x SN MFMA tiles of 16x16.
+template <int DT, bool BLK, int MATS, int BM>
+__global__ __launch_bounds__(kThreads) void k_mxg(MxgArgs p) {
+  constexpr bool FP4 = DT == kFP4;
+  constexpr int WAVES_M = BM >= 32 ? 2 : 1;
+  constexpr int WAVES_N = 4 / WAVES_M;
+  constexpr int WM = BM / WAVES_M, WN = kBN / WAVES_N;
+  constexpr int SM = WM / 16, SN = WN / 16;
+  constexpr int AROW = 128 + 16;                 // padded LDS row of A (bytes)
+  constexpr int BROW = (FP4 ? 64 : 128) + 16;    // padded LDS row of W
+  constexpr int WBYTES = FP4 ? 64 : 128;         // code bytes per row per K step
+
+  __shared__ __attribute__((aligned(16))) uint8_t sa[kTerms * BM * AROW];
+  __shared__ __attribute__((aligned(16))) uint8_t sb[MATS * kBN * BROW];
+  __shared__ uint8_t ssa[kTerms * BM * 4];
+  __shared__ uint8_t ssb[MATS * kBN * 4];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+  const int i16 = lane & 15, g = lane >> 4;
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * kBN;
+  const int S = p.kpad / 128;
+  const int nblk_a = p.kpad / 32;
+
+  v4f acc[MATS][SM][SN];
+#pragma unroll
+  for (int m = 0; m < MATS; ++m)
+#pragma unroll
+    for (int a = 0; a < SM; ++a)
+#pragma unroll
+      for (int b = 0; b < SN; ++b) acc[m][a][b] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  for (int s = 0; s < S; ++s) {
+    // stage A terms: kTerms*BM rows x 8 chunks of 16 B
+    for (int c = tid; c < kTerms * BM * 8; c += kThreads) {
+      const int t = c / (BM * 8), row = (c / 8) % BM, j = c % 8;
+      const uint4 v = *reinterpret_cast<const uint4*>(
+          p.a + ((size_t)t * p.mpad + m0 + row) * p.kpad + (size_t)s * 128 + j * 16);
+      *reinterpret_cast<uint4*>(sa + (t * BM + row) * AROW + j * 16) = v;
+    }
+    for (int c = tid; c < kTerms * BM; c += kThreads) {
+      const int t = c / BM, row = c % BM;
+      *reinterpret_cast<uint32_t*>(ssa + c * 4) = *reinterpret_cast<const uint32_t*>(
+          p.as + ((size_t)t * p.mpad + m0 + row) * nblk_a + s * 4);
+    }
+    // stage weight codes: MATS*64 rows x (WBYTES/16) chunks
+    constexpr int WCH = WBYTES / 16;
+    for (int c = tid; c < MATS * kBN * WCH; c += kThreads) {
+      const int m = c / (kBN * WCH), row = (c / WCH) % kBN, j = c % WCH;
+      const uint4 v = *reinterpret_cast<const uint4*>(
+          p.codes[m] + (size_t)(n0 + row) * p.pitch + (size_t)s * WBYTES + j * 16);
+      *reinterpret_cast<uint4*>(sb + (m * kBN + row) * BROW + j * 16) = v;
+    }
+    if constexpr (BLK) {
+      for (int c = tid; c < MATS * kBN; c += kThreads) {
+        const int m = c / kBN, row = c % kBN;
+        *reinterpret_cast<uint32_t*>(ssb + c * 4) = *reinterpret_cast<const uint32_t*>(
+            p.blk[m] + (size_t)(n0 + row) * p.nblk + s * 4);
+      }
+    }
+    __syncthreads();
+    v8i bf[MATS][SN];
+    int bsc[MATS][SN];
+#pragma unroll
+    for (int m = 0; m < MATS; ++m)
+#pragma unroll
+      for (int b = 0; b < SN; ++b) {
+        const int row = wn * WN + b * 16 + i16;
+        const uint8_t* src = sb + (m * kBN + row) * BROW + 16 * g;
+        const int4 lo = *reinterpret_cast<const int4*>(src);
+        int4 hi = make_int4(0, 0, 0, 0);
+        if constexpr (!FP4) hi = *reinterpret_cast<const int4*>(src + 64);
+        bf[m][b] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+        bsc[m][b] = BLK ? (int)ssb[(m * kBN + row) * 4 + g] : 127;
+      }
+#pragma unroll
+    for (int t = 0; t < kTerms; ++t) {
+#pragma unroll
+      for (int a = 0; a < SM; ++a) {
+        const int row = wm * WM + a * 16 + i16;
+        const uint8_t* src = sa + (t * BM + row) * AROW + 16 * g;
+        const int4 lo = *reinterpret_cast<const int4*>(src);
+        const int4 hi = *reinterpret_cast<const int4*>(src + 64);
+        const v8i af = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+        const int asc = ssa[(t * BM + row) * 4 + g];
+#pragma unroll
+        for (int m = 0; m < MATS; ++m)
+#pragma unroll
+          for (int b = 0; b < SN; ++b)
+            acc[m][a][b] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                af, bf[m][b], acc[m][a][b], 0, wfmt<DT>(), 0, asc, 0, bsc[m][b]);
+      }
+    }
+    __syncthreads();
+  }
+
+  // epilogue: lane holds rows 4g + r of each 16x16 tile, column i16
+#pragma unroll
+  for (int a = 0; a < SM; ++a)
+#pragma unroll
+    for (int b = 0; b < SN; ++b) {
+      const int n = n0 + wn * WN + b * 16 + i16;
+      if (n >= p.N) continue;
+      float sc[MATS];
+#pragma unroll
+      for (int m = 0; m < MATS; ++m) sc[m] = p.scale[m][n];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int mrow = m0 + wm * WM + a * 16 + 4 * g + r;
+        if (mrow >= p.M) continue;
+        const size_t oi = (size_t)mrow * p.out_stride + n;
+        if constexpr (MATS == 2) {
+          const float gv = acc[0][a][b][r] * sc[0], uv = acc[1][a][b][r] * sc[1];
+          const float gs = (float)act_f64(kSilu, (double)gv);
+          p.pre[oi] = (float)((double)gs * (double)uv);
+        } else {
+          float y = acc[0][a][b][r] * sc[0];
+          if (p.need_epi) {
+            double v = (double)y;
+            if (p.bias && n < p.bias_len) {
+              v += p.bias[n];
+              y = (float)v;
+            }
+            p.pre[oi] = y;
+            p.post[oi] = (float)act_f64(p.act, v);
+          } else {
+            p.pre[oi] = y;
+            if (p.post) p.post[oi] = y;
+          }
+        }
+      }
+    }
+}
+
+template <int DT, bool BLK, int MATS>
+Status launch_t(const MxgArgs& p, int bm, hipStream_t st) {
+  const dim3 grid((unsigned)((p.N + kBN - 1) / kBN), (unsigned)(p.mpad / bm));
+  if (bm == 16) k_mxg<DT, BLK, MATS, 16><<<grid, kThreads, 0, st>>>(p);
+  else k_mxg<DT, BLK, MATS, 64><<<grid, kThreads, 0, st>>>(p);
+  return hip_status(hipGetLastError(), "mxg launch");
+}
+
+template <int MATS>
+Status launch_m(const MxgArgs& p, int dtype, bool blk, int bm, hipStream_t st) {
+  switch (dtype) {
+  case kE4M3: return blk ? launch_t<kE4M3, true, MATS>(p, bm, st) : launch_t<kE4M3, false, MATS>(p, bm, st);
+  case kE5M2: return blk ? launch_t<kE5M2, true, MATS>(p, bm, st) : launch_t<kE5M2, false, MATS>(p, bm, st);
+  case kFP4: return blk ? launch_t<kFP4, true, MATS>(p, bm, st) : launch_t<kFP4, false, MATS>(p, bm, st);
+  }
+  return Status::err(kUnsupported, "mxg: dtype");
+}
+
+}  // namespace
+
+int mxg_block_m(int M) { return M <= 16 ? 16 : 64; }
+
+size_t split_bytes(int M, int kpad) {
+  const size_t mpad = (size_t)round_up(M, mxg_block_m(M));
+  return (size_t)kTerms * mpad * kpad + (size_t)kTerms * mpad * (kpad / 32);
+}
+
+Status launch_split(const float* x, int x_stride, int M, int cols, int kpad, uint8_t* buf,
+                    hipStream_t st) {
+  const int mpad = (int)round_up(M, mxg_block_m(M));
+  uint8_t* a = buf;
+  uint8_t* as = buf + (size_t)kTerms * mpad * kpad;
+  const int64_t items = (int64_t)mpad * (kpad / 8);
+  k_split<<<(unsigned)((items + kThreads - 1) / kThreads), kThreads, 0, st>>>(x, x_stride, M, cols,
+                                                                             mpad, kpad, a, as);
+  return hip_status(hipGetLastError(), "split launch");
+}
+
+Status launch_mxg(const MxgArgs& p, int dtype, bool blk, hipStream_t st) {
+  const int bm = mxg_block_m(p.M);
+  if (p.mpad % bm != 0 || p.kpad % 256 != 0) return Status::err(kInvalid, "mxg: layout");
+  return p.mats == 2 ? launch_m<2>(p, dtype, blk, bm, st) : launch_m<1>(p, dtype, blk, bm, st);
+}
+
+}  // namespace wv
