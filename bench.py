@@ -25,6 +25,22 @@ sys.path.insert(0, os.path.join(ROOT, "welvet.cuda_amd"))
 
 HBM_PEAK_GBS = 8000.0
 
+# rocprof summaries (kernel stats + FETCH_SIZE/WRITE_SIZE scaled by a copy of
+# known size) per workload; `traffic_bytes:` is the measured HBM bytes per launch.
+PROFILES = {"c2": "gemv_fp8e4m3_rowscale_4096x4096_b1.txt"}
+
+
+def measured_traffic(config):
+    name = PROFILES.get(config)
+    path = os.path.join(ROOT, "profiles", name) if name else None
+    if not path or not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            if line.startswith("traffic_bytes:"):
+                return int(line.split(":")[1])
+    return None
+
 
 def workloads():
     # name: (desc, dtype, scheme, batch, in, out, algorithmic bytes, flops)
@@ -69,6 +85,27 @@ def cpu_baseline(dtype, scheme, batch, K, N, W, x, nbytes, budget_s=10.0):
     }
 
 
+def copy_calibration(pw, nbytes, steps):
+    """Times `steps` device-to-device copies of nbytes (read nbytes, write nbytes)."""
+    pw.check(pw.lib().welvet_cuda_init())
+    hip = pw.Hip()
+    src, dst = hip.malloc(nbytes), hip.malloc(nbytes)
+    hip.memset(src, 1, nbytes)
+    stream = hip.stream()
+    hip.copy_async(dst, src, nbytes, stream)
+    hip.sync()
+    e0, e1 = hip.event(), hip.event()
+    hip.record(e0, stream)
+    for _ in range(steps):
+        hip.copy_async(dst, src, nbytes, stream)
+    hip.record(e1, stream)
+    ms = hip.elapsed_ms(e0, e1) / steps
+    print(json.dumps({"copy_bytes": nbytes, "steps": steps, "ms_per_copy": round(ms, 6),
+                      "GB/s_read_plus_write": round(2 * nbytes / ms / 1e6, 1)}), flush=True)
+    hip.free(src)
+    hip.free(dst)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -77,6 +114,9 @@ def main():
     ap.add_argument("--config", default="c2", choices=sorted(workloads()))
     ap.add_argument("--copies", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run device-to-device copies of MIB MiB (the known-size copy "
+                         "that scales the FETCH_SIZE/WRITE_SIZE counters) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU; --gpus above 1 is not part of it",
@@ -86,6 +126,10 @@ def main():
     import numpy as np
 
     import pywelvet as pw
+
+    if args.copy_calibration:
+        copy_calibration(pw, args.copy_calibration << 20, args.steps)
+        return
 
     desc, dtype, scheme, batch, K, N, nbytes, flops = workloads()[args.config]
     pw.check(pw.lib().welvet_cuda_init())
@@ -146,7 +190,8 @@ def main():
                    "weight_copies_rotated": copies, "algorithmic_bytes_per_step": nbytes,
                    "tflops": round(flops / per_step_s / 1e12, 4), "wall_s": round(t_wall, 4)},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(args.config)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

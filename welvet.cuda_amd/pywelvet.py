@@ -180,6 +180,7 @@ class Hip:
         _sig(h, "hipFree", ctypes.c_int, [_vp])
         _sig(h, "hipMemcpy", ctypes.c_int, [_vp, _vp, _sz, ctypes.c_int])
         _sig(h, "hipMemset", ctypes.c_int, [_vp, ctypes.c_int, _sz])
+        _sig(h, "hipMemcpyAsync", ctypes.c_int, [_vp, _vp, _sz, ctypes.c_int, _vp])
         _sig(h, "hipDeviceSynchronize", ctypes.c_int, [])
         _sig(h, "hipStreamCreate", ctypes.c_int, [ctypes.POINTER(_vp)])
         _sig(h, "hipStreamDestroy", ctypes.c_int, [_vp])
@@ -222,6 +223,11 @@ class Hip:
         out = np.empty(shape, dtype=dtype)
         self._ok(self.h.hipMemcpy(out.ctypes.data_as(_vp), _vp(p), out.nbytes, self.D2H), "D2H")
         return out
+
+    def copy_async(self, dst, src, nbytes, stream):
+        """Device-to-device copy queued on `stream`."""
+        self._ok(self.h.hipMemcpyAsync(_vp(dst), _vp(src), nbytes, self.D2D, _vp(stream)),
+                 "hipMemcpyAsync")
 
     def memset(self, p, value, nbytes):
         self._ok(self.h.hipMemset(_vp(p), value, nbytes), "hipMemset")
