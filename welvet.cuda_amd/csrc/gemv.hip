@@ -29,6 +29,9 @@ __device__ __forceinline__ uint4 load_stream(const uint8_t* p) {
 }
 
 typedef float v2f __attribute__((ext_vector_type(2)));
+// Pointer into the constant address space (read-only for the kernel's
+// lifetime): uniform loads through it compile to scalar loads.
+typedef const float __attribute__((address_space(4)))* ConstF32;
 
 __device__ __forceinline__ double act_f64(int act, double x) {
   switch (act) {
@@ -93,34 +96,135 @@ __device__ __forceinline__ float dot_chunk(const uint4 q, const float* xv) {
   return s0 + s1;
 }
 
-// Folds v[0..N) across lanes that differ in bit `d`: the lane with the bit
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Value of lane (lane ^ D). Distances inside a 16-lane row are DPP moves
+// (VALU, no LDS round trip): quad_perm for 1 and 2, row_shl/row_shr:4 with
+// a select for 4, row_ror:8 for 8; 16 and 32 cross rows and use bpermute.
+// A DPP move must run with every lane active: a disabled source lane reads
+// as out of bounds. So both moves for distance 4 execute unconditionally and
+// a select picks between them; they may not sit in the arms of a branch.
+template <int D>
+__device__ __forceinline__ float xor_lane(float v, int lane) {
+  if constexpr (D == 1) {
+    return dpp<0xB1>(v);
+  } else if constexpr (D == 2) {
+    return dpp<0x4E>(v);
+  } else if constexpr (D == 4) {
+    const float from_above = dpp<0x104>(v);  // row_shl:4, lane i reads i + 4
+    const float from_below = dpp<0x114>(v);  // row_shr:4, lane i reads i - 4
+    return (lane & 4) ? from_below : from_above;
+  } else if constexpr (D == 8) {
+    return dpp<0x128>(v);
+  } else {
+    return __shfl_xor(v, D, 64);
+  }
+}
+
+// Folds v[0..N) across lanes that differ in bit D: the lane with the bit
 // clear keeps the lower half, the other the upper half.
-template <int N>
-__device__ __forceinline__ void fold(float* v, int lane, int d) {
-  const bool up = (lane & d) != 0;
+template <int N, int D>
+__device__ __forceinline__ void fold(float* v, int lane) {
+  const bool up = (lane & D) != 0;
 #pragma unroll
   for (int i = 0; i < N / 2; ++i) {
     const float send = up ? v[i] : v[i + N / 2];
     const float keep = up ? v[i + N / 2] : v[i];
-    v[i] = keep + __shfl_xor(send, d, 64);
+    v[i] = keep + xor_lane<D>(send, lane);
   }
-}
-
-// Reduces v[0..R) over the 64 lanes; afterwards lane l holds in v[0] the total
-// of row (l >> (6 - log2 R)) & (R - 1).
-template <int R>
-__device__ __forceinline__ void wave_reduce_rows(float* v, int lane) {
-  int d = 32;
-  if constexpr (R >= 16) { fold<16>(v, lane, d); d >>= 1; }
-  if constexpr (R >= 8) { fold<8>(v, lane, d); d >>= 1; }
-  if constexpr (R >= 4) { fold<4>(v, lane, d); d >>= 1; }
-  if constexpr (R >= 2) { fold<2>(v, lane, d); d >>= 1; }
-  for (; d > 0; d >>= 1) v[0] += __shfl_xor(v[0], d, 64);
 }
 
 template <int R>
 constexpr int log2c() {
   return R >= 16 ? 4 : R >= 8 ? 3 : R >= 4 ? 2 : R >= 2 ? 1 : 0;
+}
+
+// Reduces v[0..R) over the 64 lanes with a transposing butterfly (R/2 + R/4
+// + ... exchanges instead of 6 per row), folding the low lane bits first so
+// the multi-value steps are DPP moves. Afterwards lanes 0..R-1 hold in v[0]
+// the totals of rows reduced_row<R>(lane).
+template <int R>
+__device__ __forceinline__ void wave_reduce_rows(float* v, int lane) {
+  constexpr int L = log2c<R>();
+  if constexpr (L >= 4) fold<16, 1>(v, lane);
+  if constexpr (L >= 3) fold<8, (L >= 4 ? 2 : 1)>(v, lane);
+  if constexpr (L >= 2) fold<4, (1 << (L - 2))>(v, lane);
+  if constexpr (L >= 1) fold<2, (1 << (L - 1))>(v, lane);
+  if constexpr (L < 1) v[0] += xor_lane<1>(v[0], lane);
+  if constexpr (L < 2) v[0] += xor_lane<2>(v[0], lane);
+  if constexpr (L < 3) v[0] += xor_lane<4>(v[0], lane);
+  if constexpr (L < 4) v[0] += xor_lane<8>(v[0], lane);
+  v[0] += xor_lane<16>(v[0], lane);
+  v[0] += xor_lane<32>(v[0], lane);
+}
+
+// Row whose total lane `lane` holds after wave_reduce_rows<R>: lane bit b
+// decided row bit (L - 1 - b).
+template <int R>
+__device__ __forceinline__ int reduced_row(int lane) {
+  constexpr int L = log2c<R>();
+  int row = 0;
+#pragma unroll
+  for (int b = 0; b < L; ++b) row |= ((lane >> b) & 1) << (L - 1 - b);
+  return row;
+}
+
+// One 1 KiB-per-wave chunk c of K: loads first (x slice, then the weight rows
+// and block exponents), all in flight before any of them is used, then the
+// decode and FMAs into acc. With CLAMP, x reads past cols are clamped to the
+// last element and zeroed after the loads (the codes there are zero).
+template <int DT, bool BLK, int R, int MATS, bool VECX, bool CLAMP>
+__device__ __forceinline__ void gemv_chunk(int c, int lane, int cols, const float* __restrict__ x,
+                                           const uint8_t* __restrict__ w0,
+                                           const uint8_t* __restrict__ w1,
+                                           const uint8_t* __restrict__ e0,
+                                           const uint8_t* __restrict__ e1, uint32_t pitch,
+                                           uint32_t nblk, float (&acc)[MATS][R]) {
+  constexpr int KS = Codec<DT>::KS;
+  const int k0 = c * 64 * KS + lane * KS;
+  float xr[KS];
+  if constexpr (VECX) {
+#pragma unroll
+    for (int i = 0; i < KS; i += 4) {
+      const int k = k0 + i;
+      const float4 t = *reinterpret_cast<const float4*>(x + (!CLAMP || k < cols ? k : cols - 4));
+      xr[i] = t.x, xr[i + 1] = t.y, xr[i + 2] = t.z, xr[i + 3] = t.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < KS; ++i) xr[i] = x[!CLAMP || k0 + i < cols ? k0 + i : cols - 1];
+  }
+  // 32-bit offsets from the wave-uniform row-group bases: one add per row
+  // and loads addressed as scalar base + vector offset
+  const uint32_t boff = (uint32_t)c * 1024u + (uint32_t)lane * 16u;
+  const uint32_t eoff = (uint32_t)k0 >> 5;
+  uint4 q[MATS][R];
+  uint8_t e[MATS][R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    q[0][r] = load_stream(w0 + (r * pitch + boff));
+    if constexpr (MATS == 2) q[1][r] = load_stream(w1 + (r * pitch + boff));
+    if constexpr (BLK) {
+      e[0][r] = e0[r * nblk + eoff];
+      if constexpr (MATS == 2) e[1][r] = e1[r * nblk + eoff];
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  float xv[KS];
+#pragma unroll
+  for (int i = 0; i < KS; ++i) xv[i] = !CLAMP || k0 + i < cols ? xr[i] : 0.0f;
+#pragma unroll
+  for (int m = 0; m < MATS; ++m) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float p = dot_chunk<DT>(q[m][r], xv);
+      if constexpr (BLK) acc[m][r] = fmaf(p, pow2f((int)e[m][r] - 127), acc[m][r]);
+      else acc[m][r] += p;
+    }
+  }
 }
 
 // MATS = 1: y = W x with the Dense epilogue into pre/post.
@@ -131,9 +235,32 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemv(GemvArgs a) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int r0 = blockIdx.x * R;
-  const int b = blockIdx.y;
-  const float* __restrict__ x = a.x + (size_t)b * a.x_stride;
-  const int nchunks = (a.kpad + 64 * KS - 1) / (64 * KS);
+  // Every argument the K loop uses is read before its first branch, so the
+  // scalar loads of the argument block are issued together and waited on
+  // once (otherwise the loop guard is loaded first and the pointers after).
+  const int kpad = a.kpad, cols = a.cols;
+  const uint32_t nblk = (uint32_t)a.nblk, pitch = (uint32_t)a.pitch;
+  const float* __restrict__ x = a.x + (size_t)blockIdx.y * a.x_stride;
+  const uint8_t* __restrict__ w0 = a.codes[0] + (size_t)r0 * pitch;
+  const uint8_t* __restrict__ w1 = a.codes[MATS - 1] + (size_t)r0 * pitch;
+  const uint8_t* __restrict__ e0 = BLK ? a.blk[0] + (size_t)r0 * nblk : nullptr;
+  const uint8_t* __restrict__ e1 = BLK ? a.blk[MATS - 1] + (size_t)r0 * nblk : nullptr;
+
+  asm volatile("" ::"s"(kpad), "s"(cols), "s"(nblk), "s"(pitch), "s"(x), "s"(w0), "s"(w1),
+               "s"(e0), "s"(e1));
+  const int nchunks = (kpad + 64 * KS - 1) / (64 * KS);
+  // The R row scales of this group are wave-uniform; they are read through
+  // the constant address space so they become scalar loads (own counter, so
+  // no vector-memory wait in the K loop covers them), finished long before
+  // the epilogue. The scale array is padded to the row padding, a multiple
+  // of R.
+  float scs[MATS][R];
+#pragma unroll
+  for (int m = 0; m < MATS; ++m) {
+    const ConstF32 sp = (ConstF32)a.scale[m];  // address-space cast: C-style only
+#pragma unroll
+    for (int r = 0; r < R; ++r) scs[m][r] = sp[r0 + r];
+  }
 
   float acc[MATS][R];
 #pragma unroll
@@ -142,41 +269,12 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemv(GemvArgs a) {
     for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
 
   for (int c = wave; c < nchunks; c += WAVES) {
-    const int k0 = c * 64 * KS + lane * KS;
-    if (k0 >= a.kpad) continue;
-    float xv[KS];
-    if constexpr (VECX) {
-#pragma unroll
-      for (int i = 0; i < KS; i += 4) {
-        float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (k0 + i < a.cols) t = *reinterpret_cast<const float4*>(x + k0 + i);
-        xv[i] = t.x, xv[i + 1] = t.y, xv[i + 2] = t.z, xv[i + 3] = t.w;
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < KS; ++i) xv[i] = (k0 + i < a.cols) ? x[k0 + i] : 0.0f;
-    }
-    const size_t boff = (size_t)c * 1024 + (size_t)lane * 16;
-    uint4 q[MATS][R];
-#pragma unroll
-    for (int m = 0; m < MATS; ++m)
-#pragma unroll
-      for (int r = 0; r < R; ++r)
-        q[m][r] = load_stream(a.codes[m] + (size_t)(r0 + r) * a.pitch + boff);
-    // every weight load of this chunk is in flight before any decode starts
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int m = 0; m < MATS; ++m) {
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const float p = dot_chunk<DT>(q[m][r], xv);
-        if constexpr (BLK) {
-          const uint8_t e = a.blk[m][(size_t)(r0 + r) * a.nblk + (k0 >> 5)];
-          acc[m][r] = fmaf(p, pow2f((int)e - 127), acc[m][r]);
-        } else {
-          acc[m][r] += p;
-        }
-      }
+    // Chunks wholly inside cols (all but a ragged last one) read x without
+    // clamps or selects; the test is wave-uniform.
+    if ((c + 1) * 64 * KS <= cols) {
+      gemv_chunk<DT, BLK, R, MATS, VECX, false>(c, lane, cols, x, w0, w1, e0, e1, pitch, nblk, acc);
+    } else if (c * 64 * KS + lane * KS < kpad) {
+      gemv_chunk<DT, BLK, R, MATS, VECX, true>(c, lane, cols, x, w0, w1, e0, e1, pitch, nblk, acc);
     }
   }
 
@@ -184,22 +282,24 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemv(GemvArgs a) {
 #pragma unroll
   for (int m = 0; m < MATS; ++m) {
     wave_reduce_rows<R>(acc[m], lane);
-    constexpr int shift = 6 - log2c<R>();
-    if ((lane & ((1 << shift) - 1)) == 0) part[m][wave][(lane >> shift) & (R - 1)] = acc[m][0];
+    if (lane < R) part[m][wave][reduced_row<R>(lane)] = acc[m][0];
   }
   __syncthreads();
-  if (threadIdx.x >= R) return;
-  const int o = r0 + threadIdx.x;
-  if (o >= a.rows) return;
+  const int t = threadIdx.x;
+  const int o = r0 + t;
+  if (t >= R || o >= a.rows) return;
   float tot[MATS];
 #pragma unroll
   for (int m = 0; m < MATS; ++m) {
-    float t = part[m][0][threadIdx.x];
+    float sum = part[m][0][t];
 #pragma unroll
-    for (int w = 1; w < WAVES; ++w) t += part[m][w][threadIdx.x];
-    tot[m] = t * a.scale[m][o];
+    for (int w = 1; w < WAVES; ++w) sum += part[m][w][t];
+    float sc = scs[m][0];
+#pragma unroll
+    for (int r = 1; r < R; ++r) sc = t == r ? scs[m][r] : sc;
+    tot[m] = sum * sc;
   }
-  const size_t oi = (size_t)b * a.out_stride + o;
+  const size_t oi = (size_t)blockIdx.y * a.out_stride + o;
   if constexpr (MATS == 2) {
     const float g = (float)act_f64(kSilu, (double)tot[0]);
     a.pre[oi] = (float)((double)g * (double)tot[1]);
