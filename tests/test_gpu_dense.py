@@ -64,7 +64,7 @@ def test_release_smoke_known_answer(gpu):
 ])
 def test_integer_exact_bit_for_bit(gpu, oracle, dt, values):
     rng = np.random.default_rng(dt)
-    for rows, cols, batch in [(129, 1000, 1), (64, 4096, 1), (5, 77, 3)]:
+    for rows, cols, batch in [(129, 1000, 1), (64, 4096, 1), (5, 77, 3), (9, 300, 9)]:
         W = rng.choice(np.array(values, np.float32), (rows, cols))
         x = rng.integers(-4, 5, (batch, cols)).astype(np.float32)
         pre, post = run(gpu, dt, 0, W, x)
