@@ -1,20 +1,29 @@
 """Throughput of the quantized-weight Dense hot path on one MI355X.
 
-Workload (default): Dense GEMV 4096 -> 4096, FP8 E4M3 weights with one fp32
+Default workload (c2): Dense GEMV 4096 -> 4096, FP8 E4M3 weights with one fp32
 scale per output row, fp32 in/out, batch 1. One step = one GEMV over one
 batch. Weights are mounted (quantized on the device) once per copy; 64
 distinct copies (1.07 GB, > 4x the 256 MB MALL) are rotated so each step
-streams its weights from HBM. The steps are captured in a HIP graph so the
-timing measures the GPU, not Python's launch rate.
+streams its weights from HBM. The steps are captured in a HIP graph and timed
+with HIP events on the launch stream.
 
-Metric: algorithmic bytes / time, with bytes = codes + row scales + x + y
-= 16,826,368 B per step (TFLOPS reported beside it). The CPU baseline is the
-oracle's restatement of the reference contract (f64 decode, f64 serial-K
+Metric: algorithmic bytes / time for the HBM-bound GEMV workloads (bytes =
+codes + scales + x + y, 16,826,368 B per c2 step), useful FLOP/s (2*M*N*K)
+for the matrix-core GEMM workloads. The CPU baseline is the oracle's
+restatement of the reference contract (f64 decode at mount, f64 serial-K
 matvec) on this host's cores, timed on a bounded sample of the same workload.
+
+Other workloads (--config), each its own line:
+  c1     Dense 512 -> 512, E4M3, per-tensor scale, batch 1
+  c3     SwiGLU 4096 / 11008, FP4 E2M1 + E8M0 per 32, batch 1 (c3b16: batch 16)
+  c4     MHA projection GEMM: 4096 tokens x 1024 -> 1024, E5M2 per-row scales
+  c4mha  whole MHA layer: B=8, S=512, d=1024, 16 heads x 64, causal, RoPE
+  c5     64 cells x (Dense 1024^2 E4M3 row -> FP4 block-32 -> E4M3 row), batch 256
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2]
 """
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -24,6 +33,10 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "welvet.cuda_amd"))
 
 HBM_PEAK_GBS = 8000.0
+# dense MFMA peak of the f8f6f4 instruction with an FP8 operand (the activation
+# terms are E4M3, so FP4 weights run at the FP8 rate)
+MFMA_FP8_PEAK_TFLOPS = 5000.0
+METRIC = "FP8/FP4 Dense GEMV GB/s + GEMM TFLOPS (% roofline), 1 MI355X vs host CPU"
 
 # rocprof summaries (kernel stats + FETCH_SIZE/WRITE_SIZE scaled by a copy of
 # known size) per workload; `traffic_bytes:` is the measured HBM bytes per launch.
@@ -42,47 +55,247 @@ def measured_traffic(config):
     return None
 
 
-def workloads():
-    # name: (desc, dtype, scheme, batch, in, out, algorithmic bytes, flops)
-    d = {}
-    K = N = 4096
-    d["c2"] = ("dense_gemv_4096x4096_fp8e4m3_rowscale_b1", 4, 2, 1, K, N,
-               N * K + 4 * N + 4 * K + 4 * N, 2 * N * K)
-    d["c1"] = ("dense_512x512_fp8e4m3_tensorscale_b1", 4, 1, 1, 512, 512,
-               512 * 512 + 4 + 4 * 512 + 4 * 512, 2 * 512 * 512)
-    return d
-
-
-def cpu_baseline(dtype, scheme, batch, K, N, W, x, nbytes, budget_s=10.0):
+def oracle():
     sys.path.insert(0, os.path.join(ROOT, "tests"))
-    import numpy as np
-
     import oracle_lib
 
-    orc = oracle_lib.Oracle()
-    native, rs, blk = orc.quantize(dtype, scheme, N, K, W)
-    threads = max(1, min(16, os.cpu_count() or 1))
-    y = np.zeros((batch, N), np.float32)
-    import ctypes
+    return oracle_lib.Oracle()
 
+
+def cpu_dense_seconds(orc, dtype, scheme, batch, K, N, W, x, threads, budget_s):
+    """Seconds per execute of the oracle's reference-contract Dense (f64 W)."""
+    import numpy as np
+
+    native, rs, blk = orc.quantize(dtype, scheme, N, K, W)
+    y = np.zeros((batch, N), np.float32)
     mount = ctypes.c_double()
     u8 = ctypes.POINTER(ctypes.c_uint8)
     fp = ctypes.POINTER(ctypes.c_float)
+    x = np.ascontiguousarray(x, np.float32)
     args = (dtype, scheme, batch, K, N, native.ctypes.data_as(u8), rs.ctypes.data_as(fp),
             blk.ctypes.data_as(u8), x.ctypes.data_as(fp), y.ctypes.data_as(fp), threads)
-    t1 = orc.L.or_cpu_dense_bench(*args, 1, 3, ctypes.byref(mount))
-    iters = max(3, int(budget_s / max(t1, 1e-6)))
-    per = orc.L.or_cpu_dense_bench(*args, 2, iters, ctypes.byref(mount))
-    return {
-        "value": round(nbytes / per / 1e9, 3),
-        "unit": "GB/s",
-        "cores": threads,
-        "kind": "port",
-        "sample": (f"oracle restatement of the reference Dense contract on this host: f64 decode "
-                   f"of the codes ({mount.value * 1e3:.0f} ms mount), then {iters} f64 serial-K "
-                   f"matvecs {N}x{K} batch {batch} split over {threads} threads, "
-                   f"{per * 1e3:.3f} ms each"),
-    }
+    t1 = orc.L.or_cpu_dense_bench(*args, 1, 1, ctypes.byref(mount))
+    iters = max(2, int(budget_s / max(t1, 1e-6)))
+    return orc.L.or_cpu_dense_bench(*args, 1, iters, ctypes.byref(mount)), iters, mount.value
+
+
+def cpu_threads():
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+# --------------------------------------------------------------------------
+# workloads: each builds its sessions and returns a dict with
+#   desc, enqueue(i, stream), per_graph, bytes, flops, bound, dtype, config,
+#   cpu(budget_s) -> cpu_baseline dict, close()
+
+
+def dense_workload(pw, hip, name, cfg_id, dtype, scheme, batch, K, N, copies, bound):
+    import numpy as np
+
+    seed = pw.seed_for(cfg_id)
+    W = pw.normal(seed, N * K, 1 / np.sqrt(K)).reshape(N, K)
+    x = pw.normal(seed + 500, batch * K).reshape(batch, K)
+    sessions = [pw.DenseSession(batch, K, N, -1, dtype, scheme, W) for _ in range(copies)]
+    dx = hip.upload(x)
+    dy = hip.malloc(batch * N * 4)
+    b = 1 if dtype != 16 else 0.5
+    scale_bytes = 4 * N if scheme in (1, 2) else (N * ((K + 31) // 32) if scheme == 3 else 0)
+    nbytes = int(N * K * b) + scale_bytes + 4 * batch * K + 4 * batch * N
+    flops = 2 * batch * N * K
+    dname = {4: "fp8e4m3", 5: "fp8e5m2", 16: "fp4e2m1"}[dtype]
+    sname = {0: "none", 1: "per-tensor fp32", 2: "per-row fp32", 3: "e8m0 per 32"}[scheme]
+
+    def enqueue(i, stream):
+        sessions[i % copies].execute_device(dx, dy, dy, stream)
+
+    def cpu(budget_s):
+        orc = oracle()
+        rows = min(batch, 256)
+        per, iters, mount = cpu_dense_seconds(orc, dtype, scheme, rows, K, N, W, x[:rows],
+                                              cpu_threads(), budget_s)
+        per_step = per * batch / rows
+        val = (nbytes / per_step / 1e9) if bound == "hbm" else (flops / per_step / 1e12)
+        return {"value": round(val, 4), "unit": "GB/s" if bound == "hbm" else "TFLOP/s",
+                "cores": cpu_threads(), "kind": "port",
+                "sample": (f"oracle restatement of the reference Dense contract on this host: f64 "
+                           f"decode of the codes ({mount * 1e3:.0f} ms mount), then {iters} f64 "
+                           f"serial-K executes {N}x{K} of {rows} of the {batch} rows over "
+                           f"{cpu_threads()} threads, {per * 1e3:.3f} ms each"
+                           + (f", scaled x{batch // rows} to the full batch" if rows < batch else ""))}
+
+    def close():
+        for s in sessions:
+            s.close()
+        hip.free(dx)
+        hip.free(dy)
+
+    return {"desc": name, "enqueue": enqueue, "per_graph": copies, "bytes": nbytes,
+            "flops": flops, "bound": bound, "dtype": dname,
+            "config": {"workload": name, "in": K, "out": N, "batch": batch, "scale": sname,
+                       "weight_copies_rotated": copies},
+            "cpu": cpu, "close": close}
+
+
+def swiglu_workload(pw, hip, name, batch, copies):
+    import numpy as np
+
+    d, f = 4096, 11008
+    seed = pw.seed_for(3)
+    G = pw.normal(seed, f * d, 1 / np.sqrt(d)).reshape(f, d)
+    U = pw.normal(seed + 1, f * d, 1 / np.sqrt(d)).reshape(f, d)
+    D = pw.normal(seed + 2, d * f, 1 / np.sqrt(f)).reshape(d, f)
+    x = pw.normal(seed + 500, batch * d).reshape(batch, d)
+    sessions = [pw.SwiGLUSession(batch, 1, d, f, 16, 3, G, U, D) for _ in range(copies)]
+    dx = hip.upload(x)
+    dh = hip.malloc(batch * f * 4)
+    dy = hip.malloc(batch * d * 4)
+    codes = 3 * f * d // 2
+    e8m0 = 2 * f * (d // 32) + d * ((f + 31) // 32)
+    # h is materialized: written by gate/up, read by down
+    nbytes = codes + e8m0 + batch * (4 * d + 4 * d + 2 * 4 * f)
+    flops = 2 * batch * 3 * f * d
+
+    def enqueue(i, stream):
+        sessions[i % copies].execute_device(dx, dh, dy, stream)
+
+    def cpu(budget_s):
+        orc = oracle()
+        t = 0.0
+        parts = []
+        for (K, N, Wm) in ((d, f, G), (d, f, U), (f, d, D)):
+            xs = x if K == d else np.random.default_rng(1).standard_normal((batch, f)).astype(np.float32)
+            per, iters, _ = cpu_dense_seconds(orc, 16, 3, batch, K, N, Wm, xs, cpu_threads(),
+                                              budget_s / 3)
+            t += per
+            parts.append(f"{N}x{K}: {per * 1e3:.2f} ms ({iters} runs)")
+        return {"value": round(nbytes / t / 1e9, 4), "unit": "GB/s", "cores": cpu_threads(),
+                "kind": "port",
+                "sample": ("oracle restatement of the reference Dense contract (f64 W, serial K) "
+                           "for gate, up and down at batch " + str(batch) + " over "
+                           + str(cpu_threads()) + " threads: " + "; ".join(parts)
+                           + " (SiLU product not timed)")}
+
+    def close():
+        for s in sessions:
+            s.close()
+        for p in (dx, dh, dy):
+            hip.free(p)
+
+    return {"desc": name, "enqueue": enqueue, "per_graph": copies, "bytes": nbytes,
+            "flops": flops, "bound": "hbm", "dtype": "fp4e2m1",
+            "config": {"workload": name, "d_model": d, "d_ff": f, "batch": batch,
+                       "scale": "e8m0 per 32", "weight_copies_rotated": copies,
+                       "h_materialized": True},
+            "cpu": cpu, "close": close}
+
+
+def mha_workload(pw, hip, name):
+    import numpy as np
+
+    B, S, d, H, hd = 8, 512, 1024, 16, 64
+    seed = pw.seed_for(4)
+    Ws = [pw.normal(seed + i, d * d, 1 / np.sqrt(d)).reshape(d, d) for i in range(4)]
+    x = pw.normal(seed + 500, B * S * d).reshape(B * S, d)
+    s = pw.MHASession(B, S, d, H, H, hd, S, 1, 0, 5, 2, *Ws)
+    dx = hip.upload(x)
+    da = hip.malloc(B * S * d * 4)
+    dy = hip.malloc(B * S * d * 4)
+    proj = 4 * 2 * B * S * d * d
+    # attention under the reference's semantics: query t sees keys [0, b*S + s]
+    pairs = sum(sum(b * S + s_ + 1 for s_ in range(S)) for b in range(B))
+    att = pairs * H * hd * 4
+    nbytes = 4 * (d * d + 4 * d) + 4 * B * S * d * 3
+
+    def enqueue(i, stream):
+        s.execute_device(dx, da, dy, stream)
+
+    def close():
+        s.close()
+        for p in (dx, da, dy):
+            hip.free(p)
+
+    return {"desc": name, "enqueue": enqueue, "per_graph": 4, "bytes": nbytes,
+            "flops": proj + att, "bound": "mfma", "dtype": "fp8e5m2",
+            "config": {"workload": name, "batch": B, "seq": S, "d_model": d, "heads": H,
+                       "head_dim": hd, "mask": "causal", "pos": "rope",
+                       "projection_flops": proj, "attention_flops": att},
+            "cpu": None, "close": close}
+
+
+def cells_workload(pw, hip, name):
+    import numpy as np
+
+    cells, batch, d = 64, 256, 1024
+    kinds = [(4, 2), (16, 3), (4, 2)]
+    sessions, bufs = [], []
+    for c in range(cells):
+        seed = pw.seed_for(5, c)
+        row = []
+        for li, (dt, sc) in enumerate(kinds):
+            W = pw.normal(seed + 10 * li, d * d, 1 / np.sqrt(d)).reshape(d, d)
+            row.append(pw.DenseSession(batch, d, d, -1, dt, sc, W))
+        sessions.append(row)
+        x = pw.normal(seed + 500, batch * d).reshape(batch, d)
+        bufs.append([hip.upload(x)] + [hip.malloc(batch * d * 4) for _ in kinds])
+    flops = cells * len(kinds) * 2 * batch * d * d
+
+    def enqueue(i, stream):
+        for c in range(cells):
+            b = bufs[c]
+            for li in range(len(kinds)):
+                sessions[c][li].execute_device(b[li], b[li + 1], b[li + 1], stream)
+
+    def cpu(budget_s):
+        orc = oracle()
+        t = 0.0
+        rng = np.random.default_rng(5)
+        for dt, sc in kinds:
+            W = rng.standard_normal((d, d)).astype(np.float32) / 32
+            xs = rng.standard_normal((batch, d)).astype(np.float32)
+            per, _, _ = cpu_dense_seconds(orc, dt, sc, batch, d, d, W, xs, cpu_threads(),
+                                          budget_s / 3)
+            t += per
+        per_step = t * cells
+        return {"value": round(flops / per_step / 1e12, 5), "unit": "TFLOP/s",
+                "cores": cpu_threads(), "kind": "port",
+                "sample": (f"oracle restatement of the reference Dense contract for one cell "
+                           f"(3 layers 1024x1024 at batch {batch}, {t * 1e3:.1f} ms over "
+                           f"{cpu_threads()} threads), scaled x{cells} to the 64 cells")}
+
+    def close():
+        for row in sessions:
+            for s in row:
+                s.close()
+        for b in bufs:
+            for p in b:
+                hip.free(p)
+
+    return {"desc": name, "enqueue": enqueue, "per_graph": 1, "bytes": None, "flops": flops,
+            "bound": "mfma", "dtype": "fp8e4m3+fp4e2m1",
+            "config": {"workload": name, "cells": cells, "layers_per_cell": 3, "batch": batch,
+                       "width": d, "layer_kinds": "E4M3 per-row, FP4 E8M0/32, E4M3 per-row"},
+            "cpu": cpu, "close": close}
+
+
+def make_workload(pw, hip, config, copies):
+    if config == "c2":
+        return dense_workload(pw, hip, "dense_gemv_4096x4096_fp8e4m3_rowscale_b1", 2, 4, 2, 1,
+                              4096, 4096, copies, "hbm")
+    if config == "c1":
+        return dense_workload(pw, hip, "dense_512x512_fp8e4m3_tensorscale_b1", 1, 4, 1, 1,
+                              512, 512, copies, "hbm")
+    if config == "c3":
+        return swiglu_workload(pw, hip, "swiglu_4096x11008_fp4_e8m0_b1", 1, min(copies, 8))
+    if config == "c3b16":
+        return swiglu_workload(pw, hip, "swiglu_4096x11008_fp4_e8m0_b16", 16, min(copies, 8))
+    if config == "c4":
+        return dense_workload(pw, hip, "mha_projection_gemm_4096x1024x1024_fp8e5m2_rowscale", 4,
+                              5, 2, 4096, 1024, 1024, min(copies, 4), "mfma")
+    if config == "c4mha":
+        return mha_workload(pw, hip, "mha_layer_b8_s512_d1024_h16_fp8e5m2_rowscale")
+    if config == "c5":
+        return cells_workload(pw, hip, "volume_64_cells_3x_dense_1024_b256")
+    raise SystemExit(f"unknown config {config}")
 
 
 def copy_calibration(pw, nbytes, steps):
@@ -106,12 +319,16 @@ def copy_calibration(pw, nbytes, steps):
     hip.free(dst)
 
 
+CONFIGS = ["c1", "c2", "c3", "c3b16", "c4", "c4mha", "c5"]
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=1280)
-    ap.add_argument("--warmup", type=int, default=128)
-    ap.add_argument("--config", default="c2", choices=sorted(workloads()))
+    ap.add_argument("--steps", type=int, default=None,
+                    help="timed steps (default: 1280 for the GEMV workloads, fewer for the rest)")
+    ap.add_argument("--warmup", type=int, default=None)
+    ap.add_argument("--config", default="c2", choices=CONFIGS)
     ap.add_argument("--copies", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -128,31 +345,28 @@ def main():
     import pywelvet as pw
 
     if args.copy_calibration:
-        copy_calibration(pw, args.copy_calibration << 20, args.steps)
+        copy_calibration(pw, args.copy_calibration << 20, args.steps or 10)
         return
 
-    desc, dtype, scheme, batch, K, N, nbytes, flops = workloads()[args.config]
     pw.check(pw.lib().welvet_cuda_init())
     hip = pw.Hip()
-    seed = pw.seed_for(2 if args.config == "c2" else 1)
-    W = pw.normal(seed, N * K, 1 / np.sqrt(K)).reshape(N, K)
-    x = pw.normal(seed + 500, batch * K).reshape(batch, K)
-    copies = max(1, args.copies)
-    sessions = [pw.DenseSession(batch, K, N, -1, dtype, scheme, W) for _ in range(copies)]
-    dx = hip.upload(x)
-    dy = hip.malloc(batch * N * 4)
+    wl = make_workload(pw, hip, args.config, max(1, args.copies))
+    gemv = args.config in ("c1", "c2", "c3", "c3b16")
+    steps = args.steps if args.steps is not None else (1280 if gemv else 64)
+    warmup = args.warmup if args.warmup is not None else (128 if gemv else 8)
+    per = max(1, min(wl["per_graph"], steps))
     stream = hip.stream()
 
     def enqueue(n):
         def go():
             for i in range(n):
-                sessions[i % copies].execute_device(dx, dy, dy, stream)
+                wl["enqueue"](i, stream)
         return go
 
-    full, rem = divmod(args.steps, copies)
-    g_full = hip.capture(stream, enqueue(copies))
+    full, rem = divmod(steps, per)
+    g_full = hip.capture(stream, enqueue(per))
     g_rem = hip.capture(stream, enqueue(rem)) if rem else None
-    for _ in range(max(1, (args.warmup + copies - 1) // copies)):
+    for _ in range(max(1, (warmup + per - 1) // per)):
         hip.launch(g_full, stream)
     hip.sync()
     e0, e1 = hip.event(), hip.event()
@@ -166,40 +380,46 @@ def main():
     hip.sync()
     t_wall = time.perf_counter() - t_wall
     ms = hip.elapsed_ms(e0, e1)
-    per_step_s = ms * 1e-3 / args.steps
-    gbs = nbytes / per_step_s / 1e9
-    y = hip.download(dy, (batch, N))
-    assert np.all(np.isfinite(y))
+    per_step_s = ms * 1e-3 / steps
 
-    cpu = None if args.no_cpu else cpu_baseline(dtype, scheme, batch, K, N, W, x, nbytes)
+    tflops = wl["flops"] / per_step_s / 1e12
+    gbs = wl["bytes"] / per_step_s / 1e9 if wl["bytes"] else None
+    if wl["bound"] == "hbm":
+        value, unit = gbs, "GB/s"
+        roof = {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(args.config)}
+    else:
+        value, unit = tflops, "TFLOP/s"
+        roof = {"bound": "mfma", "achieved": round(tflops, 3), "peak": MFMA_FP8_PEAK_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(tflops / MFMA_FP8_PEAK_TFLOPS, 4),
+                "traffic": measured_traffic(args.config)}
+    cpu = None if (args.no_cpu or wl["cpu"] is None) else wl["cpu"](10.0)
+    config = dict(wl["config"])
+    config.update({"tflops": round(tflops, 4), "wall_s": round(t_wall, 4)})
+    if wl["bytes"]:
+        config.update({"algorithmic_bytes_per_step": wl["bytes"], "gbs": round(gbs, 2)})
     line = {
-        "metric": "FP8/FP4 Dense GEMV GB/s + GEMM TFLOPS (% roofline), 1 MI355X vs host CPU",
-        "value": round(gbs, 2),
-        "unit": "GB/s",
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": unit,
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms / args.steps, 6),
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(ms / steps, 6),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp8e4m3",
+        "dtype": wl["dtype"],
         "data": "synthetic (seeded splitmix64 normal weights/inputs, random-init)",
-        "config": {"workload": desc, "in": K, "out": N, "batch": batch,
-                   "scale": "per-row fp32" if scheme == 2 else "per-tensor fp32",
-                   "weight_copies_rotated": copies, "algorithmic_bytes_per_step": nbytes,
-                   "tflops": round(flops / per_step_s / 1e12, 4), "wall_s": round(t_wall, 4)},
-        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic(args.config)},
+        "config": config,
+        "roofline": roof,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
     hip.graph_free(g_full)
     if g_rem:
         hip.graph_free(g_rem)
-    for s in sessions:
-        s.close()
+    wl["close"]()
 
 
 if __name__ == "__main__":

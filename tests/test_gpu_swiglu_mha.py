@@ -32,7 +32,8 @@ def oracle_swiglu(oracle, dt, scheme, G, U, D, x):
 
 
 @pytest.mark.parametrize("dt,scheme", [(16, 3), (4, 2), (5, 1), (16, 0)])
-@pytest.mark.parametrize("batch,seq,d,inter", [(1, 1, 64, 160), (2, 3, 96, 200), (16, 1, 128, 352)])
+@pytest.mark.parametrize("batch,seq,d,inter", [(1, 1, 64, 160), (2, 3, 96, 200), (16, 1, 128, 352),
+                                               (40, 2, 96, 200)])
 def test_swiglu_matches_oracle(gpu, oracle, dt, scheme, batch, seq, d, inter):
     rng = np.random.default_rng(d + inter + dt + batch)
     G = (rng.standard_normal((inter, d)) / np.sqrt(d)).astype(np.float32)
@@ -79,6 +80,7 @@ def oracle_mha(oracle, dt, scheme, Q, K, V, O, x, B, S, H, KVH, hd, msl, mask, p
     (2, 6, 32, 2, 2, 16, 2, 1),    # bidirectional, no positions
     (2, 6, 48, 3, 3, 6, 3, 2),     # sliding window (msl), ALiBi
     (1, 9, 64, 4, 1, 9, 4, 3),     # prefix LM (prefix 0), RoPE + ALiBi, MQA
+    (4, 12, 64, 4, 4, 12, 1, 0),   # 48 tokens: projections on the large-tile GEMM
 ])
 def test_mha_matches_oracle(gpu, oracle, B, S, d, H, KVH, msl, mask, pos):
     dt, scheme = 5, 2

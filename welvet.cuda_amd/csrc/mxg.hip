@@ -232,11 +232,264 @@ __global__ __launch_bounds__(kThreads) void k_mxg(MxgArgs p) {
     }
 }
 
+// Large-M tile: 128 activation rows x 128 weight rows (64 per matrix when
+// MATS = 2) per workgroup, 4 waves of 64 x 64 (x 3 terms: 48 MFMAs per wave
+// per 128-wide K step).
+//
+// Operands move global -> LDS with the gfx950 direct-to-LDS loads
+// (global_load_lds_dwordx4: lane i of a wave writes 16 bytes at
+// base + 16 i), double-buffered: while the MFMAs of step s run, step s+1 is
+// copied into the other buffer, with no register staging. LDS rows are
+// unpadded (128 bytes: A terms and FP8 codes; 64 bytes: FP4 codes) and the
+// 16-byte chunks of row r are stored at chunk j ^ ((r >> 1) & 7) (FP4:
+// j ^ ((r >> 2) & 3)), which makes the 16-lane groups of a fragment read hit
+// 16 distinct 16-byte bank groups.
+//
+// Tiles are ordered so that each XCD (workgroups are dealt round-robin to the
+// 8 XCDs) works on a contiguous band of activation rows against all weight
+// tiles: its L2 holds that band of A and the whole weight matrix.
+constexpr int kBM2 = 128;
+
+typedef __attribute__((address_space(3))) void* LdsPtr;
+typedef const __attribute__((address_space(1))) void* GlobalPtr;
+
+// The copy size of the builtin must be a literal.
+__device__ __forceinline__ void lds_dma16(const void* src, void* lds_base) {
+  __builtin_amdgcn_global_load_lds((GlobalPtr)src, (LdsPtr)lds_base, 16, 0, 0);
+}
+__device__ __forceinline__ void lds_dma4(const void* src, void* lds_base) {
+  __builtin_amdgcn_global_load_lds((GlobalPtr)src, (LdsPtr)lds_base, 4, 0, 0);
+}
+
+template <int DT, bool BLK, int MATS>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_mxg2(
+    MxgArgs p, int tiles_m, int tiles_n) {
+  constexpr bool FP4 = DT == kFP4;
+  constexpr int BM = kBM2;
+  constexpr int BNM = MATS == 2 ? 64 : 128;     // weight rows per matrix per tile
+  constexpr int WB = FP4 ? 64 : 128;            // code bytes per weight row per K step
+  constexpr int SM = 4, SN = BNM / 32;          // 16x16 blocks per wave (waves 2 x 2)
+  constexpr int A_BYTES = kTerms * BM * 128;    // one buffer of A terms
+  constexpr int B_BYTES = MATS * BNM * WB;
+  constexpr int A_SEG = A_BYTES / 1024;         // 1 KiB wave copies per step
+  constexpr int B_SEG = B_BYTES / 1024;
+  constexpr int B_RPS = 1024 / WB;              // weight rows per 1 KiB copy
+
+  __shared__ __attribute__((aligned(1024))) uint8_t sa[2][A_BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t sb[2][B_BYTES];
+  __shared__ __attribute__((aligned(256))) uint32_t ssa[2][kTerms * BM];
+  __shared__ __attribute__((aligned(256))) uint32_t ssb[2][MATS * BNM];
+
+  const int T = tiles_m * tiles_n;
+  const int b = blockIdx.x;
+  const int lt = (T % 8 == 0) ? (b % 8) * (T / 8) + b / 8 : b;
+  const int m0 = (lt / tiles_n) * BM, n0 = (lt % tiles_n) * BNM;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int i16 = lane & 15, g = lane >> 4;
+  const int S = p.kpad / 128;
+  const int nblk_a = p.kpad / 32;
+
+  // Per-lane source of each copy this wave issues (K step 0; step s adds
+  // s * 128 bytes of A / s * WB bytes of codes / s * 4 bytes of exponents).
+  uint32_t aoff[A_SEG / 4], boff[B_SEG / 4 > 0 ? B_SEG / 4 : 1];
+#pragma unroll
+  for (int k = 0; k < A_SEG / 4; ++k) {
+    const int q = wave + 4 * k;                          // segment: 8 rows of one term
+    const int t = q / (BM / 8), row = (q % (BM / 8)) * 8 + lane / 8;
+    const int j = (lane % 8) ^ ((row >> 1) & 7);
+    aoff[k] = (uint32_t)(((size_t)t * p.mpad + m0 + row) * p.kpad + j * 16);
+  }
+  const uint8_t* bbase[B_SEG / 4 > 0 ? B_SEG / 4 : 1];
+#pragma unroll
+  for (int k = 0; k < B_SEG / 4; ++k) {
+    const int q = wave + 4 * k;
+    const int row = q * B_RPS + lane / (WB / 16);       // tile row (both matrices)
+    const int jj = lane % (WB / 16);
+    const int j = FP4 ? (jj ^ ((row >> 2) & 3)) : (jj ^ ((row >> 1) & 7));
+    bbase[k] = p.codes[row / BNM];
+    boff[k] = (uint32_t)((size_t)(n0 + row % BNM) * p.pitch + j * 16);
+  }
+  // exponent copies (one dword per lane): A terms 6 x 64, weights 2 x 64
+  const int ea0 = wave * 64 + lane, ea1 = (wave + 4) * 64 + lane;
+  const uint32_t asoff0 = (uint32_t)(((size_t)(ea0 / BM) * p.mpad + m0 + ea0 % BM) * nblk_a);
+  const bool has_a1 = wave + 4 < kTerms * BM / 64;
+  const uint32_t asoff1 =
+      has_a1 ? (uint32_t)(((size_t)(ea1 / BM) * p.mpad + m0 + ea1 % BM) * nblk_a) : 0u;
+  const bool has_b = BLK && wave < MATS * BNM / 64;
+  const uint8_t* bsrc = has_b ? p.blk[(wave * 64 + lane) / BNM] +
+                                    (size_t)(n0 + (wave * 64 + lane) % BNM) * p.nblk
+                              : nullptr;
+  if constexpr (!BLK) {
+    for (int i = tid; i < 2 * MATS * BNM; i += kThreads) (&ssb[0][0])[i] = 0x7F7F7F7Fu;
+  }
+
+  auto issue = [&](int s, int buf) {
+#pragma unroll
+    for (int k = 0; k < A_SEG / 4; ++k)
+      lds_dma16(p.a + (aoff[k] + (uint32_t)s * 128u), &sa[buf][(wave + 4 * k) * 1024]);
+#pragma unroll
+    for (int k = 0; k < B_SEG / 4; ++k)
+      lds_dma16(bbase[k] + (boff[k] + (uint32_t)s * WB), &sb[buf][(wave + 4 * k) * 1024]);
+    lds_dma4(p.as + (asoff0 + s * 4), &ssa[buf][wave * 64]);
+    if (has_a1) lds_dma4(p.as + (asoff1 + s * 4), &ssa[buf][(wave + 4) * 64]);
+    if (has_b) lds_dma4(bsrc + s * 4, &ssb[buf][wave * 64]);
+  };
+
+  v4f acc[MATS][SM][SN];
+#pragma unroll
+  for (int m = 0; m < MATS; ++m)
+#pragma unroll
+    for (int a = 0; a < SM; ++a)
+#pragma unroll
+      for (int c = 0; c < SN; ++c) acc[m][a][c] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  issue(0, 0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int s = 0; s < S; ++s) {
+    const int cur = s & 1;
+    v8i bf[MATS][SN];
+    int bsc[MATS][SN];
+#pragma unroll
+    for (int m = 0; m < MATS; ++m)
+#pragma unroll
+      for (int c = 0; c < SN; ++c) {
+        const int row = m * BNM + wn * (BNM / 2) + c * 16 + i16;
+        int4 lo, hi = make_int4(0, 0, 0, 0);
+        if constexpr (FP4) {
+          lo = *reinterpret_cast<const int4*>(&sb[cur][row * 64 + ((g ^ ((row >> 2) & 3)) * 16)]);
+        } else {
+          const int sw = (row >> 1) & 7;
+          lo = *reinterpret_cast<const int4*>(&sb[cur][row * 128 + ((g ^ sw) * 16)]);
+          hi = *reinterpret_cast<const int4*>(&sb[cur][row * 128 + (((4 + g) ^ sw) * 16)]);
+        }
+        bf[m][c] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+        bsc[m][c] = (int)((ssb[cur][row] >> (8 * g)) & 0xFFu);
+      }
+    v8i af[kTerms][SM];
+    int asc[kTerms][SM];
+#pragma unroll
+    for (int t = 0; t < kTerms; ++t)
+#pragma unroll
+      for (int a = 0; a < SM; ++a) {
+        const int row = t * BM + wm * 64 + a * 16 + i16;
+        const int sw = (row >> 1) & 7;
+        const int4 lo = *reinterpret_cast<const int4*>(&sa[cur][row * 128 + ((g ^ sw) * 16)]);
+        const int4 hi = *reinterpret_cast<const int4*>(&sa[cur][row * 128 + (((4 + g) ^ sw) * 16)]);
+        af[t][a] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+        asc[t][a] = (int)((ssa[cur][row] >> (8 * g)) & 0xFFu);
+      }
+    // the next step streams into the other buffer while the MFMAs run (that
+    // buffer's last readers finished before the previous barrier)
+    if (s + 1 < S) issue(s + 1, cur ^ 1);
+    // keep the copies ahead of the MFMAs and the wait + barrier behind them
+    // (the MFMAs touch only registers, so the scheduler could otherwise move
+    // them past the barrier and expose the copy latency every step)
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 0; t < kTerms; ++t)
+#pragma unroll
+      for (int a = 0; a < SM; ++a)
+#pragma unroll
+        for (int m = 0; m < MATS; ++m)
+#pragma unroll
+          for (int c = 0; c < SN; ++c)
+            acc[m][a][c] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                bf[m][c], af[t][a], acc[m][a][c], wfmt<DT>(), 0, 0, bsc[m][c], 0, asc[t][a]);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+
+  // Epilogue. The weights are the MFMA's first operand, so a lane holds
+  // output row m = i16 of each block and the 4 consecutive columns 4g..4g+3:
+  // one 16-byte store per lane and block when the output allows it. The
+  // scale arrays are padded to the row padding, so the float4 scale loads
+  // stay in bounds.
+  const bool vec_out = (p.out_stride & 3) == 0 && ((reinterpret_cast<uintptr_t>(p.pre) & 15) == 0) &&
+                       ((reinterpret_cast<uintptr_t>(p.post) & 15) == 0);
+#pragma unroll
+  for (int a = 0; a < SM; ++a)
+#pragma unroll
+    for (int c = 0; c < SN; ++c) {
+      const int mrow = m0 + wm * 64 + a * 16 + i16;
+      const int nb = n0 + wn * (BNM / 2) + c * 16 + 4 * g;
+      if (mrow >= p.M || nb >= p.N) continue;
+      float4 sc[MATS];
+#pragma unroll
+      for (int m = 0; m < MATS; ++m) sc[m] = *reinterpret_cast<const float4*>(p.scale[m] + nb);
+      float pre[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float s0 = r == 0 ? sc[0].x : r == 1 ? sc[0].y : r == 2 ? sc[0].z : sc[0].w;
+        if constexpr (MATS == 2) {
+          const float s1 = r == 0 ? sc[1].x : r == 1 ? sc[1].y : r == 2 ? sc[1].z : sc[1].w;
+          const float gv = acc[0][a][c][r] * s0, uv = acc[1][a][c][r] * s1;
+          const float gs = (float)act_f64(kSilu, (double)gv);
+          pre[r] = (float)((double)gs * (double)uv);
+        } else {
+          pre[r] = acc[0][a][c][r] * s0;
+        }
+      }
+      // Dense with bias or activation: pre holds y here; the second pass
+      // below rewrites it (pre = y + bias, post = act) without accumulators
+      // live, so the f64 activation code is not unrolled per element.
+      const bool plain = MATS == 2 || !p.need_epi;
+      const size_t oi = (size_t)mrow * p.out_stride + nb;
+      if (vec_out && nb + 3 < p.N) {
+        const float4 v = make_float4(pre[0], pre[1], pre[2], pre[3]);
+        *reinterpret_cast<float4*>(p.pre + oi) = v;
+        if (plain && MATS == 1 && p.post) *reinterpret_cast<float4*>(p.post + oi) = v;
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          if (nb + r >= p.N) break;
+          p.pre[oi + r] = pre[r];
+          if (plain && MATS == 1 && p.post) p.post[oi + r] = pre[r];
+        }
+      }
+    }
+  if constexpr (MATS == 1) {
+    if (p.need_epi) {
+#pragma unroll 1
+      for (int ac = 0; ac < SM * SN; ++ac) {
+        const int a = ac / SN, c = ac % SN;
+        const int mrow = m0 + wm * 64 + a * 16 + i16;
+        const int nb = n0 + wn * (BNM / 2) + c * 16 + 4 * g;
+        if (mrow >= p.M) continue;
+#pragma unroll 1
+        for (int r = 0; r < 4 && nb + r < p.N; ++r) {
+          const int n = nb + r;
+          const size_t oi = (size_t)mrow * p.out_stride + n;
+          float y = p.pre[oi];
+          double v = (double)y;
+          if (p.bias && n < p.bias_len) {
+            v += p.bias[n];
+            y = (float)v;
+          }
+          p.pre[oi] = y;
+          p.post[oi] = (float)act_f64(p.act, v);
+        }
+      }
+    }
+  }
+}
+
 template <int DT, bool BLK, int MATS>
 Status launch_t(const MxgArgs& p, int bm, hipStream_t st) {
-  const dim3 grid((unsigned)((p.N + kBN - 1) / kBN), (unsigned)(p.mpad / bm));
-  if (bm == 16) k_mxg<DT, BLK, MATS, 16><<<grid, kThreads, 0, st>>>(p);
-  else k_mxg<DT, BLK, MATS, 64><<<grid, kThreads, 0, st>>>(p);
+  if (bm == kBM2) {
+    constexpr int bn = MATS == 2 ? 64 : 128;
+    if ((size_t)kTerms * p.mpad * p.kpad >= (1ull << 31) ||
+        (size_t)round_up(p.N, 128) * p.pitch >= (1ull << 31))
+      return Status::err(kUnsupported, "mxg: operands above 2 GiB");
+    const int tiles_m = p.mpad / kBM2, tiles_n = (p.N + bn - 1) / bn;
+    k_mxg2<DT, BLK, MATS><<<(unsigned)(tiles_m * tiles_n), kThreads, 0, st>>>(p, tiles_m, tiles_n);
+  } else {
+    const dim3 grid((unsigned)((p.N + kBN - 1) / kBN), (unsigned)(p.mpad / bm));
+    k_mxg<DT, BLK, MATS, 16><<<grid, kThreads, 0, st>>>(p);
+  }
   return hip_status(hipGetLastError(), "mxg launch");
 }
 
@@ -252,7 +505,7 @@ Status launch_m(const MxgArgs& p, int dtype, bool blk, int bm, hipStream_t st) {
 
 }  // namespace
 
-int mxg_block_m(int M) { return M <= 16 ? 16 : 64; }
+int mxg_block_m(int M) { return M <= 32 ? 16 : kBM2; }
 
 size_t split_bytes(int M, int kpad) {
   const size_t mpad = (size_t)round_up(M, mxg_block_m(M));
