@@ -238,12 +238,16 @@ def cells_workload(pw, hip, name):
         x = pw.normal(seed + 500, batch * d).reshape(batch, d)
         bufs.append([hip.upload(x)] + [hip.malloc(batch * d * 4) for _ in kinds])
     flops = cells * len(kinds) * 2 * batch * d * d
+    # the 64 cells are independent: layer li of every cell runs as one group
+    # (one split launch and one matrix-core launch per layer position)
+    groups = [pw.DenseGroup([sessions[c][li] for c in range(cells)],
+                            [bufs[c][li] for c in range(cells)],
+                            [bufs[c][li + 1] for c in range(cells)],
+                            [bufs[c][li + 1] for c in range(cells)]) for li in range(len(kinds))]
 
     def enqueue(i, stream):
-        for c in range(cells):
-            b = bufs[c]
-            for li in range(len(kinds)):
-                sessions[c][li].execute_device(b[li], b[li + 1], b[li + 1], stream)
+        for grp in groups:
+            grp.execute(stream)
 
     def cpu(budget_s):
         orc = oracle()
@@ -263,6 +267,8 @@ def cells_workload(pw, hip, name):
                            f"{cpu_threads()} threads), scaled x{cells} to the 64 cells")}
 
     def close():
+        for grp in groups:
+            grp.close()
         for row in sessions:
             for s in row:
                 s.close()
@@ -273,7 +279,8 @@ def cells_workload(pw, hip, name):
     return {"desc": name, "enqueue": enqueue, "per_graph": 1, "bytes": None, "flops": flops,
             "bound": "mfma", "dtype": "fp8e4m3+fp4e2m1",
             "config": {"workload": name, "cells": cells, "layers_per_cell": 3, "batch": batch,
-                       "width": d, "layer_kinds": "E4M3 per-row, FP4 E8M0/32, E4M3 per-row"},
+                       "width": d, "layer_kinds": "E4M3 per-row, FP4 E8M0/32, E4M3 per-row",
+                       "execution": "independent cells, one grouped launch per layer position"},
             "cpu": cpu, "close": close}
 
 

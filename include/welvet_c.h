@@ -129,6 +129,20 @@ WELVET_API welvet_status welvet_dense_export_store(welvet_dense_session* sess, u
                                                    float* row_scale, uint8_t* blk_exp,
                                                    float* tensor_scale);
 
+/* Grouped execution of Dense sessions of one shape (no counterpart in the
+ * reference; for the independent cells of a volume): every session must have
+ * the same batch, in, out, activation, dtype and scheme. x[i], pre[i],
+ * post[i] are device buffers of member i, fixed at mount; execute queues all
+ * members on `stream` (NULL = the group's stream) as one split launch and one
+ * matrix-core launch when the batch exceeds 32 rows, else member by member.
+ * The sessions must outlive the group; calls on a group must not overlap. */
+typedef struct welvet_dense_group welvet_dense_group;
+WELVET_API welvet_status welvet_dense_group_mount(welvet_dense_session* const* sessions, int32_t n,
+                                                  const float* const* x, float* const* pre,
+                                                  float* const* post, welvet_dense_group** out);
+WELVET_API welvet_status welvet_dense_group_execute(welvet_dense_group* g, void* stream);
+WELVET_API void welvet_dense_group_release(welvet_dense_group* g);
+
 /* SwiGLU / MHA sessions: mount once, execute many (host or device buffers). */
 typedef struct welvet_swiglu_session welvet_swiglu_session;
 WELVET_API welvet_status welvet_swiglu_mount(int32_t batch, int32_t seq, int32_t input_dim,

@@ -166,6 +166,66 @@ welvet_status welvet_dense_execute_device(welvet_dense_session* s, const float* 
   });
 }
 
+// ---- grouped Dense execution (extension) ----
+struct welvet_dense_group {
+  wv::Stream stream;
+  std::vector<welvet_dense_session*> members;
+  std::vector<const float*> x;
+  std::vector<float*> pre, post;
+  bool fused = false;
+  wv::DenseGroup g;
+};
+
+welvet_status welvet_dense_group_mount(welvet_dense_session* const* sessions, int32_t n,
+                                       const float* const* x, float* const* pre,
+                                       float* const* post, welvet_dense_group** out) {
+  if (!out) return invalid("null group out");
+  *out = nullptr;
+  if (n <= 0 || !sessions || !x || !pre || !post) return invalid("group: null or empty arguments");
+  return guarded([&]() -> Status {
+    auto grp = std::make_unique<welvet_dense_group>();
+    for (int i = 0; i < n; ++i) {
+      welvet_dense_session* s = sessions[i];
+      if (!s) return wv::Status::err(wv::kInvalid, "group: null session");
+      if (s->batch != sessions[0]->batch)
+        return wv::Status::err(wv::kInvalid, "group: sessions differ in batch");
+      if (!x[i] || !pre[i] || !post[i]) return wv::Status::err(wv::kInvalid, "group: null buffer");
+      if (pre[i] == post[i] && s->layer.need_epi())
+        return wv::Status::err(wv::kInvalid, "group: pre and post must differ");
+      grp->members.push_back(s);
+      grp->x.push_back(x[i]);
+      grp->pre.push_back(pre[i]);
+      grp->post.push_back(post[i]);
+    }
+    const int batch = sessions[0]->batch;
+    WV_TRY(grp->stream.create());
+    grp->fused = wv::dense_group_fused(batch);
+    if (grp->fused) {
+      std::vector<const wv::DenseLayer*> layers;
+      for (auto* s : grp->members) layers.push_back(&s->layer);
+      WV_TRY(wv::dense_group_build(layers.data(), n, batch, grp->x.data(), grp->pre.data(),
+                                   grp->post.data(), &grp->g));
+    }
+    *out = grp.release();
+    return Status::ok();
+  });
+}
+
+welvet_status welvet_dense_group_execute(welvet_dense_group* g, void* stream) {
+  if (!g) return invalid("null group");
+  return guarded([&]() -> Status {
+    hipStream_t st = pick(stream, g->stream.s);
+    if (g->fused) return wv::dense_group_forward(g->g, st);
+    for (size_t i = 0; i < g->members.size(); ++i) {
+      welvet_dense_session* s = g->members[i];
+      WV_TRY(wv::dense_forward(s->layer, s->batch, g->x[i], g->pre[i], g->post[i], &s->ws, st));
+    }
+    return Status::ok();
+  });
+}
+
+void welvet_dense_group_release(welvet_dense_group* g) { delete g; }
+
 welvet_status welvet_dense_export_store(welvet_dense_session* s, uint8_t* native,
                                         size_t native_cap, size_t* native_len, float* row_scale,
                                         uint8_t* blk_exp, float* tensor_scale) {

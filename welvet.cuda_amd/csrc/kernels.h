@@ -93,6 +93,18 @@ size_t split_bytes(int M, int kpad);
 Status launch_split(const float* x, int x_stride, int M, int cols, int kpad, uint8_t* buf,
                     hipStream_t st);
 Status launch_mxg(const MxgArgs& p, int dtype, bool blk, hipStream_t st);
+// Grouped forms over n members that share every shape field: `jobs` / `tab`
+// are device arrays of n entries (one split input and buffer / one GEMM
+// argument block per member). One launch covers all members.
+struct SplitJob {
+  const float* x = nullptr;
+  uint8_t* buf = nullptr;
+};
+Status launch_split_group(const SplitJob* jobs, int n, bool vec, int x_stride, int M, int cols,
+                          int kpad, hipStream_t st);
+// Members must take the large-tile GEMM (M above 32 rows).
+Status launch_mxg_group(const MxgArgs* tab, const MxgArgs& shape, int n, int dtype, bool blk,
+                        hipStream_t st);
 
 // ---- attention core (attention.hip) ----
 struct AttnArgs {

@@ -236,6 +236,57 @@ Status dense_forward(const DenseLayer& L, int batch, const float* x, float* pre,
 }
 
 // ---------------------------------------------------------------------------
+bool dense_group_fused(int batch) { return uses_split(batch) && mxg_block_m(batch) > 16; }
+
+Status dense_group_build(const DenseLayer* const* layers, int n, int batch,
+                         const float* const* x, float* const* pre, float* const* post,
+                         DenseGroup* g) {
+  if (n <= 0 || !layers || !x || !pre || !g) return Status::err(kInvalid, "dense group: bad args");
+  if (!dense_group_fused(batch)) return Status::err(kInvalid, "dense group: batch too small");
+  const DenseLayer& L0 = *layers[0];
+  std::vector<SplitJob> jobs(n);
+  std::vector<MxgArgs> tab(n);
+  const size_t sb = split_bytes(batch, L0.dev.kpad);
+  WV_TRY(g->split.alloc(sb * n));
+  bool vec = (L0.in % 4) == 0;
+  for (int i = 0; i < n; ++i) {
+    const DenseLayer* L = layers[i];
+    if (!L || L->in != L0.in || L->out != L0.out || L->act != L0.act ||
+        L->dev.dtype != L0.dev.dtype || L->dev.scheme != L0.dev.scheme ||
+        L->need_epi() != L0.need_epi())
+      return Status::err(kInvalid, "dense group: members differ in shape, dtype, scheme or epilogue");
+    if (!x[i] || !pre[i] || (L->need_epi() && (!post || !post[i])))
+      return Status::err(kInvalid, "dense group: null member buffer");
+    uint8_t* buf = g->split.as<uint8_t>() + sb * i;
+    jobs[i].x = x[i];
+    jobs[i].buf = buf;
+    vec = vec && (reinterpret_cast<uintptr_t>(x[i]) & 15u) == 0;
+    tab[i] = mxg_args(*L, batch, buf);
+    tab[i].pre = pre[i];
+    tab[i].post = post ? post[i] : nullptr;
+  }
+  WV_TRY(g->jobs.alloc(sizeof(SplitJob) * n));
+  WV_TRY(g->tab.alloc(sizeof(MxgArgs) * n));
+  WV_HIP(hipMemcpy(g->jobs.p, jobs.data(), sizeof(SplitJob) * n, hipMemcpyHostToDevice));
+  WV_HIP(hipMemcpy(g->tab.p, tab.data(), sizeof(MxgArgs) * n, hipMemcpyHostToDevice));
+  g->n = n;
+  g->batch = batch;
+  g->dtype = L0.dev.dtype;
+  g->blk = L0.dev.scheme == kSchemeBlock32;
+  g->vec = vec;
+  g->in = L0.in;
+  g->kpad = L0.dev.kpad;
+  g->shape = tab[0];
+  return Status::ok();
+}
+
+Status dense_group_forward(const DenseGroup& g, hipStream_t st) {
+  WV_TRY(launch_split_group(g.jobs.as<const SplitJob>(), g.n, g.vec, g.in, g.batch, g.in, g.kpad,
+                            st));
+  return launch_mxg_group(g.tab.as<const MxgArgs>(), g.shape, g.n, g.dtype, g.blk, st);
+}
+
+// ---------------------------------------------------------------------------
 Status swiglu_build(int in, int inter, int dtype, int scheme, const float* G, const float* U,
                     const float* D, SwiGLULayer* L, hipStream_t st) {
   if (in <= 0 || inter <= 0)

@@ -67,6 +67,26 @@ Status dense_forward_split(const DenseLayer& L, int batch, const uint8_t* split,
 // small allocates, which a captured graph cannot do).
 Status ensure_split(Workspace* ws, size_t n);
 
+// Dense layers of one shape run together (independent cells of a volume):
+// one split launch and one GEMM launch for all members. Inputs and outputs
+// are fixed device buffers given at build time, so a group can be replayed
+// (and captured) without host work. Only batches above 32 rows use the
+// grouped kernels (dense_group_fused); smaller ones run member by member.
+struct DenseGroup {
+  int n = 0, batch = 0, dtype = 0;
+  bool blk = false, vec = false;
+  int in = 0, kpad = 0;
+  MxgArgs shape;
+  DevBuf split;  // n slices of split_bytes(batch, kpad)
+  DevBuf jobs;   // SplitJob[n]
+  DevBuf tab;    // MxgArgs[n]
+};
+bool dense_group_fused(int batch);
+Status dense_group_build(const DenseLayer* const* layers, int n, int batch,
+                         const float* const* x, float* const* pre, float* const* post,
+                         DenseGroup* g);
+Status dense_group_forward(const DenseGroup& g, hipStream_t st);
+
 struct SwiGLULayer {
   int in = 0, inter = 0;
   DenseLayer gate, up, down;

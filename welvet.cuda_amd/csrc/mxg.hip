@@ -47,48 +47,69 @@ __device__ __forceinline__ double act_f64(int act, double x) {
   }
 }
 
-__device__ __forceinline__ float quad_max(float v) {
-  int o = __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false);
-  v = fmaxf(v, __builtin_bit_cast(float, o));
-  o = __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false);
-  return fmaxf(v, __builtin_bit_cast(float, o));
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
 
-// One thread per 8 consecutive elements of a row; the 4 lanes of a quad hold
-// one 32-element block. Rows >= M (padding up to mpad) get zero codes.
+// Maximum over the 8 lanes l ^ {1, 2, 4} (one 32-element block of 4 per
+// lane). DPP moves read every lane, so all 64 lanes must be active; both
+// row shifts for distance 4 run unconditionally and a select picks one.
+__device__ __forceinline__ float max8(float v, int lane) {
+  v = fmaxf(v, dpp_f<0xB1>(v));  // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp_f<0x4E>(v));  // quad_perm [2,3,0,1]
+  const float up = dpp_f<0x104>(v), down = dpp_f<0x114>(v);  // row_shl:4, row_shr:4
+  return fmaxf(v, (lane & 4) ? down : up);
+}
+
+// One thread per 4 consecutive elements of a row (one float4 load: a wave
+// reads 1 KiB contiguous); the 8 lanes of a 32-element block find its amax
+// with DPP. Each term stores one dword of 4 E4M3 codes per lane (a wave
+// writes 256 contiguous bytes) and lane 0 of the block its E8M0 exponent.
+// Rows >= M (padding up to mpad) and columns >= cols get zero codes.
+template <bool VEC>
 __global__ __launch_bounds__(kThreads) void k_split(const float* __restrict__ x, int x_stride,
                                                     int M, int cols, int mpad, int kpad,
                                                     uint8_t* __restrict__ a,
-                                                    uint8_t* __restrict__ as) {
-  const int per_row = kpad / 8;
+                                                    uint8_t* __restrict__ as,
+                                                    const SplitJob* __restrict__ jobs) {
+  if (jobs) {  // grouped: member blockIdx.y
+    const SplitJob j = jobs[blockIdx.y];
+    x = j.x;
+    a = j.buf;
+    as = j.buf + (size_t)kTerms * mpad * kpad;
+  }
+  const int per_row = kpad / 4;
   const int64_t item = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  if (item >= (int64_t)mpad * per_row) return;  // whole quads exit together
-  const int m = (int)(item / per_row), k = (int)(item % per_row) * 8;
-  float r[8];
+  if (item >= (int64_t)mpad * per_row) return;  // whole 8-lane blocks exit together
+  const int lane = threadIdx.x & 63;
+  const int m = (int)(item / per_row), k = (int)(item % per_row) * 4;
+  float r[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (m < M) {
+    const float* row = x + (size_t)m * x_stride;
+    if (VEC && k + 4 <= cols) {
+      const float4 v = *reinterpret_cast<const float4*>(row + k);
+      r[0] = v.x, r[1] = v.y, r[2] = v.z, r[3] = v.w;
+    } else {
 #pragma unroll
-  for (int i = 0; i < 8; ++i) r[i] = (m < M && k + i < cols) ? x[(size_t)m * x_stride + k + i] : 0.0f;
+      for (int i = 0; i < 4; ++i) r[i] = k + i < cols ? row[k + i] : 0.0f;
+    }
+  }
   const int nblk = kpad / 32;
 #pragma unroll
   for (int t = 0; t < kTerms; ++t) {
-    float am = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) am = fmaxf(am, fabsf(r[i]));
-    am = quad_max(am);
+    float am = fmaxf(fmaxf(fabsf(r[0]), fabsf(r[1])), fmaxf(fabsf(r[2]), fabsf(r[3])));
+    am = max8(am, lane);
     const int e = e8m0_exponent(am, 448.0f);
     const float inv = pow2f(-e), sc = pow2f(e);
-    int w0 = __builtin_amdgcn_cvt_pk_fp8_f32(r[0] * inv, r[1] * inv, 0, false);
-    w0 = __builtin_amdgcn_cvt_pk_fp8_f32(r[2] * inv, r[3] * inv, w0, true);
-    int w1 = __builtin_amdgcn_cvt_pk_fp8_f32(r[4] * inv, r[5] * inv, 0, false);
-    w1 = __builtin_amdgcn_cvt_pk_fp8_f32(r[6] * inv, r[7] * inv, w1, true);
-    *reinterpret_cast<int2*>(a + ((size_t)t * mpad + m) * kpad + k) = make_int2(w0, w1);
-    if ((threadIdx.x & 3) == 0) as[((size_t)t * mpad + m) * nblk + k / 32] = (uint8_t)(e + 127);
+    int w = __builtin_amdgcn_cvt_pk_fp8_f32(r[0] * inv, r[1] * inv, 0, false);
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(r[2] * inv, r[3] * inv, w, true);
+    *reinterpret_cast<int*>(a + ((size_t)t * mpad + m) * kpad + k) = w;
+    if ((lane & 7) == 0) as[((size_t)t * mpad + m) * nblk + k / 32] = (uint8_t)(e + 127);
     if (t + 1 < kTerms) {
-      const v2f q0 = __builtin_amdgcn_cvt_pk_f32_fp8(w0, false);
-      const v2f q1 = __builtin_amdgcn_cvt_pk_f32_fp8(w0, true);
-      const v2f q2 = __builtin_amdgcn_cvt_pk_f32_fp8(w1, false);
-      const v2f q3 = __builtin_amdgcn_cvt_pk_f32_fp8(w1, true);
+      const v2f q0 = __builtin_amdgcn_cvt_pk_f32_fp8(w, false);
+      const v2f q1 = __builtin_amdgcn_cvt_pk_f32_fp8(w, true);
       r[0] -= q0.x * sc, r[1] -= q0.y * sc, r[2] -= q1.x * sc, r[3] -= q1.y * sc;
-      r[4] -= q2.x * sc, r[5] -= q2.y * sc, r[6] -= q3.x * sc, r[7] -= q3.y * sc;
     }
   }
 }
@@ -261,9 +282,9 @@ __device__ __forceinline__ void lds_dma4(const void* src, void* lds_base) {
   __builtin_amdgcn_global_load_lds((GlobalPtr)src, (LdsPtr)lds_base, 4, 0, 0);
 }
 
-template <int DT, bool BLK, int MATS>
+template <int DT, bool BLK, int MATS, bool GROUP>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_mxg2(
-    MxgArgs p, int tiles_m, int tiles_n) {
+    MxgArgs p0, const MxgArgs* __restrict__ tab, int tiles_m, int tiles_n) {
   constexpr bool FP4 = DT == kFP4;
   constexpr int BM = kBM2;
   constexpr int BNM = MATS == 2 ? 64 : 128;     // weight rows per matrix per tile
@@ -281,7 +302,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   __shared__ __attribute__((aligned(256))) uint32_t ssb[2][MATS * BNM];
 
   const int T = tiles_m * tiles_n;
-  const int b = blockIdx.x;
+  // grouped launches: member blockIdx.x / T, whose arguments come from tab
+  const MxgArgs p = GROUP ? tab[blockIdx.x / T] : p0;
+  const int b = GROUP ? blockIdx.x % T : blockIdx.x;
   const int lt = (T % 8 == 0) ? (b % 8) * (T / 8) + b / 8 : b;
   const int m0 = (lt / tiles_n) * BM, n0 = (lt % tiles_n) * BNM;
 
@@ -485,7 +508,8 @@ Status launch_t(const MxgArgs& p, int bm, hipStream_t st) {
         (size_t)round_up(p.N, 128) * p.pitch >= (1ull << 31))
       return Status::err(kUnsupported, "mxg: operands above 2 GiB");
     const int tiles_m = p.mpad / kBM2, tiles_n = (p.N + bn - 1) / bn;
-    k_mxg2<DT, BLK, MATS><<<(unsigned)(tiles_m * tiles_n), kThreads, 0, st>>>(p, tiles_m, tiles_n);
+    k_mxg2<DT, BLK, MATS, false><<<(unsigned)(tiles_m * tiles_n), kThreads, 0, st>>>(
+        p, nullptr, tiles_m, tiles_n);
   } else {
     const dim3 grid((unsigned)((p.N + kBN - 1) / kBN), (unsigned)(p.mpad / bm));
     k_mxg<DT, BLK, MATS, 16><<<grid, kThreads, 0, st>>>(p);
@@ -517,10 +541,55 @@ Status launch_split(const float* x, int x_stride, int M, int cols, int kpad, uin
   const int mpad = (int)round_up(M, mxg_block_m(M));
   uint8_t* a = buf;
   uint8_t* as = buf + (size_t)kTerms * mpad * kpad;
-  const int64_t items = (int64_t)mpad * (kpad / 8);
-  k_split<<<(unsigned)((items + kThreads - 1) / kThreads), kThreads, 0, st>>>(x, x_stride, M, cols,
-                                                                             mpad, kpad, a, as);
+  const int64_t items = (int64_t)mpad * (kpad / 4);
+  const unsigned grid = (unsigned)((items + kThreads - 1) / kThreads);
+  const bool vec = (x_stride % 4 == 0) && ((reinterpret_cast<uintptr_t>(x) & 15u) == 0);
+  if (vec) k_split<true><<<grid, kThreads, 0, st>>>(x, x_stride, M, cols, mpad, kpad, a, as, nullptr);
+  else k_split<false><<<grid, kThreads, 0, st>>>(x, x_stride, M, cols, mpad, kpad, a, as, nullptr);
   return hip_status(hipGetLastError(), "split launch");
+}
+
+Status launch_split_group(const SplitJob* jobs, int n, bool vec, int x_stride, int M, int cols,
+                          int kpad, hipStream_t st) {
+  if (n <= 0 || !jobs) return Status::err(kInvalid, "split group: no members");
+  const int mpad = (int)round_up(M, mxg_block_m(M));
+  const int64_t items = (int64_t)mpad * (kpad / 4);
+  const dim3 grid((unsigned)((items + kThreads - 1) / kThreads), (unsigned)n);
+  if (vec) k_split<true><<<grid, kThreads, 0, st>>>(nullptr, x_stride, M, cols, mpad, kpad, nullptr, nullptr, jobs);
+  else k_split<false><<<grid, kThreads, 0, st>>>(nullptr, x_stride, M, cols, mpad, kpad, nullptr, nullptr, jobs);
+  return hip_status(hipGetLastError(), "split group launch");
+}
+
+template <int DT, bool BLK, int MATS>
+Status launch_group_t(const MxgArgs* tab, const MxgArgs& p, int n, hipStream_t st) {
+  constexpr int bn = MATS == 2 ? 64 : 128;
+  const int tiles_m = p.mpad / kBM2, tiles_n = (p.N + bn - 1) / bn;
+  k_mxg2<DT, BLK, MATS, true><<<(unsigned)(n * tiles_m * tiles_n), kThreads, 0, st>>>(
+      p, tab, tiles_m, tiles_n);
+  return hip_status(hipGetLastError(), "mxg group launch");
+}
+
+Status launch_mxg_group(const MxgArgs* tab, const MxgArgs& p, int n, int dtype, bool blk,
+                        hipStream_t st) {
+  if (n <= 0 || !tab) return Status::err(kInvalid, "mxg group: no members");
+  if (mxg_block_m(p.M) != kBM2 || p.mpad % kBM2 != 0 || p.kpad % 256 != 0)
+    return Status::err(kInvalid, "mxg group: needs the large-tile layout");
+  if ((size_t)kTerms * p.mpad * p.kpad >= (1ull << 31) ||
+      (size_t)round_up(p.N, 128) * p.pitch >= (1ull << 31))
+    return Status::err(kUnsupported, "mxg: operands above 2 GiB");
+  const bool two = p.mats == 2;
+  switch (dtype) {
+  case kE4M3:
+    if (two) return blk ? launch_group_t<kE4M3, true, 2>(tab, p, n, st) : launch_group_t<kE4M3, false, 2>(tab, p, n, st);
+    return blk ? launch_group_t<kE4M3, true, 1>(tab, p, n, st) : launch_group_t<kE4M3, false, 1>(tab, p, n, st);
+  case kE5M2:
+    if (two) return blk ? launch_group_t<kE5M2, true, 2>(tab, p, n, st) : launch_group_t<kE5M2, false, 2>(tab, p, n, st);
+    return blk ? launch_group_t<kE5M2, true, 1>(tab, p, n, st) : launch_group_t<kE5M2, false, 1>(tab, p, n, st);
+  case kFP4:
+    if (two) return blk ? launch_group_t<kFP4, true, 2>(tab, p, n, st) : launch_group_t<kFP4, false, 2>(tab, p, n, st);
+    return blk ? launch_group_t<kFP4, true, 1>(tab, p, n, st) : launch_group_t<kFP4, false, 1>(tab, p, n, st);
+  }
+  return Status::err(kUnsupported, "mxg group: dtype");
 }
 
 Status launch_mxg(const MxgArgs& p, int dtype, bool blk, hipStream_t st) {

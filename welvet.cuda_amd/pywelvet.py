@@ -95,6 +95,11 @@ def lib():
     _sig(L, "welvet_dense_export_store", Status,
          [_vp, _u8p, _sz, ctypes.POINTER(_sz), _fp, _u8p, _fp])
     _sig(L, "welvet_dense_release", None, [_vp])
+    _sig(L, "welvet_dense_group_mount", Status,
+         [ctypes.POINTER(_vp), _i32, ctypes.POINTER(_vp), ctypes.POINTER(_vp),
+          ctypes.POINTER(_vp), ctypes.POINTER(_vp)])
+    _sig(L, "welvet_dense_group_execute", Status, [_vp, _vp])
+    _sig(L, "welvet_dense_group_release", None, [_vp])
     _sig(L, "welvet_swiglu_forward_f32", Status,
          [_i32, _i32, _i32, _i32, _i32, _i32, _fp, _fp, _fp, _fp, _fp, _fp])
     _sig(L, "welvet_swiglu_mount", Status,
@@ -279,6 +284,33 @@ class Hip:
 
 
 # --------------------------------------------------------------------------
+class DenseGroup:
+    """Grouped execution of same-shape Dense sessions over fixed device buffers."""
+
+    def __init__(self, sessions, xs, pres, posts):
+        n = len(sessions)
+        arr = lambda vals: (_vp * n)(*[_vp(v) for v in vals])
+        self._sessions = list(sessions)  # the sessions must outlive the group
+        h = _vp()
+        check(lib().welvet_dense_group_mount(arr([s.h.value for s in sessions]), n, arr(xs),
+                                             arr(pres), arr(posts), ctypes.byref(h)))
+        self.h = h
+
+    def execute(self, stream=None):
+        check(lib().welvet_dense_group_execute(self.h, _vp(stream) if stream else None))
+
+    def close(self):
+        if self.h:
+            lib().welvet_dense_group_release(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class DenseSession:
     """welvet_dense_mount_q / execute / execute_device / export_store / release."""
 
