@@ -282,6 +282,37 @@ __device__ __forceinline__ void lds_dma4(const void* src, void* lds_base) {
   __builtin_amdgcn_global_load_lds((GlobalPtr)src, (LdsPtr)lds_base, 4, 0, 0);
 }
 
+// A grouped member's argument block, read field by field through the constant
+// address space: scalar loads into SGPRs (copying the struct as a whole
+// would go through a private-memory temporary).
+typedef const __attribute__((address_space(4))) MxgArgs* ConstArgs;
+__device__ __forceinline__ MxgArgs load_args(ConstArgs t) {
+  MxgArgs p;
+  p.a = t->a;
+  p.as = t->as;
+  p.M = t->M;
+  p.mpad = t->mpad;
+  p.codes[0] = t->codes[0];
+  p.codes[1] = t->codes[1];
+  p.scale[0] = t->scale[0];
+  p.scale[1] = t->scale[1];
+  p.blk[0] = t->blk[0];
+  p.blk[1] = t->blk[1];
+  p.mats = t->mats;
+  p.pitch = t->pitch;
+  p.nblk = t->nblk;
+  p.kpad = t->kpad;
+  p.N = t->N;
+  p.pre = t->pre;
+  p.post = t->post;
+  p.out_stride = t->out_stride;
+  p.act = t->act;
+  p.need_epi = t->need_epi;
+  p.bias = t->bias;
+  p.bias_len = t->bias_len;
+  return p;
+}
+
 template <int DT, bool BLK, int MATS, bool GROUP>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_mxg2(
     MxgArgs p0, const MxgArgs* __restrict__ tab, int tiles_m, int tiles_n) {
@@ -303,7 +334,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
 
   const int T = tiles_m * tiles_n;
   // grouped launches: member blockIdx.x / T, whose arguments come from tab
-  const MxgArgs p = GROUP ? tab[blockIdx.x / T] : p0;
+  MxgArgs p;
+  if constexpr (GROUP) p = load_args((ConstArgs)tab + blockIdx.x / T);
+  else p = p0;
   const int b = GROUP ? blockIdx.x % T : blockIdx.x;
   const int lt = (T % 8 == 0) ? (b % 8) * (T / 8) + b / 8 : b;
   const int m0 = (lt / tiles_n) * BM, n0 = (lt % tiles_n) * BNM;
@@ -331,7 +364,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     const int row = q * B_RPS + lane / (WB / 16);       // tile row (both matrices)
     const int jj = lane % (WB / 16);
     const int j = FP4 ? (jj ^ ((row >> 2) & 3)) : (jj ^ ((row >> 1) & 7));
-    bbase[k] = p.codes[row / BNM];
+    bbase[k] = row / BNM == 0 ? p.codes[0] : p.codes[MATS - 1];  // no dynamic index into p
     boff[k] = (uint32_t)((size_t)(n0 + row % BNM) * p.pitch + j * 16);
   }
   // exponent copies (one dword per lane): A terms 6 x 64, weights 2 x 64
@@ -341,7 +374,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   const uint32_t asoff1 =
       has_a1 ? (uint32_t)(((size_t)(ea1 / BM) * p.mpad + m0 + ea1 % BM) * nblk_a) : 0u;
   const bool has_b = BLK && wave < MATS * BNM / 64;
-  const uint8_t* bsrc = has_b ? p.blk[(wave * 64 + lane) / BNM] +
+  const uint8_t* bsrc = has_b ? ((wave * 64 + lane) / BNM == 0 ? p.blk[0] : p.blk[MATS - 1]) +
                                     (size_t)(n0 + (wave * 64 + lane) % BNM) * p.nblk
                               : nullptr;
   if constexpr (!BLK) {
@@ -500,6 +533,182 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   }
 }
 
+// Small-M GEMM (M <= 32 activation rows: the weight-streaming regime). A
+// workgroup owns RB blocks of 16 weight rows (per matrix) and all K; its 8
+// waves take the 128-wide K chunks round-robin. Each wave loads the weight
+// fragments of a chunk straight from HBM into registers (non-temporal, no
+// LDS) and the activation-term fragments from the split buffer (small,
+// L2-resident; RB weight blocks share each of them), and runs kTerms MFMAs
+// per weight fragment and 16-row activation block; the next chunk's loads
+// are issued before the current chunk's MFMAs. The 8 partial tiles meet in
+// LDS for the epilogue.
+constexpr int kSmallWaves = 8;
+
+template <int DT, bool BLK, int MATS, int MB, int RB>
+__global__ __launch_bounds__(64 * kSmallWaves) void k_mxs(MxgArgs p) {
+  constexpr bool FP4 = DT == kFP4;
+  constexpr int WB = FP4 ? 64 : 128;  // code bytes per weight row per chunk
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int i16 = lane & 15, g = lane >> 4;
+  const int n0 = blockIdx.x * 16 * RB;
+  const int S = p.kpad / 128;
+  const int nblk_a = p.kpad / 32;
+
+  const uint8_t* wrow[MATS][RB];
+  const uint8_t* erow[MATS][RB];
+#pragma unroll
+  for (int m = 0; m < MATS; ++m)
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      const int row = n0 + rb * 16 + i16;
+      wrow[m][rb] = p.codes[m] + (size_t)row * p.pitch + 16 * g;
+      erow[m][rb] = BLK ? p.blk[m] + (size_t)row * p.nblk + g : nullptr;
+    }
+  const uint8_t* xrow[kTerms][MB];
+  const uint8_t* srow[kTerms][MB];
+#pragma unroll
+  for (int t = 0; t < kTerms; ++t)
+#pragma unroll
+    for (int b = 0; b < MB; ++b) {
+      const size_t r = (size_t)t * p.mpad + b * 16 + i16;
+      xrow[t][b] = p.a + r * p.kpad + 16 * g;
+      srow[t][b] = p.as + r * nblk_a + g;
+    }
+
+  struct Frag {
+    v8i w[MATS][RB];
+    int ws[MATS][RB];
+    v8i x[kTerms][MB];
+    int xs[kTerms][MB];
+  };
+  auto load = [&](int c, Frag& f) {
+    typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+    for (int m = 0; m < MATS; ++m)
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        const uint8_t* src = wrow[m][rb] + (size_t)c * WB;
+        const u4 lo = __builtin_nontemporal_load(reinterpret_cast<const u4*>(src));
+        u4 hi = u4{0u, 0u, 0u, 0u};
+        if constexpr (!FP4) hi = __builtin_nontemporal_load(reinterpret_cast<const u4*>(src + 64));
+        f.w[m][rb] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
+                         (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+        f.ws[m][rb] = BLK ? (int)erow[m][rb][c * 4] : 127;
+      }
+#pragma unroll
+    for (int t = 0; t < kTerms; ++t)
+#pragma unroll
+      for (int b = 0; b < MB; ++b) {
+        const uint8_t* src = xrow[t][b] + (size_t)c * 128;
+        const int4 lo = *reinterpret_cast<const int4*>(src);
+        const int4 hi = *reinterpret_cast<const int4*>(src + 64);
+        f.x[t][b] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+        f.xs[t][b] = srow[t][b][c * 4];
+      }
+  };
+
+  v4f acc[MATS][RB][MB];
+#pragma unroll
+  for (int m = 0; m < MATS; ++m)
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int b = 0; b < MB; ++b) acc[m][rb][b] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  // ring of NB fragment sets: NB - 1 chunks in flight while one is computed
+  // (the body is unrolled NB times so every ring index is a constant); two
+  // sets where three would not fit the register budget
+  constexpr int NB = RB * MATS + kTerms * MB <= 7 ? 3 : 2;
+  Frag f[NB];
+#pragma unroll
+  for (int i = 0; i < NB - 1; ++i) {
+    const int cc = wave + i * kSmallWaves;
+    if (cc < S) load(cc, f[i]);
+  }
+  for (int base = wave; base < S; base += NB * kSmallWaves) {
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const int cc = base + i * kSmallWaves;
+      if (cc < S) {
+        const int pf = cc + (NB - 1) * kSmallWaves;
+        if (pf < S) load(pf, f[(i + NB - 1) % NB]);
+#pragma unroll
+        for (int m = 0; m < MATS; ++m)
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int t = 0; t < kTerms; ++t)
+#pragma unroll
+              for (int b = 0; b < MB; ++b)
+                acc[m][rb][b] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                    f[i].w[m][rb], f[i].x[t][b], acc[m][rb][b], wfmt<DT>(), 0, 0, f[i].ws[m][rb],
+                    0, f[i].xs[t][b]);
+      }
+    }
+  }
+
+  // acc[m][rb][b]: lane holds weight rows n0 + rb*16 + 4g + r (r = 0..3) and
+  // activation row b*16 + i16
+  __shared__ float part[kSmallWaves][MATS][RB * MB][64][4];
+#pragma unroll
+  for (int m = 0; m < MATS; ++m)
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int b = 0; b < MB; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) part[wave][m][rb * MB + b][lane][r] = acc[m][rb][b][r];
+  __syncthreads();
+  // RB*MB tiles x 256 outputs; thread -> (tile, lane, r) positions
+  for (int o = threadIdx.x; o < RB * MB * 256; o += 64 * kSmallWaves) {
+    const int tile = o / 256, l = (o / 4) % 64, r = o % 4;
+    const int rb = tile / MB, b = tile % MB;
+    const int mrow = b * 16 + (l & 15), n = n0 + rb * 16 + 4 * (l >> 4) + r;
+    if (mrow >= p.M || n >= p.N) continue;
+    float tot[MATS];
+#pragma unroll
+    for (int m = 0; m < MATS; ++m) {
+      float sum = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kSmallWaves; ++w) sum += part[w][m][tile][l][r];
+      tot[m] = sum * p.scale[m][n];
+    }
+    const size_t oi = (size_t)mrow * p.out_stride + n;
+    if constexpr (MATS == 2) {
+      const float gs = (float)act_f64(kSilu, (double)tot[0]);
+      p.pre[oi] = (float)((double)gs * (double)tot[1]);
+    } else {
+      float y = tot[0];
+      if (p.need_epi) {
+        double v = (double)y;
+        if (p.bias && n < p.bias_len) {
+          v += p.bias[n];
+          y = (float)v;
+        }
+        p.pre[oi] = y;
+        p.post[oi] = (float)act_f64(p.act, v);
+      } else {
+        p.pre[oi] = y;
+        if (p.post) p.post[oi] = y;
+      }
+    }
+  }
+}
+
+template <int DT, bool BLK, int MATS, int MB>
+void launch_small(const MxgArgs& p, hipStream_t st) {
+  // the largest weight-row group that still gives >= 256 workgroups, capped
+  // where the register budget of two waves per SIMD would spill
+  constexpr int kMaxRB = MATS * MB == 1 ? 4 : MATS * MB == 2 ? 2 : 1;
+  const int n16 = (p.N + 15) / 16;
+  if (kMaxRB >= 4 && n16 >= 4 * 256)
+    k_mxs<DT, BLK, MATS, MB, (kMaxRB >= 4 ? 4 : 1)><<<(n16 + 3) / 4, 64 * kSmallWaves, 0, st>>>(p);
+  else if (kMaxRB >= 2 && n16 >= 2 * 256)
+    k_mxs<DT, BLK, MATS, MB, (kMaxRB >= 2 ? 2 : 1)><<<(n16 + 1) / 2, 64 * kSmallWaves, 0, st>>>(p);
+  else
+    k_mxs<DT, BLK, MATS, MB, 1><<<n16, 64 * kSmallWaves, 0, st>>>(p);
+}
+
 template <int DT, bool BLK, int MATS>
 Status launch_t(const MxgArgs& p, int bm, hipStream_t st) {
   if (bm == kBM2) {
@@ -511,8 +720,8 @@ Status launch_t(const MxgArgs& p, int bm, hipStream_t st) {
     k_mxg2<DT, BLK, MATS, false><<<(unsigned)(tiles_m * tiles_n), kThreads, 0, st>>>(
         p, nullptr, tiles_m, tiles_n);
   } else {
-    const dim3 grid((unsigned)((p.N + kBN - 1) / kBN), (unsigned)(p.mpad / bm));
-    k_mxg<DT, BLK, MATS, 16><<<grid, kThreads, 0, st>>>(p);
+    if (p.mpad <= 16) launch_small<DT, BLK, MATS, 1>(p, st);
+    else launch_small<DT, BLK, MATS, 2>(p, st);
   }
   return hip_status(hipGetLastError(), "mxg launch");
 }
