@@ -204,6 +204,9 @@ def mha_workload(pw, hip, name):
     # attention under the reference's semantics: query t sees keys [0, b*S + s]
     pairs = sum(sum(b * S + s_ + 1 for s_ in range(S)) for b in range(B))
     att = pairs * H * hd * 4
+    # the kernel folds the repeated KV-ring rows into multiplicity weights:
+    # the same result from B * S * min(S, msl) distinct (query, row) pairs
+    att_computed = B * S * S * H * hd * 4
     nbytes = 4 * (d * d + 4 * d) + 4 * B * S * d * 3
 
     def enqueue(i, stream):
@@ -218,7 +221,10 @@ def mha_workload(pw, hip, name):
             "flops": proj + att, "bound": "mfma", "dtype": "fp8e5m2",
             "config": {"workload": name, "batch": B, "seq": S, "d_model": d, "heads": H,
                        "head_dim": hd, "mask": "causal", "pos": "rope",
-                       "projection_flops": proj, "attention_flops": att},
+                       "projection_flops": proj,
+                       "attention_flops_reference_semantics": att,
+                       "attention_flops_computed": att_computed,
+                       "flops_basis": "value counts the reference's per-key-position attention"},
             "cpu": None, "close": close}
 
 

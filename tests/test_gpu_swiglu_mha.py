@@ -99,6 +99,31 @@ def test_mha_matches_oracle(gpu, oracle, B, S, d, H, KVH, msl, mask, pos):
     assert rel_l2(y, oy) <= 1e-4
 
 
+@pytest.mark.parametrize("B,S,d,H,KVH,msl,mask", [
+    (3, 70, 128, 2, 2, 80, 1),     # ring of 80 rows < 210 positions: multiplicities 1..3
+    (2, 64, 128, 4, 2, 64, 2),     # bidirectional, GQA, hd 32
+    (2, 40, 128, 1, 1, 100, 1),    # hd 128, ragged query block
+    (4, 512, 1024, 16, 16, 512, 1),  # the benchmark layer at half the batch
+])
+def test_mha_matrix_core_attention(gpu, oracle, B, S, d, H, KVH, msl, mask):
+    """Causal / bidirectional attention without ALiBi runs on the matrix cores
+    over the distinct KV-ring rows with multiplicity weights."""
+    dt, scheme, pos = 5, 2, 0
+    hd = d // H
+    rng = np.random.default_rng(B * 7 + S + d)
+    Q = (rng.standard_normal((H * hd, d)) / np.sqrt(d)).astype(np.float32)
+    K = (rng.standard_normal((KVH * hd, d)) / np.sqrt(d)).astype(np.float32)
+    V = (rng.standard_normal((KVH * hd, d)) / np.sqrt(d)).astype(np.float32)
+    O = (rng.standard_normal((d, H * hd)) / np.sqrt(H * hd)).astype(np.float32)
+    x = rng.standard_normal((B * S, d)).astype(np.float32)
+    s = gpu.MHASession(B, S, d, H, KVH, 0, msl, mask, pos, dt, scheme, Q, K, V, O)
+    attn, y = s.execute(x)
+    s.close()
+    oattn, oy = oracle_mha(oracle, dt, scheme, Q, K, V, O, x, B, S, H, KVH, hd, msl, mask, pos)
+    assert rel_l2(attn, oattn) <= 1e-4
+    assert rel_l2(y, oy) <= 1e-4
+
+
 def test_mha_seq_above_max_is_invalid(gpu):
     import pywelvet as pw
     W = np.zeros((16, 16), np.float32)

@@ -16,6 +16,8 @@
 namespace wv {
 namespace {
 
+typedef float v4f __attribute__((ext_vector_type(4)));
+
 __device__ __forceinline__ bool allow(int qp, int kp, const AttnArgs& a) {
   if (a.mask == 2) return true;
   if (a.mask == 3) {
@@ -141,6 +143,145 @@ __global__ __launch_bounds__(64) void k_attention(AttnArgs a) {
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// Matrix-core path for the causal and bidirectional masks without ALiBi.
+//
+// Under the reference indexing a query of batch b scans key positions
+// kp in [0, b*seq + seq), and kp reads ring row p = last - ((last - kp) mod
+// msl), so only the rows p in [max(0, last - msl + 1), last] occur, row p
+// once for every allowed kp == p (mod msl). The score of a key depends on
+// its row only (no ALiBi), so the softmax over key positions equals a
+// softmax over distinct rows with multiplicity weights:
+//   bidirectional: c(p) = floor(p / msl) + 1 (every kp = p - i*msl >= 0),
+//   causal:        c(p) - 1 when p > qp (only kp = p itself is masked out:
+//                  p - msl <= last - msl < b*seq <= qp since msl >= seq).
+// Scores and sums are the same function of the same values; only the fp32
+// summation order differs from the per-position loop.
+//
+// A workgroup of 4 waves takes 64 queries (16 per wave) of one (batch, head)
+// and walks the distinct rows in tiles of 64 keys staged in LDS (rows padded
+// to hd + 4 floats: conflict-free reads below). Per 16-key block a wave runs
+//   S^T = K Q^T  (v_mfma_f32_16x16x4f32, hd/4 steps): lane l holds the
+//                scores of query l%16 for keys 4*(l/16) + i, i = 0..3;
+//   O^T += V^T P^T: the same 4 values per lane are the B operand (MFMA k
+//                index l/16 <-> key 4*(l/16) + j at step j), V^T the A
+//                operand, so no transpose is needed.
+// Softmax is online in fp32 per query (max and sum over the 4 lanes that
+// share a query, xor 16 / xor 32).
+constexpr int kQB = 64;  // queries per workgroup
+constexpr int kKT = 64;  // keys per LDS tile
+
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_mfma(AttnArgs a, int qblocks) {
+  constexpr int ST = HD / 4;       // QK MFMA steps
+  constexpr int DT = HD / 16;      // 16-wide head-dim tiles of O
+  constexpr int ROW = HD + 4;      // padded LDS row (floats)
+  __shared__ float ks[kKT * ROW];
+  __shared__ float vs[kKT * ROW];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c16 = lane & 15, g = lane >> 4;
+  const int b = blockIdx.x / qblocks, qb = blockIdx.x % qblocks;
+  const int h = blockIdx.y;
+  const int kvh = h / (a.heads / a.kv_heads);
+  const int qd = a.heads * HD, kvd = a.kv_heads * HD;
+  const int last = b * a.seq + a.seq - 1;
+  const int p_lo = last - a.msl + 1 > 0 ? last - a.msl + 1 : 0;
+  const int s_q = qb * kQB + wave * 16 + c16;      // query within the sequence
+  const bool q_ok = s_q < a.seq;
+  const int qp = b * a.seq + (q_ok ? s_q : a.seq - 1);
+  const bool causal = a.mask == 1;
+
+  float qr[ST];
+  {
+    const float* qrow = a.q + (size_t)qp * qd + (size_t)h * HD;
+#pragma unroll
+    for (int st = 0; st < ST; ++st) qr[st] = qrow[4 * st + g];
+  }
+  v4f o[DT];
+#pragma unroll
+  for (int d = 0; d < DT; ++d) o[d] = v4f{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, l = 0.0f;
+
+  for (int t0 = p_lo; t0 <= last; t0 += kKT) {
+    __syncthreads();
+    for (int i = tid; i < kKT * (HD / 4); i += 256) {
+      const int r = i / (HD / 4), c4 = (i % (HD / 4)) * 4;
+      const int p = t0 + r;
+      float4 kk = make_float4(0.f, 0.f, 0.f, 0.f), vv = kk;
+      if (p <= last) {
+        kk = *reinterpret_cast<const float4*>(a.k + (size_t)p * kvd + (size_t)kvh * HD + c4);
+        vv = *reinterpret_cast<const float4*>(a.v + (size_t)p * kvd + (size_t)kvh * HD + c4);
+      }
+      *reinterpret_cast<float4*>(&ks[r * ROW + c4]) = kk;
+      *reinterpret_cast<float4*>(&vs[r * ROW + c4]) = vv;
+    }
+    __syncthreads();
+    // multiplicity base of the tile start: floor(t0 / msl) + 1 (msl >= 64, so
+    // the tile crosses at most one multiple of msl)
+    const int base0 = t0 / a.msl + 1;
+    const int next_mult = (base0) * a.msl;  // first p with a larger base
+#pragma unroll 1
+    for (int kb = 0; kb < kKT; kb += 16) {
+      if (t0 + kb > last) break;
+      v4f sc = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int st = 0; st < ST; ++st)
+        sc = __builtin_amdgcn_mfma_f32_16x16x4f32(ks[(kb + c16) * ROW + 4 * st + g], qr[st], sc,
+                                                  0, 0, 0);
+      float w[4], smax = -INFINITY;
+      int cnt[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int p = t0 + kb + 4 * g + i;
+        int c = p <= last ? base0 + (p >= next_mult ? 1 : 0) : 0;
+        if (causal && p > qp) c -= 1;
+        cnt[i] = c;
+        w[i] = (float)((double)sc[i] * a.scale);
+        if (c > 0) smax = fmaxf(smax, w[i]);
+      }
+      if (a.sigmoid) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[i] = cnt[i] > 0 ? (float)cnt[i] / (1.0f + expf(-w[i])) : 0.0f;
+      } else {
+        smax = fmaxf(smax, __shfl_xor(smax, 16, 64));
+        smax = fmaxf(smax, __shfl_xor(smax, 32, 64));
+        const float nm = fmaxf(m, smax);
+        const float corr = (m == -INFINITY) ? 0.0f : expf(m - nm);
+        float ws = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          w[i] = cnt[i] > 0 ? (float)cnt[i] * expf(w[i] - nm) : 0.0f;
+          ws += w[i];
+        }
+        ws += __shfl_xor(ws, 16, 64);
+        ws += __shfl_xor(ws, 32, 64);
+        if (nm != -INFINITY) {
+          l = l * corr + ws;
+#pragma unroll
+          for (int d = 0; d < DT; ++d) o[d] *= corr;
+          m = nm;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int d = 0; d < DT; ++d)
+          o[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(vs[(kb + 4 * g + j) * ROW + d * 16 + c16],
+                                                      w[j], o[d], 0, 0, 0);
+    }
+  }
+  if (!q_ok) return;
+  // o[d]: lane holds query c16, head dims d*16 + 4g + i
+  const float inv = a.sigmoid ? 1.0f : (l > 0.0f ? 1.0f / l : 0.0f);
+  float* out = a.out + (size_t)qp * qd + (size_t)h * HD;
+#pragma unroll
+  for (int d = 0; d < DT; ++d) {
+    const float4 v = make_float4(o[d][0] * inv, o[d][1] * inv, o[d][2] * inv, o[d][3] * inv);
+    *reinterpret_cast<float4*>(out + d * 16 + 4 * g) = v;
+  }
+}
+
 }  // namespace
 
 Status launch_attention(const AttnArgs& a, hipStream_t st) {
@@ -150,6 +291,21 @@ Status launch_attention(const AttnArgs& a, hipStream_t st) {
     k_rope<<<a.tokens, 256, 0, st>>>(const_cast<float*>(a.q), const_cast<float*>(a.k), a.tokens,
                                      a.heads, a.kv_heads, a.hd, a.rope_theta);
     WV_HIP(hipGetLastError());
+  }
+  // the tile multiplicity update assumes at most one multiple of msl per
+  // 64-key tile, hence msl >= 64
+  const bool fast = (a.mask == 1 || a.mask == 2) && !a.alibi && a.msl >= kKT &&
+                    a.msl >= a.seq && (a.hd == 32 || a.hd == 64 || a.hd == 128) &&
+                    a.seq > 0 && a.tokens % a.seq == 0;
+  if (fast) {
+    const int qblocks = (a.seq + kQB - 1) / kQB;
+    dim3 grid((unsigned)(a.tokens / a.seq * qblocks), (unsigned)a.heads);
+    switch (a.hd) {
+    case 32: k_attn_mfma<32><<<grid, 256, 0, st>>>(a, qblocks); break;
+    case 64: k_attn_mfma<64><<<grid, 256, 0, st>>>(a, qblocks); break;
+    default: k_attn_mfma<128><<<grid, 256, 0, st>>>(a, qblocks); break;
+    }
+    return hip_status(hipGetLastError(), "attention launch");
   }
   dim3 grid(a.tokens, a.heads);
   k_attention<<<grid, 64, 0, st>>>(a);
