@@ -33,10 +33,24 @@ __device__ __forceinline__ bool allow(int qp, int kp, const AttnArgs& a) {
   return kp <= qp;
 }
 
+__device__ __forceinline__ double rope_angle(int t, int d, int hd, double theta) {
+  return (double)t / pow(theta, (double)(2 * d) / (double)hd);
+}
+
+__global__ void k_rope_table(double* __restrict__ tab, int tokens, int hd, double theta) {
+  const int half = hd / 2;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= tokens * half) return;
+  const double ang = rope_angle(i / half, i % half, hd, theta);
+  tab[2 * i] = cos(ang);
+  tab[2 * i + 1] = sin(ang);
+}
+
 // Rotates the pair (d, d + hd/2) of every head of Q (num_heads) and K
-// (num_kv) rows of token t by angle t / theta^(2d/hd), in f64.
+// (num_kv) rows of token t by angle t / theta^(2d/hd), in f64 (cos and sin
+// from the table when one is given).
 __global__ void k_rope(float* __restrict__ q, float* __restrict__ k, int tokens, int heads,
-                       int kv_heads, int hd, double theta) {
+                       int kv_heads, int hd, double theta, const double* __restrict__ tab) {
   const int t = blockIdx.x;
   const int half = hd / 2;
   const int per_tok = (heads + kv_heads) * half;
@@ -44,8 +58,14 @@ __global__ void k_rope(float* __restrict__ q, float* __restrict__ k, int tokens,
     const int h = i / half, d = i % half;
     float* row = h < heads ? q + ((size_t)t * heads + h) * hd
                            : k + ((size_t)t * kv_heads + (h - heads)) * hd;
-    const double ang = (double)t / pow(theta, (double)(2 * d) / (double)hd);
-    const double c = cos(ang), s = sin(ang);
+    double c, s;
+    if (tab) {
+      c = tab[2 * (t * half + d)];
+      s = tab[2 * (t * half + d) + 1];
+    } else {
+      const double ang = rope_angle(t, d, hd, theta);
+      c = cos(ang), s = sin(ang);
+    }
     const double a0 = row[d], a1 = row[d + half];
     row[d] = (float)(a0 * c - a1 * s);
     row[d + half] = (float)(a0 * s + a1 * c);
@@ -284,12 +304,19 @@ __global__ __launch_bounds__(256) void k_attn_mfma(AttnArgs a, int qblocks) {
 
 }  // namespace
 
+Status build_rope_table(double* tab, int tokens, int hd, double theta, hipStream_t st) {
+  const int n = tokens * (hd / 2);
+  if (n <= 0) return Status::ok();
+  k_rope_table<<<(n + 255) / 256, 256, 0, st>>>(tab, tokens, hd, theta);
+  return hip_status(hipGetLastError(), "rope table launch");
+}
+
 Status launch_attention(const AttnArgs& a, hipStream_t st) {
   if (a.hd > 64 * kMaxHdPerLane || a.hd % 4 != 0)
     return Status::err(kUnsupported, "attention: head_dim must be a multiple of 4 and <= 256");
   if (a.rope) {
     k_rope<<<a.tokens, 256, 0, st>>>(const_cast<float*>(a.q), const_cast<float*>(a.k), a.tokens,
-                                     a.heads, a.kv_heads, a.hd, a.rope_theta);
+                                     a.heads, a.kv_heads, a.hd, a.rope_theta, a.rope_tab);
     WV_HIP(hipGetLastError());
   }
   // the tile multiplicity update assumes at most one multiple of msl per

@@ -116,7 +116,13 @@ struct AttnArgs {
   int mask = 1, window = 0, prefix_len = 0, window_causal = 1;
   int rope = 0, alibi = 0, sigmoid = 0;
   double rope_theta = 10000.0, scale = 0.125;
+  // optional (cos, sin) per [token][pair] in f64 (build_rope_table); without
+  // it the rotation angles are computed per call
+  const double* rope_tab = nullptr;
 };
 Status launch_attention(const AttnArgs& a, hipStream_t st);
+// (cos, sin) of t / theta^(2d/hd) for tokens t < tokens and pairs d < hd/2,
+// in f64: tab[2 * (t * (hd/2) + d) + {0, 1}].
+Status build_rope_table(double* tab, int tokens, int hd, double theta, hipStream_t st);
 
 }  // namespace wv

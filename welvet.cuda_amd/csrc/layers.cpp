@@ -389,9 +389,23 @@ static size_t mha_split_bytes(const MHALayer& L, int T) {
   return a > b ? a : b;
 }
 
+static bool mha_rope(const MHAConfig& c) { return (c.pos == 0 || c.pos == 3) && c.head_dim / 2 > 0; }
+
+// The RoPE table covers token positions [0, T); built once (mount) and
+// reused, so a forward of at most T tokens queues no trigonometry.
+static Status ensure_rope_table(const MHALayer& L, int T, Workspace* ws, hipStream_t st) {
+  if (!mha_rope(L.cfg) || ws->rope_tokens >= T) return Status::ok();
+  WV_TRY(ws->c.alloc((size_t)T * (L.cfg.head_dim / 2) * 2 * sizeof(double)));
+  WV_TRY(build_rope_table(ws->c.as<double>(), T, L.cfg.head_dim, L.cfg.rope_theta, st));
+  WV_HIP(hipStreamSynchronize(st));
+  ws->rope_tokens = T;
+  return Status::ok();
+}
+
 Status mha_prepare(const MHALayer& L, int batch, int seq, Workspace* ws) {
   const size_t need = mha_workspace_bytes(L, batch, seq);
   if (ws->a.bytes < need) WV_TRY(ws->a.alloc(need));
+  WV_TRY(ensure_rope_table(L, batch * seq, ws, nullptr));
   return ensure_split(ws, mha_split_bytes(L, batch * seq));
 }
 
@@ -425,7 +439,11 @@ Status mha_forward(const MHALayer& L, int batch, int seq, const float* x, float*
   a.hd = c.head_dim, a.msl = c.max_seq_len;
   a.mask = c.mask, a.window = c.window, a.prefix_len = c.prefix_len;
   a.window_causal = (c.window_causal || c.mask == 1) ? 1 : 0;
-  a.rope = (c.pos == 0 || c.pos == 3) && c.head_dim / 2 > 0 ? 1 : 0;
+  a.rope = mha_rope(c) ? 1 : 0;
+  if (a.rope) {
+    WV_TRY(ensure_rope_table(L, T, ws, st));
+    a.rope_tab = ws->c.as<const double>();
+  }
   a.alibi = (c.pos == 2 || c.pos == 3) ? 1 : 0;
   a.sigmoid = c.softmax == 1 ? 1 : 0;
   a.rope_theta = c.rope_theta;

@@ -29,8 +29,9 @@ Status check_dtype_scheme(int dtype, int scheme);
 struct Workspace {
   DevBuf a;  // quantized activations / intermediates
   DevBuf b;
-  DevBuf c;
+  DevBuf c;  // MHA: RoPE (cos, sin) table for rope_tokens tokens
   DevBuf d;
+  int rope_tokens = 0;
 };
 
 struct DenseLayer {
