@@ -70,8 +70,11 @@ Status launch_mxv(const MxvArgs& a, int dtype, bool blk, hipStream_t st);
 // Activations are split into kTerms E4M3 terms with per-32 E8M0 scales.
 constexpr int kTerms = 3;
 struct MxgArgs {
-  const uint8_t* a = nullptr;   // [kTerms][mpad][kpad] term codes
-  const uint8_t* as = nullptr;  // [kTerms][mpad][kpad/32] term scales
+  // term codes in MFMA operand order, [mpad/16][kpad/128][kTerms][2][64][16]
+  // (16-row block, K chunk, term, operand half, lane, byte)
+  const uint8_t* a = nullptr;
+  // E8M0 exponents, [mpad/16][kpad/128][64] dwords; byte t is term t's
+  const uint8_t* as = nullptr;
   int M = 0, mpad = 0;
   const uint8_t* codes[2] = {nullptr, nullptr};
   const float* scale[2] = {nullptr, nullptr};

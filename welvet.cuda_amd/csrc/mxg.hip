@@ -1,22 +1,27 @@
-// Batched quantized GEMM on the CDNA4 scaled matrix cores.
+// Batched quantized GEMM on the CDNA4 scaled matrix cores (batch > 4 rows).
 //
 //   C[m][n] = rowscale[n] * sum_k x[m][k] * dec(W[n][k]) * blockscale[n][k/32]
 //
 // x (fp32) is first split into kTerms E4M3 terms with per-32 E8M0 scales
 // (k_split: each term quantizes the residual of the previous ones, so
 // x ~ sum_t a_t 2^e_t with a relative residual of ~2^-12 for three terms).
-// The terms act as extra K: every term is multiplied by the same weight tile
-// and accumulated into the same fp32 accumulator by
+// The terms act as extra K: every term is multiplied by the same weight
+// fragment and accumulated into the same fp32 accumulator by
 // v_mfma_scale_f32_16x16x128_f8f6f4, which takes the stored FP8/FP4 weight
 // codes and their E8M0 block scales directly.
 //
-// Tiling: a 256-thread workgroup computes a BM x 64 tile of C; per 128-wide K
-// step it stages the A terms, the weight codes and both scale sets in LDS
-// (rows padded by 16 bytes so 16-byte fragment reads are bank-conflict free),
-// then each wave runs its MFMAs. Operand layout of the instruction (lane l,
-// group g = l/16): FP8 bytes 0-15 -> k = 16g + j, bytes 16-31 -> k = 64 + 16g
-// + j; FP4 nibble j -> k = 32g + j; scale of lane l: row l%16, block g;
-// D: col l%16, rows 4g + r.
+// Operand layouts of the instruction (lane l, group g = l / 16): FP8 bytes
+// 0-15 -> k = 16g + j, bytes 16-31 -> k = 64 + 16g + j; FP4 nibble j ->
+// k = 32g + j; scale of lane l: row l % 16, block g; D: col l % 16, rows
+// 4g + r. The weights are the first operand, so a lane's accumulator holds 4
+// consecutive output columns of one activation row.
+//
+// The split buffer is stored in that operand order. For each 16-row block rb
+// and 128-wide K chunk kc the kTerms fragments are contiguous (2 KiB each:
+// half h holds bytes 16h..16h+15 of every lane's operand, lane l at 16 l), so
+// a wave fetches an operand with two fully coalesced 1 KiB loads and needs no
+// LDS for it; the kTerms E8M0 exponents a lane passes to the instruction sit
+// in one dword (byte t), also at 4 l.
 #include "codec.h"
 #include "common.h"
 #include "kernels.h"
@@ -24,8 +29,10 @@
 namespace wv {
 namespace {
 
-constexpr int kBN = 64;
 constexpr int kThreads = 256;
+constexpr int kFragBytes = 2048;                  // one 16 x 128 E4M3 operand
+constexpr int kChunkBytes = kTerms * kFragBytes;  // the terms of one (rb, kc)
+constexpr int kChunkScaleBytes = 256;             // one exponent dword per lane
 
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
@@ -47,26 +54,34 @@ __device__ __forceinline__ double act_f64(int act, double x) {
   }
 }
 
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+template <int DT>
+constexpr int wfmt() {
+  return DT == kE4M3 ? 0 : DT == kE5M2 ? 1 : 4;
 }
 
-// Maximum over the 8 lanes l ^ {1, 2, 4} (one 32-element block of 4 per
-// lane). DPP moves read every lane, so all 64 lanes must be active; both
-// row shifts for distance 4 run unconditionally and a select picks one.
-__device__ __forceinline__ float max8(float v, int lane) {
-  v = fmaxf(v, dpp_f<0xB1>(v));  // quad_perm [1,0,3,2]
-  v = fmaxf(v, dpp_f<0x4E>(v));  // quad_perm [2,3,0,1]
-  const float up = dpp_f<0x104>(v), down = dpp_f<0x114>(v);  // row_shl:4, row_shr:4
-  return fmaxf(v, (lane & 4) ? down : up);
+// One scaled MFMA with the weights as first operand and activation term T
+// as second: `xs` holds the exponents of all terms (byte t = term t) and the
+// instruction's op_sel picks byte T, so no per-term extraction is needed.
+template <int DT, int T>
+__device__ __forceinline__ v4f mfma_term(v8i w, v8i x, v4f c, int wsc, uint32_t xs) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(w, x, c, wfmt<DT>(), 0, 0, wsc, T, (int)xs);
 }
 
-// One thread per 4 consecutive elements of a row (one float4 load: a wave
-// reads 1 KiB contiguous); the 8 lanes of a 32-element block find its amax
-// with DPP. Each term stores one dword of 4 E4M3 codes per lane (a wave
-// writes 256 contiguous bytes) and lane 0 of the block its E8M0 exponent.
-// Rows >= M (padding up to mpad) and columns >= cols get zero codes.
+// s_waitcnt immediate (gfx9 encoding) waiting for at most `vm` outstanding
+// vector-memory operations and `lgkm` LDS/scalar operations.
+constexpr int waitcnt_imm(int vm, int lgkm) {
+  return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | ((lgkm & 15) << 8);
+}
+
+// The activation split, written in operand order. One wave per (16-row block
+// rb, 128-wide K chunk kc): the 16 x 128 fp32 slice is staged in LDS with
+// row-contiguous loads; then lane l (row i16 = l % 16, group g = l / 16)
+// takes the 32 values of its operand, k = 64h + 16g + j (h = 0, 1; j < 16).
+// A 32-element block is held by lanes l and l ^ 16, which exchange their
+// amax. Per term and half the lane stores its 16 codes with one 16-byte
+// store; the block exponents are gathered to the lanes that pass them to the
+// instruction (row l % 16, block l / 16) and stored as one dword per lane
+// (byte t: term t). Rows >= M and columns >= cols give zero codes.
 template <bool VEC>
 __global__ __launch_bounds__(kThreads) void k_split(const float* __restrict__ x, int x_stride,
                                                     int M, int cols, int mpad, int kpad,
@@ -79,208 +94,106 @@ __global__ __launch_bounds__(kThreads) void k_split(const float* __restrict__ x,
     a = j.buf;
     as = j.buf + (size_t)kTerms * mpad * kpad;
   }
-  const int per_row = kpad / 4;
-  const int64_t item = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  if (item >= (int64_t)mpad * per_row) return;  // whole 8-lane blocks exit together
-  const int lane = threadIdx.x & 63;
-  const int m = (int)(item / per_row), k = (int)(item % per_row) * 4;
-  float r[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  if (m < M) {
-    const float* row = x + (size_t)m * x_stride;
-    if (VEC && k + 4 <= cols) {
-      const float4 v = *reinterpret_cast<const float4*>(row + k);
-      r[0] = v.x, r[1] = v.y, r[2] = v.z, r[3] = v.w;
-    } else {
+  constexpr int kWaves = kThreads / 64;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int KC = kpad / 128;
+  const int w = blockIdx.x * kWaves + wave;
+  if (w >= (mpad / 16) * KC) return;  // whole waves; no workgroup barrier below
+  const int rb = w / KC, kc = w % KC;
+
+  __shared__ __attribute__((aligned(16))) float stage[kWaves][16][132];
+  float(*sl)[132] = stage[wave];  // rows padded by 16 bytes: no bank conflicts below
+  const int c4 = 4 * (lane & 31), k = kc * 128 + c4;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) r[i] = k + i < cols ? row[k + i] : 0.0f;
+  for (int i = 0; i < 8; ++i) {
+    const int r = 2 * i + (lane >> 5), m = rb * 16 + r;
+    float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (m < M) {
+      const float* row = x + (size_t)m * x_stride;
+      if (VEC && k + 4 <= cols) {
+        v = *reinterpret_cast<const float4*>(row + k);
+      } else {
+        v.x = k < cols ? row[k] : 0.0f;
+        v.y = k + 1 < cols ? row[k + 1] : 0.0f;
+        v.z = k + 2 < cols ? row[k + 2] : 0.0f;
+        v.w = k + 3 < cols ? row[k + 3] : 0.0f;
+      }
     }
+    *reinterpret_cast<float4*>(&sl[r][c4]) = v;
   }
-  const int nblk = kpad / 32;
+  // The LDS operations of one wave execute in order, so the reads below see
+  // this wave's writes.
+  const int i16 = lane & 15, g = lane >> 4;
+  float v[2][16];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float4 t = *reinterpret_cast<const float4*>(&sl[i16][64 * h + 16 * g + 4 * q]);
+      v[h][4 * q] = t.x, v[h][4 * q + 1] = t.y, v[h][4 * q + 2] = t.z, v[h][4 * q + 3] = t.w;
+    }
+
+  uint8_t* dst = a + (size_t)(rb * KC + kc) * kChunkBytes + lane * 16;
+  // exponent of block b = l / 16 for row i16 comes from lane 32 (b & 1) + i16,
+  // half b >> 1
+  const int src = ((lane >> 4) & 1) * 32 + i16;
+  uint32_t sword = 0x7F000000u;  // byte 3 unused
 #pragma unroll
   for (int t = 0; t < kTerms; ++t) {
-    float am = fmaxf(fmaxf(fabsf(r[0]), fabsf(r[1])), fmaxf(fabsf(r[2]), fabsf(r[3])));
-    am = max8(am, lane);
-    const int e = e8m0_exponent(am, 448.0f);
-    const float inv = pow2f(-e), sc = pow2f(e);
-    int w = __builtin_amdgcn_cvt_pk_fp8_f32(r[0] * inv, r[1] * inv, 0, false);
-    w = __builtin_amdgcn_cvt_pk_fp8_f32(r[2] * inv, r[3] * inv, w, true);
-    *reinterpret_cast<int*>(a + ((size_t)t * mpad + m) * kpad + k) = w;
-    if ((lane & 7) == 0) as[((size_t)t * mpad + m) * nblk + k / 32] = (uint8_t)(e + 127);
-    if (t + 1 < kTerms) {
-      const v2f q0 = __builtin_amdgcn_cvt_pk_f32_fp8(w, false);
-      const v2f q1 = __builtin_amdgcn_cvt_pk_f32_fp8(w, true);
-      r[0] -= q0.x * sc, r[1] -= q0.y * sc, r[2] -= q1.x * sc, r[3] -= q1.y * sc;
-    }
-  }
-}
-
-template <int DT>
-constexpr int wfmt() {
-  return DT == kE4M3 ? 0 : DT == kE5M2 ? 1 : 4;
-}
-
-// BM x 64 tile; waves WAVES_M x WAVES_N; each wave SM x SN MFMA tiles of 16x16.
-template <int DT, bool BLK, int MATS, int BM>
-__global__ __launch_bounds__(kThreads) void k_mxg(MxgArgs p) {
-  constexpr bool FP4 = DT == kFP4;
-  constexpr int WAVES_M = BM >= 32 ? 2 : 1;
-  constexpr int WAVES_N = 4 / WAVES_M;
-  constexpr int WM = BM / WAVES_M, WN = kBN / WAVES_N;
-  constexpr int SM = WM / 16, SN = WN / 16;
-  constexpr int AROW = 128 + 16;                 // padded LDS row of A (bytes)
-  constexpr int BROW = (FP4 ? 64 : 128) + 16;    // padded LDS row of W
-  constexpr int WBYTES = FP4 ? 64 : 128;         // code bytes per row per K step
-
-  __shared__ __attribute__((aligned(16))) uint8_t sa[kTerms * BM * AROW];
-  __shared__ __attribute__((aligned(16))) uint8_t sb[MATS * kBN * BROW];
-  __shared__ uint8_t ssa[kTerms * BM * 4];
-  __shared__ uint8_t ssb[MATS * kBN * 4];
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
-  const int i16 = lane & 15, g = lane >> 4;
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * kBN;
-  const int S = p.kpad / 128;
-  const int nblk_a = p.kpad / 32;
-
-  v4f acc[MATS][SM][SN];
+    int e[2];
 #pragma unroll
-  for (int m = 0; m < MATS; ++m)
+    for (int h = 0; h < 2; ++h) {
+      float am = 0.0f;
 #pragma unroll
-    for (int a = 0; a < SM; ++a)
+      for (int j = 0; j < 16; ++j) am = fmaxf(am, fabsf(v[h][j]));
+      am = fmaxf(am, __shfl_xor(am, 16, 64));
+      e[h] = e8m0_exponent(am, 448.0f);
+      const float inv = pow2f(-e[h]), sc = pow2f(e[h]);
+      int wq[4];
 #pragma unroll
-      for (int b = 0; b < SN; ++b) acc[m][a][b] = v4f{0.f, 0.f, 0.f, 0.f};
-
-  for (int s = 0; s < S; ++s) {
-    // stage A terms: kTerms*BM rows x 8 chunks of 16 B
-    for (int c = tid; c < kTerms * BM * 8; c += kThreads) {
-      const int t = c / (BM * 8), row = (c / 8) % BM, j = c % 8;
-      const uint4 v = *reinterpret_cast<const uint4*>(
-          p.a + ((size_t)t * p.mpad + m0 + row) * p.kpad + (size_t)s * 128 + j * 16);
-      *reinterpret_cast<uint4*>(sa + (t * BM + row) * AROW + j * 16) = v;
-    }
-    for (int c = tid; c < kTerms * BM; c += kThreads) {
-      const int t = c / BM, row = c % BM;
-      *reinterpret_cast<uint32_t*>(ssa + c * 4) = *reinterpret_cast<const uint32_t*>(
-          p.as + ((size_t)t * p.mpad + m0 + row) * nblk_a + s * 4);
-    }
-    // stage weight codes: MATS*64 rows x (WBYTES/16) chunks
-    constexpr int WCH = WBYTES / 16;
-    for (int c = tid; c < MATS * kBN * WCH; c += kThreads) {
-      const int m = c / (kBN * WCH), row = (c / WCH) % kBN, j = c % WCH;
-      const uint4 v = *reinterpret_cast<const uint4*>(
-          p.codes[m] + (size_t)(n0 + row) * p.pitch + (size_t)s * WBYTES + j * 16);
-      *reinterpret_cast<uint4*>(sb + (m * kBN + row) * BROW + j * 16) = v;
-    }
-    if constexpr (BLK) {
-      for (int c = tid; c < MATS * kBN; c += kThreads) {
-        const int m = c / kBN, row = c % kBN;
-        *reinterpret_cast<uint32_t*>(ssb + c * 4) = *reinterpret_cast<const uint32_t*>(
-            p.blk[m] + (size_t)(n0 + row) * p.nblk + s * 4);
-      }
-    }
-    __syncthreads();
-    v8i bf[MATS][SN];
-    int bsc[MATS][SN];
-#pragma unroll
-    for (int m = 0; m < MATS; ++m)
-#pragma unroll
-      for (int b = 0; b < SN; ++b) {
-        const int row = wn * WN + b * 16 + i16;
-        const uint8_t* src = sb + (m * kBN + row) * BROW + 16 * g;
-        const int4 lo = *reinterpret_cast<const int4*>(src);
-        int4 hi = make_int4(0, 0, 0, 0);
-        if constexpr (!FP4) hi = *reinterpret_cast<const int4*>(src + 64);
-        bf[m][b] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-        bsc[m][b] = BLK ? (int)ssb[(m * kBN + row) * 4 + g] : 127;
-      }
-#pragma unroll
-    for (int t = 0; t < kTerms; ++t) {
-#pragma unroll
-      for (int a = 0; a < SM; ++a) {
-        const int row = wm * WM + a * 16 + i16;
-        const uint8_t* src = sa + (t * BM + row) * AROW + 16 * g;
-        const int4 lo = *reinterpret_cast<const int4*>(src);
-        const int4 hi = *reinterpret_cast<const int4*>(src + 64);
-        const v8i af = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-        const int asc = ssa[(t * BM + row) * 4 + g];
-#pragma unroll
-        for (int m = 0; m < MATS; ++m)
-#pragma unroll
-          for (int b = 0; b < SN; ++b)
-            acc[m][a][b] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-                af, bf[m][b], acc[m][a][b], 0, wfmt<DT>(), 0, asc, 0, bsc[m][b]);
-      }
-    }
-    __syncthreads();
-  }
-
-  // epilogue: lane holds rows 4g + r of each 16x16 tile, column i16
-#pragma unroll
-  for (int a = 0; a < SM; ++a)
-#pragma unroll
-    for (int b = 0; b < SN; ++b) {
-      const int n = n0 + wn * WN + b * 16 + i16;
-      if (n >= p.N) continue;
-      float sc[MATS];
-#pragma unroll
-      for (int m = 0; m < MATS; ++m) sc[m] = p.scale[m][n];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int mrow = m0 + wm * WM + a * 16 + 4 * g + r;
-        if (mrow >= p.M) continue;
-        const size_t oi = (size_t)mrow * p.out_stride + n;
-        if constexpr (MATS == 2) {
-          const float gv = acc[0][a][b][r] * sc[0], uv = acc[1][a][b][r] * sc[1];
-          const float gs = (float)act_f64(kSilu, (double)gv);
-          p.pre[oi] = (float)((double)gs * (double)uv);
-        } else {
-          float y = acc[0][a][b][r] * sc[0];
-          if (p.need_epi) {
-            double v = (double)y;
-            if (p.bias && n < p.bias_len) {
-              v += p.bias[n];
-              y = (float)v;
-            }
-            p.pre[oi] = y;
-            p.post[oi] = (float)act_f64(p.act, v);
-          } else {
-            p.pre[oi] = y;
-            if (p.post) p.post[oi] = y;
-          }
+      for (int q = 0; q < 4; ++q) {
+        int w4 = __builtin_amdgcn_cvt_pk_fp8_f32(v[h][4 * q] * inv, v[h][4 * q + 1] * inv, 0, false);
+        w4 = __builtin_amdgcn_cvt_pk_fp8_f32(v[h][4 * q + 2] * inv, v[h][4 * q + 3] * inv, w4, true);
+        wq[q] = w4;
+        if (t + 1 < kTerms) {
+          const v2f q0 = __builtin_amdgcn_cvt_pk_f32_fp8(w4, false);
+          const v2f q1 = __builtin_amdgcn_cvt_pk_f32_fp8(w4, true);
+          v[h][4 * q] -= q0.x * sc, v[h][4 * q + 1] -= q0.y * sc;
+          v[h][4 * q + 2] -= q1.x * sc, v[h][4 * q + 3] -= q1.y * sc;
         }
       }
+      *reinterpret_cast<int4*>(dst + t * kFragBytes + h * 1024) = make_int4(wq[0], wq[1], wq[2], wq[3]);
     }
+    const int e0 = __shfl(e[0], src, 64), e1 = __shfl(e[1], src, 64);
+    sword |= (uint32_t)(((lane >> 5) ? e1 : e0) + 127) << (8 * t);
+  }
+  *reinterpret_cast<uint32_t*>(as + (size_t)(rb * KC + kc) * kChunkScaleBytes + lane * 4) = sword;
 }
 
-// Large-M tile: 128 activation rows x 128 weight rows (64 per matrix when
-// MATS = 2) per workgroup, 4 waves of 64 x 64 (x 3 terms: 48 MFMAs per wave
-// per 128-wide K step).
+// Large-M tile (M > 32): 128 activation rows x 128 staged weight rows (64 per
+// matrix when MATS = 2) per 256-thread workgroup; wave w owns activation rows
+// 32w..32w+31 against all 128 weight rows (2 x 8 blocks of 16 x 16, x 3
+// terms: 48 MFMAs per 128-wide K step).
 //
-// Operands move global -> LDS with the gfx950 direct-to-LDS loads
-// (global_load_lds_dwordx4: lane i of a wave writes 16 bytes at
-// base + 16 i), double-buffered: while the MFMAs of step s run, step s+1 is
-// copied into the other buffer, with no register staging. LDS rows are
-// unpadded (128 bytes: A terms and FP8 codes; 64 bytes: FP4 codes) and the
-// 16-byte chunks of row r are stored at chunk j ^ ((r >> 1) & 7) (FP4:
-// j ^ ((r >> 2) & 3)), which makes the 16-lane groups of a fragment read hit
-// 16 distinct 16-byte bank groups.
+// Activation operands go straight from the split buffer into registers, each
+// wave its own rows, double-buffered: the loads of step s+1 run under the
+// MFMAs of step s. The weight tile, which all four waves use, goes through
+// LDS, double-buffered the same way: each wave loads its quarter of step
+// s+1 (one 16-byte load per lane and KiB) before the MFMAs of step s and
+// stores it to the other buffer after them. LDS rows are unpadded (128 bytes
+// FP8, 64 bytes FP4) and the 16-byte chunks of row r sit at chunk
+// j ^ ((r >> 1) & 7) (FP4: j ^ ((r >> 2) & 3)), so the 16-lane groups of a
+// fragment read hit distinct bank groups. A step ends with an LDS wait and a
+// plain s_barrier (no fence: the activation loads stay in flight).
 //
-// Tiles are ordered so that each XCD (workgroups are dealt round-robin to the
-// 8 XCDs) works on a contiguous band of activation rows against all weight
-// tiles: its L2 holds that band of A and the whole weight matrix.
-constexpr int kBM2 = 128;
-
-typedef __attribute__((address_space(3))) void* LdsPtr;
-typedef const __attribute__((address_space(1))) void* GlobalPtr;
-
-// The copy size of the builtin must be a literal.
-__device__ __forceinline__ void lds_dma16(const void* src, void* lds_base) {
-  __builtin_amdgcn_global_load_lds((GlobalPtr)src, (LdsPtr)lds_base, 16, 0, 0);
-}
-__device__ __forceinline__ void lds_dma4(const void* src, void* lds_base) {
-  __builtin_amdgcn_global_load_lds((GlobalPtr)src, (LdsPtr)lds_base, 4, 0, 0);
-}
+// Workgroups are dealt round-robin to the 8 XCDs, each with its own L2;
+// tiles are renumbered so that every XCD owns one contiguous run of tiles: a
+// band of activation rows against all weight tiles, or in grouped launches
+// whole members.
+constexpr int kBM = 128;
+// waves per large-tile workgroup: 8 = two per SIMD, so one wave's MFMAs run
+// while the other waits on memory
+constexpr int kMxgWaves = 8;
 
 // A grouped member's argument block, read field by field through the constant
 // address space: scalar loads into SGPRs (copying the struct as a whole
@@ -313,221 +226,300 @@ __device__ __forceinline__ MxgArgs load_args(ConstArgs t) {
   return p;
 }
 
-template <int DT, bool BLK, int MATS, bool GROUP>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_mxg2(
+template <int DT, bool BLK, int MATS, bool GROUP, int W>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W / 4))) void k_mxg(
     MxgArgs p0, const MxgArgs* __restrict__ tab, int tiles_m, int tiles_n) {
   constexpr bool FP4 = DT == kFP4;
-  constexpr int BM = kBM2;
-  constexpr int BNM = MATS == 2 ? 64 : 128;     // weight rows per matrix per tile
-  constexpr int WB = FP4 ? 64 : 128;            // code bytes per weight row per K step
-  constexpr int SM = 4, SN = BNM / 32;          // 16x16 blocks per wave (waves 2 x 2)
-  constexpr int A_BYTES = kTerms * BM * 128;    // one buffer of A terms
-  constexpr int B_BYTES = MATS * BNM * WB;
-  constexpr int A_SEG = A_BYTES / 1024;         // 1 KiB wave copies per step
-  constexpr int B_SEG = B_BYTES / 1024;
-  constexpr int B_RPS = 1024 / WB;              // weight rows per 1 KiB copy
+  constexpr int BNM = MATS == 2 ? 64 : 128;  // weight rows per matrix per tile
+  constexpr int BR = MATS * BNM;             // staged weight rows
+  constexpr int WB = FP4 ? 64 : 128;         // code bytes per weight row per K step
+  constexpr int SM = kBM / 16 / W;           // 16-row activation blocks per wave
+  constexpr int SN = BR / 16;                // 16-row weight blocks
+  constexpr int NC = SN / MATS;              // output column blocks
+  constexpr int B_BYTES = BR * WB;
+  constexpr int B_CPW = B_BYTES / 1024 / W;  // 1 KiB weight copies per wave per step
+  constexpr int B_RPS = 1024 / WB;           // weight rows per 1 KiB copy
 
-  __shared__ __attribute__((aligned(1024))) uint8_t sa[2][A_BYTES];
   __shared__ __attribute__((aligned(1024))) uint8_t sb[2][B_BYTES];
-  __shared__ __attribute__((aligned(256))) uint32_t ssa[2][kTerms * BM];
-  __shared__ __attribute__((aligned(256))) uint32_t ssb[2][MATS * BNM];
+  __shared__ __attribute__((aligned(256))) uint32_t ssb[2][BR];
 
   const int T = tiles_m * tiles_n;
-  // grouped launches: member blockIdx.x / T, whose arguments come from tab
+  const int nb = gridDim.x;
+  const int f = (nb % 8 == 0) ? (blockIdx.x % 8) * (nb / 8) + blockIdx.x / 8 : blockIdx.x;
+  // grouped launches: member f / T, whose arguments come from tab
   MxgArgs p;
-  if constexpr (GROUP) p = load_args((ConstArgs)tab + blockIdx.x / T);
+  if constexpr (GROUP) p = load_args((ConstArgs)tab + f / T);
   else p = p0;
-  const int b = GROUP ? blockIdx.x % T : blockIdx.x;
-  const int lt = (T % 8 == 0) ? (b % 8) * (T / 8) + b / 8 : b;
-  const int m0 = (lt / tiles_n) * BM, n0 = (lt % tiles_n) * BNM;
+  const int lt = GROUP ? f % T : f;
+  const int m0 = (lt / tiles_n) * kBM, n0 = (lt % tiles_n) * BNM;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
   const int i16 = lane & 15, g = lane >> 4;
-  const int S = p.kpad / 128;
-  const int nblk_a = p.kpad / 32;
+  const int KC = p.kpad / 128, S = KC;
 
-  // Per-lane source of each copy this wave issues (K step 0; step s adds
-  // s * 128 bytes of A / s * WB bytes of codes / s * 4 bytes of exponents).
-  uint32_t aoff[A_SEG / 4], boff[B_SEG / 4 > 0 ? B_SEG / 4 : 1];
+  // activation fragments of this wave (step s adds s * kChunkBytes / s * 256)
+  const uint8_t* abase[SM];
+  const uint32_t* sbase[SM];
 #pragma unroll
-  for (int k = 0; k < A_SEG / 4; ++k) {
-    const int q = wave + 4 * k;                          // segment: 8 rows of one term
-    const int t = q / (BM / 8), row = (q % (BM / 8)) * 8 + lane / 8;
-    const int j = (lane % 8) ^ ((row >> 1) & 7);
-    aoff[k] = (uint32_t)(((size_t)t * p.mpad + m0 + row) * p.kpad + j * 16);
+  for (int a = 0; a < SM; ++a) {
+    const size_t rb = (size_t)(m0 / 16 + wave * SM + a);
+    abase[a] = p.a + rb * KC * kChunkBytes + lane * 16;
+    sbase[a] = reinterpret_cast<const uint32_t*>(p.as + rb * KC * kChunkScaleBytes) + lane;
   }
-  const uint8_t* bbase[B_SEG / 4 > 0 ? B_SEG / 4 : 1];
+  // weight copies: per-lane source of each 1 KiB copy this wave issues at
+  // step 0 (step s adds s * WB bytes)
+  const uint8_t* bbase[B_CPW];
+  uint32_t boff[B_CPW];
 #pragma unroll
-  for (int k = 0; k < B_SEG / 4; ++k) {
-    const int q = wave + 4 * k;
-    const int row = q * B_RPS + lane / (WB / 16);       // tile row (both matrices)
+  for (int k = 0; k < B_CPW; ++k) {
+    const int q = wave + W * k;
+    const int row = q * B_RPS + lane / (WB / 16);  // staged row (both matrices)
     const int jj = lane % (WB / 16);
     const int j = FP4 ? (jj ^ ((row >> 2) & 3)) : (jj ^ ((row >> 1) & 7));
     bbase[k] = row / BNM == 0 ? p.codes[0] : p.codes[MATS - 1];  // no dynamic index into p
     boff[k] = (uint32_t)((size_t)(n0 + row % BNM) * p.pitch + j * 16);
   }
-  // exponent copies (one dword per lane): A terms 6 x 64, weights 2 x 64
-  const int ea0 = wave * 64 + lane, ea1 = (wave + 4) * 64 + lane;
-  const uint32_t asoff0 = (uint32_t)(((size_t)(ea0 / BM) * p.mpad + m0 + ea0 % BM) * nblk_a);
-  const bool has_a1 = wave + 4 < kTerms * BM / 64;
-  const uint32_t asoff1 =
-      has_a1 ? (uint32_t)(((size_t)(ea1 / BM) * p.mpad + m0 + ea1 % BM) * nblk_a) : 0u;
-  const bool has_b = BLK && wave < MATS * BNM / 64;
-  const uint8_t* bsrc = has_b ? ((wave * 64 + lane) / BNM == 0 ? p.blk[0] : p.blk[MATS - 1]) +
-                                    (size_t)(n0 + (wave * 64 + lane) % BNM) * p.nblk
-                              : nullptr;
-  if constexpr (!BLK) {
-    for (int i = tid; i < 2 * MATS * BNM; i += kThreads) (&ssb[0][0])[i] = 0x7F7F7F7Fu;
-  }
+  // weight block exponents: one dword (4 blocks) per staged row and step;
+  // waves of the same parity copy the same 64 rows (identical bytes)
+  const int erow = (wave & 1) * 64 + lane;
+  const uint8_t* bsrc =
+      BLK ? (erow / BNM == 0 ? p.blk[0] : p.blk[MATS - 1]) + (size_t)(n0 + erow % BNM) * p.nblk
+          : nullptr;
 
-  auto issue = [&](int s, int buf) {
-#pragma unroll
-    for (int k = 0; k < A_SEG / 4; ++k)
-      lds_dma16(p.a + (aoff[k] + (uint32_t)s * 128u), &sa[buf][(wave + 4 * k) * 1024]);
-#pragma unroll
-    for (int k = 0; k < B_SEG / 4; ++k)
-      lds_dma16(bbase[k] + (boff[k] + (uint32_t)s * WB), &sb[buf][(wave + 4 * k) * 1024]);
-    lds_dma4(p.as + (asoff0 + s * 4), &ssa[buf][wave * 64]);
-    if (has_a1) lds_dma4(p.as + (asoff1 + s * 4), &ssa[buf][(wave + 4) * 64]);
-    if (has_b) lds_dma4(bsrc + s * 4, &ssb[buf][wave * 64]);
+  struct AFrag {
+    v8i x[kTerms][SM];
+    uint32_t xs[SM];
   };
-
-  v4f acc[MATS][SM][SN];
+  auto load_a = [&](int s, AFrag& fr) {
 #pragma unroll
-  for (int m = 0; m < MATS; ++m)
+    for (int a = 0; a < SM; ++a) {
+      const uint8_t* src = abase[a] + (size_t)s * kChunkBytes;
 #pragma unroll
-    for (int a = 0; a < SM; ++a)
-#pragma unroll
-      for (int c = 0; c < SN; ++c) acc[m][a][c] = v4f{0.f, 0.f, 0.f, 0.f};
-
-  issue(0, 0);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  for (int s = 0; s < S; ++s) {
-    const int cur = s & 1;
-    v8i bf[MATS][SN];
-    int bsc[MATS][SN];
-#pragma unroll
-    for (int m = 0; m < MATS; ++m)
-#pragma unroll
-      for (int c = 0; c < SN; ++c) {
-        const int row = m * BNM + wn * (BNM / 2) + c * 16 + i16;
-        int4 lo, hi = make_int4(0, 0, 0, 0);
-        if constexpr (FP4) {
-          lo = *reinterpret_cast<const int4*>(&sb[cur][row * 64 + ((g ^ ((row >> 2) & 3)) * 16)]);
-        } else {
-          const int sw = (row >> 1) & 7;
-          lo = *reinterpret_cast<const int4*>(&sb[cur][row * 128 + ((g ^ sw) * 16)]);
-          hi = *reinterpret_cast<const int4*>(&sb[cur][row * 128 + (((4 + g) ^ sw) * 16)]);
-        }
-        bf[m][c] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-        bsc[m][c] = (int)((ssb[cur][row] >> (8 * g)) & 0xFFu);
+      for (int t = 0; t < kTerms; ++t) {
+        const int4 lo = *reinterpret_cast<const int4*>(src + t * kFragBytes);
+        const int4 hi = *reinterpret_cast<const int4*>(src + t * kFragBytes + 1024);
+        fr.x[t][a] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
       }
-    v8i af[kTerms][SM];
-    int asc[kTerms][SM];
-#pragma unroll
-    for (int t = 0; t < kTerms; ++t)
-#pragma unroll
-      for (int a = 0; a < SM; ++a) {
-        const int row = t * BM + wm * 64 + a * 16 + i16;
-        const int sw = (row >> 1) & 7;
-        const int4 lo = *reinterpret_cast<const int4*>(&sa[cur][row * 128 + ((g ^ sw) * 16)]);
-        const int4 hi = *reinterpret_cast<const int4*>(&sa[cur][row * 128 + (((4 + g) ^ sw) * 16)]);
-        af[t][a] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-        asc[t][a] = (int)((ssa[cur][row] >> (8 * g)) & 0xFFu);
-      }
-    // the next step streams into the other buffer while the MFMAs run (that
-    // buffer's last readers finished before the previous barrier)
-    if (s + 1 < S) issue(s + 1, cur ^ 1);
-    // keep the copies ahead of the MFMAs and the wait + barrier behind them
-    // (the MFMAs touch only registers, so the scheduler could otherwise move
-    // them past the barrier and expose the copy latency every step)
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int t = 0; t < kTerms; ++t)
-#pragma unroll
-      for (int a = 0; a < SM; ++a)
-#pragma unroll
-        for (int m = 0; m < MATS; ++m)
-#pragma unroll
-          for (int c = 0; c < SN; ++c)
-            acc[m][a][c] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-                bf[m][c], af[t][a], acc[m][a][c], wfmt<DT>(), 0, 0, bsc[m][c], 0, asc[t][a]);
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-  }
+      fr.xs[a] = sbase[a][s * (kChunkScaleBytes / 4)];
+    }
+  };
+  // The weight tile moves global -> registers -> LDS: loads issued before a
+  // step's MFMAs, LDS stores after them. (With direct-to-LDS copies in
+  // flight beside the activation loads the compiler treats the load counter
+  // as out of order and waits for every load before the MFMAs.)
+  // (named registers, not an array: an array here ends up in scratch or LDS
+  // before the loops that index it are unrolled)
+  static_assert(B_CPW == 1 || B_CPW == 2 || B_CPW == 4, "weight copies per wave");
+#define WV_BSRC(k, s) reinterpret_cast<const uint4*>(bbase[k] + (boff[k] + (uint32_t)(s) * WB))
+#define WV_BDST(k, buf) reinterpret_cast<uint4*>(&sb[buf][(wave + W * (k)) * 1024 + lane * 16])
+#define WV_LOAD_B(s)                                           \
+  do {                                                         \
+    q0 = *WV_BSRC(0, s);                                       \
+    if constexpr (B_CPW >= 2) q1 = *WV_BSRC(1, s);             \
+    if constexpr (B_CPW == 4) {                                \
+      q2 = *WV_BSRC(2, s);                                     \
+      q3 = *WV_BSRC(3, s);                                     \
+    }                                                          \
+    if constexpr (BLK) be = *reinterpret_cast<const uint32_t*>(bsrc + (s) * 4); \
+  } while (0)
+#define WV_STORE_B(buf)                                        \
+  do {                                                         \
+    *WV_BDST(0, buf) = q0;                                     \
+    if constexpr (B_CPW >= 2) *WV_BDST(1, buf) = q1;           \
+    if constexpr (B_CPW == 4) {                                \
+      *WV_BDST(2, buf) = q2;                                   \
+      *WV_BDST(3, buf) = q3;                                   \
+    }                                                          \
+    if constexpr (BLK) ssb[buf][(wave & 1) * 64 + lane] = be;  \
+  } while (0)
 
-  // Epilogue. The weights are the MFMA's first operand, so a lane holds
-  // output row m = i16 of each block and the 4 consecutive columns 4g..4g+3:
-  // one 16-byte store per lane and block when the output allows it. The
-  // scale arrays are padded to the row padding, so the float4 scale loads
-  // stay in bounds.
-  const bool vec_out = (p.out_stride & 3) == 0 && ((reinterpret_cast<uintptr_t>(p.pre) & 15) == 0) &&
-                       ((reinterpret_cast<uintptr_t>(p.post) & 15) == 0);
+  v4f acc[SM][SN];
 #pragma unroll
   for (int a = 0; a < SM; ++a)
 #pragma unroll
-    for (int c = 0; c < SN; ++c) {
-      const int mrow = m0 + wm * 64 + a * 16 + i16;
-      const int nb = n0 + wn * (BNM / 2) + c * 16 + 4 * g;
-      if (mrow >= p.M || nb >= p.N) continue;
+    for (int c = 0; c < SN; ++c) acc[a][c] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  // Two fragment sets and two weight buffers; step s computes from set and
+  // buffer s & 1 while step s + 1 streams into the others. kpad is a multiple
+  // of 256, so S is even and the loop body is unrolled by two with constant
+  // indices and no condition around any load: the compiler then knows
+  // exactly which loads are outstanding and waits only for the ones a step
+  // uses (a conditional load makes it wait for all of them).
+  AFrag fr[2];
+  {
+    uint4 q0, q1, q2, q3;
+    uint32_t be = 0;
+    WV_LOAD_B(0);
+    WV_STORE_B(0);
+  }
+  load_a(0, fr[0]);
+  if constexpr (!BLK) {
+    for (int i = tid; i < 2 * BR; i += 64 * W) (&ssb[0][0])[i] = 0x7F7F7F7Fu;
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // nothing may be in flight on entry to the loop either (same reason as at
+  // its back-edge below)
+  __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
+  asm volatile("s_barrier" ::: "memory");
+
+  for (int s0 = 0; s0 < S; s0 += 2) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int s = s0 + i, cur = i;
+      {
+        // weight fragments of this step first: a copy into LDS issued before
+        // them would make the compiler wait for it (it cannot tell the two
+        // buffers apart)
+        v8i bf[SN];
+        int bsc[SN];
+#pragma unroll
+        for (int c = 0; c < SN; ++c) {
+          const int row = c * 16 + i16;
+          int4 lo, hi = make_int4(0, 0, 0, 0);
+          if constexpr (FP4) {
+            lo = *reinterpret_cast<const int4*>(&sb[cur][row * 64 + ((g ^ ((row >> 2) & 3)) * 16)]);
+          } else {
+            const int sw = (row >> 1) & 7;
+            lo = *reinterpret_cast<const int4*>(&sb[cur][row * 128 + ((g ^ sw) * 16)]);
+            hi = *reinterpret_cast<const int4*>(&sb[cur][row * 128 + (((4 + g) ^ sw) * 16)]);
+          }
+          bf[c] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+          bsc[c] = (int)((ssb[cur][row] >> (8 * g)) & 0xFFu);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // next step into the other buffer and set (their last readers
+        // finished before the previous barrier); the last step fetches
+        // itself again into them, which nothing reads
+        const int nx = s + 1 < S ? s + 1 : S - 1;
+        uint4 q0, q1, q2, q3;
+        uint32_t be = 0;
+        WV_LOAD_B(nx);
+        load_a(nx, fr[cur ^ 1]);
+        // keep the copies ahead of the MFMAs and the wait + barrier behind
+        // them (the MFMAs touch only registers)
+        __builtin_amdgcn_sched_barrier(0);
+        static_assert(kTerms == 3, "three activation terms");
+#pragma unroll
+        for (int a = 0; a < SM; ++a)
+#pragma unroll
+          for (int c = 0; c < SN; ++c)
+            acc[a][c] = mfma_term<DT, 0>(bf[c], fr[cur].x[0][a], acc[a][c], bsc[c], fr[cur].xs[a]);
+#pragma unroll
+        for (int a = 0; a < SM; ++a)
+#pragma unroll
+          for (int c = 0; c < SN; ++c)
+            acc[a][c] = mfma_term<DT, 1>(bf[c], fr[cur].x[1][a], acc[a][c], bsc[c], fr[cur].xs[a]);
+#pragma unroll
+        for (int a = 0; a < SM; ++a)
+#pragma unroll
+          for (int c = 0; c < SN; ++c)
+            acc[a][c] = mfma_term<DT, 2>(bf[c], fr[cur].x[2][a], acc[a][c], bsc[c], fr[cur].xs[a]);
+        __builtin_amdgcn_sched_barrier(0);
+        // weight tile of step s+1 into the other buffer (the compiler waits
+        // for its loads only: the activation loads issued after them stay in
+        // flight), visible to all waves after the barrier. After the second
+        // step of the pair every load is waited for: one still in flight at
+        // the loop back-edge makes the compiler wait for all loads before the
+        // first MFMA of the next pass. Unconditional (also after the last
+        // step): a branch here would end the basic block, and the compiler
+        // sinks the MFMAs past it, behind the next step's loads.
+        WV_STORE_B(cur ^ 1);
+        if (i == 0) __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 0));
+        else __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
+        asm volatile("s_barrier" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  }
+
+#undef WV_BSRC
+#undef WV_BDST
+#undef WV_LOAD_B
+#undef WV_STORE_B
+
+  // Epilogue. A lane's accumulators hold activation row i16 of each 16-row
+  // block and 4 consecutive output columns: stored as they are, every store
+  // would write 64-byte pieces of 16 rows. Each wave instead stages its
+  // 32 x COLS result in LDS (its own region: no barrier) and writes whole
+  // rows, RPI rows of COLS floats per store instruction, with the bias and
+  // activation applied in that pass. The scale arrays are padded to the row
+  // padding, so the float4 scale loads stay in bounds.
+  constexpr int COLS = NC * 16;  // output columns of the tile
+  constexpr int LPR = COLS / 4;  // lanes per output row, a float4 each
+  constexpr int RPI = 64 / LPR;  // rows per store instruction
+  __shared__ __attribute__((aligned(16))) float stage[W][SM * 16][COLS + 4];
+#pragma unroll
+  for (int a = 0; a < SM; ++a)
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int nb = n0 + c * 16 + 4 * g;
       float4 sc[MATS];
 #pragma unroll
       for (int m = 0; m < MATS; ++m) sc[m] = *reinterpret_cast<const float4*>(p.scale[m] + nb);
-      float pre[4];
+      float y[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const float s0 = r == 0 ? sc[0].x : r == 1 ? sc[0].y : r == 2 ? sc[0].z : sc[0].w;
         if constexpr (MATS == 2) {
           const float s1 = r == 0 ? sc[1].x : r == 1 ? sc[1].y : r == 2 ? sc[1].z : sc[1].w;
-          const float gv = acc[0][a][c][r] * s0, uv = acc[1][a][c][r] * s1;
+          const float gv = acc[a][c][r] * s0, uv = acc[a][c + NC][r] * s1;
           const float gs = (float)act_f64(kSilu, (double)gv);
-          pre[r] = (float)((double)gs * (double)uv);
+          y[r] = (float)((double)gs * (double)uv);
         } else {
-          pre[r] = acc[0][a][c][r] * s0;
+          y[r] = acc[a][c][r] * s0;
         }
       }
-      // Dense with bias or activation: pre holds y here; the second pass
-      // below rewrites it (pre = y + bias, post = act) without accumulators
-      // live, so the f64 activation code is not unrolled per element.
-      const bool plain = MATS == 2 || !p.need_epi;
-      const size_t oi = (size_t)mrow * p.out_stride + nb;
-      if (vec_out && nb + 3 < p.N) {
-        const float4 v = make_float4(pre[0], pre[1], pre[2], pre[3]);
-        *reinterpret_cast<float4*>(p.pre + oi) = v;
-        if (plain && MATS == 1 && p.post) *reinterpret_cast<float4*>(p.post + oi) = v;
-      } else {
+      *reinterpret_cast<float4*>(&stage[wave][a * 16 + i16][c * 16 + 4 * g]) =
+          make_float4(y[0], y[1], y[2], y[3]);
+    }
+  const bool vec_out = (p.out_stride & 3) == 0 && ((reinterpret_cast<uintptr_t>(p.pre) & 15) == 0) &&
+                       ((reinterpret_cast<uintptr_t>(p.post) & 15) == 0);
+  const int cl = 4 * (lane % LPR), n = n0 + cl;
+  const int rbase = m0 + wave * SM * 16;
+  if (MATS == 2 || !p.need_epi) {
+    // post = pre here; a caller that passes one buffer for both gets it
+    // written once
+    float* post = MATS == 1 && p.post != p.pre ? p.post : nullptr;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          if (nb + r >= p.N) break;
-          p.pre[oi + r] = pre[r];
-          if (plain && MATS == 1 && p.post) p.post[oi + r] = pre[r];
+    for (int rr = 0; rr < SM * 16 / RPI; ++rr) {
+      const int r = rr * RPI + lane / LPR;
+      const float4 y = *reinterpret_cast<const float4*>(&stage[wave][r][cl]);
+      if (rbase + r >= p.M || n >= p.N) continue;
+      const size_t oi = (size_t)(rbase + r) * p.out_stride + n;
+      if (vec_out && n + 3 < p.N) {
+        *reinterpret_cast<float4*>(p.pre + oi) = y;
+        if (post) *reinterpret_cast<float4*>(post + oi) = y;
+      } else {
+        const float yv[4] = {y.x, y.y, y.z, y.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (n + i >= p.N) break;
+          p.pre[oi + i] = yv[i];
+          if (post) post[oi + i] = yv[i];
         }
       }
     }
-  if constexpr (MATS == 1) {
-    if (p.need_epi) {
+  } else {
+    // Dense with bias or activation (reference rule: pre = f32(y + bias),
+    // post = act evaluated in f64 on y + bias); rolled, so the f64 activation
+    // code appears once
 #pragma unroll 1
-      for (int ac = 0; ac < SM * SN; ++ac) {
-        const int a = ac / SN, c = ac % SN;
-        const int mrow = m0 + wm * 64 + a * 16 + i16;
-        const int nb = n0 + wn * (BNM / 2) + c * 16 + 4 * g;
-        if (mrow >= p.M) continue;
+    for (int rr = 0; rr < SM * 16 / RPI; ++rr) {
+      const int r = rr * RPI + lane / LPR;
+      const float4 y4 = *reinterpret_cast<const float4*>(&stage[wave][r][cl]);
+      if (rbase + r >= p.M || n >= p.N) continue;
+      const size_t oi = (size_t)(rbase + r) * p.out_stride + n;
+      const float yv[4] = {y4.x, y4.y, y4.z, y4.w};
 #pragma unroll 1
-        for (int r = 0; r < 4 && nb + r < p.N; ++r) {
-          const int n = nb + r;
-          const size_t oi = (size_t)mrow * p.out_stride + n;
-          float y = p.pre[oi];
-          double v = (double)y;
-          if (p.bias && n < p.bias_len) {
-            v += p.bias[n];
-            y = (float)v;
-          }
-          p.pre[oi] = y;
-          p.post[oi] = (float)act_f64(p.act, v);
+      for (int i = 0; i < 4 && n + i < p.N; ++i) {
+        float y = yv[i];
+        double v = (double)y;
+        if (p.bias && n + i < p.bias_len) {
+          v += p.bias[n + i];
+          y = (float)v;
         }
+        p.pre[oi + i] = y;
+        p.post[oi + i] = (float)act_f64(p.act, v);
       }
     }
   }
@@ -552,7 +544,6 @@ __global__ __launch_bounds__(64 * kSmallWaves) void k_mxs(MxgArgs p) {
   const int i16 = lane & 15, g = lane >> 4;
   const int n0 = blockIdx.x * 16 * RB;
   const int S = p.kpad / 128;
-  const int nblk_a = p.kpad / 32;
 
   const uint8_t* wrow[MATS][RB];
   const uint8_t* erow[MATS][RB];
@@ -564,22 +555,21 @@ __global__ __launch_bounds__(64 * kSmallWaves) void k_mxs(MxgArgs p) {
       wrow[m][rb] = p.codes[m] + (size_t)row * p.pitch + 16 * g;
       erow[m][rb] = BLK ? p.blk[m] + (size_t)row * p.nblk + g : nullptr;
     }
-  const uint8_t* xrow[kTerms][MB];
-  const uint8_t* srow[kTerms][MB];
+  // activation block b, chunk c: fragments at xrow[b] + c * kChunkBytes,
+  // exponent dword at srow[b][c * 64]
+  const uint8_t* xrow[MB];
+  const uint32_t* srow[MB];
 #pragma unroll
-  for (int t = 0; t < kTerms; ++t)
-#pragma unroll
-    for (int b = 0; b < MB; ++b) {
-      const size_t r = (size_t)t * p.mpad + b * 16 + i16;
-      xrow[t][b] = p.a + r * p.kpad + 16 * g;
-      srow[t][b] = p.as + r * nblk_a + g;
-    }
+  for (int b = 0; b < MB; ++b) {
+    xrow[b] = p.a + (size_t)b * S * kChunkBytes + lane * 16;
+    srow[b] = reinterpret_cast<const uint32_t*>(p.as + (size_t)b * S * kChunkScaleBytes) + lane;
+  }
 
   struct Frag {
     v8i w[MATS][RB];
     int ws[MATS][RB];
     v8i x[kTerms][MB];
-    int xs[kTerms][MB];
+    uint32_t xs[MB];
   };
   auto load = [&](int c, Frag& f) {
     typedef unsigned int u4 __attribute__((ext_vector_type(4)));
@@ -596,15 +586,16 @@ __global__ __launch_bounds__(64 * kSmallWaves) void k_mxs(MxgArgs p) {
         f.ws[m][rb] = BLK ? (int)erow[m][rb][c * 4] : 127;
       }
 #pragma unroll
-    for (int t = 0; t < kTerms; ++t)
+    for (int b = 0; b < MB; ++b) {
+      const uint8_t* src = xrow[b] + (size_t)c * kChunkBytes;
 #pragma unroll
-      for (int b = 0; b < MB; ++b) {
-        const uint8_t* src = xrow[t][b] + (size_t)c * 128;
-        const int4 lo = *reinterpret_cast<const int4*>(src);
-        const int4 hi = *reinterpret_cast<const int4*>(src + 64);
+      for (int t = 0; t < kTerms; ++t) {
+        const int4 lo = *reinterpret_cast<const int4*>(src + t * kFragBytes);
+        const int4 hi = *reinterpret_cast<const int4*>(src + t * kFragBytes + 1024);
         f.x[t][b] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-        f.xs[t][b] = srow[t][b][c * 4];
       }
+      f.xs[b] = srow[b][c * (kChunkScaleBytes / 4)];
+    }
   };
 
   v4f acc[MATS][RB][MB];
@@ -642,7 +633,7 @@ __global__ __launch_bounds__(64 * kSmallWaves) void k_mxs(MxgArgs p) {
               for (int b = 0; b < MB; ++b)
                 acc[m][rb][b] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
                     f[i].w[m][rb], f[i].x[t][b], acc[m][rb][b], wfmt<DT>(), 0, 0, f[i].ws[m][rb],
-                    0, f[i].xs[t][b]);
+                    0, (int)((f[i].xs[b] >> (8 * t)) & 0xFFu));
       }
     }
   }
@@ -689,7 +680,7 @@ __global__ __launch_bounds__(64 * kSmallWaves) void k_mxs(MxgArgs p) {
         p.post[oi] = (float)act_f64(p.act, v);
       } else {
         p.pre[oi] = y;
-        if (p.post) p.post[oi] = y;
+        if (p.post && p.post != p.pre) p.post[oi] = y;
       }
     }
   }
@@ -711,13 +702,13 @@ void launch_small(const MxgArgs& p, hipStream_t st) {
 
 template <int DT, bool BLK, int MATS>
 Status launch_t(const MxgArgs& p, int bm, hipStream_t st) {
-  if (bm == kBM2) {
+  if (bm == kBM) {
     constexpr int bn = MATS == 2 ? 64 : 128;
     if ((size_t)kTerms * p.mpad * p.kpad >= (1ull << 31) ||
         (size_t)round_up(p.N, 128) * p.pitch >= (1ull << 31))
       return Status::err(kUnsupported, "mxg: operands above 2 GiB");
-    const int tiles_m = p.mpad / kBM2, tiles_n = (p.N + bn - 1) / bn;
-    k_mxg2<DT, BLK, MATS, false><<<(unsigned)(tiles_m * tiles_n), kThreads, 0, st>>>(
+    const int tiles_m = p.mpad / kBM, tiles_n = (p.N + bn - 1) / bn;
+    k_mxg<DT, BLK, MATS, false, kMxgWaves><<<(unsigned)(tiles_m * tiles_n), 64 * kMxgWaves, 0, st>>>(
         p, nullptr, tiles_m, tiles_n);
   } else {
     if (p.mpad <= 16) launch_small<DT, BLK, MATS, 1>(p, st);
@@ -738,11 +729,12 @@ Status launch_m(const MxgArgs& p, int dtype, bool blk, int bm, hipStream_t st) {
 
 }  // namespace
 
-int mxg_block_m(int M) { return M <= 32 ? 16 : kBM2; }
+int mxg_block_m(int M) { return M <= 32 ? 16 : kBM; }
 
 size_t split_bytes(int M, int kpad) {
   const size_t mpad = (size_t)round_up(M, mxg_block_m(M));
-  return (size_t)kTerms * mpad * kpad + (size_t)kTerms * mpad * (kpad / 32);
+  // term codes, then one exponent dword per (16-row block, K chunk, lane)
+  return (size_t)kTerms * mpad * kpad + mpad * (size_t)kpad / 8;
 }
 
 Status launch_split(const float* x, int x_stride, int M, int cols, int kpad, uint8_t* buf,
@@ -750,8 +742,8 @@ Status launch_split(const float* x, int x_stride, int M, int cols, int kpad, uin
   const int mpad = (int)round_up(M, mxg_block_m(M));
   uint8_t* a = buf;
   uint8_t* as = buf + (size_t)kTerms * mpad * kpad;
-  const int64_t items = (int64_t)mpad * (kpad / 4);
-  const unsigned grid = (unsigned)((items + kThreads - 1) / kThreads);
+  const int64_t waves = (int64_t)(mpad / 16) * (kpad / 128);
+  const unsigned grid = (unsigned)((waves + kThreads / 64 - 1) / (kThreads / 64));
   const bool vec = (x_stride % 4 == 0) && ((reinterpret_cast<uintptr_t>(x) & 15u) == 0);
   if (vec) k_split<true><<<grid, kThreads, 0, st>>>(x, x_stride, M, cols, mpad, kpad, a, as, nullptr);
   else k_split<false><<<grid, kThreads, 0, st>>>(x, x_stride, M, cols, mpad, kpad, a, as, nullptr);
@@ -762,8 +754,8 @@ Status launch_split_group(const SplitJob* jobs, int n, bool vec, int x_stride, i
                           int kpad, hipStream_t st) {
   if (n <= 0 || !jobs) return Status::err(kInvalid, "split group: no members");
   const int mpad = (int)round_up(M, mxg_block_m(M));
-  const int64_t items = (int64_t)mpad * (kpad / 4);
-  const dim3 grid((unsigned)((items + kThreads - 1) / kThreads), (unsigned)n);
+  const int64_t waves = (int64_t)(mpad / 16) * (kpad / 128);
+  const dim3 grid((unsigned)((waves + kThreads / 64 - 1) / (kThreads / 64)), (unsigned)n);
   if (vec) k_split<true><<<grid, kThreads, 0, st>>>(nullptr, x_stride, M, cols, mpad, kpad, nullptr, nullptr, jobs);
   else k_split<false><<<grid, kThreads, 0, st>>>(nullptr, x_stride, M, cols, mpad, kpad, nullptr, nullptr, jobs);
   return hip_status(hipGetLastError(), "split group launch");
@@ -772,8 +764,8 @@ Status launch_split_group(const SplitJob* jobs, int n, bool vec, int x_stride, i
 template <int DT, bool BLK, int MATS>
 Status launch_group_t(const MxgArgs* tab, const MxgArgs& p, int n, hipStream_t st) {
   constexpr int bn = MATS == 2 ? 64 : 128;
-  const int tiles_m = p.mpad / kBM2, tiles_n = (p.N + bn - 1) / bn;
-  k_mxg2<DT, BLK, MATS, true><<<(unsigned)(n * tiles_m * tiles_n), kThreads, 0, st>>>(
+  const int tiles_m = p.mpad / kBM, tiles_n = (p.N + bn - 1) / bn;
+  k_mxg<DT, BLK, MATS, true, kMxgWaves><<<(unsigned)(n * tiles_m * tiles_n), 64 * kMxgWaves, 0, st>>>(
       p, tab, tiles_m, tiles_n);
   return hip_status(hipGetLastError(), "mxg group launch");
 }
@@ -781,7 +773,7 @@ Status launch_group_t(const MxgArgs* tab, const MxgArgs& p, int n, hipStream_t s
 Status launch_mxg_group(const MxgArgs* tab, const MxgArgs& p, int n, int dtype, bool blk,
                         hipStream_t st) {
   if (n <= 0 || !tab) return Status::err(kInvalid, "mxg group: no members");
-  if (mxg_block_m(p.M) != kBM2 || p.mpad % kBM2 != 0 || p.kpad % 256 != 0)
+  if (mxg_block_m(p.M) != kBM || p.mpad % kBM != 0 || p.kpad % 256 != 0)
     return Status::err(kInvalid, "mxg group: needs the large-tile layout");
   if ((size_t)kTerms * p.mpad * p.kpad >= (1ull << 31) ||
       (size_t)round_up(p.N, 128) * p.pitch >= (1ull << 31))
