@@ -64,13 +64,27 @@ def test_release_smoke_known_answer(gpu):
 ])
 def test_integer_exact_bit_for_bit(gpu, oracle, dt, values):
     rng = np.random.default_rng(dt)
-    for rows, cols, batch in [(129, 1000, 1), (64, 4096, 1), (5, 77, 3), (9, 300, 9)]:
+    for rows, cols, batch in [(129, 1000, 1), (64, 4096, 1), (5, 77, 3), (9, 300, 9), (24, 9300, 1)]:
         W = rng.choice(np.array(values, np.float32), (rows, cols))
         x = rng.integers(-4, 5, (batch, cols)).astype(np.float32)
         pre, post = run(gpu, dt, 0, W, x)
         o_pre, _ = oracle_dense(oracle, dt, 0, W, x)
         assert np.array_equal(pre, o_pre), (rows, cols, batch)
         assert np.array_equal(post, o_pre)
+
+
+@pytest.mark.parametrize("dt", [4, 16])
+@pytest.mark.parametrize("scheme", [2, 3])
+@pytest.mark.parametrize("rows,cols", [(70, 3000), (40, 5000), (24, 8000), (16, 9300)])
+def test_gemv_k_split_over_waves(gpu, oracle, dt, scheme, rows, cols):
+    """Batch-1 GEMV whose K axis spans 2-10 chunks of 1 KiB per wave (FP8: 3, 5,
+    8, 10; FP4: 2, 3, 4, 5), so groups of 2, 3, 4, 6 and 8 waves split it."""
+    rng = np.random.default_rng(rows * cols + dt + scheme)
+    W = rng.standard_normal((rows, cols)).astype(np.float32) / np.sqrt(cols)
+    x = rng.standard_normal((1, cols)).astype(np.float32)
+    pre, _ = run(gpu, dt, scheme, W, x)
+    o_pre, _ = oracle_dense(oracle, dt, scheme, W, x)
+    assert rel_l2(pre, o_pre) <= TOL_GEMV, (rows, cols)
 
 
 @pytest.mark.parametrize("dt", [4, 5, 16])

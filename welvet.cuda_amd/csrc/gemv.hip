@@ -355,6 +355,10 @@ Status launch_m(const GemvArgs& a, int dtype, bool blk, int batch, GemvTile t, h
   switch (t.waves) {
   case 1: return launch_w<MATS, 1>(a, dtype, blk, batch, t.rows, st);
   case 2: return launch_w<MATS, 2>(a, dtype, blk, batch, t.rows, st);
+  // 3, 6 and 8 waves (K axes of 3, 5-6 and 7-8 chunks) come with 8 rows only
+  case 3: return launch_r<8, MATS, 3>(a, dtype, blk, batch, st);
+  case 6: return launch_r<8, MATS, 6>(a, dtype, blk, batch, st);
+  case 8: return launch_r<8, MATS, 8>(a, dtype, blk, batch, st);
   default: return launch_w<MATS, 4>(a, dtype, blk, batch, t.rows, st);
   }
 }
@@ -362,12 +366,18 @@ Status launch_m(const GemvArgs& a, int dtype, bool blk, int batch, GemvTile t, h
 }  // namespace
 
 GemvTile gemv_tile(int dtype, int kpad, int rows, int mats, int cus) {
-  // K chunks of 1 KiB per wave: waves per group = chunks (at most 4), then
-  // rows per group so that the grid has >= 8 waves per CU when it can.
+  // K chunks of 1 KiB per wave. Waves per group: one per chunk up to 8
+  // chunks (5 -> 6, 7 -> 8), so no wave streams two chunks while another
+  // idles; 4 beyond that. Then rows per group so that the grid has >= 8
+  // waves per CU when it can (8 rows with 3, 6 or 8 waves).
   const int ks = dtype == kFP4 ? 32 : 16;
   const int chunks = (kpad + 64 * ks - 1) / (64 * ks);
   GemvTile t;
-  t.waves = chunks >= 4 ? 4 : chunks >= 2 ? 2 : 1;
+  t.waves = chunks <= 4 ? chunks : chunks <= 6 ? 6 : chunks <= 8 ? 8 : 4;
+  if (t.waves == 3 || t.waves >= 6) {
+    t.rows = 8;
+    return t;
+  }
   const long want = 8L * (cus > 0 ? cus : 256);
   t.rows = 16;
   while (t.rows > 2 && ((long)rows + t.rows - 1) / t.rows * t.waves < want) t.rows /= 2;
@@ -378,6 +388,8 @@ GemvTile gemv_tile(int dtype, int kpad, int rows, int mats, int cus) {
 Status launch_gemv(const GemvArgs& a, int dtype, bool blk, int batch, GemvTile t, hipStream_t st) {
   if (t.rows != 2 && t.rows != 4 && t.rows != 8 && t.rows != 16)
     return Status::err(kInvalid, "gemv: rows per group must be 2, 4, 8 or 16");
+  if ((t.waves == 3 || t.waves == 6 || t.waves == 8) && t.rows != 8)
+    return Status::err(kInvalid, "gemv: 3, 6 or 8 waves need 8 rows per group");
   return a.mats == 2 ? launch_m<2>(a, dtype, blk, batch, t, st)
                      : launch_m<1>(a, dtype, blk, batch, t, st);
 }

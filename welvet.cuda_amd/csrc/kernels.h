@@ -36,7 +36,8 @@ struct GemvArgs {
   const double* bias = nullptr;
   int bias_len = 0;
 };
-// Rows per workgroup (2, 4, 8, 16) and waves per workgroup (1, 2, 4; they split K).
+// Rows per workgroup (2, 4, 8, 16) and waves per workgroup (1, 2, 4, or 3, 6,
+// 8 with 8 rows; they split K).
 struct GemvTile {
   int rows = 8;
   int waves = 4;
