@@ -87,6 +87,26 @@ def test_gemv_k_split_over_waves(gpu, oracle, dt, scheme, rows, cols):
     assert rel_l2(pre, o_pre) <= TOL_GEMV, (rows, cols)
 
 
+@pytest.mark.parametrize("dt,scheme", [(4, 2), (16, 3), (5, 0)])
+@pytest.mark.parametrize("rows,cols,batch", [
+    (2176, 1000, 9),    # 2 row blocks per wave, grid past the 128-row padding
+    (4096, 3000, 16),   # K split 16 ways
+    (300, 4096, 30),    # 2 activation row blocks, 1 row block per wave
+    (2100, 3000, 17),   # both, ragged N
+])
+def test_small_batch_k_split(gpu, oracle, dt, scheme, rows, cols, batch):
+    """Batches of 5-32 rows take the weight-streaming GEMM, split along K into
+    partial sums that a second kernel adds (bias and activation there)."""
+    rng = np.random.default_rng(rows + cols + batch + dt)
+    W = rng.standard_normal((rows, cols)).astype(np.float32) / np.sqrt(cols)
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    bias = rng.standard_normal(rows) * 0.1
+    pre, post = run(gpu, dt, scheme, W, x, act=2, bias=bias)
+    o_pre, o_post = oracle_dense(oracle, dt, scheme, W, x, act=2, bias=bias)
+    assert rel_l2(pre, o_pre) <= TOL_MFMA, (rows, cols, batch)
+    assert rel_l2(post, o_post) <= TOL_MFMA, (rows, cols, batch)
+
+
 @pytest.mark.parametrize("dt", [4, 5, 16])
 @pytest.mark.parametrize("scheme", [0, 1, 2, 3])
 @pytest.mark.parametrize("rows,cols,batch", [(33, 70, 1), (300, 1024, 2), (7, 33, 3), (1, 1, 1)])

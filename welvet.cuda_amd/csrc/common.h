@@ -91,9 +91,15 @@ struct DeviceWeights {
   DevBuf codes;      // [rpad][pitch]
   DevBuf row_scale;  // float[rpad]
   DevBuf blk;        // uint8[rpad][nblk], BLOCK32 only
+  // the same exponents in matrix-core lane order, BLOCK32 only: per 16-row
+  // block and group of 4 K chunks of 128, one dword per lane l (row l % 16,
+  // block l / 16 of each chunk), byte j = chunk j of the group:
+  // uint8[rpad / 16][ceil(kpad / 512)][64][4]
+  DevBuf blk_frag;
   const uint8_t* d_codes() const { return codes.as<const uint8_t>(); }
   const float* d_scale() const { return row_scale.as<const float>(); }
   const uint8_t* d_blk() const { return scheme == 3 ? blk.as<const uint8_t>() : nullptr; }
+  const uint8_t* d_blkf() const { return scheme == 3 ? blk_frag.as<const uint8_t>() : nullptr; }
 };
 
 constexpr int kRowPad = 128;

@@ -89,8 +89,15 @@ struct MxgArgs {
   int need_epi = 0;
   const double* bias = nullptr;
   int bias_len = 0;
+  // small-M products split along K: raw partial sums (mxg_part_bytes)
+  float* part = nullptr;
+  // block exponents in lane order (DeviceWeights::blk_frag), BLOCK32 only
+  const uint8_t* blkf[2] = {nullptr, nullptr};
 };
 int mxg_block_m(int M);
+// Bytes of the K-split partial buffer the product of M rows with N outputs
+// (per matrix) needs; 0 when it takes no split.
+size_t mxg_part_bytes(int M, int kpad, int N, int mats);
 // Bytes of the split buffer for M rows of kpad columns.
 size_t split_bytes(int M, int kpad);
 // x [M][cols] (row stride x_stride) -> split terms in buf.

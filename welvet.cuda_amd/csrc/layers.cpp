@@ -174,8 +174,13 @@ static MxvArgs mxv_args(const DenseLayer& L, const float* x, int x_stride, int b
 
 bool uses_split(int batch) { return batch > kMxvMaxBatch; }
 
+// Split activations plus, for small batches split along K, the partial sums.
+static size_t gemm_ws_bytes(const DenseLayer& L, int batch, int mats) {
+  return split_bytes(batch, L.dev.kpad) + mxg_part_bytes(batch, L.dev.kpad, L.out, mats);
+}
+
 size_t dense_workspace_bytes(const DenseLayer& L, int batch) {
-  return uses_split(batch) ? split_bytes(batch, L.dev.kpad) : 0;
+  return uses_split(batch) ? gemm_ws_bytes(L, batch, 1) : 0;
 }
 
 Status ensure_split(Workspace* ws, size_t n) {
@@ -193,6 +198,7 @@ static MxgArgs mxg_args(const DenseLayer& L, int batch, const uint8_t* split) {
   p.codes[0] = L.dev.d_codes();
   p.scale[0] = L.dev.d_scale();
   p.blk[0] = L.dev.d_blk();
+  p.blkf[0] = L.dev.d_blkf();
   p.pitch = L.dev.pitch;
   p.nblk = L.dev.nblk;
   p.kpad = L.dev.kpad;
@@ -202,12 +208,14 @@ static MxgArgs mxg_args(const DenseLayer& L, int batch, const uint8_t* split) {
   p.need_epi = L.need_epi() ? 1 : 0;
   p.bias = L.bias_dev.as<const double>();
   p.bias_len = L.bias_len;
+  // the partial sums follow the split terms (gemm_ws_bytes)
+  p.part = reinterpret_cast<float*>(const_cast<uint8_t*>(split) + split_bytes(batch, L.dev.kpad));
   return p;
 }
 
-Status dense_forward_split(const DenseLayer& L, int batch, const uint8_t* split, float* pre,
-                           float* post, hipStream_t st) {
-  MxgArgs p = mxg_args(L, batch, split);
+Status dense_forward_split(const DenseLayer& L, int batch, Workspace* ws, float* pre, float* post,
+                           hipStream_t st) {
+  MxgArgs p = mxg_args(L, batch, split_buf(ws));
   p.pre = pre;
   p.post = post;
   return launch_mxg(p, L.dev.dtype, L.dev.scheme == kSchemeBlock32, st);
@@ -218,9 +226,9 @@ Status dense_forward(const DenseLayer& L, int batch, const float* x, float* pre,
   if (batch <= 0 || !x || !pre) return Status::err(kInvalid, "dense forward: bad args");
   if (L.need_epi() && !post) return Status::err(kInvalid, "dense forward: post needed");
   if (uses_split(batch)) {
-    WV_TRY(ensure_split(ws, split_bytes(batch, L.dev.kpad)));
-    WV_TRY(launch_split(x, L.in, batch, L.in, L.dev.kpad, ws->b.as<uint8_t>(), st));
-    return dense_forward_split(L, batch, ws->b.as<uint8_t>(), pre, post, st);
+    WV_TRY(ensure_split(ws, gemm_ws_bytes(L, batch, 1)));
+    WV_TRY(launch_split(x, L.in, batch, L.in, L.dev.kpad, split_buf(ws), st));
+    return dense_forward_split(L, batch, ws, pre, post, st);
   }
   if (batch >= 2 && batch <= kMxvMaxBatch) {
     MxvArgs m = mxv_args(L, x, L.in, batch);
@@ -262,6 +270,7 @@ Status dense_group_build(const DenseLayer* const* layers, int n, int batch,
     jobs[i].buf = buf;
     vec = vec && (reinterpret_cast<uintptr_t>(x[i]) & 15u) == 0;
     tab[i] = mxg_args(*L, batch, buf);
+    tab[i].part = nullptr;  // large tiles: no K split
     tab[i].pre = pre[i];
     tab[i].post = post ? post[i] : nullptr;
   }
@@ -300,7 +309,7 @@ Status swiglu_build(int in, int inter, int dtype, int scheme, const float* G, co
 
 size_t swiglu_workspace_bytes(const SwiGLULayer& L, int rows) {
   if (!uses_split(rows)) return 0;
-  const size_t a = split_bytes(rows, L.gate.dev.kpad), b = split_bytes(rows, L.down.dev.kpad);
+  const size_t a = gemm_ws_bytes(L.gate, rows, 2), b = gemm_ws_bytes(L.down, rows, 1);
   return a > b ? a : b;
 }
 
@@ -320,18 +329,19 @@ Status swiglu_forward(const SwiGLULayer& L, int rows, const float* x, float* h, 
   }
   if (uses_split(rows)) {
     WV_TRY(ensure_split(ws, swiglu_workspace_bytes(L, rows)));
-    uint8_t* buf = ws->b.as<uint8_t>();
+    uint8_t* buf = split_buf(ws);
     WV_TRY(launch_split(x, L.in, rows, L.in, L.gate.dev.kpad, buf, st));
     MxgArgs p = mxg_args(L.gate, rows, buf);
     p.mats = 2;
     p.codes[1] = L.up.dev.d_codes();
     p.scale[1] = L.up.dev.d_scale();
     p.blk[1] = L.up.dev.d_blk();
+    p.blkf[1] = L.up.dev.d_blkf();
     p.pre = h;
     p.need_epi = 0;
     WV_TRY(launch_mxg(p, L.gate.dev.dtype, L.gate.dev.scheme == kSchemeBlock32, st));
     WV_TRY(launch_split(h, L.inter, rows, L.inter, L.down.dev.kpad, buf, st));
-    return dense_forward_split(L.down, rows, buf, y, nullptr, st);
+    return dense_forward_split(L.down, rows, ws, y, nullptr, st);
   }
   GemvArgs a = gemv_args(L.gate, x, L.in);
   a.mats = 2;
@@ -385,8 +395,12 @@ size_t mha_workspace_bytes(const MHALayer& L, int batch, int seq) {
 
 static size_t mha_split_bytes(const MHALayer& L, int T) {
   if (!uses_split(T)) return 0;
-  const size_t a = split_bytes(T, L.q.dev.kpad), b = split_bytes(T, L.o.dev.kpad);
-  return a > b ? a : b;
+  size_t n = 0;
+  for (const DenseLayer* d : {&L.q, &L.k, &L.v, &L.o}) {
+    const size_t b = gemm_ws_bytes(*d, T, 1);
+    n = b > n ? b : n;
+  }
+  return n;
 }
 
 static bool mha_rope(const MHAConfig& c) { return (c.pos == 0 || c.pos == 3) && c.head_dim / 2 > 0; }
@@ -424,10 +438,10 @@ Status mha_forward(const MHALayer& L, int batch, int seq, const float* x, float*
   if (uses_split(T)) {
     // Q, K and V read the same activations: split them once
     WV_TRY(ensure_split(ws, mha_split_bytes(L, T)));
-    WV_TRY(launch_split(x, c.d_model, T, c.d_model, L.q.dev.kpad, ws->b.as<uint8_t>(), st));
-    WV_TRY(dense_forward_split(L.q, T, ws->b.as<uint8_t>(), qb, nullptr, st));
-    WV_TRY(dense_forward_split(L.k, T, ws->b.as<uint8_t>(), kb, nullptr, st));
-    WV_TRY(dense_forward_split(L.v, T, ws->b.as<uint8_t>(), vb, nullptr, st));
+    WV_TRY(launch_split(x, c.d_model, T, c.d_model, L.q.dev.kpad, split_buf(ws), st));
+    WV_TRY(dense_forward_split(L.q, T, ws, qb, nullptr, st));
+    WV_TRY(dense_forward_split(L.k, T, ws, kb, nullptr, st));
+    WV_TRY(dense_forward_split(L.v, T, ws, vb, nullptr, st));
   } else {
     WV_TRY(dense_forward(L.q, T, x, qb, nullptr, ws, st));
     WV_TRY(dense_forward(L.k, T, x, kb, nullptr, ws, st));

@@ -61,9 +61,13 @@ Status dense_forward(const DenseLayer& L, int batch, const float* x, float* pre,
 size_t dense_workspace_bytes(const DenseLayer& L, int batch);
 // True when `batch` rows take the split + batched-MFMA path.
 bool uses_split(int batch);
-// Batched path with activations already split (launch_split with L.dev.kpad).
-Status dense_forward_split(const DenseLayer& L, int batch, const uint8_t* split, float* pre,
-                           float* post, hipStream_t st);
+// The activation-split workspace (Workspace::b): the split terms, then the
+// K-split partial sums of the products that use them.
+inline uint8_t* split_buf(Workspace* ws) { return ws->b.as<uint8_t>(); }
+// Batched path with activations already split into split_buf(ws)
+// (launch_split with L.dev.kpad).
+Status dense_forward_split(const DenseLayer& L, int batch, Workspace* ws, float* pre, float* post,
+                           hipStream_t st);
 // Grows ws->b to at least n bytes (mount time; a forward that finds it too
 // small allocates, which a captured graph cannot do).
 Status ensure_split(Workspace* ws, size_t n);

@@ -37,6 +37,7 @@ constexpr int kChunkScaleBytes = 256;             // one exponent dword per lane
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef float v2f __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ double act_f64(int act, double x) {
   switch (act) {
@@ -223,6 +224,9 @@ __device__ __forceinline__ MxgArgs load_args(ConstArgs t) {
   p.need_epi = t->need_epi;
   p.bias = t->bias;
   p.bias_len = t->bias_len;
+  p.part = t->part;
+  p.blkf[0] = t->blkf[0];
+  p.blkf[1] = t->blkf[1];
   return p;
 }
 
@@ -525,151 +529,282 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
   }
 }
 
-// Small-M GEMM (M <= 32 activation rows: the weight-streaming regime). A
-// workgroup owns RB blocks of 16 weight rows (per matrix) and all K; its 8
-// waves take the 128-wide K chunks round-robin. Each wave loads the weight
-// fragments of a chunk straight from HBM into registers (non-temporal, no
-// LDS) and the activation-term fragments from the split buffer (small,
-// L2-resident; RB weight blocks share each of them), and runs kTerms MFMAs
-// per weight fragment and 16-row activation block; the next chunk's loads
-// are issued before the current chunk's MFMAs. The 8 partial tiles meet in
-// LDS for the epilogue.
+// Small-M GEMM (M <= 32 activation rows: the weight-streaming regime), split
+// along K. Workgroup (g, ks) has 8 waves; wave w owns RB blocks of 16 weight
+// rows (of each matrix), rows 128 RB g + 16 (RB w + j) + .., over the K
+// chunks [k0, k1) of split ks (at most KRT chunks). A CU streams HBM at a
+// bounded rate (~30-40 GB/s), so the split fills all CUs with one round of
+// workgroups, and RB = 2 halves the activation terms each CU stages. The activation terms of that K range (all M
+// rows, in operand order) are staged in LDS once; the weights then stream
+// from HBM straight into registers D - 1 chunks ahead, in the order they are
+// consumed, so 8 (D - 1) chunks per CU are in flight. The KRT steps are
+// straight-line code (no loop back-edge, which makes the compiler wait for
+// every outstanding load) and every load is unconditional: a step past the
+// range repeats the last chunk with its weights zeroed. With one split the
+// epilogue is applied here; otherwise each split writes its raw sums to the
+// partial buffer and k_mxs_reduce adds them and applies the epilogue.
+typedef __attribute__((address_space(3))) void* LdsPtr;
+typedef const __attribute__((address_space(1))) void* GlobalPtr;
+
+// Direct-to-LDS copies: lane i of the wave writes its bytes at base + size * i.
+// (The copy size of the builtin must be a literal.)
+__device__ __forceinline__ void lds_dma16(const void* src, void* lds_base) {
+  __builtin_amdgcn_global_load_lds((GlobalPtr)src, (LdsPtr)lds_base, 16, 0, 0);
+}
+__device__ __forceinline__ void lds_dma4(const void* src, void* lds_base) {
+  __builtin_amdgcn_global_load_lds((GlobalPtr)src, (LdsPtr)lds_base, 4, 0, 0);
+}
+
 constexpr int kSmallWaves = 8;
 
-template <int DT, bool BLK, int MATS, int MB, int RB>
-__global__ __launch_bounds__(64 * kSmallWaves) void k_mxs(MxgArgs p) {
+// Weight row blocks per wave: two once there are enough rows.
+int mxs_rb(int N) { return N >= 2048 ? 2 : 1; }
+
+// Largest K range per workgroup (chunks) for 1 or 2 activation row blocks:
+// its staged terms fill at most ~150 KB of LDS.
+constexpr int small_krt_max(int mb) { return mb == 1 ? 24 : 12; }
+
+// Splits so that the grid is one round of at most 256 workgroups (one per
+// CU), unless the K range of a workgroup would exceed the LDS.
+int mxs_ksplit(int N, int kpad, int mpad) {
+  const int S = kpad / 128, MB = mpad / 16;
+  const int rows = 16 * kSmallWaves * mxs_rb(N);
+  const int groups = (N + rows - 1) / rows;
+  int ks = 256 / groups > 1 ? 256 / groups : 1;
+  const int krt = small_krt_max(MB);
+  if (ks < (S + krt - 1) / krt) ks = (S + krt - 1) / krt;
+  return ks < S ? ks : S;
+}
+
+template <int DT, bool BLK, int MATS, int MB, int RB, int KRT, int D>
+__global__ __launch_bounds__(64 * kSmallWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_mxs(
+    MxgArgs p, int ksplit) {
+  constexpr int ROWS = 16 * kSmallWaves * RB;  // weight rows per workgroup
   constexpr bool FP4 = DT == kFP4;
   constexpr int WB = FP4 ? 64 : 128;  // code bytes per weight row per chunk
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int i16 = lane & 15, g = lane >> 4;
-  const int n0 = blockIdx.x * 16 * RB;
-  const int S = p.kpad / 128;
+  __shared__ __attribute__((aligned(16))) uint8_t sA[MB * KRT * kChunkBytes];
+  __shared__ __attribute__((aligned(16))) uint32_t sS[MB * KRT * 64];
 
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int i16 = lane & 15, g = lane >> 4;
+  const int S = p.kpad / 128, ks = blockIdx.y;
+  const int k0 = (int)((long)S * ks / ksplit), k1 = (int)((long)S * (ks + 1) / ksplit);
+  const int KR = k1 - k0;  // 1 .. KRT (the launcher's split guarantees it)
+  const int n0 = blockIdx.x * ROWS + wave * 16 * RB;
+
+  // weight rows: the codes are padded to a multiple of 128 rows; the grid
+  // may cover up to 128 more (RB = 2), whose loads are clamped to the last
+  // padded row (their outputs are never stored)
+  // Block exponents come from the lane-order copy: the dword of chunk group
+  // c / 4 (256 contiguous bytes per wave load), byte c % 4.
+  const int rmax = (p.N + 127) / 128 * 128 - 1;
+  const int egroups = (S + 3) / 4;
   const uint8_t* wrow[MATS][RB];
   const uint8_t* erow[MATS][RB];
 #pragma unroll
   for (int m = 0; m < MATS; ++m)
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-      const int row = n0 + rb * 16 + i16;
-      wrow[m][rb] = p.codes[m] + (size_t)row * p.pitch + 16 * g;
-      erow[m][rb] = BLK ? p.blk[m] + (size_t)row * p.nblk + g : nullptr;
+    for (int j = 0; j < RB; ++j) {
+      const int row = n0 + 16 * j + i16 < rmax ? n0 + 16 * j + i16 : rmax;
+      const int rb16 = (n0 + 16 * j < rmax ? n0 + 16 * j : rmax) / 16;
+      wrow[m][j] = p.codes[m] + (size_t)row * p.pitch + 16 * g;
+      erow[m][j] = BLK ? p.blkf[m] + (size_t)rb16 * egroups * 256 + lane * 4 : nullptr;
     }
-  // activation block b, chunk c: fragments at xrow[b] + c * kChunkBytes,
-  // exponent dword at srow[b][c * 64]
-  const uint8_t* xrow[MB];
-  const uint32_t* srow[MB];
-#pragma unroll
-  for (int b = 0; b < MB; ++b) {
-    xrow[b] = p.a + (size_t)b * S * kChunkBytes + lane * 16;
-    srow[b] = reinterpret_cast<const uint32_t*>(p.as + (size_t)b * S * kChunkScaleBytes) + lane;
-  }
-
-  struct Frag {
-    v8i w[MATS][RB];
-    int ws[MATS][RB];
-    v8i x[kTerms][MB];
-    uint32_t xs[MB];
+  struct WFrag {
+    u32x4 lo[MATS][RB], hi[MATS][RB];
+    uint32_t e[MATS][RB];  // exponent dword (4 chunks)
   };
-  auto load = [&](int c, Frag& f) {
-    typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+  auto load_w = [&](int r, WFrag& f) {  // chunk k0 + r, clamped to the range
+    const int c = k0 + (r < KR ? r : KR - 1);
 #pragma unroll
     for (int m = 0; m < MATS; ++m)
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb) {
-        const uint8_t* src = wrow[m][rb] + (size_t)c * WB;
-        const u4 lo = __builtin_nontemporal_load(reinterpret_cast<const u4*>(src));
-        u4 hi = u4{0u, 0u, 0u, 0u};
-        if constexpr (!FP4) hi = __builtin_nontemporal_load(reinterpret_cast<const u4*>(src + 64));
-        f.w[m][rb] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
-                         (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-        f.ws[m][rb] = BLK ? (int)erow[m][rb][c * 4] : 127;
+      for (int j = 0; j < RB; ++j) {
+        const uint8_t* src = wrow[m][j] + (size_t)c * WB;
+        f.lo[m][j] = *reinterpret_cast<const u32x4*>(src);
+        if constexpr (!FP4) f.hi[m][j] = *reinterpret_cast<const u32x4*>(src + 64);
+        f.e[m][j] = BLK ? *reinterpret_cast<const uint32_t*>(erow[m][j] + (size_t)(c >> 2) * 256)
+                        : 0x7F7F7F7Fu;
       }
-#pragma unroll
-    for (int b = 0; b < MB; ++b) {
-      const uint8_t* src = xrow[b] + (size_t)c * kChunkBytes;
-#pragma unroll
-      for (int t = 0; t < kTerms; ++t) {
-        const int4 lo = *reinterpret_cast<const int4*>(src + t * kFragBytes);
-        const int4 hi = *reinterpret_cast<const int4*>(src + t * kFragBytes + 1024);
-        f.x[t][b] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-      }
-      f.xs[b] = srow[b][c * (kChunkScaleBytes / 4)];
-    }
   };
+
+  // Activation terms into LDS with direct-to-LDS copies (1 KiB per wave
+  // instruction; exponent dwords: 256 bytes per chunk), then the first
+  // D - 1 chunks of weights; the wait leaves those weight loads in flight.
+  {
+    const int pieces = MB * KR * (kChunkBytes / 1024);
+    for (int j = wave; j < pieces; j += kSmallWaves) {
+      const int b = j / (KR * (kChunkBytes / 1024)), r = j % (KR * (kChunkBytes / 1024));
+      lds_dma16(p.a + ((size_t)b * S + k0) * kChunkBytes + r * 1024 + lane * 16, sA + j * 1024);
+    }
+    for (int j = wave; j < MB * KR; j += kSmallWaves) {
+      const int b = j / KR, r = j % KR;
+      lds_dma4(p.as + ((size_t)b * S + k0 + r) * kChunkScaleBytes + lane * 4, sS + j * 64);
+    }
+  }
+  WFrag f[D];
+#pragma unroll
+  for (int i = 0; i < D - 1; ++i) load_w(i, f[i]);
+  constexpr int PREFILL = (D - 1) * MATS * RB * (1 + (FP4 ? 0 : 1) + (BLK ? 1 : 0));
+  __builtin_amdgcn_s_waitcnt(waitcnt_imm(PREFILL, 15));
+  asm volatile("s_barrier" ::: "memory");
 
   v4f acc[MATS][RB][MB];
 #pragma unroll
   for (int m = 0; m < MATS; ++m)
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb)
+    for (int j = 0; j < RB; ++j)
 #pragma unroll
-      for (int b = 0; b < MB; ++b) acc[m][rb][b] = v4f{0.f, 0.f, 0.f, 0.f};
+      for (int b = 0; b < MB; ++b) acc[m][j][b] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  // ring of NB fragment sets: NB - 1 chunks in flight while one is computed
-  // (the body is unrolled NB times so every ring index is a constant); two
-  // sets where three would not fit the register budget
-  constexpr int NB = RB * MATS + kTerms * MB <= 7 ? 3 : 2;
-  Frag f[NB];
 #pragma unroll
-  for (int i = 0; i < NB - 1; ++i) {
-    const int cc = wave + i * kSmallWaves;
-    if (cc < S) load(cc, f[i]);
-  }
-  for (int base = wave; base < S; base += NB * kSmallWaves) {
+  for (int r = 0; r < KRT; ++r) {
+    if (r + D - 1 < KRT) load_w(r + D - 1, f[(r + D - 1) % D]);  // compile-time condition
+    __builtin_amdgcn_sched_barrier(0);
+    const bool live = r < KR;  // uniform
+    const int rr = live ? r : KR - 1;
+    v8i x[kTerms][MB];
+    uint32_t xs[MB];
 #pragma unroll
-    for (int i = 0; i < NB; ++i) {
-      const int cc = base + i * kSmallWaves;
-      if (cc < S) {
-        const int pf = cc + (NB - 1) * kSmallWaves;
-        if (pf < S) load(pf, f[(i + NB - 1) % NB]);
+    for (int b = 0; b < MB; ++b) {
+      const uint8_t* src = sA + (size_t)(b * KR + rr) * kChunkBytes + lane * 16;
 #pragma unroll
-        for (int m = 0; m < MATS; ++m)
-#pragma unroll
-          for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-            for (int t = 0; t < kTerms; ++t)
-#pragma unroll
-              for (int b = 0; b < MB; ++b)
-                acc[m][rb][b] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-                    f[i].w[m][rb], f[i].x[t][b], acc[m][rb][b], wfmt<DT>(), 0, 0, f[i].ws[m][rb],
-                    0, (int)((f[i].xs[b] >> (8 * t)) & 0xFFu));
+      for (int t = 0; t < kTerms; ++t) {
+        const int4 lo = *reinterpret_cast<const int4*>(src + t * kFragBytes);
+        const int4 hi = *reinterpret_cast<const int4*>(src + t * kFragBytes + 1024);
+        x[t][b] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
       }
+      xs[b] = sS[(b * KR + rr) * 64 + lane];
     }
+    // a step past the range repeats the last chunk: zero weights add
+    // exactly nothing (its activations are those of a live step)
+    const WFrag& fr = f[r % D];
+    const int eb = 8 * ((k0 + rr) & 3);  // byte of this chunk in the exponent dwords
+    int we[MATS][RB];
+#pragma unroll
+    for (int m = 0; m < MATS; ++m)
+#pragma unroll
+      for (int j = 0; j < RB; ++j) we[m][j] = (int)((fr.e[m][j] >> eb) & 0xFFu);
+    v8i w[MATS][RB];
+#pragma unroll
+    for (int m = 0; m < MATS; ++m)
+#pragma unroll
+      for (int j = 0; j < RB; ++j) {
+        const u32x4 lo = fr.lo[m][j];
+        const u32x4 hi = FP4 ? u32x4{0u, 0u, 0u, 0u} : fr.hi[m][j];
+        w[m][j] = live ? v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y,
+                             (int)hi.z, (int)hi.w}
+                       : v8i{0, 0, 0, 0, 0, 0, 0, 0};
+      }
+#pragma unroll
+    for (int m = 0; m < MATS; ++m)
+#pragma unroll
+      for (int j = 0; j < RB; ++j)
+#pragma unroll
+        for (int b = 0; b < MB; ++b)
+          acc[m][j][b] = mfma_term<DT, 0>(w[m][j], x[0][b], acc[m][j][b], we[m][j], xs[b]);
+#pragma unroll
+    for (int m = 0; m < MATS; ++m)
+#pragma unroll
+      for (int j = 0; j < RB; ++j)
+#pragma unroll
+        for (int b = 0; b < MB; ++b)
+          acc[m][j][b] = mfma_term<DT, 1>(w[m][j], x[1][b], acc[m][j][b], we[m][j], xs[b]);
+#pragma unroll
+    for (int m = 0; m < MATS; ++m)
+#pragma unroll
+      for (int j = 0; j < RB; ++j)
+#pragma unroll
+        for (int b = 0; b < MB; ++b)
+          acc[m][j][b] = mfma_term<DT, 2>(w[m][j], x[2][b], acc[m][j][b], we[m][j], xs[b]);
+    __builtin_amdgcn_sched_barrier(0);
   }
 
-  // acc[m][rb][b]: lane holds weight rows n0 + rb*16 + 4g + r (r = 0..3) and
-  // activation row b*16 + i16
-  __shared__ float part[kSmallWaves][MATS][RB * MB][64][4];
+  // acc[m][j][b]: lane holds activation row 16 b + i16 and weight rows
+  // n0 + 16 j + 4g + r (r = 0..3)
+  if (ksplit > 1) {
+    const size_t npad = ((size_t)p.N + ROWS - 1) / ROWS * ROWS;
 #pragma unroll
-  for (int m = 0; m < MATS; ++m)
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb)
+    for (int j = 0; j < RB; ++j)
 #pragma unroll
       for (int b = 0; b < MB; ++b)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) part[wave][m][rb * MB + b][lane][r] = acc[m][rb][b][r];
-  __syncthreads();
-  // RB*MB tiles x 256 outputs; thread -> (tile, lane, r) positions
-  for (int o = threadIdx.x; o < RB * MB * 256; o += 64 * kSmallWaves) {
-    const int tile = o / 256, l = (o / 4) % 64, r = o % 4;
-    const int rb = tile / MB, b = tile % MB;
-    const int mrow = b * 16 + (l & 15), n = n0 + rb * 16 + 4 * (l >> 4) + r;
-    if (mrow >= p.M || n >= p.N) continue;
-    float tot[MATS];
+        for (int m = 0; m < MATS; ++m)
+          *reinterpret_cast<v4f*>(p.part + (((size_t)ks * MATS + m) * p.mpad + b * 16 + i16) * npad +
+                                  n0 + 16 * j + 4 * g) = acc[m][j][b];
+    return;
+  }
 #pragma unroll
-    for (int m = 0; m < MATS; ++m) {
-      float sum = 0.0f;
+  for (int j = 0; j < RB; ++j)
 #pragma unroll
-      for (int w = 0; w < kSmallWaves; ++w) sum += part[w][m][tile][l][r];
-      tot[m] = sum * p.scale[m][n];
+  for (int b = 0; b < MB; ++b) {
+    const int mrow = b * 16 + i16;
+    const int nb = n0 + 16 * j + 4 * g;
+    if (mrow >= p.M) continue;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int n = nb + r;
+      if (n >= p.N) break;
+      const size_t oi = (size_t)mrow * p.out_stride + n;
+      if constexpr (MATS == 2) {
+        const float gs = (float)act_f64(kSilu, (double)(acc[0][j][b][r] * p.scale[0][n]));
+        p.pre[oi] = (float)((double)gs * (double)(acc[1][j][b][r] * p.scale[1][n]));
+      } else {
+        float y = acc[0][j][b][r] * p.scale[0][n];
+        if (p.need_epi) {
+          double v = (double)y;
+          if (p.bias && n < p.bias_len) {
+            v += p.bias[n];
+            y = (float)v;
+          }
+          p.pre[oi] = y;
+          p.post[oi] = (float)act_f64(p.act, v);
+        } else {
+          p.pre[oi] = y;
+          if (p.post && p.post != p.pre) p.post[oi] = y;
+        }
+      }
     }
+  }
+}
+
+// Adds the K-split partial sums of k_mxs (in split order) and applies the
+// epilogue; one thread per 4 consecutive outputs, the partial loads of 8
+// splits in flight at a time.
+template <int MATS>
+__global__ __launch_bounds__(kThreads) void k_mxs_reduce(MxgArgs p, int ksplit, int rows) {
+  const int n4 = (p.N + 3) / 4;
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= (int64_t)p.M * n4) return;
+  const int mrow = (int)(i / n4), nb = (int)(i % n4) * 4;
+  const size_t npad = ((size_t)p.N + rows - 1) / rows * rows;
+  v4f tot[MATS];
+#pragma unroll
+  for (int m = 0; m < MATS; ++m) tot[m] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+  for (int k2 = 0; k2 < ksplit; k2 += 8) {
+    v4f t[MATS][8];
+#pragma unroll
+    for (int m = 0; m < MATS; ++m)
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int kk = k2 + u < ksplit ? k2 + u : ksplit - 1;
+        t[m][u] = *reinterpret_cast<const v4f*>(p.part + (((size_t)kk * MATS + m) * p.mpad + mrow) * npad + nb);
+      }
+#pragma unroll
+    for (int m = 0; m < MATS; ++m)
+#pragma unroll
+      for (int u = 0; u < 8; ++u) tot[m] += k2 + u < ksplit ? t[m][u] : v4f{0.f, 0.f, 0.f, 0.f};
+  }
+#pragma unroll 1
+  for (int r = 0; r < 4 && nb + r < p.N; ++r) {
+    const int n = nb + r;
     const size_t oi = (size_t)mrow * p.out_stride + n;
     if constexpr (MATS == 2) {
-      const float gs = (float)act_f64(kSilu, (double)tot[0]);
-      p.pre[oi] = (float)((double)gs * (double)tot[1]);
+      const float gs = (float)act_f64(kSilu, (double)(tot[0][r] * p.scale[0][n]));
+      p.pre[oi] = (float)((double)gs * (double)(tot[1][r] * p.scale[1][n]));
     } else {
-      float y = tot[0];
+      float y = tot[0][r] * p.scale[0][n];
       if (p.need_epi) {
         double v = (double)y;
         if (p.bias && n < p.bias_len) {
@@ -686,18 +821,44 @@ __global__ __launch_bounds__(64 * kSmallWaves) void k_mxs(MxgArgs p) {
   }
 }
 
+template <int DT, bool BLK, int MATS, int MB, int RB, int KRT>
+void launch_small_krt(const MxgArgs& p, int ksplit, hipStream_t st) {
+  // ring depth: 6-14 KiB of weights in flight per wave within the register
+  // budget of two waves per SIMD
+  constexpr int D0 = (DT == kFP4 ? 8 : 6) / MATS + (DT == kFP4 && MATS == 2 ? 2 : 0);
+  constexpr int D1 = RB == 2 ? (D0 + 1) / 2 + 1 : D0;
+  constexpr int D = D1 < KRT ? D1 : KRT;
+  const int rows = 16 * kSmallWaves * RB;
+  const dim3 grid((unsigned)((p.N + rows - 1) / rows), (unsigned)ksplit);
+  k_mxs<DT, BLK, MATS, MB, RB, KRT, D><<<grid, 64 * kSmallWaves, 0, st>>>(p, ksplit);
+}
+
+template <int DT, bool BLK, int MATS, int MB, int RB>
+void launch_small_rb(const MxgArgs& p, int ksplit, hipStream_t st) {
+  const int S = p.kpad / 128, kr = (S + ksplit - 1) / ksplit;  // largest range
+  constexpr int K1 = MB == 1 ? 4 : 4, K2 = MB == 1 ? 8 : 8, K3 = MB == 1 ? 12 : 12;
+  if (kr <= K1) launch_small_krt<DT, BLK, MATS, MB, RB, K1>(p, ksplit, st);
+  else if (kr <= K2) launch_small_krt<DT, BLK, MATS, MB, RB, K2>(p, ksplit, st);
+  else if (kr <= K3 || MB == 2) launch_small_krt<DT, BLK, MATS, MB, RB, K3>(p, ksplit, st);
+  else if (kr <= 16) launch_small_krt<DT, BLK, MATS, MB, RB, (MB == 1 ? 16 : 12)>(p, ksplit, st);
+  else launch_small_krt<DT, BLK, MATS, MB, RB, small_krt_max(MB)>(p, ksplit, st);
+}
+
 template <int DT, bool BLK, int MATS, int MB>
-void launch_small(const MxgArgs& p, hipStream_t st) {
-  // the largest weight-row group that still gives >= 256 workgroups, capped
-  // where the register budget of two waves per SIMD would spill
-  constexpr int kMaxRB = MATS * MB == 1 ? 4 : MATS * MB == 2 ? 2 : 1;
-  const int n16 = (p.N + 15) / 16;
-  if (kMaxRB >= 4 && n16 >= 4 * 256)
-    k_mxs<DT, BLK, MATS, MB, (kMaxRB >= 4 ? 4 : 1)><<<(n16 + 3) / 4, 64 * kSmallWaves, 0, st>>>(p);
-  else if (kMaxRB >= 2 && n16 >= 2 * 256)
-    k_mxs<DT, BLK, MATS, MB, (kMaxRB >= 2 ? 2 : 1)><<<(n16 + 1) / 2, 64 * kSmallWaves, 0, st>>>(p);
-  else
-    k_mxs<DT, BLK, MATS, MB, 1><<<n16, 64 * kSmallWaves, 0, st>>>(p);
+Status launch_small(const MxgArgs& p, hipStream_t st) {
+  const int ksplit = mxs_ksplit(p.N, p.kpad, p.mpad);
+  if (ksplit > 1 && !p.part) return Status::err(kInvalid, "mxg: K-split partial buffer missing");
+  const int rb = mxs_rb(p.N);
+  if (rb == 2) launch_small_rb<DT, BLK, MATS, MB, 2>(p, ksplit, st);
+  else launch_small_rb<DT, BLK, MATS, MB, 1>(p, ksplit, st);
+  if (ksplit > 1) {
+    // the kernel boundary makes every split's partial sums visible (the
+    // XCDs' L2 caches are not coherent with each other)
+    const int64_t n = (int64_t)p.M * ((p.N + 3) / 4);
+    k_mxs_reduce<MATS><<<(unsigned)((n + kThreads - 1) / kThreads), kThreads, 0, st>>>(
+        p, ksplit, 16 * kSmallWaves * rb);
+  }
+  return hip_status(hipGetLastError(), "mxs launch");
 }
 
 template <int DT, bool BLK, int MATS>
@@ -711,8 +872,7 @@ Status launch_t(const MxgArgs& p, int bm, hipStream_t st) {
     k_mxg<DT, BLK, MATS, false, kMxgWaves><<<(unsigned)(tiles_m * tiles_n), 64 * kMxgWaves, 0, st>>>(
         p, nullptr, tiles_m, tiles_n);
   } else {
-    if (p.mpad <= 16) launch_small<DT, BLK, MATS, 1>(p, st);
-    else launch_small<DT, BLK, MATS, 2>(p, st);
+    return p.mpad <= 16 ? launch_small<DT, BLK, MATS, 1>(p, st) : launch_small<DT, BLK, MATS, 2>(p, st);
   }
   return hip_status(hipGetLastError(), "mxg launch");
 }
@@ -730,6 +890,14 @@ Status launch_m(const MxgArgs& p, int dtype, bool blk, int bm, hipStream_t st) {
 }  // namespace
 
 int mxg_block_m(int M) { return M <= 32 ? 16 : kBM; }
+
+size_t mxg_part_bytes(int M, int kpad, int N, int mats) {
+  if (mxg_block_m(M) != 16) return 0;
+  const int mpad = (int)round_up(M, 16);
+  const int ks = mxs_ksplit(N, kpad, mpad);
+  const int rows = 16 * kSmallWaves * mxs_rb(N);
+  return ks > 1 ? (size_t)ks * mats * mpad * round_up(N, rows) * sizeof(float) : 0;
+}
 
 size_t split_bytes(int M, int kpad) {
   const size_t mpad = (size_t)round_up(M, mxg_block_m(M));

@@ -239,6 +239,29 @@ __global__ __launch_bounds__(kThreads) void k_sweep(int dtype, uint32_t first_ch
 
 inline unsigned grid_for(int64_t n) { return (unsigned)((n + kThreads - 1) / kThreads); }
 
+// Lane-order copy of the E8M0 block exponents (DeviceWeights::blk_frag): one
+// thread per output byte; chunks past the K padding get 127 (2^0).
+__global__ __launch_bounds__(kThreads) void k_blk_frag(const uint8_t* __restrict__ blk, int rpad,
+                                                       int nblk, int chunks, int groups,
+                                                       uint8_t* __restrict__ out) {
+  const int64_t t = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (t >= (int64_t)(rpad / 16) * groups * 256) return;
+  const int j = (int)(t & 3), l = (int)((t >> 2) & 63);
+  const int64_t rest = t >> 8;
+  const int q = (int)(rest % groups), rb = (int)(rest / groups);
+  const int c = 4 * q + j;
+  out[t] = c < chunks ? blk[(size_t)(rb * 16 + (l & 15)) * nblk + c * 4 + (l >> 4)] : (uint8_t)127;
+}
+
+Status build_blk_frag(DeviceWeights* dw, hipStream_t st) {
+  const int chunks = dw->kpad / 128, groups = (chunks + 3) / 4;
+  const int64_t n = (int64_t)(dw->rpad / 16) * groups * 256;
+  WV_TRY(dw->blk_frag.alloc((size_t)n));
+  k_blk_frag<<<grid_for(n), kThreads, 0, st>>>(dw->blk.as<const uint8_t>(), dw->rpad, dw->nblk,
+                                               chunks, groups, dw->blk_frag.as<uint8_t>());
+  return hip_status(hipGetLastError(), "blk_frag");
+}
+
 }  // namespace
 
 Status quantize_to_device(const float* dW, int dtype, int scheme, int rows, int cols,
@@ -270,6 +293,7 @@ Status quantize_to_device(const float* dW, int dtype, int scheme, int rows, int 
     k_block_exp<<<grid_for((int64_t)dw->rpad * dw->nblk), kThreads, 0, st>>>(
         dW, rows, cols, dw->rpad, dw->nblk, maxrep, blk);
     WV_HIP(hipGetLastError());
+    WV_TRY(build_blk_frag(dw, st));
   }
   const float* sc = dw->row_scale.as<float>();
   if (dtype == kFP4) {
@@ -325,6 +349,7 @@ Status relayout_to_device(const uint8_t* d_raw, int dtype, int scheme, int rows,
       WV_HIP(hipMemcpy2DAsync(dw->blk.as<uint8_t>(), dw->nblk, d_blk_rows, src_nblk, src_nblk, rows,
                               hipMemcpyDeviceToDevice, st));
     }
+    WV_TRY(build_blk_frag(dw, st));
   }
   WV_HIP(hipStreamSynchronize(st));
   return Status::ok();
