@@ -87,6 +87,21 @@ def test_gemv_k_split_over_waves(gpu, oracle, dt, scheme, rows, cols):
     assert rel_l2(pre, o_pre) <= TOL_GEMV, (rows, cols)
 
 
+@pytest.mark.parametrize("dt,scheme,act", [(4, 2, -1), (16, 3, 1), (5, 1, 3)])
+def test_batched_wide_tiles(gpu, oracle, dt, scheme, act):
+    """A product large enough for the wide tiles (256 staged weight rows per
+    step, 256 workgroups): 1024 rows x 8192 outputs."""
+    rng = np.random.default_rng(dt + 7 * scheme)
+    rows, cols, batch = 8192, 200, 1024
+    W = rng.standard_normal((rows, cols)).astype(np.float32) / np.sqrt(cols)
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    bias = rng.standard_normal(rows) * 0.1
+    pre, post = run(gpu, dt, scheme, W, x, act=act, bias=bias)
+    o_pre, o_post = oracle_dense(oracle, dt, scheme, W, x, act=act, bias=bias)
+    assert rel_l2(pre, o_pre) <= TOL_MFMA
+    assert rel_l2(post, o_post) <= TOL_MFMA
+
+
 @pytest.mark.parametrize("dt,scheme", [(4, 2), (16, 3), (5, 0)])
 @pytest.mark.parametrize("rows,cols,batch", [
     (2176, 1000, 9),    # 2 row blocks per wave, grid past the 128-row padding

@@ -11,13 +11,15 @@ from test_gpu_dense import TOL_MFMA, oracle_dense, rel_l2
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("dt,scheme,batch,act,bias", [(4, 2, 40, -1, False), (16, 3, 130, 1, True),
-                                                      (5, 1, 8, 3, True)])
-def test_group_matches_members_and_oracle(gpu, oracle, dt, scheme, batch, act, bias):
+@pytest.mark.parametrize("dt,scheme,batch,act,bias,n,K,N", [
+    (4, 2, 40, -1, False, 5, 96, 160), (16, 3, 130, 1, True, 5, 96, 160),
+    (5, 1, 8, 3, True, 5, 96, 160),
+    (4, 2, 256, -1, False, 16, 128, 2048),   # wide tiles: 16 x 2 x 8 workgroups
+    (16, 3, 256, 2, True, 16, 128, 2048)])
+def test_group_matches_members_and_oracle(gpu, oracle, dt, scheme, batch, act, bias, n, K, N):
     import pywelvet as pw
     hip = pw.Hip()
     rng = np.random.default_rng(batch + dt)
-    n, K, N = 5, 96, 160
     Ws = [(rng.standard_normal((N, K)) / np.sqrt(K)).astype(np.float32) for _ in range(n)]
     bs = [rng.standard_normal(N) if bias else None for _ in range(n)]
     xs = [rng.standard_normal((batch, K)).astype(np.float32) for _ in range(n)]

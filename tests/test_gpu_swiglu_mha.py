@@ -33,7 +33,8 @@ def oracle_swiglu(oracle, dt, scheme, G, U, D, x):
 
 @pytest.mark.parametrize("dt,scheme", [(16, 3), (4, 2), (5, 1), (16, 0)])
 @pytest.mark.parametrize("batch,seq,d,inter", [(1, 1, 64, 160), (2, 3, 96, 200), (16, 1, 128, 352),
-                                               (40, 2, 96, 200)])
+                                               (40, 2, 96, 200),
+                                               (8, 128, 128, 4096)])  # gate+up on wide tiles
 def test_swiglu_matches_oracle(gpu, oracle, dt, scheme, batch, seq, d, inter):
     rng = np.random.default_rng(d + inter + dt + batch)
     G = (rng.standard_normal((inter, d)) / np.sqrt(d)).astype(np.float32)

@@ -196,6 +196,14 @@ constexpr int kBM = 128;
 // while the other waits on memory
 constexpr int kMxgWaves = 8;
 
+// Wide tiles (256 staged weight rows per step) move half the activation
+// bytes per MFMA; taken when they still give every CU a workgroup and N is a
+// multiple of their width (the weight rows and scales are padded to 128).
+bool mxg_wide(int members, int tiles_m, int N, int mats) {
+  const int bn = 256 / mats;
+  return N % bn == 0 && (long)members * tiles_m * (N / bn) >= 256;
+}
+
 // A grouped member's argument block, read field by field through the constant
 // address space: scalar loads into SGPRs (copying the struct as a whole
 // would go through a private-memory temporary).
@@ -230,12 +238,13 @@ __device__ __forceinline__ MxgArgs load_args(ConstArgs t) {
   return p;
 }
 
-template <int DT, bool BLK, int MATS, bool GROUP, int W>
+template <int DT, bool BLK, int MATS, bool GROUP, int W, int BR>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W / 4))) void k_mxg(
     MxgArgs p0, const MxgArgs* __restrict__ tab, int tiles_m, int tiles_n) {
   constexpr bool FP4 = DT == kFP4;
-  constexpr int BNM = MATS == 2 ? 64 : 128;  // weight rows per matrix per tile
-  constexpr int BR = MATS * BNM;             // staged weight rows
+  // BR staged weight rows per step (128, or 256 for wide tiles: twice the
+  // MFMAs per byte of activation terms moved), BNM per matrix
+  constexpr int BNM = BR / MATS;
   constexpr int WB = FP4 ? 64 : 128;         // code bytes per weight row per K step
   constexpr int SM = kBM / 16 / W;           // 16-row activation blocks per wave
   constexpr int SN = BR / 16;                // 16-row weight blocks
@@ -284,8 +293,10 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
     boff[k] = (uint32_t)((size_t)(n0 + row % BNM) * p.pitch + j * 16);
   }
   // weight block exponents: one dword (4 blocks) per staged row and step;
-  // waves of the same parity copy the same 64 rows (identical bytes)
-  const int erow = (wave & 1) * 64 + lane;
+  // waves w and w + BR / 64 copy the same 64 rows (identical bytes)
+  constexpr int EC = BR / 64;
+  static_assert(W % EC == 0, "exponent copies");
+  const int erow = (wave % EC) * 64 + lane;
   const uint8_t* bsrc =
       BLK ? (erow / BNM == 0 ? p.blk[0] : p.blk[MATS - 1]) + (size_t)(n0 + erow % BNM) * p.nblk
           : nullptr;
@@ -334,7 +345,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
       *WV_BDST(2, buf) = q2;                                   \
       *WV_BDST(3, buf) = q3;                                   \
     }                                                          \
-    if constexpr (BLK) ssb[buf][(wave & 1) * 64 + lane] = be;  \
+    if constexpr (BLK) ssb[buf][(wave % EC) * 64 + lane] = be; \
   } while (0)
 
   v4f acc[SM][SN];
@@ -371,25 +382,48 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
     for (int i = 0; i < 2; ++i) {
       const int s = s0 + i, cur = i;
       {
-        // weight fragments of this step first: a copy into LDS issued before
-        // them would make the compiler wait for it (it cannot tell the two
-        // buffers apart)
-        v8i bf[SN];
-        int bsc[SN];
+        // Weight fragments in groups of HB blocks (register budget; 4 for
+        // FP8 wide tiles, whose fragments take 8 registers): the first group
+        // before the next step's loads are issued, the others after the
+        // previous group's MFMAs.
+        constexpr int HB = SN < 8 ? SN : (SN == 16 && !FP4) ? 4 : 8;
+        v8i bf[HB];
+        int bsc[HB];
+        auto read_b = [&](int c0) {
 #pragma unroll
-        for (int c = 0; c < SN; ++c) {
-          const int row = c * 16 + i16;
-          int4 lo, hi = make_int4(0, 0, 0, 0);
-          if constexpr (FP4) {
-            lo = *reinterpret_cast<const int4*>(&sb[cur][row * 64 + ((g ^ ((row >> 2) & 3)) * 16)]);
-          } else {
-            const int sw = (row >> 1) & 7;
-            lo = *reinterpret_cast<const int4*>(&sb[cur][row * 128 + ((g ^ sw) * 16)]);
-            hi = *reinterpret_cast<const int4*>(&sb[cur][row * 128 + (((4 + g) ^ sw) * 16)]);
+          for (int c = 0; c < HB; ++c) {
+            const int row = (c0 + c) * 16 + i16;
+            int4 lo, hi = make_int4(0, 0, 0, 0);
+            if constexpr (FP4) {
+              lo = *reinterpret_cast<const int4*>(&sb[cur][row * 64 + ((g ^ ((row >> 2) & 3)) * 16)]);
+            } else {
+              const int sw = (row >> 1) & 7;
+              lo = *reinterpret_cast<const int4*>(&sb[cur][row * 128 + ((g ^ sw) * 16)]);
+              hi = *reinterpret_cast<const int4*>(&sb[cur][row * 128 + (((4 + g) ^ sw) * 16)]);
+            }
+            bf[c] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+            bsc[c] = (int)((ssb[cur][row] >> (8 * g)) & 0xFFu);
           }
-          bf[c] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-          bsc[c] = (int)((ssb[cur][row] >> (8 * g)) & 0xFFu);
-        }
+        };
+        auto mfma_half = [&](int c0) {
+          static_assert(kTerms == 3, "three activation terms");
+#pragma unroll
+          for (int a = 0; a < SM; ++a)
+#pragma unroll
+            for (int c = 0; c < HB; ++c)
+              acc[a][c0 + c] = mfma_term<DT, 0>(bf[c], fr[cur].x[0][a], acc[a][c0 + c], bsc[c], fr[cur].xs[a]);
+#pragma unroll
+          for (int a = 0; a < SM; ++a)
+#pragma unroll
+            for (int c = 0; c < HB; ++c)
+              acc[a][c0 + c] = mfma_term<DT, 1>(bf[c], fr[cur].x[1][a], acc[a][c0 + c], bsc[c], fr[cur].xs[a]);
+#pragma unroll
+          for (int a = 0; a < SM; ++a)
+#pragma unroll
+            for (int c = 0; c < HB; ++c)
+              acc[a][c0 + c] = mfma_term<DT, 2>(bf[c], fr[cur].x[2][a], acc[a][c0 + c], bsc[c], fr[cur].xs[a]);
+        };
+        read_b(0);
         __builtin_amdgcn_sched_barrier(0);
         // next step into the other buffer and set (their last readers
         // finished before the previous barrier); the last step fetches
@@ -402,22 +436,14 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
         // keep the copies ahead of the MFMAs and the wait + barrier behind
         // them (the MFMAs touch only registers)
         __builtin_amdgcn_sched_barrier(0);
-        static_assert(kTerms == 3, "three activation terms");
+        mfma_half(0);
 #pragma unroll
-        for (int a = 0; a < SM; ++a)
-#pragma unroll
-          for (int c = 0; c < SN; ++c)
-            acc[a][c] = mfma_term<DT, 0>(bf[c], fr[cur].x[0][a], acc[a][c], bsc[c], fr[cur].xs[a]);
-#pragma unroll
-        for (int a = 0; a < SM; ++a)
-#pragma unroll
-          for (int c = 0; c < SN; ++c)
-            acc[a][c] = mfma_term<DT, 1>(bf[c], fr[cur].x[1][a], acc[a][c], bsc[c], fr[cur].xs[a]);
-#pragma unroll
-        for (int a = 0; a < SM; ++a)
-#pragma unroll
-          for (int c = 0; c < SN; ++c)
-            acc[a][c] = mfma_term<DT, 2>(bf[c], fr[cur].x[2][a], acc[a][c], bsc[c], fr[cur].xs[a]);
+        for (int h = 1; h < SN / HB; ++h) {
+          __builtin_amdgcn_sched_barrier(0);
+          read_b(h * HB);
+          __builtin_amdgcn_sched_barrier(0);
+          mfma_half(h * HB);
+        }
         __builtin_amdgcn_sched_barrier(0);
         // weight tile of step s+1 into the other buffer (the compiler waits
         // for its loads only: the activation loads issued after them stay in
@@ -444,86 +470,92 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
   // Epilogue. A lane's accumulators hold activation row i16 of each 16-row
   // block and 4 consecutive output columns: stored as they are, every store
   // would write 64-byte pieces of 16 rows. Each wave instead stages its
-  // 32 x COLS result in LDS (its own region: no barrier) and writes whole
-  // rows, RPI rows of COLS floats per store instruction, with the bias and
-  // activation applied in that pass. The scale arrays are padded to the row
-  // padding, so the float4 scale loads stay in bounds.
-  constexpr int COLS = NC * 16;  // output columns of the tile
-  constexpr int LPR = COLS / 4;  // lanes per output row, a float4 each
-  constexpr int RPI = 64 / LPR;  // rows per store instruction
-  __shared__ __attribute__((aligned(16))) float stage[W][SM * 16][COLS + 4];
-#pragma unroll
-  for (int a = 0; a < SM; ++a)
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      const int nb = n0 + c * 16 + 4 * g;
-      float4 sc[MATS];
-#pragma unroll
-      for (int m = 0; m < MATS; ++m) sc[m] = *reinterpret_cast<const float4*>(p.scale[m] + nb);
-      float y[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float s0 = r == 0 ? sc[0].x : r == 1 ? sc[0].y : r == 2 ? sc[0].z : sc[0].w;
-        if constexpr (MATS == 2) {
-          const float s1 = r == 0 ? sc[1].x : r == 1 ? sc[1].y : r == 2 ? sc[1].z : sc[1].w;
-          const float gv = acc[a][c][r] * s0, uv = acc[a][c + NC][r] * s1;
-          const float gs = (float)act_f64(kSilu, (double)gv);
-          y[r] = (float)((double)gs * (double)uv);
-        } else {
-          y[r] = acc[a][c][r] * s0;
-        }
-      }
-      *reinterpret_cast<float4*>(&stage[wave][a * 16 + i16][c * 16 + 4 * g]) =
-          make_float4(y[0], y[1], y[2], y[3]);
-    }
+  // result in LDS, CH columns at a time (its own region: no barrier), and
+  // writes whole rows, RPI rows of CH floats per store instruction, with the
+  // bias and activation applied in that pass. The scale arrays are padded to
+  // the row padding, so the float4 scale loads stay in bounds.
+  constexpr int COLS = NC * 16;              // output columns of the tile
+  constexpr int CH = COLS < 128 ? COLS : 128;  // columns staged at a time
+  constexpr int LPR = CH / 4;                // lanes per output row, a float4 each
+  constexpr int RPI = 64 / LPR;              // rows per store instruction
+  __shared__ __attribute__((aligned(16))) float stage[W][SM * 16][CH + 4];
   const bool vec_out = (p.out_stride & 3) == 0 && ((reinterpret_cast<uintptr_t>(p.pre) & 15) == 0) &&
                        ((reinterpret_cast<uintptr_t>(p.post) & 15) == 0);
-  const int cl = 4 * (lane % LPR), n = n0 + cl;
+  const int cl = 4 * (lane % LPR);
   const int rbase = m0 + wave * SM * 16;
-  if (MATS == 2 || !p.need_epi) {
-    // post = pre here; a caller that passes one buffer for both gets it
-    // written once
-    float* post = MATS == 1 && p.post != p.pre ? p.post : nullptr;
 #pragma unroll
-    for (int rr = 0; rr < SM * 16 / RPI; ++rr) {
-      const int r = rr * RPI + lane / LPR;
-      const float4 y = *reinterpret_cast<const float4*>(&stage[wave][r][cl]);
-      if (rbase + r >= p.M || n >= p.N) continue;
-      const size_t oi = (size_t)(rbase + r) * p.out_stride + n;
-      if (vec_out && n + 3 < p.N) {
-        *reinterpret_cast<float4*>(p.pre + oi) = y;
-        if (post) *reinterpret_cast<float4*>(post + oi) = y;
-      } else {
-        const float yv[4] = {y.x, y.y, y.z, y.w};
+  for (int hc = 0; hc < COLS / CH; ++hc) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          if (n + i >= p.N) break;
-          p.pre[oi + i] = yv[i];
-          if (post) post[oi + i] = yv[i];
+    for (int a = 0; a < SM; ++a)
+#pragma unroll
+      for (int cc = 0; cc < CH / 16; ++cc) {
+        const int c = hc * (CH / 16) + cc;
+        const int nb = n0 + c * 16 + 4 * g;
+        float4 sc[MATS];
+#pragma unroll
+        for (int m = 0; m < MATS; ++m) sc[m] = *reinterpret_cast<const float4*>(p.scale[m] + nb);
+        float y[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float s0 = r == 0 ? sc[0].x : r == 1 ? sc[0].y : r == 2 ? sc[0].z : sc[0].w;
+          if constexpr (MATS == 2) {
+            const float s1 = r == 0 ? sc[1].x : r == 1 ? sc[1].y : r == 2 ? sc[1].z : sc[1].w;
+            const float gv = acc[a][c][r] * s0, uv = acc[a][c + NC][r] * s1;
+            const float gs = (float)act_f64(kSilu, (double)gv);
+            y[r] = (float)((double)gs * (double)uv);
+          } else {
+            y[r] = acc[a][c][r] * s0;
+          }
+        }
+        *reinterpret_cast<float4*>(&stage[wave][a * 16 + i16][cc * 16 + 4 * g]) =
+            make_float4(y[0], y[1], y[2], y[3]);
+      }
+    const int n = n0 + hc * CH + cl;
+    if (MATS == 2 || !p.need_epi) {
+      // post = pre here; a caller that passes one buffer for both gets it
+      // written once
+      float* post = MATS == 1 && p.post != p.pre ? p.post : nullptr;
+#pragma unroll
+      for (int rr = 0; rr < SM * 16 / RPI; ++rr) {
+        const int r = rr * RPI + lane / LPR;
+        const float4 y = *reinterpret_cast<const float4*>(&stage[wave][r][cl]);
+        if (rbase + r >= p.M || n >= p.N) continue;
+        const size_t oi = (size_t)(rbase + r) * p.out_stride + n;
+        if (vec_out && n + 3 < p.N) {
+          *reinterpret_cast<float4*>(p.pre + oi) = y;
+          if (post) *reinterpret_cast<float4*>(post + oi) = y;
+        } else {
+          const float yv[4] = {y.x, y.y, y.z, y.w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            if (n + i >= p.N) break;
+            p.pre[oi + i] = yv[i];
+            if (post) post[oi + i] = yv[i];
+          }
         }
       }
-    }
-  } else {
-    // Dense with bias or activation (reference rule: pre = f32(y + bias),
-    // post = act evaluated in f64 on y + bias); rolled, so the f64 activation
-    // code appears once
+    } else {
+      // Dense with bias or activation (reference rule: pre = f32(y + bias),
+      // post = act evaluated in f64 on y + bias); rolled, so the f64
+      // activation code appears once
 #pragma unroll 1
-    for (int rr = 0; rr < SM * 16 / RPI; ++rr) {
-      const int r = rr * RPI + lane / LPR;
-      const float4 y4 = *reinterpret_cast<const float4*>(&stage[wave][r][cl]);
-      if (rbase + r >= p.M || n >= p.N) continue;
-      const size_t oi = (size_t)(rbase + r) * p.out_stride + n;
-      const float yv[4] = {y4.x, y4.y, y4.z, y4.w};
+      for (int rr = 0; rr < SM * 16 / RPI; ++rr) {
+        const int r = rr * RPI + lane / LPR;
+        const float4 y4 = *reinterpret_cast<const float4*>(&stage[wave][r][cl]);
+        if (rbase + r >= p.M || n >= p.N) continue;
+        const size_t oi = (size_t)(rbase + r) * p.out_stride + n;
+        const float yv[4] = {y4.x, y4.y, y4.z, y4.w};
 #pragma unroll 1
-      for (int i = 0; i < 4 && n + i < p.N; ++i) {
-        float y = yv[i];
-        double v = (double)y;
-        if (p.bias && n + i < p.bias_len) {
-          v += p.bias[n + i];
-          y = (float)v;
+        for (int i = 0; i < 4 && n + i < p.N; ++i) {
+          float y = yv[i];
+          double v = (double)y;
+          if (p.bias && n + i < p.bias_len) {
+            v += p.bias[n + i];
+            y = (float)v;
+          }
+          p.pre[oi + i] = y;
+          p.post[oi + i] = (float)act_f64(p.act, v);
         }
-        p.pre[oi + i] = y;
-        p.post[oi + i] = (float)act_f64(p.act, v);
       }
     }
   }
@@ -864,13 +896,19 @@ Status launch_small(const MxgArgs& p, hipStream_t st) {
 template <int DT, bool BLK, int MATS>
 Status launch_t(const MxgArgs& p, int bm, hipStream_t st) {
   if (bm == kBM) {
-    constexpr int bn = MATS == 2 ? 64 : 128;
     if ((size_t)kTerms * p.mpad * p.kpad >= (1ull << 31) ||
-        (size_t)round_up(p.N, 128) * p.pitch >= (1ull << 31))
+        (size_t)round_up(p.N, 256) * p.pitch >= (1ull << 31))
       return Status::err(kUnsupported, "mxg: operands above 2 GiB");
-    const int tiles_m = p.mpad / kBM, tiles_n = (p.N + bn - 1) / bn;
-    k_mxg<DT, BLK, MATS, false, kMxgWaves><<<(unsigned)(tiles_m * tiles_n), 64 * kMxgWaves, 0, st>>>(
-        p, nullptr, tiles_m, tiles_n);
+    const int tiles_m = p.mpad / kBM;
+    if (mxg_wide(1, tiles_m, p.N, MATS)) {
+      const int tiles_n = (p.N + 256 / MATS - 1) / (256 / MATS);
+      k_mxg<DT, BLK, MATS, false, kMxgWaves, 256><<<(unsigned)(tiles_m * tiles_n), 64 * kMxgWaves, 0, st>>>(
+          p, nullptr, tiles_m, tiles_n);
+    } else {
+      const int tiles_n = (p.N + 128 / MATS - 1) / (128 / MATS);
+      k_mxg<DT, BLK, MATS, false, kMxgWaves, 128><<<(unsigned)(tiles_m * tiles_n), 64 * kMxgWaves, 0, st>>>(
+          p, nullptr, tiles_m, tiles_n);
+    }
   } else {
     return p.mpad <= 16 ? launch_small<DT, BLK, MATS, 1>(p, st) : launch_small<DT, BLK, MATS, 2>(p, st);
   }
@@ -931,10 +969,16 @@ Status launch_split_group(const SplitJob* jobs, int n, bool vec, int x_stride, i
 
 template <int DT, bool BLK, int MATS>
 Status launch_group_t(const MxgArgs* tab, const MxgArgs& p, int n, hipStream_t st) {
-  constexpr int bn = MATS == 2 ? 64 : 128;
-  const int tiles_m = p.mpad / kBM, tiles_n = (p.N + bn - 1) / bn;
-  k_mxg<DT, BLK, MATS, true, kMxgWaves><<<(unsigned)(n * tiles_m * tiles_n), 64 * kMxgWaves, 0, st>>>(
-      p, tab, tiles_m, tiles_n);
+  const int tiles_m = p.mpad / kBM;
+  if (mxg_wide(n, tiles_m, p.N, MATS)) {
+    const int tiles_n = (p.N + 256 / MATS - 1) / (256 / MATS);
+    k_mxg<DT, BLK, MATS, true, kMxgWaves, 256><<<(unsigned)(n * tiles_m * tiles_n), 64 * kMxgWaves, 0, st>>>(
+        p, tab, tiles_m, tiles_n);
+  } else {
+    const int tiles_n = (p.N + 128 / MATS - 1) / (128 / MATS);
+    k_mxg<DT, BLK, MATS, true, kMxgWaves, 128><<<(unsigned)(n * tiles_m * tiles_n), 64 * kMxgWaves, 0, st>>>(
+        p, tab, tiles_m, tiles_n);
+  }
   return hip_status(hipGetLastError(), "mxg group launch");
 }
 
@@ -944,7 +988,7 @@ Status launch_mxg_group(const MxgArgs* tab, const MxgArgs& p, int n, int dtype, 
   if (mxg_block_m(p.M) != kBM || p.mpad % kBM != 0 || p.kpad % 256 != 0)
     return Status::err(kInvalid, "mxg group: needs the large-tile layout");
   if ((size_t)kTerms * p.mpad * p.kpad >= (1ull << 31) ||
-      (size_t)round_up(p.N, 128) * p.pitch >= (1ull << 31))
+      (size_t)round_up(p.N, 256) * p.pitch >= (1ull << 31))
     return Status::err(kUnsupported, "mxg: operands above 2 GiB");
   const bool two = p.mats == 2;
   switch (dtype) {
