@@ -245,15 +245,17 @@ def cells_workload(pw, hip, name):
         bufs.append([hip.upload(x)] + [hip.malloc(batch * d * 4) for _ in kinds])
     flops = cells * len(kinds) * 2 * batch * d * d
     # the 64 cells are independent: layer li of every cell runs as one group
-    # (one split launch and one matrix-core launch per layer position)
+    # (one matrix-core launch per layer position); the groups form a chain,
+    # so each layer's epilogue also writes the next layer's activation split
+    # and only the first layer runs the split kernel
     groups = [pw.DenseGroup([sessions[c][li] for c in range(cells)],
                             [bufs[c][li] for c in range(cells)],
                             [bufs[c][li + 1] for c in range(cells)],
                             [bufs[c][li + 1] for c in range(cells)]) for li in range(len(kinds))]
+    chain = pw.DenseChain(groups)
 
     def enqueue(i, stream):
-        for grp in groups:
-            grp.execute(stream)
+        chain.execute(stream)
 
     def cpu(budget_s):
         orc = oracle()
@@ -273,6 +275,7 @@ def cells_workload(pw, hip, name):
                            f"{cpu_threads()} threads), scaled x{cells} to the 64 cells")}
 
     def close():
+        chain.close()
         for grp in groups:
             grp.close()
         for row in sessions:
@@ -286,7 +289,8 @@ def cells_workload(pw, hip, name):
             "bound": "mfma", "dtype": "fp8e4m3+fp4e2m1",
             "config": {"workload": name, "cells": cells, "layers_per_cell": 3, "batch": batch,
                        "width": d, "layer_kinds": "E4M3 per-row, FP4 E8M0/32, E4M3 per-row",
-                       "execution": "independent cells, one grouped launch per layer position"},
+                       "execution": ("independent cells, one grouped launch per layer position, "
+                                     "chained: each epilogue writes the next layer's split")},
             "cpu": cpu, "close": close}
 
 

@@ -143,6 +143,21 @@ WELVET_API welvet_status welvet_dense_group_mount(welvet_dense_session* const* s
 WELVET_API welvet_status welvet_dense_group_execute(welvet_dense_group* g, void* stream);
 WELVET_API void welvet_dense_group_release(welvet_dense_group* g);
 
+/* Chained groups (no counterpart in the reference; for the layers of a
+ * volume's cells, the serial Stack of each cell run for all cells at once):
+ * groups[k + 1] reads what groups[k] writes, i.e. for every member i,
+ * x[i] of group k + 1 is post[i] of group k (or its pre when that group's
+ * activation is Linear without bias). execute runs the groups in order on
+ * `stream` (NULL = the chain's stream) with the same outputs as executing
+ * them one by one. Above 32 rows, where a group's out is a multiple of 256
+ * its matrix-core epilogue also writes the next group's activation split, so
+ * that group skips its split launch. The groups must outlive the chain. */
+typedef struct welvet_dense_chain welvet_dense_chain;
+WELVET_API welvet_status welvet_dense_chain_mount(welvet_dense_group* const* groups, int32_t n,
+                                                  welvet_dense_chain** out);
+WELVET_API welvet_status welvet_dense_chain_execute(welvet_dense_chain* c, void* stream);
+WELVET_API void welvet_dense_chain_release(welvet_dense_chain* c);
+
 /* SwiGLU / MHA sessions: mount once, execute many (host or device buffers). */
 typedef struct welvet_swiglu_session welvet_swiglu_session;
 WELVET_API welvet_status welvet_swiglu_mount(int32_t batch, int32_t seq, int32_t input_dim,

@@ -58,3 +58,101 @@ def test_group_rejects_mixed_shapes(gpu):
         hip.free(p)
     a.close()
     b.close()
+
+
+def _chain_setup(hip, pw, rng, batch, n, widths, layers):
+    """n cells, each a Stack of Dense layers widths[k] -> widths[k + 1];
+    layers[k] = (dtype, scheme, act, bias). Linear layers without bias get one
+    buffer for pre and post (as a volume keeps it); the others two."""
+    Ws, bs, sessions, bufs, groups = [], [], [], [], []
+    x0 = [hip.malloc(batch * widths[0] * 4) for _ in range(n)]
+    cur = x0
+    for k, (dt, sc, act, bias) in enumerate(layers):
+        K, N = widths[k], widths[k + 1]
+        Wk = [(rng.standard_normal((N, K)) / np.sqrt(K)).astype(np.float32) for _ in range(n)]
+        bk = [rng.standard_normal(N) if bias else None for _ in range(n)]
+        sk = [pw.DenseSession(batch, K, N, act, dt, sc, W, b) for W, b in zip(Wk, bk)]
+        pre = [hip.malloc(batch * N * 4) for _ in range(n)]
+        post = pre if (act == -1 and not bias) else [hip.malloc(batch * N * 4) for _ in range(n)]
+        groups.append(pw.DenseGroup(sk, cur, pre, post))
+        Ws.append(Wk), bs.append(bk), sessions.append(sk), bufs.append((pre, post))
+        cur = post
+    return Ws, bs, sessions, x0, bufs, groups
+
+
+@pytest.mark.parametrize("batch,n,widths,layers", [
+    # volume cells: E4M3 per-row -> FP4 E8M0/32 -> E4M3 per-row (wide tiles)
+    (256, 16, [1024, 1024, 1024, 1024], [(4, 2, -1, False), (16, 3, -1, False), (4, 2, -1, False)]),
+    # ragged rows (200 of 256 padded), an activation + bias producer, 128-wide tiles
+    (200, 3, [256, 512, 256, 384], [(5, 1, -1, False), (4, 3, 1, True), (16, 3, 2, True)]),
+    # a link whose width is not a multiple of 256 runs its own split
+    (130, 2, [128, 384, 256, 128], [(4, 2, 0, False), (16, 3, -1, False), (4, 2, -1, True)]),
+    # 16 rows: the groups run member by member
+    (16, 3, [256, 256, 256], [(4, 2, -1, False), (16, 3, 3, True)]),
+])
+def test_chain_matches_groups(gpu, oracle, batch, n, widths, layers):
+    import pywelvet as pw
+    hip = pw.Hip()
+    rng = np.random.default_rng(batch * 7 + n)
+    Ws, bs, sessions, x0, bufs, groups = _chain_setup(hip, pw, rng, batch, n, widths, layers)
+    chain = pw.DenseChain(groups)
+    xa = [rng.standard_normal((batch, widths[0])).astype(np.float32) for _ in range(n)]
+    xb = [rng.standard_normal((batch, widths[0])).astype(np.float32) for _ in range(n)]
+    # a first input, then a second: a consumer that skipped reading its own
+    # split would still hold the first input's terms
+    for i in range(n):
+        hip.copy_in(x0[i], xa[i])
+    chain.execute()
+    hip.sync()
+    for i in range(n):
+        hip.copy_in(x0[i], xb[i])
+    chain.execute()
+    hip.sync()
+    L = len(layers)
+    got = [[(hip.download(bufs[k][0][i], (batch, widths[k + 1])),
+             hip.download(bufs[k][1][i], (batch, widths[k + 1]))) for i in range(n)] for k in range(L)]
+    for g in groups:  # the same layers one group at a time
+        g.execute()
+    hip.sync()
+    for k in range(L):
+        for i in range(n):
+            pre = hip.download(bufs[k][0][i], (batch, widths[k + 1]))
+            post = hip.download(bufs[k][1][i], (batch, widths[k + 1]))
+            assert np.array_equal(got[k][i][0], pre) and np.array_equal(got[k][i][1], post), (k, i)
+            # each layer against the oracle on the GPU's own input to it
+            xin = xb[i] if k == 0 else hip.download(bufs[k - 1][1][i], (batch, widths[k]))
+            dt, sc, act, _ = layers[k]
+            o_pre, o_post = oracle_dense(oracle, dt, sc, Ws[k][i], xin, act, bs[k][i])
+            tol = TOL_MFMA if batch > 4 else 1e-5
+            assert rel_l2(pre, o_pre) <= tol and rel_l2(post, o_post) <= tol, (k, i)
+    chain.close()
+    for g in groups:
+        g.close()
+    seen = set()
+    for p in x0 + [q for pre, post in bufs for q in pre + post]:
+        if p not in seen:
+            seen.add(p)
+            hip.free(p)
+    for sk in sessions:
+        for s in sk:
+            s.close()
+
+
+def test_chain_rejects_unlinked_groups(gpu):
+    import pywelvet as pw
+    hip = pw.Hip()
+    W = np.ones((256, 256), np.float32) / 256
+    a = pw.DenseSession(64, 256, 256, -1, 4, 2, W)
+    b = pw.DenseSession(64, 256, 256, -1, 4, 2, W)
+    bufs = [hip.malloc(64 * 256 * 4) for _ in range(3)]
+    g1 = pw.DenseGroup([a], [bufs[0]], [bufs[1]], [bufs[1]])
+    g2 = pw.DenseGroup([b], [bufs[0]], [bufs[2]], [bufs[2]])  # reads x, not g1's output
+    with pytest.raises(pw.WelvetError) as e:
+        pw.DenseChain([g1, g2])
+    assert e.value.code == 1
+    for g in (g1, g2):
+        g.close()
+    for p in bufs:
+        hip.free(p)
+    a.close()
+    b.close()

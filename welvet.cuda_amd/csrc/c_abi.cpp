@@ -226,6 +226,65 @@ welvet_status welvet_dense_group_execute(welvet_dense_group* g, void* stream) {
 
 void welvet_dense_group_release(welvet_dense_group* g) { delete g; }
 
+// ---- chained groups (extension) ----
+struct welvet_dense_chain {
+  wv::Stream stream;
+  std::vector<welvet_dense_group*> groups;
+  bool fused = false;
+  wv::DenseChain c;
+};
+
+welvet_status welvet_dense_chain_mount(welvet_dense_group* const* groups, int32_t n,
+                                       welvet_dense_chain** out) {
+  if (!out) return invalid("null chain out");
+  *out = nullptr;
+  if (n <= 0 || !groups) return invalid("chain: null or empty arguments");
+  return guarded([&]() -> Status {
+    auto ch = std::make_unique<welvet_dense_chain>();
+    bool fused = true;
+    for (int k = 0; k < n; ++k) {
+      welvet_dense_group* g = groups[k];
+      if (!g) return wv::Status::err(wv::kInvalid, "chain: null group");
+      if (k > 0) {
+        const welvet_dense_group* p = groups[k - 1];
+        if (g->members.size() != p->members.size() ||
+            g->members[0]->batch != p->members[0]->batch)
+          return wv::Status::err(wv::kInvalid, "chain: groups differ in members or batch");
+        for (size_t i = 0; i < g->members.size(); ++i)
+          if (g->members[i]->layer.in != p->members[i]->layer.out ||
+              (g->x[i] != p->post[i] && g->x[i] != p->pre[i]) ||
+              (g->x[i] == p->pre[i] && g->x[i] != p->post[i] && p->members[i]->layer.need_epi()))
+            return wv::Status::err(wv::kInvalid,
+                                   "chain: member input is not the previous member's output");
+      }
+      fused = fused && g->fused;
+      ch->groups.push_back(g);
+    }
+    WV_TRY(ch->stream.create());
+    ch->fused = fused;
+    if (fused) {
+      std::vector<const wv::DenseGroup*> gs;
+      for (auto* g : ch->groups) gs.push_back(&g->g);
+      WV_TRY(wv::dense_chain_build(gs.data(), n, &ch->c));
+    }
+    *out = ch.release();
+    return Status::ok();
+  });
+}
+
+welvet_status welvet_dense_chain_execute(welvet_dense_chain* c, void* stream) {
+  if (!c) return invalid("null chain");
+  hipStream_t st = pick(stream, c->stream.s);
+  if (c->fused) return guarded([&]() -> Status { return wv::dense_chain_forward(c->c, st); });
+  for (auto* g : c->groups) {
+    welvet_status r = welvet_dense_group_execute(g, st);
+    if (r.code != 0) return r;
+  }
+  return to_c(Status::ok());
+}
+
+void welvet_dense_chain_release(welvet_dense_chain* c) { delete c; }
+
 welvet_status welvet_dense_export_store(welvet_dense_session* s, uint8_t* native,
                                         size_t native_cap, size_t* native_len, float* row_scale,
                                         uint8_t* blk_exp, float* tensor_scale) {

@@ -93,6 +93,10 @@ struct MxgArgs {
   float* part = nullptr;
   // block exponents in lane order (DeviceWeights::blk_frag), BLOCK32 only
   const uint8_t* blkf[2] = {nullptr, nullptr};
+  // large tiles, one matrix, N a multiple of 256: when set, the epilogue also
+  // writes the split of post here, laid out as the split buffer of a layer
+  // with the same rows (mpad) and kpad = N (the next layer of a chain)
+  uint8_t* next = nullptr;
 };
 int mxg_block_m(int M);
 // Bytes of the K-split partial buffer the product of M rows with N outputs

@@ -278,6 +278,8 @@ Status dense_group_build(const DenseLayer* const* layers, int n, int batch,
   WV_TRY(g->tab.alloc(sizeof(MxgArgs) * n));
   WV_HIP(hipMemcpy(g->jobs.p, jobs.data(), sizeof(SplitJob) * n, hipMemcpyHostToDevice));
   WV_HIP(hipMemcpy(g->tab.p, tab.data(), sizeof(MxgArgs) * n, hipMemcpyHostToDevice));
+  g->hjobs = jobs;
+  g->htab = tab;
   g->n = n;
   g->batch = batch;
   g->dtype = L0.dev.dtype;
@@ -293,6 +295,51 @@ Status dense_group_forward(const DenseGroup& g, hipStream_t st) {
   WV_TRY(launch_split_group(g.jobs.as<const SplitJob>(), g.n, g.vec, g.in, g.batch, g.in, g.kpad,
                             st));
   return launch_mxg_group(g.tab.as<const MxgArgs>(), g.shape, g.n, g.dtype, g.blk, st);
+}
+
+Status dense_chain_build(const DenseGroup* const* groups, int count, DenseChain* c) {
+  if (count <= 0 || !groups || !c) return Status::err(kInvalid, "dense chain: bad args");
+  for (int k = 0; k < count; ++k)
+    if (!groups[k] || groups[k]->n <= 0) return Status::err(kInvalid, "dense chain: null group");
+  c->groups.assign(groups, groups + count);
+  c->tabs.clear();
+  c->tabs.resize(count);
+  c->fused.assign(count, 0);
+  for (int k = 0; k + 1 < count; ++k) {
+    const DenseGroup& P = *groups[k];
+    const DenseGroup& C = *groups[k + 1];
+    if (P.n != C.n || P.batch != C.batch)
+      return Status::err(kInvalid, "dense chain: groups differ in members or batch");
+    if (P.shape.N != C.in)
+      return Status::err(kInvalid, "dense chain: out differs from the next group's in");
+    for (int i = 0; i < P.n; ++i) {
+      const MxgArgs& a = P.htab[i];
+      const bool linked = C.hjobs[i].x == (a.post ? a.post : a.pre) ||
+                          (!a.need_epi && C.hjobs[i].x == a.pre);
+      if (!linked)
+        return Status::err(kInvalid, "dense chain: member input is not the previous member's output");
+    }
+    if (P.shape.N % 256 != 0 || C.kpad != P.shape.N || P.shape.mats != 1) continue;
+    std::vector<MxgArgs> tab = P.htab;
+    for (int i = 0; i < P.n; ++i) tab[i].next = C.hjobs[i].buf;
+    WV_TRY(c->tabs[k].alloc(sizeof(MxgArgs) * P.n));
+    WV_HIP(hipMemcpy(c->tabs[k].p, tab.data(), sizeof(MxgArgs) * P.n, hipMemcpyHostToDevice));
+    c->fused[k] = 1;
+  }
+  return Status::ok();
+}
+
+Status dense_chain_forward(const DenseChain& c, hipStream_t st) {
+  if (c.groups.empty()) return Status::err(kInvalid, "dense chain: empty");
+  for (size_t k = 0; k < c.groups.size(); ++k) {
+    const DenseGroup& g = *c.groups[k];
+    if (k == 0 || !c.fused[k - 1])
+      WV_TRY(launch_split_group(g.jobs.as<const SplitJob>(), g.n, g.vec, g.in, g.batch, g.in,
+                                g.kpad, st));
+    const MxgArgs* tab = c.fused[k] ? c.tabs[k].as<const MxgArgs>() : g.tab.as<const MxgArgs>();
+    WV_TRY(launch_mxg_group(tab, g.shape, g.n, g.dtype, g.blk, st));
+  }
+  return Status::ok();
 }
 
 // ---------------------------------------------------------------------------

@@ -85,12 +85,27 @@ struct DenseGroup {
   DevBuf split;  // n slices of split_bytes(batch, kpad)
   DevBuf jobs;   // SplitJob[n]
   DevBuf tab;    // MxgArgs[n]
+  std::vector<SplitJob> hjobs;  // host copies of jobs and tab
+  std::vector<MxgArgs> htab;
 };
 bool dense_group_fused(int batch);
 Status dense_group_build(const DenseLayer* const* layers, int n, int batch,
                          const float* const* x, float* const* pre, float* const* post,
                          DenseGroup* g);
 Status dense_group_forward(const DenseGroup& g, hipStream_t st);
+
+// Groups run in order where group k + 1 reads what group k writes (member i's
+// x is member i's post, or its pre when the two are one buffer): the layers
+// of a volume's cells. Where group k's out is a multiple of 256 (then the
+// consumer's kpad equals it), group k's GEMM epilogue writes group k + 1's
+// split buffer as well and group k + 1 runs no split kernel.
+struct DenseChain {
+  std::vector<const DenseGroup*> groups;
+  std::vector<DevBuf> tabs;  // per link k -> k + 1: group k's MxgArgs[n] with `next` set
+  std::vector<char> fused;   // per link: the epilogue writes the next split
+};
+Status dense_chain_build(const DenseGroup* const* groups, int count, DenseChain* c);
+Status dense_chain_forward(const DenseChain& c, hipStream_t st);
 
 struct SwiGLULayer {
   int in = 0, inter = 0;

@@ -74,15 +74,58 @@ constexpr int waitcnt_imm(int vm, int lgkm) {
   return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | ((lgkm & 15) << 8);
 }
 
+// The terms of one (16-row block, 128-wide K chunk) operand slice: lane l
+// (row l % 16, group g = l / 16) holds its 32 values v[h][j], k = 64h + 16g +
+// j. A 32-element block is held by lanes l and l ^ 16, which exchange their
+// amax. Per term and half the lane stores its 16 codes with one 16-byte
+// store at chunk + t * kFragBytes + h * 1024 + 16 l; the block exponents are
+// gathered to the lanes that pass them to the instruction (row l % 16, block
+// l / 16) and stored as one dword per lane at scales + 4 l (byte t: term t).
+__device__ __forceinline__ void split_terms(float (&v)[2][16], uint8_t* __restrict__ chunk,
+                                            uint8_t* __restrict__ scales, int lane) {
+  uint8_t* dst = chunk + lane * 16;
+  const int i16 = lane & 15;
+  // exponent of block b = l / 16 for row i16 comes from lane 32 (b & 1) + i16,
+  // half b >> 1
+  const int src = ((lane >> 4) & 1) * 32 + i16;
+  uint32_t sword = 0x7F000000u;  // byte 3 unused
+#pragma unroll
+  for (int t = 0; t < kTerms; ++t) {
+    int e[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      float am = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) am = fmaxf(am, fabsf(v[h][j]));
+      am = fmaxf(am, __shfl_xor(am, 16, 64));
+      e[h] = e8m0_exponent(am, 448.0f);
+      const float inv = pow2f(-e[h]), sc = pow2f(e[h]);
+      int wq[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        int w4 = __builtin_amdgcn_cvt_pk_fp8_f32(v[h][4 * q] * inv, v[h][4 * q + 1] * inv, 0, false);
+        w4 = __builtin_amdgcn_cvt_pk_fp8_f32(v[h][4 * q + 2] * inv, v[h][4 * q + 3] * inv, w4, true);
+        wq[q] = w4;
+        if (t + 1 < kTerms) {
+          const v2f q0 = __builtin_amdgcn_cvt_pk_f32_fp8(w4, false);
+          const v2f q1 = __builtin_amdgcn_cvt_pk_f32_fp8(w4, true);
+          v[h][4 * q] -= q0.x * sc, v[h][4 * q + 1] -= q0.y * sc;
+          v[h][4 * q + 2] -= q1.x * sc, v[h][4 * q + 3] -= q1.y * sc;
+        }
+      }
+      *reinterpret_cast<int4*>(dst + t * kFragBytes + h * 1024) = make_int4(wq[0], wq[1], wq[2], wq[3]);
+    }
+    const int e0 = __shfl(e[0], src, 64), e1 = __shfl(e[1], src, 64);
+    sword |= (uint32_t)(((lane >> 5) ? e1 : e0) + 127) << (8 * t);
+  }
+  *reinterpret_cast<uint32_t*>(scales + lane * 4) = sword;
+}
+
 // The activation split, written in operand order. One wave per (16-row block
 // rb, 128-wide K chunk kc): the 16 x 128 fp32 slice is staged in LDS with
 // row-contiguous loads; then lane l (row i16 = l % 16, group g = l / 16)
-// takes the 32 values of its operand, k = 64h + 16g + j (h = 0, 1; j < 16).
-// A 32-element block is held by lanes l and l ^ 16, which exchange their
-// amax. Per term and half the lane stores its 16 codes with one 16-byte
-// store; the block exponents are gathered to the lanes that pass them to the
-// instruction (row l % 16, block l / 16) and stored as one dword per lane
-// (byte t: term t). Rows >= M and columns >= cols give zero codes.
+// takes the 32 values of its operand, k = 64h + 16g + j (h = 0, 1; j < 16),
+// and split_terms writes them. Rows >= M and columns >= cols give zero codes.
 template <bool VEC>
 __global__ __launch_bounds__(kThreads) void k_split(const float* __restrict__ x, int x_stride,
                                                     int M, int cols, int mpad, int kpad,
@@ -134,41 +177,8 @@ __global__ __launch_bounds__(kThreads) void k_split(const float* __restrict__ x,
       v[h][4 * q] = t.x, v[h][4 * q + 1] = t.y, v[h][4 * q + 2] = t.z, v[h][4 * q + 3] = t.w;
     }
 
-  uint8_t* dst = a + (size_t)(rb * KC + kc) * kChunkBytes + lane * 16;
-  // exponent of block b = l / 16 for row i16 comes from lane 32 (b & 1) + i16,
-  // half b >> 1
-  const int src = ((lane >> 4) & 1) * 32 + i16;
-  uint32_t sword = 0x7F000000u;  // byte 3 unused
-#pragma unroll
-  for (int t = 0; t < kTerms; ++t) {
-    int e[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      float am = 0.0f;
-#pragma unroll
-      for (int j = 0; j < 16; ++j) am = fmaxf(am, fabsf(v[h][j]));
-      am = fmaxf(am, __shfl_xor(am, 16, 64));
-      e[h] = e8m0_exponent(am, 448.0f);
-      const float inv = pow2f(-e[h]), sc = pow2f(e[h]);
-      int wq[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        int w4 = __builtin_amdgcn_cvt_pk_fp8_f32(v[h][4 * q] * inv, v[h][4 * q + 1] * inv, 0, false);
-        w4 = __builtin_amdgcn_cvt_pk_fp8_f32(v[h][4 * q + 2] * inv, v[h][4 * q + 3] * inv, w4, true);
-        wq[q] = w4;
-        if (t + 1 < kTerms) {
-          const v2f q0 = __builtin_amdgcn_cvt_pk_f32_fp8(w4, false);
-          const v2f q1 = __builtin_amdgcn_cvt_pk_f32_fp8(w4, true);
-          v[h][4 * q] -= q0.x * sc, v[h][4 * q + 1] -= q0.y * sc;
-          v[h][4 * q + 2] -= q1.x * sc, v[h][4 * q + 3] -= q1.y * sc;
-        }
-      }
-      *reinterpret_cast<int4*>(dst + t * kFragBytes + h * 1024) = make_int4(wq[0], wq[1], wq[2], wq[3]);
-    }
-    const int e0 = __shfl(e[0], src, 64), e1 = __shfl(e[1], src, 64);
-    sword |= (uint32_t)(((lane >> 5) ? e1 : e0) + 127) << (8 * t);
-  }
-  *reinterpret_cast<uint32_t*>(as + (size_t)(rb * KC + kc) * kChunkScaleBytes + lane * 4) = sword;
+  split_terms(v, a + (size_t)(rb * KC + kc) * kChunkBytes,
+              as + (size_t)(rb * KC + kc) * kChunkScaleBytes, lane);
 }
 
 // Large-M tile (M > 32): 128 activation rows x 128 staged weight rows (64 per
@@ -235,6 +245,7 @@ __device__ __forceinline__ MxgArgs load_args(ConstArgs t) {
   p.part = t->part;
   p.blkf[0] = t->blkf[0];
   p.blkf[1] = t->blkf[1];
+  p.next = t->next;
   return p;
 }
 
@@ -544,7 +555,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
         const float4 y4 = *reinterpret_cast<const float4*>(&stage[wave][r][cl]);
         if (rbase + r >= p.M || n >= p.N) continue;
         const size_t oi = (size_t)(rbase + r) * p.out_stride + n;
-        const float yv[4] = {y4.x, y4.y, y4.z, y4.w};
+        float yv[4] = {y4.x, y4.y, y4.z, y4.w};
 #pragma unroll 1
         for (int i = 0; i < 4 && n + i < p.N; ++i) {
           float y = yv[i];
@@ -554,8 +565,40 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
             y = (float)v;
           }
           p.pre[oi + i] = y;
-          p.post[oi + i] = (float)act_f64(p.act, v);
+          yv[i] = (float)act_f64(p.act, v);
+          p.post[oi + i] = yv[i];
         }
+        // post stays in the stage for the split below (same lane, same place)
+        *reinterpret_cast<float4*>(&stage[wave][r][cl]) = make_float4(yv[0], yv[1], yv[2], yv[3]);
+      }
+    }
+    if constexpr (MATS == 1 && CH == 128) {
+      // Chained layer: the next layer's split of post, written from the
+      // stage (the same terms k_split would make from post in memory). The
+      // next layer has the same rows (mpad) and kpad = N. Rows >= M get zero
+      // codes; the stage reads follow this wave's own stage writes in program
+      // order.
+      if (p.next && n0 + hc * CH < p.N) {
+        __builtin_amdgcn_wave_barrier();
+        const int kcn = p.N / 128, kc = (n0 + hc * CH) / 128;
+        uint8_t* nscale = p.next + (size_t)kTerms * p.mpad * p.N;
+#pragma unroll
+        for (int a = 0; a < SM; ++a) {
+          const int rb = rbase / 16 + a;
+          const bool live = rb * 16 + i16 < p.M;
+          float v[2][16];
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const float4 t = *reinterpret_cast<const float4*>(&stage[wave][a * 16 + i16][64 * h + 16 * g + 4 * q]);
+              v[h][4 * q] = live ? t.x : 0.0f, v[h][4 * q + 1] = live ? t.y : 0.0f;
+              v[h][4 * q + 2] = live ? t.z : 0.0f, v[h][4 * q + 3] = live ? t.w : 0.0f;
+            }
+          split_terms(v, p.next + (size_t)(rb * kcn + kc) * kChunkBytes,
+                      nscale + (size_t)(rb * kcn + kc) * kChunkScaleBytes, lane);
+        }
+        __builtin_amdgcn_wave_barrier();
       }
     }
   }

@@ -100,6 +100,9 @@ def lib():
           ctypes.POINTER(_vp), ctypes.POINTER(_vp)])
     _sig(L, "welvet_dense_group_execute", Status, [_vp, _vp])
     _sig(L, "welvet_dense_group_release", None, [_vp])
+    _sig(L, "welvet_dense_chain_mount", Status, [_vp, ctypes.c_int32, _vp])
+    _sig(L, "welvet_dense_chain_execute", Status, [_vp, _vp])
+    _sig(L, "welvet_dense_chain_release", None, [_vp])
     _sig(L, "welvet_swiglu_forward_f32", Status,
          [_i32, _i32, _i32, _i32, _i32, _i32, _fp, _fp, _fp, _fp, _fp, _fp])
     _sig(L, "welvet_swiglu_mount", Status,
@@ -224,6 +227,12 @@ class Hip:
         self._ok(self.h.hipMemcpy(_vp(p), arr.ctypes.data_as(_vp), arr.nbytes, self.H2D), "H2D")
         return p
 
+    def copy_in(self, p, arr):
+        """Host array into an existing device buffer; returns once it has landed."""
+        arr = np.ascontiguousarray(arr)
+        self._ok(self.h.hipMemcpy(_vp(p), arr.ctypes.data_as(_vp), arr.nbytes, self.H2D), "H2D")
+        self.sync()
+
     def download(self, p, shape, dtype=np.float32):
         out = np.empty(shape, dtype=dtype)
         self._ok(self.h.hipMemcpy(out.ctypes.data_as(_vp), _vp(p), out.nbytes, self.D2H), "D2H")
@@ -284,6 +293,31 @@ class Hip:
 
 
 # --------------------------------------------------------------------------
+class DenseChain:
+    """Groups run in order, each reading the previous group's outputs."""
+
+    def __init__(self, groups):
+        n = len(groups)
+        self._groups = list(groups)  # the groups must outlive the chain
+        h = _vp()
+        check(lib().welvet_dense_chain_mount((_vp * n)(*[g.h for g in groups]), n, ctypes.byref(h)))
+        self.h = h
+
+    def execute(self, stream=None):
+        check(lib().welvet_dense_chain_execute(self.h, _vp(stream) if stream else None))
+
+    def close(self):
+        if self.h:
+            lib().welvet_dense_chain_release(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class DenseGroup:
     """Grouped execution of same-shape Dense sessions over fixed device buffers."""
 
