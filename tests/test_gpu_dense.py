@@ -64,7 +64,8 @@ def test_release_smoke_known_answer(gpu):
 ])
 def test_integer_exact_bit_for_bit(gpu, oracle, dt, values):
     rng = np.random.default_rng(dt)
-    for rows, cols, batch in [(129, 1000, 1), (64, 4096, 1), (5, 77, 3), (9, 300, 9), (24, 9300, 1)]:
+    for rows, cols, batch in [(129, 1000, 1), (64, 4096, 1), (5, 77, 3), (9, 300, 9), (24, 9300, 1),
+                              (40, 301, 9)]:
         W = rng.choice(np.array(values, np.float32), (rows, cols))
         x = rng.integers(-4, 5, (batch, cols)).astype(np.float32)
         pre, post = run(gpu, dt, 0, W, x)
@@ -108,6 +109,7 @@ def test_batched_wide_tiles(gpu, oracle, dt, scheme, act):
     (4096, 3000, 16),   # K split 16 ways
     (300, 4096, 30),    # 2 activation row blocks, 1 row block per wave
     (2100, 3000, 17),   # both, ragged N
+    (500, 1001, 7),     # K not a multiple of 4: element loads of the input
 ])
 def test_small_batch_k_split(gpu, oracle, dt, scheme, rows, cols, batch):
     """Batches of 5-32 rows take the weight-streaming GEMM, split along K into

@@ -93,6 +93,11 @@ struct MxgArgs {
   float* part = nullptr;
   // block exponents in lane order (DeviceWeights::blk_frag), BLOCK32 only
   const uint8_t* blkf[2] = {nullptr, nullptr};
+  // small M (mxg_block_m(M) == 16): the fp32 input [M][cols] (row stride
+  // x_stride), split into terms by the GEMM kernel itself (a / as unused);
+  // x_vec: x 16-byte aligned, cols and x_stride multiples of 4
+  const float* x = nullptr;
+  int x_stride = 0, cols = 0, x_vec = 0;
   // large tiles, one matrix, N a multiple of 256: when set, the epilogue also
   // writes the split of post here, laid out as the split buffer of a layer
   // with the same rows (mpad) and kpad = N (the next layer of a chain)

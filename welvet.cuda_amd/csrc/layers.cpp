@@ -213,11 +213,24 @@ static MxgArgs mxg_args(const DenseLayer& L, int batch, const uint8_t* split) {
   return p;
 }
 
-Status dense_forward_split(const DenseLayer& L, int batch, Workspace* ws, float* pre, float* post,
-                           hipStream_t st) {
+// The fp32 input of a small-M GEMM, which splits it itself.
+static void set_input(MxgArgs& p, const float* x, int stride, int cols) {
+  p.x = x;
+  p.x_stride = stride;
+  p.cols = cols;
+  p.x_vec = stride % 4 == 0 && cols % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+}
+
+Status dense_forward_split(const DenseLayer& L, int batch, const float* x, bool split_ready,
+                           Workspace* ws, float* pre, float* post, hipStream_t st) {
   MxgArgs p = mxg_args(L, batch, split_buf(ws));
   p.pre = pre;
   p.post = post;
+  if (mxg_block_m(batch) > 16) {
+    if (!split_ready) WV_TRY(launch_split(x, L.in, batch, L.in, L.dev.kpad, split_buf(ws), st));
+  } else {
+    set_input(p, x, L.in, L.in);
+  }
   return launch_mxg(p, L.dev.dtype, L.dev.scheme == kSchemeBlock32, st);
 }
 
@@ -227,8 +240,7 @@ Status dense_forward(const DenseLayer& L, int batch, const float* x, float* pre,
   if (L.need_epi() && !post) return Status::err(kInvalid, "dense forward: post needed");
   if (uses_split(batch)) {
     WV_TRY(ensure_split(ws, gemm_ws_bytes(L, batch, 1)));
-    WV_TRY(launch_split(x, L.in, batch, L.in, L.dev.kpad, split_buf(ws), st));
-    return dense_forward_split(L, batch, ws, pre, post, st);
+    return dense_forward_split(L, batch, x, false, ws, pre, post, st);
   }
   if (batch >= 2 && batch <= kMxvMaxBatch) {
     MxvArgs m = mxv_args(L, x, L.in, batch);
@@ -377,8 +389,9 @@ Status swiglu_forward(const SwiGLULayer& L, int rows, const float* x, float* h, 
   if (uses_split(rows)) {
     WV_TRY(ensure_split(ws, swiglu_workspace_bytes(L, rows)));
     uint8_t* buf = split_buf(ws);
-    WV_TRY(launch_split(x, L.in, rows, L.in, L.gate.dev.kpad, buf, st));
     MxgArgs p = mxg_args(L.gate, rows, buf);
+    if (mxg_block_m(rows) > 16) WV_TRY(launch_split(x, L.in, rows, L.in, L.gate.dev.kpad, buf, st));
+    else set_input(p, x, L.in, L.in);
     p.mats = 2;
     p.codes[1] = L.up.dev.d_codes();
     p.scale[1] = L.up.dev.d_scale();
@@ -387,8 +400,7 @@ Status swiglu_forward(const SwiGLULayer& L, int rows, const float* x, float* h, 
     p.pre = h;
     p.need_epi = 0;
     WV_TRY(launch_mxg(p, L.gate.dev.dtype, L.gate.dev.scheme == kSchemeBlock32, st));
-    WV_TRY(launch_split(h, L.inter, rows, L.inter, L.down.dev.kpad, buf, st));
-    return dense_forward_split(L.down, rows, ws, y, nullptr, st);
+    return dense_forward_split(L.down, rows, h, false, ws, y, nullptr, st);
   }
   GemvArgs a = gemv_args(L.gate, x, L.in);
   a.mats = 2;
@@ -483,12 +495,14 @@ Status mha_forward(const MHALayer& L, int batch, int seq, const float* x, float*
   float* kb = qb + (size_t)T * c.q_dim();
   float* vb = kb + (size_t)T * c.kv_dim();
   if (uses_split(T)) {
-    // Q, K and V read the same activations: split them once
+    // Q, K and V read the same activations: above 32 rows they are split
+    // once (up to 32 rows each GEMM kernel splits its own K range)
     WV_TRY(ensure_split(ws, mha_split_bytes(L, T)));
-    WV_TRY(launch_split(x, c.d_model, T, c.d_model, L.q.dev.kpad, split_buf(ws), st));
-    WV_TRY(dense_forward_split(L.q, T, ws, qb, nullptr, st));
-    WV_TRY(dense_forward_split(L.k, T, ws, kb, nullptr, st));
-    WV_TRY(dense_forward_split(L.v, T, ws, vb, nullptr, st));
+    const bool once = mxg_block_m(T) > 16;
+    if (once) WV_TRY(launch_split(x, c.d_model, T, c.d_model, L.q.dev.kpad, split_buf(ws), st));
+    WV_TRY(dense_forward_split(L.q, T, x, once, ws, qb, nullptr, st));
+    WV_TRY(dense_forward_split(L.k, T, x, once, ws, kb, nullptr, st));
+    WV_TRY(dense_forward_split(L.v, T, x, once, ws, vb, nullptr, st));
   } else {
     WV_TRY(dense_forward(L.q, T, x, qb, nullptr, ws, st));
     WV_TRY(dense_forward(L.k, T, x, kb, nullptr, ws, st));

@@ -64,10 +64,12 @@ bool uses_split(int batch);
 // The activation-split workspace (Workspace::b): the split terms, then the
 // K-split partial sums of the products that use them.
 inline uint8_t* split_buf(Workspace* ws) { return ws->b.as<uint8_t>(); }
-// Batched path with activations already split into split_buf(ws)
-// (launch_split with L.dev.kpad).
-Status dense_forward_split(const DenseLayer& L, int batch, Workspace* ws, float* pre, float* post,
-                           hipStream_t st);
+// Batched path (batch > 4 rows) on x [batch][L.in]. Above 32 rows the GEMM
+// reads the split terms of x from split_buf(ws), made here unless
+// `split_ready` (launch_split of x with L.dev.kpad already ran); up to 32
+// rows the GEMM kernel splits x itself.
+Status dense_forward_split(const DenseLayer& L, int batch, const float* x, bool split_ready,
+                           Workspace* ws, float* pre, float* post, hipStream_t st);
 // Grows ws->b to at least n bytes (mount time; a forward that finds it too
 // small allocates, which a captured graph cannot do).
 Status ensure_split(Workspace* ws, size_t n);

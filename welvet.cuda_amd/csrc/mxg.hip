@@ -609,8 +609,9 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
 // rows (of each matrix), rows 128 RB g + 16 (RB w + j) + .., over the K
 // chunks [k0, k1) of split ks (at most KRT chunks). A CU streams HBM at a
 // bounded rate (~30-40 GB/s), so the split fills all CUs with one round of
-// workgroups, and RB = 2 halves the activation terms each CU stages. The activation terms of that K range (all M
-// rows, in operand order) are staged in LDS once; the weights then stream
+// workgroups, and RB = 2 halves the activation terms each CU stages. The
+// activation terms of that K range (all M rows, in operand order) are made
+// from the fp32 input in the prologue and kept in LDS; the weights stream
 // from HBM straight into registers D - 1 chunks ahead, in the order they are
 // consumed, so 8 (D - 1) chunks per CU are in flight. The KRT steps are
 // straight-line code (no loop back-edge, which makes the compiler wait for
@@ -618,18 +619,6 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
 // range repeats the last chunk with its weights zeroed. With one split the
 // epilogue is applied here; otherwise each split writes its raw sums to the
 // partial buffer and k_mxs_reduce adds them and applies the epilogue.
-typedef __attribute__((address_space(3))) void* LdsPtr;
-typedef const __attribute__((address_space(1))) void* GlobalPtr;
-
-// Direct-to-LDS copies: lane i of the wave writes its bytes at base + size * i.
-// (The copy size of the builtin must be a literal.)
-__device__ __forceinline__ void lds_dma16(const void* src, void* lds_base) {
-  __builtin_amdgcn_global_load_lds((GlobalPtr)src, (LdsPtr)lds_base, 16, 0, 0);
-}
-__device__ __forceinline__ void lds_dma4(const void* src, void* lds_base) {
-  __builtin_amdgcn_global_load_lds((GlobalPtr)src, (LdsPtr)lds_base, 4, 0, 0);
-}
-
 constexpr int kSmallWaves = 8;
 
 // Weight row blocks per wave: two once there are enough rows.
@@ -651,7 +640,7 @@ int mxs_ksplit(int N, int kpad, int mpad) {
   return ks < S ? ks : S;
 }
 
-template <int DT, bool BLK, int MATS, int MB, int RB, int KRT, int D>
+template <int DT, bool BLK, int MATS, int MB, int RB, int KRT, int D, bool XV>
 __global__ __launch_bounds__(64 * kSmallWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_mxs(
     MxgArgs p, int ksplit) {
   constexpr int ROWS = 16 * kSmallWaves * RB;  // weight rows per workgroup
@@ -660,7 +649,8 @@ __global__ __launch_bounds__(64 * kSmallWaves) __attribute__((amdgpu_waves_per_e
   __shared__ __attribute__((aligned(16))) uint8_t sA[MB * KRT * kChunkBytes];
   __shared__ __attribute__((aligned(16))) uint32_t sS[MB * KRT * 64];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // the wave index in a scalar register: branches on it are uniform
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int i16 = lane & 15, g = lane >> 4;
   const int S = p.kpad / 128, ks = blockIdx.y;
   const int k0 = (int)((long)S * ks / ksplit), k1 = (int)((long)S * (ks + 1) / ksplit);
@@ -703,25 +693,70 @@ __global__ __launch_bounds__(64 * kSmallWaves) __attribute__((amdgpu_waves_per_e
       }
   };
 
-  // Activation terms into LDS with direct-to-LDS copies (1 KiB per wave
-  // instruction; exponent dwords: 256 bytes per chunk), then the first
-  // D - 1 chunks of weights; the wait leaves those weight loads in flight.
-  {
-    const int pieces = MB * KR * (kChunkBytes / 1024);
-    for (int j = wave; j < pieces; j += kSmallWaves) {
-      const int b = j / (KR * (kChunkBytes / 1024)), r = j % (KR * (kChunkBytes / 1024));
-      lds_dma16(p.a + ((size_t)b * S + k0) * kChunkBytes + r * 1024 + lane * 16, sA + j * 1024);
+  // The activation terms of the K range, made here from the fp32 input with
+  // the code k_split uses and kept in LDS: split unit j = (row block b,
+  // chunk r), j = b * KR + r, goes to wave j % 8. Each lane loads the 32
+  // values of its operand (row b * 16 + i16, k = 64h + 16g + ..), with
+  // unconditional loads clamped to the last unit, row and column (16-byte
+  // loads when XV: x aligned, cols and stride multiples of 4). The first
+  // unit's loads are issued before the first D - 1 chunks of weights, so its
+  // split waits for them only and the weights stay in flight under it; a
+  // wave's further units (K ranges above 8 chunks) load after it.
+  constexpr int U = (MB * KRT + kSmallWaves - 1) / kSmallWaves;  // units per wave
+  const int units = MB * KR;
+  float4 xin[8];
+  auto load_unit = [&](int u) {
+    const int j = wave + kSmallWaves * u < units ? wave + kSmallWaves * u : units - 1;
+    const int row = (j / KR) * 16 + i16;
+    const float* src = p.x + (size_t)(row < p.M ? row : p.M - 1) * p.x_stride;
+    const int kb = (k0 + j % KR) * 128 + 16 * g;
+    if constexpr (XV) {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int k = kb + 64 * (q >> 2) + 4 * (q & 3);
+        xin[q] = *reinterpret_cast<const float4*>(src + (k < p.cols ? k : 0));
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int k = kb + 64 * (q >> 2) + 4 * (q & 3);
+        xin[q].x = src[k < p.cols ? k : p.cols - 1];
+        xin[q].y = src[k + 1 < p.cols ? k + 1 : p.cols - 1];
+        xin[q].z = src[k + 2 < p.cols ? k + 2 : p.cols - 1];
+        xin[q].w = src[k + 3 < p.cols ? k + 3 : p.cols - 1];
+      }
     }
-    for (int j = wave; j < MB * KR; j += kSmallWaves) {
-      const int b = j / KR, r = j % KR;
-      lds_dma4(p.as + ((size_t)b * S + k0 + r) * kChunkScaleBytes + lane * 4, sS + j * 64);
-    }
-  }
+  };
+  load_unit(0);
+  __builtin_amdgcn_sched_barrier(0);
   WFrag f[D];
 #pragma unroll
   for (int i = 0; i < D - 1; ++i) load_w(i, f[i]);
   constexpr int PREFILL = (D - 1) * MATS * RB * (1 + (FP4 ? 0 : 1) + (BLK ? 1 : 0));
-  __builtin_amdgcn_s_waitcnt(waitcnt_imm(PREFILL, 15));
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int j = wave + kSmallWaves * u;
+    if (j < units) {  // uniform
+      const bool rowok = (j / KR) * 16 + i16 < p.M;
+      const int kb = (k0 + j % KR) * 128 + 16 * g;
+      float v[2][16];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int k = kb + 64 * (q >> 2) + 4 * (q & 3);
+        const float4 t = xin[q];
+        float* d = &v[q >> 2][4 * (q & 3)];
+        d[0] = rowok && k < p.cols ? t.x : 0.0f;
+        d[1] = rowok && k + 1 < p.cols ? t.y : 0.0f;
+        d[2] = rowok && k + 2 < p.cols ? t.z : 0.0f;
+        d[3] = rowok && k + 3 < p.cols ? t.w : 0.0f;
+      }
+      split_terms(v, sA + (size_t)j * kChunkBytes, reinterpret_cast<uint8_t*>(sS + j * 64), lane);
+    }
+    if (u + 1 < U) load_unit(u + 1);
+  }
+  // the terms written by every wave are visible after the barrier; the
+  // weight loads stay in flight
+  __builtin_amdgcn_s_waitcnt(waitcnt_imm(PREFILL, 0));
   asm volatile("s_barrier" ::: "memory");
 
   v4f acc[MATS][RB][MB];
@@ -896,7 +931,7 @@ __global__ __launch_bounds__(kThreads) void k_mxs_reduce(MxgArgs p, int ksplit, 
   }
 }
 
-template <int DT, bool BLK, int MATS, int MB, int RB, int KRT>
+template <int DT, bool BLK, int MATS, int MB, int RB, int KRT, bool XV = true>
 void launch_small_krt(const MxgArgs& p, int ksplit, hipStream_t st) {
   // ring depth: 6-14 KiB of weights in flight per wave within the register
   // budget of two waves per SIMD
@@ -905,14 +940,16 @@ void launch_small_krt(const MxgArgs& p, int ksplit, hipStream_t st) {
   constexpr int D = D1 < KRT ? D1 : KRT;
   const int rows = 16 * kSmallWaves * RB;
   const dim3 grid((unsigned)((p.N + rows - 1) / rows), (unsigned)ksplit);
-  k_mxs<DT, BLK, MATS, MB, RB, KRT, D><<<grid, 64 * kSmallWaves, 0, st>>>(p, ksplit);
+  k_mxs<DT, BLK, MATS, MB, RB, KRT, D, XV><<<grid, 64 * kSmallWaves, 0, st>>>(p, ksplit);
 }
 
 template <int DT, bool BLK, int MATS, int MB, int RB>
 void launch_small_rb(const MxgArgs& p, int ksplit, hipStream_t st) {
   const int S = p.kpad / 128, kr = (S + ksplit - 1) / ksplit;  // largest range
   constexpr int K1 = MB == 1 ? 4 : 4, K2 = MB == 1 ? 8 : 8, K3 = MB == 1 ? 12 : 12;
-  if (kr <= K1) launch_small_krt<DT, BLK, MATS, MB, RB, K1>(p, ksplit, st);
+  // element loads of an unaligned input: one variant (the largest range)
+  if (!p.x_vec) launch_small_krt<DT, BLK, MATS, MB, RB, small_krt_max(MB), false>(p, ksplit, st);
+  else if (kr <= K1) launch_small_krt<DT, BLK, MATS, MB, RB, K1>(p, ksplit, st);
   else if (kr <= K2) launch_small_krt<DT, BLK, MATS, MB, RB, K2>(p, ksplit, st);
   else if (kr <= K3 || MB == 2) launch_small_krt<DT, BLK, MATS, MB, RB, K3>(p, ksplit, st);
   else if (kr <= 16) launch_small_krt<DT, BLK, MATS, MB, RB, (MB == 1 ? 16 : 12)>(p, ksplit, st);
@@ -923,6 +960,8 @@ template <int DT, bool BLK, int MATS, int MB>
 Status launch_small(const MxgArgs& p, hipStream_t st) {
   const int ksplit = mxs_ksplit(p.N, p.kpad, p.mpad);
   if (ksplit > 1 && !p.part) return Status::err(kInvalid, "mxg: K-split partial buffer missing");
+  if (!p.x || p.cols <= 0 || p.cols > p.kpad || p.x_stride < p.cols || p.M <= 0 || p.M > p.mpad)
+    return Status::err(kInvalid, "mxg: small-M input");
   const int rb = mxs_rb(p.N);
   if (rb == 2) launch_small_rb<DT, BLK, MATS, MB, 2>(p, ksplit, st);
   else launch_small_rb<DT, BLK, MATS, MB, 1>(p, ksplit, st);
