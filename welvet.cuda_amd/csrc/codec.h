@@ -169,29 +169,19 @@ WV_HD float scale_for(float amax, float maxrep) {
   return s == 0.0f ? 1.0f : s;
 }
 
-// Least e in [-127, 127] with amax <= maxrep * 2^e (amax == 0 or NaN -> 0).
-// With amax = A * 2^qa and maxrep = R * 2^qr (A, R in [1, 2)), the answer is
-// qa - qr + (A > R), clamped.
+// Least e in [-127, 127] with amax <= maxrep * 2^e (amax == 0 or NaN -> 0;
+// inf -> 127). With amax = A * 2^qa and maxrep = R * 2^qr (A, R in [1, 2)),
+// the answer is qa - qr + (A > R), clamped. Written without branches (it
+// runs per block in the activation split). A subnormal amax (below 2^-126)
+// gives at most -126 - qr, which clamps to -127 for every maxrep >= 2 (the
+// FP8 / FP4 maxima), so its significand is never normalized.
 WV_HD int e8m0_exponent(float amax, float maxrep) {
-  uint32_t a = bits_of(amax) & 0x7FFFFFFFu;
-  if (a == 0u || a > 0x7F800000u) return 0;
-  if (a == 0x7F800000u) return 127;
-  int qa = (int)(a >> 23) - 127;
-  uint32_t fa = a & 0x7FFFFFu;
-  if ((a >> 23) == 0u) {  // subnormal: normalize the significand
-    qa = -126;
-    while ((fa & 0x800000u) == 0u) {
-      fa <<= 1;
-      --qa;
-    }
-    fa &= 0x7FFFFFu;
-  }
+  const uint32_t a = bits_of(amax) & 0x7FFFFFFFu;
   const uint32_t r = bits_of(maxrep);
-  const int qr = (int)(r >> 23) - 127;
-  int e = qa - qr + ((fa > (r & 0x7FFFFFu)) ? 1 : 0);
-  if (e < -127) e = -127;
-  if (e > 127) e = 127;
-  return e;
+  int e = (int)(a >> 23) - (int)(r >> 23) + ((a & 0x7FFFFFu) > (r & 0x7FFFFFu) ? 1 : 0);
+  e = e < -127 ? -127 : e > 127 ? 127 : e;
+  e = a == 0x7F800000u ? 127 : e;
+  return a == 0u || a > 0x7F800000u ? 0 : e;
 }
 
 // 2^e as f32 for e in [-127, 127] (2^-127 is the subnormal 0x00400000).

@@ -38,6 +38,12 @@ typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef float v2f __attribute__((ext_vector_type(2)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+// fp32 input rows in the global address space (global, not flat, loads)
+typedef const __attribute__((address_space(1))) float* GlobalF;
+typedef __attribute__((address_space(1))) uint8_t* GlobalU8;
+typedef __attribute__((address_space(3))) uint8_t* LdsU8;
 
 __device__ __forceinline__ double act_f64(int act, double x) {
   switch (act) {
@@ -81,9 +87,15 @@ constexpr int waitcnt_imm(int vm, int lgkm) {
 // store at chunk + t * kFragBytes + h * 1024 + 16 l; the block exponents are
 // gathered to the lanes that pass them to the instruction (row l % 16, block
 // l / 16) and stored as one dword per lane at scales + 4 l (byte t: term t).
-__device__ __forceinline__ void split_terms(float (&v)[2][16], uint8_t* __restrict__ chunk,
-                                            uint8_t* __restrict__ scales, int lane) {
-  uint8_t* dst = chunk + lane * 16;
+// AS: the address space of the destination (1 global, 3 LDS).
+template <int AS>
+__device__ __forceinline__ void split_terms(float (&v)[2][16],
+                                            __attribute__((address_space(AS))) uint8_t* chunk,
+                                            __attribute__((address_space(AS))) uint8_t* scales,
+                                            int lane) {
+  typedef __attribute__((address_space(AS))) i32x4 I4;
+  typedef __attribute__((address_space(AS))) uint32_t U32;
+  __attribute__((address_space(AS))) uint8_t* dst = chunk + lane * 16;
   const int i16 = lane & 15;
   // exponent of block b = l / 16 for row i16 comes from lane 32 (b & 1) + i16,
   // half b >> 1
@@ -113,12 +125,12 @@ __device__ __forceinline__ void split_terms(float (&v)[2][16], uint8_t* __restri
           v[h][4 * q + 2] -= q1.x * sc, v[h][4 * q + 3] -= q1.y * sc;
         }
       }
-      *reinterpret_cast<int4*>(dst + t * kFragBytes + h * 1024) = make_int4(wq[0], wq[1], wq[2], wq[3]);
+      *reinterpret_cast<I4*>(dst + t * kFragBytes + h * 1024) = i32x4{wq[0], wq[1], wq[2], wq[3]};
     }
     const int e0 = __shfl(e[0], src, 64), e1 = __shfl(e[1], src, 64);
     sword |= (uint32_t)(((lane >> 5) ? e1 : e0) + 127) << (8 * t);
   }
-  *reinterpret_cast<uint32_t*>(scales + lane * 4) = sword;
+  *reinterpret_cast<U32*>(scales + lane * 4) = sword;
 }
 
 // The activation split, written in operand order. One wave per (16-row block
@@ -126,6 +138,7 @@ __device__ __forceinline__ void split_terms(float (&v)[2][16], uint8_t* __restri
 // row-contiguous loads; then lane l (row i16 = l % 16, group g = l / 16)
 // takes the 32 values of its operand, k = 64h + 16g + j (h = 0, 1; j < 16),
 // and split_terms writes them. Rows >= M and columns >= cols give zero codes.
+// VEC: x 16-byte aligned, cols and x_stride multiples of 4.
 template <bool VEC>
 __global__ __launch_bounds__(kThreads) void k_split(const float* __restrict__ x, int x_stride,
                                                     int M, int cols, int mpad, int kpad,
@@ -139,7 +152,7 @@ __global__ __launch_bounds__(kThreads) void k_split(const float* __restrict__ x,
     as = j.buf + (size_t)kTerms * mpad * kpad;
   }
   constexpr int kWaves = kThreads / 64;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int KC = kpad / 128;
   const int w = blockIdx.x * kWaves + wave;
   if (w >= (mpad / 16) * KC) return;  // whole waves; no workgroup barrier below
@@ -147,23 +160,36 @@ __global__ __launch_bounds__(kThreads) void k_split(const float* __restrict__ x,
 
   __shared__ __attribute__((aligned(16))) float stage[kWaves][16][132];
   float(*sl)[132] = stage[wave];  // rows padded by 16 bytes: no bank conflicts below
+  // Unconditional loads clamped to the last row and column (16-byte loads
+  // when VEC: x aligned, cols and x_stride multiples of 4), then zeroed
+  // outside [0, M) x [0, cols).
+  const GlobalF xg = (GlobalF)x;
   const int c4 = 4 * (lane & 31), k = kc * 128 + c4;
+  float4 xv[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const int r = 2 * i + (lane >> 5), m = rb * 16 + r;
-    float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (m < M) {
-      const float* row = x + (size_t)m * x_stride;
-      if (VEC && k + 4 <= cols) {
-        v = *reinterpret_cast<const float4*>(row + k);
-      } else {
-        v.x = k < cols ? row[k] : 0.0f;
-        v.y = k + 1 < cols ? row[k + 1] : 0.0f;
-        v.z = k + 2 < cols ? row[k + 2] : 0.0f;
-        v.w = k + 3 < cols ? row[k + 3] : 0.0f;
-      }
+    const int m = rb * 16 + 2 * i + (lane >> 5);
+    const GlobalF row = xg + (size_t)(m < M ? m : M - 1) * x_stride;
+    if constexpr (VEC) {
+      const f32x4 t = *reinterpret_cast<const __attribute__((address_space(1))) f32x4*>(row + (k < cols ? k : 0));
+      xv[i] = make_float4(t.x, t.y, t.z, t.w);
+    } else {
+      xv[i].x = row[k < cols ? k : cols - 1];
+      xv[i].y = row[k + 1 < cols ? k + 1 : cols - 1];
+      xv[i].z = row[k + 2 < cols ? k + 2 : cols - 1];
+      xv[i].w = row[k + 3 < cols ? k + 3 : cols - 1];
     }
-    *reinterpret_cast<float4*>(&sl[r][c4]) = v;
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int r = 2 * i + (lane >> 5);
+    const bool ok = rb * 16 + r < M;
+    float4 t;
+    t.x = ok && k < cols ? xv[i].x : 0.0f;
+    t.y = ok && k + 1 < cols ? xv[i].y : 0.0f;
+    t.z = ok && k + 2 < cols ? xv[i].z : 0.0f;
+    t.w = ok && k + 3 < cols ? xv[i].w : 0.0f;
+    *reinterpret_cast<float4*>(&sl[r][c4]) = t;
   }
   // The LDS operations of one wave execute in order, so the reads below see
   // this wave's writes.
@@ -177,8 +203,8 @@ __global__ __launch_bounds__(kThreads) void k_split(const float* __restrict__ x,
       v[h][4 * q] = t.x, v[h][4 * q + 1] = t.y, v[h][4 * q + 2] = t.z, v[h][4 * q + 3] = t.w;
     }
 
-  split_terms(v, a + (size_t)(rb * KC + kc) * kChunkBytes,
-              as + (size_t)(rb * KC + kc) * kChunkScaleBytes, lane);
+  split_terms<1>(v, (GlobalU8)(a + (size_t)(rb * KC + kc) * kChunkBytes),
+                 (GlobalU8)(as + (size_t)(rb * KC + kc) * kChunkScaleBytes), lane);
 }
 
 // Large-M tile (M > 32): 128 activation rows x 128 staged weight rows (64 per
@@ -595,8 +621,8 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
               v[h][4 * q] = live ? t.x : 0.0f, v[h][4 * q + 1] = live ? t.y : 0.0f;
               v[h][4 * q + 2] = live ? t.z : 0.0f, v[h][4 * q + 3] = live ? t.w : 0.0f;
             }
-          split_terms(v, p.next + (size_t)(rb * kcn + kc) * kChunkBytes,
-                      nscale + (size_t)(rb * kcn + kc) * kChunkScaleBytes, lane);
+          split_terms<1>(v, (GlobalU8)(p.next + (size_t)(rb * kcn + kc) * kChunkBytes),
+                         (GlobalU8)(nscale + (size_t)(rb * kcn + kc) * kChunkScaleBytes), lane);
         }
         __builtin_amdgcn_wave_barrier();
       }
@@ -750,7 +776,7 @@ __global__ __launch_bounds__(64 * kSmallWaves) __attribute__((amdgpu_waves_per_e
         d[2] = rowok && k + 2 < p.cols ? t.z : 0.0f;
         d[3] = rowok && k + 3 < p.cols ? t.w : 0.0f;
       }
-      split_terms(v, sA + (size_t)j * kChunkBytes, reinterpret_cast<uint8_t*>(sS + j * 64), lane);
+      split_terms<3>(v, (LdsU8)(sA + (size_t)j * kChunkBytes), (LdsU8)(sS + j * 64), lane);
     }
     if (u + 1 < U) load_unit(u + 1);
   }
@@ -1032,7 +1058,7 @@ Status launch_split(const float* x, int x_stride, int M, int cols, int kpad, uin
   uint8_t* as = buf + (size_t)kTerms * mpad * kpad;
   const int64_t waves = (int64_t)(mpad / 16) * (kpad / 128);
   const unsigned grid = (unsigned)((waves + kThreads / 64 - 1) / (kThreads / 64));
-  const bool vec = (x_stride % 4 == 0) && ((reinterpret_cast<uintptr_t>(x) & 15u) == 0);
+  const bool vec = x_stride % 4 == 0 && cols % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
   if (vec) k_split<true><<<grid, kThreads, 0, st>>>(x, x_stride, M, cols, mpad, kpad, a, as, nullptr);
   else k_split<false><<<grid, kThreads, 0, st>>>(x, x_stride, M, cols, mpad, kpad, a, as, nullptr);
   return hip_status(hipGetLastError(), "split launch");
