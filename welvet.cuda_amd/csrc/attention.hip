@@ -179,26 +179,38 @@ __global__ __launch_bounds__(64) void k_attention(AttnArgs a) {
 // Scores and sums are the same function of the same values; only the fp32
 // summation order differs from the per-position loop.
 //
-// A workgroup of 4 waves takes 64 queries (16 per wave) of one (batch, head)
-// and walks the distinct rows in tiles of 64 keys staged in LDS (rows padded
-// to hd + 4 floats: conflict-free reads below). Per 16-key block a wave runs
+// A workgroup of 8 waves takes 128 queries (16 per wave) of one (batch,
+// head) and walks the distinct rows in tiles of 64 keys staged in LDS (rows
+// padded to hd + 4 floats: conflict-free reads below), double-buffered: the
+// loads of tile i+1 are issued into registers before tile i's products and
+// stored to the other buffer after them, one barrier per tile. Per 16-key
+// block a wave runs
 //   S^T = K Q^T  (v_mfma_f32_16x16x4f32, hd/4 steps): lane l holds the
 //                scores of query l%16 for keys 4*(l/16) + i, i = 0..3;
 //   O^T += V^T P^T: the same 4 values per lane are the B operand (MFMA k
 //                index l/16 <-> key 4*(l/16) + j at step j), V^T the A
 //                operand, so no transpose is needed.
-// Softmax is online in fp32 per query (max and sum over the 4 lanes that
-// share a query, xor 16 / xor 32).
-constexpr int kQB = 64;  // queries per workgroup
-constexpr int kKT = 64;  // keys per LDS tile
+// The scores of a whole tile (4 blocks) are formed first, so the online
+// softmax (fp32, per query: max and sum over the 4 lanes that share a
+// query, xor 16 / xor 32) and the rescaling of O happen once per 64 keys.
+constexpr int kAttnWaves = 8;
+
+// e^x for the softmax weights (x <= 0): the hardware base-2 exponential of
+// x log2(e), within a few ulp; results below the f32 normal range are 0.
+__device__ __forceinline__ float exp_fast(float x) {
+  return __builtin_amdgcn_exp2f(x * 1.44269504088896341f);
+}
+constexpr int kQB = 16 * kAttnWaves;  // queries per workgroup
+constexpr int kKT = 64;               // keys per LDS tile
 
 template <int HD>
-__global__ __launch_bounds__(256) void k_attn_mfma(AttnArgs a, int qblocks) {
-  constexpr int ST = HD / 4;       // QK MFMA steps
-  constexpr int DT = HD / 16;      // 16-wide head-dim tiles of O
-  constexpr int ROW = HD + 4;      // padded LDS row (floats)
-  __shared__ float ks[kKT * ROW];
-  __shared__ float vs[kKT * ROW];
+__global__ __launch_bounds__(64 * kAttnWaves) void k_attn_mfma(AttnArgs a, int qblocks) {
+  constexpr int ST = HD / 4;                            // QK MFMA steps
+  constexpr int DT = HD / 16;                           // 16-wide head-dim tiles of O
+  constexpr int ROW = HD + 4;                           // padded LDS row (floats)
+  constexpr int NT = 64 * kAttnWaves;                   // threads
+  __shared__ float ks[2][kKT * ROW];
+  __shared__ float vs[2][kKT * ROW];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c16 = lane & 15, g = lane >> 4;
   const int b = blockIdx.x / qblocks, qb = blockIdx.x % qblocks;
@@ -217,79 +229,141 @@ __global__ __launch_bounds__(256) void k_attn_mfma(AttnArgs a, int qblocks) {
     const float* qrow = a.q + (size_t)qp * qd + (size_t)h * HD;
 #pragma unroll
     for (int st = 0; st < ST; ++st) qr[st] = qrow[4 * st + g];
+    if (a.rope) {
+      // the lane holds both members of its pairs (d, d + HD/2), d = 4 st + g
+      const double* tq = a.rope_tab + 2 * (size_t)qp * (HD / 2);
+#pragma unroll
+      for (int st = 0; st < ST / 2; ++st) {
+        const int d = 4 * st + g;
+        const double c = tq[2 * d], sn = tq[2 * d + 1];
+        const double a0 = qr[st], a1 = qr[st + ST / 2];
+        qr[st] = (float)(a0 * c - a1 * sn);
+        qr[st + ST / 2] = (float)(a0 * sn + a1 * c);
+      }
+    }
   }
   v4f o[DT];
 #pragma unroll
   for (int d = 0; d < DT; ++d) o[d] = v4f{0.f, 0.f, 0.f, 0.f};
   float m = -INFINITY, l = 0.0f;
 
-  for (int t0 = p_lo; t0 <= last; t0 += kKT) {
-    __syncthreads();
-    for (int i = tid; i < kKT * (HD / 4); i += 256) {
-      const int r = i / (HD / 4), c4 = (i % (HD / 4)) * 4;
-      const int p = t0 + r;
-      float4 kk = make_float4(0.f, 0.f, 0.f, 0.f), vv = kk;
-      if (p <= last) {
-        kk = *reinterpret_cast<const float4*>(a.k + (size_t)p * kvd + (size_t)kvh * HD + c4);
-        vv = *reinterpret_cast<const float4*>(a.v + (size_t)p * kvd + (size_t)kvh * HD + c4);
+  // K and V rows of a tile in pair units: unit i = tid + NT u covers row
+  // i / (HD/8) and the column quads c4 and c4 + HD/2, c4 = 4 (i % (HD/8)),
+  // so a thread holds both members of the RoPE pairs (d, d + HD/2) it
+  // rotates. Rows past `last` are exact zeros.
+  constexpr int UNITS = kKT * HD / 8, PU = (UNITS + NT - 1) / NT;
+  v4f kreg[2 * PU], vreg[2 * PU];
+  auto load_tile = [&](int t0) {
+#pragma unroll
+    for (int u = 0; u < PU; ++u) {
+      const int i = tid + NT * u;
+      if (UNITS % NT != 0 && i >= UNITS) break;  // whole waves (HD = 32)
+      const int r = i / (HD / 8), c4 = (i % (HD / 8)) * 4;
+      const int p = t0 + r, pc = p <= last ? p : last;
+      const size_t off = (size_t)pc * kvd + (size_t)kvh * HD + c4;
+      v4f k0 = *reinterpret_cast<const v4f*>(a.k + off);
+      v4f k1 = *reinterpret_cast<const v4f*>(a.k + off + HD / 2);
+      const v4f v0 = *reinterpret_cast<const v4f*>(a.v + off);
+      const v4f v1 = *reinterpret_cast<const v4f*>(a.v + off + HD / 2);
+      if (a.rope) {
+        const double* tk = a.rope_tab + 2 * ((size_t)pc * (HD / 2) + c4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const double c = tk[2 * e], sn = tk[2 * e + 1];
+          const double a0 = k0[e], a1 = k1[e];
+          k0[e] = (float)(a0 * c - a1 * sn);
+          k1[e] = (float)(a0 * sn + a1 * c);
+        }
       }
-      *reinterpret_cast<float4*>(&ks[r * ROW + c4]) = kk;
-      *reinterpret_cast<float4*>(&vs[r * ROW + c4]) = vv;
+      const v4f z = v4f{0.f, 0.f, 0.f, 0.f};
+      kreg[2 * u] = p <= last ? k0 : z;
+      kreg[2 * u + 1] = p <= last ? k1 : z;
+      vreg[2 * u] = p <= last ? v0 : z;
+      vreg[2 * u + 1] = p <= last ? v1 : z;
     }
-    __syncthreads();
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < PU; ++u) {
+      const int i = tid + NT * u;
+      if (UNITS % NT != 0 && i >= UNITS) break;
+      const int r = i / (HD / 8), c4 = (i % (HD / 8)) * 4;
+      *reinterpret_cast<v4f*>(&ks[buf][r * ROW + c4]) = kreg[2 * u];
+      *reinterpret_cast<v4f*>(&ks[buf][r * ROW + c4 + HD / 2]) = kreg[2 * u + 1];
+      *reinterpret_cast<v4f*>(&vs[buf][r * ROW + c4]) = vreg[2 * u];
+      *reinterpret_cast<v4f*>(&vs[buf][r * ROW + c4 + HD / 2]) = vreg[2 * u + 1];
+    }
+  };
+  load_tile(p_lo);
+  store_tile(0);
+  __syncthreads();
+
+#pragma unroll 1
+  for (int t0 = p_lo, cur = 0; t0 <= last; t0 += kKT, cur ^= 1) {
+    const bool more = t0 + kKT <= last;  // uniform
+    if (more) load_tile(t0 + kKT);
+    const float* kt = ks[cur];
+    const float* vt = vs[cur];
     // multiplicity base of the tile start: floor(t0 / msl) + 1 (msl >= 64, so
     // the tile crosses at most one multiple of msl)
     const int base0 = t0 / a.msl + 1;
-    const int next_mult = (base0) * a.msl;  // first p with a larger base
-#pragma unroll 1
-    for (int kb = 0; kb < kKT; kb += 16) {
-      if (t0 + kb > last) break;
-      v4f sc = v4f{0.f, 0.f, 0.f, 0.f};
+    const int next_mult = base0 * a.msl;  // first p with a larger base
+    v4f sc[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      sc[kb] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int st = 0; st < ST; ++st)
-        sc = __builtin_amdgcn_mfma_f32_16x16x4f32(ks[(kb + c16) * ROW + 4 * st + g], qr[st], sc,
-                                                  0, 0, 0);
-      float w[4], smax = -INFINITY;
-      int cnt[4];
+        sc[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kt[(16 * kb + c16) * ROW + 4 * st + g], qr[st],
+                                                      sc[kb], 0, 0, 0);
+    }
+    float w[16], smax = -INFINITY;
+    int cnt[16];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int p = t0 + kb + 4 * g + i;
+        const int p = t0 + 16 * kb + 4 * g + i;
         int c = p <= last ? base0 + (p >= next_mult ? 1 : 0) : 0;
         if (causal && p > qp) c -= 1;
-        cnt[i] = c;
-        w[i] = (float)((double)sc[i] * a.scale);
-        if (c > 0) smax = fmaxf(smax, w[i]);
+        cnt[4 * kb + i] = c;
+        w[4 * kb + i] = (float)((double)sc[kb][i] * a.scale);
+        if (c > 0) smax = fmaxf(smax, w[4 * kb + i]);
       }
-      if (a.sigmoid) {
+    if (a.sigmoid) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) w[i] = cnt[i] > 0 ? (float)cnt[i] / (1.0f + expf(-w[i])) : 0.0f;
-      } else {
-        smax = fmaxf(smax, __shfl_xor(smax, 16, 64));
-        smax = fmaxf(smax, __shfl_xor(smax, 32, 64));
-        const float nm = fmaxf(m, smax);
-        const float corr = (m == -INFINITY) ? 0.0f : expf(m - nm);
-        float ws = 0.0f;
+      for (int i = 0; i < 16; ++i) w[i] = cnt[i] > 0 ? (float)cnt[i] / (1.0f + expf(-w[i])) : 0.0f;
+    } else {
+      smax = fmaxf(smax, __shfl_xor(smax, 16, 64));
+      smax = fmaxf(smax, __shfl_xor(smax, 32, 64));
+      const float nm = fmaxf(m, smax);
+      const float corr = (m == -INFINITY) ? 0.0f : exp_fast(m - nm);
+      float ws = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          w[i] = cnt[i] > 0 ? (float)cnt[i] * expf(w[i] - nm) : 0.0f;
-          ws += w[i];
-        }
-        ws += __shfl_xor(ws, 16, 64);
-        ws += __shfl_xor(ws, 32, 64);
-        if (nm != -INFINITY) {
-          l = l * corr + ws;
-#pragma unroll
-          for (int d = 0; d < DT; ++d) o[d] *= corr;
-          m = nm;
-        }
+      for (int i = 0; i < 16; ++i) {
+        w[i] = cnt[i] > 0 ? (float)cnt[i] * exp_fast(w[i] - nm) : 0.0f;
+        ws += w[i];
       }
+      ws += __shfl_xor(ws, 16, 64);
+      ws += __shfl_xor(ws, 32, 64);
+      if (nm != -INFINITY) {
+        l = l * corr + ws;
+#pragma unroll
+        for (int d = 0; d < DT; ++d) o[d] *= corr;
+        m = nm;
+      }
+    }
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int d = 0; d < DT; ++d)
-          o[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(vs[(kb + 4 * g + j) * ROW + d * 16 + c16],
-                                                      w[j], o[d], 0, 0, 0);
-    }
+          o[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(vt[(16 * kb + 4 * g + j) * ROW + d * 16 + c16],
+                                                      w[4 * kb + j], o[d], 0, 0, 0);
+    // the other buffer was last read before the previous barrier
+    if (more) store_tile(cur ^ 1);
+    __syncthreads();
   }
   if (!q_ok) return;
   // o[d]: lane holds query c16, head dims d*16 + 4g + i
@@ -314,23 +388,23 @@ Status build_rope_table(double* tab, int tokens, int hd, double theta, hipStream
 Status launch_attention(const AttnArgs& a, hipStream_t st) {
   if (a.hd > 64 * kMaxHdPerLane || a.hd % 4 != 0)
     return Status::err(kUnsupported, "attention: head_dim must be a multiple of 4 and <= 256");
-  if (a.rope) {
+  // the tile multiplicity update assumes at most one multiple of msl per
+  // 64-key tile, hence msl >= 64; RoPE is applied inside (table required)
+  const bool fast = (a.mask == 1 || a.mask == 2) && !a.alibi && a.msl >= kKT &&
+                    a.msl >= a.seq && (a.hd == 32 || a.hd == 64 || a.hd == 128) &&
+                    a.seq > 0 && a.tokens % a.seq == 0 && (!a.rope || a.rope_tab);
+  if (a.rope && !fast) {
     k_rope<<<a.tokens, 256, 0, st>>>(const_cast<float*>(a.q), const_cast<float*>(a.k), a.tokens,
                                      a.heads, a.kv_heads, a.hd, a.rope_theta, a.rope_tab);
     WV_HIP(hipGetLastError());
   }
-  // the tile multiplicity update assumes at most one multiple of msl per
-  // 64-key tile, hence msl >= 64
-  const bool fast = (a.mask == 1 || a.mask == 2) && !a.alibi && a.msl >= kKT &&
-                    a.msl >= a.seq && (a.hd == 32 || a.hd == 64 || a.hd == 128) &&
-                    a.seq > 0 && a.tokens % a.seq == 0;
   if (fast) {
     const int qblocks = (a.seq + kQB - 1) / kQB;
     dim3 grid((unsigned)(a.tokens / a.seq * qblocks), (unsigned)a.heads);
     switch (a.hd) {
-    case 32: k_attn_mfma<32><<<grid, 256, 0, st>>>(a, qblocks); break;
-    case 64: k_attn_mfma<64><<<grid, 256, 0, st>>>(a, qblocks); break;
-    default: k_attn_mfma<128><<<grid, 256, 0, st>>>(a, qblocks); break;
+    case 32: k_attn_mfma<32><<<grid, 64 * kAttnWaves, 0, st>>>(a, qblocks); break;
+    case 64: k_attn_mfma<64><<<grid, 64 * kAttnWaves, 0, st>>>(a, qblocks); break;
+    default: k_attn_mfma<128><<<grid, 64 * kAttnWaves, 0, st>>>(a, qblocks); break;
     }
     return hip_status(hipGetLastError(), "attention launch");
   }

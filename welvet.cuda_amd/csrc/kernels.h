@@ -98,6 +98,12 @@ struct MxgArgs {
   // x_vec: x 16-byte aligned, cols and x_stride multiples of 4
   const float* x = nullptr;
   int x_stride = 0, cols = 0, x_vec = 0;
+  // large tiles, one matrix, no bias or activation: when set, the epilogue
+  // applies RoPE to the output (row m = token position m, heads of rope_hd
+  // columns, 128 % rope_hd == 0): pairs (d, d + rope_hd/2) rotated by the
+  // (cos, sin) table [token][pair] in f64, as build_rope_table makes it
+  const double* rope_tab = nullptr;
+  int rope_hd = 0;
   // large tiles, one matrix, N a multiple of 256: when set, the epilogue also
   // writes the split of post here, laid out as the split buffer of a layer
   // with the same rows (mpad) and kpad = N (the next layer of a chain)

@@ -222,10 +222,13 @@ static void set_input(MxgArgs& p, const float* x, int stride, int cols) {
 }
 
 Status dense_forward_split(const DenseLayer& L, int batch, const float* x, bool split_ready,
-                           Workspace* ws, float* pre, float* post, hipStream_t st) {
+                           Workspace* ws, float* pre, float* post, hipStream_t st,
+                           const double* rope_tab, int rope_hd) {
   MxgArgs p = mxg_args(L, batch, split_buf(ws));
   p.pre = pre;
   p.post = post;
+  p.rope_tab = rope_tab;
+  p.rope_hd = rope_hd;
   if (mxg_block_m(batch) > 16) {
     if (!split_ready) WV_TRY(launch_split(x, L.in, batch, L.in, L.dev.kpad, split_buf(ws), st));
   } else {
@@ -494,14 +497,22 @@ Status mha_forward(const MHALayer& L, int batch, int seq, const float* x, float*
   float* qb = ws->a.as<float>();
   float* kb = qb + (size_t)T * c.q_dim();
   float* vb = kb + (size_t)T * c.kv_dim();
+  // RoPE in the Q and K GEMM epilogues (large tiles): the attention kernel
+  // then reads rotated rows
+  const bool rope = mha_rope(c);
+  const bool rope_epi = rope && uses_split(T) && mxg_block_m(T) > 16 && c.head_dim % 8 == 0 &&
+                        128 % c.head_dim == 0 && !L.q.need_epi() && !L.k.need_epi();
+  if (rope) WV_TRY(ensure_rope_table(L, T, ws, st));
   if (uses_split(T)) {
     // Q, K and V read the same activations: above 32 rows they are split
     // once (up to 32 rows each GEMM kernel splits its own K range)
     WV_TRY(ensure_split(ws, mha_split_bytes(L, T)));
     const bool once = mxg_block_m(T) > 16;
+    const double* tab = rope_epi ? ws->c.as<const double>() : nullptr;
+    const int rhd = rope_epi ? c.head_dim : 0;
     if (once) WV_TRY(launch_split(x, c.d_model, T, c.d_model, L.q.dev.kpad, split_buf(ws), st));
-    WV_TRY(dense_forward_split(L.q, T, x, once, ws, qb, nullptr, st));
-    WV_TRY(dense_forward_split(L.k, T, x, once, ws, kb, nullptr, st));
+    WV_TRY(dense_forward_split(L.q, T, x, once, ws, qb, nullptr, st, tab, rhd));
+    WV_TRY(dense_forward_split(L.k, T, x, once, ws, kb, nullptr, st, tab, rhd));
     WV_TRY(dense_forward_split(L.v, T, x, once, ws, vb, nullptr, st));
   } else {
     WV_TRY(dense_forward(L.q, T, x, qb, nullptr, ws, st));
@@ -514,11 +525,8 @@ Status mha_forward(const MHALayer& L, int batch, int seq, const float* x, float*
   a.hd = c.head_dim, a.msl = c.max_seq_len;
   a.mask = c.mask, a.window = c.window, a.prefix_len = c.prefix_len;
   a.window_causal = (c.window_causal || c.mask == 1) ? 1 : 0;
-  a.rope = mha_rope(c) ? 1 : 0;
-  if (a.rope) {
-    WV_TRY(ensure_rope_table(L, T, ws, st));
-    a.rope_tab = ws->c.as<const double>();
-  }
+  a.rope = rope && !rope_epi ? 1 : 0;
+  if (a.rope) a.rope_tab = ws->c.as<const double>();
   a.alibi = (c.pos == 2 || c.pos == 3) ? 1 : 0;
   a.sigmoid = c.softmax == 1 ? 1 : 0;
   a.rope_theta = c.rope_theta;

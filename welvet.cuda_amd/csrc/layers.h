@@ -69,7 +69,8 @@ inline uint8_t* split_buf(Workspace* ws) { return ws->b.as<uint8_t>(); }
 // `split_ready` (launch_split of x with L.dev.kpad already ran); up to 32
 // rows the GEMM kernel splits x itself.
 Status dense_forward_split(const DenseLayer& L, int batch, const float* x, bool split_ready,
-                           Workspace* ws, float* pre, float* post, hipStream_t st);
+                           Workspace* ws, float* pre, float* post, hipStream_t st,
+                           const double* rope_tab = nullptr, int rope_hd = 0);
 // Grows ws->b to at least n bytes (mount time; a forward that finds it too
 // small allocates, which a captured graph cannot do).
 Status ensure_split(Workspace* ws, size_t n);

@@ -272,6 +272,8 @@ __device__ __forceinline__ MxgArgs load_args(ConstArgs t) {
   p.blkf[0] = t->blkf[0];
   p.blkf[1] = t->blkf[1];
   p.next = t->next;
+  p.rope_tab = t->rope_tab;
+  p.rope_hd = t->rope_hd;
   return p;
 }
 
@@ -555,7 +557,28 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
 #pragma unroll
       for (int rr = 0; rr < SM * 16 / RPI; ++rr) {
         const int r = rr * RPI + lane / LPR;
-        const float4 y = *reinterpret_cast<const float4*>(&stage[wave][r][cl]);
+        float4 y = *reinterpret_cast<const float4*>(&stage[wave][r][cl]);
+        if constexpr (MATS == 1 && CH == 128) {
+          if (p.rope_tab) {
+            // the 4 columns sit in one half of one head; the partner columns
+            // are in the same staged chunk (128 % rope_hd == 0)
+            const int half = p.rope_hd >> 1;
+            const int d = (hc * CH + cl) % p.rope_hd;  // n0 is a multiple of 128
+            const bool lo = d < half;
+            const float4 yp = *reinterpret_cast<const float4*>(&stage[wave][r][lo ? cl + half : cl - half]);
+            const int tok = rbase + r < p.M ? rbase + r : p.M - 1;
+            const double* tb = p.rope_tab + 2 * ((size_t)tok * half + (lo ? d : d - half));
+            const float ya[4] = {y.x, y.y, y.z, y.w}, yb[4] = {yp.x, yp.y, yp.z, yp.w};
+            float yo[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const double c = tb[2 * e], sn = tb[2 * e + 1];
+              const double a0 = lo ? ya[e] : yb[e], a1 = lo ? yb[e] : ya[e];
+              yo[e] = lo ? (float)(a0 * c - a1 * sn) : (float)(a0 * sn + a1 * c);
+            }
+            y = make_float4(yo[0], yo[1], yo[2], yo[3]);
+          }
+        }
         if (rbase + r >= p.M || n >= p.N) continue;
         const size_t oi = (size_t)(rbase + r) * p.out_stride + n;
         if (vec_out && n + 3 < p.N) {
@@ -1003,6 +1026,9 @@ Status launch_small(const MxgArgs& p, hipStream_t st) {
 
 template <int DT, bool BLK, int MATS>
 Status launch_t(const MxgArgs& p, int bm, hipStream_t st) {
+  if (p.rope_tab && (bm != kBM || MATS != 1 || p.need_epi || p.next || p.rope_hd <= 0 ||
+                     p.rope_hd % 8 != 0 || 128 % p.rope_hd != 0))
+    return Status::err(kInvalid, "mxg: RoPE epilogue needs the large tiles, one matrix, no epilogue");
   if (bm == kBM) {
     if ((size_t)kTerms * p.mpad * p.kpad >= (1ull << 31) ||
         (size_t)round_up(p.N, 256) * p.pitch >= (1ull << 31))
