@@ -181,9 +181,8 @@ __global__ __launch_bounds__(64) void k_attention(AttnArgs a) {
 //
 // A workgroup of 8 waves takes 128 queries (16 per wave) of one (batch,
 // head) and walks the distinct rows in tiles of 64 keys staged in LDS (rows
-// padded to hd + 4 floats: conflict-free reads below), double-buffered: the
-// loads of tile i+1 are issued into registers before tile i's products and
-// stored to the other buffer after them, one barrier per tile. Per 16-key
+// padded to hd + 4 floats: conflict-free reads below), double-buffered
+// through registers, one barrier per tile. Per 16-key
 // block a wave runs
 //   S^T = K Q^T  (v_mfma_f32_16x16x4f32, hd/4 steps): lane l holds the
 //                scores of query l%16 for keys 4*(l/16) + i, i = 0..3;
@@ -193,18 +192,16 @@ __global__ __launch_bounds__(64) void k_attention(AttnArgs a) {
 // The scores of a whole tile (4 blocks) are formed first, so the online
 // softmax (fp32, per query: max and sum over the 4 lanes that share a
 // query, xor 16 / xor 32) and the rescaling of O happen once per 64 keys.
+// The softmax runs in base 2 (scores scaled by log2 e, weights from the
+// hardware exp2, within a few ulp of e^x).
 constexpr int kAttnWaves = 8;
-
-// e^x for the softmax weights (x <= 0): the hardware base-2 exponential of
-// x log2(e), within a few ulp; results below the f32 normal range are 0.
-__device__ __forceinline__ float exp_fast(float x) {
-  return __builtin_amdgcn_exp2f(x * 1.44269504088896341f);
-}
 constexpr int kQB = 16 * kAttnWaves;  // queries per workgroup
 constexpr int kKT = 64;               // keys per LDS tile
 
-template <int HD>
-__global__ __launch_bounds__(64 * kAttnWaves) void k_attn_mfma(AttnArgs a, int qblocks) {
+// two workgroups per CU (four waves per SIMD) up to head_dim 64
+template <int HD, bool SIG>
+__global__ __launch_bounds__(64 * kAttnWaves) __attribute__((amdgpu_waves_per_eu(HD <= 64 ? 4 : 2, 8)))
+void k_attn_mfma(AttnArgs a, int qblocks) {
   constexpr int ST = HD / 4;                            // QK MFMA steps
   constexpr int DT = HD / 16;                           // 16-wide head-dim tiles of O
   constexpr int ROW = HD + 4;                           // padded LDS row (floats)
@@ -223,24 +220,15 @@ __global__ __launch_bounds__(64 * kAttnWaves) void k_attn_mfma(AttnArgs a, int q
   const bool q_ok = s_q < a.seq;
   const int qp = b * a.seq + (q_ok ? s_q : a.seq - 1);
   const bool causal = a.mask == 1;
+  // score scales: softmax weights are 2^(s log2 e - max), in log2 units
+  const float scale_nat = (float)a.scale, scale_log2 = (float)(a.scale * 1.4426950408889634);
+  (void)scale_nat;
 
   float qr[ST];
   {
     const float* qrow = a.q + (size_t)qp * qd + (size_t)h * HD;
 #pragma unroll
     for (int st = 0; st < ST; ++st) qr[st] = qrow[4 * st + g];
-    if (a.rope) {
-      // the lane holds both members of its pairs (d, d + HD/2), d = 4 st + g
-      const double* tq = a.rope_tab + 2 * (size_t)qp * (HD / 2);
-#pragma unroll
-      for (int st = 0; st < ST / 2; ++st) {
-        const int d = 4 * st + g;
-        const double c = tq[2 * d], sn = tq[2 * d + 1];
-        const double a0 = qr[st], a1 = qr[st + ST / 2];
-        qr[st] = (float)(a0 * c - a1 * sn);
-        qr[st + ST / 2] = (float)(a0 * sn + a1 * c);
-      }
-    }
   }
   v4f o[DT];
 #pragma unroll
@@ -248,12 +236,12 @@ __global__ __launch_bounds__(64 * kAttnWaves) void k_attn_mfma(AttnArgs a, int q
   float m = -INFINITY, l = 0.0f;
 
   // K and V rows of a tile in pair units: unit i = tid + NT u covers row
-  // i / (HD/8) and the column quads c4 and c4 + HD/2, c4 = 4 (i % (HD/8)),
-  // so a thread holds both members of the RoPE pairs (d, d + HD/2) it
-  // rotates. Rows past `last` are exact zeros.
+  // i / (HD/8) and the column quads c4 and c4 + HD/2, c4 = 4 (i % (HD/8)).
+  // Rows past `last` are exact zeros (a tile wholly past it is a zero tile:
+  // the loads stay unconditional).
   constexpr int UNITS = kKT * HD / 8, PU = (UNITS + NT - 1) / NT;
   v4f kreg[2 * PU], vreg[2 * PU];
-  auto load_tile = [&](int t0) {
+  auto load_k = [&](int t0) {
 #pragma unroll
     for (int u = 0; u < PU; ++u) {
       const int i = tid + NT * u;
@@ -261,28 +249,29 @@ __global__ __launch_bounds__(64 * kAttnWaves) void k_attn_mfma(AttnArgs a, int q
       const int r = i / (HD / 8), c4 = (i % (HD / 8)) * 4;
       const int p = t0 + r, pc = p <= last ? p : last;
       const size_t off = (size_t)pc * kvd + (size_t)kvh * HD + c4;
-      v4f k0 = *reinterpret_cast<const v4f*>(a.k + off);
-      v4f k1 = *reinterpret_cast<const v4f*>(a.k + off + HD / 2);
-      const v4f v0 = *reinterpret_cast<const v4f*>(a.v + off);
-      const v4f v1 = *reinterpret_cast<const v4f*>(a.v + off + HD / 2);
-      if (a.rope) {
-        const double* tk = a.rope_tab + 2 * ((size_t)pc * (HD / 2) + c4);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const double c = tk[2 * e], sn = tk[2 * e + 1];
-          const double a0 = k0[e], a1 = k1[e];
-          k0[e] = (float)(a0 * c - a1 * sn);
-          k1[e] = (float)(a0 * sn + a1 * c);
-        }
-      }
+      const v4f k0 = *reinterpret_cast<const v4f*>(a.k + off);
+      const v4f k1 = *reinterpret_cast<const v4f*>(a.k + off + HD / 2);
       const v4f z = v4f{0.f, 0.f, 0.f, 0.f};
       kreg[2 * u] = p <= last ? k0 : z;
       kreg[2 * u + 1] = p <= last ? k1 : z;
+    }
+  };
+  auto load_v = [&](int t0) {
+#pragma unroll
+    for (int u = 0; u < PU; ++u) {
+      const int i = tid + NT * u;
+      if (UNITS % NT != 0 && i >= UNITS) break;
+      const int r = i / (HD / 8), c4 = (i % (HD / 8)) * 4;
+      const int p = t0 + r, pc = p <= last ? p : last;
+      const size_t off = (size_t)pc * kvd + (size_t)kvh * HD + c4;
+      const v4f v0 = *reinterpret_cast<const v4f*>(a.v + off);
+      const v4f v1 = *reinterpret_cast<const v4f*>(a.v + off + HD / 2);
+      const v4f z = v4f{0.f, 0.f, 0.f, 0.f};
       vreg[2 * u] = p <= last ? v0 : z;
       vreg[2 * u + 1] = p <= last ? v1 : z;
     }
   };
-  auto store_tile = [&](int buf) {
+  auto store_k = [&](int buf) {
 #pragma unroll
     for (int u = 0; u < PU; ++u) {
       const int i = tid + NT * u;
@@ -290,25 +279,20 @@ __global__ __launch_bounds__(64 * kAttnWaves) void k_attn_mfma(AttnArgs a, int q
       const int r = i / (HD / 8), c4 = (i % (HD / 8)) * 4;
       *reinterpret_cast<v4f*>(&ks[buf][r * ROW + c4]) = kreg[2 * u];
       *reinterpret_cast<v4f*>(&ks[buf][r * ROW + c4 + HD / 2]) = kreg[2 * u + 1];
+    }
+  };
+  auto store_v = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < PU; ++u) {
+      const int i = tid + NT * u;
+      if (UNITS % NT != 0 && i >= UNITS) break;
+      const int r = i / (HD / 8), c4 = (i % (HD / 8)) * 4;
       *reinterpret_cast<v4f*>(&vs[buf][r * ROW + c4]) = vreg[2 * u];
       *reinterpret_cast<v4f*>(&vs[buf][r * ROW + c4 + HD / 2]) = vreg[2 * u + 1];
     }
   };
-  load_tile(p_lo);
-  store_tile(0);
-  __syncthreads();
-
-#pragma unroll 1
-  for (int t0 = p_lo, cur = 0; t0 <= last; t0 += kKT, cur ^= 1) {
-    const bool more = t0 + kKT <= last;  // uniform
-    if (more) load_tile(t0 + kKT);
-    const float* kt = ks[cur];
-    const float* vt = vs[cur];
-    // multiplicity base of the tile start: floor(t0 / msl) + 1 (msl >= 64, so
-    // the tile crosses at most one multiple of msl)
-    const int base0 = t0 / a.msl + 1;
-    const int next_mult = base0 * a.msl;  // first p with a larger base
-    v4f sc[4];
+  // S^T of a tile: 4 blocks of 16 keys
+  auto scores = [&](const float* kt, v4f (&sc)[4]) {
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
       sc[kb] = v4f{0.f, 0.f, 0.f, 0.f};
@@ -317,41 +301,74 @@ __global__ __launch_bounds__(64 * kAttnWaves) void k_attn_mfma(AttnArgs a, int q
         sc[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kt[(16 * kb + c16) * ROW + 4 * st + g], qr[st],
                                                       sc[kb], 0, 0, 0);
     }
-    float w[16], smax = -INFINITY;
-    int cnt[16];
+  };
+
+  load_k(p_lo);
+  load_v(p_lo);
+  store_k(0);
+  store_v(0);
+  __syncthreads();
+
+  // tile i in buffer i & 1; the loads of tile i+1 are issued into registers
+  // before tile i's products and stored to the other buffer after them (it
+  // was last read before the previous barrier). All loads are unconditional
+  // (a tile past the range is a zero tile, stored but never read).
+#pragma unroll 1
+  for (int t0 = p_lo, cur = 0; t0 <= last; t0 += kKT, cur ^= 1) {
+    load_k(t0 + kKT);
+    load_v(t0 + kKT);
+    v4f sc[4];
+    scores(ks[cur], sc);
+    const float* vt = vs[cur];
+    // multiplicity base of the tile start: floor(t0 / msl) + 1 (msl >= 64, so
+    // the tile crosses at most one multiple of msl)
+    const int base0 = t0 / a.msl + 1;
+    const int next_mult = base0 * a.msl;  // first p with a larger base
+    // multiplicity of the row of key k (block kb, lane key i) for this query
+    const float base0f = (float)base0;
+    auto mult = [&](int kb, int i) {
+      const int p = t0 + 16 * kb + 4 * g + i;
+      const float c = p <= last ? base0f + (p >= next_mult ? 1.0f : 0.0f) : 0.0f;
+      return c - (causal && p > qp ? 1.0f : 0.0f);
+    };
+    float w[16];
+    if constexpr (SIG) {
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
+      for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int p = t0 + 16 * kb + 4 * g + i;
-        int c = p <= last ? base0 + (p >= next_mult ? 1 : 0) : 0;
-        if (causal && p > qp) c -= 1;
-        cnt[4 * kb + i] = c;
-        w[4 * kb + i] = (float)((double)sc[kb][i] * a.scale);
-        if (c > 0) smax = fmaxf(smax, w[4 * kb + i]);
-      }
-    if (a.sigmoid) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) w[i] = cnt[i] > 0 ? (float)cnt[i] / (1.0f + expf(-w[i])) : 0.0f;
+        for (int i = 0; i < 4; ++i) {
+          const float c = mult(kb, i);
+          w[4 * kb + i] = c > 0.0f ? c / (1.0f + expf(-sc[kb][i] * scale_nat)) : 0.0f;
+        }
     } else {
+      // base-2 scores with the multiplicity folded into the exponent
+      // (c 2^x = 2^(x + log2 c)); masked keys at -inf
+      float smax = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float c = mult(kb, i);
+          w[4 * kb + i] = c > 0.0f ? sc[kb][i] * scale_log2 + __builtin_amdgcn_logf(c) : -INFINITY;
+          smax = fmaxf(smax, w[4 * kb + i]);
+        }
       smax = fmaxf(smax, __shfl_xor(smax, 16, 64));
       smax = fmaxf(smax, __shfl_xor(smax, 32, 64));
       const float nm = fmaxf(m, smax);
-      const float corr = (m == -INFINITY) ? 0.0f : exp_fast(m - nm);
+      const float nz = nm == -INFINITY ? 0.0f : nm;  // all masked so far: weights 0
+      const float corr = __builtin_amdgcn_exp2f(m - nz);  // m = -inf: 0
       float ws = 0.0f;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        w[i] = cnt[i] > 0 ? (float)cnt[i] * exp_fast(w[i] - nm) : 0.0f;
+        w[i] = __builtin_amdgcn_exp2f(w[i] - nz);
         ws += w[i];
       }
       ws += __shfl_xor(ws, 16, 64);
       ws += __shfl_xor(ws, 32, 64);
-      if (nm != -INFINITY) {
-        l = l * corr + ws;
+      l = l * corr + ws;
 #pragma unroll
-        for (int d = 0; d < DT; ++d) o[d] *= corr;
-        m = nm;
-      }
+      for (int d = 0; d < DT; ++d) o[d] *= corr;
+      m = nm;
     }
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
@@ -361,13 +378,13 @@ __global__ __launch_bounds__(64 * kAttnWaves) void k_attn_mfma(AttnArgs a, int q
         for (int d = 0; d < DT; ++d)
           o[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(vt[(16 * kb + 4 * g + j) * ROW + d * 16 + c16],
                                                       w[4 * kb + j], o[d], 0, 0, 0);
-    // the other buffer was last read before the previous barrier
-    if (more) store_tile(cur ^ 1);
+    store_k(cur ^ 1);
+    store_v(cur ^ 1);
     __syncthreads();
   }
   if (!q_ok) return;
   // o[d]: lane holds query c16, head dims d*16 + 4g + i
-  const float inv = a.sigmoid ? 1.0f : (l > 0.0f ? 1.0f / l : 0.0f);
+  const float inv = SIG ? 1.0f : (l > 0.0f ? 1.0f / l : 0.0f);
   float* out = a.out + (size_t)qp * qd + (size_t)h * HD;
 #pragma unroll
   for (int d = 0; d < DT; ++d) {
@@ -389,11 +406,11 @@ Status launch_attention(const AttnArgs& a, hipStream_t st) {
   if (a.hd > 64 * kMaxHdPerLane || a.hd % 4 != 0)
     return Status::err(kUnsupported, "attention: head_dim must be a multiple of 4 and <= 256");
   // the tile multiplicity update assumes at most one multiple of msl per
-  // 64-key tile, hence msl >= 64; RoPE is applied inside (table required)
+  // 64-key tile, hence msl >= 64
   const bool fast = (a.mask == 1 || a.mask == 2) && !a.alibi && a.msl >= kKT &&
                     a.msl >= a.seq && (a.hd == 32 || a.hd == 64 || a.hd == 128) &&
-                    a.seq > 0 && a.tokens % a.seq == 0 && (!a.rope || a.rope_tab);
-  if (a.rope && !fast) {
+                    a.seq > 0 && a.tokens % a.seq == 0;
+  if (a.rope) {
     k_rope<<<a.tokens, 256, 0, st>>>(const_cast<float*>(a.q), const_cast<float*>(a.k), a.tokens,
                                      a.heads, a.kv_heads, a.hd, a.rope_theta, a.rope_tab);
     WV_HIP(hipGetLastError());
@@ -401,10 +418,20 @@ Status launch_attention(const AttnArgs& a, hipStream_t st) {
   if (fast) {
     const int qblocks = (a.seq + kQB - 1) / kQB;
     dim3 grid((unsigned)(a.tokens / a.seq * qblocks), (unsigned)a.heads);
+    const dim3 blk(64 * kAttnWaves);
     switch (a.hd) {
-    case 32: k_attn_mfma<32><<<grid, 64 * kAttnWaves, 0, st>>>(a, qblocks); break;
-    case 64: k_attn_mfma<64><<<grid, 64 * kAttnWaves, 0, st>>>(a, qblocks); break;
-    default: k_attn_mfma<128><<<grid, 64 * kAttnWaves, 0, st>>>(a, qblocks); break;
+    case 32:
+      if (a.sigmoid) k_attn_mfma<32, true><<<grid, blk, 0, st>>>(a, qblocks);
+      else k_attn_mfma<32, false><<<grid, blk, 0, st>>>(a, qblocks);
+      break;
+    case 64:
+      if (a.sigmoid) k_attn_mfma<64, true><<<grid, blk, 0, st>>>(a, qblocks);
+      else k_attn_mfma<64, false><<<grid, blk, 0, st>>>(a, qblocks);
+      break;
+    default:
+      if (a.sigmoid) k_attn_mfma<128, true><<<grid, blk, 0, st>>>(a, qblocks);
+      else k_attn_mfma<128, false><<<grid, blk, 0, st>>>(a, qblocks);
+      break;
     }
     return hip_status(hipGetLastError(), "attention launch");
   }
