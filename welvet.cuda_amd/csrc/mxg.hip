@@ -421,11 +421,12 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
     for (int i = 0; i < 2; ++i) {
       const int s = s0 + i, cur = i;
       {
-        // Weight fragments in groups of HB blocks (register budget; 4 for
-        // FP8 wide tiles, whose fragments take 8 registers): the first group
+        // Weight fragments in groups of HB = 4 blocks: the first group
         // before the next step's loads are issued, the others after the
-        // previous group's MFMAs.
-        constexpr int HB = SN < 8 ? SN : (SN == 16 && !FP4) ? 4 : 8;
+        // previous group's MFMAs, so the MFMAs start after 4 fragment reads
+        // rather than after the whole tile (every wave reads the tile right
+        // after the barrier). Measured: groups of 8 and of 2 are slower.
+        constexpr int HB = SN < 4 ? SN : 4;
         v8i bf[HB];
         int bsc[HB];
         auto read_b = [&](int c0) {
