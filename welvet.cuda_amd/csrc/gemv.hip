@@ -374,6 +374,9 @@ GemvTile gemv_tile(int dtype, int kpad, int rows, int mats, int cus) {
   const int chunks = (kpad + 64 * ks - 1) / (64 * ks);
   GemvTile t;
   t.waves = chunks <= 4 ? chunks : chunks <= 6 ? 6 : chunks <= 8 ? 8 : 4;
+  // FP4 with 5-6 chunks (the 11008-wide SwiGLU down projection): 3 waves of
+  // two chunks each measured 7.8 us against 8.5 us for 6 waves of one
+  if (dtype == kFP4 && (chunks == 5 || chunks == 6)) t.waves = 3;
   if (t.waves == 3 || t.waves >= 6) {
     t.rows = 8;
     return t;
