@@ -17,6 +17,7 @@ namespace wv {
 namespace {
 
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 __device__ __forceinline__ bool allow(int qp, int kp, const AttnArgs& a) {
   if (a.mask == 2) return true;
@@ -207,7 +208,9 @@ void k_attn_mfma(AttnArgs a, int qblocks) {
   constexpr int ROW = HD + 4;                           // padded LDS row (floats)
   constexpr int NT = 64 * kAttnWaves;                   // threads
   __shared__ float ks[2][kKT * ROW];
-  __shared__ float vs[2][kKT * ROW];
+  // V in bf16 operand order: [32-key group q][head-dim tile dt][hi, lo][lane][8]
+  constexpr int VBYTES = 2 * DT * 2 * 1024;
+  __shared__ __attribute__((aligned(16))) uint8_t vsb[2][VBYTES];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c16 = lane & 15, g = lane >> 4;
   const int b = blockIdx.x / qblocks, qb = blockIdx.x % qblocks;
@@ -281,14 +284,30 @@ void k_attn_mfma(AttnArgs a, int qblocks) {
       *reinterpret_cast<v4f*>(&ks[buf][r * ROW + c4 + HD / 2]) = kreg[2 * u + 1];
     }
   };
+  // V row r (key) and head dim d go to the bf16 A operand of the P V
+  // products: 32-key group q = r / 32, and within it the lane group g and
+  // element j that also hold that key's weight in the score layout (key
+  // 16 kb + 4 g + i of the group <-> g, j = 4 kb + i); lane 16 g + d % 16 of
+  // head-dim tile d / 16. Each value is stored as bf16 hi and lo = v - hi.
   auto store_v = [&](int buf) {
 #pragma unroll
     for (int u = 0; u < PU; ++u) {
       const int i = tid + NT * u;
       if (UNITS % NT != 0 && i >= UNITS) break;
       const int r = i / (HD / 8), c4 = (i % (HD / 8)) * 4;
-      *reinterpret_cast<v4f*>(&vs[buf][r * ROW + c4]) = vreg[2 * u];
-      *reinterpret_cast<v4f*>(&vs[buf][r * ROW + c4 + HD / 2]) = vreg[2 * u + 1];
+      const int q = r >> 5, rr = r & 31;
+      const int gk = (rr >> 2) & 3, j = 4 * (rr >> 4) + (rr & 3);
+#pragma unroll
+      for (int half = 0; half < 2; ++half)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int d = c4 + e + half * (HD / 2);
+          const float v = vreg[2 * u + half][e];
+          const __bf16 hi = (__bf16)v, lo = (__bf16)(v - (float)hi);
+          uint8_t* dst = vsb[buf] + (size_t)((q * DT + (d >> 4)) * 2) * 1024 + (gk * 16 + (d & 15)) * 16 + j * 2;
+          *reinterpret_cast<__bf16*>(dst) = hi;
+          *reinterpret_cast<__bf16*>(dst + 1024) = lo;
+        }
     }
   };
   // S^T of a tile: 4 blocks of 16 keys
@@ -319,7 +338,7 @@ void k_attn_mfma(AttnArgs a, int qblocks) {
     load_v(t0 + kKT);
     v4f sc[4];
     scores(ks[cur], sc);
-    const float* vt = vs[cur];
+    const uint8_t* vt = vsb[cur];
     // multiplicity base of the tile start: floor(t0 / msl) + 1 (msl >= 64, so
     // the tile crosses at most one multiple of msl)
     const int base0 = t0 / a.msl + 1;
@@ -370,14 +389,31 @@ void k_attn_mfma(AttnArgs a, int qblocks) {
       for (int d = 0; d < DT; ++d) o[d] *= corr;
       m = nm;
     }
+    // O^T += V^T P^T on the bf16 matrix cores, 32 keys per product, each
+    // operand split into bf16 hi + lo: hi*hi + hi*lo + lo*hi (the dropped
+    // lo*lo term and the split leave ~2^-16 relative error per product).
+    // Lane (query c16, group g) passes the weights it already holds: element
+    // j of group g is key 16 (2q + j / 4) + 4g + j % 4 of the tile.
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
+    for (int q = 0; q < 2; ++q) {
+      bf16x8 ph, pl;
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < 8; ++j) {
+        const float wv = w[4 * (2 * q + (j >> 2)) + (j & 3)];
+        const __bf16 h = (__bf16)wv;
+        ph[j] = h;
+        pl[j] = (__bf16)(wv - (float)h);
+      }
 #pragma unroll
-        for (int d = 0; d < DT; ++d)
-          o[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(vt[(16 * kb + 4 * g + j) * ROW + d * 16 + c16],
-                                                      w[4 * kb + j], o[d], 0, 0, 0);
+      for (int d = 0; d < DT; ++d) {
+        const uint8_t* vb = vt + (size_t)((q * DT + d) * 2) * 1024 + lane * 16;
+        const bf16x8 vh = *reinterpret_cast<const bf16x8*>(vb);
+        const bf16x8 vl = *reinterpret_cast<const bf16x8*>(vb + 1024);
+        o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, ph, o[d], 0, 0, 0);
+        o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, pl, o[d], 0, 0, 0);
+        o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vl, ph, o[d], 0, 0, 0);
+      }
+    }
     store_k(cur ^ 1);
     store_v(cur ^ 1);
     __syncthreads();
