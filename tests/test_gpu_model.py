@@ -100,3 +100,19 @@ def test_c1_volume_single_dense_cell(gpu, oracle):
     y = m.forward(x)
     assert rel_l2(y, oracle_chain(oracle, layers[0], x, scheme=1)) <= 1e-5
     m.close()
+
+
+def test_repeated_forwards_reuse_device_buffers(gpu, oracle):
+    """A model keeps its pass buffers and workspace between forwards: batches
+    that take every path (GEMV 1, small-batch matrix cores 3, K-split 16,
+    large tiles 40), in an order that grows and shrinks them, all match."""
+    rng = np.random.default_rng(9)
+    layers = [(dt, (rng.standard_normal((256, 256)) / 16).astype(np.float32), act)
+              for dt, act in ((4, -1), (16, 1), (5, -1))]
+    m = pw.ModelSession(build_stack([layers]), scheme=2)
+    for batch in (1, 3, 16, 40, 3, 40, 1):
+        x = rng.standard_normal((batch, 256)).astype(np.float32)
+        y = m.forward(x)
+        assert y.shape == (batch, 256)
+        assert rel_l2(y, oracle_chain(oracle, layers, x, scheme=2)) <= tol(batch, chain=3), batch
+    m.close()

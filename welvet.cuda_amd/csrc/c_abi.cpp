@@ -546,13 +546,13 @@ welvet_status welvet_model_forward(welvet_model_session* s, const uint8_t* input
     if ((size - off) / 4 < n) return Status::err(wv::kInvalid, "short tensor data");
     if (size - off != n * 4) return Status::err(wv::kInvalid, "trailing descriptor bytes");
     hipStream_t st = s->stream.s;
-    wv::DevBuf dx, dy;
-    WV_TRY(dx.alloc(n * 4));
+    // the input buffer and the pass's buffers are kept by the model
+    wv::DevBuf& dx = s->model.scratch.in;
+    if (dx.bytes < n * 4) WV_TRY(dx.alloc(n * 4));
     WV_HIP(hipMemcpyAsync(dx.p, input + off, n * 4, hipMemcpyHostToDevice, st));
-    const size_t cap = size_t(1) << 26;
-    WV_TRY(dy.alloc(cap * 4));
     std::vector<int> oshape;
-    WV_TRY(wv::model_forward(s->model, shape, dx.as<float>(), &oshape, dy.as<float>(), cap, st));
+    const float* dy = nullptr;
+    WV_TRY(wv::model_forward_view(s->model, shape, dx.as<float>(), &oshape, &dy, st));
     size_t on = 1;
     for (int d : oshape) on *= (size_t)d;
     std::vector<uint8_t> blob;
@@ -570,7 +570,7 @@ welvet_status welvet_model_forward(welvet_model_session* s, const uint8_t* input
     put(&cnt, 4);
     const size_t hdr = blob.size();
     blob.resize(hdr + on * 4);
-    WV_HIP(hipMemcpyAsync(blob.data() + hdr, dy.p, on * 4, hipMemcpyDeviceToHost, st));
+    WV_HIP(hipMemcpyAsync(blob.data() + hdr, dy, on * 4, hipMemcpyDeviceToHost, st));
     WV_HIP(hipStreamSynchronize(st));
     out->data = static_cast<uint8_t*>(std::malloc(blob.size()));
     if (!out->data) return Status::err(wv::kInternal, "out of host memory");

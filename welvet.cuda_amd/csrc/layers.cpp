@@ -470,11 +470,17 @@ static bool mha_rope(const MHAConfig& c) { return (c.pos == 0 || c.pos == 3) && 
 // The RoPE table covers token positions [0, T); built once (mount) and
 // reused, so a forward of at most T tokens queues no trigonometry.
 static Status ensure_rope_table(const MHALayer& L, int T, Workspace* ws, hipStream_t st) {
-  if (!mha_rope(L.cfg) || ws->rope_tokens >= T) return Status::ok();
+  if (!mha_rope(L.cfg)) return Status::ok();
+  // a workspace shared by MHA layers of different head_dim or theta (a model
+  // session) rebuilds the table when the layer differs
+  if (ws->rope_tokens >= T && ws->rope_hd == L.cfg.head_dim && ws->rope_theta == L.cfg.rope_theta)
+    return Status::ok();
   WV_TRY(ws->c.alloc((size_t)T * (L.cfg.head_dim / 2) * 2 * sizeof(double)));
   WV_TRY(build_rope_table(ws->c.as<double>(), T, L.cfg.head_dim, L.cfg.rope_theta, st));
   WV_HIP(hipStreamSynchronize(st));
   ws->rope_tokens = T;
+  ws->rope_hd = L.cfg.head_dim;
+  ws->rope_theta = L.cfg.rope_theta;
   return Status::ok();
 }
 

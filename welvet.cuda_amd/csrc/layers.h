@@ -29,9 +29,10 @@ Status check_dtype_scheme(int dtype, int scheme);
 struct Workspace {
   DevBuf a;  // quantized activations / intermediates
   DevBuf b;
-  DevBuf c;  // MHA: RoPE (cos, sin) table for rope_tokens tokens
+  DevBuf c;  // MHA: RoPE (cos, sin) table for rope_tokens tokens of rope_hd, rope_theta
   DevBuf d;
-  int rope_tokens = 0;
+  int rope_tokens = 0, rope_hd = 0;
+  double rope_theta = 0.0;
 };
 
 struct DenseLayer {

@@ -295,13 +295,14 @@ struct Tensor {
   }
 };
 
-// Device arena for a forward pass.
+// Op outputs from the model's scratch, in op order (reused pass after pass).
 struct Arena {
-  std::vector<DevBuf> bufs;
+  ModelScratch& sc;
   float* get(size_t n) {
-    bufs.emplace_back();
-    good(bufs.back().alloc(n * sizeof(float)));
-    return bufs.back().as<float>();
+    if (sc.next == sc.bufs.size()) sc.bufs.emplace_back();
+    DevBuf& b = sc.bufs[sc.next++];
+    if (b.bytes < n * sizeof(float)) good(b.alloc(n * sizeof(float)));
+    return b.as<float>();
   }
 };
 
@@ -423,11 +424,12 @@ Status model_build(Model* m, hipStream_t st) {
   }
 }
 
-Status model_forward(Model& m, const std::vector<int>& in_shape, const float* x,
-                     std::vector<int>* out_shape, float* y, size_t y_cap, hipStream_t st) {
+Status model_forward_view(Model& m, const std::vector<int>& in_shape, const float* x,
+                          std::vector<int>* out_shape, const float** y, hipStream_t st) {
   try {
-    Arena ar;
-    Workspace ws;
+    m.scratch.next = 0;
+    Arena ar{m.scratch};
+    Workspace& ws = m.scratch.ws;
     Tensor in;
     in.shape = in_shape;
     in.data = const_cast<float*>(x);
@@ -465,9 +467,7 @@ Status model_forward(Model& m, const std::vector<int>& in_shape, const float* x,
       out = cur;
     }
     *out_shape = out.shape;
-    const size_t n = out.numel();
-    if (n > y_cap) return Status::err(kInvalid, "model forward: output buffer too small");
-    WV_HIP(hipMemcpyAsync(y, out.data, n * sizeof(float), hipMemcpyDeviceToDevice, st));
+    *y = out.data;
     WV_HIP(hipStreamSynchronize(st));
     return Status::ok();
   } catch (const StatusError& e) {
@@ -477,6 +477,18 @@ Status model_forward(Model& m, const std::vector<int>& in_shape, const float* x,
   } catch (const std::exception& e) {
     return Status::err(kInternal, e.what());
   }
+}
+
+Status model_forward(Model& m, const std::vector<int>& in_shape, const float* x,
+                     std::vector<int>* out_shape, float* y, size_t y_cap, hipStream_t st) {
+  const float* out = nullptr;
+  WV_TRY(model_forward_view(m, in_shape, x, out_shape, &out, st));
+  size_t n = 1;
+  for (int d : *out_shape) n *= (size_t)d;
+  if (n > y_cap) return Status::err(kInvalid, "model forward: output buffer too small");
+  WV_HIP(hipMemcpyAsync(y, out, n * sizeof(float), hipMemcpyDeviceToDevice, st));
+  WV_HIP(hipStreamSynchronize(st));
+  return Status::ok();
 }
 
 namespace {

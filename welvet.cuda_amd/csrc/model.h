@@ -34,12 +34,25 @@ struct GridCell {
   int enabled = 0, remote = 0, tz = 0, ty = 0, tx = 0, tl = 0;
 };
 
+// Device memory a forward pass uses, kept across passes: the op outputs are
+// taken from `bufs` in op order (the same sizes pass after pass, so a steady
+// state allocates nothing), `ws` holds the split and K-split buffers, `in`
+// the uploaded input of a host-buffer call. Calls on one model must not
+// overlap (the session serializes them).
+struct ModelScratch {
+  std::vector<DevBuf> bufs;
+  size_t next = 0;
+  Workspace ws;
+  DevBuf in;
+};
+
 struct Model {
   int root = 0;  // 0 Stack, 2 Grid
   int dims[4] = {1, 1, 1, 1};
   std::vector<ModelNode> children;  // Stack children or Grid cells in hop order
   std::vector<GridCell> cells;
   int scheme = 0;
+  ModelScratch scratch;
 };
 
 // Parses and validates a WMN1 descriptor (src/interop/model_session.cpp:
@@ -55,6 +68,10 @@ Status model_build(Model* m, hipStream_t st);
 // stack/stack.cpp:470-494 for Stack.)
 Status model_forward(Model& m, const std::vector<int>& in_shape, const float* x,
                      std::vector<int>* out_shape, float* y, size_t y_cap, hipStream_t st);
+// The same pass, leaving the output in the model's scratch: *out points to
+// it until the next pass on this model. Returns after the stream is idle.
+Status model_forward_view(Model& m, const std::vector<int>& in_shape, const float* x,
+                          std::vector<int>* out_shape, const float** out, hipStream_t st);
 
 // NWS1 snapshot of all stores (model_session.cpp:523-550).
 Status model_export(const Model& m, std::vector<uint8_t>* out);
