@@ -929,54 +929,50 @@ __global__ __launch_bounds__(64 * kSmallWaves) __attribute__((amdgpu_waves_per_e
 }
 
 // Adds the K-split partial sums of k_mxs (in split order) and applies the
-// epilogue; one thread per 4 consecutive outputs, the partial loads of 8
-// splits in flight at a time.
+// epilogue; one thread per output, the partial loads of up to 16 splits in
+// flight at a time (consecutive threads read consecutive floats of a plane).
 template <int MATS>
 __global__ __launch_bounds__(kThreads) void k_mxs_reduce(MxgArgs p, int ksplit, int rows) {
-  const int n4 = (p.N + 3) / 4;
   const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  if (i >= (int64_t)p.M * n4) return;
-  const int mrow = (int)(i / n4), nb = (int)(i % n4) * 4;
+  if (i >= (int64_t)p.M * p.N) return;
+  const int mrow = (int)(i / p.N), n = (int)(i % p.N);
   const size_t npad = ((size_t)p.N + rows - 1) / rows * rows;
-  v4f tot[MATS];
+  const size_t plane = (size_t)p.mpad * npad;  // one (split, matrix) plane
+  const float* src = p.part + (size_t)mrow * npad + n;
+  float tot[MATS];
 #pragma unroll
-  for (int m = 0; m < MATS; ++m) tot[m] = v4f{0.f, 0.f, 0.f, 0.f};
+  for (int m = 0; m < MATS; ++m) tot[m] = 0.0f;
 #pragma unroll 1
-  for (int k2 = 0; k2 < ksplit; k2 += 8) {
-    v4f t[MATS][8];
+  for (int k0 = 0; k0 < ksplit; k0 += 16) {
+    float t[MATS][16];
 #pragma unroll
-    for (int m = 0; m < MATS; ++m)
+    for (int u = 0; u < 16; ++u) {
+      const int kk = k0 + u < ksplit ? k0 + u : ksplit - 1;
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int kk = k2 + u < ksplit ? k2 + u : ksplit - 1;
-        t[m][u] = *reinterpret_cast<const v4f*>(p.part + (((size_t)kk * MATS + m) * p.mpad + mrow) * npad + nb);
-      }
+      for (int m = 0; m < MATS; ++m) t[m][u] = src[((size_t)kk * MATS + m) * plane];
+    }
 #pragma unroll
-    for (int m = 0; m < MATS; ++m)
+    for (int u = 0; u < 16; ++u)
 #pragma unroll
-      for (int u = 0; u < 8; ++u) tot[m] += k2 + u < ksplit ? t[m][u] : v4f{0.f, 0.f, 0.f, 0.f};
+      for (int m = 0; m < MATS; ++m) tot[m] += k0 + u < ksplit ? t[m][u] : 0.0f;
   }
-#pragma unroll 1
-  for (int r = 0; r < 4 && nb + r < p.N; ++r) {
-    const int n = nb + r;
-    const size_t oi = (size_t)mrow * p.out_stride + n;
-    if constexpr (MATS == 2) {
-      const float gs = (float)act_f64(kSilu, (double)(tot[0][r] * p.scale[0][n]));
-      p.pre[oi] = (float)((double)gs * (double)(tot[1][r] * p.scale[1][n]));
-    } else {
-      float y = tot[0][r] * p.scale[0][n];
-      if (p.need_epi) {
-        double v = (double)y;
-        if (p.bias && n < p.bias_len) {
-          v += p.bias[n];
-          y = (float)v;
-        }
-        p.pre[oi] = y;
-        p.post[oi] = (float)act_f64(p.act, v);
-      } else {
-        p.pre[oi] = y;
-        if (p.post && p.post != p.pre) p.post[oi] = y;
+  const size_t oi = (size_t)mrow * p.out_stride + n;
+  if constexpr (MATS == 2) {
+    const float gs = (float)act_f64(kSilu, (double)(tot[0] * p.scale[0][n]));
+    p.pre[oi] = (float)((double)gs * (double)(tot[1] * p.scale[1][n]));
+  } else {
+    float y = tot[0] * p.scale[0][n];
+    if (p.need_epi) {
+      double v = (double)y;
+      if (p.bias && n < p.bias_len) {
+        v += p.bias[n];
+        y = (float)v;
       }
+      p.pre[oi] = y;
+      p.post[oi] = (float)act_f64(p.act, v);
+    } else {
+      p.pre[oi] = y;
+      if (p.post && p.post != p.pre) p.post[oi] = y;
     }
   }
 }
@@ -1018,7 +1014,7 @@ Status launch_small(const MxgArgs& p, hipStream_t st) {
   if (ksplit > 1) {
     // the kernel boundary makes every split's partial sums visible (the
     // XCDs' L2 caches are not coherent with each other)
-    const int64_t n = (int64_t)p.M * ((p.N + 3) / 4);
+    const int64_t n = (int64_t)p.M * p.N;
     k_mxs_reduce<MATS><<<(unsigned)((n + kThreads - 1) / kThreads), kThreads, 0, st>>>(
         p, ksplit, 16 * kSmallWaves * rb);
   }
