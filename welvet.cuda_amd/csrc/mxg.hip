@@ -1076,6 +1076,7 @@ size_t split_bytes(int M, int kpad) {
 
 Status launch_split(const float* x, int x_stride, int M, int cols, int kpad, uint8_t* buf,
                     hipStream_t st) {
+  if (kpad % 128 != 0) return Status::err(kInvalid, "split: kpad must be a multiple of 128");
   const int mpad = (int)round_up(M, mxg_block_m(M));
   uint8_t* a = buf;
   uint8_t* as = buf + (size_t)kTerms * mpad * kpad;
@@ -1090,6 +1091,7 @@ Status launch_split(const float* x, int x_stride, int M, int cols, int kpad, uin
 Status launch_split_group(const SplitJob* jobs, int n, bool vec, int x_stride, int M, int cols,
                           int kpad, hipStream_t st) {
   if (n <= 0 || !jobs) return Status::err(kInvalid, "split group: no members");
+  if (kpad % 128 != 0) return Status::err(kInvalid, "split: kpad must be a multiple of 128");
   const int mpad = (int)round_up(M, mxg_block_m(M));
   const int64_t waves = (int64_t)(mpad / 16) * (kpad / 128);
   const dim3 grid((unsigned)((waves + kThreads / 64 - 1) / (kThreads / 64)), (unsigned)n);
