@@ -7,9 +7,13 @@
 //   p == k_pos (mod msl): p = last - ((last - k_pos) mod msl);
 //   RoPE rotates Q and K at their global position (:487-504), ALiBi uses
 //   k_pos (:526-533); softmax or sigmoid over the allowed keys (:603-619).
-// The reference loop is serial f64 on one thread; here one wave handles one
+// The reference loop is serial f64 on one thread. Here the causal and
+// bidirectional masks without ALiBi run on the matrix cores (k_attn_mfma,
+// below); the other masks take k_attention, where one wave handles one
 // (token, head), keys are scored 64 at a time (one per lane), and the
-// softmax is accumulated online in fp32.
+// softmax is accumulated online in fp32. RoPE is applied by the Q and K
+// projections' GEMM epilogue when they run on the large tiles, else by
+// k_rope before either kernel.
 #include "common.h"
 #include "kernels.h"
 
@@ -223,9 +227,10 @@ void k_attn_mfma(AttnArgs a, int qblocks) {
   const bool q_ok = s_q < a.seq;
   const int qp = b * a.seq + (q_ok ? s_q : a.seq - 1);
   const bool causal = a.mask == 1;
-  // score scales: softmax weights are 2^(s log2 e - max), in log2 units
-  const float scale_nat = (float)a.scale, scale_log2 = (float)(a.scale * 1.4426950408889634);
-  (void)scale_nat;
+  // score scales: softmax weights are 2^(s log2 e - max), in log2 units;
+  // the sigmoid variant works in natural units
+  const float scale_log2 = (float)(a.scale * 1.4426950408889634);
+  const float scale_nat = (float)a.scale;
 
   float qr[ST];
   {
