@@ -33,6 +33,8 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "welvet.cuda_amd"))
 
 HBM_PEAK_GBS = 8000.0
+REPEATS = 3  # timed regions per run; the median is reported
+WARMUP_S = 0.2  # default warmup: at least this long (seconds) of replays
 # dense MFMA peak of the f8f6f4 instruction with an FP8 operand (the activation
 # terms are E4M3, so FP4 weights run at the FP8 rate)
 MFMA_FP8_PEAK_TFLOPS = 5000.0
@@ -344,7 +346,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None,
                     help="timed steps (default: 1280 for the GEMV workloads, fewer for the rest)")
-    ap.add_argument("--warmup", type=int, default=None)
+    ap.add_argument("--warmup", type=int, default=None,
+                    help="untimed warmup steps (default: graph replays for at least WARMUP_S seconds)")
     ap.add_argument("--config", default="c2", choices=CONFIGS)
     ap.add_argument("--copies", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true")
@@ -370,7 +373,9 @@ def main():
     wl = make_workload(pw, hip, args.config, max(1, args.copies))
     gemv = args.config in ("c1", "c2", "c3", "c3b16")
     steps = args.steps if args.steps is not None else (1280 if gemv else 64)
-    warmup = args.warmup if args.warmup is not None else (128 if gemv else 8)
+    # default warmup: replays until at least WARMUP_S of GPU time has passed,
+    # so the clocks have left their idle level (reported as the step count)
+    warmup = args.warmup
     per = max(1, min(wl["per_graph"], steps))
     stream = hip.stream()
 
@@ -383,20 +388,35 @@ def main():
     full, rem = divmod(steps, per)
     g_full = hip.capture(stream, enqueue(per))
     g_rem = hip.capture(stream, enqueue(rem)) if rem else None
-    for _ in range(max(1, (warmup + per - 1) // per)):
-        hip.launch(g_full, stream)
+    if warmup is not None:
+        for _ in range(max(1, (warmup + per - 1) // per)):
+            hip.launch(g_full, stream)
+        hip.sync()
+    else:
+        warmup, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < WARMUP_S or warmup < steps:
+            hip.launch(g_full, stream)
+            hip.sync()
+            warmup += per
     hip.sync()
+    # The timed region (exactly `steps` steps between device synchronizations)
+    # runs REPEATS times; the median is reported, so one disturbed run does not
+    # become the result (the three times are in config.ms_runs).
     e0, e1 = hip.event(), hip.event()
+    runs = []
     t_wall = time.perf_counter()
-    hip.record(e0, stream)
-    for _ in range(full):
-        hip.launch(g_full, stream)
-    if g_rem:
-        hip.launch(g_rem, stream)
-    hip.record(e1, stream)
-    hip.sync()
-    t_wall = time.perf_counter() - t_wall
-    ms = hip.elapsed_ms(e0, e1)
+    for _ in range(REPEATS):
+        hip.sync()
+        hip.record(e0, stream)
+        for _ in range(full):
+            hip.launch(g_full, stream)
+        if g_rem:
+            hip.launch(g_rem, stream)
+        hip.record(e1, stream)
+        hip.sync()
+        runs.append(hip.elapsed_ms(e0, e1))
+    t_wall = (time.perf_counter() - t_wall) / REPEATS
+    ms = sorted(runs)[len(runs) // 2]
     per_step_s = ms * 1e-3 / steps
 
     tflops = wl["flops"] / per_step_s / 1e12
@@ -412,7 +432,8 @@ def main():
                 "traffic": measured_traffic(args.config)}
     cpu = None if (args.no_cpu or wl["cpu"] is None) else wl["cpu"](10.0)
     config = dict(wl["config"])
-    config.update({"tflops": round(tflops, 4), "wall_s": round(t_wall, 4)})
+    config.update({"tflops": round(tflops, 4), "wall_s": round(t_wall, 4),
+                   "ms_runs": [round(r, 4) for r in runs], "timed_regions": REPEATS})
     if wl["bytes"]:
         config.update({"algorithmic_bytes_per_step": wl["bytes"], "gbs": round(gbs, 2)})
     line = {
