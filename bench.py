@@ -19,6 +19,7 @@ Other workloads (--config), each its own line:
   c4     MHA projection GEMM: 4096 tokens x 1024 -> 1024, E5M2 per-row scales
   c4mha  whole MHA layer: B=8, S=512, d=1024, 16 heads x 64, causal, RoPE
   c5     64 cells x (Dense 1024^2 E4M3 row -> FP4 block-32 -> E4M3 row), batch 256
+  c5chain  the same cells as the reference's volume: one 192-layer serial chain (model session)
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2]
 """
@@ -296,6 +297,60 @@ def cells_workload(pw, hip, name):
             "cpu": cpu, "close": close}
 
 
+def chain_workload(pw, hip, name):
+    """The reference's volume semantics for the C5 cells: a WMN1 Grid 4x4x4 of
+    Stack cells (E4M3 / FP4 / E4M3 Dense 1024^2 each), run as one 192-layer
+    serial chain by welvet_model_forward_device (runtime/forward.cpp:98-156).
+    One model session has one scale scheme: E8M0 per 32 for all layers."""
+    import numpy as np
+
+    cells, batch, d = 64, 256, 1024
+    kinds = [4, 16, 4]
+    w = pw.Wire()
+    w.u32(0x314E4D57)
+    w.i32(2, cells, 4, 4, 4, 1)
+    for c in range(cells):
+        seed = pw.seed_for(5, c)
+        w.i32(19, len(kinds))
+        for li, dt in enumerate(kinds):
+            W = pw.normal(seed + 10 * li, d * d, 1 / np.sqrt(d)).reshape(d, d)
+            pw.dense_child(w, d, d, -1, dt, W)
+    pw.empty_controls(w)
+    for c in range(cells):
+        pw.empty_controls(w)
+        for _ in kinds:
+            pw.empty_controls(w)
+    w.i32(cells * len(kinds))
+    for c in range(cells):
+        for dt in kinds:
+            # FormatNone payload of the right size; the session re-quantizes
+            # the fp32 W with the scheme
+            pw.store_payload(w, dt, d, d, np.zeros(d * d if dt != 16 else (d * d + 1) // 2, np.uint8))
+    for c in range(cells):
+        w.i32(1, 0, 0, 0, 0, 0)
+    model = pw.ModelSession(w.bytes(), scheme=3)
+    x = hip.upload(pw.normal(pw.seed_for(5, 0) + 500, batch * d).reshape(batch, d))
+    y = hip.malloc(batch * d * 4)
+    flops = cells * len(kinds) * 2 * batch * d * d
+
+    def enqueue(i, stream):
+        model.forward_device(x, batch, d, y, batch * d, stream)
+
+    def close():
+        model.close()
+        hip.free(x)
+        hip.free(y)
+
+    return {"desc": name, "enqueue": enqueue, "per_graph": 1, "bytes": None, "flops": flops,
+            "bound": "mfma", "dtype": "fp8e4m3+fp4e2m1", "direct": True,
+            "config": {"workload": name, "cells": cells, "layers_per_cell": 3, "batch": batch,
+                       "width": d, "layer_kinds": "E4M3, FP4, E4M3, E8M0 per 32 (one scheme per model)",
+                       "execution": ("reference volume semantics: Grid 4x4x4 of Stack cells, a "
+                                     "192-layer serial chain, one welvet_model_forward_device "
+                                     "per step (synchronous, not graph-captured)")},
+            "cpu": None, "close": close}
+
+
 def make_workload(pw, hip, config, copies):
     if config == "c2":
         return dense_workload(pw, hip, "dense_gemv_4096x4096_fp8e4m3_rowscale_b1", 2, 4, 2, 1,
@@ -312,6 +367,8 @@ def make_workload(pw, hip, config, copies):
                               5, 2, 4096, 1024, 1024, min(copies, 4), "mfma")
     if config == "c4mha":
         return mha_workload(pw, hip, "mha_layer_b8_s512_d1024_h16_fp8e5m2_rowscale")
+    if config == "c5chain":
+        return chain_workload(pw, hip, "volume_grid_4x4x4_stack3_dense_1024_b256_serial")
     if config == "c5":
         return cells_workload(pw, hip, "volume_64_cells_3x_dense_1024_b256")
     raise SystemExit(f"unknown config {config}")
@@ -338,7 +395,7 @@ def copy_calibration(pw, nbytes, steps):
     hip.free(dst)
 
 
-CONFIGS = ["c1", "c2", "c3", "c3b16", "c4", "c4mha", "c5"]
+CONFIGS = ["c1", "c2", "c3", "c3b16", "c4", "c4mha", "c5", "c5chain"]
 
 
 def main():
@@ -386,16 +443,18 @@ def main():
         return go
 
     full, rem = divmod(steps, per)
-    g_full = hip.capture(stream, enqueue(per))
-    g_rem = hip.capture(stream, enqueue(rem)) if rem else None
+    direct = wl.get("direct", False)  # synchronous calls: no graph capture
+    g_full = enqueue(per) if direct else hip.capture(stream, enqueue(per))
+    g_rem = (enqueue(rem) if direct else hip.capture(stream, enqueue(rem))) if rem else None
+    launch = (lambda g, st: g()) if direct else hip.launch
     if warmup is not None:
         for _ in range(max(1, (warmup + per - 1) // per)):
-            hip.launch(g_full, stream)
+            launch(g_full, stream)
         hip.sync()
     else:
         warmup, t0 = 0, time.perf_counter()
         while time.perf_counter() - t0 < WARMUP_S or warmup < steps:
-            hip.launch(g_full, stream)
+            launch(g_full, stream)
             hip.sync()
             warmup += per
     hip.sync()
@@ -409,9 +468,9 @@ def main():
         hip.sync()
         hip.record(e0, stream)
         for _ in range(full):
-            hip.launch(g_full, stream)
+            launch(g_full, stream)
         if g_rem:
-            hip.launch(g_rem, stream)
+            launch(g_rem, stream)
         hip.record(e1, stream)
         hip.sync()
         runs.append(hip.elapsed_ms(e0, e1))
@@ -454,9 +513,10 @@ def main():
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
-    hip.graph_free(g_full)
-    if g_rem:
-        hip.graph_free(g_rem)
+    if not direct:
+        hip.graph_free(g_full)
+        if g_rem:
+            hip.graph_free(g_rem)
     wl["close"]()
 
 

@@ -362,7 +362,7 @@ Tensor stack_forward(std::vector<ModelNode>& children, const Tensor& in, Arena& 
 
 Status model_parse(const uint8_t* data, size_t size, int scheme, Model* m) {
   try {
-    require(data && size >= 28 && size <= (1u << 28), "invalid mount arguments");
+    require(data && size >= 28 && size <= (1ull << 32), "invalid mount arguments");
     if (scheme < 0 || scheme > 3) return Status::err(kInvalid, "backend (scale scheme) must be 0..3");
     Reader r{data, size};
     require(r.one<uint32_t>() == 0x314e4d57u, "unsupported model descriptor version");
