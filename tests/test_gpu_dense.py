@@ -65,7 +65,7 @@ def test_release_smoke_known_answer(gpu):
 def test_integer_exact_bit_for_bit(gpu, oracle, dt, values):
     rng = np.random.default_rng(dt)
     for rows, cols, batch in [(129, 1000, 1), (64, 4096, 1), (5, 77, 3), (9, 300, 9), (24, 9300, 1),
-                              (40, 301, 9)]:
+                              (40, 301, 9), (130, 4096, 40)]:
         W = rng.choice(np.array(values, np.float32), (rows, cols))
         x = rng.integers(-4, 5, (batch, cols)).astype(np.float32)
         pre, post = run(gpu, dt, 0, W, x)
@@ -223,6 +223,32 @@ def test_batched_mfma_matches_oracle(gpu, oracle, dt, scheme, rows, cols, batch)
     e = rel_l2(pre, o_pre)
     assert e <= TOL_MFMA, e
     assert np.array_equal(pre, post)
+
+
+@pytest.mark.parametrize("dt,scheme", [(4, 2), (16, 3), (5, 0), (4, 1)])
+@pytest.mark.parametrize("rows,cols,batch", [
+    (384, 2000, 200),   # 6 tiles, K split 8 ways, ragged M
+    (1000, 4096, 40),   # 8 tiles, 16 splits, ragged N
+    (130, 8192, 129),   # 4 tiles, 32 splits: the reduce adds them 16 at a time
+    (256, 512, 300),    # 2 splits of one step pair each
+])
+def test_batched_k_split(gpu, oracle, dt, scheme, rows, cols, batch):
+    """Batches above 32 rows with few 128 x 128 tiles split K over the CUs:
+    raw partial sums per split, added in split order by a second kernel
+    (scale, bias and activation there)."""
+    rng = np.random.default_rng(rows + 3 * cols + batch + dt + scheme)
+    W = rng.standard_normal((rows, cols)).astype(np.float32) / np.sqrt(cols)
+    if scheme == 0:
+        W *= 8.0
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    bias = rng.standard_normal(rows) * 0.1
+    pre, post = run(gpu, dt, scheme, W, x, act=2, bias=bias)
+    o_pre, o_post = oracle_dense(oracle, dt, scheme, W, x, act=2, bias=bias)
+    assert rel_l2(pre, o_pre) <= TOL_MFMA, (rows, cols, batch)
+    assert rel_l2(post, o_post) <= TOL_MFMA, (rows, cols, batch)
+    pre2, _ = run(gpu, dt, scheme, W, x)  # linear, no bias: post is pre
+    o_pre2, _ = oracle_dense(oracle, dt, scheme, W, x)
+    assert rel_l2(pre2, o_pre2) <= TOL_MFMA
 
 
 def test_batched_epilogue_bias_act(gpu, oracle):

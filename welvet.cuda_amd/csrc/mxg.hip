@@ -277,7 +277,7 @@ __device__ __forceinline__ MxgArgs load_args(ConstArgs t) {
   return p;
 }
 
-template <int DT, bool BLK, int MATS, bool GROUP, int W, int BR>
+template <int DT, bool BLK, int MATS, bool GROUP, int W, int BR, bool KS = false>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W / 4))) void k_mxg(
     MxgArgs p0, const MxgArgs* __restrict__ tab, int tiles_m, int tiles_n) {
   constexpr bool FP4 = DT == kFP4;
@@ -308,6 +308,14 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int i16 = lane & 15, g = lane >> 4;
   const int KC = p.kpad / 128, S = KC;
+  // K steps [kb, ke): all of K, or with KS (split along K, blockIdx.y of
+  // gridDim.y) a range of whole step pairs
+  int kb = 0, ke = S;
+  if constexpr (KS) {
+    const int P = S / 2, ks = blockIdx.y, nks = gridDim.y;
+    kb = 2 * (int)((long)P * ks / nks);
+    ke = 2 * (int)((long)P * (ks + 1) / nks);
+  }
 
   // activation fragments of this wave (step s adds s * kChunkBytes / s * 256)
   const uint8_t* abase[SM];
@@ -403,10 +411,10 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
   {
     uint4 q0, q1, q2, q3;
     uint32_t be = 0;
-    WV_LOAD_B(0);
+    WV_LOAD_B(kb);
     WV_STORE_B(0);
   }
-  load_a(0, fr[0]);
+  load_a(kb, fr[0]);
   if constexpr (!BLK) {
     for (int i = tid; i < 2 * BR; i += 64 * W) (&ssb[0][0])[i] = 0x7F7F7F7Fu;
   }
@@ -416,7 +424,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
   __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
   asm volatile("s_barrier" ::: "memory");
 
-  for (int s0 = 0; s0 < S; s0 += 2) {
+  for (int s0 = kb; s0 < ke; s0 += 2) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int s = s0 + i, cur = i;
@@ -468,7 +476,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
         // next step into the other buffer and set (their last readers
         // finished before the previous barrier); the last step fetches
         // itself again into them, which nothing reads
-        const int nx = s + 1 < S ? s + 1 : S - 1;
+        const int nx = s + 1 < ke ? s + 1 : ke - 1;
         uint4 q0, q1, q2, q3;
         uint32_t be = 0;
         WV_LOAD_B(nx);
@@ -533,7 +541,8 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
         const int nb = n0 + c * 16 + 4 * g;
         float4 sc[MATS];
 #pragma unroll
-        for (int m = 0; m < MATS; ++m) sc[m] = *reinterpret_cast<const float4*>(p.scale[m] + nb);
+        for (int m = 0; m < MATS; ++m)
+          sc[m] = KS ? make_float4(1.f, 1.f, 1.f, 1.f) : *reinterpret_cast<const float4*>(p.scale[m] + nb);
         float y[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -551,7 +560,22 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
             make_float4(y[0], y[1], y[2], y[3]);
       }
     const int n = n0 + hc * CH + cl;
-    if (MATS == 2 || !p.need_epi) {
+    if constexpr (KS) {
+      // raw sums of this K range into split blockIdx.y's plane of the
+      // partial buffer (rows of round_up(N, 256) floats; k_mxs_reduce adds
+      // the planes in split order and applies the scale and epilogue). The
+      // tile's columns stay below round_up(N, 256), so every float4 is in
+      // the plane.
+      const size_t npad = ((size_t)p.N + 255) / 256 * 256;
+      float* dst = p.part + (size_t)blockIdx.y * p.mpad * npad;
+#pragma unroll
+      for (int rr = 0; rr < SM * 16 / RPI; ++rr) {
+        const int r = rr * RPI + lane / LPR;
+        if (rbase + r >= p.M) continue;
+        *reinterpret_cast<float4*>(dst + (size_t)(rbase + r) * npad + n) =
+            *reinterpret_cast<const float4*>(&stage[wave][r][cl]);
+      }
+    } else if (MATS == 2 || !p.need_epi) {
       // post = pre here; a caller that passes one buffer for both gets it
       // written once
       float* post = MATS == 1 && p.post != p.pre ? p.post : nullptr;
@@ -622,7 +646,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
         *reinterpret_cast<float4*>(&stage[wave][r][cl]) = make_float4(yv[0], yv[1], yv[2], yv[3]);
       }
     }
-    if constexpr (MATS == 1 && CH == 128) {
+    if constexpr (MATS == 1 && CH == 128 && !KS) {
       // Chained layer: the next layer's split of post, written from the
       // stage (the same terms k_split would make from post in memory). The
       // next layer has the same rows (mpad) and kpad = N. Rows >= M get zero
@@ -1021,6 +1045,19 @@ Status launch_small(const MxgArgs& p, hipStream_t st) {
   return hip_status(hipGetLastError(), "mxs launch");
 }
 
+// Split along K for a large-tile product of one matrix with few tiles (fewer
+// than 128 of 128 columns): whole step pairs per split, about 256 workgroups
+// in all. Used when nothing else is fused into the epilogue (no RoPE, no
+// chained split): the reduce kernel applies the scale and epilogue.
+int mxg_ksplit(int M, int kpad, int N, int mats) {
+  if (M <= 32 || mats != 1) return 1;
+  const int64_t tiles = round_up(M, kBM) / kBM * ((N + 127) / 128);
+  const int pairs = kpad / 256;
+  if (tiles >= 128 || pairs < 2) return 1;
+  const int ks = (int)(256 / tiles);
+  return ks < pairs ? ks : pairs;
+}
+
 template <int DT, bool BLK, int MATS>
 Status launch_t(const MxgArgs& p, int bm, hipStream_t st) {
   if (p.rope_tab && (bm != kBM || MATS != 1 || p.need_epi || p.next || p.rope_hd <= 0 ||
@@ -1031,6 +1068,20 @@ Status launch_t(const MxgArgs& p, int bm, hipStream_t st) {
         (size_t)round_up(p.N, 256) * p.pitch >= (1ull << 31))
       return Status::err(kUnsupported, "mxg: operands above 2 GiB");
     const int tiles_m = p.mpad / kBM;
+    const int ks = p.rope_tab || p.next ? 1 : mxg_ksplit(p.M, p.kpad, p.N, MATS);
+    if constexpr (MATS == 1) {
+      if (ks > 1) {
+        if (!p.part) return Status::err(kInvalid, "mxg: K-split partial buffer missing");
+        const int tiles_n = (p.N + 127) / 128;
+        k_mxg<DT, BLK, 1, false, kMxgWaves, 128, true>
+            <<<dim3((unsigned)(tiles_m * tiles_n), (unsigned)ks), 64 * kMxgWaves, 0, st>>>(
+                p, nullptr, tiles_m, tiles_n);
+        // the kernel boundary makes every split's partial sums visible
+        const int64_t n = (int64_t)p.M * p.N;
+        k_mxs_reduce<1><<<(unsigned)((n + kThreads - 1) / kThreads), kThreads, 0, st>>>(p, ks, 256);
+        return hip_status(hipGetLastError(), "mxg K-split launch");
+      }
+    }
     if (mxg_wide(1, tiles_m, p.N, MATS)) {
       const int tiles_n = (p.N + 256 / MATS - 1) / (256 / MATS);
       k_mxg<DT, BLK, MATS, false, kMxgWaves, 256><<<(unsigned)(tiles_m * tiles_n), 64 * kMxgWaves, 0, st>>>(
@@ -1061,7 +1112,10 @@ Status launch_m(const MxgArgs& p, int dtype, bool blk, int bm, hipStream_t st) {
 int mxg_block_m(int M) { return M <= 32 ? 16 : kBM; }
 
 size_t mxg_part_bytes(int M, int kpad, int N, int mats) {
-  if (mxg_block_m(M) != 16) return 0;
+  if (mxg_block_m(M) != 16) {
+    const int ks = mxg_ksplit(M, kpad, N, mats);
+    return ks > 1 ? (size_t)ks * round_up(M, kBM) * round_up(N, 256) * sizeof(float) : 0;
+  }
   const int mpad = (int)round_up(M, 16);
   const int ks = mxs_ksplit(N, kpad, mpad);
   const int rows = 16 * kSmallWaves * mxs_rb(N);
