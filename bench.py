@@ -20,6 +20,7 @@ Other workloads (--config), each its own line:
   c4mha  whole MHA layer: B=8, S=512, d=1024, 16 heads x 64, causal, RoPE
   c5     64 cells x (Dense 1024^2 E4M3 row -> FP4 block-32 -> E4M3 row), batch 256
   c5chain  the same cells as the reference's volume: one 192-layer serial chain (model session)
+  c2bwd  Dense backward at the GEMV shape: d_pre, dX = W^T d_pre, dW (4096^2 E4M3 per-row, batch 1)
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2]
 """
@@ -43,7 +44,8 @@ METRIC = "FP8/FP4 Dense GEMV GB/s + GEMM TFLOPS (% roofline), 1 MI355X vs host C
 
 # rocprof summaries (kernel stats + FETCH_SIZE/WRITE_SIZE scaled by a copy of
 # known size) per workload; `traffic_bytes:` is the measured HBM bytes per launch.
-PROFILES = {"c2": "gemv_fp8e4m3_rowscale_4096x4096_b1.txt"}
+PROFILES = {"c2": "gemv_fp8e4m3_rowscale_4096x4096_b1.txt",
+            "c2bwd": "dense_backward_4096x4096_fp8e4m3_rowscale_b1.txt"}
 
 
 def measured_traffic(config):
@@ -351,6 +353,68 @@ def chain_workload(pw, hip, name):
             "cpu": None, "close": close}
 
 
+def backward_workload(pw, hip, name, copies):
+    """Dense backward (the NormalBP leaf, kernels.cu:83-127) at the GEMV shape:
+    4096 x 4096 E4M3 with per-row scales, batch 1, Linear. A step is one
+    welvet_dense_backward_device: d_pre, dX = W^T d_pre from the codes, and
+    the f32 dW [4096][4096]. Weight copies and dW buffers rotate (16 each,
+    1.3 GB in all, over 4x the MALL)."""
+    import numpy as np
+
+    K = N = 4096
+    batch = 1
+    seed = pw.seed_for(2)
+    W = pw.normal(seed, N * K, 1 / np.sqrt(K)).reshape(N, K)
+    x = pw.normal(seed + 500, batch * K).reshape(batch, K)
+    g = pw.normal(seed + 600, batch * N).reshape(batch, N)
+    sessions = [pw.DenseSession(batch, K, N, -1, 4, 2, W) for _ in range(copies)]
+    dx_in, dg = hip.upload(x), hip.upload(g)
+    dpre_f = hip.malloc(batch * N * 4)
+    dd, ddx = hip.malloc(batch * N * 4), hip.malloc(batch * K * 4)
+    ddw = [hip.malloc(N * K * 4) for _ in range(copies)]
+    sessions[0].execute_device(dx_in, dpre_f, dpre_f)
+    for i, s in enumerate(sessions):  # allocates each session's dX partials before capture
+        s.backward_device(dx_in, dpre_f, dpre_f, dg, False, dd, ddx, ddw[i])
+    hip.sync()
+    # codes + row scales + x + pre + g (inputs), d_pre + dX + dW (outputs)
+    nbytes = N * K + 4 * N + 4 * K * batch + 8 * N * batch + 4 * N * batch + 4 * K * batch + 4 * N * K
+    flops = 2 * N * K * batch * 2
+
+    def enqueue(i, stream):
+        sessions[i % copies].backward_device(dx_in, dpre_f, dpre_f, dg, False, dd, ddx,
+                                             ddw[i % copies], None, stream)
+
+    def cpu(budget_s):
+        orc = oracle()
+        native, rs, blk = orc.quantize(4, 2, N, K, W)
+        Wd = orc.dequant(4, 2, N, K, native, rs, blk)
+        pre = (x.astype(np.float64) @ Wd.T.astype(np.float64)).astype(np.float32)
+        th = cpu_threads()
+        orc.backward(Wd, g, pre, x, -1, threads=th)  # warm
+        t0, iters = time.perf_counter(), 0
+        while time.perf_counter() - t0 < budget_s or iters < 2:
+            orc.backward(Wd, g, pre, x, -1, threads=th)
+            iters += 1
+        per = (time.perf_counter() - t0) / iters
+        return {"value": round(nbytes / per / 1e9, 4), "unit": "GB/s", "cores": th, "kind": "port",
+                "sample": (f"oracle restatement of the reference NormalBP backward (act', f64 serial "
+                           f"MatVec^T over {th} threads, per-batch-row f32 outer product) on the "
+                           f"dequantized f32 W: {iters} runs, {per * 1e3:.2f} ms each")}
+
+    def close():
+        for s in sessions:
+            s.close()
+        for p in [dx_in, dg, dpre_f, dd, ddx] + ddw:
+            hip.free(p)
+
+    return {"desc": name, "enqueue": enqueue, "per_graph": copies, "bytes": nbytes, "flops": flops,
+            "bound": "hbm", "dtype": "fp8e4m3",
+            "config": {"workload": name, "in": K, "out": N, "batch": batch, "scale": "per-row fp32",
+                       "act": "linear", "weight_copies_rotated": copies,
+                       "outputs": "d_pre, dX [1][4096], dW [4096][4096] f32"},
+            "cpu": cpu, "close": close}
+
+
 def make_workload(pw, hip, config, copies):
     if config == "c2":
         return dense_workload(pw, hip, "dense_gemv_4096x4096_fp8e4m3_rowscale_b1", 2, 4, 2, 1,
@@ -367,6 +431,8 @@ def make_workload(pw, hip, config, copies):
                               5, 2, 4096, 1024, 1024, min(copies, 4), "mfma")
     if config == "c4mha":
         return mha_workload(pw, hip, "mha_layer_b8_s512_d1024_h16_fp8e5m2_rowscale")
+    if config == "c2bwd":
+        return backward_workload(pw, hip, "dense_backward_4096x4096_fp8e4m3_rowscale_b1", 16)
     if config == "c5chain":
         return chain_workload(pw, hip, "volume_grid_4x4x4_stack3_dense_1024_b256_serial")
     if config == "c5":
@@ -395,7 +461,7 @@ def copy_calibration(pw, nbytes, steps):
     hip.free(dst)
 
 
-CONFIGS = ["c1", "c2", "c3", "c3b16", "c4", "c4mha", "c5", "c5chain"]
+CONFIGS = ["c1", "c2", "c3", "c3b16", "c4", "c4mha", "c5", "c5chain", "c2bwd"]
 
 
 def main():

@@ -121,6 +121,19 @@ WELVET_API welvet_status welvet_dense_mount_q(int32_t batch, int32_t in, int32_t
  * only for Linear without bias. */
 WELVET_API welvet_status welvet_dense_execute_device(welvet_dense_session* sess, const float* x,
                                                      float* pre, float* post, void* stream);
+/* Extension: backward of a mounted session on device buffers, queued on
+ * `stream` (the session's own when null), returning without waiting. x
+ * [batch*in], pre and post [batch*out] from the forward; g is the output
+ * gradient (use_target 0) or an MSE target (use_target 1: post is read and
+ * loss_part[ceil(batch*out/256)] receives partial sums of (post - g)^2).
+ * Writes d_pre [batch*out], dX [batch*in], dW [out*in]: the arithmetic of
+ * welvet_dense_normalbp_f32. The first call allocates the session's dX
+ * partial buffer; later calls allocate nothing (graph-capturable). */
+WELVET_API welvet_status welvet_dense_backward_device(welvet_dense_session* sess, const float* x,
+                                                      const float* pre, const float* post,
+                                                      const float* g, int32_t use_target,
+                                                      float* dpre, float* dX, float* dW,
+                                                      double* loss_part, void* stream);
 /* Copies the session's quantized store to host memory: the reference
  * FormatNone payload (native_cap bytes available; *native_len set), the
  * per-row scales [out] and, for scheme 3, the E8M0 bytes [out*ceil(in/32)]. */
@@ -201,6 +214,20 @@ WELVET_API welvet_status welvet_model_forward_device(welvet_model_session* s, co
 WELVET_API welvet_status welvet_codec_sweep(int32_t dtype, uint32_t first_chunk,
                                             uint32_t n_chunks, int64_t* out);
 
+/* Dense NormalBP leaf (replaces reference include/welvet_c.h:69-79,
+ * src/interop/c_abi.cpp:119-200): forward, then the gradient (grad_or_target
+ * is gradOut, or with use_target = 1 an MSE target: loss = mean (post - t)^2),
+ * the backward over the quantized weights (dX [batch*in], dW [out*in]) and,
+ * if lr != 0, SGD on the quantized store: W <- quantize(f32(f64(W) - lr dW))
+ * with the scale scheme in `backend` (0 = the reference's element re-encode).
+ * W_after [out*in] is the resulting store dequantized to f32. Host buffers;
+ * the call synchronizes. Codes: 1 bad arguments, 2 unsupported dtype/scheme. */
+WELVET_API welvet_status welvet_dense_normalbp_f32(
+    int32_t batch, int32_t in, int32_t out, int32_t act, int32_t dtype, int32_t backend,
+    const float* W_init, const double* bias, size_t bias_len, const float* x,
+    const float* grad_or_target, int32_t use_target, double lr, float* pre, float* post, float* dX,
+    float* dW, float* W_after, double* loss);
+
 /* ==== reference entry points outside this path: code 3 ("gap?") ====
  * Same signatures as reference include/welvet_c.h:50-59, 74-130, 142-162,
  * 175-386. */
@@ -218,11 +245,6 @@ WELVET_API welvet_status welvet_model_train_mse(welvet_model_session*, int32_t m
                                                 int32_t ticks, const uint8_t*, size_t,
                                                 double* loss);
 WELVET_API welvet_status welvet_model_sync(welvet_model_session*, int32_t event);
-WELVET_API welvet_status welvet_dense_normalbp_f32(
-    int32_t batch, int32_t in, int32_t out, int32_t act, int32_t dtype, int32_t backend,
-    const float* W_init, const double* bias, size_t bias_len, const float* x,
-    const float* grad_or_target, int32_t use_target, double lr, float* pre, float* post, float* dX,
-    float* dW, float* W_after, double* loss);
 WELVET_API welvet_status welvet_rmsnorm_forward_f32(int32_t batch, int32_t seq, int32_t dim,
                                                     double eps, int32_t dtype, int32_t backend,
                                                     const float* gamma, const float* x, float* pre,

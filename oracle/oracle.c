@@ -426,6 +426,106 @@ void or_swiglu_product(const float* g, const float* u, float* h, int64_t n) {
 }
 
 /* ------------------------------------------------------------------------- */
+/* activate_deriv_dev, kernels.cu:48-81 (activate.cpp:31-63 on the host). */
+double or_act_deriv(int act, double x) {
+  switch (act) {
+  case -1: return 1.0;
+  case 0: return x > 0.0 ? 1.0 : 0.0;
+  case 6: return x > 0.0 ? 2.0 * x : 0.0;
+  case 5: return x > 0.0 ? 1.0 : 0.01;
+  case 1: {
+    const double sg = 1.0 / (1.0 + exp(-x));
+    return sg * (1.0 + x * (1.0 - sg));
+  }
+  case 2: {
+    const double k = 0.7978845608028654;
+    const double u = k * (x + 0.044715 * x * x * x);
+    const double th = tanh(u);
+    const double du = k * (1.0 + 3.0 * 0.044715 * x * x);
+    return 0.5 * (1.0 + th) + 0.5 * x * (1.0 - th * th) * du;
+  }
+  case 3: {
+    const double t = tanh(x);
+    return 1.0 - t * t;
+  }
+  case 4: {
+    const double sg = 1.0 / (1.0 + exp(-x));
+    return sg * (1.0 - sg);
+  }
+  }
+  return 1.0;
+}
+
+typedef struct {
+  int batch, in, out, i0, i1;
+  const float *W, *dpre;
+  float* dX;
+} matvect_job;
+
+/* dense_matvect_f64_batch, kernels.cu:92-107: columns [i0, i1). */
+static void* matvect_cols(void* p) {
+  const matvect_job* j = (const matvect_job*)p;
+  for (int b = 0; b < j->batch; ++b)
+    for (int i = j->i0; i < j->i1; ++i) {
+      double sum = 0.0;
+      for (int o = 0; o < j->out; ++o)
+        sum += (double)j->W[(int64_t)o * j->in + i] * (double)j->dpre[(int64_t)b * j->out + o];
+      j->dX[(int64_t)b * j->in + i] = (float)sum;
+    }
+  return NULL;
+}
+
+void or_dense_backward(int batch, int in, int out, int act, const float* W, const float* gy,
+                       const float* pre, const float* x, float* dpre, float* dX, float* dW,
+                       int nthreads) {
+  /* dense_act_deriv, kernels.cu:83-90 */
+  for (int64_t i = 0; i < (int64_t)batch * out; ++i)
+    dpre[i] = (float)((double)gy[i] * or_act_deriv(act, (double)pre[i]));
+  if (nthreads < 1) nthreads = 1;
+  if (nthreads > in) nthreads = in;
+  pthread_t* th = (pthread_t*)calloc((size_t)nthreads, sizeof(pthread_t));
+  matvect_job* jobs = (matvect_job*)calloc((size_t)nthreads, sizeof(matvect_job));
+  for (int t = 0; t < nthreads; ++t) {
+    matvect_job j = {batch, in, out, (int)((int64_t)in * t / nthreads),
+                     (int)((int64_t)in * (t + 1) / nthreads), W, dpre, dX};
+    jobs[t] = j;
+    pthread_create(&th[t], NULL, matvect_cols, &jobs[t]);
+  }
+  for (int t = 0; t < nthreads; ++t) pthread_join(th[t], NULL);
+  free(th);
+  free(jobs);
+  /* dense_outer_f64_batch, kernels.cu:109-127 */
+  for (int o = 0; o < out; ++o)
+    for (int i = 0; i < in; ++i) {
+      float acc = 0.0f;
+      for (int b = 0; b < batch; ++b)
+        acc = (float)((double)acc + (double)dpre[(int64_t)b * out + o] * (double)x[(int64_t)b * in + i]);
+      dW[(int64_t)o * in + i] = acc;
+    }
+}
+
+/* training.cpp:44-56 */
+double or_mse(int64_t n, const float* pred, const float* target) {
+  double sum = 0.0;
+  for (int64_t i = 0; i < n; ++i) {
+    const double d = (double)pred[i] - (double)target[i];
+    sum += d * d;
+  }
+  return sum / (double)n;
+}
+
+/* training.cpp:58-69 */
+void or_mse_grad(int64_t n, const float* pred, const float* target, float* grad) {
+  const double scale = 2.0 / (double)n;
+  for (int64_t i = 0; i < n; ++i) grad[i] = (float)(scale * ((double)pred[i] - (double)target[i]));
+}
+
+/* native_codec.cpp:1123-1127 */
+void or_sgd(int64_t n, const float* w, const float* dW, double lr, float* next) {
+  for (int64_t i = 0; i < n; ++i) next[i] = (float)((double)w[i] - lr * (double)dW[i]);
+}
+
+/* ------------------------------------------------------------------------- */
 /* kernels.cu:470-485 */
 static int attn_allow(int qp, int kp, int mask, int window, int msl, int prefix_len,
                       int window_causal) {

@@ -103,6 +103,29 @@ void or_mha_attention(const float* q, const float* k, const float* v, float* att
                       int pos_kind, int softmax_kind, int window, int prefix_len, int window_causal,
                       double rope_theta, double scale_override);
 
+/* --- Dense backward (NormalBP) and SGD --------------------------------------
+ * act'(x) in f64: src/cuda/kernels.cu:48-81 (host twin src/core/activate.cpp:31-63).
+ * Pinned by: the compiled reference activate_deriv_f64 (oracle/_ref), and
+ * central differences of or_activate. */
+double or_act_deriv(int act, double x);
+/* kernels.cu:83-127 with W the dequantized f32 matrix [out][in]:
+ *   dpre[b][o] = f32(f64(gy[b][o]) * act'(f64 pre[b][o]));
+ *   dX[b][i]   = f32(sum over o in order of f64(W[o][i]) * f64(dpre[b][o]));
+ *   dW[o][i]   = acc over b in order, acc = f32(f64(acc) + f64(dpre) * f64(x)).
+ * Pinned by: W^T dpre and the outer product in numpy f64, exact-integer cases,
+ * and central differences of the forward. nthreads splits the columns of dX. */
+void or_dense_backward(int batch, int in, int out, int act, const float* W, const float* gy,
+                       const float* pre, const float* x, float* dpre, float* dX, float* dW,
+                       int nthreads);
+/* src/runtime/training.cpp:44-69: loss = sum (p - t)^2 / n in f64 (serial);
+ * grad = f32(2/n * (f64 p - f64 t)). Pinned by numpy closed forms. */
+double or_mse(int64_t n, const float* pred, const float* target);
+void or_mse_grad(int64_t n, const float* pred, const float* target, float* grad);
+/* src/weights/native_codec.cpp:1112-1128 (WeightStore::apply_sgd per element):
+ * next = f32(f64(w) - lr * f64(dW)); the caller re-encodes next. Pinned by the
+ * compiled reference WeightStore::apply_sgd (oracle/_ref). */
+void or_sgd(int64_t n, const float* w, const float* dW, double lr, float* next);
+
 /* --- CPU baseline timing (reported beside the GPU) ---------------------------
  * Mount: decode codes to an f64 row-major W (src/layers/dense/dense.cpp:28-39).
  * Execute: or_dense semantics with f64 W, rows split over nthreads.

@@ -1,6 +1,7 @@
 // C bridge over the reference's own host codec and FormatNone store, compiled
 // from the reference sources where they lie (see oracle/Makefile). Test
 // infrastructure only: used to generate and check golden vectors.
+#include "welvet/activate.hpp"
 #include "welvet/float_codecs.hpp"
 #include "welvet/weights.hpp"
 
@@ -82,6 +83,29 @@ int ref_store_decode_row(int dtype, int rows, int cols, const uint8_t* native, s
   std::memcpy(s.native.data(), native, native_len);
   st = s.decode_row_f64(row, out);
   return static_cast<int>(st.code);
+}
+
+// activate_f64 / activate_deriv_f64 (src/core/activate.cpp:7-63).
+double ref_activate(int act, double x) {
+  return welvet::activate_f64(x, static_cast<welvet::Activation>(act));
+}
+double ref_act_deriv(int act, double x) {
+  return welvet::activate_deriv_f64(x, static_cast<welvet::Activation>(act));
+}
+
+// WeightStore::apply_sgd (native_codec.cpp:1080-1133) on a store holding the
+// native bytes; the updated bytes are written back in place.
+int ref_store_apply_sgd(int dtype, int rows, int cols, uint8_t* native, size_t native_len,
+                        const double* dW, double lr) {
+  welvet::WeightStore s;
+  auto st = welvet::WeightStore::make(rows, cols, static_cast<welvet::DType>(dtype), nullptr, &s);
+  if (!st) return static_cast<int>(st.code);
+  if (native_len != s.native.size()) return 1;
+  std::memcpy(s.native.data(), native, native_len);
+  st = s.apply_sgd(dW, lr);
+  if (!st) return static_cast<int>(st.code);
+  std::memcpy(native, s.native.data(), native_len);
+  return 0;
 }
 
 }  // extern "C"

@@ -44,6 +44,13 @@ class Oracle:
         L.or_dense_forward.argtypes = [_i, _i, _i, _i, _fp, _dp, _i, _fp, _fp, _fp, _i]
         L.or_swiglu_product.argtypes = [_fp, _fp, _fp, ctypes.c_int64]
         L.or_mha_attention.argtypes = [_fp, _fp, _fp, _fp] + [_i] * 12 + [ctypes.c_double] * 2
+        L.or_act_deriv.restype = ctypes.c_double
+        L.or_act_deriv.argtypes = [_i, ctypes.c_double]
+        L.or_dense_backward.argtypes = [_i, _i, _i, _i, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _i]
+        L.or_mse.restype = ctypes.c_double
+        L.or_mse.argtypes = [ctypes.c_int64, _fp, _fp]
+        L.or_mse_grad.argtypes = [ctypes.c_int64, _fp, _fp, _fp]
+        L.or_sgd.argtypes = [ctypes.c_int64, _fp, _fp, ctypes.c_double, _fp]
         L.or_cpu_dense_bench.restype = ctypes.c_double
         L.or_cpu_dense_bench.argtypes = [_i, _i, _i, _i, _i, _u8p, _fp, _u8p, _fp, _fp, _i, _i, _i,
                                          _dp]
@@ -121,3 +128,40 @@ class Oracle:
 
     def activate(self, act, x):
         return self.L.or_activate(act, float(x))
+
+    def act_deriv(self, act, x):
+        return self.L.or_act_deriv(act, float(x))
+
+    def backward(self, W, gy, pre, x, act=-1, threads=8):
+        """dpre, dX, dW of the reference NormalBP contract (W dequantized f32)."""
+        W = np.ascontiguousarray(W, np.float32)
+        gy = np.ascontiguousarray(gy, np.float32)
+        pre = np.ascontiguousarray(pre, np.float32)
+        x = np.ascontiguousarray(x, np.float32)
+        out, in_dim = W.shape
+        batch = x.shape[0]
+        dpre = np.zeros((batch, out), np.float32)
+        dx = np.zeros((batch, in_dim), np.float32)
+        dw = np.zeros((out, in_dim), np.float32)
+        self.L.or_dense_backward(batch, in_dim, out, act, _f(W), _f(gy), _f(pre), _f(x), _f(dpre),
+                                 _f(dx), _f(dw), threads)
+        return dpre, dx, dw
+
+    def mse(self, pred, target):
+        p = np.ascontiguousarray(pred, np.float32)
+        t = np.ascontiguousarray(target, np.float32)
+        return self.L.or_mse(p.size, _f(p), _f(t))
+
+    def mse_grad(self, pred, target):
+        p = np.ascontiguousarray(pred, np.float32)
+        t = np.ascontiguousarray(target, np.float32)
+        g = np.zeros_like(p)
+        self.L.or_mse_grad(p.size, _f(p), _f(t), _f(g))
+        return g
+
+    def sgd(self, w, dw, lr):
+        w = np.ascontiguousarray(w, np.float32)
+        dw = np.ascontiguousarray(dw, np.float32)
+        nxt = np.zeros_like(w)
+        self.L.or_sgd(w.size, _f(w), _f(dw), float(lr), _f(nxt))
+        return nxt

@@ -60,6 +60,9 @@ def test_invalid_arguments_return_code_1():
     assert L.welvet_mha_forward_f32(1, 1, 0, 1, 1, 0, 0, 1, 0, 4, 0, *[pw.fptr(W)] * 5, pw.fptr(y), pw.fptr(y)).code == 1
     out = np.zeros(2, np.int64)
     assert L.welvet_codec_sweep(4, 4095, 2, out.ctypes.data_as(ctypes.POINTER(ctypes.c_int64))).code == 1
+    loss = np.zeros(1)
+    assert L.welvet_dense_normalbp_f32(0, 2, 2, -1, 4, 0, pw.fptr(W), None, 0, pw.fptr(W), pw.fptr(W), 0, 0.0,
+                                       *[pw.fptr(y)] * 5, pw.dptr(loss)).code == 1
 
 
 def test_out_of_path_entry_points_report_gap():

@@ -1,0 +1,162 @@
+"""Dense backward and SGD on the GPU (welvet_dense_normalbp_f32) against the
+oracle.
+
+The backward is checked on the GPU's own forward outputs (pre, post), so each
+stage is compared with exactly the inputs it received:
+  * d_pre and dW (kernels.cu:83-127): bit-exact for the piecewise-polynomial
+    activations (Linear, ReLU, LeakyReLU, ReLU2): the f64 product of two
+    floats is exact and the f32 roundings happen at the same points. With
+    exp/tanh in act' the device and host math libraries may differ in the
+    last f64 bit: relative L2 <= 1e-6;
+  * dX = W^T d_pre (kernels.cu:92-107): f64 accumulation of exact terms in a
+    different order than the reference's serial sum: relative L2 <= 1e-6;
+  * the MSE loss (training.cpp:44-56): relative difference <= 1e-12;
+  * W_after: the oracle's SGD element rule (native_codec.cpp:1112-1128) on the
+    GPU's dW, re-quantized with the layer's scheme, then dequantized:
+    bit-exact (scheme 0 re-encodes every element with the reference codec).
+The forward outputs themselves are checked against the oracle with the
+Dense tolerances.
+"""
+import numpy as np
+import pytest
+
+from test_gpu_dense import rel_l2, tol
+
+pytestmark = pytest.mark.gpu
+
+EXACT_ACTS = (-1, 0, 5, 6)
+
+
+def check_normalbp(gpu, oracle, dt, scheme, batch, inn, out, act, use_target, lr, bias, seed):
+    rng = np.random.default_rng(seed)
+    W = (rng.standard_normal((out, inn)) / np.sqrt(inn)).astype(np.float32)
+    if scheme == 0:
+        W *= 8.0
+    x = rng.standard_normal((batch, inn)).astype(np.float32)
+    g = rng.standard_normal((batch, out)).astype(np.float32)
+    b = rng.standard_normal(out) * 0.1 if bias else None
+    pre, post, dx, dw, wa, loss = gpu.dense_normalbp(batch, inn, out, act, dt, scheme, W, x, g,
+                                                     use_target, lr, b)
+    native, rs, blk = oracle.quantize(dt, scheme, out, inn, W)
+    Wd = oracle.dequant(dt, scheme, out, inn, native, rs, blk)
+    o_pre, o_post = oracle.dense(Wd, x, act, b)
+    assert rel_l2(pre, o_pre) <= tol(batch) and rel_l2(post, o_post) <= tol(batch)
+
+    gy = oracle.mse_grad(post, g) if use_target else g
+    dpre_o, dx_o, dw_o = oracle.backward(Wd, gy, pre, x, act)
+    if act in EXACT_ACTS:
+        assert np.array_equal(dw, dw_o)
+    else:
+        assert rel_l2(dw, dw_o) <= 1e-6
+    assert rel_l2(dx, dx_o) <= 1e-6
+    if use_target:
+        lo = oracle.mse(post, g)
+        assert abs(loss - lo) <= 1e-12 * lo
+    else:
+        assert loss == 0.0
+    if lr == 0.0:
+        assert np.array_equal(wa, Wd)
+    else:
+        nxt = oracle.sgd(Wd, dw, lr)
+        n2, rs2, blk2 = oracle.quantize(dt, scheme, out, inn, nxt)
+        assert np.array_equal(wa, oracle.dequant(dt, scheme, out, inn, n2, rs2, blk2))
+    return dx, dw
+
+
+@pytest.mark.parametrize("dt,scheme", [(4, 0), (5, 0), (16, 0), (4, 2), (16, 3), (5, 1)])
+@pytest.mark.parametrize("batch,inn,out,act,use_target,lr,bias", [
+    (1, 300, 70, -1, False, 0.0, False),     # ragged, one partial band
+    (3, 1000, 33, 0, True, 0.05, True),      # MSE target, ReLU, bias, SGD
+    (5, 513, 129, 1, False, 0.5, False),     # SiLU, odd widths (FP4 nibbles straddle rows)
+    (40, 256, 512, 2, True, 0.01, False),    # matrix-core forward, GELU
+    (9, 1536, 1100, 5, False, 1.0, True),    # two d_pre chunks + one, LeakyReLU
+])
+def test_normalbp_matches_oracle(gpu, oracle, dt, scheme, batch, inn, out, act, use_target, lr,
+                                 bias):
+    check_normalbp(gpu, oracle, dt, scheme, batch, inn, out, act, use_target, lr, bias,
+                   seed=batch * 131 + inn + out + dt + scheme)
+
+
+def test_normalbp_c2_shape(gpu, oracle):
+    """GEMV 4096 x 4096, E4M3 per-row scales, batch 1 (the headline GEMV shape)."""
+    check_normalbp(gpu, oracle, 4, 2, 1, 4096, 4096, -1, True, 0.1, False, seed=2)
+
+
+@pytest.mark.parametrize("dt", [4, 5, 16])
+def test_normalbp_integer_exact(gpu, oracle, dt):
+    """Integer weights that every format holds, integer inputs and gradients:
+    every term and sum is exact, so dX is the integer product bit for bit."""
+    rng = np.random.default_rng(dt)
+    vals = np.array([-4, -2, -1, 0, 1, 2, 4], np.float32)
+    W = rng.choice(vals, (70, 300))
+    x = rng.integers(-4, 5, (3, 300)).astype(np.float32)
+    g = rng.integers(-4, 5, (3, 70)).astype(np.float32)
+    _, _, dx, dw, _, _ = gpu.dense_normalbp(3, 300, 70, -1, dt, 0, W, x, g)
+    assert np.array_equal(dx, (g.astype(np.int64) @ W.astype(np.int64)).astype(np.float32))
+    assert np.array_equal(dw, (g.T.astype(np.int64) @ x.astype(np.int64)).astype(np.float32))
+
+
+def test_normalbp_sgd_descends(gpu, oracle):
+    """A few SGD steps on an MSE target lower the loss (E4M3 per-row, the
+    weights re-quantized after every step)."""
+    rng = np.random.default_rng(8)
+    W = (rng.standard_normal((32, 64)) / 8).astype(np.float32)
+    x = rng.standard_normal((16, 64)).astype(np.float32)
+    t = (x @ (rng.standard_normal((32, 64)).astype(np.float32) / 8).T).astype(np.float32)
+    losses = []
+    for _ in range(4):
+        _, _, _, _, W, loss = gpu.dense_normalbp(16, 64, 32, -1, 4, 2, W, x, t, True, 0.5)
+        losses.append(loss)
+    assert all(b < a for a, b in zip(losses, losses[1:])), losses
+
+
+def test_normalbp_rejects_bad_arguments(gpu):
+    W = np.ones((4, 4), np.float32)
+    x = np.ones((1, 4), np.float32)
+    with pytest.raises(gpu.WelvetError) as e:
+        gpu.dense_normalbp(0, 4, 4, -1, 4, 0, W, x, np.ones((1, 4), np.float32))
+    assert e.value.code == 1
+    with pytest.raises(gpu.WelvetError) as e:
+        gpu.dense_normalbp(1, 4, 4, -1, 1, 0, W, x, np.ones((1, 4), np.float32))
+    assert e.value.code == 2
+
+
+@pytest.mark.parametrize("dt,scheme,batch,act,use_target", [(4, 2, 1, -1, True), (16, 3, 6, 1, False),
+                                                            (5, 0, 40, 5, True)])
+def test_backward_device_matches_normalbp(gpu, dt, scheme, batch, act, use_target):
+    """welvet_dense_backward_device on a mounted session (device buffers, the
+    session stream) gives the bits of welvet_dense_normalbp_f32, twice in a
+    row over the same buffers (the second call reuses the dX partials)."""
+    rng = np.random.default_rng(batch + dt)
+    inn, out = 700, 300
+    W = (rng.standard_normal((out, inn)) / np.sqrt(inn)).astype(np.float32)
+    x = rng.standard_normal((batch, inn)).astype(np.float32)
+    g = rng.standard_normal((batch, out)).astype(np.float32)
+    pre, post, dx, dw, _, loss = gpu.dense_normalbp(batch, inn, out, act, dt, scheme, W, x, g,
+                                                    use_target)
+    hip = gpu.Hip()
+    s = gpu.DenseSession(batch, inn, out, act, dt, scheme, W)
+    bufs = {k: hip.malloc(n * 4) for k, n in [("x", batch * inn), ("pre", batch * out),
+                                              ("post", batch * out), ("g", batch * out),
+                                              ("d", batch * out), ("dx", batch * inn),
+                                              ("dw", out * inn)]}
+    nparts = (batch * out + 255) // 256
+    lp = hip.malloc(nparts * 8)
+    hip.copy_in(bufs["x"], x)
+    hip.copy_in(bufs["g"], g)
+    s.execute_device(bufs["x"], bufs["pre"], bufs["post"])
+    for _ in range(2):
+        s.backward_device(bufs["x"], bufs["pre"], bufs["post"], bufs["g"], use_target, bufs["d"],
+                          bufs["dx"], bufs["dw"], lp)
+        hip.sync()
+        assert np.array_equal(hip.download(bufs["pre"], (batch, out)), pre)
+        assert np.array_equal(hip.download(bufs["dx"], (batch, inn)), dx)
+        assert np.array_equal(hip.download(bufs["dw"], (out, inn)), dw)
+        if use_target:
+            total = 0.0
+            for v in hip.download(lp, (nparts,), np.float64):  # in order, as the library adds them
+                total += float(v)
+            assert total / (batch * out) == loss
+    for p in list(bufs.values()) + [lp]:
+        hip.free(p)
+    s.close()

@@ -166,6 +166,18 @@ welvet_status welvet_dense_execute_device(welvet_dense_session* s, const float* 
   });
 }
 
+welvet_status welvet_dense_backward_device(welvet_dense_session* s, const float* x,
+                                           const float* pre, const float* post, const float* g,
+                                           int32_t use_target, float* dpre, float* dX, float* dW,
+                                           double* loss_part, void* stream) {
+  if (!s || !x || !pre || !g || !dpre || !dX || !dW || (use_target && (!post || !loss_part)))
+    return invalid("null backward args");
+  return guarded([&]() -> Status {
+    return wv::dense_backward(s->layer, s->batch, x, pre, post, g, use_target != 0, dpre, dX, dW,
+                              loss_part, &s->ws, pick(stream, s->stream.s));
+  });
+}
+
 // ---- grouped Dense execution (extension) ----
 struct welvet_dense_group {
   wv::Stream stream;
@@ -319,6 +331,66 @@ welvet_status welvet_dense_forward_f32(int32_t batch, int32_t in, int32_t out, i
   st = welvet_dense_execute(s, x, pre, post);
   welvet_dense_release(s);
   return st;
+}
+
+// Dense NormalBP leaf (src/interop/c_abi.cpp:119-200): forward, gradient
+// (the caller's, or MSE from a target), backward over the quantized weights,
+// optional SGD on the quantized store, then the updated weights as f32. The
+// scale scheme comes in `backend` as for the other entry points.
+welvet_status welvet_dense_normalbp_f32(int32_t batch, int32_t in, int32_t out, int32_t act,
+                                        int32_t dtype, int32_t backend, const float* W_init,
+                                        const double* bias, size_t bias_len, const float* x,
+                                        const float* grad_or_target, int32_t use_target, double lr,
+                                        float* pre, float* post, float* dX, float* dW,
+                                        float* W_after, double* loss) {
+  if (batch <= 0 || in <= 0 || out <= 0 || !W_init || !x || !grad_or_target || !pre || !post ||
+      !dX || !dW || !W_after || !loss)
+    return invalid("invalid argument");
+  return guarded([&]() -> Status {
+    WV_TRY(wv::init_device());
+    wv::Stream stream;
+    WV_TRY(stream.create());
+    hipStream_t st = stream.s;
+    wv::DenseLayer L;
+    wv::Workspace ws;
+    WV_TRY(wv::dense_build(in, out, act, dtype, backend, W_init, bias, bias_len, &L, st));
+    const size_t nx = (size_t)batch * in, ny = (size_t)batch * out, nw = (size_t)in * out;
+    const int64_t parts = wv::dpre_blocks((int64_t)ny);
+    wv::DevBuf dx_in, dpre_out, dpost, dg, dd, ddx, ddw, dwa, dloss;
+    WV_TRY(dx_in.alloc(nx * sizeof(float)));
+    WV_TRY(dpre_out.alloc(ny * sizeof(float)));
+    WV_TRY(dpost.alloc(ny * sizeof(float)));
+    WV_TRY(dg.alloc(ny * sizeof(float)));
+    WV_TRY(dd.alloc(ny * sizeof(float)));
+    WV_TRY(ddx.alloc(nx * sizeof(float)));
+    WV_TRY(ddw.alloc(nw * sizeof(float)));
+    WV_TRY(dwa.alloc(nw * sizeof(float)));
+    WV_TRY(dloss.alloc((size_t)parts * sizeof(double)));
+    WV_HIP(hipMemcpyAsync(dx_in.p, x, nx * sizeof(float), hipMemcpyHostToDevice, st));
+    WV_HIP(hipMemcpyAsync(dg.p, grad_or_target, ny * sizeof(float), hipMemcpyHostToDevice, st));
+    WV_TRY(wv::ensure_split(&ws, wv::dense_workspace_bytes(L, batch)));
+    WV_TRY(wv::dense_forward(L, batch, dx_in.as<float>(), dpre_out.as<float>(), dpost.as<float>(),
+                             &ws, st));
+    WV_TRY(wv::dense_backward(L, batch, dx_in.as<float>(), dpre_out.as<float>(), dpost.as<float>(),
+                              dg.as<float>(), use_target != 0, dd.as<float>(), ddx.as<float>(),
+                              ddw.as<float>(), dloss.as<double>(), &ws, st));
+    if (lr != 0.0) WV_TRY(wv::dense_apply_sgd(&L, ddw.as<float>(), lr, st));
+    WV_TRY(wv::launch_dequant(L.dev, dwa.as<float>(), st));
+    std::vector<double> lp(use_target ? (size_t)parts : 0);
+    WV_HIP(hipMemcpyAsync(pre, dpre_out.p, ny * sizeof(float), hipMemcpyDeviceToHost, st));
+    WV_HIP(hipMemcpyAsync(post, dpost.p, ny * sizeof(float), hipMemcpyDeviceToHost, st));
+    WV_HIP(hipMemcpyAsync(dX, ddx.p, nx * sizeof(float), hipMemcpyDeviceToHost, st));
+    WV_HIP(hipMemcpyAsync(dW, ddw.p, nw * sizeof(float), hipMemcpyDeviceToHost, st));
+    WV_HIP(hipMemcpyAsync(W_after, dwa.p, nw * sizeof(float), hipMemcpyDeviceToHost, st));
+    if (use_target)
+      WV_HIP(hipMemcpyAsync(lp.data(), dloss.p, lp.size() * sizeof(double), hipMemcpyDeviceToHost,
+                            st));
+    WV_HIP(hipStreamSynchronize(st));
+    double sum = 0.0;
+    for (double v : lp) sum += v;
+    *loss = use_target ? sum / (double)ny : 0.0;
+    return Status::ok();
+  });
 }
 
 // --------------------------------------------------------------- SwiGLU ----
@@ -680,9 +752,6 @@ welvet_status welvet_model_sync(welvet_model_session*, int32_t) { return gap("mo
 #define WV_GAP_NBP(name, ...) \
   welvet_status name(__VA_ARGS__) { return gap(#name); }
 
-WV_GAP_NBP(welvet_dense_normalbp_f32, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t,
-           const float*, const double*, size_t, const float*, const float*, int32_t, double, float*,
-           float*, float*, float*, float*, double*)
 WV_GAP_NBP(welvet_rmsnorm_forward_f32, int32_t, int32_t, int32_t, double, int32_t, int32_t,
            const float*, const float*, float*, float*)
 WV_GAP_NBP(welvet_rmsnorm_normalbp_f32, int32_t, int32_t, int32_t, double, int32_t, int32_t,

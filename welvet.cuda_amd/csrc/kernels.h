@@ -151,4 +151,31 @@ Status launch_attention(const AttnArgs& a, hipStream_t st);
 // in f64: tab[2 * (t * (hd/2) + d) + {0, 1}].
 Status build_rope_table(double* tab, int tokens, int hd, double theta, hipStream_t st);
 
+// ---- Dense backward and SGD (backward.hip) ----
+// d_pre = f32(f64(gy) * act'(f64 pre)) over n = batch * out elements; with
+// use_target, g holds the target and gy = f32(2/n (post - target)), and
+// loss_part[dpre_blocks(n)] receives the per-block sums of (post - target)^2.
+int64_t dpre_blocks(int64_t n);
+Status launch_dpre(const float* g, const float* post, const float* pre, int act, int use_target,
+                   int64_t n, float* dpre, double* loss_part, hipStream_t st);
+struct GemvtArgs {
+  const uint8_t* codes = nullptr;  // device codes [rpad][pitch]
+  const float* scale = nullptr;    // [rpad]
+  const uint8_t* blk = nullptr;    // [rpad][nblk] E8M0, scheme 3
+  int pitch = 0, nblk = 0, kpad = 0, in = 0, out = 0;
+  const float* dpre = nullptr;     // [batch][out]
+};
+// Bytes of the f64 partial buffer launch_backward_products needs.
+size_t gemvt_part_bytes(int in, int out);
+// dX [batch][in] = W^T d_pre (f64 accumulation, rounded once to f32) and dW
+// [out][in] (the reference's per-batch-row f32 accumulation) from d_pre.
+Status launch_backward_products(const GemvtArgs& a, int dtype, bool blk, int batch,
+                                const float* x, float* dw, double* part, float* dx,
+                                hipStream_t st);
+// w_next [rows][cols] = f32(f64(dequant(W)) - lr * f64(dW)).
+Status launch_sgd(const DeviceWeights& d, const float* dw, double lr, float* w_next,
+                  hipStream_t st);
+// W as f32 [rows][cols]: decode times the scales.
+Status launch_dequant(const DeviceWeights& d, float* w, hipStream_t st);
+
 }  // namespace wv

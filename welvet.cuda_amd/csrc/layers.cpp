@@ -259,6 +259,43 @@ Status dense_forward(const DenseLayer& L, int batch, const float* x, float* pre,
 }
 
 // ---------------------------------------------------------------------------
+Status dense_backward(const DenseLayer& L, int batch, const float* x, const float* pre,
+                      const float* post, const float* g, bool use_target, float* dpre, float* dx,
+                      float* dw, double* loss_part, Workspace* ws, hipStream_t st) {
+  if (batch <= 0 || !x || !pre || !g || !dpre || !dx || !dw || !ws || (use_target && !post))
+    return Status::err(kInvalid, "dense backward: bad args");
+  const int64_t n = (int64_t)batch * L.out;
+  WV_TRY(launch_dpre(g, post, pre, L.act, use_target ? 1 : 0, n, dpre, loss_part, st));
+  const size_t pb = gemvt_part_bytes(L.in, L.out);
+  if (ws->d.bytes < pb) WV_TRY(ws->d.alloc(pb));
+  GemvtArgs a;
+  a.codes = L.dev.d_codes();
+  a.scale = L.dev.d_scale();
+  a.blk = L.dev.d_blk();
+  a.pitch = L.dev.pitch;
+  a.nblk = L.dev.nblk;
+  a.kpad = L.dev.kpad;
+  a.in = L.in;
+  a.out = L.out;
+  a.dpre = dpre;
+  return launch_backward_products(a, L.dev.dtype, L.dev.scheme == kSchemeBlock32, batch, x, dw,
+                                  ws->d.as<double>(), dx, st);
+}
+
+Status dense_apply_sgd(DenseLayer* L, const float* dw, double lr, hipStream_t st) {
+  if (!L || !dw) return Status::err(kInvalid, "dense sgd: bad args");
+  const int64_t n = (int64_t)L->in * L->out;
+  DevBuf next, raw;
+  WV_TRY(next.alloc((size_t)n * sizeof(float)));
+  WV_TRY(launch_sgd(L->dev, dw, lr, next.as<float>(), st));
+  WV_TRY(raw.alloc(L->dev.dtype == kFP4 ? (size_t)((n + 1) / 2) : (size_t)n));
+  DeviceWeights fresh;
+  WV_TRY(quantize_to_device(next.as<float>(), L->dev.dtype, L->dev.scheme, L->out, L->in, &fresh,
+                            raw.as<uint8_t>(), st));
+  L->dev = std::move(fresh);
+  return download_store(L, raw.as<uint8_t>(), st);
+}
+
 bool dense_group_fused(int batch) { return uses_split(batch) && mxg_block_m(batch) > 16; }
 
 Status dense_group_build(const DenseLayer* const* layers, int n, int batch,

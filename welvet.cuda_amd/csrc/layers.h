@@ -60,6 +60,20 @@ Status dense_forward(const DenseLayer& L, int batch, const float* x, float* pre,
                      Workspace* ws, hipStream_t st);
 // Workspace bytes dense_forward needs for this batch.
 size_t dense_workspace_bytes(const DenseLayer& L, int batch);
+
+// Dense backward on device buffers (the NormalBP leaf,
+// src/interop/c_abi.cpp:119-200): from the forward's x, pre and post and
+// either the output gradient (use_target false) or an MSE target in g,
+// d_pre [batch][out], dX [batch][in] and dW [out][in]; with a target,
+// loss_part [dpre_blocks(batch * out)] gets the partial sums of the squared
+// differences. ws->d holds the dX partial sums.
+Status dense_backward(const DenseLayer& L, int batch, const float* x, const float* pre,
+                      const float* post, const float* g, bool use_target, float* dpre, float* dx,
+                      float* dw, double* loss_part, Workspace* ws, hipStream_t st);
+// SGD on the quantized store (native_codec.cpp:1080-1133): W <- quantize(
+// f32(f64(dequant(W)) - lr * f64(dW))) with the layer's scheme; the device
+// copy and the host store are replaced.
+Status dense_apply_sgd(DenseLayer* L, const float* dw, double lr, hipStream_t st);
 // True when `batch` rows take the split + batched-MFMA path.
 bool uses_split(int batch);
 // The activation-split workspace (Workspace::b): the split terms, then the

@@ -40,7 +40,7 @@ _LIB = None
 OUT_OF_PATH = (
     "welvet_model_train_credit", "welvet_model_dense_proxy", "welvet_model_forward_pair",
     "welvet_model_backward", "welvet_model_apply_sgd", "welvet_model_train_mse", "welvet_model_sync",
-    "welvet_dense_normalbp_f32", "welvet_rmsnorm_forward_f32", "welvet_rmsnorm_normalbp_f32",
+    "welvet_rmsnorm_forward_f32", "welvet_rmsnorm_normalbp_f32",
     "welvet_layernorm_forward_f32", "welvet_layernorm_normalbp_f32", "welvet_softmax_forward_f32",
     "welvet_softmax_normalbp_f32", "welvet_swiglu_normalbp_f32", "welvet_embedding_forward_f32",
     "welvet_embedding_normalbp_f32", "welvet_mha_normalbp_f32", "welvet_cnn1_forward_f32",
@@ -86,12 +86,17 @@ def lib():
     _sig(L, "welvet_gaps_done", _i32, [])
     _sig(L, "welvet_dense_forward_f32", Status,
          [_i32, _i32, _i32, _i32, _i32, _i32, _fp, _dp, _sz, _fp, _fp, _fp])
+    _sig(L, "welvet_dense_normalbp_f32", Status,
+         [_i32, _i32, _i32, _i32, _i32, _i32, _fp, _dp, _sz, _fp, _fp, _i32, _f64, _fp, _fp, _fp,
+          _fp, _fp, _dp])
     _sig(L, "welvet_dense_mount", Status,
          [_i32, _i32, _i32, _i32, _i32, _fp, _dp, _sz, ctypes.POINTER(_vp)])
     _sig(L, "welvet_dense_mount_q", Status,
          [_i32, _i32, _i32, _i32, _i32, _i32, _fp, _dp, _sz, ctypes.POINTER(_vp)])
     _sig(L, "welvet_dense_execute", Status, [_vp, _fp, _fp, _fp])
     _sig(L, "welvet_dense_execute_device", Status, [_vp, _vp, _vp, _vp, _vp])
+    _sig(L, "welvet_dense_backward_device", Status,
+         [_vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp])
     _sig(L, "welvet_dense_export_store", Status,
          [_vp, _u8p, _sz, ctypes.POINTER(_sz), _fp, _u8p, _fp])
     _sig(L, "welvet_dense_release", None, [_vp])
@@ -369,6 +374,13 @@ class DenseSession:
         check(lib().welvet_dense_execute_device(self.h, _vp(x), _vp(pre), _vp(post),
                                                 _vp(stream) if stream else None))
 
+    def backward_device(self, x, pre, post, g, use_target, dpre, dx, dw, loss_part=None,
+                        stream=None):
+        check(lib().welvet_dense_backward_device(self.h, _vp(x), _vp(pre), _vp(post), _vp(g),
+                                                 1 if use_target else 0, _vp(dpre), _vp(dx),
+                                                 _vp(dw), _vp(loss_part) if loss_part else None,
+                                                 _vp(stream) if stream else None))
+
     def export_store(self, dtype):
         n = self.in_dim * self.out_dim
         cap = n if dtype != FP4 else (n + 1) // 2
@@ -476,6 +488,27 @@ def dense_forward(batch, in_dim, out_dim, act, dtype, scheme, W, x, bias=None):
                                          dptr(b), 0 if b is None else b.size, fptr(x), fptr(pre),
                                          fptr(post)))
     return pre, post
+
+
+def dense_normalbp(batch, in_dim, out_dim, act, dtype, scheme, W, x, grad_or_target,
+                   use_target=False, lr=0.0, bias=None):
+    """welvet_dense_normalbp_f32: forward, backward over the quantized weights
+    and optional SGD. Returns pre, post, dX, dW, W_after, loss."""
+    W = np.ascontiguousarray(W, dtype=np.float32)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    g = np.ascontiguousarray(grad_or_target, dtype=np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float64)
+    pre = np.empty((batch, out_dim), np.float32)
+    post = np.empty_like(pre)
+    dx = np.empty((batch, in_dim), np.float32)
+    dw = np.empty((out_dim, in_dim), np.float32)
+    wa = np.empty((out_dim, in_dim), np.float32)
+    loss = np.zeros(1, np.float64)
+    check(lib().welvet_dense_normalbp_f32(batch, in_dim, out_dim, act, dtype, scheme, fptr(W),
+                                          dptr(b), 0 if b is None else b.size, fptr(x), fptr(g),
+                                          1 if use_target else 0, float(lr), fptr(pre),
+                                          fptr(post), fptr(dx), fptr(dw), fptr(wa), dptr(loss)))
+    return pre, post, dx, dw, wa, float(loss[0])
 
 
 def codec_sweep(dtype, first_chunk=0, n_chunks=4096):
