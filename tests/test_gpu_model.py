@@ -116,3 +116,31 @@ def test_repeated_forwards_reuse_device_buffers(gpu, oracle):
         assert y.shape == (batch, 256)
         assert rel_l2(y, oracle_chain(oracle, layers, x, scheme=2)) <= tol(batch, chain=3), batch
     m.close()
+
+
+@pytest.mark.parametrize("scheme", [2, 3])
+def test_grid_chain_matches_layer_by_layer(gpu, oracle, scheme):
+    """A grid of two Stack cells run as one chain gives the bits of running
+    each layer as its own session (same kernels: split-K products at 200
+    rows, 56 padding rows). Layers: 1024 -> 1024 (SiLU) -> 1024 -> 512 |
+    512 -> 768 -> 256."""
+    rng = np.random.default_rng(10 + scheme)
+    widths = [1024, 1024, 1024, 512, 768, 256]
+    kinds = [(4, 1), (16, -1), (5, -1), (4, 0), (16, -1)]
+    seq = [(dt, (rng.standard_normal((widths[i + 1], widths[i])) / np.sqrt(widths[i])).astype(np.float32), act)
+           for i, (dt, act) in enumerate(kinds)]
+    cells = [(1, 0, 0, 0, 0, 0), (1, 0, 0, 0, 0, 0)]
+    m = pw.ModelSession(build_stack([seq[:3], seq[3:]], root=2, dims=(2, 1, 1, 1), cells=cells),
+                        scheme=scheme)
+    x = rng.standard_normal((200, 1024)).astype(np.float32)
+    y = m.forward(x)
+    cur = x
+    for dt, W, act in seq:
+        s = pw.DenseSession(200, W.shape[1], W.shape[0], act, dt, scheme, W)
+        _, cur = s.execute(cur)
+        s.close()
+    assert np.array_equal(y, cur)
+    assert rel_l2(y, oracle_chain(oracle, seq, x, scheme)) <= tol(200, chain=5)
+    y2 = m.forward(x)  # a second pass over the same buffers
+    assert np.array_equal(y2, y)
+    m.close()
