@@ -144,3 +144,118 @@ def test_grid_chain_matches_layer_by_layer(gpu, oracle, scheme):
     y2 = m.forward(x)  # a second pass over the same buffers
     assert np.array_equal(y2, y)
     m.close()
+
+
+def parse_nws1(snap):
+    """Stores of an NWS1 snapshot: (dtype, rows, cols, scale, native bytes)."""
+    assert snap[:4] == b"NWS1"
+    n = int(np.frombuffer(snap[4:8], "<i4")[0])
+    off, out = 8, []
+    for _ in range(n):
+        dt, rows, cols = np.frombuffer(snap[off:off + 12], "<i4").tolist()
+        scale = float(np.frombuffer(snap[off + 12:off + 16], "<f4")[0])
+        nf = int(np.frombuffer(snap[off + 16:off + 20], "<i4")[0])
+        off += 20 + 4 * nf
+        nn = int(np.frombuffer(snap[off:off + 4], "<i4")[0])
+        native = np.frombuffer(snap[off + 4:off + 4 + nn], np.uint8)
+        off += 4 + nn
+        nb = int(np.frombuffer(snap[off:off + 4], "<i4")[0])
+        off += 4 + 8 * nb
+        out.append((dt, rows, cols, scale, native))
+    return out
+
+
+def _segment_layers(rng):
+    dims = [96, 128, 64, 80]
+    return [(dt, (rng.standard_normal((dims[i + 1], dims[i])) / np.sqrt(dims[i])).astype(np.float32), act)
+            for i, (dt, act) in enumerate([(4, 0), (16, -1), (5, 1)])]
+
+
+@pytest.mark.parametrize("scheme,batch", [(0, 3), (2, 40), (3, 1)])
+def test_segment_backward_matches_layer_by_layer(gpu, oracle, scheme, batch):
+    """welvet_model_backward of a Stack (model_session.cpp:435-455): the
+    input gradient and the concatenated dW are the bits of running the Dense
+    NormalBP leaf layer by layer in reverse on the forward's activations
+    (same kernels), and match the oracle's chain within the chained bound."""
+    rng = np.random.default_rng(20 + scheme + batch)
+    layers = _segment_layers(rng)
+    m = pw.ModelSession(build_stack([layers]), scheme=scheme)
+    x = rng.standard_normal((batch, 96)).astype(np.float32)
+    gy = rng.standard_normal((batch, 80)).astype(np.float32)
+    gx, dw = m.backward(x, gy)
+    assert gx.shape == (batch, 96) and dw.shape == (1, 128 * 96 + 64 * 128 + 80 * 64)
+    ins, cur = [], x
+    for dt, W, act in layers:
+        ins.append(cur)
+        _, cur = pw.dense_forward(batch, W.shape[1], W.shape[0], act, dt, scheme, W, cur)
+    g, parts = gy, []
+    for (dt, W, act), xi in reversed(list(zip(layers, ins))):
+        _, _, g, dwi, _, _ = pw.dense_normalbp(batch, W.shape[1], W.shape[0], act, dt, scheme, W, xi, g)
+        parts.insert(0, dwi.ravel())
+    assert np.array_equal(gx, g)
+    assert np.array_equal(dw.ravel(), np.concatenate(parts))
+    # the oracle's chain: its own forward, then the backward in reverse
+    Wd = []
+    for dt, W, _ in layers:
+        native, rs, blk = oracle.quantize(dt, scheme, W.shape[0], W.shape[1], W)
+        Wd.append(oracle.dequant(dt, scheme, W.shape[0], W.shape[1], native, rs, blk))
+    ins_o, pres_o, cur = [], [], x
+    for (dt, W, act), Wq in zip(layers, Wd):
+        ins_o.append(cur)
+        pre, cur = oracle.dense(Wq, cur, act)
+        pres_o.append(pre)
+    g, parts = gy, []
+    for (dt, W, act), Wq, xi, pre in reversed(list(zip(layers, Wd, ins_o, pres_o))):
+        _, g, dwi = oracle.backward(Wq, g, pre, xi, act)
+        parts.insert(0, dwi.ravel())
+    assert rel_l2(gx, g) <= 1e-4 and rel_l2(dw.ravel(), np.concatenate(parts)) <= 1e-4
+    m.close()
+
+
+@pytest.mark.parametrize("scheme", [0, 2, 3])
+def test_segment_sgd_requantizes_every_store(gpu, oracle, scheme):
+    """welvet_model_apply_sgd (model_session.cpp:494-507, stack.cpp:561-580):
+    each Dense store becomes quantize(f32(f64(dequant(W)) - lr * f64(dW slice)))
+    with the model's scheme; the exported payloads match the oracle's bytes."""
+    rng = np.random.default_rng(30 + scheme)
+    layers = _segment_layers(rng)
+    m = pw.ModelSession(build_stack([layers]), scheme=scheme)
+    x = rng.standard_normal((8, 96)).astype(np.float32)
+    _, dw = m.backward(x, rng.standard_normal((8, 80)).astype(np.float32))
+    lr = 0.25
+    m.apply_sgd(dw, lr)
+    stores = parse_nws1(m.export())
+    off = 0
+    for (dt, W, _), (sdt, rows, cols, _, native) in zip(layers, stores):
+        n = W.size
+        nat, rs, blk = oracle.quantize(dt, scheme, rows, cols, W)
+        Wq = oracle.dequant(dt, scheme, rows, cols, nat, rs, blk)
+        nxt = oracle.sgd(Wq, dw.ravel()[off:off + n].reshape(W.shape), lr)
+        nat2, _, _ = oracle.quantize(dt, scheme, rows, cols, nxt)
+        assert sdt == dt and np.array_equal(native, nat2), dt
+        off += n
+    m.close()
+
+
+def test_segment_training_errors(gpu):
+    rng = np.random.default_rng(40)
+    layers = _segment_layers(rng)
+    m = pw.ModelSession(build_stack([layers]))
+    x = rng.standard_normal((2, 96)).astype(np.float32)
+    with pytest.raises(pw.WelvetError) as e:  # gradient of the wrong shape
+        m.backward(x, np.zeros((2, 79), np.float32))
+    assert e.value.code == 1
+    with pytest.raises(pw.WelvetError) as e:  # dW of the wrong size
+        m.apply_sgd(np.zeros((1, 7), np.float32), 0.1)
+    assert e.value.code == 1
+    with pytest.raises(pw.WelvetError) as e:
+        m.apply_sgd(np.zeros((1, 7), np.float32), float("nan"))
+    assert e.value.code == 1
+    m.close()
+    W = (rng.standard_normal((32, 32)) / 4).astype(np.float32)
+    g = pw.ModelSession(build_stack([[(4, W, -1)]], root=2, dims=(1, 1, 1, 1),
+                                    cells=[(1, 0, 0, 0, 0, 0)]))
+    with pytest.raises(pw.WelvetError) as e:  # segment calls take Stack roots
+        g.backward(np.zeros((1, 32), np.float32), np.zeros((1, 32), np.float32))
+    assert e.value.code == 1
+    g.close()

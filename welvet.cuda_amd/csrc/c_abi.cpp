@@ -5,6 +5,7 @@
 
 #include <cstdio>
 #include <cstdlib>
+#include <cmath>
 #include <cstring>
 #include <memory>
 #include <mutex>
@@ -736,12 +737,110 @@ welvet_status welvet_model_forward_pair(welvet_model_session*, const uint8_t*, s
                                         welvet_cuda_blob*) {
   return gap("model forward pair");
 }
-welvet_status welvet_model_backward(welvet_model_session*, const uint8_t*, size_t,
-                                    welvet_cuda_blob*) {
-  return gap("model backward");
+// A model-wire tensor (model_session.cpp tensor(): int32 rank 1..5, the
+// dims, float32 data) read at *off; *data points into the blob.
+static Status read_tensor(const uint8_t* p, size_t size, size_t* off, std::vector<int>* shape,
+                          const float** data, size_t* n) {
+  auto rd = [&](void* dst, size_t k) {
+    if (size - *off < k) return false;
+    std::memcpy(dst, p + *off, k);
+    *off += k;
+    return true;
+  };
+  int32_t rank = 0;
+  if (!rd(&rank, 4) || rank <= 0 || rank > 5) return Status::err(wv::kInvalid, "tensor rank must be 1..5");
+  shape->assign((size_t)rank, 0);
+  *n = 1;
+  for (auto& d : *shape) {
+    int32_t v = 0;
+    if (!rd(&v, 4) || v <= 0 || *n > (size_t(1) << 26) / (size_t)v)
+      return Status::err(wv::kInvalid, "invalid tensor shape");
+    d = v;
+    *n *= (size_t)v;
+  }
+  if ((size - *off) / 4 < *n) return Status::err(wv::kInvalid, "short tensor data");
+  *data = reinterpret_cast<const float*>(p + *off);
+  *off += *n * 4;
+  return Status::ok();
 }
-welvet_status welvet_model_apply_sgd(welvet_model_session*, double, const uint8_t*, size_t) {
-  return gap("model SGD");
+
+static void put_tensor(std::vector<uint8_t>* blob, const std::vector<int>& shape, size_t n,
+                       size_t* data_at) {
+  auto put = [&](const void* q, size_t k) {
+    const uint8_t* b = static_cast<const uint8_t*>(q);
+    blob->insert(blob->end(), b, b + k);
+  };
+  const int32_t rank = (int32_t)shape.size();
+  put(&rank, 4);
+  for (int d : shape) {
+    const int32_t v = d;
+    put(&v, 4);
+  }
+  const int32_t cnt = (int32_t)n;
+  put(&cnt, 4);
+  *data_at = blob->size();
+  blob->resize(blob->size() + n * 4);
+}
+
+// Segment backward (reference model_session.cpp:435-455): x and gy in, the
+// input gradient and the concatenated dW (shape [1, n]) out.
+welvet_status welvet_model_backward(welvet_model_session* s, const uint8_t* data, size_t size,
+                                    welvet_cuda_blob* out) {
+  if (!s || !data || !out) return invalid("invalid segment backward arguments");
+  out->data = nullptr;
+  out->size = 0;
+  return guarded([&]() -> Status {
+    std::lock_guard<std::mutex> lock(s->mu);
+    size_t off = 0, nx = 0, ng = 0;
+    std::vector<int> xs, gs;
+    const float *hx = nullptr, *hg = nullptr;
+    WV_TRY(read_tensor(data, size, &off, &xs, &hx, &nx));
+    WV_TRY(read_tensor(data, size, &off, &gs, &hg, &ng));
+    if (off != size) return Status::err(wv::kInvalid, "trailing descriptor bytes");
+    hipStream_t st = s->stream.s;
+    wv::DevBuf dx, dg;
+    WV_TRY(dx.alloc(nx * 4));
+    WV_TRY(dg.alloc(ng * 4));
+    WV_HIP(hipMemcpyAsync(dx.p, hx, nx * 4, hipMemcpyHostToDevice, st));
+    WV_HIP(hipMemcpyAsync(dg.p, hg, ng * 4, hipMemcpyHostToDevice, st));
+    const float *gx = nullptr, *dw = nullptr;
+    size_t nw = 0;
+    WV_TRY(wv::model_backward(s->model, xs, dx.as<float>(), gs, dg.as<float>(), &gx, &dw, &nw, st));
+    std::vector<uint8_t> blob;
+    size_t at_x = 0, at_w = 0;
+    put_tensor(&blob, xs, nx, &at_x);
+    put_tensor(&blob, {1, (int)nw}, nw, &at_w);
+    WV_HIP(hipMemcpyAsync(blob.data() + at_x, gx, nx * 4, hipMemcpyDeviceToHost, st));
+    if (nw) WV_HIP(hipMemcpyAsync(blob.data() + at_w, dw, nw * 4, hipMemcpyDeviceToHost, st));
+    WV_HIP(hipStreamSynchronize(st));
+    out->data = static_cast<uint8_t*>(std::malloc(blob.size()));
+    if (!out->data) return Status::err(wv::kInternal, "out of host memory");
+    std::memcpy(out->data, blob.data(), blob.size());
+    out->size = blob.size();
+    return Status::ok();
+  });
+}
+
+// Segment SGD (reference model_session.cpp:494-507): one tensor, the
+// concatenated dW; each Dense store is updated and re-quantized.
+welvet_status welvet_model_apply_sgd(welvet_model_session* s, double lr, const uint8_t* data,
+                                     size_t size) {
+  if (!s || !data || !std::isfinite(lr)) return invalid("invalid segment SGD arguments");
+  return guarded([&]() -> Status {
+    std::lock_guard<std::mutex> lock(s->mu);
+    size_t off = 0, n = 0;
+    std::vector<int> shape;
+    const float* hw = nullptr;
+    WV_TRY(read_tensor(data, size, &off, &shape, &hw, &n));
+    if (off != size) return Status::err(wv::kInvalid, "trailing descriptor bytes");
+    hipStream_t st = s->stream.s;
+    wv::DevBuf d;
+    WV_TRY(d.alloc(n * 4));
+    WV_HIP(hipMemcpyAsync(d.p, hw, n * 4, hipMemcpyHostToDevice, st));
+    WV_TRY(wv::model_apply_sgd(s->model, d.as<float>(), n, lr, st));
+    WV_HIP(hipStreamSynchronize(st));
+    return Status::ok();
+  });
 }
 welvet_status welvet_model_train_mse(welvet_model_session*, int32_t, double, int32_t,
                                      const uint8_t*, size_t, double*) {

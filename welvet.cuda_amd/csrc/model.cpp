@@ -307,7 +307,10 @@ struct Arena {
 };
 
 // One op (stack.cpp:58ff child_forward) on device tensors; returns post.
-Tensor op_forward(ModelNode& c, const Tensor& in, Arena& ar, Workspace* ws, hipStream_t st) {
+// pre_out (Dense) receives the pre-activation (post itself when the layer
+// has no epilogue).
+Tensor op_forward(ModelNode& c, const Tensor& in, Arena& ar, Workspace* ws, hipStream_t st,
+                  Tensor* pre_out = nullptr) {
   Tensor out;
   switch (c.kind) {
   case 1: {
@@ -319,6 +322,10 @@ Tensor op_forward(ModelNode& c, const Tensor& in, Arena& ar, Workspace* ws, hipS
     float* pre = c.dense->need_epi() ? ar.get(out.numel()) : nullptr;
     if (pre) good(dense_forward(*c.dense, b, in.data, pre, out.data, ws, st));
     else good(dense_forward(*c.dense, b, in.data, out.data, nullptr, ws, st));
+    if (pre_out) {
+      pre_out->shape = out.shape;
+      pre_out->data = pre ? pre : out.data;
+    }
     break;
   }
   case 4: {
@@ -477,6 +484,97 @@ Status model_forward_view(Model& m, const std::vector<int>& in_shape, const floa
   } catch (const std::exception& e) {
     return Status::err(kInternal, e.what());
   }
+}
+
+namespace {
+
+// The ops of a Stack model for the segment training calls: Dense only here
+// (the other children's backward is not part of this build).
+std::vector<ModelNode*> dense_ops(Model& m) {
+  require(m.root == 0, "segment backward expects Stack or Parallel");
+  std::vector<ModelNode*> ops;
+  for (auto& c : m.children) flatten(c, &ops);
+  for (ModelNode* op : ops)
+    if (op->kind != 1)
+      throw StatusError(Status::err(kGap, "gap? segment backward of SwiGLU / MHA children is "
+                                          "outside the quantized Dense path of this build"));
+  return ops;
+}
+
+template <class F>
+Status model_guard(F&& fn) {
+  try {
+    fn();
+    return Status::ok();
+  } catch (const StatusError& e) {
+    return Status::err(e.code, e.what());
+  } catch (const std::invalid_argument& e) {
+    return Status::err(kInvalid, e.what());
+  } catch (const std::exception& e) {
+    return Status::err(kInternal, e.what());
+  }
+}
+
+}  // namespace
+
+Status model_backward(Model& m, const std::vector<int>& in_shape, const float* x,
+                      const std::vector<int>& gy_shape, const float* gy, const float** gx,
+                      const float** dw, size_t* dw_n, hipStream_t st) {
+  return model_guard([&] {
+    std::vector<ModelNode*> ops = dense_ops(m);
+    require(in_shape.size() == 2, "dense: input shape need [batch,in]");
+    m.scratch.next = 0;
+    Arena ar{m.scratch};
+    Workspace& ws = m.scratch.ws;
+    // recompute the forward, keeping each op's input and pre-activation
+    // (stack.cpp:519-530)
+    Tensor cur;
+    cur.shape = in_shape;
+    cur.data = const_cast<float*>(x);
+    std::vector<Tensor> ins, pres;
+    for (ModelNode* op : ops) {
+      ins.push_back(cur);
+      Tensor pre;
+      cur = op_forward(*op, cur, ar, &ws, st, &pre);
+      pres.push_back(pre);
+    }
+    require(gy_shape == cur.shape, "segment output gradient shape mismatch");
+    size_t total = 0;
+    for (ModelNode* op : ops) total += (size_t)op->dense->out * op->dense->in;
+    float* dwall = ar.get(total > 0 ? total : 1);
+    // backward in reverse (stack.cpp:532-557): op i's input gradient is op
+    // i - 1's output gradient; dW slices in op order
+    const int b = in_shape[0];
+    const float* g = gy;
+    size_t off = total;
+    for (size_t k = ops.size(); k-- > 0;) {
+      DenseLayer& L = *ops[k]->dense;
+      off -= (size_t)L.out * L.in;
+      float* dpre = ar.get((size_t)b * L.out);
+      float* dxk = ar.get((size_t)b * L.in);
+      good(dense_backward(L, b, ins[k].data, pres[k].data, nullptr, g, false, dpre, dxk,
+                          dwall + off, nullptr, &ws, st));
+      g = dxk;
+    }
+    good(hip_status(hipStreamSynchronize(st), "segment backward"));
+    *gx = g;
+    *dw = dwall;
+    *dw_n = total;
+  });
+}
+
+Status model_apply_sgd(Model& m, const float* dw, size_t n, double lr, hipStream_t st) {
+  return model_guard([&] {
+    std::vector<ModelNode*> ops = dense_ops(m);
+    size_t total = 0;
+    for (ModelNode* op : ops) total += (size_t)op->dense->out * op->dense->in;
+    require(n == total, "segment weight gradient size mismatch");
+    size_t off = 0;
+    for (ModelNode* op : ops) {
+      good(dense_apply_sgd(op->dense.get(), dw + off, lr, st));
+      off += (size_t)op->dense->out * op->dense->in;
+    }
+  });
 }
 
 Status model_forward(Model& m, const std::vector<int>& in_shape, const float* x,

@@ -39,7 +39,7 @@ class WelvetError(RuntimeError):
 _LIB = None
 OUT_OF_PATH = (
     "welvet_model_train_credit", "welvet_model_dense_proxy", "welvet_model_forward_pair",
-    "welvet_model_backward", "welvet_model_apply_sgd", "welvet_model_train_mse", "welvet_model_sync",
+    "welvet_model_train_mse", "welvet_model_sync",
     "welvet_rmsnorm_forward_f32", "welvet_rmsnorm_normalbp_f32",
     "welvet_layernorm_forward_f32", "welvet_layernorm_normalbp_f32", "welvet_softmax_forward_f32",
     "welvet_softmax_normalbp_f32", "welvet_swiglu_normalbp_f32", "welvet_embedding_forward_f32",
@@ -127,6 +127,8 @@ def lib():
     _sig(L, "welvet_model_forward", Status, [_vp, _u8p, _sz, ctypes.POINTER(Blob)])
     _sig(L, "welvet_model_forward_device", Status, [_vp, _vp, _i32, _i32, _vp, _i32, _vp])
     _sig(L, "welvet_model_export_weights", Status, [_vp, ctypes.POINTER(Blob)])
+    _sig(L, "welvet_model_backward", Status, [_vp, _u8p, _sz, ctypes.POINTER(Blob)])
+    _sig(L, "welvet_model_apply_sgd", Status, [_vp, _f64, _u8p, _sz])
     _sig(L, "welvet_model_release", None, [_vp])
     _sig(L, "welvet_cuda_blob_free", None, [ctypes.POINTER(Blob)])
     _sig(L, "welvet_codec_sweep", Status, [_i32, _u32, _u32, _i64p])
@@ -605,6 +607,39 @@ class ModelSession:
         data = np.frombuffer(raw[8 + 4 * rank:], "<f4")
         assert data.size == count
         return data.reshape(shape)
+
+    @staticmethod
+    def _tensors(raw, n):
+        """n model-wire tensors (rank, dims, count, float32 data) from a blob."""
+        out, off = [], 0
+        for _ in range(n):
+            rank = int(np.frombuffer(raw[off:off + 4], "<i4")[0])
+            shape = tuple(np.frombuffer(raw[off + 4:off + 4 + 4 * rank], "<i4").tolist())
+            off += 4 + 4 * rank
+            count = int(np.frombuffer(raw[off:off + 4], "<i4")[0])
+            off += 4
+            out.append(np.frombuffer(raw[off:off + 4 * count], "<f4").reshape(shape).copy())
+            off += 4 * count
+        assert off == len(raw)
+        return out
+
+    def backward(self, x, gy):
+        """welvet_model_backward: (input gradient, concatenated dW [1, n])."""
+        data = np.frombuffer(tensor_bytes(np.ascontiguousarray(x, np.float32))
+                             + tensor_bytes(np.ascontiguousarray(gy, np.float32)), np.uint8).copy()
+        blob = Blob()
+        check(lib().welvet_model_backward(self.h, data.ctypes.data_as(_u8p), data.size,
+                                          ctypes.byref(blob)))
+        try:
+            raw = bytes(ctypes.cast(blob.data, ctypes.POINTER(ctypes.c_uint8 * blob.size)).contents)
+        finally:
+            lib().welvet_cuda_blob_free(ctypes.byref(blob))
+        gx, dw = self._tensors(raw, 2)
+        return gx, dw
+
+    def apply_sgd(self, dw, lr):
+        data = np.frombuffer(tensor_bytes(np.ascontiguousarray(dw, np.float32)), np.uint8).copy()
+        check(lib().welvet_model_apply_sgd(self.h, float(lr), data.ctypes.data_as(_u8p), data.size))
 
     def forward_device(self, x, batch, width, y, y_cap, stream=None):
         check(lib().welvet_model_forward_device(self.h, _vp(x), batch, width, _vp(y), y_cap,
