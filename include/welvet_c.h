@@ -222,6 +222,18 @@ WELVET_API welvet_status welvet_codec_sweep(int32_t dtype, uint32_t first_chunk,
  * children give code 3 ("gap?"), Grid roots code 1. */
 WELVET_API welvet_status welvet_model_backward(welvet_model_session*, const uint8_t*, size_t,
                                                welvet_cuda_blob*);
+/* Segment forward (replaces reference include/welvet_c.h:54,
+ * model_session.cpp:420-434): x in; the blob holds the last op's
+ * pre-activation and the output (Stack roots; a Dense last op here). */
+WELVET_API welvet_status welvet_model_forward_pair(welvet_model_session*, const uint8_t*, size_t,
+                                                   welvet_cuda_blob*);
+/* Dense proxy of a Stack holding one Dense (replaces reference
+ * include/welvet_c.h:52, model_session.cpp:475-493): x, gy, int32 flag, and
+ * with flag 1 pre; gy is remapped to batch*out values (dense.cpp:121-139).
+ * kind 0: the linear input gradient [batch, in]; kind 1: dW [out, in] with
+ * act' at pre (zeros when absent or short). */
+WELVET_API welvet_status welvet_model_dense_proxy(welvet_model_session*, int32_t, const uint8_t*,
+                                                  size_t, welvet_cuda_blob*);
 /* Segment SGD (replaces reference include/welvet_c.h:56, model_session.cpp:
  * 494-507): one tensor, the concatenated dW; every Dense store becomes
  * quantize(f32(f64(W) - lr dW)) with the session's scale scheme. */
@@ -246,10 +258,6 @@ WELVET_API welvet_status welvet_dense_normalbp_f32(
  * 175-386. */
 WELVET_API welvet_status welvet_model_train_credit(welvet_model_session*, int32_t, double,
                                                    const uint8_t*, size_t);
-WELVET_API welvet_status welvet_model_dense_proxy(welvet_model_session*, int32_t, const uint8_t*,
-                                                  size_t, welvet_cuda_blob*);
-WELVET_API welvet_status welvet_model_forward_pair(welvet_model_session*, const uint8_t*, size_t,
-                                                   welvet_cuda_blob*);
 WELVET_API welvet_status welvet_model_train_mse(welvet_model_session*, int32_t mode, double lr,
                                                 int32_t ticks, const uint8_t*, size_t,
                                                 double* loss);

@@ -259,3 +259,59 @@ def test_segment_training_errors(gpu):
         g.backward(np.zeros((1, 32), np.float32), np.zeros((1, 32), np.float32))
     assert e.value.code == 1
     g.close()
+
+
+@pytest.mark.parametrize("batch", [3, 40])
+def test_segment_forward_pair(gpu, batch):
+    """welvet_model_forward_pair: the last op's pre-activation and the output,
+    the bits of the layers run one by one."""
+    rng = np.random.default_rng(50 + batch)
+    layers = _segment_layers(rng)  # last op SiLU: pre and post differ
+    m = pw.ModelSession(build_stack([layers]), scheme=2)
+    x = rng.standard_normal((batch, 96)).astype(np.float32)
+    pre, post = m.forward_pair(x)
+    cur = x
+    for dt, W, act in layers:
+        want_pre, cur = pw.dense_forward(batch, W.shape[1], W.shape[0], act, dt, 2, W, cur)
+    assert np.array_equal(pre, want_pre) and np.array_equal(post, cur)
+    assert not np.array_equal(pre, post)
+    m.close()
+
+
+@pytest.mark.parametrize("dt,scheme,act", [(4, 2, 1), (16, 3, 0), (5, 0, 2)])
+def test_segment_dense_proxy(gpu, oracle, dt, scheme, act):
+    """welvet_model_dense_proxy (dense.cpp:141-191): kind 0 is the linear
+    input gradient (act' = 1), kind 1 dW with act' at the given pre, at zeros
+    without one; a gradient of another length is remapped by range means."""
+    rng = np.random.default_rng(60 + dt)
+    W = (rng.standard_normal((48, 80)) / 9).astype(np.float32)
+    # a Stack whose single child is the Dense itself (not a NestedStack)
+    w = pw.Wire()
+    w.u32(0x314E4D57)
+    w.i32(0, 1, 1, 1, 1, 1)
+    pw.dense_child(w, 80, 48, act, dt, W)
+    pw.empty_controls(w)
+    pw.empty_controls(w)
+    w.i32(1)
+    pw.store_payload(w, dt, 48, 80, oracle.pack(dt, W))
+    m = pw.ModelSession(w.bytes(), scheme=scheme)
+    x = rng.standard_normal((5, 80)).astype(np.float32)
+    gy = rng.standard_normal((5, 48)).astype(np.float32)
+    pre, _, dx_lin, _, _, _ = pw.dense_normalbp(5, 80, 48, -1, dt, scheme, W, x, gy)
+    gx = m.dense_proxy(0, x, gy)
+    assert gx.shape == (5, 80) and np.array_equal(gx, dx_lin)
+    pre_a, _, _, dw_a, _, _ = pw.dense_normalbp(5, 80, 48, act, dt, scheme, W, x, gy)
+    assert np.array_equal(m.dense_proxy(1, x, gy, pre_a), dw_a)
+    native, rs, blk = oracle.quantize(dt, scheme, 48, 80, W)
+    Wd = oracle.dequant(dt, scheme, 48, 80, native, rs, blk)
+    _, _, dw_z = oracle.backward(Wd, gy, np.zeros((5, 48), np.float32), x, act)
+    got = m.dense_proxy(1, x, gy)
+    if act in (0, 5, 6, -1):
+        assert np.array_equal(got, dw_z)
+    else:
+        assert rel_l2(got, dw_z) <= 1e-6
+    # a gradient twice as long: each value the mean of a pair (f64, then f32)
+    g2 = rng.standard_normal(2 * 5 * 48).astype(np.float32)
+    mean = ((g2[0::2].astype(np.float64) + g2[1::2].astype(np.float64)) / 2).astype(np.float32)
+    assert np.array_equal(m.dense_proxy(0, x, g2.reshape(10, 48)), m.dense_proxy(0, x, mean.reshape(5, 48)))
+    m.close()

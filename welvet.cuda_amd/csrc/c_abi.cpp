@@ -729,14 +729,6 @@ welvet_status welvet_model_train_credit(welvet_model_session*, int32_t, double, 
                                         size_t) {
   return gap("model train credit");
 }
-welvet_status welvet_model_dense_proxy(welvet_model_session*, int32_t, const uint8_t*, size_t,
-                                       welvet_cuda_blob*) {
-  return gap("model dense proxy");
-}
-welvet_status welvet_model_forward_pair(welvet_model_session*, const uint8_t*, size_t,
-                                        welvet_cuda_blob*) {
-  return gap("model forward pair");
-}
 // A model-wire tensor (model_session.cpp tensor(): int32 rank 1..5, the
 // dims, float32 data) read at *off; *data points into the blob.
 static Status read_tensor(const uint8_t* p, size_t size, size_t* off, std::vector<int>* shape,
@@ -818,6 +810,125 @@ welvet_status welvet_model_backward(welvet_model_session* s, const uint8_t* data
     std::memcpy(out->data, blob.data(), blob.size());
     out->size = blob.size();
     return Status::ok();
+  });
+}
+
+static Status blob_out(const std::vector<uint8_t>& blob, welvet_cuda_blob* out) {
+  out->data = static_cast<uint8_t*>(std::malloc(blob.size()));
+  if (!out->data) return Status::err(wv::kInternal, "out of host memory");
+  std::memcpy(out->data, blob.data(), blob.size());
+  out->size = blob.size();
+  return Status::ok();
+}
+
+// Segment forward (reference model_session.cpp:420-434): x in; the last
+// op's pre-activation and the output out.
+welvet_status welvet_model_forward_pair(welvet_model_session* s, const uint8_t* data, size_t size,
+                                        welvet_cuda_blob* out) {
+  if (!s || !data || !out) return invalid("invalid segment forward arguments");
+  out->data = nullptr;
+  out->size = 0;
+  return guarded([&]() -> Status {
+    std::lock_guard<std::mutex> lock(s->mu);
+    size_t off = 0, nx = 0;
+    std::vector<int> xs;
+    const float* hx = nullptr;
+    WV_TRY(read_tensor(data, size, &off, &xs, &hx, &nx));
+    if (off != size) return Status::err(wv::kInvalid, "trailing descriptor bytes");
+    hipStream_t st = s->stream.s;
+    wv::DevBuf& dx = s->model.scratch.in;
+    if (dx.bytes < nx * 4) WV_TRY(dx.alloc(nx * 4));
+    WV_HIP(hipMemcpyAsync(dx.p, hx, nx * 4, hipMemcpyHostToDevice, st));
+    std::vector<int> shape;
+    const float *pre = nullptr, *post = nullptr;
+    WV_TRY(wv::model_forward_pair(s->model, xs, dx.as<float>(), &shape, &pre, &post, st));
+    size_t n = 1;
+    for (int d : shape) n *= (size_t)d;
+    std::vector<uint8_t> blob;
+    size_t at_pre = 0, at_post = 0;
+    put_tensor(&blob, shape, n, &at_pre);
+    put_tensor(&blob, shape, n, &at_post);
+    WV_HIP(hipMemcpyAsync(blob.data() + at_pre, pre, n * 4, hipMemcpyDeviceToHost, st));
+    WV_HIP(hipMemcpyAsync(blob.data() + at_post, post, n * 4, hipMemcpyDeviceToHost, st));
+    WV_HIP(hipStreamSynchronize(st));
+    return blob_out(blob, out);
+  });
+}
+
+// remap_gap_len (reference src/layers/dense/dense.cpp:121-139): src resized
+// to `need` values; a different length averages ranges of src in f64.
+static std::vector<float> remap_len(const float* src, size_t sn, size_t need) {
+  std::vector<float> out(need, 0.0f);
+  if (sn == 0 || need == 0) return out;
+  if (sn == need) {
+    std::memcpy(out.data(), src, need * sizeof(float));
+    return out;
+  }
+  for (size_t i = 0; i < need; ++i) {
+    size_t lo = i * sn / need, hi = (i + 1) * sn / need;
+    if (hi <= lo) hi = lo + 1;
+    if (hi > sn) hi = sn;
+    double sum = 0.0;
+    for (size_t j = lo; j < hi; ++j) sum += (double)src[j];
+    out[i] = (float)(sum / (double)(hi - lo));
+  }
+  return out;
+}
+
+// Dense proxy (reference model_session.cpp:475-493) of a Stack holding one
+// Dense: x, gy, an int32 flag and (flag 1) pre in; kind 0 the linear input
+// gradient [batch, in], kind 1 dW [out, in] out.
+welvet_status welvet_model_dense_proxy(welvet_model_session* s, int32_t kind, const uint8_t* data,
+                                       size_t size, welvet_cuda_blob* out) {
+  if (!s || !data || !out || kind < 0 || kind > 1) return invalid("invalid Dense proxy arguments");
+  out->data = nullptr;
+  out->size = 0;
+  return guarded([&]() -> Status {
+    std::lock_guard<std::mutex> lock(s->mu);
+    wv::Model& m = s->model;
+    if (m.root != 0 || m.children.size() != 1 || m.children[0].kind != 1)
+      return Status::err(wv::kInvalid, "proxy expects one Dense");
+    const wv::DenseLayer& L = *m.children[0].dense;
+    size_t off = 0, nx = 0, ng = 0, np = 0;
+    std::vector<int> xs, gs, ps;
+    const float *hx = nullptr, *hg = nullptr, *hp = nullptr;
+    WV_TRY(read_tensor(data, size, &off, &xs, &hx, &nx));
+    WV_TRY(read_tensor(data, size, &off, &gs, &hg, &ng));
+    int32_t present = 0;
+    if (size - off < 4) return Status::err(wv::kInvalid, "short descriptor");
+    std::memcpy(&present, data + off, 4);
+    off += 4;
+    if (present != 0 && present != 1) return Status::err(wv::kInvalid, "invalid pre flag");
+    if (present) WV_TRY(read_tensor(data, size, &off, &ps, &hp, &np));
+    if (off != size) return Status::err(wv::kInvalid, "trailing descriptor bytes");
+    if (xs.size() != 2 || xs[0] <= 0 || ng == 0 || (size_t)xs[0] * L.in != nx)
+      return Status::err(wv::kInvalid, kind == 0 ? "dense: LinearGradIn shape" : "dense: GradWOnly shape");
+    const size_t b = (size_t)xs[0], ny = b * L.out;
+    const std::vector<float> g = remap_len(hg, ng, ny);
+    // kind 1 uses pre only when it is 2-D and long enough (dense.cpp:183-187)
+    const bool use_pre = kind == 1 && present && ps.size() == 2 && np >= ny;
+    hipStream_t st = s->stream.s;
+    wv::DevBuf dx, dg, dp;
+    WV_TRY(dx.alloc(nx * 4));
+    WV_TRY(dg.alloc(ny * 4));
+    WV_HIP(hipMemcpyAsync(dx.p, hx, nx * 4, hipMemcpyHostToDevice, st));
+    WV_HIP(hipMemcpyAsync(dg.p, g.data(), ny * 4, hipMemcpyHostToDevice, st));
+    if (use_pre) {
+      WV_TRY(dp.alloc(ny * 4));
+      WV_HIP(hipMemcpyAsync(dp.p, hp, ny * 4, hipMemcpyHostToDevice, st));
+    }
+    const float* res = nullptr;
+    WV_TRY(wv::model_dense_proxy(m, kind, xs, dx.as<float>(), dg.as<float>(),
+                                 use_pre ? dp.as<float>() : nullptr, &res, st));
+    const std::vector<int> shape = kind == 0 ? std::vector<int>{(int)b, L.in}
+                                             : std::vector<int>{L.out, L.in};
+    const size_t n = (size_t)shape[0] * shape[1];
+    std::vector<uint8_t> blob;
+    size_t at = 0;
+    put_tensor(&blob, shape, n, &at);
+    WV_HIP(hipMemcpyAsync(blob.data() + at, res, n * 4, hipMemcpyDeviceToHost, st));
+    WV_HIP(hipStreamSynchronize(st));
+    return blob_out(blob, out);
   });
 }
 

@@ -261,11 +261,13 @@ Status dense_forward(const DenseLayer& L, int batch, const float* x, float* pre,
 // ---------------------------------------------------------------------------
 Status dense_backward(const DenseLayer& L, int batch, const float* x, const float* pre,
                       const float* post, const float* g, bool use_target, float* dpre, float* dx,
-                      float* dw, double* loss_part, Workspace* ws, hipStream_t st) {
+                      float* dw, double* loss_part, Workspace* ws, hipStream_t st,
+                      bool linear_act) {
   if (batch <= 0 || !x || !pre || !g || !dpre || !dx || !dw || !ws || (use_target && !post))
     return Status::err(kInvalid, "dense backward: bad args");
   const int64_t n = (int64_t)batch * L.out;
-  WV_TRY(launch_dpre(g, post, pre, L.act, use_target ? 1 : 0, n, dpre, loss_part, st));
+  WV_TRY(launch_dpre(g, post, pre, linear_act ? kLinear : L.act, use_target ? 1 : 0, n, dpre,
+                     loss_part, st));
   const size_t pb = gemvt_part_bytes(L.in, L.out);
   if (ws->d.bytes < pb) WV_TRY(ws->d.alloc(pb));
   GemvtArgs a;

@@ -67,9 +67,12 @@ size_t dense_workspace_bytes(const DenseLayer& L, int batch);
 // d_pre [batch][out], dX [batch][in] and dW [out][in]; with a target,
 // loss_part [dpre_blocks(batch * out)] gets the partial sums of the squared
 // differences. ws->d holds the dX partial sums.
+// linear_act takes act' as 1 (the reference's linear backward,
+// resident_backward(..., linear = true)).
 Status dense_backward(const DenseLayer& L, int batch, const float* x, const float* pre,
                       const float* post, const float* g, bool use_target, float* dpre, float* dx,
-                      float* dw, double* loss_part, Workspace* ws, hipStream_t st);
+                      float* dw, double* loss_part, Workspace* ws, hipStream_t st,
+                      bool linear_act = false);
 // SGD on the quantized store (native_codec.cpp:1080-1133): W <- quantize(
 // f32(f64(dequant(W)) - lr * f64(dW))) with the layer's scheme; the device
 // copy and the host store are replaced.

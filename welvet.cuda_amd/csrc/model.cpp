@@ -563,6 +563,60 @@ Status model_backward(Model& m, const std::vector<int>& in_shape, const float* x
   });
 }
 
+Status model_forward_pair(Model& m, const std::vector<int>& in_shape, const float* x,
+                          std::vector<int>* shape, const float** pre, const float** post,
+                          hipStream_t st) {
+  return model_guard([&] {
+    require(m.root == 0, "segment forward expects Stack or Parallel");
+    std::vector<ModelNode*> ops;
+    for (auto& c : m.children) flatten(c, &ops);
+    m.scratch.next = 0;
+    Arena ar{m.scratch};
+    Tensor cur;
+    cur.shape = in_shape;
+    cur.data = const_cast<float*>(x);
+    Tensor last_pre = cur;  // no ops: pre = post = input (stack.cpp:476-480)
+    for (size_t i = 0; i < ops.size(); ++i) {
+      if (i + 1 == ops.size() && ops[i]->kind != 1)
+        throw StatusError(Status::err(kGap, "gap? segment forward ending in a SwiGLU / MHA child "
+                                            "is outside the quantized Dense path of this build"));
+      cur = op_forward(*ops[i], cur, ar, &m.scratch.ws, st, i + 1 == ops.size() ? &last_pre : nullptr);
+    }
+    good(hip_status(hipStreamSynchronize(st), "segment forward"));
+    *shape = cur.shape;
+    *pre = last_pre.data;
+    *post = cur.data;
+  });
+}
+
+Status model_dense_proxy(Model& m, int kind, const std::vector<int>& in_shape, const float* x,
+                         const float* gy, const float* pre, const float** result, hipStream_t st) {
+  return model_guard([&] {
+    require(m.root == 0 && m.children.size() == 1 && m.children[0].kind == 1,
+            "proxy expects one Dense");
+    require(kind == 0 || kind == 1, "invalid Dense proxy arguments");
+    DenseLayer& L = *m.children[0].dense;
+    require(in_shape.size() == 2 && in_shape[0] > 0, "dense: proxy input shape");
+    if (kind == 0) require(in_shape[1] == L.in, "dense: LinearGradIn shape");
+    const int b = in_shape[0];
+    m.scratch.next = 0;
+    Arena ar{m.scratch};
+    float* dpre = ar.get((size_t)b * L.out);
+    float* dx = ar.get((size_t)b * L.in);
+    float* dw = ar.get((size_t)L.out * L.in);
+    const float* use_pre = pre;
+    if (!use_pre) {  // zeros (dense.cpp:160, :183-187)
+      float* z = ar.get((size_t)b * L.out);
+      good(hip_status(hipMemsetAsync(z, 0, (size_t)b * L.out * sizeof(float), st), "proxy pre"));
+      use_pre = z;
+    }
+    good(dense_backward(L, b, x, use_pre, nullptr, gy, false, dpre, dx, dw, nullptr,
+                        &m.scratch.ws, st, kind == 0));
+    good(hip_status(hipStreamSynchronize(st), "dense proxy"));
+    *result = kind == 0 ? dx : dw;
+  });
+}
+
 Status model_apply_sgd(Model& m, const float* dw, size_t n, double lr, hipStream_t st) {
   return model_guard([&] {
     std::vector<ModelNode*> ops = dense_ops(m);

@@ -84,6 +84,18 @@ Status model_backward(Model& m, const std::vector<int>& in_shape, const float* x
                       const std::vector<int>& gy_shape, const float* gy, const float** gx,
                       const float** dw, size_t* dw_n, hipStream_t st);
 Status model_apply_sgd(Model& m, const float* dw, size_t n, double lr, hipStream_t st);
+// Segment forward of a Stack (model_session.cpp:420-434, stack.cpp:470-494):
+// the last op's pre-activation and the output, both of *shape, in the
+// model's scratch. The last op must be Dense here.
+Status model_forward_pair(Model& m, const std::vector<int>& in_shape, const float* x,
+                          std::vector<int>* shape, const float** pre, const float** post,
+                          hipStream_t st);
+// Dense proxy of a one-Dense Stack (model_session.cpp:475-493): kind 0 the
+// linear input gradient (dense.cpp:141-166, act' = 1), kind 1 dW from the
+// given pre-activation, or zeros when pre is null (dense.cpp:168-191). gy
+// already has batch * out elements (the caller remaps it).
+Status model_dense_proxy(Model& m, int kind, const std::vector<int>& in_shape, const float* x,
+                         const float* gy, const float* pre, const float** result, hipStream_t st);
 
 // NWS1 snapshot of all stores (model_session.cpp:523-550).
 Status model_export(const Model& m, std::vector<uint8_t>* out);

@@ -38,8 +38,7 @@ class WelvetError(RuntimeError):
 
 _LIB = None
 OUT_OF_PATH = (
-    "welvet_model_train_credit", "welvet_model_dense_proxy", "welvet_model_forward_pair",
-    "welvet_model_train_mse", "welvet_model_sync",
+    "welvet_model_train_credit", "welvet_model_train_mse", "welvet_model_sync",
     "welvet_rmsnorm_forward_f32", "welvet_rmsnorm_normalbp_f32",
     "welvet_layernorm_forward_f32", "welvet_layernorm_normalbp_f32", "welvet_softmax_forward_f32",
     "welvet_softmax_normalbp_f32", "welvet_swiglu_normalbp_f32", "welvet_embedding_forward_f32",
@@ -129,6 +128,8 @@ def lib():
     _sig(L, "welvet_model_export_weights", Status, [_vp, ctypes.POINTER(Blob)])
     _sig(L, "welvet_model_backward", Status, [_vp, _u8p, _sz, ctypes.POINTER(Blob)])
     _sig(L, "welvet_model_apply_sgd", Status, [_vp, _f64, _u8p, _sz])
+    _sig(L, "welvet_model_forward_pair", Status, [_vp, _u8p, _sz, ctypes.POINTER(Blob)])
+    _sig(L, "welvet_model_dense_proxy", Status, [_vp, _i32, _u8p, _sz, ctypes.POINTER(Blob)])
     _sig(L, "welvet_model_release", None, [_vp])
     _sig(L, "welvet_cuda_blob_free", None, [ctypes.POINTER(Blob)])
     _sig(L, "welvet_codec_sweep", Status, [_i32, _u32, _u32, _i64p])
@@ -636,6 +637,32 @@ class ModelSession:
             lib().welvet_cuda_blob_free(ctypes.byref(blob))
         gx, dw = self._tensors(raw, 2)
         return gx, dw
+
+    def _call_blob(self, fn, data, n, *lead):
+        data = np.frombuffer(data, np.uint8).copy()
+        blob = Blob()
+        check(fn(self.h, *lead, data.ctypes.data_as(_u8p), data.size, ctypes.byref(blob)))
+        try:
+            raw = bytes(ctypes.cast(blob.data, ctypes.POINTER(ctypes.c_uint8 * blob.size)).contents)
+        finally:
+            lib().welvet_cuda_blob_free(ctypes.byref(blob))
+        return self._tensors(raw, n)
+
+    def forward_pair(self, x):
+        """welvet_model_forward_pair: (last op's pre-activation, output)."""
+        return tuple(self._call_blob(lib().welvet_model_forward_pair,
+                                     tensor_bytes(np.ascontiguousarray(x, np.float32)), 2))
+
+    def dense_proxy(self, kind, x, gy, pre=None):
+        """welvet_model_dense_proxy: kind 0 linear input gradient, 1 dW."""
+        w = Wire()
+        data = (tensor_bytes(np.ascontiguousarray(x, np.float32))
+                + tensor_bytes(np.ascontiguousarray(gy, np.float32)))
+        w.i32(0 if pre is None else 1)
+        data += w.bytes()
+        if pre is not None:
+            data += tensor_bytes(np.ascontiguousarray(pre, np.float32))
+        return self._call_blob(lib().welvet_model_dense_proxy, data, 1, kind)[0]
 
     def apply_sgd(self, dw, lr):
         data = np.frombuffer(tensor_bytes(np.ascontiguousarray(dw, np.float32)), np.uint8).copy()
