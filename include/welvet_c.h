@@ -253,6 +253,18 @@ WELVET_API welvet_status welvet_dense_normalbp_f32(
     const float* grad_or_target, int32_t use_target, double lr, float* pre, float* post, float* dX,
     float* dW, float* W_after, double* loss);
 
+/* SwiGLU NormalBP leaf (replaces reference include/welvet_c.h:137-146,
+ * src/interop/c_abi.cpp:581-652): forward (pre = h [B*S*inter], post = y
+ * [B*S*in]), the gradient (gradOut, or with use_target an MSE target), the
+ * backward over the three quantized matrices (dX [B*S*in], dW = Gate | Up |
+ * Down, 3*inter*in), SGD on each store if lr != 0, W_after in the same order,
+ * dequantized. Scale scheme in `backend`. */
+WELVET_API welvet_status welvet_swiglu_normalbp_f32(
+    int32_t batch, int32_t seq, int32_t input_dim, int32_t intermediate_dim, int32_t dtype,
+    int32_t backend, const float* Gate, const float* Up, const float* Down, const float* x,
+    const float* grad_or_target, int32_t use_target, double lr, float* pre, float* post, float* dX,
+    float* dW, float* W_after, double* loss);
+
 /* ==== reference entry points outside this path: code 3 ("gap?") ====
  * Same signatures as reference include/welvet_c.h:50-59, 74-130, 142-162,
  * 175-386. */
@@ -290,11 +302,6 @@ WELVET_API welvet_status welvet_softmax_normalbp_f32(
     int32_t rank, const int32_t* shape, const uint8_t* mask, int32_t mask_len, const int32_t* hier,
     int32_t hier_len, const float* x, const float* grad_or_target, int32_t use_target, double lr,
     float* pre, float* post, float* dX, double* loss);
-WELVET_API welvet_status welvet_swiglu_normalbp_f32(
-    int32_t batch, int32_t seq, int32_t input_dim, int32_t intermediate_dim, int32_t dtype,
-    int32_t backend, const float* Gate, const float* Up, const float* Down, const float* x,
-    const float* grad_or_target, int32_t use_target, double lr, float* pre, float* post, float* dX,
-    float* dW, float* W_after, double* loss);
 WELVET_API welvet_status welvet_embedding_forward_f32(
     int32_t batch, int32_t vocab, int32_t emb, int32_t seq_len, int32_t in_rank, int32_t in_last,
     int32_t act, int32_t dtype, int32_t backend, const float* W, const float* x, float* pre,

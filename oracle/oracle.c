@@ -525,6 +525,19 @@ void or_sgd(int64_t n, const float* w, const float* dW, double lr, float* next) 
   for (int64_t i = 0; i < n; ++i) next[i] = (float)((double)w[i] - lr * (double)dW[i]);
 }
 
+/* kernels.cu:307-320 */
+void or_swiglu_bwd_product(const float* g, const float* u, const float* gh, float* d_up,
+                           float* d_gate, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) {
+    const double gp = (double)g[i];
+    const float s = (float)or_activate(1, gp);
+    const float ds = (float)or_act_deriv(1, gp);
+    const double dh = (double)gh[i], up = (double)u[i];
+    d_up[i] = (float)(dh * (double)s);
+    d_gate[i] = (float)(dh * up * (double)ds);
+  }
+}
+
 /* ------------------------------------------------------------------------- */
 /* kernels.cu:470-485 */
 static int attn_allow(int qp, int kp, int mask, int window, int msl, int prefix_len,

@@ -125,6 +125,12 @@ void or_mse_grad(int64_t n, const float* pred, const float* target, float* grad)
  * next = f32(f64(w) - lr * f64(dW)); the caller re-encodes next. Pinned by the
  * compiled reference WeightStore::apply_sgd (oracle/_ref). */
 void or_sgd(int64_t n, const float* w, const float* dW, double lr, float* next);
+/* SwiGLU backward product, src/cuda/kernels.cu:307-320: s = f32(SiLU(f64 g)),
+ * ds = f32(SiLU'(f64 g)); d_up = f32(f64(gh) * f64(s)); d_gate =
+ * f32(f64(gh) * f64(u) * f64(ds)). Pinned by central differences of the
+ * forward product h = SiLU(g) * u and by the compiled reference act'. */
+void or_swiglu_bwd_product(const float* g, const float* u, const float* gh, float* d_up,
+                           float* d_gate, int64_t n);
 
 /* --- CPU baseline timing (reported beside the GPU) ---------------------------
  * Mount: decode codes to an f64 row-major W (src/layers/dense/dense.cpp:28-39).

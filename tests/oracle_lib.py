@@ -51,6 +51,7 @@ class Oracle:
         L.or_mse.argtypes = [ctypes.c_int64, _fp, _fp]
         L.or_mse_grad.argtypes = [ctypes.c_int64, _fp, _fp, _fp]
         L.or_sgd.argtypes = [ctypes.c_int64, _fp, _fp, ctypes.c_double, _fp]
+        L.or_swiglu_bwd_product.argtypes = [_fp, _fp, _fp, _fp, _fp, ctypes.c_int64]
         L.or_cpu_dense_bench.restype = ctypes.c_double
         L.or_cpu_dense_bench.argtypes = [_i, _i, _i, _i, _i, _u8p, _fp, _u8p, _fp, _fp, _i, _i, _i,
                                          _dp]
@@ -165,3 +166,9 @@ class Oracle:
         nxt = np.zeros_like(w)
         self.L.or_sgd(w.size, _f(w), _f(dw), float(lr), _f(nxt))
         return nxt
+
+    def swiglu_bwd_product(self, g, u, gh):
+        g, u, gh = (np.ascontiguousarray(a, np.float32) for a in (g, u, gh))
+        d_up, d_gate = np.zeros_like(g), np.zeros_like(g)
+        self.L.or_swiglu_bwd_product(_f(g), _f(u), _f(gh), _f(d_up), _f(d_gate), g.size)
+        return d_up, d_gate

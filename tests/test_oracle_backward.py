@@ -144,3 +144,22 @@ def test_backward_central_differences(oracle, act):
             e[o, i] = h
             fd = (loss(W64 + e, x64) - loss(W64 - e, x64)) / (2 * h)
             assert abs(dw[o, i] - fd) < 1e-4 * (1 + abs(fd)), (o, i)
+
+
+def test_swiglu_bwd_product_central_differences(oracle):
+    """d_up and d_gate against central differences of h = SiLU(g) * u in f64
+    (the rounding points of the product rule aside: relative 1e-6)."""
+    rng = np.random.default_rng(12)
+    g = (rng.standard_normal(300) * 3).astype(np.float32)
+    u = rng.standard_normal(300).astype(np.float32)
+    gh = rng.standard_normal(300).astype(np.float32)
+    d_up, d_gate = oracle.swiglu_bwd_product(g, u, gh)
+    g64, u64, h = g.astype(np.float64), u.astype(np.float64), 1e-6
+
+    def silu(v):
+        return v / (1.0 + np.exp(-v))
+
+    fd_g = gh * u64 * (silu(g64 + h) - silu(g64 - h)) / (2 * h)
+    fd_u = gh * silu(g64)
+    assert np.max(np.abs(d_gate - fd_g) / (np.abs(fd_g) + 1e-6)) < 1e-5
+    assert np.max(np.abs(d_up - fd_u) / (np.abs(fd_u) + 1e-6)) < 1e-6

@@ -311,6 +311,32 @@ __global__ __launch_bounds__(kThreads) void k_gemvt_reduce(const double* __restr
     dx[(size_t)b * in + i] = (float)(((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane]);
 }
 
+// SwiGLU backward product (kernels.cu:307-320): with gp = f64(gate_pre),
+// s = f32(SiLU(gp)), ds = f32(SiLU'(gp)), dh = f64(grad_h):
+// d_up = f32(dh * f64(s)), d_gate = f32(dh * f64(up) * f64(ds)).
+__global__ __launch_bounds__(kThreads) void k_swiglu_bwd(const float* __restrict__ gate_pre,
+                                                         const float* __restrict__ up_post,
+                                                         const float* __restrict__ grad_h,
+                                                         float* __restrict__ d_up,
+                                                         float* __restrict__ d_gate, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= n) return;
+  const double gp = (double)gate_pre[i];
+  const float s = (float)(gp / (1.0 + exp(-gp)));  // activate_dev Silu (kernels.cu:33)
+  const float ds = (float)act_deriv(kSilu, gp);
+  const double dh = (double)grad_h[i], up = (double)up_post[i];
+  d_up[i] = (float)(dh * (double)s);
+  d_gate[i] = (float)(dh * up * (double)ds);
+}
+
+// out = f32(f64(a) + f64(b)) (swiglu.cpp:231-234).
+__global__ __launch_bounds__(kThreads) void k_add_f64(const float* __restrict__ a,
+                                                      const float* __restrict__ b,
+                                                      float* __restrict__ out, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i < n) out[i] = (float)((double)a[i] + (double)b[i]);
+}
+
 struct DequantView {
   int dtype, rows, cols, pitch, nblk;
 };
@@ -430,6 +456,20 @@ Status launch_backward_products(const GemvtArgs& a, int dtype, bool blk, int bat
     WV_HIP(hipGetLastError());
   }
   return Status::ok();
+}
+
+Status launch_swiglu_bwd(const float* gate_pre, const float* up_post, const float* grad_h,
+                         float* d_up, float* d_gate, int64_t n, hipStream_t st) {
+  if (n <= 0 || !gate_pre || !up_post || !grad_h || !d_up || !d_gate)
+    return Status::err(kInvalid, "swiglu bwd: bad args");
+  k_swiglu_bwd<<<grid_for(n), kThreads, 0, st>>>(gate_pre, up_post, grad_h, d_up, d_gate, n);
+  return hip_status(hipGetLastError(), "swiglu bwd launch");
+}
+
+Status launch_add_f64(const float* a, const float* b, float* out, int64_t n, hipStream_t st) {
+  if (n <= 0 || !a || !b || !out) return Status::err(kInvalid, "add: bad args");
+  k_add_f64<<<grid_for(n), kThreads, 0, st>>>(a, b, out, n);
+  return hip_status(hipGetLastError(), "add launch");
 }
 
 Status launch_sgd(const DeviceWeights& d, const float* dw, double lr, float* w_next,

@@ -394,7 +394,69 @@ welvet_status welvet_dense_normalbp_f32(int32_t batch, int32_t in, int32_t out, 
   });
 }
 
-// --------------------------------------------------------------- SwiGLU ----
+// SwiGLU NormalBP leaf (src/interop/c_abi.cpp:581-652): forward (pre = h,
+// post = y), the gradient (gradOut or MSE from a target), the backward over
+// the three quantized matrices, optional SGD on each store, then the
+// updated weights as f32 [Gate | Up | Down]. Scale scheme in `backend`.
+welvet_status welvet_swiglu_normalbp_f32(int32_t batch, int32_t seq, int32_t input_dim,
+                                         int32_t intermediate_dim, int32_t dtype, int32_t backend,
+                                         const float* Gate, const float* Up, const float* Down,
+                                         const float* x, const float* grad_or_target,
+                                         int32_t use_target, double lr, float* pre, float* post,
+                                         float* dX, float* dW, float* W_after, double* loss) {
+  if (batch <= 0 || seq <= 0 || input_dim <= 0 || intermediate_dim <= 0 || !Gate || !Up || !Down ||
+      !x || !grad_or_target || !pre || !post || !dX || !dW || !W_after || !loss)
+    return invalid("swiglu nbp: invalid argument");
+  return guarded([&]() -> Status {
+    WV_TRY(wv::init_device());
+    wv::Stream stream;
+    WV_TRY(stream.create());
+    hipStream_t st = stream.s;
+    wv::SwiGLULayer L;
+    wv::Workspace ws;
+    WV_TRY(wv::swiglu_build(input_dim, intermediate_dim, dtype, backend, Gate, Up, Down, &L, st));
+    const int rows = batch * seq;
+    const size_t nx = (size_t)rows * input_dim, nh = (size_t)rows * intermediate_dim;
+    const size_t wf = (size_t)intermediate_dim * input_dim, nw = 3 * wf;
+    const int64_t parts = wv::dpre_blocks((int64_t)nx);
+    wv::DevBuf dx_in, dh, dy, dg, ddx, ddw, dwa, dloss;
+    WV_TRY(dx_in.alloc(nx * sizeof(float)));
+    WV_TRY(dh.alloc(nh * sizeof(float)));
+    WV_TRY(dy.alloc(nx * sizeof(float)));
+    WV_TRY(dg.alloc(nx * sizeof(float)));
+    WV_TRY(ddx.alloc(nx * sizeof(float)));
+    WV_TRY(ddw.alloc(nw * sizeof(float)));
+    WV_TRY(dwa.alloc(nw * sizeof(float)));
+    WV_TRY(dloss.alloc((size_t)parts * sizeof(double)));
+    WV_HIP(hipMemcpyAsync(dx_in.p, x, nx * sizeof(float), hipMemcpyHostToDevice, st));
+    WV_HIP(hipMemcpyAsync(dg.p, grad_or_target, nx * sizeof(float), hipMemcpyHostToDevice, st));
+    WV_TRY(wv::ensure_split(&ws, wv::swiglu_workspace_bytes(L, rows)));
+    WV_TRY(wv::swiglu_forward(L, rows, dx_in.as<float>(), dh.as<float>(), dy.as<float>(), &ws, st));
+    WV_TRY(wv::swiglu_backward(L, rows, dx_in.as<float>(), dh.as<float>(), dy.as<float>(),
+                               dg.as<float>(), use_target != 0, ddx.as<float>(), ddw.as<float>(),
+                               dloss.as<double>(), &ws, st));
+    if (lr != 0.0) WV_TRY(wv::swiglu_apply_sgd(&L, ddw.as<float>(), lr, st));
+    WV_TRY(wv::launch_dequant(L.gate.dev, dwa.as<float>(), st));
+    WV_TRY(wv::launch_dequant(L.up.dev, dwa.as<float>() + wf, st));
+    WV_TRY(wv::launch_dequant(L.down.dev, dwa.as<float>() + 2 * wf, st));
+    std::vector<double> lp(use_target ? (size_t)parts : 0);
+    WV_HIP(hipMemcpyAsync(pre, dh.p, nh * sizeof(float), hipMemcpyDeviceToHost, st));
+    WV_HIP(hipMemcpyAsync(post, dy.p, nx * sizeof(float), hipMemcpyDeviceToHost, st));
+    WV_HIP(hipMemcpyAsync(dX, ddx.p, nx * sizeof(float), hipMemcpyDeviceToHost, st));
+    WV_HIP(hipMemcpyAsync(dW, ddw.p, nw * sizeof(float), hipMemcpyDeviceToHost, st));
+    WV_HIP(hipMemcpyAsync(W_after, dwa.p, nw * sizeof(float), hipMemcpyDeviceToHost, st));
+    if (use_target)
+      WV_HIP(hipMemcpyAsync(lp.data(), dloss.p, lp.size() * sizeof(double), hipMemcpyDeviceToHost,
+                            st));
+    WV_HIP(hipStreamSynchronize(st));
+    double sum = 0.0;
+    for (double v : lp) sum += v;
+    *loss = use_target ? sum / (double)nx : 0.0;
+    return Status::ok();
+  });
+}
+
+// --------------------------------------------------------------- SwiGLU ----// --------------------------------------------------------------- SwiGLU ----
 welvet_status welvet_swiglu_mount(int32_t batch, int32_t seq, int32_t input_dim,
                                   int32_t intermediate_dim, int32_t dtype, int32_t backend,
                                   const float* Gate, const float* Up, const float* Down,
@@ -979,9 +1041,6 @@ WV_GAP_NBP(welvet_softmax_normalbp_f32, int32_t, int32_t, int32_t, int32_t, int3
            double, double, int32_t, int32_t, int32_t, int32_t, const int32_t*, const uint8_t*,
            int32_t, const int32_t*, int32_t, const float*, const float*, int32_t, double, float*,
            float*, float*, double*)
-WV_GAP_NBP(welvet_swiglu_normalbp_f32, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t,
-           const float*, const float*, const float*, const float*, const float*, int32_t, double,
-           float*, float*, float*, float*, float*, double*)
 WV_GAP_NBP(welvet_embedding_forward_f32, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t,
            int32_t, int32_t, int32_t, const float*, const float*, float*, float*)
 WV_GAP_NBP(welvet_embedding_normalbp_f32, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t,

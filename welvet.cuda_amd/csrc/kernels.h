@@ -172,6 +172,11 @@ size_t gemvt_part_bytes(int in, int out);
 Status launch_backward_products(const GemvtArgs& a, int dtype, bool blk, int batch,
                                 const float* x, float* dw, double* part, float* dx,
                                 hipStream_t st);
+// SwiGLU backward product (d_up, d_gate from gate_pre, up_post, grad_h) and
+// the f64 sum of two gradients, rounded to f32.
+Status launch_swiglu_bwd(const float* gate_pre, const float* up_post, const float* grad_h,
+                         float* d_up, float* d_gate, int64_t n, hipStream_t st);
+Status launch_add_f64(const float* a, const float* b, float* out, int64_t n, hipStream_t st);
 // w_next [rows][cols] = f32(f64(dequant(W)) - lr * f64(dW)).
 Status launch_sgd(const DeviceWeights& d, const float* dw, double lr, float* w_next,
                   hipStream_t st);

@@ -457,6 +457,49 @@ Status swiglu_forward(const SwiGLULayer& L, int rows, const float* x, float* h, 
   return dense_forward(L.down, rows, h, y, nullptr, ws, st);
 }
 
+Status swiglu_backward(const SwiGLULayer& L, int rows, const float* x, const float* h,
+                       const float* y, const float* g, bool use_target, float* dx, float* dw,
+                       double* loss_part, Workspace* ws, hipStream_t st) {
+  if (rows <= 0 || !x || !h || !y || !g || !dx || !dw || !ws)
+    return Status::err(kInvalid, "swiglu backward: bad args");
+  const int in = L.gate.in, inter = L.gate.out;
+  const size_t ri = (size_t)rows * in, rf = (size_t)rows * inter, wf = (size_t)inter * in;
+  DevBuf b_dpre_d, b_gh, b_gp, b_up, b_dg, b_du, b_dpre, b_gxg, b_gxu;
+  WV_TRY(b_dpre_d.alloc(ri * sizeof(float)));
+  WV_TRY(b_gh.alloc(rf * sizeof(float)));
+  WV_TRY(b_gp.alloc(rf * sizeof(float)));
+  WV_TRY(b_up.alloc(rf * sizeof(float)));
+  WV_TRY(b_dg.alloc(rf * sizeof(float)));
+  WV_TRY(b_du.alloc(rf * sizeof(float)));
+  WV_TRY(b_dpre.alloc(rf * sizeof(float)));
+  WV_TRY(b_gxg.alloc(ri * sizeof(float)));
+  WV_TRY(b_gxu.alloc(ri * sizeof(float)));
+  // Down (Linear): its backward takes gy (or forms the MSE gradient from y)
+  // on h; the recomputed Down(h) is y itself (same kernels, same input)
+  WV_TRY(dense_backward(L.down, rows, h, y, y, g, use_target, b_dpre_d.as<float>(),
+                        b_gh.as<float>(), dw + 2 * wf, loss_part, ws, st));
+  // Gate and Up recomputed on x (Linear), then the product rule
+  WV_TRY(dense_forward(L.gate, rows, x, b_gp.as<float>(), nullptr, ws, st));
+  WV_TRY(dense_forward(L.up, rows, x, b_up.as<float>(), nullptr, ws, st));
+  WV_TRY(launch_swiglu_bwd(b_gp.as<float>(), b_up.as<float>(), b_gh.as<float>(),
+                           b_du.as<float>(), b_dg.as<float>(), (int64_t)rf, st));
+  WV_TRY(dense_backward(L.gate, rows, x, b_gp.as<float>(), nullptr, b_dg.as<float>(), false,
+                        b_dpre.as<float>(), b_gxg.as<float>(), dw, nullptr, ws, st));
+  WV_TRY(dense_backward(L.up, rows, x, b_up.as<float>(), nullptr, b_du.as<float>(), false,
+                        b_dpre.as<float>(), b_gxu.as<float>(), dw + wf, nullptr, ws, st));
+  WV_TRY(launch_add_f64(b_gxg.as<float>(), b_gxu.as<float>(), dx, (int64_t)ri, st));
+  // the scratch buffers are freed on return: the queued work must be done
+  return hip_status(hipStreamSynchronize(st), "swiglu backward");
+}
+
+Status swiglu_apply_sgd(SwiGLULayer* L, const float* dw, double lr, hipStream_t st) {
+  if (!L || !dw) return Status::err(kInvalid, "swiglu sgd: bad args");
+  const size_t wf = (size_t)L->gate.out * L->gate.in;
+  WV_TRY(dense_apply_sgd(&L->gate, dw, lr, st));
+  WV_TRY(dense_apply_sgd(&L->up, dw + wf, lr, st));
+  return dense_apply_sgd(&L->down, dw + 2 * wf, lr, st);
+}
+
 // ---------------------------------------------------------------------------
 Status mha_validate(MHAConfig* c) {
   if (c->d_model <= 0 || c->num_heads <= 0)

@@ -138,6 +138,16 @@ Status swiglu_build(int in, int inter, int dtype, int scheme, const float* G, co
 Status swiglu_forward(const SwiGLULayer& L, int rows, const float* x, float* h, float* y,
                       Workspace* ws, hipStream_t st);
 size_t swiglu_workspace_bytes(const SwiGLULayer& L, int rows);
+// SwiGLU backward on device buffers (swiglu.cpp:156-248): from x [rows][in],
+// the forward's h and y, and the output gradient (or, with use_target, the
+// MSE target) in g: dx [rows][in] and dw = [dGate | dUp | dDown] (each
+// [out][in] of its matrix); with a target, loss_part as dense_backward.
+// Gate and Up are recomputed; scratch buffers come from the call.
+Status swiglu_backward(const SwiGLULayer& L, int rows, const float* x, const float* h,
+                       const float* y, const float* g, bool use_target, float* dx, float* dw,
+                       double* loss_part, Workspace* ws, hipStream_t st);
+// SGD on the three stores with their slices of dw (swiglu.cpp:250-268).
+Status swiglu_apply_sgd(SwiGLULayer* L, const float* dw, double lr, hipStream_t st);
 
 struct MHAConfig {
   int d_model = 0, num_heads = 0, num_kv_heads = 0, head_dim = 0, max_seq_len = 0;

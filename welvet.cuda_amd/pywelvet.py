@@ -41,7 +41,7 @@ OUT_OF_PATH = (
     "welvet_model_train_credit", "welvet_model_train_mse", "welvet_model_sync",
     "welvet_rmsnorm_forward_f32", "welvet_rmsnorm_normalbp_f32",
     "welvet_layernorm_forward_f32", "welvet_layernorm_normalbp_f32", "welvet_softmax_forward_f32",
-    "welvet_softmax_normalbp_f32", "welvet_swiglu_normalbp_f32", "welvet_embedding_forward_f32",
+    "welvet_softmax_normalbp_f32", "welvet_embedding_forward_f32",
     "welvet_embedding_normalbp_f32", "welvet_mha_normalbp_f32", "welvet_cnn1_forward_f32",
     "welvet_cnn1_normalbp_f32", "welvet_cnn2_forward_f32", "welvet_cnn2_normalbp_f32",
     "welvet_cnn3_forward_f32", "welvet_cnn3_normalbp_f32", "welvet_convt1_forward_f32",
@@ -88,6 +88,8 @@ def lib():
     _sig(L, "welvet_dense_normalbp_f32", Status,
          [_i32, _i32, _i32, _i32, _i32, _i32, _fp, _dp, _sz, _fp, _fp, _i32, _f64, _fp, _fp, _fp,
           _fp, _fp, _dp])
+    _sig(L, "welvet_swiglu_normalbp_f32", Status,
+         [_i32] * 6 + [_fp] * 5 + [_i32, _f64] + [_fp] * 5 + [_dp])
     _sig(L, "welvet_dense_mount", Status,
          [_i32, _i32, _i32, _i32, _i32, _fp, _dp, _sz, ctypes.POINTER(_vp)])
     _sig(L, "welvet_dense_mount_q", Status,
@@ -511,6 +513,24 @@ def dense_normalbp(batch, in_dim, out_dim, act, dtype, scheme, W, x, grad_or_tar
                                           dptr(b), 0 if b is None else b.size, fptr(x), fptr(g),
                                           1 if use_target else 0, float(lr), fptr(pre),
                                           fptr(post), fptr(dx), fptr(dw), fptr(wa), dptr(loss)))
+    return pre, post, dx, dw, wa, float(loss[0])
+
+
+def swiglu_normalbp(batch, seq, in_dim, inter, dtype, scheme, G, U, D, x, grad_or_target,
+                    use_target=False, lr=0.0):
+    """welvet_swiglu_normalbp_f32: pre (h), post (y), dX, dW, W_after, loss."""
+    arrs = [np.ascontiguousarray(a, dtype=np.float32) for a in (G, U, D, x, grad_or_target)]
+    rows = batch * seq
+    pre = np.empty((rows, inter), np.float32)
+    post = np.empty((rows, in_dim), np.float32)
+    dx = np.empty((rows, in_dim), np.float32)
+    dw = np.empty(3 * inter * in_dim, np.float32)
+    wa = np.empty_like(dw)
+    loss = np.zeros(1, np.float64)
+    check(lib().welvet_swiglu_normalbp_f32(batch, seq, in_dim, inter, dtype, scheme,
+                                           *[fptr(a) for a in arrs], 1 if use_target else 0,
+                                           float(lr), fptr(pre), fptr(post), fptr(dx), fptr(dw),
+                                           fptr(wa), dptr(loss)))
     return pre, post, dx, dw, wa, float(loss[0])
 
 
