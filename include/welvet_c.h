@@ -214,12 +214,12 @@ WELVET_API welvet_status welvet_model_forward_device(welvet_model_session* s, co
 WELVET_API welvet_status welvet_codec_sweep(int32_t dtype, uint32_t first_chunk,
                                             uint32_t n_chunks, int64_t* out);
 
-/* Segment backward of a Stack model of Dense children (replaces reference
+/* Segment backward of a Stack model of Dense / SwiGLU children (replaces reference
  * include/welvet_c.h:55, src/interop/model_session.cpp:435-455): the input
  * blob holds the tensors x and gy (model wire: rank, dims, float32 data);
  * the forward is recomputed and the output blob holds the input gradient and
- * the dW of the Dense ops concatenated in op order, shape [1, n]. Other
- * children give code 3 ("gap?"), Grid roots code 1. */
+ * the dW of the ops concatenated in op order (SwiGLU: Gate, Up, Down),
+ * shape [1, n]. MHA children give code 3 ("gap?"), Grid roots code 1. */
 WELVET_API welvet_status welvet_model_backward(welvet_model_session*, const uint8_t*, size_t,
                                                welvet_cuda_blob*);
 /* Segment forward (replaces reference include/welvet_c.h:54,
@@ -235,7 +235,7 @@ WELVET_API welvet_status welvet_model_forward_pair(welvet_model_session*, const 
 WELVET_API welvet_status welvet_model_dense_proxy(welvet_model_session*, int32_t, const uint8_t*,
                                                   size_t, welvet_cuda_blob*);
 /* Segment SGD (replaces reference include/welvet_c.h:56, model_session.cpp:
- * 494-507): one tensor, the concatenated dW; every Dense store becomes
+ * 494-507): one tensor, the concatenated dW; every store becomes
  * quantize(f32(f64(W) - lr dW)) with the session's scale scheme. */
 WELVET_API welvet_status welvet_model_apply_sgd(welvet_model_session*, double, const uint8_t*,
                                                 size_t);

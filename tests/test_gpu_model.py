@@ -315,3 +315,58 @@ def test_segment_dense_proxy(gpu, oracle, dt, scheme, act):
     mean = ((g2[0::2].astype(np.float64) + g2[1::2].astype(np.float64)) / 2).astype(np.float32)
     assert np.array_equal(m.dense_proxy(0, x, g2.reshape(10, 48)), m.dense_proxy(0, x, mean.reshape(5, 48)))
     m.close()
+
+
+def _mixed_stack(oracle, rng, scheme):
+    """Stack: Dense 96 -> 128 (ReLU, E4M3) | SwiGLU 128 / 192 (FP4) | Dense
+    128 -> 80 (SiLU, E5M2), as one NestedStack child."""
+    W1 = (rng.standard_normal((128, 96)) / np.sqrt(96)).astype(np.float32)
+    G = (rng.standard_normal((192, 128)) / np.sqrt(128)).astype(np.float32)
+    U = (rng.standard_normal((192, 128)) / np.sqrt(128)).astype(np.float32)
+    D = (rng.standard_normal((128, 192)) / np.sqrt(192)).astype(np.float32)
+    W3 = (rng.standard_normal((80, 128)) / np.sqrt(128)).astype(np.float32)
+    w = pw.Wire()
+    w.u32(0x314E4D57)
+    w.i32(0, 1, 1, 1, 1, 1)
+    w.i32(19, 3)
+    pw.dense_child(w, 96, 128, 0, 4, W1)
+    pw.swiglu_child(w, 128, 192, 16, G, U, D)
+    pw.dense_child(w, 128, 80, 1, 5, W3)
+    for _ in range(5):  # the stack, its child and the child's three ops
+        pw.empty_controls(w)
+    stores = [(4, W1), (16, G), (16, U), (16, D), (5, W3)]
+    w.i32(len(stores))
+    for dt, W in stores:
+        pw.store_payload(w, dt, W.shape[0], W.shape[1], oracle.pack(dt, W))
+    return pw.ModelSession(w.bytes(), scheme=scheme), (W1, G, U, D, W3), stores
+
+
+@pytest.mark.parametrize("scheme,batch", [(0, 2), (3, 40)])
+def test_segment_training_through_swiglu(gpu, oracle, scheme, batch):
+    """A Stack mixing Dense and SwiGLU: welvet_model_backward gives the bits
+    of the NormalBP leaves run by hand in reverse (dW: Dense, then Gate | Up |
+    Down, then Dense), and SGD re-quantizes all five stores as the oracle."""
+    rng = np.random.default_rng(70 + batch)
+    m, (W1, G, U, D, W3), stores = _mixed_stack(oracle, rng, scheme)
+    x = rng.standard_normal((batch, 96)).astype(np.float32)
+    gy = rng.standard_normal((batch, 80)).astype(np.float32)
+    gx, dw = m.backward(x, gy)
+    _, a1 = pw.dense_forward(batch, 96, 128, 0, 4, scheme, W1, x)
+    _, a2, _, _, _, _ = pw.swiglu_normalbp(batch, 1, 128, 192, 16, scheme, G, U, D, a1,
+                                           np.zeros((batch, 128), np.float32))
+    _, _, g3, dw3, _, _ = pw.dense_normalbp(batch, 128, 80, 1, 5, scheme, W3, a2, gy)
+    _, _, g2, dw2, _, _ = pw.swiglu_normalbp(batch, 1, 128, 192, 16, scheme, G, U, D, a1, g3)
+    _, _, g1, dw1, _, _ = pw.dense_normalbp(batch, 96, 128, 0, 4, scheme, W1, x, g2)
+    assert np.array_equal(gx, g1)
+    assert np.array_equal(dw.ravel(), np.concatenate([dw1.ravel(), dw2, dw3.ravel()]))
+    lr = 0.1
+    m.apply_sgd(dw, lr)
+    off = 0
+    for (dt, W), (sdt, rows, cols, _, native) in zip(stores, parse_nws1(m.export())):
+        nat, rs, blk = oracle.quantize(dt, scheme, rows, cols, W)
+        Wq = oracle.dequant(dt, scheme, rows, cols, nat, rs, blk)
+        nxt = oracle.sgd(Wq, dw.ravel()[off:off + W.size].reshape(W.shape), lr)
+        nat2, _, _ = oracle.quantize(dt, scheme, rows, cols, nxt)
+        assert sdt == dt and np.array_equal(native, nat2), (dt, rows, cols)
+        off += W.size
+    m.close()

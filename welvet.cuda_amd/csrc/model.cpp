@@ -337,6 +337,10 @@ Tensor op_forward(ModelNode& c, const Tensor& in, Arena& ar, Workspace* ws, hipS
     out.data = ar.get(out.numel());
     float* h = ar.get((size_t)rows * c.inter);
     good(swiglu_forward(*c.swiglu, rows, in.data, h, out.data, ws, st));
+    if (pre_out) {
+      pre_out->shape = {rows, c.inter};
+      pre_out->data = h;
+    }
     break;
   }
   case 7: {
@@ -488,17 +492,24 @@ Status model_forward_view(Model& m, const std::vector<int>& in_shape, const floa
 
 namespace {
 
-// The ops of a Stack model for the segment training calls: Dense only here
-// (the other children's backward is not part of this build).
-std::vector<ModelNode*> dense_ops(Model& m) {
+// The ops of a Stack model for the segment training calls: Dense and SwiGLU
+// (the MHA backward is not part of this build).
+std::vector<ModelNode*> train_ops(Model& m) {
   require(m.root == 0, "segment backward expects Stack or Parallel");
   std::vector<ModelNode*> ops;
   for (auto& c : m.children) flatten(c, &ops);
   for (ModelNode* op : ops)
-    if (op->kind != 1)
-      throw StatusError(Status::err(kGap, "gap? segment backward of SwiGLU / MHA children is "
-                                          "outside the quantized Dense path of this build"));
+    if (op->kind != 1 && op->kind != 4)
+      throw StatusError(Status::err(kGap, "gap? segment backward of MHA children is outside the "
+                                          "quantized Dense path of this build"));
   return ops;
+}
+
+// Weights of an op in the concatenated dW (stack.cpp:308-330): Dense out*in,
+// SwiGLU Gate | Up | Down.
+size_t op_grad_w(const ModelNode& op) {
+  return op.kind == 1 ? (size_t)op.dense->out * op.dense->in
+                      : 3 * (size_t)op.swiglu->gate.out * op.swiglu->gate.in;
 }
 
 template <class F>
@@ -521,7 +532,7 @@ Status model_backward(Model& m, const std::vector<int>& in_shape, const float* x
                       const std::vector<int>& gy_shape, const float* gy, const float** gx,
                       const float** dw, size_t* dw_n, hipStream_t st) {
   return model_guard([&] {
-    std::vector<ModelNode*> ops = dense_ops(m);
+    std::vector<ModelNode*> ops = train_ops(m);
     require(in_shape.size() == 2, "dense: input shape need [batch,in]");
     m.scratch.next = 0;
     Arena ar{m.scratch};
@@ -540,7 +551,7 @@ Status model_backward(Model& m, const std::vector<int>& in_shape, const float* x
     }
     require(gy_shape == cur.shape, "segment output gradient shape mismatch");
     size_t total = 0;
-    for (ModelNode* op : ops) total += (size_t)op->dense->out * op->dense->in;
+    for (ModelNode* op : ops) total += op_grad_w(*op);
     float* dwall = ar.get(total > 0 ? total : 1);
     // backward in reverse (stack.cpp:532-557): op i's input gradient is op
     // i - 1's output gradient; dW slices in op order
@@ -548,13 +559,23 @@ Status model_backward(Model& m, const std::vector<int>& in_shape, const float* x
     const float* g = gy;
     size_t off = total;
     for (size_t k = ops.size(); k-- > 0;) {
-      DenseLayer& L = *ops[k]->dense;
-      off -= (size_t)L.out * L.in;
-      float* dpre = ar.get((size_t)b * L.out);
-      float* dxk = ar.get((size_t)b * L.in);
-      good(dense_backward(L, b, ins[k].data, pres[k].data, nullptr, g, false, dpre, dxk,
-                          dwall + off, nullptr, &ws, st));
-      g = dxk;
+      off -= op_grad_w(*ops[k]);
+      if (ops[k]->kind == 1) {
+        DenseLayer& L = *ops[k]->dense;
+        float* dpre = ar.get((size_t)b * L.out);
+        float* dxk = ar.get((size_t)b * L.in);
+        good(dense_backward(L, b, ins[k].data, pres[k].data, nullptr, g, false, dpre, dxk,
+                            dwall + off, nullptr, &ws, st));
+        g = dxk;
+      } else {
+        // SwiGLU (swiglu.cpp:156-248): h is the recorded pre, y the op's output
+        const SwiGLULayer& L = *ops[k]->swiglu;
+        const float* y = k + 1 < ops.size() ? ins[k + 1].data : cur.data;
+        float* dxk = ar.get((size_t)b * L.gate.in);
+        good(swiglu_backward(L, b, ins[k].data, pres[k].data, y, g, false, dxk, dwall + off,
+                             nullptr, &ws, st));
+        g = dxk;
+      }
     }
     good(hip_status(hipStreamSynchronize(st), "segment backward"));
     *gx = g;
@@ -619,14 +640,15 @@ Status model_dense_proxy(Model& m, int kind, const std::vector<int>& in_shape, c
 
 Status model_apply_sgd(Model& m, const float* dw, size_t n, double lr, hipStream_t st) {
   return model_guard([&] {
-    std::vector<ModelNode*> ops = dense_ops(m);
+    std::vector<ModelNode*> ops = train_ops(m);
     size_t total = 0;
-    for (ModelNode* op : ops) total += (size_t)op->dense->out * op->dense->in;
+    for (ModelNode* op : ops) total += op_grad_w(*op);
     require(n == total, "segment weight gradient size mismatch");
     size_t off = 0;
     for (ModelNode* op : ops) {
-      good(dense_apply_sgd(op->dense.get(), dw + off, lr, st));
-      off += (size_t)op->dense->out * op->dense->in;
+      if (op->kind == 1) good(dense_apply_sgd(op->dense.get(), dw + off, lr, st));
+      else good(swiglu_apply_sgd(op->swiglu.get(), dw + off, lr, st));
+      off += op_grad_w(*op);
     }
   });
 }

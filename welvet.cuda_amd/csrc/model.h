@@ -73,13 +73,13 @@ Status model_forward(Model& m, const std::vector<int>& in_shape, const float* x,
 Status model_forward_view(Model& m, const std::vector<int>& in_shape, const float* x,
                           std::vector<int>* out_shape, const float** out, hipStream_t st);
 
-// Segment training of a Stack model of Dense ops (model_session.cpp:435-507,
+// Segment training of a Stack model of Dense and SwiGLU ops (model_session.cpp:435-507,
 // stack.cpp:496-580). model_backward recomputes the forward of x (device)
 // and backpropagates gy (device, the output's shape): *gx (input gradient,
 // in_shape) and *dw (dW of the ops concatenated in op order, *dw_n floats)
 // point into the model's scratch until its next pass. model_apply_sgd
 // applies SGD to every op with its slice of dw (device), re-quantizing with
-// the model's scheme. Other children give code 3, other roots code 1.
+// the model's scheme. MHA children give code 3, other roots code 1.
 Status model_backward(Model& m, const std::vector<int>& in_shape, const float* x,
                       const std::vector<int>& gy_shape, const float* gy, const float** gx,
                       const float** dw, size_t* dw_n, hipStream_t st);

@@ -576,6 +576,12 @@ def dense_child(w, in_dim, out_dim, act, dtype, W, bias=None):
         w.f64(b)
 
 
+def swiglu_child(w, in_dim, inter, dtype, G, U, D):
+    """SwiGLU child (child_wire.hpp:95-118): dims, dtype, then Gate, Up, Down."""
+    w.i32(4, in_dim, inter, dtype)
+    w.f32(np.concatenate([np.ravel(G), np.ravel(U), np.ravel(D)]))
+
+
 def empty_controls(w):
     # modes, branch_lrs, shadow_coef, surprise_thresh, last_loss, sync present
     w.i32(0, 0)
