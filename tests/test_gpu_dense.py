@@ -124,6 +124,43 @@ def test_small_batch_k_split(gpu, oracle, dt, scheme, rows, cols, batch):
     assert rel_l2(post, o_post) <= TOL_MFMA, (rows, cols, batch)
 
 
+@pytest.mark.parametrize("dt,scheme", [(4, 2), (5, 3), (16, 3), (16, 0)])
+@pytest.mark.parametrize("rows,cols,batch", [(2176, 1000, 9), (500, 1001, 7), (300, 4096, 30)])
+def test_small_batch_operand_order_codes_bit_identical(gpu, dt, scheme, rows, cols, batch):
+    """Sessions whose batch runs the 5..32-row GEMM mount an operand-order
+    copy of the codes and read it instead of the row-major codes. The NormalBP
+    leaf mounts without that copy, so its forward reads the row-major codes:
+    both must give the same bits (same bytes, same order of operations)."""
+    rng = np.random.default_rng(7 * rows + cols + batch + dt)
+    W = rng.standard_normal((rows, cols)).astype(np.float32) / np.sqrt(cols)
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    bias = rng.standard_normal(rows) * 0.1
+    pre, post = gpu.dense_forward(batch, cols, rows, 2, dt, scheme, W, x, bias=bias)
+    g = np.zeros((batch, rows), np.float32)
+    pre_rm, post_rm, *_ = gpu.dense_normalbp(batch, cols, rows, 2, dt, scheme, W, x, g, bias=bias)
+    assert np.array_equal(pre.view(np.uint32), pre_rm.view(np.uint32)), (dt, rows, cols, batch)
+    assert np.array_equal(post.view(np.uint32), post_rm.view(np.uint32)), (dt, rows, cols, batch)
+
+
+def test_small_batch_operand_order_codes_swiglu_bit_identical(gpu):
+    """The same for SwiGLU (two matrices in one product): the session reads
+    the operand-order copies, the NormalBP leaf the row-major codes."""
+    rng = np.random.default_rng(11)
+    d, f, rows = 256, 640, 12
+    G, U = [(rng.standard_normal((f, d)) / np.sqrt(d)).astype(np.float32) for _ in range(2)]
+    D = (rng.standard_normal((d, f)) / np.sqrt(f)).astype(np.float32)
+    x = rng.standard_normal((rows, d)).astype(np.float32)
+    s = gpu.SwiGLUSession(1, rows, d, f, 16, 3, G, U, D)
+    try:
+        h, y = s.execute(x)
+    finally:
+        s.close()
+    g = np.zeros((rows, d), np.float32)
+    h_rm, y_rm, *_ = gpu.swiglu_normalbp(1, rows, d, f, 16, 3, G, U, D, x, g)
+    assert np.array_equal(h.view(np.uint32), h_rm.view(np.uint32))
+    assert np.array_equal(y.view(np.uint32), y_rm.view(np.uint32))
+
+
 @pytest.mark.parametrize("dt", [4, 5, 16])
 @pytest.mark.parametrize("scheme", [0, 1, 2, 3])
 @pytest.mark.parametrize("rows,cols,batch", [(33, 70, 1), (300, 1024, 2), (7, 33, 3), (1, 1, 1)])

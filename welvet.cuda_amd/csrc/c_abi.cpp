@@ -117,6 +117,7 @@ static welvet_status dense_mount(int32_t batch, int32_t in, int32_t out, int32_t
     Status st = s->stream.create();
     if (st) st = wv::dense_build(in, out, act, dtype, backend, W_init, bias, bias_len, &s->layer,
                                  s->stream.s);
+    if (st) st = wv::dense_prepare_rows(&s->layer, batch, s->stream.s);
     if (st) st = wv::ensure_split(&s->ws, wv::dense_workspace_bytes(s->layer, batch));
     if (st) st = s->x.alloc((size_t)batch * in * sizeof(float));
     if (st) st = s->pre.alloc((size_t)batch * out * sizeof(float));
@@ -472,6 +473,7 @@ welvet_status welvet_swiglu_mount(int32_t batch, int32_t seq, int32_t input_dim,
     Status st = s->stream.create();
     if (st) st = wv::swiglu_build(input_dim, intermediate_dim, dtype, backend, Gate, Up, Down,
                                   &s->layer, s->stream.s);
+    if (st) st = wv::swiglu_prepare_rows(&s->layer, rows, s->stream.s);
     if (st) st = wv::ensure_split(&s->ws, wv::swiglu_workspace_bytes(s->layer, rows));
     if (st) st = s->x.alloc((size_t)rows * input_dim * sizeof(float));
     if (st) st = s->pre.alloc((size_t)rows * intermediate_dim * sizeof(float));

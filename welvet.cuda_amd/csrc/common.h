@@ -96,10 +96,17 @@ struct DeviceWeights {
   // block l / 16 of each chunk), byte j = chunk j of the group:
   // uint8[rpad / 16][ceil(kpad / 512)][64][4]
   DevBuf blk_frag;
+  // optional copy of the codes in matrix-core operand order for the 5..32-row
+  // GEMM (built by sessions whose batch runs it): per 16-row block, K chunk
+  // of 128 and operand half (FP8: 2, FP4: 1), lane l's 16 bytes (row l % 16,
+  // chunk bytes 64 h + 16 (l / 16) ..) at 16 l, so a wave's operand load is
+  // 1 KiB contiguous: uint8[rpad / 16][kpad / 128][halves][64][16]
+  DevBuf codes_frag;
   const uint8_t* d_codes() const { return codes.as<const uint8_t>(); }
   const float* d_scale() const { return row_scale.as<const float>(); }
   const uint8_t* d_blk() const { return scheme == 3 ? blk.as<const uint8_t>() : nullptr; }
   const uint8_t* d_blkf() const { return scheme == 3 ? blk_frag.as<const uint8_t>() : nullptr; }
+  const uint8_t* d_codesf() const { return codes_frag.as<const uint8_t>(); }
 };
 
 constexpr int kRowPad = 128;

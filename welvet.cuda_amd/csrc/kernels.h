@@ -8,6 +8,9 @@ namespace wv {
 // ---- mount-time quantization (quant.hip) ----
 // Quantizes the device fp32 matrix dW [rows x cols] into dw (allocates it) and,
 // if d_raw is set, writes the reference FormatNone payload there.
+// Builds DeviceWeights::codes_frag from the codes (operand-order copy read
+// by the 5..32-row GEMM when present).
+Status build_codes_frag(DeviceWeights* dw, hipStream_t st);
 Status quantize_to_device(const float* dW, int dtype, int scheme, int rows, int cols,
                           DeviceWeights* dw, uint8_t* d_raw, hipStream_t st);
 // Builds dw from a reference payload already on the device plus optional
@@ -93,6 +96,9 @@ struct MxgArgs {
   float* part = nullptr;
   // block exponents in lane order (DeviceWeights::blk_frag), BLOCK32 only
   const uint8_t* blkf[2] = {nullptr, nullptr};
+  // codes in operand order (DeviceWeights::codes_frag) or null; the 5..32-row
+  // GEMM reads them instead of `codes` when every matrix has them
+  const uint8_t* codesf[2] = {nullptr, nullptr};
   // small M (mxg_block_m(M) == 16): the fp32 input [M][cols] (row stride
   // x_stride), split into terms by the GEMM kernel itself (a / as unused);
   // x_vec: x 16-byte aligned, cols and x_stride multiples of 4

@@ -174,6 +174,19 @@ static MxvArgs mxv_args(const DenseLayer& L, const float* x, int x_stride, int b
 
 bool uses_split(int batch) { return batch > kMxvMaxBatch; }
 
+Status dense_prepare_rows(DenseLayer* L, int batch, hipStream_t st) {
+  if (!uses_split(batch) || mxg_block_m(batch) != 16 || L->dev.codes_frag.p)
+    return Status::ok();
+  WV_TRY(build_codes_frag(&L->dev, st));
+  return hip_status(hipStreamSynchronize(st), "codes_frag");
+}
+
+Status swiglu_prepare_rows(SwiGLULayer* L, int rows, hipStream_t st) {
+  WV_TRY(dense_prepare_rows(&L->gate, rows, st));
+  WV_TRY(dense_prepare_rows(&L->up, rows, st));
+  return dense_prepare_rows(&L->down, rows, st);
+}
+
 // Split activations plus, for small batches split along K, the partial sums.
 static size_t gemm_ws_bytes(const DenseLayer& L, int batch, int mats) {
   return split_bytes(batch, L.dev.kpad) + mxg_part_bytes(batch, L.dev.kpad, L.out, mats);
@@ -199,6 +212,7 @@ static MxgArgs mxg_args(const DenseLayer& L, int batch, const uint8_t* split) {
   p.scale[0] = L.dev.d_scale();
   p.blk[0] = L.dev.d_blk();
   p.blkf[0] = L.dev.d_blkf();
+  p.codesf[0] = L.dev.d_codesf();
   p.pitch = L.dev.pitch;
   p.nblk = L.dev.nblk;
   p.kpad = L.dev.kpad;
@@ -294,6 +308,7 @@ Status dense_apply_sgd(DenseLayer* L, const float* dw, double lr, hipStream_t st
   DeviceWeights fresh;
   WV_TRY(quantize_to_device(next.as<float>(), L->dev.dtype, L->dev.scheme, L->out, L->in, &fresh,
                             raw.as<uint8_t>(), st));
+  if (L->dev.codes_frag.p) WV_TRY(build_codes_frag(&fresh, st));
   L->dev = std::move(fresh);
   return download_store(L, raw.as<uint8_t>(), st);
 }
@@ -439,6 +454,7 @@ Status swiglu_forward(const SwiGLULayer& L, int rows, const float* x, float* h, 
     p.scale[1] = L.up.dev.d_scale();
     p.blk[1] = L.up.dev.d_blk();
     p.blkf[1] = L.up.dev.d_blkf();
+    p.codesf[1] = L.up.dev.d_codesf();
     p.pre = h;
     p.need_epi = 0;
     WV_TRY(launch_mxg(p, L.gate.dev.dtype, L.gate.dev.scheme == kSchemeBlock32, st));

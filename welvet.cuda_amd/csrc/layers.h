@@ -79,6 +79,11 @@ Status dense_backward(const DenseLayer& L, int batch, const float* x, const floa
 Status dense_apply_sgd(DenseLayer* L, const float* dw, double lr, hipStream_t st);
 // True when `batch` rows take the split + batched-MFMA path.
 bool uses_split(int batch);
+// Builds the operand-order code copy when `batch` rows run the 5..32-row
+// GEMM (sessions call this at mount, their batch being fixed); a no-op
+// otherwise or when the copy exists. Without it that GEMM reads the
+// row-major codes, with the same results.
+Status dense_prepare_rows(DenseLayer* L, int batch, hipStream_t st);
 // The activation-split workspace (Workspace::b): the split terms, then the
 // K-split partial sums of the products that use them.
 inline uint8_t* split_buf(Workspace* ws) { return ws->b.as<uint8_t>(); }
@@ -138,6 +143,8 @@ Status swiglu_build(int in, int inter, int dtype, int scheme, const float* G, co
 Status swiglu_forward(const SwiGLULayer& L, int rows, const float* x, float* h, float* y,
                       Workspace* ws, hipStream_t st);
 size_t swiglu_workspace_bytes(const SwiGLULayer& L, int rows);
+// dense_prepare_rows for the three matrices.
+Status swiglu_prepare_rows(SwiGLULayer* L, int rows, hipStream_t st);
 // SwiGLU backward on device buffers (swiglu.cpp:156-248): from x [rows][in],
 // the forward's h and y, and the output gradient (or, with use_target, the
 // MSE target) in g: dx [rows][in] and dw = [dGate | dUp | dDown] (each

@@ -736,8 +736,15 @@ __global__ __launch_bounds__(64 * kSmallWaves) __attribute__((amdgpu_waves_per_e
   // padded row (their outputs are never stored)
   // Block exponents come from the lane-order copy: the dword of chunk group
   // c / 4 (256 contiguous bytes per wave load), byte c % 4.
+  // With the operand-order copy (codesf) a wave's operand is the 1 KiB at
+  // lane * 16 of its (row block, chunk, half) slot: chunk stride WB * 16
+  // bytes, half stride 1 KiB. Without it, lane (i16, g) reads 16 bytes of
+  // row-major row i16 at chunk offset 16 g: chunk stride WB, half stride 64.
+  // The choice is made once here (uniform); the K loop has no branch on it.
   const int rmax = (p.N + 127) / 128 * 128 - 1;
   const int egroups = (S + 3) / 4;
+  const bool frag = p.codesf[0] != nullptr && (MATS == 1 || p.codesf[MATS - 1] != nullptr);
+  const uint32_t cstride = frag ? WB * 16 : WB, hstride = frag ? 1024 : 64;
   const uint8_t* wrow[MATS][RB];
   const uint8_t* erow[MATS][RB];
 #pragma unroll
@@ -746,7 +753,8 @@ __global__ __launch_bounds__(64 * kSmallWaves) __attribute__((amdgpu_waves_per_e
     for (int j = 0; j < RB; ++j) {
       const int row = n0 + 16 * j + i16 < rmax ? n0 + 16 * j + i16 : rmax;
       const int rb16 = (n0 + 16 * j < rmax ? n0 + 16 * j : rmax) / 16;
-      wrow[m][j] = p.codes[m] + (size_t)row * p.pitch + 16 * g;
+      wrow[m][j] = frag ? p.codesf[m] + (size_t)rb16 * S * (WB * 16) + lane * 16
+                        : p.codes[m] + (size_t)row * p.pitch + 16 * g;
       erow[m][j] = BLK ? p.blkf[m] + (size_t)rb16 * egroups * 256 + lane * 4 : nullptr;
     }
   struct WFrag {
@@ -759,9 +767,9 @@ __global__ __launch_bounds__(64 * kSmallWaves) __attribute__((amdgpu_waves_per_e
     for (int m = 0; m < MATS; ++m)
 #pragma unroll
       for (int j = 0; j < RB; ++j) {
-        const uint8_t* src = wrow[m][j] + (size_t)c * WB;
+        const uint8_t* src = wrow[m][j] + (size_t)c * cstride;
         f.lo[m][j] = *reinterpret_cast<const u32x4*>(src);
-        if constexpr (!FP4) f.hi[m][j] = *reinterpret_cast<const u32x4*>(src + 64);
+        if constexpr (!FP4) f.hi[m][j] = *reinterpret_cast<const u32x4*>(src + hstride);
         f.e[m][j] = BLK ? *reinterpret_cast<const uint32_t*>(erow[m][j] + (size_t)(c >> 2) * 256)
                         : 0x7F7F7F7Fu;
       }

@@ -262,7 +262,36 @@ Status build_blk_frag(DeviceWeights* dw, hipStream_t st) {
   return hip_status(hipGetLastError(), "blk_frag");
 }
 
+// Operand-order copy of the codes (DeviceWeights::codes_frag): one thread
+// per 16-byte lane slot t = ((rb * chunks + c) * halves + h) * 64 + l.
+__global__ __launch_bounds__(kThreads) void k_codes_frag(const uint8_t* __restrict__ codes,
+                                                         int pitch, int chunks, int halves,
+                                                         int64_t n, uint8_t* __restrict__ out) {
+  const int64_t t = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (t >= n) return;
+  const int l = (int)(t & 63);
+  int64_t rest = t >> 6;
+  const int h = (int)(rest % halves);
+  rest /= halves;
+  const int c = (int)(rest % chunks);
+  const int64_t rb = rest / chunks;
+  const int wb = 64 * halves;  // code bytes per row per chunk
+  const uint4 v = *reinterpret_cast<const uint4*>(
+      codes + (size_t)(rb * 16 + (l & 15)) * pitch + (size_t)c * wb + 64 * h + 16 * (l >> 4));
+  *reinterpret_cast<uint4*>(out + (size_t)t * 16) = v;
+}
+
 }  // namespace
+
+Status build_codes_frag(DeviceWeights* dw, hipStream_t st) {
+  if (!dw->codes.p) return Status::err(kInvalid, "codes_frag: no codes");
+  const int chunks = dw->kpad / 128, halves = dw->dtype == kFP4 ? 1 : 2;
+  const int64_t n = (int64_t)(dw->rpad / 16) * chunks * halves * 64;
+  WV_TRY(dw->codes_frag.alloc((size_t)n * 16));
+  k_codes_frag<<<grid_for(n), kThreads, 0, st>>>(dw->codes.as<const uint8_t>(), dw->pitch, chunks,
+                                                 halves, n, dw->codes_frag.as<uint8_t>());
+  return hip_status(hipGetLastError(), "codes_frag");
+}
 
 Status quantize_to_device(const float* dW, int dtype, int scheme, int rows, int cols,
                           DeviceWeights* dw, uint8_t* d_raw, hipStream_t st) {
