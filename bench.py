@@ -3,15 +3,19 @@
 Default workload (c2): Dense GEMV 4096 -> 4096, FP8 E4M3 weights with one fp32
 scale per output row, fp32 in/out, batch 1. One step = one GEMV over one
 batch. Weights are mounted (quantized on the device) once per copy; 64
-distinct copies (1.07 GB, > 4x the 256 MB MALL) are rotated so each step
-streams its weights from HBM. The steps are captured in a HIP graph and timed
-with HIP events on the launch stream.
+distinct copies (1.07 GB, > 4x the 256 MB MALL) are used in a fixed rotation
+that continues across the warmup and the timed regions, so every step reads
+a copy last read 64 steps (1.07 GB of weight traffic) earlier and streams it
+from HBM. Steps are replayed from captured HIP graphs and timed with HIP
+events on the launch stream.
 
 Metric: algorithmic bytes / time for the HBM-bound GEMV workloads (bytes =
 codes + scales + x + y, 16,826,368 B per c2 step), useful FLOP/s (2*M*N*K)
 for the matrix-core GEMM workloads. The CPU baseline is the oracle's
 restatement of the reference contract (f64 decode at mount, f64 serial-K
-matvec) on this host's cores, timed on a bounded sample of the same workload.
+matvec) on this host's cores, timed on a bounded sample of the same workload,
+on all the CPU threads this job is given (at most 16) and on one thread, with
+mount and execute reported separately.
 
 Other workloads (--config), each its own line:
   c1     Dense 512 -> 512, E4M3, per-tensor scale, batch 1
@@ -21,6 +25,9 @@ Other workloads (--config), each its own line:
   c5     64 cells x (Dense 1024^2 E4M3 row -> FP4 block-32 -> E4M3 row), batch 256
   c5chain  the same cells as the reference's volume: one 192-layer serial chain (model session)
   c2bwd  Dense backward at the GEMV shape: d_pre, dX = W^T d_pre, dW (4096^2 E4M3 per-row, batch 1)
+--read-floor BYTES instead times one streaming read of BYTES (default: the c2
+step's 16,826,368) over 64 rotated buffers, the same way: the floor for any
+kernel that reads those bytes once.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2]
 """
@@ -36,11 +43,15 @@ sys.path.insert(0, os.path.join(ROOT, "welvet.cuda_amd"))
 
 HBM_PEAK_GBS = 8000.0
 REPEATS = 3  # timed regions per run; the median is reported
-WARMUP_S = 0.2  # default warmup: at least this long (seconds) of replays
+WARMUP_S = 0.2  # warmup lasts at least this long (clocks leave their idle level)
 # dense MFMA peak of the f8f6f4 instruction with an FP8 operand (the activation
 # terms are E4M3, so FP4 weights run at the FP8 rate)
 MFMA_FP8_PEAK_TFLOPS = 5000.0
 METRIC = "FP8/FP4 Dense GEMV GB/s + GEMM TFLOPS (% roofline), 1 MI355X vs host CPU"
+# CPU threads for the baseline: the job's CPU share (the affinity mask),
+# capped at the 16 threads a one-GPU job is given on the GPU hosts
+CPU_THREAD_CAP = 16
+C2_BYTES = 16826368
 
 # rocprof summaries (kernel stats + FETCH_SIZE/WRITE_SIZE scaled by a copy of
 # known size) per workload; `traffic_bytes:` is the measured HBM bytes per launch.
@@ -67,8 +78,18 @@ def oracle():
     return oracle_lib.Oracle()
 
 
+def cpu_threads():
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    return max(1, min(CPU_THREAD_CAP, n))
+
+
 def cpu_dense_seconds(orc, dtype, scheme, batch, K, N, W, x, threads, budget_s):
-    """Seconds per execute of the oracle's reference-contract Dense (f64 W)."""
+    """(seconds per execute, executes timed, mount seconds) of the oracle's
+    reference-contract Dense (f64 W, serial K) on `threads` threads: 3 warmup
+    executes, then as many as fit the budget (at least 2)."""
     import numpy as np
 
     native, rs, blk = orc.quantize(dtype, scheme, N, K, W)
@@ -79,13 +100,37 @@ def cpu_dense_seconds(orc, dtype, scheme, batch, K, N, W, x, threads, budget_s):
     x = np.ascontiguousarray(x, np.float32)
     args = (dtype, scheme, batch, K, N, native.ctypes.data_as(u8), rs.ctypes.data_as(fp),
             blk.ctypes.data_as(u8), x.ctypes.data_as(fp), y.ctypes.data_as(fp), threads)
-    t1 = orc.L.or_cpu_dense_bench(*args, 1, 1, ctypes.byref(mount))
+    t1 = orc.L.or_cpu_dense_bench(*args, 0, 1, ctypes.byref(mount))
     iters = max(2, int(budget_s / max(t1, 1e-6)))
-    return orc.L.or_cpu_dense_bench(*args, 1, iters, ctypes.byref(mount)), iters, mount.value
+    per = orc.L.or_cpu_dense_bench(*args, 3, iters, ctypes.byref(mount))
+    return per, iters, mount.value
 
 
-def cpu_threads():
-    return max(1, min(16, os.cpu_count() or 1))
+def cpu_layers(layers, budget_s):
+    """Times the Dense layers of one step (list of (dtype, scheme, batch, K,
+    N, W, x)) on cpu_threads() threads and on one thread. Returns seconds per
+    step for both, the mount seconds and a description."""
+    orc = oracle()
+    th = cpu_threads()
+    per_n = per_1 = mount = 0.0
+    parts = []
+    share = budget_s / (2 * len(layers))
+    for (dt, sc, batch, K, N, W, x) in layers:
+        pn, itn, mn = cpu_dense_seconds(orc, dt, sc, batch, K, N, W, x, th, share)
+        p1, it1, _ = cpu_dense_seconds(orc, dt, sc, batch, K, N, W, x, 1, share)
+        per_n += pn
+        per_1 += p1
+        mount += mn
+        parts.append(f"{N}x{K} batch {batch}: {pn * 1e3:.3f} ms ({itn} runs) on {th} threads, "
+                     f"{p1 * 1e3:.3f} ms ({it1} runs) on 1")
+    return per_n, per_1, mount, th, "; ".join(parts)
+
+
+def cpu_record(value_n, value_1, unit, th, per_n, per_1, mount, sample):
+    return {"value": value_n, "unit": unit, "cores": th, "kind": "port",
+            "value_1thread": value_1, "execute_s": round(per_n, 6),
+            "execute_s_1thread": round(per_1, 6), "mount_s": round(mount, 4),
+            "host_threads_visible": os.cpu_count(), "sample": sample}
 
 
 # --------------------------------------------------------------------------
@@ -114,19 +159,23 @@ def dense_workload(pw, hip, name, cfg_id, dtype, scheme, batch, K, N, copies, bo
         sessions[i % copies].execute_device(dx, dy, dy, stream)
 
     def cpu(budget_s):
-        orc = oracle()
         rows = min(batch, 256)
-        per, iters, mount = cpu_dense_seconds(orc, dtype, scheme, rows, K, N, W, x[:rows],
-                                              cpu_threads(), budget_s)
-        per_step = per * batch / rows
-        val = (nbytes / per_step / 1e9) if bound == "hbm" else (flops / per_step / 1e12)
-        return {"value": round(val, 4), "unit": "GB/s" if bound == "hbm" else "TFLOP/s",
-                "cores": cpu_threads(), "kind": "port",
-                "sample": (f"oracle restatement of the reference Dense contract on this host: f64 "
-                           f"decode of the codes ({mount * 1e3:.0f} ms mount), then {iters} f64 "
-                           f"serial-K executes {N}x{K} of {rows} of the {batch} rows over "
-                           f"{cpu_threads()} threads, {per * 1e3:.3f} ms each"
-                           + (f", scaled x{batch // rows} to the full batch" if rows < batch else ""))}
+        per_n, per_1, mount, th, desc = cpu_layers([(dtype, scheme, rows, K, N, W, x[:rows])],
+                                                   budget_s)
+        f = batch / rows
+
+        def val(per):
+            per_step = per * f
+            return round(nbytes / per_step / 1e9, 4) if bound == "hbm" else round(
+                flops / per_step / 1e12, 5)
+
+        return cpu_record(val(per_n), val(per_1), "GB/s" if bound == "hbm" else "TFLOP/s", th,
+                          per_n * f, per_1 * f, mount,
+                          "oracle restatement of the reference Dense contract on this host: f64 "
+                          f"decode of the codes at mount ({mount * 1e3:.0f} ms), then f64 serial-K "
+                          f"executes: {desc}"
+                          + (f"; {rows} of the {batch} rows timed, scaled x{f:g}" if rows < batch
+                             else ""))
 
     def close():
         for s in sessions:
@@ -164,21 +213,15 @@ def swiglu_workload(pw, hip, name, batch, copies):
         sessions[i % copies].execute_device(dx, dh, dy, stream)
 
     def cpu(budget_s):
-        orc = oracle()
-        t = 0.0
-        parts = []
-        for (K, N, Wm) in ((d, f, G), (d, f, U), (f, d, D)):
-            xs = x if K == d else np.random.default_rng(1).standard_normal((batch, f)).astype(np.float32)
-            per, iters, _ = cpu_dense_seconds(orc, 16, 3, batch, K, N, Wm, xs, cpu_threads(),
-                                              budget_s / 3)
-            t += per
-            parts.append(f"{N}x{K}: {per * 1e3:.2f} ms ({iters} runs)")
-        return {"value": round(nbytes / t / 1e9, 4), "unit": "GB/s", "cores": cpu_threads(),
-                "kind": "port",
-                "sample": ("oracle restatement of the reference Dense contract (f64 W, serial K) "
-                           "for gate, up and down at batch " + str(batch) + " over "
-                           + str(cpu_threads()) + " threads: " + "; ".join(parts)
-                           + " (SiLU product not timed)")}
+        hx = np.random.default_rng(1).standard_normal((batch, f)).astype(np.float32)
+        per_n, per_1, mount, th, desc = cpu_layers(
+            [(16, 3, batch, d, f, G, x), (16, 3, batch, d, f, U, x), (16, 3, batch, f, d, D, hx)],
+            budget_s)
+        return cpu_record(round(nbytes / per_n / 1e9, 4), round(nbytes / per_1 / 1e9, 4), "GB/s",
+                          th, per_n, per_1, mount,
+                          "oracle restatement of the reference Dense contract (f64 W, serial K) "
+                          f"for gate, up and down at batch {batch} (SiLU product not timed): "
+                          + desc)
 
     def close():
         for s in sessions:
@@ -263,21 +306,16 @@ def cells_workload(pw, hip, name):
         chain.execute(stream)
 
     def cpu(budget_s):
-        orc = oracle()
-        t = 0.0
         rng = np.random.default_rng(5)
-        for dt, sc in kinds:
-            W = rng.standard_normal((d, d)).astype(np.float32) / 32
-            xs = rng.standard_normal((batch, d)).astype(np.float32)
-            per, _, _ = cpu_dense_seconds(orc, dt, sc, batch, d, d, W, xs, cpu_threads(),
-                                          budget_s / 3)
-            t += per
-        per_step = t * cells
-        return {"value": round(flops / per_step / 1e12, 5), "unit": "TFLOP/s",
-                "cores": cpu_threads(), "kind": "port",
-                "sample": (f"oracle restatement of the reference Dense contract for one cell "
-                           f"(3 layers 1024x1024 at batch {batch}, {t * 1e3:.1f} ms over "
-                           f"{cpu_threads()} threads), scaled x{cells} to the 64 cells")}
+        layers = [(dt, sc, batch, d, d, rng.standard_normal((d, d)).astype(np.float32) / 32,
+                   rng.standard_normal((batch, d)).astype(np.float32)) for dt, sc in kinds]
+        per_n, per_1, mount, th, desc = cpu_layers(layers, budget_s)
+        return cpu_record(round(flops / (per_n * cells) / 1e12, 5),
+                          round(flops / (per_1 * cells) / 1e12, 6), "TFLOP/s", th, per_n * cells,
+                          per_1 * cells, mount * cells,
+                          "oracle restatement of the reference Dense contract for one cell (3 "
+                          f"layers 1024x1024 at batch {batch}): {desc}; scaled x{cells} to the "
+                          "64 cells")
 
     def close():
         chain.close()
@@ -386,20 +424,30 @@ def backward_workload(pw, hip, name, copies):
 
     def cpu(budget_s):
         orc = oracle()
+        t0 = time.perf_counter()
         native, rs, blk = orc.quantize(4, 2, N, K, W)
         Wd = orc.dequant(4, 2, N, K, native, rs, blk)
+        mount = time.perf_counter() - t0
         pre = (x.astype(np.float64) @ Wd.T.astype(np.float64)).astype(np.float32)
         th = cpu_threads()
-        orc.backward(Wd, g, pre, x, -1, threads=th)  # warm
-        t0, iters = time.perf_counter(), 0
-        while time.perf_counter() - t0 < budget_s or iters < 2:
-            orc.backward(Wd, g, pre, x, -1, threads=th)
-            iters += 1
-        per = (time.perf_counter() - t0) / iters
-        return {"value": round(nbytes / per / 1e9, 4), "unit": "GB/s", "cores": th, "kind": "port",
-                "sample": (f"oracle restatement of the reference NormalBP backward (act', f64 serial "
-                           f"MatVec^T over {th} threads, per-batch-row f32 outer product) on the "
-                           f"dequantized f32 W: {iters} runs, {per * 1e3:.2f} ms each")}
+
+        def timed(threads, budget):
+            for _ in range(3):
+                orc.backward(Wd, g, pre, x, -1, threads=threads)
+            t1, iters = time.perf_counter(), 0
+            while time.perf_counter() - t1 < budget or iters < 2:
+                orc.backward(Wd, g, pre, x, -1, threads=threads)
+                iters += 1
+            return (time.perf_counter() - t1) / iters, iters
+
+        per_n, itn = timed(th, budget_s / 2)
+        per_1, it1 = timed(1, budget_s / 2)
+        return cpu_record(round(nbytes / per_n / 1e9, 4), round(nbytes / per_1 / 1e9, 4), "GB/s",
+                          th, per_n, per_1, mount,
+                          "oracle restatement of the reference NormalBP backward (act', f64 serial "
+                          "MatVec^T, per-batch-row f32 outer product) on the dequantized f32 W: "
+                          f"{per_n * 1e3:.2f} ms ({itn} runs) on {th} threads, {per_1 * 1e3:.2f} "
+                          f"ms ({it1} runs) on 1")
 
     def close():
         for s in sessions:
@@ -461,29 +509,107 @@ def copy_calibration(pw, nbytes, steps):
     hip.free(dst)
 
 
+def read_floor_workload(pw, hip, nbytes, copies):
+    """One streaming read of nbytes per step over `copies` rotated buffers."""
+    bufs = [hip.malloc(nbytes) for _ in range(copies)]
+    for b in bufs:
+        hip.memset(b, 0x5A, nbytes)
+    words = pw.lib().welvet_read_probe_words(nbytes)
+    out = hip.malloc(4 * words)
+
+    def enqueue(i, stream):
+        pw.check(pw.lib().welvet_read_probe(ctypes.c_void_p(bufs[i % copies]), nbytes,
+                                            ctypes.c_void_p(out), words, ctypes.c_void_p(stream)))
+
+    def close():
+        for b in bufs + [out]:
+            hip.free(b)
+
+    return {"desc": "read_floor", "enqueue": enqueue, "per_graph": copies, "bytes": nbytes,
+            "flops": 0, "bound": "hbm", "dtype": "u8",
+            "config": {"workload": f"streaming_read_{nbytes}B", "buffers_rotated": copies,
+                       "loads": "16-byte non-temporal, 4 per lane in flight, one XOR digest "
+                                "per 256-lane workgroup"},
+            "cpu": None, "close": close}
+
+
 CONFIGS = ["c1", "c2", "c3", "c3b16", "c4", "c4mha", "c5", "c5chain", "c2bwd"]
+
+
+class Runner:
+    """Steps replayed from captured graphs in one rotation over the workload's
+    copies (step i uses copy i mod copies) that continues from one call to the
+    next, so every step reads the copy least recently used. A graph of n
+    steps from rotation offset o is captured once and kept."""
+
+    def __init__(self, hip, wl, stream):
+        self.hip, self.wl, self.stream = hip, wl, stream
+        self.per = max(1, wl["per_graph"])
+        self.direct = wl.get("direct", False)  # synchronous calls: no capture
+        self.offset = 0
+        self.graphs = {}
+
+    def _graph(self, start, count):
+        key = (start % self.per, count)
+        if key not in self.graphs:
+            def go():
+                for i in range(start, start + count):
+                    self.wl["enqueue"](i, self.stream)
+            self.graphs[key] = self.hip.capture(self.stream, go)
+        return self.graphs[key]
+
+    def prepare(self, n):
+        """Captures the graphs a call of n steps from the current offset uses."""
+        if self.direct:
+            return
+        full, rem = divmod(n, self.per)
+        if full:
+            self._graph(self.offset, self.per)
+        if rem:
+            self._graph(self.offset, rem)
+
+    def run(self, n):
+        """Queues n steps (call prepare(n) first to keep capture out of timing)."""
+        if self.direct:
+            for i in range(self.offset, self.offset + n):
+                self.wl["enqueue"](i, self.stream)
+            self.offset = (self.offset + n) % self.per
+            return
+        full, rem = divmod(n, self.per)
+        for _ in range(full):
+            self.hip.launch(self._graph(self.offset, self.per), self.stream)
+        if rem:
+            self.hip.launch(self._graph(self.offset, rem), self.stream)
+            self.offset = (self.offset + rem) % self.per
+
+    def close(self):
+        for g in self.graphs.values():
+            self.hip.graph_free(g)
+        self.graphs = {}
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None,
-                    help="timed steps (default: 1280 for the GEMV workloads, fewer for the rest)")
+                    help="timed steps (default: 1280 for the GEMV workloads, 64 for the rest)")
     ap.add_argument("--warmup", type=int, default=None,
-                    help="untimed warmup steps (default: graph replays for at least WARMUP_S seconds)")
+                    help="untimed warmup steps; the warmup also lasts at least WARMUP_S seconds")
     ap.add_argument("--config", default="c2", choices=CONFIGS)
     ap.add_argument("--copies", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run device-to-device copies of MIB MiB (the known-size copy "
                          "that scales the FETCH_SIZE/WRITE_SIZE counters) and exit")
+    ap.add_argument("--read-floor", type=int, nargs="?", const=C2_BYTES, default=0,
+                    metavar="BYTES",
+                    help="time a plain streaming read of BYTES (default: the c2 step's bytes) "
+                         "instead of a workload")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU; --gpus above 1 is not part of it",
               file=sys.stderr)
         sys.exit(2)
-
-    import numpy as np
 
     import pywelvet as pw
 
@@ -493,54 +619,43 @@ def main():
 
     pw.check(pw.lib().welvet_cuda_init())
     hip = pw.Hip()
-    wl = make_workload(pw, hip, args.config, max(1, args.copies))
-    gemv = args.config in ("c1", "c2", "c3", "c3b16")
-    steps = args.steps if args.steps is not None else (1280 if gemv else 64)
-    # default warmup: replays until at least WARMUP_S of GPU time has passed,
-    # so the clocks have left their idle level (reported as the step count)
-    warmup = args.warmup
-    per = max(1, min(wl["per_graph"], steps))
-    stream = hip.stream()
-
-    def enqueue(n):
-        def go():
-            for i in range(n):
-                wl["enqueue"](i, stream)
-        return go
-
-    full, rem = divmod(steps, per)
-    direct = wl.get("direct", False)  # synchronous calls: no graph capture
-    g_full = enqueue(per) if direct else hip.capture(stream, enqueue(per))
-    g_rem = (enqueue(rem) if direct else hip.capture(stream, enqueue(rem))) if rem else None
-    launch = (lambda g, st: g()) if direct else hip.launch
-    if warmup is not None:
-        for _ in range(max(1, (warmup + per - 1) // per)):
-            launch(g_full, stream)
-        hip.sync()
+    if args.read_floor:
+        wl = read_floor_workload(pw, hip, args.read_floor, max(1, args.copies))
+        gemv = True
     else:
-        warmup, t0 = 0, time.perf_counter()
-        while time.perf_counter() - t0 < WARMUP_S or warmup < steps:
-            launch(g_full, stream)
-            hip.sync()
-            warmup += per
-    hip.sync()
+        wl = make_workload(pw, hip, args.config, max(1, args.copies))
+        gemv = args.config in ("c1", "c2", "c3", "c3b16")
+    steps = args.steps if args.steps is not None else (1280 if gemv else 64)
+    steps = max(1, steps)
+    stream = hip.stream()
+    runner = Runner(hip, wl, stream)
+
+    # warmup: at least the requested steps and at least WARMUP_S seconds, in
+    # whole rotations (the clocks start from their idle level)
+    want = args.warmup if args.warmup is not None else 0
+    runner.prepare(runner.per)
+    warmup, t0 = 0, time.perf_counter()
+    while warmup < want or time.perf_counter() - t0 < WARMUP_S:
+        runner.run(runner.per)
+        hip.sync()
+        warmup += runner.per
     # The timed region (exactly `steps` steps between device synchronizations)
     # runs REPEATS times; the median is reported, so one disturbed run does not
     # become the result (the three times are in config.ms_runs).
     e0, e1 = hip.event(), hip.event()
     runs = []
-    t_wall = time.perf_counter()
+    t_wall = 0.0
     for _ in range(REPEATS):
+        runner.prepare(steps)
         hip.sync()
+        t1 = time.perf_counter()
         hip.record(e0, stream)
-        for _ in range(full):
-            launch(g_full, stream)
-        if g_rem:
-            launch(g_rem, stream)
+        runner.run(steps)
         hip.record(e1, stream)
         hip.sync()
+        t_wall += time.perf_counter() - t1
         runs.append(hip.elapsed_ms(e0, e1))
-    t_wall = (time.perf_counter() - t_wall) / REPEATS
+    t_wall /= REPEATS
     ms = sorted(runs)[len(runs) // 2]
     per_step_s = ms * 1e-3 / steps
 
@@ -549,16 +664,22 @@ def main():
     if wl["bound"] == "hbm":
         value, unit = gbs, "GB/s"
         roof = {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(args.config)}
+                "frac": round(gbs / HBM_PEAK_GBS, 4),
+                "traffic": None if args.read_floor else measured_traffic(args.config)}
     else:
         value, unit = tflops, "TFLOP/s"
         roof = {"bound": "mfma", "achieved": round(tflops, 3), "peak": MFMA_FP8_PEAK_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(tflops / MFMA_FP8_PEAK_TFLOPS, 4),
                 "traffic": measured_traffic(args.config)}
-    cpu = None if (args.no_cpu or wl["cpu"] is None) else wl["cpu"](10.0)
+    cpu = None if (args.no_cpu or wl["cpu"] is None) else wl["cpu"](16.0)
     config = dict(wl["config"])
+    rotated = min(runner.per, steps) if runner.direct else runner.per
     config.update({"tflops": round(tflops, 4), "wall_s": round(t_wall, 4),
-                   "ms_runs": [round(r, 4) for r in runs], "timed_regions": REPEATS})
+                   "ms_runs": [round(r, 4) for r in runs], "timed_regions": REPEATS,
+                   "copies_rotated": rotated,
+                   "rotation": ("one rotation over the copies continuing across warmup and "
+                                "timed regions: each step reads the least recently used copy")})
+    config.pop("weight_copies_rotated", None)
     if wl["bytes"]:
         config.update({"algorithmic_bytes_per_step": wl["bytes"], "gbs": round(gbs, 2)})
     line = {
@@ -579,10 +700,7 @@ def main():
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
-    if not direct:
-        hip.graph_free(g_full)
-        if g_rem:
-            hip.graph_free(g_rem)
+    runner.close()
     wl["close"]()
 
 

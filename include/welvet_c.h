@@ -214,6 +214,16 @@ WELVET_API welvet_status welvet_model_forward_device(welvet_model_session* s, co
 WELVET_API welvet_status welvet_codec_sweep(int32_t dtype, uint32_t first_chunk,
                                             uint32_t n_chunks, int64_t* out);
 
+/* Measurement extension, no reference counterpart: one streaming read of the
+ * device buffer buf (bytes a positive multiple of 16) with 16-byte loads,
+ * queued on `stream` (null: the default stream); out_words (device,
+ * welvet_read_probe_words(bytes) entries, out_cap of them available)
+ * receives one XOR digest per workgroup. Its duration is the floor for any
+ * kernel that reads the same bytes once. */
+WELVET_API welvet_status welvet_read_probe(const void* buf, size_t bytes, uint32_t* out_words,
+                                           size_t out_cap, void* stream);
+WELVET_API size_t welvet_read_probe_words(size_t bytes);
+
 /* Segment backward of a Stack model of Dense / SwiGLU children (replaces reference
  * include/welvet_c.h:55, src/interop/model_session.cpp:435-455): the input
  * blob holds the tensors x and gy (model wire: rank, dims, float32 data);

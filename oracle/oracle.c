@@ -581,15 +581,28 @@ static double alibi(int head, int heads, int qp, int kp, int on) {
   return -slope * (double)d;
 }
 
-void or_mha_attention(const float* q, const float* k, const float* v, float* attn, int batch,
-                      int seq, int num_heads, int num_kv, int head_dim, int msl, int mask,
-                      int pos_kind, int softmax_kind, int window, int prefix_len, int window_causal,
-                      double rope_theta, double scale_override) {
+/* The attention of one set of query heads (h = h0, h0 + hstep, ...). Each
+ * head's arithmetic is the reference's loop (kernels.cu:536-631) restricted
+ * to that head: the ring rows of its KV head and its query rows, rotated per
+ * head as the reference rotates them (heads are rotated independently), so
+ * the result does not depend on how heads are spread over threads. */
+typedef struct {
+  const float *q, *k, *v;
+  float* attn;
+  int batch, seq, num_heads, num_kv, head_dim, msl, mask, pos_kind, softmax_kind, window,
+      prefix_len, window_causal;
+  double rope_theta, scale_override;
+  int h0, hstep;
+} attn_job;
+
+static void attn_heads(const attn_job* j) {
+  const int batch = j->batch, seq = j->seq, num_heads = j->num_heads, num_kv = j->num_kv;
+  const int head_dim = j->head_dim, msl = j->msl;
   const int qd = num_heads * head_dim, kvd = num_kv * head_dim;
   const int per_kv = num_heads / num_kv;
-  const double scale = scale_override > 0.0 ? scale_override : 1.0 / sqrt((double)head_dim);
-  const int rope = (pos_kind == 0 || pos_kind == 3);
-  const int use_alibi = (pos_kind == 2 || pos_kind == 3);
+  const double scale = j->scale_override > 0.0 ? j->scale_override : 1.0 / sqrt((double)head_dim);
+  const int rope = (j->pos_kind == 0 || j->pos_kind == 3);
+  const int use_alibi = (j->pos_kind == 2 || j->pos_kind == 3);
   double* ck = (double*)calloc((size_t)msl * kvd, sizeof(double));
   double* cv = (double*)calloc((size_t)msl * kvd, sizeof(double));
   double* Q = (double*)malloc((size_t)seq * qd * sizeof(double));
@@ -601,29 +614,32 @@ void or_mha_attention(const float* q, const float* k, const float* v, float* att
     for (int s = 0; s < seq; ++s) {
       const int pos = base + s;
       const int64_t tok = (int64_t)b * seq + s;
-      for (int i = 0; i < qd; ++i) Q[(int64_t)s * qd + i] = (double)q[tok * qd + i];
+      for (int i = 0; i < qd; ++i) Q[(int64_t)s * qd + i] = (double)j->q[tok * qd + i];
       double* kr = ck + (int64_t)(pos % msl) * kvd;
       double* vr = cv + (int64_t)(pos % msl) * kvd;
       for (int i = 0; i < kvd; ++i) {
-        kr[i] = (double)k[tok * kvd + i];
-        vr[i] = (double)v[tok * kvd + i];
+        kr[i] = (double)j->k[tok * kvd + i];
+        vr[i] = (double)j->v[tok * kvd + i];
       }
       if (rope) {
-        rope_rotate(Q + (int64_t)s * qd, pos, num_heads, head_dim, rope_theta);
-        rope_rotate(kr, pos, num_kv, head_dim, rope_theta);
+        for (int h = j->h0; h < num_heads; h += j->hstep)
+          rope_rotate(Q + (int64_t)s * qd + (int64_t)h * head_dim, pos, 1, head_dim, j->rope_theta);
+        for (int kh = 0; kh < num_kv; ++kh)
+          rope_rotate(kr + (int64_t)kh * head_dim, pos, 1, head_dim, j->rope_theta);
       }
     }
     const int kv_len = base + seq;
     for (int s = 0; s < seq; ++s) {
       const int qp = base + s;
-      for (int h = 0; h < num_heads; ++h) {
+      for (int h = j->h0; h < num_heads; h += j->hstep) {
         const int kvh = h / per_kv;
         const double* qv = Q + (int64_t)s * qd + (int64_t)h * head_dim;
-        float* out = attn + ((int64_t)b * seq + s) * qd + (int64_t)h * head_dim;
+        float* out = j->attn + ((int64_t)b * seq + s) * qd + (int64_t)h * head_dim;
         int n = 0;
         double mx = -1e9;
         for (int kp = 0; kp < kv_len; ++kp) {
-          if (!attn_allow(qp, kp, mask, window, msl, prefix_len, window_causal)) continue;
+          if (!attn_allow(qp, kp, j->mask, j->window, msl, j->prefix_len, j->window_causal))
+            continue;
           const double* kr = ck + (int64_t)(kp % msl) * kvd + (int64_t)kvh * head_dim;
           double dot = 0.0;
           for (int d = 0; d < head_dim; ++d) dot += qv[d] * kr[d];
@@ -637,7 +653,7 @@ void or_mha_attention(const float* q, const float* k, const float* v, float* att
           for (int d = 0; d < head_dim; ++d) out[d] = 0.0f;
           continue;
         }
-        if (softmax_kind == 1) {
+        if (j->softmax_kind == 1) {
           for (int i = 0; i < n; ++i) sc[i] = 1.0 / (1.0 + exp(-sc[i]));
         } else {
           double sum = 0.0;
@@ -662,6 +678,47 @@ void or_mha_attention(const float* q, const float* k, const float* v, float* att
   free(Q);
   free(sc);
   free(kpos);
+}
+
+static void* attn_worker(void* p) {
+  attn_heads((const attn_job*)p);
+  return NULL;
+}
+
+void or_mha_attention_mt(const float* q, const float* k, const float* v, float* attn, int batch,
+                         int seq, int num_heads, int num_kv, int head_dim, int msl, int mask,
+                         int pos_kind, int softmax_kind, int window, int prefix_len,
+                         int window_causal, double rope_theta, double scale_override,
+                         int nthreads) {
+  attn_job base = {q, k, v, attn, batch, seq, num_heads, num_kv, head_dim, msl, mask, pos_kind,
+                   softmax_kind, window, prefix_len, window_causal, rope_theta, scale_override,
+                   0, 1};
+  if (nthreads < 1) nthreads = 1;
+  if (nthreads > num_heads) nthreads = num_heads;
+  if (nthreads == 1) {
+    attn_heads(&base);
+    return;
+  }
+  pthread_t* th = (pthread_t*)calloc((size_t)nthreads, sizeof(pthread_t));
+  attn_job* jobs = (attn_job*)calloc((size_t)nthreads, sizeof(attn_job));
+  for (int t = 0; t < nthreads; ++t) {
+    jobs[t] = base;
+    jobs[t].h0 = t;
+    jobs[t].hstep = nthreads;
+    pthread_create(&th[t], NULL, attn_worker, &jobs[t]);
+  }
+  for (int t = 0; t < nthreads; ++t) pthread_join(th[t], NULL);
+  free(th);
+  free(jobs);
+}
+
+void or_mha_attention(const float* q, const float* k, const float* v, float* attn, int batch,
+                      int seq, int num_heads, int num_kv, int head_dim, int msl, int mask,
+                      int pos_kind, int softmax_kind, int window, int prefix_len, int window_causal,
+                      double rope_theta, double scale_override) {
+  or_mha_attention_mt(q, k, v, attn, batch, seq, num_heads, num_kv, head_dim, msl, mask, pos_kind,
+                      softmax_kind, window, prefix_len, window_causal, rope_theta, scale_override,
+                      1);
 }
 
 /* ------------------------------------------------------------------------- */

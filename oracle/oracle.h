@@ -102,6 +102,13 @@ void or_mha_attention(const float* q, const float* k, const float* v, float* att
                       int seq, int num_heads, int num_kv, int head_dim, int msl, int mask,
                       int pos_kind, int softmax_kind, int window, int prefix_len, int window_causal,
                       double rope_theta, double scale_override);
+/* The same on nthreads threads, heads spread over them (bit-identical: each
+ * head's arithmetic is unchanged). */
+void or_mha_attention_mt(const float* q, const float* k, const float* v, float* attn, int batch,
+                         int seq, int num_heads, int num_kv, int head_dim, int msl, int mask,
+                         int pos_kind, int softmax_kind, int window, int prefix_len,
+                         int window_causal, double rope_theta, double scale_override,
+                         int nthreads);
 
 /* --- Dense backward (NormalBP) and SGD --------------------------------------
  * act'(x) in f64: src/cuda/kernels.cu:48-81 (host twin src/core/activate.cpp:31-63).

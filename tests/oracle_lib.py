@@ -44,6 +44,8 @@ class Oracle:
         L.or_dense_forward.argtypes = [_i, _i, _i, _i, _fp, _dp, _i, _fp, _fp, _fp, _i]
         L.or_swiglu_product.argtypes = [_fp, _fp, _fp, ctypes.c_int64]
         L.or_mha_attention.argtypes = [_fp, _fp, _fp, _fp] + [_i] * 12 + [ctypes.c_double] * 2
+        L.or_mha_attention_mt.argtypes = ([_fp, _fp, _fp, _fp] + [_i] * 12
+                                          + [ctypes.c_double] * 2 + [_i])
         L.or_act_deriv.restype = ctypes.c_double
         L.or_act_deriv.argtypes = [_i, ctypes.c_double]
         L.or_dense_backward.argtypes = [_i, _i, _i, _i, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _i]
@@ -117,14 +119,14 @@ class Oracle:
 
     def mha_attention(self, q, k, v, batch, seq, heads, kv_heads, hd, msl, mask=1, pos=0,
                       softmax=0, window=0, prefix_len=0, window_causal=1, theta=10000.0,
-                      scale=0.0):
+                      scale=0.0, threads=1):
         q = np.ascontiguousarray(q, np.float32)
         k = np.ascontiguousarray(k, np.float32)
         v = np.ascontiguousarray(v, np.float32)
         out = np.zeros((batch * seq, heads * hd), np.float32)
-        self.L.or_mha_attention(_f(q), _f(k), _f(v), _f(out), batch, seq, heads, kv_heads, hd,
-                                msl, mask, pos, softmax, window, prefix_len, window_causal, theta,
-                                scale)
+        self.L.or_mha_attention_mt(_f(q), _f(k), _f(v), _f(out), batch, seq, heads, kv_heads, hd,
+                                   msl, mask, pos, softmax, window, prefix_len, window_causal,
+                                   theta, scale, threads)
         return out
 
     def activate(self, act, x):

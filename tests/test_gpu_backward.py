@@ -217,3 +217,24 @@ def test_swiglu_normalbp_matches_oracle(gpu, oracle, dt, scheme, batch, seq, d, 
             want = oracle.dequant(dt, scheme, W.shape[0], W.shape[1], n2, rs2, blk2)
             assert np.array_equal(wa[off:off + n].reshape(W.shape), want)
         off += n
+
+
+@pytest.mark.parametrize("dt", [4, 5])
+def test_release_smoke_normalbp_known_answer(gpu, oracle, dt):
+    """The reference's packaged check (scripts/release_smoke.py:55-70): 2x2
+    identity, x = (0.5, -0.25), MSE target 0, lr 0.1. The reference runs it
+    with FP32 weights; the identity and x are exact in FP8, so the forward,
+    the loss 0.15625 and dW hold as they are, and the updated weights
+    (0.975, 0.0125, 0.0125, 0.99375) are those values re-encoded in the
+    FP8 format (the store re-quantizes after SGD, native_codec.cpp:1080-1133)."""
+    W = np.eye(2, dtype=np.float32)
+    x = np.array([[0.5, -0.25]], np.float32)
+    t = np.zeros((1, 2), np.float32)
+    pre, post, dx, dw, wa, loss = gpu.dense_normalbp(1, 2, 2, -1, dt, 0, W, x, t, True, 0.1)
+    assert post.tolist() == [[0.5, -0.25]] and pre.tolist() == [[0.5, -0.25]]
+    assert abs(loss - 0.15625) < 1e-6
+    assert dw.tolist() == [[0.25, -0.125], [-0.125, 0.0625]]
+    assert dx.tolist() == [[0.5, -0.25]]
+    expected = np.array([0.975, 0.0125, 0.0125, 0.99375], np.float32)
+    requant = np.array([oracle.decode(dt, oracle.encode(dt, v)) for v in expected], np.float32)
+    assert np.array_equal(wa.ravel(), requant)

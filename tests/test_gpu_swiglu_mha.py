@@ -132,3 +132,36 @@ def test_mha_seq_above_max_is_invalid(gpu):
     with pytest.raises(pw.WelvetError) as e:
         pw.MHASession(1, 9, 16, 2, 2, 0, 8, 1, 0, 5, 0, W, W, W, W)
     assert e.value.code == 1
+
+
+@pytest.mark.parametrize("mask,pos", [(0, 0), (5, 0), (7, 1), (-3, 0), (1, 4), (2, -1), (5, 9)])
+def test_mha_out_of_range_kinds_match_reference(gpu, oracle, mask, pos):
+    """The reference passes mask / position kinds through unchecked
+    (c_abi.cpp:805-806): masks other than 2, 3, 4 (Unspecified 0, Custom 5
+    and any other value) attend causally, and position kinds outside 0-3
+    apply no rotation and no ALiBi (kernels.cu:470-485, 550-551). The oracle
+    follows the same reading with the raw values."""
+    B, S, d, H, KVH, msl = 2, 24, 64, 4, 2, 24
+    dt, scheme = 5, 2
+    hd = d // H
+    rng = np.random.default_rng(300 + 10 * mask + pos)
+    Q = (rng.standard_normal((H * hd, d)) / np.sqrt(d)).astype(np.float32)
+    K = (rng.standard_normal((KVH * hd, d)) / np.sqrt(d)).astype(np.float32)
+    V = (rng.standard_normal((KVH * hd, d)) / np.sqrt(d)).astype(np.float32)
+    O = (rng.standard_normal((d, H * hd)) / np.sqrt(H * hd)).astype(np.float32)
+    x = rng.standard_normal((B * S, d)).astype(np.float32)
+    s = gpu.MHASession(B, S, d, H, KVH, 0, msl, mask, pos, dt, scheme, Q, K, V, O)
+    attn, y = s.execute(x)
+    s.close()
+    oattn, oy = oracle_mha(oracle, dt, scheme, Q, K, V, O, x, B, S, H, KVH, hd, msl, mask, pos)
+    assert rel_l2(attn, oattn) <= 1e-4
+    assert rel_l2(y, oy) <= 1e-4
+
+
+def test_runtime_identity_names_the_device(gpu):
+    """The identity carries a device name (reference device.cpp:57-59:
+    "cuda:<name>:idx:..."), here "hip:<name>:idx=0:arch=...": the name field
+    is never empty."""
+    ident = gpu.lib().welvet_runtime_identity().decode()
+    parts = ident.split(":")
+    assert parts[0] == "hip" and parts[1] != "" and parts[2] == "idx=0", ident

@@ -155,3 +155,37 @@ def test_attention_matches_closed_form_ring(oracle, B, S, msl, mask, pos, softma
     got = oracle.mha_attention(q, k, v, B, S, H, KVH, hd, msl, mask, pos, softmax, window, prefix)
     want = attention_closed_form(q, k, v, B, S, H, KVH, hd, msl, mask, pos, softmax, window, prefix)
     assert np.allclose(got, want, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("mask,pos", [(0, 0), (5, 0), (9, 1), (-1, 4), (5, -2)])
+def test_attention_out_of_range_kinds(oracle, mask, pos):
+    """The reference casts mask and position kinds through unchecked
+    (c_abi.cpp:805-806); its kernel treats masks other than 2-4 as causal and
+    applies RoPE / ALiBi only for kinds 0, 3 / 2, 3 (kernels.cu:470-485,
+    550-551)."""
+    B, S, msl, H, KVH, hd = 2, 4, 4, 2, 2, 4
+    rng = np.random.default_rng(77 + mask)
+    T = B * S
+    q = rng.standard_normal((T, H * hd)).astype(np.float32)
+    k = rng.standard_normal((T, KVH * hd)).astype(np.float32)
+    v = rng.standard_normal((T, KVH * hd)).astype(np.float32)
+    got = oracle.mha_attention(q, k, v, B, S, H, KVH, hd, msl, mask, pos)
+    want_pos = pos if pos in (0, 1, 2, 3) else 1
+    want = attention_closed_form(q, k, v, B, S, H, KVH, hd, msl, 1, want_pos)
+    assert np.allclose(got, want, rtol=1e-5, atol=1e-6)
+
+
+def test_attention_threads_bit_identical(oracle):
+    """Heads spread over threads compute the same bits as one thread."""
+    B, S, msl, H, KVH, hd = 3, 6, 8, 8, 2, 8
+    rng = np.random.default_rng(3)
+    T = B * S
+    q = rng.standard_normal((T, H * hd)).astype(np.float32)
+    k = rng.standard_normal((T, KVH * hd)).astype(np.float32)
+    v = rng.standard_normal((T, KVH * hd)).astype(np.float32)
+    for mask, pos in ((1, 0), (2, 3), (4, 2)):
+        one = oracle.mha_attention(q, k, v, B, S, H, KVH, hd, msl, mask, pos, prefix_len=3)
+        for th in (2, 3, 8):
+            many = oracle.mha_attention(q, k, v, B, S, H, KVH, hd, msl, mask, pos, prefix_len=3,
+                                        threads=th)
+            assert np.array_equal(one, many)

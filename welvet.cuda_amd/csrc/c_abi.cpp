@@ -16,6 +16,7 @@
 #include "layers.h"
 #include "model.h"
 #include "runtime.h"
+#include "sessions.h"
 
 using wv::Status;
 
@@ -55,14 +56,6 @@ hipStream_t pick(void* stream, hipStream_t own) {
 
 }  // namespace
 
-struct welvet_dense_session {
-  wv::Stream stream;
-  wv::DenseLayer layer;
-  wv::Workspace ws;
-  int batch = 0;
-  wv::DevBuf x, pre, post;
-};
-
 struct welvet_swiglu_session {
   wv::Stream stream;
   wv::SwiGLULayer layer;
@@ -97,6 +90,19 @@ int32_t welvet_cuda_available(void) { return wv::device_available() ? 1 : 0; }
 // returning code 3.
 int32_t welvet_gaps_count(void) { return 41; }
 int32_t welvet_gaps_done(void) { return 18; }
+
+// Measurement extension: one streaming read of a device buffer.
+welvet_status welvet_read_probe(const void* buf, size_t bytes, uint32_t* out_words,
+                                size_t out_cap, void* stream) {
+  if (!buf || !out_words) return invalid("read probe: null buffer");
+  if (out_cap < wv::read_probe_words(bytes)) return invalid("read probe: output too small");
+  return guarded([&]() -> Status {
+    return wv::launch_read_probe(static_cast<const uint8_t*>(buf), bytes, out_words,
+                                 static_cast<hipStream_t>(stream));
+  });
+}
+
+size_t welvet_read_probe_words(size_t bytes) { return wv::read_probe_words(bytes); }
 
 // ---------------------------------------------------------------- Dense ----
 static welvet_status dense_mount(int32_t batch, int32_t in, int32_t out, int32_t act,
@@ -149,11 +155,11 @@ welvet_status welvet_dense_execute(welvet_dense_session* s, const float* x, floa
     const size_t xb = (size_t)s->batch * s->layer.in * sizeof(float);
     const size_t yb = (size_t)s->batch * s->layer.out * sizeof(float);
     hipStream_t st = s->stream.s;
-    WV_HIP(hipMemcpyAsync(s->x.p, x, xb, hipMemcpyHostToDevice, st));
+    WV_TRY(wv::copy_h2d(s->x.p, x, xb, st));
     WV_TRY(wv::dense_forward(s->layer, s->batch, s->x.as<float>(), s->pre.as<float>(),
                              s->post.as<float>(), &s->ws, st));
-    WV_HIP(hipMemcpyAsync(pre, s->pre.p, yb, hipMemcpyDeviceToHost, st));
-    WV_HIP(hipMemcpyAsync(post, s->post.p, yb, hipMemcpyDeviceToHost, st));
+    WV_TRY(wv::copy_d2h(pre, s->pre.p, yb, st));
+    WV_TRY(wv::copy_d2h(post, s->post.p, yb, st));
     WV_HIP(hipStreamSynchronize(st));
     return Status::ok();
   });
@@ -368,8 +374,8 @@ welvet_status welvet_dense_normalbp_f32(int32_t batch, int32_t in, int32_t out, 
     WV_TRY(ddw.alloc(nw * sizeof(float)));
     WV_TRY(dwa.alloc(nw * sizeof(float)));
     WV_TRY(dloss.alloc((size_t)parts * sizeof(double)));
-    WV_HIP(hipMemcpyAsync(dx_in.p, x, nx * sizeof(float), hipMemcpyHostToDevice, st));
-    WV_HIP(hipMemcpyAsync(dg.p, grad_or_target, ny * sizeof(float), hipMemcpyHostToDevice, st));
+    WV_TRY(wv::copy_h2d(dx_in.p, x, nx * sizeof(float), st));
+    WV_TRY(wv::copy_h2d(dg.p, grad_or_target, ny * sizeof(float), st));
     WV_TRY(wv::ensure_split(&ws, wv::dense_workspace_bytes(L, batch)));
     WV_TRY(wv::dense_forward(L, batch, dx_in.as<float>(), dpre_out.as<float>(), dpost.as<float>(),
                              &ws, st));
@@ -379,14 +385,13 @@ welvet_status welvet_dense_normalbp_f32(int32_t batch, int32_t in, int32_t out, 
     if (lr != 0.0) WV_TRY(wv::dense_apply_sgd(&L, ddw.as<float>(), lr, st));
     WV_TRY(wv::launch_dequant(L.dev, dwa.as<float>(), st));
     std::vector<double> lp(use_target ? (size_t)parts : 0);
-    WV_HIP(hipMemcpyAsync(pre, dpre_out.p, ny * sizeof(float), hipMemcpyDeviceToHost, st));
-    WV_HIP(hipMemcpyAsync(post, dpost.p, ny * sizeof(float), hipMemcpyDeviceToHost, st));
-    WV_HIP(hipMemcpyAsync(dX, ddx.p, nx * sizeof(float), hipMemcpyDeviceToHost, st));
-    WV_HIP(hipMemcpyAsync(dW, ddw.p, nw * sizeof(float), hipMemcpyDeviceToHost, st));
-    WV_HIP(hipMemcpyAsync(W_after, dwa.p, nw * sizeof(float), hipMemcpyDeviceToHost, st));
+    WV_TRY(wv::copy_d2h(pre, dpre_out.p, ny * sizeof(float), st));
+    WV_TRY(wv::copy_d2h(post, dpost.p, ny * sizeof(float), st));
+    WV_TRY(wv::copy_d2h(dX, ddx.p, nx * sizeof(float), st));
+    WV_TRY(wv::copy_d2h(dW, ddw.p, nw * sizeof(float), st));
+    WV_TRY(wv::copy_d2h(W_after, dwa.p, nw * sizeof(float), st));
     if (use_target)
-      WV_HIP(hipMemcpyAsync(lp.data(), dloss.p, lp.size() * sizeof(double), hipMemcpyDeviceToHost,
-                            st));
+      WV_TRY(wv::copy_d2h(lp.data(), dloss.p, lp.size() * sizeof(double), st));
     WV_HIP(hipStreamSynchronize(st));
     double sum = 0.0;
     for (double v : lp) sum += v;
@@ -429,8 +434,8 @@ welvet_status welvet_swiglu_normalbp_f32(int32_t batch, int32_t seq, int32_t inp
     WV_TRY(ddw.alloc(nw * sizeof(float)));
     WV_TRY(dwa.alloc(nw * sizeof(float)));
     WV_TRY(dloss.alloc((size_t)parts * sizeof(double)));
-    WV_HIP(hipMemcpyAsync(dx_in.p, x, nx * sizeof(float), hipMemcpyHostToDevice, st));
-    WV_HIP(hipMemcpyAsync(dg.p, grad_or_target, nx * sizeof(float), hipMemcpyHostToDevice, st));
+    WV_TRY(wv::copy_h2d(dx_in.p, x, nx * sizeof(float), st));
+    WV_TRY(wv::copy_h2d(dg.p, grad_or_target, nx * sizeof(float), st));
     WV_TRY(wv::ensure_split(&ws, wv::swiglu_workspace_bytes(L, rows)));
     WV_TRY(wv::swiglu_forward(L, rows, dx_in.as<float>(), dh.as<float>(), dy.as<float>(), &ws, st));
     WV_TRY(wv::swiglu_backward(L, rows, dx_in.as<float>(), dh.as<float>(), dy.as<float>(),
@@ -441,14 +446,13 @@ welvet_status welvet_swiglu_normalbp_f32(int32_t batch, int32_t seq, int32_t inp
     WV_TRY(wv::launch_dequant(L.up.dev, dwa.as<float>() + wf, st));
     WV_TRY(wv::launch_dequant(L.down.dev, dwa.as<float>() + 2 * wf, st));
     std::vector<double> lp(use_target ? (size_t)parts : 0);
-    WV_HIP(hipMemcpyAsync(pre, dh.p, nh * sizeof(float), hipMemcpyDeviceToHost, st));
-    WV_HIP(hipMemcpyAsync(post, dy.p, nx * sizeof(float), hipMemcpyDeviceToHost, st));
-    WV_HIP(hipMemcpyAsync(dX, ddx.p, nx * sizeof(float), hipMemcpyDeviceToHost, st));
-    WV_HIP(hipMemcpyAsync(dW, ddw.p, nw * sizeof(float), hipMemcpyDeviceToHost, st));
-    WV_HIP(hipMemcpyAsync(W_after, dwa.p, nw * sizeof(float), hipMemcpyDeviceToHost, st));
+    WV_TRY(wv::copy_d2h(pre, dh.p, nh * sizeof(float), st));
+    WV_TRY(wv::copy_d2h(post, dy.p, nx * sizeof(float), st));
+    WV_TRY(wv::copy_d2h(dX, ddx.p, nx * sizeof(float), st));
+    WV_TRY(wv::copy_d2h(dW, ddw.p, nw * sizeof(float), st));
+    WV_TRY(wv::copy_d2h(W_after, dwa.p, nw * sizeof(float), st));
     if (use_target)
-      WV_HIP(hipMemcpyAsync(lp.data(), dloss.p, lp.size() * sizeof(double), hipMemcpyDeviceToHost,
-                            st));
+      WV_TRY(wv::copy_d2h(lp.data(), dloss.p, lp.size() * sizeof(double), st));
     WV_HIP(hipStreamSynchronize(st));
     double sum = 0.0;
     for (double v : lp) sum += v;
@@ -495,11 +499,11 @@ welvet_status welvet_swiglu_execute(welvet_swiglu_session* s, const float* x, fl
     const size_t xb = (size_t)s->rows * s->layer.in * sizeof(float);
     const size_t hb = (size_t)s->rows * s->layer.inter * sizeof(float);
     hipStream_t st = s->stream.s;
-    WV_HIP(hipMemcpyAsync(s->x.p, x, xb, hipMemcpyHostToDevice, st));
+    WV_TRY(wv::copy_h2d(s->x.p, x, xb, st));
     WV_TRY(wv::swiglu_forward(s->layer, s->rows, s->x.as<float>(), s->pre.as<float>(),
                               s->post.as<float>(), &s->ws, st));
-    WV_HIP(hipMemcpyAsync(pre, s->pre.p, hb, hipMemcpyDeviceToHost, st));
-    WV_HIP(hipMemcpyAsync(post, s->post.p, xb, hipMemcpyDeviceToHost, st));
+    WV_TRY(wv::copy_d2h(pre, s->pre.p, hb, st));
+    WV_TRY(wv::copy_d2h(post, s->post.p, xb, st));
     WV_HIP(hipStreamSynchronize(st));
     return Status::ok();
   });
@@ -541,8 +545,6 @@ welvet_status welvet_mha_mount(int32_t batch, int32_t seq, int32_t d_model, int3
   *out = nullptr;
   if (batch <= 0 || seq <= 0 || d_model <= 0 || num_heads <= 0 || !Q || !K || !V || !O)
     return invalid("mha: invalid argument");
-  if (mask < 0 || mask > 5 || pos < 0 || pos > 3) return invalid("mha: bad mask/pos kind");
-  if (mask == 5) return to_c(Status::err(wv::kGap, "gap? mha custom mask"));
   return guarded([&]() -> Status {
     WV_TRY(wv::init_device());
     wv::MHAConfig cfg;
@@ -581,11 +583,11 @@ welvet_status welvet_mha_execute(welvet_mha_session* s, const float* x, float* p
     const size_t xb = T * s->layer.cfg.d_model * sizeof(float);
     const size_t ab = T * s->layer.cfg.q_dim() * sizeof(float);
     hipStream_t st = s->stream.s;
-    WV_HIP(hipMemcpyAsync(s->x.p, x, xb, hipMemcpyHostToDevice, st));
+    WV_TRY(wv::copy_h2d(s->x.p, x, xb, st));
     WV_TRY(wv::mha_forward(s->layer, s->batch, s->seq, s->x.as<float>(), s->pre.as<float>(),
                            s->post.as<float>(), &s->ws, st));
-    WV_HIP(hipMemcpyAsync(pre, s->pre.p, ab, hipMemcpyDeviceToHost, st));
-    WV_HIP(hipMemcpyAsync(post, s->post.p, xb, hipMemcpyDeviceToHost, st));
+    WV_TRY(wv::copy_d2h(pre, s->pre.p, ab, st));
+    WV_TRY(wv::copy_d2h(post, s->post.p, xb, st));
     WV_HIP(hipStreamSynchronize(st));
     return Status::ok();
   });
@@ -686,7 +688,7 @@ welvet_status welvet_model_forward(welvet_model_session* s, const uint8_t* input
     // the input buffer and the pass's buffers are kept by the model
     wv::DevBuf& dx = s->model.scratch.in;
     if (dx.bytes < n * 4) WV_TRY(dx.alloc(n * 4));
-    WV_HIP(hipMemcpyAsync(dx.p, input + off, n * 4, hipMemcpyHostToDevice, st));
+    WV_TRY(wv::copy_h2d(dx.p, input + off, n * 4, st));
     std::vector<int> oshape;
     const float* dy = nullptr;
     WV_TRY(wv::model_forward_view(s->model, shape, dx.as<float>(), &oshape, &dy, st));
@@ -707,7 +709,7 @@ welvet_status welvet_model_forward(welvet_model_session* s, const uint8_t* input
     put(&cnt, 4);
     const size_t hdr = blob.size();
     blob.resize(hdr + on * 4);
-    WV_HIP(hipMemcpyAsync(blob.data() + hdr, dy, on * 4, hipMemcpyDeviceToHost, st));
+    WV_TRY(wv::copy_d2h(blob.data() + hdr, dy, on * 4, st));
     WV_HIP(hipStreamSynchronize(st));
     out->data = static_cast<uint8_t*>(std::malloc(blob.size()));
     if (!out->data) return Status::err(wv::kInternal, "out of host memory");
@@ -857,8 +859,8 @@ welvet_status welvet_model_backward(welvet_model_session* s, const uint8_t* data
     wv::DevBuf dx, dg;
     WV_TRY(dx.alloc(nx * 4));
     WV_TRY(dg.alloc(ng * 4));
-    WV_HIP(hipMemcpyAsync(dx.p, hx, nx * 4, hipMemcpyHostToDevice, st));
-    WV_HIP(hipMemcpyAsync(dg.p, hg, ng * 4, hipMemcpyHostToDevice, st));
+    WV_TRY(wv::copy_h2d(dx.p, hx, nx * 4, st));
+    WV_TRY(wv::copy_h2d(dg.p, hg, ng * 4, st));
     const float *gx = nullptr, *dw = nullptr;
     size_t nw = 0;
     WV_TRY(wv::model_backward(s->model, xs, dx.as<float>(), gs, dg.as<float>(), &gx, &dw, &nw, st));
@@ -866,8 +868,8 @@ welvet_status welvet_model_backward(welvet_model_session* s, const uint8_t* data
     size_t at_x = 0, at_w = 0;
     put_tensor(&blob, xs, nx, &at_x);
     put_tensor(&blob, {1, (int)nw}, nw, &at_w);
-    WV_HIP(hipMemcpyAsync(blob.data() + at_x, gx, nx * 4, hipMemcpyDeviceToHost, st));
-    if (nw) WV_HIP(hipMemcpyAsync(blob.data() + at_w, dw, nw * 4, hipMemcpyDeviceToHost, st));
+    WV_TRY(wv::copy_d2h(blob.data() + at_x, gx, nx * 4, st));
+    if (nw) WV_TRY(wv::copy_d2h(blob.data() + at_w, dw, nw * 4, st));
     WV_HIP(hipStreamSynchronize(st));
     out->data = static_cast<uint8_t*>(std::malloc(blob.size()));
     if (!out->data) return Status::err(wv::kInternal, "out of host memory");
@@ -902,7 +904,7 @@ welvet_status welvet_model_forward_pair(welvet_model_session* s, const uint8_t* 
     hipStream_t st = s->stream.s;
     wv::DevBuf& dx = s->model.scratch.in;
     if (dx.bytes < nx * 4) WV_TRY(dx.alloc(nx * 4));
-    WV_HIP(hipMemcpyAsync(dx.p, hx, nx * 4, hipMemcpyHostToDevice, st));
+    WV_TRY(wv::copy_h2d(dx.p, hx, nx * 4, st));
     std::vector<int> shape;
     const float *pre = nullptr, *post = nullptr;
     WV_TRY(wv::model_forward_pair(s->model, xs, dx.as<float>(), &shape, &pre, &post, st));
@@ -912,8 +914,8 @@ welvet_status welvet_model_forward_pair(welvet_model_session* s, const uint8_t* 
     size_t at_pre = 0, at_post = 0;
     put_tensor(&blob, shape, n, &at_pre);
     put_tensor(&blob, shape, n, &at_post);
-    WV_HIP(hipMemcpyAsync(blob.data() + at_pre, pre, n * 4, hipMemcpyDeviceToHost, st));
-    WV_HIP(hipMemcpyAsync(blob.data() + at_post, post, n * 4, hipMemcpyDeviceToHost, st));
+    WV_TRY(wv::copy_d2h(blob.data() + at_pre, pre, n * 4, st));
+    WV_TRY(wv::copy_d2h(blob.data() + at_post, post, n * 4, st));
     WV_HIP(hipStreamSynchronize(st));
     return blob_out(blob, out);
   });
@@ -975,11 +977,11 @@ welvet_status welvet_model_dense_proxy(welvet_model_session* s, int32_t kind, co
     wv::DevBuf dx, dg, dp;
     WV_TRY(dx.alloc(nx * 4));
     WV_TRY(dg.alloc(ny * 4));
-    WV_HIP(hipMemcpyAsync(dx.p, hx, nx * 4, hipMemcpyHostToDevice, st));
-    WV_HIP(hipMemcpyAsync(dg.p, g.data(), ny * 4, hipMemcpyHostToDevice, st));
+    WV_TRY(wv::copy_h2d(dx.p, hx, nx * 4, st));
+    WV_TRY(wv::copy_h2d(dg.p, g.data(), ny * 4, st));
     if (use_pre) {
       WV_TRY(dp.alloc(ny * 4));
-      WV_HIP(hipMemcpyAsync(dp.p, hp, ny * 4, hipMemcpyHostToDevice, st));
+      WV_TRY(wv::copy_h2d(dp.p, hp, ny * 4, st));
     }
     const float* res = nullptr;
     WV_TRY(wv::model_dense_proxy(m, kind, xs, dx.as<float>(), dg.as<float>(),
@@ -990,7 +992,7 @@ welvet_status welvet_model_dense_proxy(welvet_model_session* s, int32_t kind, co
     std::vector<uint8_t> blob;
     size_t at = 0;
     put_tensor(&blob, shape, n, &at);
-    WV_HIP(hipMemcpyAsync(blob.data() + at, res, n * 4, hipMemcpyDeviceToHost, st));
+    WV_TRY(wv::copy_d2h(blob.data() + at, res, n * 4, st));
     WV_HIP(hipStreamSynchronize(st));
     return blob_out(blob, out);
   });
@@ -1011,7 +1013,7 @@ welvet_status welvet_model_apply_sgd(welvet_model_session* s, double lr, const u
     hipStream_t st = s->stream.s;
     wv::DevBuf d;
     WV_TRY(d.alloc(n * 4));
-    WV_HIP(hipMemcpyAsync(d.p, hw, n * 4, hipMemcpyHostToDevice, st));
+    WV_TRY(wv::copy_h2d(d.p, hw, n * 4, st));
     WV_TRY(wv::model_apply_sgd(s->model, d.as<float>(), n, lr, st));
     WV_HIP(hipStreamSynchronize(st));
     return Status::ok();

@@ -102,6 +102,10 @@ struct DeviceWeights {
   // chunk bytes 64 h + 16 (l / 16) ..) at 16 l, so a wave's operand load is
   // 1 KiB contiguous: uint8[rpad / 16][kpad / 128][halves][64][16]
   DevBuf codes_frag;
+  // rows holding non-finite codes (E5M2 only), device and host copies
+  DevBuf nf_rows;
+  std::vector<int> nf_host;
+  int nf_count() const { return (int)nf_host.size(); }
   const uint8_t* d_codes() const { return codes.as<const uint8_t>(); }
   const float* d_scale() const { return row_scale.as<const float>(); }
   const uint8_t* d_blk() const { return scheme == 3 ? blk.as<const uint8_t>() : nullptr; }

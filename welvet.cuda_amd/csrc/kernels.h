@@ -22,6 +22,39 @@ Status relayout_to_device(const uint8_t* d_raw, int dtype, int scheme, int rows,
 Status codec_sweep(int dtype, uint32_t first_chunk, uint32_t n_chunks, int64_t* host_out,
                    hipStream_t st);
 
+// ---- weight rows with non-finite codes (special.hip) ----
+// Fills dw->nf_rows / nf_host with the rows holding E5M2 inf/NaN codes.
+Status find_nonfinite_rows(DeviceWeights* dw, hipStream_t st);
+// Device copy of a row list (out is reset; left empty for an empty list).
+Status upload_rows(const std::vector<int>& rows, DevBuf* out, hipStream_t st);
+// Recomputes the listed output rows of a product (decoded weights, f64 sum)
+// and applies the epilogue: bias / activation (mats 1) or the SwiGLU product
+// of matrices 0 and 1 into pre (mats 2).
+struct NfArgs {
+  const int* rows = nullptr;
+  int n = 0;
+  int dtype = 0, mats = 1;
+  const uint8_t* codes[2] = {nullptr, nullptr};
+  const float* scale[2] = {nullptr, nullptr};
+  const uint8_t* blk[2] = {nullptr, nullptr};
+  int pitch = 0, nblk = 0, cols = 0;
+  const float* x = nullptr;
+  int x_stride = 0, batch = 0;
+  float* pre = nullptr;
+  float* post = nullptr;
+  int out_stride = 0;
+  int act = kLinear;
+  int need_epi = 0;
+  const double* bias = nullptr;
+  int bias_len = 0;
+};
+Status launch_nf_fix(const NfArgs& a, hipStream_t st);
+
+// ---- streaming read of a buffer (probe.hip): the read floor ----
+// Words of `out` a read of `bytes` writes (one per workgroup).
+size_t read_probe_words(size_t bytes);
+Status launch_read_probe(const uint8_t* buf, size_t bytes, uint32_t* out, hipStream_t st);
+
 // ---- small-batch GEMV (gemv.hip) ----
 struct GemvArgs {
   const uint8_t* codes[2] = {nullptr, nullptr};

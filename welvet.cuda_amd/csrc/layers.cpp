@@ -8,6 +8,7 @@
 // there; activations stay on the device between the layer's kernels.
 #include "layers.h"
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 
@@ -30,21 +31,20 @@ static Status download_store(DenseLayer* L, const uint8_t* d_raw, hipStream_t st
   const DeviceWeights& d = L->dev;
   const int64_t n = (int64_t)d.rows * d.cols;
   s.native.resize(d.dtype == kFP4 ? (size_t)((n + 1) / 2) : (size_t)n);
-  if (d_raw) {
-    WV_HIP(hipMemcpyAsync(s.native.data(), d_raw, s.native.size(), hipMemcpyDeviceToHost, st));
-  }
+  if (d_raw) WV_TRY(copy_d2h(s.native.data(), d_raw, s.native.size(), st));
   s.row_scale.resize((size_t)d.rows);
-  WV_HIP(hipMemcpyAsync(s.row_scale.data(), d.d_scale(), (size_t)d.rows * sizeof(float),
-                        hipMemcpyDeviceToHost, st));
+  WV_TRY(copy_d2h(s.row_scale.data(), d.d_scale(), (size_t)d.rows * sizeof(float), st));
   if (d.scheme == kSchemeBlock32) {
+    // the device rows are nblk (padded) bytes long; the store keeps ceil(cols / 32)
     const int nb = (d.cols + 31) / 32;
+    std::vector<uint8_t> padded((size_t)d.rows * d.nblk);
+    WV_TRY(copy_d2h(padded.data(), d.d_blk(), padded.size(), st));
     s.blk_exp.resize((size_t)d.rows * nb);
-    WV_HIP(hipMemcpy2DAsync(s.blk_exp.data(), nb, d.d_blk(), d.nblk, nb, d.rows,
-                            hipMemcpyDeviceToHost, st));
+    for (int r = 0; r < d.rows; ++r)
+      std::memcpy(s.blk_exp.data() + (size_t)r * nb, padded.data() + (size_t)r * d.nblk, nb);
   } else {
     s.blk_exp.clear();
   }
-  WV_HIP(hipStreamSynchronize(st));
   s.scale = (d.scheme == kSchemeTensor && !s.row_scale.empty()) ? s.row_scale[0] : 1.0f;
   return Status::ok();
 }
@@ -55,8 +55,7 @@ static Status upload_bias(DenseLayer* L, const double* bias, size_t bias_len, hi
   L->bias_dev.reset();
   if (L->bias_len > 0) {
     WV_TRY(L->bias_dev.alloc(bias_len * sizeof(double)));
-    WV_HIP(hipMemcpyAsync(L->bias_dev.p, bias, bias_len * sizeof(double), hipMemcpyHostToDevice,
-                          st));
+    WV_TRY(copy_h2d(L->bias_dev.p, bias, bias_len * sizeof(double), st));
     WV_HIP(hipStreamSynchronize(st));
   }
   return Status::ok();
@@ -74,7 +73,7 @@ Status dense_build(int in, int out, int act, int dtype, int scheme, const float*
   DevBuf dW, raw;
   WV_TRY(dW.alloc((size_t)n * sizeof(float)));
   if (W_host) {
-    WV_HIP(hipMemcpyAsync(dW.p, W_host, (size_t)n * sizeof(float), hipMemcpyHostToDevice, st));
+    WV_TRY(copy_h2d(dW.p, W_host, (size_t)n * sizeof(float), st));
   } else {
     WV_HIP(hipMemsetAsync(dW.p, 0, (size_t)n * sizeof(float), st));
   }
@@ -104,19 +103,17 @@ Status dense_build_from_store(int in, int out, int act, const WeightStore& store
   L->store = store;
   DevBuf raw, sc, blk;
   WV_TRY(raw.alloc(nbytes));
-  WV_HIP(hipMemcpyAsync(raw.p, store.native.data(), nbytes, hipMemcpyHostToDevice, st));
+  WV_TRY(copy_h2d(raw.p, store.native.data(), nbytes, st));
   const float* d_sc = nullptr;
   if (!store.row_scale.empty()) {
     WV_TRY(sc.alloc(store.row_scale.size() * sizeof(float)));
-    WV_HIP(hipMemcpyAsync(sc.p, store.row_scale.data(), store.row_scale.size() * sizeof(float),
-                          hipMemcpyHostToDevice, st));
+    WV_TRY(copy_h2d(sc.p, store.row_scale.data(), store.row_scale.size() * sizeof(float), st));
     d_sc = sc.as<float>();
   }
   const uint8_t* d_blk = nullptr;
   if (store.scheme == kSchemeBlock32) {
     WV_TRY(blk.alloc(store.blk_exp.size()));
-    WV_HIP(hipMemcpyAsync(blk.p, store.blk_exp.data(), store.blk_exp.size(), hipMemcpyHostToDevice,
-                          st));
+    WV_TRY(copy_h2d(blk.p, store.blk_exp.data(), store.blk_exp.size(), st));
     d_blk = blk.as<uint8_t>();
   }
   WV_TRY(relayout_to_device(raw.as<uint8_t>(), store.dtype, store.scheme, out, in, d_sc, d_blk,
@@ -235,6 +232,34 @@ static void set_input(MxgArgs& p, const float* x, int stride, int cols) {
   p.x_vec = stride % 4 == 0 && cols % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
 }
 
+// Rows with non-finite codes, recomputed after a matrix-core product of
+// `batch` rows of x (row stride x_stride).
+static Status fix_nonfinite(const DenseLayer& L, int batch, const float* x, int x_stride,
+                            float* pre, float* post, hipStream_t st) {
+  if (L.dev.nf_count() == 0) return Status::ok();
+  NfArgs a;
+  a.rows = L.dev.nf_rows.as<const int>();
+  a.n = L.dev.nf_count();
+  a.dtype = L.dev.dtype;
+  a.codes[0] = L.dev.d_codes();
+  a.scale[0] = L.dev.d_scale();
+  a.blk[0] = L.dev.d_blk();
+  a.pitch = L.dev.pitch;
+  a.nblk = L.dev.nblk;
+  a.cols = L.in;
+  a.x = x;
+  a.x_stride = x_stride;
+  a.batch = batch;
+  a.pre = pre;
+  a.post = post;
+  a.out_stride = L.out;
+  a.act = L.act;
+  a.need_epi = L.need_epi() ? 1 : 0;
+  a.bias = L.bias_dev.as<const double>();
+  a.bias_len = L.bias_len;
+  return launch_nf_fix(a, st);
+}
+
 Status dense_forward_split(const DenseLayer& L, int batch, const float* x, bool split_ready,
                            Workspace* ws, float* pre, float* post, hipStream_t st,
                            const double* rope_tab, int rope_hd) {
@@ -248,7 +273,8 @@ Status dense_forward_split(const DenseLayer& L, int batch, const float* x, bool 
   } else {
     set_input(p, x, L.in, L.in);
   }
-  return launch_mxg(p, L.dev.dtype, L.dev.scheme == kSchemeBlock32, st);
+  WV_TRY(launch_mxg(p, L.dev.dtype, L.dev.scheme == kSchemeBlock32, st));
+  return fix_nonfinite(L, batch, x, L.in, pre, post, st);
 }
 
 Status dense_forward(const DenseLayer& L, int batch, const float* x, float* pre, float* post,
@@ -263,7 +289,8 @@ Status dense_forward(const DenseLayer& L, int batch, const float* x, float* pre,
     MxvArgs m = mxv_args(L, x, L.in, batch);
     m.pre = pre;
     m.post = post;
-    return launch_mxv(m, L.dev.dtype, L.dev.scheme == kSchemeBlock32, st);
+    WV_TRY(launch_mxv(m, L.dev.dtype, L.dev.scheme == kSchemeBlock32, st));
+    return fix_nonfinite(L, batch, x, L.in, pre, post, st);
   }
   GemvArgs a = gemv_args(L, x, L.in);
   a.pre = pre;
@@ -321,6 +348,7 @@ Status dense_group_build(const DenseLayer* const* layers, int n, int batch,
   if (n <= 0 || !layers || !x || !pre || !g) return Status::err(kInvalid, "dense group: bad args");
   if (!dense_group_fused(batch)) return Status::err(kInvalid, "dense group: batch too small");
   const DenseLayer& L0 = *layers[0];
+  g->layers.clear();
   std::vector<SplitJob> jobs(n);
   std::vector<MxgArgs> tab(n);
   const size_t sb = split_bytes(batch, L0.dev.kpad);
@@ -338,6 +366,7 @@ Status dense_group_build(const DenseLayer* const* layers, int n, int batch,
     jobs[i].x = x[i];
     jobs[i].buf = buf;
     vec = vec && (reinterpret_cast<uintptr_t>(x[i]) & 15u) == 0;
+    g->layers.push_back(L);
     tab[i] = mxg_args(*L, batch, buf);
     tab[i].part = nullptr;  // large tiles: no K split
     tab[i].pre = pre[i];
@@ -345,8 +374,9 @@ Status dense_group_build(const DenseLayer* const* layers, int n, int batch,
   }
   WV_TRY(g->jobs.alloc(sizeof(SplitJob) * n));
   WV_TRY(g->tab.alloc(sizeof(MxgArgs) * n));
-  WV_HIP(hipMemcpy(g->jobs.p, jobs.data(), sizeof(SplitJob) * n, hipMemcpyHostToDevice));
-  WV_HIP(hipMemcpy(g->tab.p, tab.data(), sizeof(MxgArgs) * n, hipMemcpyHostToDevice));
+  WV_TRY(copy_h2d(g->jobs.p, jobs.data(), sizeof(SplitJob) * n, nullptr));
+  WV_TRY(copy_h2d(g->tab.p, tab.data(), sizeof(MxgArgs) * n, nullptr));
+  WV_HIP(hipStreamSynchronize(nullptr));
   g->hjobs = jobs;
   g->htab = tab;
   g->n = n;
@@ -360,10 +390,25 @@ Status dense_group_build(const DenseLayer* const* layers, int n, int batch,
   return Status::ok();
 }
 
+// Members whose weights hold non-finite codes get their rows recomputed.
+static Status group_fix(const DenseGroup& g, hipStream_t st) {
+  for (int i = 0; i < g.n; ++i)
+    WV_TRY(fix_nonfinite(*g.layers[(size_t)i], g.batch, g.hjobs[(size_t)i].x, g.in,
+                         g.htab[(size_t)i].pre, g.htab[(size_t)i].post, st));
+  return Status::ok();
+}
+
+static bool group_has_nonfinite(const DenseGroup& g) {
+  for (const DenseLayer* L : g.layers)
+    if (L->dev.nf_count() > 0) return true;
+  return false;
+}
+
 Status dense_group_forward(const DenseGroup& g, hipStream_t st) {
   WV_TRY(launch_split_group(g.jobs.as<const SplitJob>(), g.n, g.vec, g.in, g.batch, g.in, g.kpad,
                             st));
-  return launch_mxg_group(g.tab.as<const MxgArgs>(), g.shape, g.n, g.dtype, g.blk, st);
+  WV_TRY(launch_mxg_group(g.tab.as<const MxgArgs>(), g.shape, g.n, g.dtype, g.blk, st));
+  return group_fix(g, st);
 }
 
 Status dense_chain_build(const DenseGroup* const* groups, int count, DenseChain* c) {
@@ -388,11 +433,16 @@ Status dense_chain_build(const DenseGroup* const* groups, int count, DenseChain*
       if (!linked)
         return Status::err(kInvalid, "dense chain: member input is not the previous member's output");
     }
-    if (P.shape.N % 256 != 0 || C.kpad != P.shape.N || P.shape.mats != 1) continue;
+    // the epilogue split would see the matrix-core values of rows that are
+    // recomputed afterwards: such a link runs the consumer's own split
+    if (P.shape.N % 256 != 0 || C.kpad != P.shape.N || P.shape.mats != 1 ||
+        group_has_nonfinite(P))
+      continue;
     std::vector<MxgArgs> tab = P.htab;
     for (int i = 0; i < P.n; ++i) tab[i].next = C.hjobs[i].buf;
     WV_TRY(c->tabs[k].alloc(sizeof(MxgArgs) * P.n));
-    WV_HIP(hipMemcpy(c->tabs[k].p, tab.data(), sizeof(MxgArgs) * P.n, hipMemcpyHostToDevice));
+    WV_TRY(copy_h2d(c->tabs[k].p, tab.data(), sizeof(MxgArgs) * P.n, nullptr));
+    WV_HIP(hipStreamSynchronize(nullptr));
     c->fused[k] = 1;
   }
   return Status::ok();
@@ -407,11 +457,21 @@ Status dense_chain_forward(const DenseChain& c, hipStream_t st) {
                                 g.kpad, st));
     const MxgArgs* tab = c.fused[k] ? c.tabs[k].as<const MxgArgs>() : g.tab.as<const MxgArgs>();
     WV_TRY(launch_mxg_group(tab, g.shape, g.n, g.dtype, g.blk, st));
+    WV_TRY(group_fix(g, st));
   }
   return Status::ok();
 }
 
 // ---------------------------------------------------------------------------
+Status swiglu_finish(SwiGLULayer* L, hipStream_t st) {
+  std::vector<int> u = L->gate.dev.nf_host;
+  u.insert(u.end(), L->up.dev.nf_host.begin(), L->up.dev.nf_host.end());
+  std::sort(u.begin(), u.end());
+  u.erase(std::unique(u.begin(), u.end()), u.end());
+  L->nf_gu_host = u;
+  return upload_rows(u, &L->nf_gu, st);
+}
+
 Status swiglu_build(int in, int inter, int dtype, int scheme, const float* G, const float* U,
                     const float* D, SwiGLULayer* L, hipStream_t st) {
   if (in <= 0 || inter <= 0)
@@ -420,7 +480,30 @@ Status swiglu_build(int in, int inter, int dtype, int scheme, const float* G, co
   WV_TRY(dense_build(in, inter, kLinear, dtype, scheme, G, nullptr, 0, &L->gate, st));
   WV_TRY(dense_build(in, inter, kLinear, dtype, scheme, U, nullptr, 0, &L->up, st));
   WV_TRY(dense_build(inter, in, kLinear, dtype, scheme, D, nullptr, 0, &L->down, st));
-  return Status::ok();
+  return swiglu_finish(L, st);
+}
+
+// Gate / up rows with non-finite codes, recomputed with the product rule.
+static Status swiglu_fix(const SwiGLULayer& L, int rows, const float* x, float* h,
+                         hipStream_t st) {
+  if (L.nf_gu_host.empty()) return Status::ok();
+  NfArgs a;
+  a.rows = L.nf_gu.as<const int>();
+  a.n = (int)L.nf_gu_host.size();
+  a.dtype = L.gate.dev.dtype;
+  a.mats = 2;
+  a.codes[0] = L.gate.dev.d_codes(), a.codes[1] = L.up.dev.d_codes();
+  a.scale[0] = L.gate.dev.d_scale(), a.scale[1] = L.up.dev.d_scale();
+  a.blk[0] = L.gate.dev.d_blk(), a.blk[1] = L.up.dev.d_blk();
+  a.pitch = L.gate.dev.pitch;
+  a.nblk = L.gate.dev.nblk;
+  a.cols = L.in;
+  a.x = x;
+  a.x_stride = L.in;
+  a.batch = rows;
+  a.pre = h;
+  a.out_stride = L.inter;
+  return launch_nf_fix(a, st);
 }
 
 size_t swiglu_workspace_bytes(const SwiGLULayer& L, int rows) {
@@ -441,6 +524,7 @@ Status swiglu_forward(const SwiGLULayer& L, int rows, const float* x, float* h, 
     m.pre = h;
     m.need_epi = 0;
     WV_TRY(launch_mxv(m, L.gate.dev.dtype, L.gate.dev.scheme == kSchemeBlock32, st));
+    WV_TRY(swiglu_fix(L, rows, x, h, st));
     return dense_forward(L.down, rows, h, y, nullptr, ws, st);
   }
   if (uses_split(rows)) {
@@ -458,6 +542,7 @@ Status swiglu_forward(const SwiGLULayer& L, int rows, const float* x, float* h, 
     p.pre = h;
     p.need_epi = 0;
     WV_TRY(launch_mxg(p, L.gate.dev.dtype, L.gate.dev.scheme == kSchemeBlock32, st));
+    WV_TRY(swiglu_fix(L, rows, x, h, st));
     return dense_forward_split(L.down, rows, h, false, ws, y, nullptr, st);
   }
   GemvArgs a = gemv_args(L.gate, x, L.in);
@@ -513,7 +598,8 @@ Status swiglu_apply_sgd(SwiGLULayer* L, const float* dw, double lr, hipStream_t 
   const size_t wf = (size_t)L->gate.out * L->gate.in;
   WV_TRY(dense_apply_sgd(&L->gate, dw, lr, st));
   WV_TRY(dense_apply_sgd(&L->up, dw + wf, lr, st));
-  return dense_apply_sgd(&L->down, dw + 2 * wf, lr, st);
+  WV_TRY(dense_apply_sgd(&L->down, dw + 2 * wf, lr, st));
+  return swiglu_finish(L, st);
 }
 
 // ---------------------------------------------------------------------------
@@ -529,7 +615,13 @@ Status mha_validate(MHAConfig* c) {
   if (c->num_heads % c->num_kv_heads != 0)
     return Status::err(kInvalid, "mha: NumHeads not divisible by NumKVHeads");
   if (c->max_seq_len <= 0) c->max_seq_len = 512;
-  if (c->mask == 0) c->mask = 1;
+  // The reference passes the mask and position kinds through unchecked
+  // (src/interop/c_abi.cpp:805-806, child_wire.hpp:180-181); its attention
+  // treats every mask other than 2, 3 and 4 as causal (kernels.cu:470-485)
+  // and rotates / adds ALiBi only for position kinds 0, 3 / 2, 3
+  // (kernels.cu:550-551). Both are folded to the kind that behaves the same.
+  if (c->mask != 2 && c->mask != 3 && c->mask != 4) c->mask = 1;
+  if (c->pos < 0 || c->pos > 3) c->pos = 1;
   if (c->rope_theta <= 0) c->rope_theta = 10000.0;
   if (c->softmax != 0 && c->softmax != 1) return Status::err(kInvalid, "mha: unknown Softmax");
   return Status::ok();
@@ -604,8 +696,11 @@ Status mha_forward(const MHALayer& L, int batch, int seq, const float* x, float*
   // RoPE in the Q and K GEMM epilogues (large tiles): the attention kernel
   // then reads rotated rows
   const bool rope = mha_rope(c);
+  // (not when Q or K has rows that are recomputed after the product: the
+  // rotation pairs each column with another)
   const bool rope_epi = rope && uses_split(T) && mxg_block_m(T) > 16 && c.head_dim % 8 == 0 &&
-                        128 % c.head_dim == 0 && !L.q.need_epi() && !L.k.need_epi();
+                        128 % c.head_dim == 0 && !L.q.need_epi() && !L.k.need_epi() &&
+                        L.q.dev.nf_count() == 0 && L.k.dev.nf_count() == 0;
   if (rope) WV_TRY(ensure_rope_table(L, T, ws, st));
   if (uses_split(T)) {
     // Q, K and V read the same activations: above 32 rows they are split

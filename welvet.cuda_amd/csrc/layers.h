@@ -113,6 +113,7 @@ struct DenseGroup {
   DevBuf tab;    // MxgArgs[n]
   std::vector<SplitJob> hjobs;  // host copies of jobs and tab
   std::vector<MxgArgs> htab;
+  std::vector<const DenseLayer*> layers;  // the members
 };
 bool dense_group_fused(int batch);
 Status dense_group_build(const DenseLayer* const* layers, int n, int batch,
@@ -136,7 +137,12 @@ Status dense_chain_forward(const DenseChain& c, hipStream_t st);
 struct SwiGLULayer {
   int in = 0, inter = 0;
   DenseLayer gate, up, down;
+  // union of the gate and up rows with non-finite codes
+  DevBuf nf_gu;
+  std::vector<int> nf_gu_host;
 };
+// Completes a SwiGLU layer whose three matrices are built (the row list above).
+Status swiglu_finish(SwiGLULayer* L, hipStream_t st);
 Status swiglu_build(int in, int inter, int dtype, int scheme, const float* G, const float* U,
                     const float* D, SwiGLULayer* L, hipStream_t st);
 // x [rows][in] -> h [rows][inter] (pre), y [rows][in] (post).

@@ -251,6 +251,7 @@ void build(ModelNode& c, int scheme, hipStream_t st) {
       else good(dense_build(s.cols, s.rows, kLinear, s.dtype, scheme, ws[i]->data(), s.bias.data(),
                             s.bias.size(), parts[i], st));
     }
+    good(swiglu_finish(c.swiglu.get(), st));
     break;
   }
   case 7: {

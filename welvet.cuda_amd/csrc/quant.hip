@@ -4,6 +4,7 @@
 #include "codec.h"
 #include "common.h"
 #include "kernels.h"
+#include "runtime.h"
 
 namespace wv {
 namespace {
@@ -341,6 +342,7 @@ Status quantize_to_device(const float* dW, int dtype, int scheme, int rows, int 
                                                        dw->nblk, d_raw);
     WV_HIP(hipGetLastError());
   }
+  WV_TRY(find_nonfinite_rows(dw, st));
   // amax is freed when this function returns; the kernels reading it must be done.
   WV_HIP(hipStreamSynchronize(st));
   return Status::ok();
@@ -380,6 +382,7 @@ Status relayout_to_device(const uint8_t* d_raw, int dtype, int scheme, int rows,
     }
     WV_TRY(build_blk_frag(dw, st));
   }
+  WV_TRY(find_nonfinite_rows(dw, st));
   WV_HIP(hipStreamSynchronize(st));
   return Status::ok();
 }
@@ -398,8 +401,7 @@ Status codec_sweep(int dtype, uint32_t first_chunk, uint32_t n_chunks, int64_t* 
                                             out.as<unsigned long long>() + 2 * (size_t)c);
     WV_HIP(hipGetLastError());
   }
-  WV_HIP(hipMemcpyAsync(host_out, out.p, (size_t)n_chunks * 2 * sizeof(int64_t),
-                        hipMemcpyDeviceToHost, st));
+  WV_TRY(copy_d2h(host_out, out.p, (size_t)n_chunks * 2 * sizeof(int64_t), st));
   WV_HIP(hipStreamSynchronize(st));
   return Status::ok();
 }

@@ -3,6 +3,7 @@
 // reference (init_default_device / available / runtime_identity).
 #include "runtime.h"
 
+#include <cstring>
 #include <mutex>
 #include <sstream>
 
@@ -11,6 +12,43 @@ namespace {
 std::mutex g_mu;
 bool g_ready = false;
 hipDeviceProp_t g_prop;
+
+// Device name for the identity: the runtime's marketing name, else the
+// name hipDeviceGetName reports, else one built from what the properties
+// always carry (architecture, compute units, peak engine clock).
+std::string device_name() {
+  std::string name(g_prop.name, strnlen(g_prop.name, sizeof(g_prop.name)));
+  if (name.empty()) {
+    char buf[256] = {0};
+    if (hipDeviceGetName(buf, sizeof(buf) - 1, 0) == hipSuccess) name = buf;
+    else (void)hipGetLastError();
+  }
+  if (name.empty()) {
+    std::string arch(g_prop.gcnArchName);
+    arch = arch.substr(0, arch.find(':'));
+    std::ostringstream os;
+    os << "AMD " << arch << " " << g_prop.multiProcessorCount << "CU "
+       << g_prop.clockRate / 1000 << "MHz";
+    name = os.str();
+  }
+  return name;
+}
+
+// Pinned staging: two buffers, so the host copy of one chunk overlaps the
+// DMA of the other.
+constexpr size_t kStageBytes = 8u << 20;
+std::mutex g_stage_mu;
+void* g_stage[2] = {nullptr, nullptr};
+hipEvent_t g_stage_ev[2] = {nullptr, nullptr};
+
+Status stage_ready() {
+  for (int i = 0; i < 2; ++i) {
+    if (!g_stage[i]) WV_HIP(hipHostMalloc(&g_stage[i], kStageBytes, hipHostMallocDefault));
+    if (!g_stage_ev[i])
+      WV_HIP(hipEventCreateWithFlags(&g_stage_ev[i], hipEventDisableTiming));
+  }
+  return Status::ok();
+}
 }  // namespace
 
 Status init_device() {
@@ -39,7 +77,7 @@ std::string identity() {
   if (!init_device()) return "hip:unavailable";
   std::lock_guard<std::mutex> lock(g_mu);
   std::ostringstream os;
-  os << "hip:" << g_prop.name << ":idx=0:arch=" << g_prop.gcnArchName
+  os << "hip:" << device_name() << ":idx=0:arch=" << g_prop.gcnArchName
      << ":cu=" << g_prop.multiProcessorCount << ":mem=" << (g_prop.totalGlobalMem >> 20) << "MiB";
   return os.str();
 }
@@ -47,6 +85,56 @@ std::string identity() {
 int cu_count() {
   if (!init_device()) return 0;
   return g_prop.multiProcessorCount;
+}
+
+Status copy_h2d(void* dst, const void* src, size_t n, hipStream_t st) {
+  if (n == 0) return Status::ok();
+  if (!dst || !src) return Status::err(kInvalid, "copy_h2d: null buffer");
+  std::lock_guard<std::mutex> lock(g_stage_mu);
+  WV_TRY(stage_ready());
+  bool used[2] = {false, false};
+  int i = 0;
+  for (size_t off = 0; off < n; off += kStageBytes, i ^= 1) {
+    const size_t len = n - off < kStageBytes ? n - off : kStageBytes;
+    // the DMA that last read this buffer must be done before it is refilled
+    if (used[i]) WV_HIP(hipEventSynchronize(g_stage_ev[i]));
+    std::memcpy(g_stage[i], static_cast<const char*>(src) + off, len);
+    WV_HIP(hipMemcpyAsync(static_cast<char*>(dst) + off, g_stage[i], len, hipMemcpyHostToDevice,
+                          st));
+    WV_HIP(hipEventRecord(g_stage_ev[i], st));
+    used[i] = true;
+  }
+  // the next caller refills the buffers: their DMAs must have read them
+  for (int k = 0; k < 2; ++k)
+    if (used[k]) WV_HIP(hipEventSynchronize(g_stage_ev[k]));
+  return Status::ok();
+}
+
+Status copy_d2h(void* dst, const void* src, size_t n, hipStream_t st) {
+  if (n == 0) return Status::ok();
+  if (!dst || !src) return Status::err(kInvalid, "copy_d2h: null buffer");
+  std::lock_guard<std::mutex> lock(g_stage_mu);
+  WV_TRY(stage_ready());
+  bool pend[2] = {false, false};
+  size_t pend_off[2] = {0, 0}, pend_len[2] = {0, 0};
+  auto drain = [&](int k) -> Status {
+    WV_HIP(hipEventSynchronize(g_stage_ev[k]));
+    std::memcpy(static_cast<char*>(dst) + pend_off[k], g_stage[k], pend_len[k]);
+    pend[k] = false;
+    return Status::ok();
+  };
+  int i = 0;
+  for (size_t off = 0; off < n; off += kStageBytes, i ^= 1) {
+    const size_t len = n - off < kStageBytes ? n - off : kStageBytes;
+    if (pend[i]) WV_TRY(drain(i));
+    WV_HIP(hipMemcpyAsync(g_stage[i], static_cast<const char*>(src) + off, len,
+                          hipMemcpyDeviceToHost, st));
+    WV_HIP(hipEventRecord(g_stage_ev[i], st));
+    pend[i] = true, pend_off[i] = off, pend_len[i] = len;
+  }
+  for (int k = 0; k < 2; ++k)
+    if (pend[i ^ k]) WV_TRY(drain(i ^ k));
+  return Status::ok();
 }
 
 Status Stream::create() {

@@ -135,6 +135,8 @@ def lib():
     _sig(L, "welvet_model_release", None, [_vp])
     _sig(L, "welvet_cuda_blob_free", None, [ctypes.POINTER(Blob)])
     _sig(L, "welvet_codec_sweep", Status, [_i32, _u32, _u32, _i64p])
+    _sig(L, "welvet_read_probe", Status, [_vp, _sz, _vp, _sz, _vp])
+    _sig(L, "welvet_read_probe_words", _sz, [_sz])
     _sig(L, "welvet_seqmix_kind_name", Status, [_i32, ctypes.c_char_p, _i32])
     for n in ("welvet_seqmix_mha_kind", "welvet_seqmix_mamba_kind", "welvet_seqmix_gdn_kind"):
         _sig(L, n, _i32, [])
@@ -216,7 +218,10 @@ class Hip:
         _sig(h, "hipGraphLaunch", ctypes.c_int, [_vp, _vp])
         _sig(h, "hipGraphExecDestroy", ctypes.c_int, [_vp])
         _sig(h, "hipGraphDestroy", ctypes.c_int, [_vp])
+        _sig(h, "hipHostMalloc", ctypes.c_int, [ctypes.POINTER(_vp), _sz, ctypes.c_uint])
+        _sig(h, "hipHostFree", ctypes.c_int, [_vp])
         self.h = h
+        self._stage = None
 
     def _ok(self, rc, what):
         if rc != 0:
@@ -231,21 +236,46 @@ class Hip:
         if p:
             self._ok(self.h.hipFree(_vp(p)), "hipFree")
 
+    STAGE = 8 << 20
+
+    def _staging(self):
+        """Pinned host buffer for host <-> device copies: the runtime is never
+        handed pageable memory to pin in place."""
+        if self._stage is None:
+            b = _vp()
+            self._ok(self.h.hipHostMalloc(ctypes.byref(b), self.STAGE, 0), "hipHostMalloc")
+            self._stage = b.value
+        return self._stage
+
+    def _h2d(self, dev, host_addr, nbytes):
+        st = self._staging()
+        for off in range(0, nbytes, self.STAGE):
+            n = min(self.STAGE, nbytes - off)
+            ctypes.memmove(st, host_addr + off, n)
+            self._ok(self.h.hipMemcpy(_vp(dev + off), _vp(st), n, self.H2D), "H2D")
+
+    def _d2h(self, host_addr, dev, nbytes):
+        st = self._staging()
+        for off in range(0, nbytes, self.STAGE):
+            n = min(self.STAGE, nbytes - off)
+            self._ok(self.h.hipMemcpy(_vp(st), _vp(dev + off), n, self.D2H), "D2H")
+            ctypes.memmove(host_addr + off, st, n)
+
     def upload(self, arr):
         arr = np.ascontiguousarray(arr)
         p = self.malloc(arr.nbytes)
-        self._ok(self.h.hipMemcpy(_vp(p), arr.ctypes.data_as(_vp), arr.nbytes, self.H2D), "H2D")
+        self._h2d(p, arr.ctypes.data, arr.nbytes)
         return p
 
     def copy_in(self, p, arr):
         """Host array into an existing device buffer; returns once it has landed."""
         arr = np.ascontiguousarray(arr)
-        self._ok(self.h.hipMemcpy(_vp(p), arr.ctypes.data_as(_vp), arr.nbytes, self.H2D), "H2D")
+        self._h2d(p, arr.ctypes.data, arr.nbytes)
         self.sync()
 
     def download(self, p, shape, dtype=np.float32):
         out = np.empty(shape, dtype=dtype)
-        self._ok(self.h.hipMemcpy(out.ctypes.data_as(_vp), _vp(p), out.nbytes, self.D2H), "D2H")
+        self._d2h(out.ctypes.data, p, out.nbytes)
         return out
 
     def copy_async(self, dst, src, nbytes, stream):
