@@ -214,6 +214,21 @@ WELVET_API welvet_status welvet_model_forward_device(welvet_model_session* s, co
 WELVET_API welvet_status welvet_codec_sweep(int32_t dtype, uint32_t first_chunk,
                                             uint32_t n_chunks, int64_t* out);
 
+/* No counterpart in the reference: for callers that cannot allocate (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * allocation). welvet_dense_execute_device on `rows` rows (any count, not
+ * only the mounted batch) whose scratch memory (the activation split and
+ * K-split partial sums of the matrix-core paths above 4 rows) is a fixed
+ * 64 MiB device array of the library instead of an allocation: the call
+ * allocates nothing. Code 1 when rows * in needs more than 64 MiB (about
+ * 5.3 M activations on the split path). Calls on one device share the array:
+ * calls that overlap in time on one device race; the previous call's
+ * contents are never read. x [rows*in], pre/post [rows*out] device pointers;
+ * queued on `stream` (null: the session's) without waiting. */
+WELVET_API welvet_status welvet_dense_execute_noalloc(welvet_dense_session* sess, int32_t rows,
+                                                      const float* x, float* pre, float* post,
+                                                      void* stream);
+
 /* Measurement extension, no reference counterpart: one streaming read of the
  * device buffer buf (bytes a positive multiple of 16) with 16-byte loads,
  * queued on `stream` (null: the default stream); out_words (device,

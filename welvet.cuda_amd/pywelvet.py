@@ -96,6 +96,7 @@ def lib():
          [_i32, _i32, _i32, _i32, _i32, _i32, _fp, _dp, _sz, ctypes.POINTER(_vp)])
     _sig(L, "welvet_dense_execute", Status, [_vp, _fp, _fp, _fp])
     _sig(L, "welvet_dense_execute_device", Status, [_vp, _vp, _vp, _vp, _vp])
+    _sig(L, "welvet_dense_execute_noalloc", Status, [_vp, _i32, _vp, _vp, _vp, _vp])
     _sig(L, "welvet_dense_backward_device", Status,
          [_vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp])
     _sig(L, "welvet_dense_export_store", Status,
@@ -408,6 +409,10 @@ class DenseSession:
     def execute_device(self, x, pre, post, stream=None):
         check(lib().welvet_dense_execute_device(self.h, _vp(x), _vp(pre), _vp(post),
                                                 _vp(stream) if stream else None))
+
+    def execute_noalloc(self, rows, x, pre, post, stream=None):
+        check(lib().welvet_dense_execute_noalloc(self.h, rows, _vp(x), _vp(pre), _vp(post),
+                                                 _vp(stream) if stream else None))
 
     def backward_device(self, x, pre, post, g, use_target, dpre, dx, dw, loss_part=None,
                         stream=None):
