@@ -339,36 +339,39 @@ def cells_workload(pw, hip, name):
 
 def chain_workload(pw, hip, name):
     """The reference's volume semantics for the C5 cells: a WMN1 Grid 4x4x4 of
-    Stack cells (E4M3 / FP4 / E4M3 Dense 1024^2 each), run as one 192-layer
-    serial chain by welvet_model_forward_device (runtime/forward.cpp:98-156).
-    One model session has one scale scheme: E8M0 per 32 for all layers."""
+    Stack cells (Dense 1024^2 each: E4M3 per-row, FP4 E8M0/32, E4M3 per-row),
+    run as one 192-layer serial chain by welvet_model_forward_device
+    (runtime/forward.cpp:98-156). The scaled stores are quantized by the
+    library (a Dense session per layer, exported) and carried in the
+    descriptor's store payloads; the model mounts them as stored."""
     import numpy as np
 
     cells, batch, d = 64, 256, 1024
-    kinds = [4, 16, 4]
+    kinds = [(4, 2), (16, 3), (4, 2)]
     w = pw.Wire()
     w.u32(0x314E4D57)
     w.i32(2, cells, 4, 4, 4, 1)
+    stores = []
     for c in range(cells):
         seed = pw.seed_for(5, c)
         w.i32(19, len(kinds))
-        for li, dt in enumerate(kinds):
+        for li, (dt, sc) in enumerate(kinds):
             W = pw.normal(seed + 10 * li, d * d, 1 / np.sqrt(d)).reshape(d, d)
             pw.dense_child(w, d, d, -1, dt, W)
+            sess = pw.DenseSession(1, d, d, -1, dt, sc, W)
+            stores.append((dt, sc) + sess.export_store(dt))
+            sess.close()
     pw.empty_controls(w)
     for c in range(cells):
         pw.empty_controls(w)
         for _ in kinds:
             pw.empty_controls(w)
-    w.i32(cells * len(kinds))
-    for c in range(cells):
-        for dt in kinds:
-            # FormatNone payload of the right size; the session re-quantizes
-            # the fp32 W with the scheme
-            pw.store_payload(w, dt, d, d, np.zeros(d * d if dt != 16 else (d * d + 1) // 2, np.uint8))
+    w.i32(len(stores))
+    for dt, sc, native, rs, blk, ts in stores:
+        pw.store_payload(w, dt, d, d, native, scale=ts, scheme=sc, row_scale=rs, blk_exp=blk)
     for c in range(cells):
         w.i32(1, 0, 0, 0, 0, 0)
-    model = pw.ModelSession(w.bytes(), scheme=3)
+    model = pw.ModelSession(w.bytes())
     x = hip.upload(pw.normal(pw.seed_for(5, 0) + 500, batch * d).reshape(batch, d))
     y = hip.malloc(batch * d * 4)
     flops = cells * len(kinds) * 2 * batch * d * d
@@ -384,7 +387,8 @@ def chain_workload(pw, hip, name):
     return {"desc": name, "enqueue": enqueue, "per_graph": 1, "bytes": None, "flops": flops,
             "bound": "mfma", "dtype": "fp8e4m3+fp4e2m1", "direct": True,
             "config": {"workload": name, "cells": cells, "layers_per_cell": 3, "batch": batch,
-                       "width": d, "layer_kinds": "E4M3, FP4, E4M3, E8M0 per 32 (one scheme per model)",
+                       "width": d, "layer_kinds": "E4M3 per-row, FP4 E8M0/32, E4M3 per-row "
+                                               "(scaled WMN1 store payloads)",
                        "execution": ("reference volume semantics: Grid 4x4x4 of Stack cells, a "
                                      "192-layer serial chain, one welvet_model_forward_device "
                                      "per step (synchronous, not graph-captured)")},

@@ -121,3 +121,51 @@ def test_prng_is_splitmix64_box_muller():
     a = pw.normal(pw.seed_for(2), 1 << 16)
     assert abs(a.mean()) < 0.02 and abs(a.std() - 1) < 0.02
     assert np.array_equal(a, pw.normal(pw.seed_for(2), 1 << 16))
+
+
+def _one_dense(scheme, f, tag_extra=0):
+    w = pw.Wire()
+    w.u32(0x314E4D57)
+    w.i32(0, 1, 1, 1, 1, 1)
+    w.i32(19, 1)
+    pw.dense_child(w, 40, 2, -1, 4, np.zeros((2, 40), np.float32))
+    pw.empty_controls(w)
+    pw.empty_controls(w)
+    pw.empty_controls(w)
+    w.i32(1)
+    w.i32(4 | (scheme << 8) | tag_extra, 2, 40)
+    w.f32([1.0])
+    w.i32(len(f))
+    if len(f):
+        w.f32(np.asarray(f, np.float32))
+    w.i32(80)
+    w.u8(np.zeros(80, np.uint8))
+    w.i32(0)
+    return np.frombuffer(w.bytes(), np.uint8).copy()
+
+
+@pytest.mark.parametrize("scheme,f,ok", [
+    (2, [0.5, 3.0], True),
+    (2, [0.5], False),                              # one scale per row
+    (2, [0.5, float("inf")], False),                 # finite row scales
+    (3, [2.0 ** -127, 1.0, 2.0 ** 127, 0.25], True),  # 2 rows x 2 blocks, powers of two
+    (3, [1.0, 1.5, 1.0, 1.0], False),                # 1.5 is no power of two
+    (3, [1.0, 1.0], False),                          # rows * ceil(40/32) scales
+    (1, [], True),
+    (4, [], False),                                  # no scheme 4
+])
+def test_scaled_store_payload_parse(scheme, f, ok):
+    """The scaled store extension is checked while parsing, before any device
+    work: malformed payloads give code 1; well-formed ones get past the parse
+    (code 2 here, no device; 0 on a GPU host)."""
+    L = pw.lib()
+    buf = _one_dense(scheme, f)
+    h = ctypes.c_void_p()
+    st = L.welvet_model_mount(buf.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8)), buf.size,
+                              ctypes.byref(h))
+    if ok:
+        assert st.code in (0, 2), st.message
+        if st.code == 0:
+            L.welvet_model_release(h)
+    else:
+        assert st.code == 1, st.message

@@ -148,21 +148,8 @@ def test_grid_chain_matches_layer_by_layer(gpu, oracle, scheme):
 
 def parse_nws1(snap):
     """Stores of an NWS1 snapshot: (dtype, rows, cols, scale, native bytes)."""
-    assert snap[:4] == b"NWS1"
-    n = int(np.frombuffer(snap[4:8], "<i4")[0])
-    off, out = 8, []
-    for _ in range(n):
-        dt, rows, cols = np.frombuffer(snap[off:off + 12], "<i4").tolist()
-        scale = float(np.frombuffer(snap[off + 12:off + 16], "<f4")[0])
-        nf = int(np.frombuffer(snap[off + 16:off + 20], "<i4")[0])
-        off += 20 + 4 * nf
-        nn = int(np.frombuffer(snap[off:off + 4], "<i4")[0])
-        native = np.frombuffer(snap[off + 4:off + 4 + nn], np.uint8)
-        off += 4 + nn
-        nb = int(np.frombuffer(snap[off:off + 4], "<i4")[0])
-        off += 4 + 8 * nb
-        out.append((dt, rows, cols, scale, native))
-    return out
+    stores, _ = pw.parse_snapshot(snap)
+    return [(dt, rows, cols, scale, native) for dt, _, rows, cols, scale, _, native, _ in stores]
 
 
 def _segment_layers(rng):
@@ -224,7 +211,9 @@ def test_segment_sgd_requantizes_every_store(gpu, oracle, scheme):
     _, dw = m.backward(x, rng.standard_normal((8, 80)).astype(np.float32))
     lr = 0.25
     m.apply_sgd(dw, lr)
-    stores = parse_nws1(m.export())
+    snap = m.export()
+    assert all(sc == scheme for _, sc, *_ in pw.parse_snapshot(snap)[0])
+    stores = parse_nws1(snap)
     off = 0
     for (dt, W, _), (sdt, rows, cols, _, native) in zip(layers, stores):
         n = W.size
@@ -370,3 +359,88 @@ def test_segment_training_through_swiglu(gpu, oracle, scheme, batch):
         assert sdt == dt and np.array_equal(native, nat2), (dt, rows, cols)
         off += W.size
     m.close()
+
+
+def scaled_stack(layers, stores):
+    """Stack root, one NestedStack of Dense children; stores: per layer
+    (dtype, scheme, native, scale, row_scale, blk_exp)."""
+    w = pw.Wire()
+    w.u32(0x314E4D57)
+    w.i32(0, 1, 1, 1, 1, 1)
+    w.i32(19, len(layers))
+    for dt, W, act in layers:
+        pw.dense_child(w, W.shape[1], W.shape[0], act, dt, np.zeros_like(W))
+    pw.empty_controls(w)
+    pw.empty_controls(w)
+    for _ in layers:
+        pw.empty_controls(w)
+    w.i32(len(layers))
+    for (dt, W, _), (sdt, scheme, native, scale, rs, blk) in zip(layers, stores):
+        pw.store_payload(w, sdt, W.shape[0], W.shape[1], native, scale=scale, scheme=scheme,
+                         row_scale=rs, blk_exp=blk)
+    return w.bytes()
+
+
+def test_scaled_store_payloads_mount_and_export(gpu, oracle):
+    """Scaled stores in the WMN1 payload (the C5 cell mix: E4M3 per-row, FP4
+    E8M0/32, E4M3 per-row) mount as stored, forward as the oracle chain of
+    the same codes and scales, and export to NWS1 byte for byte."""
+    rng = np.random.default_rng(21)
+    dims = [300, 256, 192, 130]
+    mix = [(4, 2), (16, 3), (4, 2)]
+    layers, stores, want_chain = [], [], []
+    for i, (dt, sc) in enumerate(mix):
+        W = (rng.standard_normal((dims[i + 1], dims[i])) / np.sqrt(dims[i])).astype(np.float32)
+        native, rs, blk = oracle.quantize(dt, sc, dims[i + 1], dims[i], W)
+        layers.append((dt, W, -1))
+        stores.append((dt, sc, native, 1.0, rs, blk))
+        want_chain.append((dt, sc, W))
+    for batch in (1, 3, 40):
+        x = rng.standard_normal((batch, dims[0])).astype(np.float32)
+        m = pw.ModelSession(scaled_stack(layers, stores))
+        y = m.forward(x)
+        cur = x
+        for dt, sc, W in want_chain:
+            native, rs, blk = oracle.quantize(dt, sc, W.shape[0], W.shape[1], W)
+            _, cur = oracle.dense(oracle.dequant(dt, sc, W.shape[0], W.shape[1], native, rs, blk), cur)
+        assert rel_l2(y, cur) <= tol(batch, chain=3)
+        snap, extras = pw.parse_snapshot(m.export())
+        m.close()
+        assert extras == 0 and len(snap) == 3
+        for (sdt, scheme, native, _, rs, blk), got in zip(stores, snap):
+            dt, gsc, rows, cols, scale, f, gnat, bias = got
+            assert (dt, gsc) == (sdt, scheme) and np.array_equal(gnat, native) and bias.size == 0
+            if scheme == 2:
+                assert np.array_equal(f, rs)
+            else:
+                e = np.frexp(f.astype(np.float64))[1] - 1  # f = 2^e exactly
+                assert np.array_equal(np.ldexp(1.0, e), f.astype(np.float64))
+                assert np.array_equal(e + 127, blk.astype(np.int64))
+
+
+@pytest.mark.parametrize("scheme", [1, 2, 3])
+def test_requantized_model_export_mounts_back_identically(gpu, oracle, scheme):
+    """A model re-quantized at mount (welvet_model_mount_q) exports its scaled
+    stores; a descriptor built from that snapshot mounts them as stored and
+    gives the same outputs bit for bit."""
+    rng = np.random.default_rng(30 + scheme)
+    layers = [(dt, (rng.standard_normal((96, 96)) / 10).astype(np.float32), act)
+              for dt, act in ((4, -1), (16, 0), (5, -1))]
+    x = rng.standard_normal((24, 96)).astype(np.float32)
+    m = pw.ModelSession(build_stack([layers]), scheme=scheme)
+    y = m.forward(x)
+    snap, _ = pw.parse_snapshot(m.export())
+    m.close()
+    stores = []
+    for dt, sc, rows, cols, scale, f, native, _ in snap:
+        assert sc == scheme
+        blk = None
+        if sc == 3:
+            blk = (np.frexp(f.astype(np.float64))[1] - 1 + 127).astype(np.uint8)
+        stores.append((dt, sc, native, scale, f if sc == 2 else None, blk))
+    m2 = pw.ModelSession(scaled_stack(layers, stores))
+    assert np.array_equal(m2.forward(x), y)
+    snap2, _ = pw.parse_snapshot(m2.export())
+    m2.close()
+    for a, b in zip(snap, snap2):
+        assert a[:5] == b[:5] and all(np.array_equal(u, v) for u, v in zip(a[5:], b[5:]))

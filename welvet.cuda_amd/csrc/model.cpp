@@ -7,7 +7,8 @@
 //   root controls, per-child control trees, i32 store count, stores,
 //   and for Grid roots per cell: i32 enabled, remote, tz, ty, tx, tl.
 // Store payload (model_session.cpp:135-153): i32 dtype, rows, cols, f32 scale,
-//   vec<f32> f32, vec<u8> native, vec<f64> bias (vec = i32 count + items).
+//   vec<f32> f32, vec<u8> native, vec<f64> bias (vec = i32 count + items);
+//   scaled stores extend it (read_store).
 // Only the quantized Dense path is served: Dense, NestedStack, SwiGLU and MHA
 // children with FP8/FP4 stores; anything else is reported as code 2/3.
 #include "model.h"
@@ -204,10 +205,35 @@ void collect(ModelNode& c, std::vector<WeightStore*>* out) {
   for (auto& ch : c.nested) collect(ch, out);
 }
 
+// Store payload (model_session.cpp:135-162): i32 dtype, rows, cols, f32
+// scale, vec<f32> f32, vec<u8> native, vec<f64> bias. The reference's FP8 /
+// FP4 stores are FormatNone: f32 empty, scale unused (native_codec.cpp:176,
+// 534-549). Scaled stores of this build are an additive extension keyed in
+// the dtype word: bits 0-7 the DType id, bits 8-15 the scale scheme (0 is
+// the reference format, and the only one a reference reader accepts):
+//   1  per tensor: `scale` holds s (finite, > 0), f32 empty;
+//   2  per output row: f32 holds rows scales (finite);
+//   3  E8M0 per 32 inputs: f32 holds rows * ceil(cols / 32) scales, each an
+//      exact power of two 2^e, e in [-127, 127] (2^-127 is the subnormal
+//      0x00400000).
+// The dequantized weight is decode(code) times the scale (times 2^e for
+// scheme 3), as the library's own quantizer produces it.
+constexpr int32_t kSchemeShift = 8;
+
+int e8m0_of_pow2(float v) {
+  const uint32_t u = bits_of(v);
+  if (u == 0x00400000u) return -127;
+  const uint32_t ex = (u >> 23) & 0xFFu;
+  require((u & 0x807FFFFFu) == 0 && ex >= 1 && ex <= 254, "block scale is not a power of two");
+  return (int)ex - 127;
+}
+
 void read_store(Reader& r, WeightStore* s) {
-  const int dt = r.one<int32_t>(), rows = r.one<int32_t>(), cols = r.one<int32_t>();
+  const int32_t tag = r.one<int32_t>(), rows = r.one<int32_t>(), cols = r.one<int32_t>();
   const float scale = r.one<float>();
-  require(dt >= 0 && dt <= 33 && rows == s->rows && cols == s->cols && std::isfinite(scale),
+  const int32_t dt = tag & 0xFF, scheme = (tag >> kSchemeShift) & 0xFF;
+  require(tag >= 0 && (tag >> 16) == 0 && dt <= 33 && scheme <= 3 && rows == s->rows &&
+              cols == s->cols && std::isfinite(scale),
           "native store metadata mismatch");
   auto f = r.vec<float>();
   auto raw = r.vec<uint8_t>();
@@ -216,14 +242,30 @@ void read_store(Reader& r, WeightStore* s) {
     throw StatusError(Status::err(kUnsupported, "model store dtype " + std::to_string(dt) +
                                                     " is outside the FP8/FP4 path"));
   const int64_t n = (int64_t)rows * cols;
-  require(f.empty() && raw.size() == (dt == kFP4 ? (size_t)((n + 1) / 2) : (size_t)n),
+  const size_t nb = (size_t)(cols + 31) / 32;
+  require(raw.size() == (dt == kFP4 ? (size_t)((n + 1) / 2) : (size_t)n),
           "native store payload length mismatch");
+  const size_t want_f = scheme == kSchemeRow ? (size_t)rows
+                        : scheme == kSchemeBlock32 ? (size_t)rows * nb : 0;
+  require(f.size() == want_f, "store scale payload length mismatch");
   s->dtype = dt;
-  s->scheme = kSchemeRef;
+  s->scheme = scheme;
   s->scale = scale;
   s->native = std::move(raw);
-  s->row_scale.assign((size_t)rows, 1.0f);
   s->blk_exp.clear();
+  if (scheme == kSchemeTensor) {
+    require(scale > 0.0f, "tensor scale must be positive");
+    s->row_scale.assign((size_t)rows, scale);
+  } else if (scheme == kSchemeRow) {
+    for (float v : f) require(std::isfinite(v), "row scale is not finite");
+    s->row_scale = std::move(f);
+  } else {
+    s->row_scale.assign((size_t)rows, 1.0f);
+    if (scheme == kSchemeBlock32) {
+      s->blk_exp.resize(f.size());
+      for (size_t i = 0; i < f.size(); ++i) s->blk_exp[i] = (uint8_t)(e8m0_of_pow2(f[i]) + 127);
+    }
+  }
   s->bias = std::move(bias);
 }
 
@@ -667,16 +709,25 @@ Status model_forward(Model& m, const std::vector<int>& in_shape, const float* x,
 }
 
 namespace {
+// The extended store payload of read_store (scheme 0: the reference format).
 void write_store(std::vector<uint8_t>* w, const WeightStore& s) {
   auto put = [&](const void* p, size_t n) {
     const uint8_t* b = static_cast<const uint8_t*>(p);
     w->insert(w->end(), b, b + n);
   };
-  const int32_t hdr[3] = {s.dtype, s.rows, s.cols};
+  const int32_t hdr[3] = {s.dtype | (s.scheme << kSchemeShift), s.rows, s.cols};
   put(hdr, sizeof hdr);
   put(&s.scale, 4);
-  const int32_t nf = 0;
+  std::vector<float> f;
+  if (s.scheme == kSchemeRow) {
+    f = s.row_scale;
+  } else if (s.scheme == kSchemeBlock32) {
+    f.resize(s.blk_exp.size());
+    for (size_t i = 0; i < f.size(); ++i) f[i] = pow2f((int)s.blk_exp[i] - 127);
+  }
+  const int32_t nf = (int32_t)f.size();
   put(&nf, 4);
+  put(f.data(), f.size() * sizeof(float));
   const int32_t nn = (int32_t)s.native.size();
   put(&nn, 4);
   put(s.native.data(), s.native.size());

@@ -624,16 +624,57 @@ def empty_controls(w):
     w.i32(0)
 
 
-def store_payload(w, dtype, rows, cols, native, scale=1.0, bias=None):
-    w.i32(dtype, rows, cols)
+def store_payload(w, dtype, rows, cols, native, scale=1.0, bias=None, scheme=0, row_scale=None,
+                  blk_exp=None):
+    """One store of a WMN1 descriptor (model_session.cpp:135-162). scheme 0 is
+    the reference's FormatNone store (no f32 payload); schemes 1-3 are this
+    library's scaled extension: the dtype word carries the scheme in bits
+    8-15, the tensor scale goes in `scale` (1), the row scales (2) or the
+    E8M0 block scales as powers of two (3) in the f32 payload."""
+    w.i32(dtype | (scheme << 8), rows, cols)
     w.f32([scale])
-    w.i32(0)  # f32 payload (FP8/FP4 stores have none)
+    if scheme == 2:
+        f = np.asarray(row_scale, np.float32)
+    elif scheme == 3:
+        e = np.asarray(blk_exp, np.int64) - 127
+        f = np.where(e >= -126, np.ldexp(1.0, e), 2.0 ** -127).astype(np.float32)
+    else:
+        f = np.zeros(0, np.float32)
+    w.i32(f.size)
+    if f.size:
+        w.f32(f)
     w.i32(len(native))
     w.u8(native)
     b = np.zeros(0) if bias is None else np.asarray(bias, np.float64)
     w.i32(b.size)
     if b.size:
         w.f64(b)
+
+
+def parse_snapshot(raw):
+    """NWS1 blob -> list of stores (dtype, scheme, rows, cols, scale, f32,
+    native, bias) and the extras count."""
+    assert raw[:4] == b"NWS1"
+    off = 4
+    n = int(np.frombuffer(raw[off:off + 4], "<i4")[0])
+    off += 4
+    out = []
+    for _ in range(n):
+        tag, rows, cols = np.frombuffer(raw[off:off + 12], "<i4").tolist()
+        scale = float(np.frombuffer(raw[off + 12:off + 16], "<f4")[0])
+        off += 16
+        nf = int(np.frombuffer(raw[off:off + 4], "<i4")[0])
+        f = np.frombuffer(raw[off + 4:off + 4 + 4 * nf], "<f4").copy()
+        off += 4 + 4 * nf
+        nn = int(np.frombuffer(raw[off:off + 4], "<i4")[0])
+        native = np.frombuffer(raw[off + 4:off + 4 + nn], np.uint8).copy()
+        off += 4 + nn
+        nb = int(np.frombuffer(raw[off:off + 4], "<i4")[0])
+        bias = np.frombuffer(raw[off + 4:off + 4 + 8 * nb], "<f8").copy()
+        off += 4 + 8 * nb
+        out.append((tag & 0xFF, (tag >> 8) & 0xFF, rows, cols, scale, f, native, bias))
+    extras = int(np.frombuffer(raw[off:off + 4], "<i4")[0])
+    return out, extras
 
 
 def tensor_bytes(x):
