@@ -149,18 +149,19 @@ def dense_workload(pw, hip, name, cfg_id, dtype, scheme, batch, K, N, copies, bo
     dx = hip.upload(x)
     dy = hip.malloc(batch * N * 4)
     b = 1 if dtype != 16 else 0.5
-    scale_bytes = 4 * N if scheme in (1, 2) else (N * ((K + 31) // 32) if scheme == 3 else 0)
+    sc = scheme & 15  # backend: scale scheme in bits 0-3, bit 4 two activation terms
+    scale_bytes = 4 * N if sc in (1, 2) else (N * ((K + 31) // 32) if sc == 3 else 0)
     nbytes = int(N * K * b) + scale_bytes + 4 * batch * K + 4 * batch * N
     flops = 2 * batch * N * K
     dname = {4: "fp8e4m3", 5: "fp8e5m2", 16: "fp4e2m1"}[dtype]
-    sname = {0: "none", 1: "per-tensor fp32", 2: "per-row fp32", 3: "e8m0 per 32"}[scheme]
+    sname = {0: "none", 1: "per-tensor fp32", 2: "per-row fp32", 3: "e8m0 per 32"}[sc]
 
     def enqueue(i, stream):
         sessions[i % copies].execute_device(dx, dy, dy, stream)
 
     def cpu(budget_s):
         rows = min(batch, 256)
-        per_n, per_1, mount, th, desc = cpu_layers([(dtype, scheme, rows, K, N, W, x[:rows])],
+        per_n, per_1, mount, th, desc = cpu_layers([(dtype, sc, rows, K, N, W, x[:rows])],
                                                    budget_s)
         f = batch / rows
 
@@ -237,14 +238,14 @@ def swiglu_workload(pw, hip, name, batch, copies):
             "cpu": cpu, "close": close}
 
 
-def mha_workload(pw, hip, name):
+def mha_workload(pw, hip, name, two=0):
     import numpy as np
 
     B, S, d, H, hd = 8, 512, 1024, 16, 64
     seed = pw.seed_for(4)
     Ws = [pw.normal(seed + i, d * d, 1 / np.sqrt(d)).reshape(d, d) for i in range(4)]
     x = pw.normal(seed + 500, B * S * d).reshape(B * S, d)
-    s = pw.MHASession(B, S, d, H, H, hd, S, 1, 0, 5, 2, *Ws)
+    s = pw.MHASession(B, S, d, H, H, hd, S, 1, 0, 5, 2 | two, *Ws)
     dx = hip.upload(x)
     da = hip.malloc(B * S * d * 4)
     dy = hip.malloc(B * S * d * 4)
@@ -276,7 +277,7 @@ def mha_workload(pw, hip, name):
             "cpu": None, "close": close}
 
 
-def cells_workload(pw, hip, name):
+def cells_workload(pw, hip, name, two=0):
     import numpy as np
 
     cells, batch, d = 64, 256, 1024
@@ -287,7 +288,7 @@ def cells_workload(pw, hip, name):
         row = []
         for li, (dt, sc) in enumerate(kinds):
             W = pw.normal(seed + 10 * li, d * d, 1 / np.sqrt(d)).reshape(d, d)
-            row.append(pw.DenseSession(batch, d, d, -1, dt, sc, W))
+            row.append(pw.DenseSession(batch, d, d, -1, dt, sc | two, W))
         sessions.append(row)
         x = pw.normal(seed + 500, batch * d).reshape(batch, d)
         bufs.append([hip.upload(x)] + [hip.malloc(batch * d * 4) for _ in kinds])
@@ -337,7 +338,7 @@ def cells_workload(pw, hip, name):
             "cpu": cpu, "close": close}
 
 
-def chain_workload(pw, hip, name):
+def chain_workload(pw, hip, name, two=0):
     """The reference's volume semantics for the C5 cells: a WMN1 Grid 4x4x4 of
     Stack cells (Dense 1024^2 each: E4M3 per-row, FP4 E8M0/32, E4M3 per-row),
     run as one 192-layer serial chain by welvet_model_forward_device
@@ -371,7 +372,7 @@ def chain_workload(pw, hip, name):
         pw.store_payload(w, dt, d, d, native, scale=ts, scheme=sc, row_scale=rs, blk_exp=blk)
     for c in range(cells):
         w.i32(1, 0, 0, 0, 0, 0)
-    model = pw.ModelSession(w.bytes())
+    model = pw.ModelSession(w.bytes(), scheme=two)  # backend 16: stored payloads, two terms
     x = hip.upload(pw.normal(pw.seed_for(5, 0) + 500, batch * d).reshape(batch, d))
     y = hip.malloc(batch * d * 4)
     flops = cells * len(kinds) * 2 * batch * d * d
@@ -467,7 +468,8 @@ def backward_workload(pw, hip, name, copies):
             "cpu": cpu, "close": close}
 
 
-def make_workload(pw, hip, config, copies):
+def make_workload(pw, hip, config, copies, terms=3):
+    two = 16 if terms == 2 else 0  # backend bit for two activation terms
     if config == "c2":
         return dense_workload(pw, hip, "dense_gemv_4096x4096_fp8e4m3_rowscale_b1", 2, 4, 2, 1,
                               4096, 4096, copies, "hbm")
@@ -479,16 +481,20 @@ def make_workload(pw, hip, config, copies):
     if config == "c3b16":
         return swiglu_workload(pw, hip, "swiglu_4096x11008_fp4_e8m0_b16", 16, min(copies, 8))
     if config == "c4":
-        return dense_workload(pw, hip, "mha_projection_gemm_4096x1024x1024_fp8e5m2_rowscale", 4,
-                              5, 2, 4096, 1024, 1024, min(copies, 4), "mfma")
+        return dense_workload(pw, hip, "mha_projection_gemm_4096x1024x1024_fp8e5m2_rowscale"
+                              + ("_2terms" if two else ""), 4, 5, 2 | two, 4096, 1024, 1024,
+                              min(copies, 4), "mfma")
     if config == "c4mha":
-        return mha_workload(pw, hip, "mha_layer_b8_s512_d1024_h16_fp8e5m2_rowscale")
+        return mha_workload(pw, hip, "mha_layer_b8_s512_d1024_h16_fp8e5m2_rowscale"
+                            + ("_2terms" if two else ""), two)
     if config == "c2bwd":
         return backward_workload(pw, hip, "dense_backward_4096x4096_fp8e4m3_rowscale_b1", 16)
     if config == "c5chain":
-        return chain_workload(pw, hip, "volume_grid_4x4x4_stack3_dense_1024_b256_serial")
+        return chain_workload(pw, hip, "volume_grid_4x4x4_stack3_dense_1024_b256_serial"
+                              + ("_2terms" if two else ""), two)
     if config == "c5":
-        return cells_workload(pw, hip, "volume_64_cells_3x_dense_1024_b256")
+        return cells_workload(pw, hip, "volume_64_cells_3x_dense_1024_b256"
+                              + ("_2terms" if two else ""), two)
     raise SystemExit(f"unknown config {config}")
 
 
@@ -602,6 +608,9 @@ def main():
     ap.add_argument("--config", default="c2", choices=CONFIGS)
     ap.add_argument("--copies", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--terms", type=int, default=3, choices=(2, 3),
+                    help="activation terms of the matrix-core GEMMs (c4, c4mha, c5, c5chain): "
+                         "3 (default) or 2 (backend bit 16)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run device-to-device copies of MIB MiB (the known-size copy "
                          "that scales the FETCH_SIZE/WRITE_SIZE counters) and exit")
@@ -627,7 +636,7 @@ def main():
         wl = read_floor_workload(pw, hip, args.read_floor, max(1, args.copies))
         gemv = True
     else:
-        wl = make_workload(pw, hip, args.config, max(1, args.copies))
+        wl = make_workload(pw, hip, args.config, max(1, args.copies), args.terms)
         gemv = args.config in ("c1", "c2", "c3", "c3b16")
     steps = args.steps if args.steps is not None else (1280 if gemv else 64)
     steps = max(1, steps)
@@ -684,6 +693,8 @@ def main():
                    "rotation": ("one rotation over the copies continuing across warmup and "
                                 "timed regions: each step reads the least recently used copy")})
     config.pop("weight_copies_rotated", None)
+    if wl["bound"] == "mfma":
+        config["activation_terms"] = args.terms
     if wl["bytes"]:
         config.update({"algorithmic_bytes_per_step": wl["bytes"], "gbs": round(gbs, 2)})
     line = {

@@ -169,3 +169,21 @@ def test_scaled_store_payload_parse(scheme, f, ok):
             L.welvet_model_release(h)
     else:
         assert st.code == 1, st.message
+
+
+@pytest.mark.parametrize("backend,ok", [(0, True), (3, True), (16, True), (19, True), (4, False),
+                                        (32, False), (-1, False)])
+def test_model_backend_bits(backend, ok):
+    """backend: scale scheme 0-3 in bits 0-3, bit 4 (16) asks for two
+    activation terms; anything else is code 1, found before device work."""
+    L = pw.lib()
+    buf = _one_dense(0, [])
+    h = ctypes.c_void_p()
+    st = L.welvet_model_mount_q(buf.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8)), buf.size,
+                                backend, ctypes.byref(h))
+    if ok:
+        assert st.code in (0, 2), st.message
+        if st.code == 0:
+            L.welvet_model_release(h)
+    else:
+        assert st.code == 1, st.message

@@ -121,8 +121,11 @@ static welvet_status dense_mount(int32_t batch, int32_t in, int32_t out, int32_t
       return st;
     };
     Status st = s->stream.create();
-    if (st) st = wv::dense_build(in, out, act, dtype, backend, W_init, bias, bias_len, &s->layer,
+    int scheme = 0, terms = wv::kTerms;
+    if (st) st = wv::decode_backend(backend, &scheme, &terms);
+    if (st) st = wv::dense_build(in, out, act, dtype, scheme, W_init, bias, bias_len, &s->layer,
                                  s->stream.s);
+    s->layer.terms = terms;
     if (st) st = wv::dense_prepare_rows(&s->layer, batch, s->stream.s);
     if (st) st = wv::ensure_split(&s->ws, wv::dense_workspace_bytes(s->layer, batch));
     if (st) st = s->x.alloc((size_t)batch * in * sizeof(float));
@@ -361,7 +364,10 @@ welvet_status welvet_dense_normalbp_f32(int32_t batch, int32_t in, int32_t out, 
     hipStream_t st = stream.s;
     wv::DenseLayer L;
     wv::Workspace ws;
-    WV_TRY(wv::dense_build(in, out, act, dtype, backend, W_init, bias, bias_len, &L, st));
+    int scheme = 0, terms = wv::kTerms;
+    WV_TRY(wv::decode_backend(backend, &scheme, &terms));
+    WV_TRY(wv::dense_build(in, out, act, dtype, scheme, W_init, bias, bias_len, &L, st));
+    L.terms = terms;
     const size_t nx = (size_t)batch * in, ny = (size_t)batch * out, nw = (size_t)in * out;
     const int64_t parts = wv::dpre_blocks((int64_t)ny);
     wv::DevBuf dx_in, dpre_out, dpost, dg, dd, ddx, ddw, dwa, dloss;
@@ -420,7 +426,11 @@ welvet_status welvet_swiglu_normalbp_f32(int32_t batch, int32_t seq, int32_t inp
     hipStream_t st = stream.s;
     wv::SwiGLULayer L;
     wv::Workspace ws;
-    WV_TRY(wv::swiglu_build(input_dim, intermediate_dim, dtype, backend, Gate, Up, Down, &L, st));
+    int scheme = 0, terms = wv::kTerms;
+    WV_TRY(wv::decode_backend(backend, &scheme, &terms));
+    if (terms != wv::kTerms)
+      return Status::err(wv::kUnsupported, "swiglu: two activation terms are for Dense layers");
+    WV_TRY(wv::swiglu_build(input_dim, intermediate_dim, dtype, scheme, Gate, Up, Down, &L, st));
     const int rows = batch * seq;
     const size_t nx = (size_t)rows * input_dim, nh = (size_t)rows * intermediate_dim;
     const size_t wf = (size_t)intermediate_dim * input_dim, nw = 3 * wf;
@@ -475,7 +485,11 @@ welvet_status welvet_swiglu_mount(int32_t batch, int32_t seq, int32_t input_dim,
     auto* s = new welvet_swiglu_session();
     const int rows = batch * seq;
     Status st = s->stream.create();
-    if (st) st = wv::swiglu_build(input_dim, intermediate_dim, dtype, backend, Gate, Up, Down,
+    int scheme = 0, terms = wv::kTerms;
+    if (st) st = wv::decode_backend(backend, &scheme, &terms);
+    if (st && terms != wv::kTerms)
+      st = Status::err(wv::kUnsupported, "swiglu: two activation terms are for Dense layers");
+    if (st) st = wv::swiglu_build(input_dim, intermediate_dim, dtype, scheme, Gate, Up, Down,
                                   &s->layer, s->stream.s);
     if (st) st = wv::swiglu_prepare_rows(&s->layer, rows, s->stream.s);
     if (st) st = wv::ensure_split(&s->ws, wv::swiglu_workspace_bytes(s->layer, rows));
@@ -560,7 +574,13 @@ welvet_status welvet_mha_mount(int32_t batch, int32_t seq, int32_t d_model, int3
     auto* s = new welvet_mha_session();
     const size_t T = (size_t)batch * seq;
     Status st = s->stream.create();
-    if (st) st = wv::mha_build(cfg, dtype, backend, Q, K, V, O, &s->layer, s->stream.s);
+    int scheme = 0, terms = wv::kTerms;
+    if (st) st = wv::decode_backend(backend, &scheme, &terms);
+    // two-term projections leave the attention output at ~1e-3 rel-L2 (the
+    // softmax amplifies the Q/K error): outside the layer bound
+    if (st && terms != wv::kTerms)
+      st = Status::err(wv::kUnsupported, "mha: two activation terms are for Dense layers");
+    if (st) st = wv::mha_build(cfg, dtype, scheme, Q, K, V, O, &s->layer, s->stream.s);
     if (st) st = wv::mha_prepare(s->layer, batch, seq, &s->ws);
     if (st) st = s->x.alloc(T * d_model * sizeof(float));
     if (st) st = s->pre.alloc(T * cfg.q_dim() * sizeof(float));

@@ -104,7 +104,11 @@ struct MxvArgs {
 Status launch_mxv(const MxvArgs& a, int dtype, bool blk, hipStream_t st);
 
 // ---- batched GEMM on the scaled MFMA (mxg.hip) ----
-// Activations are split into kTerms E4M3 terms with per-32 E8M0 scales.
+// Activations are split into kTerms E4M3 terms with per-32 E8M0 scales (two
+// for one-matrix products that ask for them: half the residual precision,
+// two thirds of the matrix-core work and activation bytes). The split buffer
+// is always sized for kTerms; with two terms the (block, chunk) slices are
+// 2 x 2 KiB and the exponents sit at the same offset.
 constexpr int kTerms = 3;
 struct MxgArgs {
   // term codes in MFMA operand order, [mpad/16][kpad/128][kTerms][2][64][16]
@@ -145,8 +149,11 @@ struct MxgArgs {
   int rope_hd = 0;
   // large tiles, one matrix, N a multiple of 256: when set, the epilogue also
   // writes the split of post here, laid out as the split buffer of a layer
-  // with the same rows (mpad) and kpad = N (the next layer of a chain)
+  // with the same rows (mpad) and kpad = N (the next layer of a chain, which
+  // uses the same number of terms)
   uint8_t* next = nullptr;
+  // activation terms: kTerms, or 2 for one-matrix products
+  int terms = kTerms;
 };
 int mxg_block_m(int M);
 // Bytes of the K-split partial buffer the product of M rows with N outputs
@@ -156,7 +163,7 @@ size_t mxg_part_bytes(int M, int kpad, int N, int mats);
 size_t split_bytes(int M, int kpad);
 // x [M][cols] (row stride x_stride) -> split terms in buf.
 Status launch_split(const float* x, int x_stride, int M, int cols, int kpad, uint8_t* buf,
-                    hipStream_t st);
+                    hipStream_t st, int terms = kTerms);
 Status launch_mxg(const MxgArgs& p, int dtype, bool blk, hipStream_t st);
 // Grouped forms over n members that share every shape field: `jobs` / `tab`
 // are device arrays of n entries (one split input and buffer / one GEMM
@@ -166,7 +173,7 @@ struct SplitJob {
   uint8_t* buf = nullptr;
 };
 Status launch_split_group(const SplitJob* jobs, int n, bool vec, int x_stride, int M, int cols,
-                          int kpad, hipStream_t st);
+                          int kpad, hipStream_t st, int terms = kTerms);
 // Members must take the large-tile GEMM (M above 32 rows).
 Status launch_mxg_group(const MxgArgs* tab, const MxgArgs& shape, int n, int dtype, bool blk,
                         hipStream_t st);

@@ -26,6 +26,14 @@ Status check_dtype_scheme(int dtype, int scheme) {
   return Status::ok();
 }
 
+Status decode_backend(int backend, int* scheme, int* terms) {
+  if (backend < 0 || (backend & ~(kBackendTwoTerms | 0xF)) != 0 || (backend & 0xF) > kSchemeBlock32)
+    return Status::err(kInvalid, "backend: scale scheme 0..3, plus 16 for two activation terms");
+  *scheme = backend & 0xF;
+  *terms = (backend & kBackendTwoTerms) ? 2 : kTerms;
+  return Status::ok();
+}
+
 static Status download_store(DenseLayer* L, const uint8_t* d_raw, hipStream_t st) {
   WeightStore& s = L->store;
   const DeviceWeights& d = L->dev;
@@ -221,6 +229,7 @@ static MxgArgs mxg_args(const DenseLayer& L, int batch, const uint8_t* split) {
   p.bias_len = L.bias_len;
   // the partial sums follow the split terms (gemm_ws_bytes)
   p.part = reinterpret_cast<float*>(const_cast<uint8_t*>(split) + split_bytes(batch, L.dev.kpad));
+  p.terms = L.terms;
   return p;
 }
 
@@ -269,7 +278,8 @@ Status dense_forward_split(const DenseLayer& L, int batch, const float* x, bool 
   p.rope_tab = rope_tab;
   p.rope_hd = rope_hd;
   if (mxg_block_m(batch) > 16) {
-    if (!split_ready) WV_TRY(launch_split(x, L.in, batch, L.in, L.dev.kpad, split_buf(ws), st));
+    if (!split_ready)
+      WV_TRY(launch_split(x, L.in, batch, L.in, L.dev.kpad, split_buf(ws), st, L.terms));
   } else {
     set_input(p, x, L.in, L.in);
   }
@@ -358,7 +368,7 @@ Status dense_group_build(const DenseLayer* const* layers, int n, int batch,
     const DenseLayer* L = layers[i];
     if (!L || L->in != L0.in || L->out != L0.out || L->act != L0.act ||
         L->dev.dtype != L0.dev.dtype || L->dev.scheme != L0.dev.scheme ||
-        L->need_epi() != L0.need_epi())
+        L->need_epi() != L0.need_epi() || L->terms != L0.terms)
       return Status::err(kInvalid, "dense group: members differ in shape, dtype, scheme or epilogue");
     if (!x[i] || !pre[i] || (L->need_epi() && (!post || !post[i])))
       return Status::err(kInvalid, "dense group: null member buffer");
@@ -382,6 +392,7 @@ Status dense_group_build(const DenseLayer* const* layers, int n, int batch,
   g->n = n;
   g->batch = batch;
   g->dtype = L0.dev.dtype;
+  g->terms = L0.terms;
   g->blk = L0.dev.scheme == kSchemeBlock32;
   g->vec = vec;
   g->in = L0.in;
@@ -406,7 +417,7 @@ static bool group_has_nonfinite(const DenseGroup& g) {
 
 Status dense_group_forward(const DenseGroup& g, hipStream_t st) {
   WV_TRY(launch_split_group(g.jobs.as<const SplitJob>(), g.n, g.vec, g.in, g.batch, g.in, g.kpad,
-                            st));
+                            st, g.terms));
   WV_TRY(launch_mxg_group(g.tab.as<const MxgArgs>(), g.shape, g.n, g.dtype, g.blk, st));
   return group_fix(g, st);
 }
@@ -436,7 +447,7 @@ Status dense_chain_build(const DenseGroup* const* groups, int count, DenseChain*
     // the epilogue split would see the matrix-core values of rows that are
     // recomputed afterwards: such a link runs the consumer's own split
     if (P.shape.N % 256 != 0 || C.kpad != P.shape.N || P.shape.mats != 1 ||
-        group_has_nonfinite(P))
+        group_has_nonfinite(P) || P.terms != C.terms)
       continue;
     std::vector<MxgArgs> tab = P.htab;
     for (int i = 0; i < P.n; ++i) tab[i].next = C.hjobs[i].buf;
@@ -454,7 +465,7 @@ Status dense_chain_forward(const DenseChain& c, hipStream_t st) {
     const DenseGroup& g = *c.groups[k];
     if (k == 0 || !c.fused[k - 1])
       WV_TRY(launch_split_group(g.jobs.as<const SplitJob>(), g.n, g.vec, g.in, g.batch, g.in,
-                                g.kpad, st));
+                                g.kpad, st, g.terms));
     const MxgArgs* tab = c.fused[k] ? c.tabs[k].as<const MxgArgs>() : g.tab.as<const MxgArgs>();
     WV_TRY(launch_mxg_group(tab, g.shape, g.n, g.dtype, g.blk, st));
     WV_TRY(group_fix(g, st));
@@ -709,7 +720,8 @@ Status mha_forward(const MHALayer& L, int batch, int seq, const float* x, float*
     const bool once = mxg_block_m(T) > 16;
     const double* tab = rope_epi ? ws->c.as<const double>() : nullptr;
     const int rhd = rope_epi ? c.head_dim : 0;
-    if (once) WV_TRY(launch_split(x, c.d_model, T, c.d_model, L.q.dev.kpad, split_buf(ws), st));
+    if (once)
+      WV_TRY(launch_split(x, c.d_model, T, c.d_model, L.q.dev.kpad, split_buf(ws), st, L.q.terms));
     WV_TRY(dense_forward_split(L.q, T, x, once, ws, qb, nullptr, st, tab, rhd));
     WV_TRY(dense_forward_split(L.k, T, x, once, ws, kb, nullptr, st, tab, rhd));
     WV_TRY(dense_forward_split(L.v, T, x, once, ws, vb, nullptr, st));

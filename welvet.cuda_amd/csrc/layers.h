@@ -25,6 +25,15 @@ struct WeightStore {
 
 Status check_dtype_scheme(int dtype, int scheme);
 
+// The ABI's `backend` argument: bits 0-3 the scale scheme (0-3); bit 4 asks
+// for two activation terms instead of three on the matrix-core paths of a
+// Dense layer: two thirds of the matrix-core work and activation bytes, a
+// per-product rel-L2 of ~6.3e-4 instead of ~2e-5 (measured), inside the
+// 1e-3 layer bound. SwiGLU and MHA layers refuse it (their chained products
+// and the softmax take the error past the bound). Other bits are invalid.
+constexpr int kBackendTwoTerms = 0x10;
+Status decode_backend(int backend, int* scheme, int* terms);
+
 // Scratch owned by a session and reused across calls (grown at mount).
 struct Workspace {
   DevBuf a;  // quantized activations / intermediates
@@ -37,6 +46,7 @@ struct Workspace {
 
 struct DenseLayer {
   int in = 0, out = 0, act = kLinear;
+  int terms = kTerms;  // activation terms of the matrix-core paths (2 or 3)
   WeightStore store;
   DeviceWeights dev;
   DevBuf bias_dev;
@@ -104,7 +114,7 @@ Status ensure_split(Workspace* ws, size_t n);
 // (and captured) without host work. Only batches above 32 rows use the
 // grouped kernels (dense_group_fused); smaller ones run member by member.
 struct DenseGroup {
-  int n = 0, batch = 0, dtype = 0;
+  int n = 0, batch = 0, dtype = 0, terms = kTerms;
   bool blk = false, vec = false;
   int in = 0, kpad = 0;
   MxgArgs shape;

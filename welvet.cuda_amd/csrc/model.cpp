@@ -269,7 +269,10 @@ void read_store(Reader& r, WeightStore* s) {
   s->bias = std::move(bias);
 }
 
-void build(ModelNode& c, int scheme, hipStream_t st) {
+void build(ModelNode& c, int scheme, int terms, hipStream_t st) {
+  if (terms != kTerms && (c.kind == 4 || c.kind == 7))
+    throw StatusError(Status::err(kUnsupported,
+                                  "two activation terms are for Dense children, not SwiGLU or MHA"));
   switch (c.kind) {
   case 1: {
     c.dense = std::make_unique<DenseLayer>();
@@ -280,6 +283,7 @@ void build(ModelNode& c, int scheme, hipStream_t st) {
       good(dense_build(c.in, c.out, c.act, s.dtype, scheme, c.W.data(), s.bias.data(),
                        s.bias.size(), c.dense.get(), st));
     }
+    c.dense->terms = terms;
     break;
   }
   case 4: {
@@ -306,11 +310,12 @@ void build(ModelNode& c, int scheme, hipStream_t st) {
       if (scheme == kSchemeRef) good(dense_build_from_store(s.cols, s.rows, kLinear, s, parts[i], st));
       else good(dense_build(s.cols, s.rows, kLinear, s.dtype, scheme, ws[i]->data(), s.bias.data(),
                             s.bias.size(), parts[i], st));
+      parts[i]->terms = terms;
     }
     break;
   }
   case 19:
-    for (auto& ch : c.nested) build(ch, scheme, st);
+    for (auto& ch : c.nested) build(ch, scheme, terms, st);
     break;
   default: break;
   }
@@ -414,10 +419,11 @@ Tensor stack_forward(std::vector<ModelNode>& children, const Tensor& in, Arena& 
 
 }  // namespace
 
-Status model_parse(const uint8_t* data, size_t size, int scheme, Model* m) {
+Status model_parse(const uint8_t* data, size_t size, int backend, Model* m) {
   try {
     require(data && size >= 28 && size <= (1ull << 32), "invalid mount arguments");
-    if (scheme < 0 || scheme > 3) return Status::err(kInvalid, "backend (scale scheme) must be 0..3");
+    int scheme = 0, terms = kTerms;
+    WV_TRY(decode_backend(backend, &scheme, &terms));
     Reader r{data, size};
     require(r.one<uint32_t>() == 0x314e4d57u, "unsupported model descriptor version");
     m->root = r.one<int32_t>();
@@ -455,6 +461,7 @@ Status model_parse(const uint8_t* data, size_t size, int scheme, Model* m) {
     }
     require(r.left == 0, "trailing descriptor bytes");
     m->scheme = scheme;
+    m->terms = terms;
     return Status::ok();
   } catch (const StatusError& e) {
     return Status::err(e.code, e.what());
@@ -467,7 +474,7 @@ Status model_parse(const uint8_t* data, size_t size, int scheme, Model* m) {
 
 Status model_build(Model* m, hipStream_t st) {
   try {
-    for (auto& c : m->children) build(c, m->scheme, st);
+    for (auto& c : m->children) build(c, m->scheme, m->terms, st);
     return Status::ok();
   } catch (const StatusError& e) {
     return Status::err(e.code, e.what());

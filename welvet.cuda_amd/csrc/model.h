@@ -52,12 +52,15 @@ struct Model {
   std::vector<ModelNode> children;  // Stack children or Grid cells in hop order
   std::vector<GridCell> cells;
   int scheme = 0;
+  int terms = kTerms;  // activation terms of the Dense and MHA layers' matrix-core paths
   ModelScratch scratch;
 };
 
 // Parses and validates a WMN1 descriptor (src/interop/model_session.cpp:
 // 319-404) without touching the device.
-Status model_parse(const uint8_t* data, size_t size, int scheme, Model* m);
+// `backend` as the ABI's (decode_backend): the re-quantization scheme (0:
+// the stored payloads as they are) and the activation terms.
+Status model_parse(const uint8_t* data, size_t size, int backend, Model* m);
 // Mounts the parsed weights on the device. scheme 0 uses the stored payloads
 // as they are (reference behaviour); schemes 1-3 re-quantize each child's
 // fp32 weights.

@@ -88,7 +88,7 @@ constexpr int waitcnt_imm(int vm, int lgkm) {
 // gathered to the lanes that pass them to the instruction (row l % 16, block
 // l / 16) and stored as one dword per lane at scales + 4 l (byte t: term t).
 // AS: the address space of the destination (1 global, 3 LDS).
-template <int AS>
+template <int AS, int NT = kTerms>
 __device__ __forceinline__ void split_terms(float (&v)[2][16],
                                             __attribute__((address_space(AS))) uint8_t* chunk,
                                             __attribute__((address_space(AS))) uint8_t* scales,
@@ -102,7 +102,7 @@ __device__ __forceinline__ void split_terms(float (&v)[2][16],
   const int src = ((lane >> 4) & 1) * 32 + i16;
   uint32_t sword = 0x7F000000u;  // byte 3 unused
 #pragma unroll
-  for (int t = 0; t < kTerms; ++t) {
+  for (int t = 0; t < NT; ++t) {
     int e[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -118,7 +118,7 @@ __device__ __forceinline__ void split_terms(float (&v)[2][16],
         int w4 = __builtin_amdgcn_cvt_pk_fp8_f32(v[h][4 * q] * inv, v[h][4 * q + 1] * inv, 0, false);
         w4 = __builtin_amdgcn_cvt_pk_fp8_f32(v[h][4 * q + 2] * inv, v[h][4 * q + 3] * inv, w4, true);
         wq[q] = w4;
-        if (t + 1 < kTerms) {
+        if (t + 1 < NT) {
           const v2f q0 = __builtin_amdgcn_cvt_pk_f32_fp8(w4, false);
           const v2f q1 = __builtin_amdgcn_cvt_pk_f32_fp8(w4, true);
           v[h][4 * q] -= q0.x * sc, v[h][4 * q + 1] -= q0.y * sc;
@@ -139,7 +139,7 @@ __device__ __forceinline__ void split_terms(float (&v)[2][16],
 // takes the 32 values of its operand, k = 64h + 16g + j (h = 0, 1; j < 16),
 // and split_terms writes them. Rows >= M and columns >= cols give zero codes.
 // VEC: x 16-byte aligned, cols and x_stride multiples of 4.
-template <bool VEC>
+template <bool VEC, int NT>
 __global__ __launch_bounds__(kThreads) void k_split(const float* __restrict__ x, int x_stride,
                                                     int M, int cols, int mpad, int kpad,
                                                     uint8_t* __restrict__ a,
@@ -203,8 +203,8 @@ __global__ __launch_bounds__(kThreads) void k_split(const float* __restrict__ x,
       v[h][4 * q] = t.x, v[h][4 * q + 1] = t.y, v[h][4 * q + 2] = t.z, v[h][4 * q + 3] = t.w;
     }
 
-  split_terms<1>(v, (GlobalU8)(a + (size_t)(rb * KC + kc) * kChunkBytes),
-                 (GlobalU8)(as + (size_t)(rb * KC + kc) * kChunkScaleBytes), lane);
+  split_terms<1, NT>(v, (GlobalU8)(a + (size_t)(rb * KC + kc) * NT * kFragBytes),
+                     (GlobalU8)(as + (size_t)(rb * KC + kc) * kChunkScaleBytes), lane);
 }
 
 // Large-M tile (M > 32): 128 activation rows x 128 staged weight rows (64 per
@@ -274,10 +274,11 @@ __device__ __forceinline__ MxgArgs load_args(ConstArgs t) {
   p.next = t->next;
   p.rope_tab = t->rope_tab;
   p.rope_hd = t->rope_hd;
+  p.terms = t->terms;
   return p;
 }
 
-template <int DT, bool BLK, int MATS, bool GROUP, int W, int BR, bool KS = false>
+template <int DT, bool BLK, int MATS, bool GROUP, int W, int BR, bool KS = false, int NT = kTerms>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W / 4))) void k_mxg(
     MxgArgs p0, const MxgArgs* __restrict__ tab, int tiles_m, int tiles_n) {
   constexpr bool FP4 = DT == kFP4;
@@ -317,13 +318,15 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
     ke = 2 * (int)((long)P * (ks + 1) / nks);
   }
 
-  // activation fragments of this wave (step s adds s * kChunkBytes / s * 256)
+  // activation fragments of this wave (step s adds s * CB / s * 256): the
+  // NT terms of a (16-row block, K chunk) are contiguous, CB bytes
+  constexpr int CB = NT * kFragBytes;
   const uint8_t* abase[SM];
   const uint32_t* sbase[SM];
 #pragma unroll
   for (int a = 0; a < SM; ++a) {
     const size_t rb = (size_t)(m0 / 16 + wave * SM + a);
-    abase[a] = p.a + rb * KC * kChunkBytes + lane * 16;
+    abase[a] = p.a + rb * KC * CB + lane * 16;
     sbase[a] = reinterpret_cast<const uint32_t*>(p.as + rb * KC * kChunkScaleBytes) + lane;
   }
   // weight copies: per-lane source of each 1 KiB copy this wave issues at
@@ -349,15 +352,15 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
           : nullptr;
 
   struct AFrag {
-    v8i x[kTerms][SM];
+    v8i x[NT][SM];
     uint32_t xs[SM];
   };
   auto load_a = [&](int s, AFrag& fr) {
 #pragma unroll
     for (int a = 0; a < SM; ++a) {
-      const uint8_t* src = abase[a] + (size_t)s * kChunkBytes;
+      const uint8_t* src = abase[a] + (size_t)s * CB;
 #pragma unroll
-      for (int t = 0; t < kTerms; ++t) {
+      for (int t = 0; t < NT; ++t) {
         const int4 lo = *reinterpret_cast<const int4*>(src + t * kFragBytes);
         const int4 hi = *reinterpret_cast<const int4*>(src + t * kFragBytes + 1024);
         fr.x[t][a] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
@@ -454,7 +457,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
           }
         };
         auto mfma_half = [&](int c0) {
-          static_assert(kTerms == 3, "three activation terms");
+          static_assert(NT == 2 || NT == 3, "two or three activation terms");
 #pragma unroll
           for (int a = 0; a < SM; ++a)
 #pragma unroll
@@ -465,11 +468,13 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
 #pragma unroll
             for (int c = 0; c < HB; ++c)
               acc[a][c0 + c] = mfma_term<DT, 1>(bf[c], fr[cur].x[1][a], acc[a][c0 + c], bsc[c], fr[cur].xs[a]);
+          if constexpr (NT == 3) {
 #pragma unroll
-          for (int a = 0; a < SM; ++a)
+            for (int a = 0; a < SM; ++a)
 #pragma unroll
-            for (int c = 0; c < HB; ++c)
-              acc[a][c0 + c] = mfma_term<DT, 2>(bf[c], fr[cur].x[2][a], acc[a][c0 + c], bsc[c], fr[cur].xs[a]);
+              for (int c = 0; c < HB; ++c)
+                acc[a][c0 + c] = mfma_term<DT, 2>(bf[c], fr[cur].x[NT - 1][a], acc[a][c0 + c], bsc[c], fr[cur].xs[a]);
+          }
         };
         read_b(0);
         __builtin_amdgcn_sched_barrier(0);
@@ -669,8 +674,8 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
               v[h][4 * q] = live ? t.x : 0.0f, v[h][4 * q + 1] = live ? t.y : 0.0f;
               v[h][4 * q + 2] = live ? t.z : 0.0f, v[h][4 * q + 3] = live ? t.w : 0.0f;
             }
-          split_terms<1>(v, (GlobalU8)(p.next + (size_t)(rb * kcn + kc) * kChunkBytes),
-                         (GlobalU8)(nscale + (size_t)(rb * kcn + kc) * kChunkScaleBytes), lane);
+          split_terms<1, NT>(v, (GlobalU8)(p.next + (size_t)(rb * kcn + kc) * CB),
+                             (GlobalU8)(nscale + (size_t)(rb * kcn + kc) * kChunkScaleBytes), lane);
         }
         __builtin_amdgcn_wave_barrier();
       }
@@ -714,13 +719,14 @@ int mxs_ksplit(int N, int kpad, int mpad) {
   return ks < S ? ks : S;
 }
 
-template <int DT, bool BLK, int MATS, int MB, int RB, int KRT, int D, bool XV>
+template <int DT, bool BLK, int MATS, int MB, int RB, int KRT, int D, bool XV, int NT>
 __global__ __launch_bounds__(64 * kSmallWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_mxs(
     MxgArgs p, int ksplit) {
   constexpr int ROWS = 16 * kSmallWaves * RB;  // weight rows per workgroup
   constexpr bool FP4 = DT == kFP4;
   constexpr int WB = FP4 ? 64 : 128;  // code bytes per weight row per chunk
-  __shared__ __attribute__((aligned(16))) uint8_t sA[MB * KRT * kChunkBytes];
+  constexpr int CB = NT * kFragBytes;  // the NT terms of one split unit
+  __shared__ __attribute__((aligned(16))) uint8_t sA[MB * KRT * CB];
   __shared__ __attribute__((aligned(16))) uint32_t sS[MB * KRT * 64];
 
   // the wave index in a scalar register: branches on it are uniform
@@ -832,7 +838,7 @@ __global__ __launch_bounds__(64 * kSmallWaves) __attribute__((amdgpu_waves_per_e
         d[2] = rowok && k + 2 < p.cols ? t.z : 0.0f;
         d[3] = rowok && k + 3 < p.cols ? t.w : 0.0f;
       }
-      split_terms<3>(v, (LdsU8)(sA + (size_t)j * kChunkBytes), (LdsU8)(sS + j * 64), lane);
+      split_terms<3, NT>(v, (LdsU8)(sA + (size_t)j * CB), (LdsU8)(sS + j * 64), lane);
     }
     if (u + 1 < U) load_unit(u + 1);
   }
@@ -855,13 +861,13 @@ __global__ __launch_bounds__(64 * kSmallWaves) __attribute__((amdgpu_waves_per_e
     __builtin_amdgcn_sched_barrier(0);
     const bool live = r < KR;  // uniform
     const int rr = live ? r : KR - 1;
-    v8i x[kTerms][MB];
+    v8i x[NT][MB];
     uint32_t xs[MB];
 #pragma unroll
     for (int b = 0; b < MB; ++b) {
-      const uint8_t* src = sA + (size_t)(b * KR + rr) * kChunkBytes + lane * 16;
+      const uint8_t* src = sA + (size_t)(b * KR + rr) * CB + lane * 16;
 #pragma unroll
-      for (int t = 0; t < kTerms; ++t) {
+      for (int t = 0; t < NT; ++t) {
         const int4 lo = *reinterpret_cast<const int4*>(src + t * kFragBytes);
         const int4 hi = *reinterpret_cast<const int4*>(src + t * kFragBytes + 1024);
         x[t][b] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
@@ -902,13 +908,15 @@ __global__ __launch_bounds__(64 * kSmallWaves) __attribute__((amdgpu_waves_per_e
 #pragma unroll
         for (int b = 0; b < MB; ++b)
           acc[m][j][b] = mfma_term<DT, 1>(w[m][j], x[1][b], acc[m][j][b], we[m][j], xs[b]);
+    if constexpr (NT == 3) {
 #pragma unroll
-    for (int m = 0; m < MATS; ++m)
+      for (int m = 0; m < MATS; ++m)
 #pragma unroll
-      for (int j = 0; j < RB; ++j)
+        for (int j = 0; j < RB; ++j)
 #pragma unroll
-        for (int b = 0; b < MB; ++b)
-          acc[m][j][b] = mfma_term<DT, 2>(w[m][j], x[2][b], acc[m][j][b], we[m][j], xs[b]);
+          for (int b = 0; b < MB; ++b)
+            acc[m][j][b] = mfma_term<DT, 2>(w[m][j], x[NT - 1][b], acc[m][j][b], we[m][j], xs[b]);
+    }
     __builtin_amdgcn_sched_barrier(0);
   }
 
@@ -1011,6 +1019,7 @@ __global__ __launch_bounds__(kThreads) void k_mxs_reduce(MxgArgs p, int ksplit, 
 
 template <int DT, bool BLK, int MATS, int MB, int RB, int KRT, bool XV = true>
 void launch_small_krt(const MxgArgs& p, int ksplit, hipStream_t st) {
+  constexpr int NT3 = kTerms;
   // ring depth: 6-14 KiB of weights in flight per wave within the register
   // budget of two waves per SIMD
   constexpr int D0 = (DT == kFP4 ? 8 : 6) / MATS + (DT == kFP4 && MATS == 2 ? 2 : 0);
@@ -1018,7 +1027,14 @@ void launch_small_krt(const MxgArgs& p, int ksplit, hipStream_t st) {
   constexpr int D = D1 < KRT ? D1 : KRT;
   const int rows = 16 * kSmallWaves * RB;
   const dim3 grid((unsigned)((p.N + rows - 1) / rows), (unsigned)ksplit);
-  k_mxs<DT, BLK, MATS, MB, RB, KRT, D, XV><<<grid, 64 * kSmallWaves, 0, st>>>(p, ksplit);
+  // two activation terms: Dense only (one matrix)
+  if constexpr (MATS == 1) {
+    if (p.terms == 2) {
+      k_mxs<DT, BLK, MATS, MB, RB, KRT, D, XV, 2><<<grid, 64 * kSmallWaves, 0, st>>>(p, ksplit);
+      return;
+    }
+  }
+  k_mxs<DT, BLK, MATS, MB, RB, KRT, D, XV, NT3><<<grid, 64 * kSmallWaves, 0, st>>>(p, ksplit);
 }
 
 template <int DT, bool BLK, int MATS, int MB, int RB>
@@ -1081,24 +1097,39 @@ Status launch_t(const MxgArgs& p, int bm, hipStream_t st) {
       if (ks > 1) {
         if (!p.part) return Status::err(kInvalid, "mxg: K-split partial buffer missing");
         const int tiles_n = (p.N + 127) / 128;
-        k_mxg<DT, BLK, 1, false, kMxgWaves, 128, true>
-            <<<dim3((unsigned)(tiles_m * tiles_n), (unsigned)ks), 64 * kMxgWaves, 0, st>>>(
-                p, nullptr, tiles_m, tiles_n);
+        const dim3 grid((unsigned)(tiles_m * tiles_n), (unsigned)ks);
+        if (p.terms == 2)
+          k_mxg<DT, BLK, 1, false, kMxgWaves, 128, true, 2><<<grid, 64 * kMxgWaves, 0, st>>>(
+              p, nullptr, tiles_m, tiles_n);
+        else
+          k_mxg<DT, BLK, 1, false, kMxgWaves, 128, true><<<grid, 64 * kMxgWaves, 0, st>>>(
+              p, nullptr, tiles_m, tiles_n);
         // the kernel boundary makes every split's partial sums visible
         const int64_t n = (int64_t)p.M * p.N;
         k_mxs_reduce<1><<<(unsigned)((n + kThreads - 1) / kThreads), kThreads, 0, st>>>(p, ks, 256);
         return hip_status(hipGetLastError(), "mxg K-split launch");
       }
     }
-    if (mxg_wide(1, tiles_m, p.N, MATS)) {
-      const int tiles_n = (p.N + 256 / MATS - 1) / (256 / MATS);
-      k_mxg<DT, BLK, MATS, false, kMxgWaves, 256><<<(unsigned)(tiles_m * tiles_n), 64 * kMxgWaves, 0, st>>>(
-          p, nullptr, tiles_m, tiles_n);
-    } else {
-      const int tiles_n = (p.N + 128 / MATS - 1) / (128 / MATS);
-      k_mxg<DT, BLK, MATS, false, kMxgWaves, 128><<<(unsigned)(tiles_m * tiles_n), 64 * kMxgWaves, 0, st>>>(
-          p, nullptr, tiles_m, tiles_n);
+    const bool wide = mxg_wide(1, tiles_m, p.N, MATS);
+    const int tiles_n = wide ? (p.N + 256 / MATS - 1) / (256 / MATS) : (p.N + 128 / MATS - 1) / (128 / MATS);
+    const unsigned grid = (unsigned)(tiles_m * tiles_n);
+    if constexpr (MATS == 1) {
+      if (p.terms == 2) {
+        if (wide)
+          k_mxg<DT, BLK, 1, false, kMxgWaves, 256, false, 2><<<grid, 64 * kMxgWaves, 0, st>>>(
+              p, nullptr, tiles_m, tiles_n);
+        else
+          k_mxg<DT, BLK, 1, false, kMxgWaves, 128, false, 2><<<grid, 64 * kMxgWaves, 0, st>>>(
+              p, nullptr, tiles_m, tiles_n);
+        return hip_status(hipGetLastError(), "mxg launch");
+      }
     }
+    if (wide)
+      k_mxg<DT, BLK, MATS, false, kMxgWaves, 256><<<grid, 64 * kMxgWaves, 0, st>>>(p, nullptr,
+                                                                                  tiles_m, tiles_n);
+    else
+      k_mxg<DT, BLK, MATS, false, kMxgWaves, 128><<<grid, 64 * kMxgWaves, 0, st>>>(p, nullptr,
+                                                                                  tiles_m, tiles_n);
   } else {
     return p.mpad <= 16 ? launch_small<DT, BLK, MATS, 1>(p, st) : launch_small<DT, BLK, MATS, 2>(p, st);
   }
@@ -1107,6 +1138,9 @@ Status launch_t(const MxgArgs& p, int bm, hipStream_t st) {
 
 template <int MATS>
 Status launch_m(const MxgArgs& p, int dtype, bool blk, int bm, hipStream_t st) {
+  if (p.terms != 2 && p.terms != kTerms) return Status::err(kInvalid, "mxg: terms must be 2 or 3");
+  if (MATS == 2 && p.terms != kTerms)
+    return Status::err(kUnsupported, "mxg: two activation terms are for one-matrix products");
   switch (dtype) {
   case kE4M3: return blk ? launch_t<kE4M3, true, MATS>(p, bm, st) : launch_t<kE4M3, false, MATS>(p, bm, st);
   case kE5M2: return blk ? launch_t<kE5M2, true, MATS>(p, bm, st) : launch_t<kE5M2, false, MATS>(p, bm, st);
@@ -1137,7 +1171,8 @@ size_t split_bytes(int M, int kpad) {
 }
 
 Status launch_split(const float* x, int x_stride, int M, int cols, int kpad, uint8_t* buf,
-                    hipStream_t st) {
+                    hipStream_t st, int terms) {
+  if (terms != 2 && terms != kTerms) return Status::err(kInvalid, "split: terms must be 2 or 3");
   if (kpad % 128 != 0) return Status::err(kInvalid, "split: kpad must be a multiple of 128");
   const int mpad = (int)round_up(M, mxg_block_m(M));
   uint8_t* a = buf;
@@ -1145,41 +1180,66 @@ Status launch_split(const float* x, int x_stride, int M, int cols, int kpad, uin
   const int64_t waves = (int64_t)(mpad / 16) * (kpad / 128);
   const unsigned grid = (unsigned)((waves + kThreads / 64 - 1) / (kThreads / 64));
   const bool vec = x_stride % 4 == 0 && cols % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
-  if (vec) k_split<true><<<grid, kThreads, 0, st>>>(x, x_stride, M, cols, mpad, kpad, a, as, nullptr);
-  else k_split<false><<<grid, kThreads, 0, st>>>(x, x_stride, M, cols, mpad, kpad, a, as, nullptr);
+  if (terms == 2) {
+    if (vec) k_split<true, 2><<<grid, kThreads, 0, st>>>(x, x_stride, M, cols, mpad, kpad, a, as, nullptr);
+    else k_split<false, 2><<<grid, kThreads, 0, st>>>(x, x_stride, M, cols, mpad, kpad, a, as, nullptr);
+  } else {
+    if (vec) k_split<true, kTerms><<<grid, kThreads, 0, st>>>(x, x_stride, M, cols, mpad, kpad, a, as, nullptr);
+    else k_split<false, kTerms><<<grid, kThreads, 0, st>>>(x, x_stride, M, cols, mpad, kpad, a, as, nullptr);
+  }
   return hip_status(hipGetLastError(), "split launch");
 }
 
 Status launch_split_group(const SplitJob* jobs, int n, bool vec, int x_stride, int M, int cols,
-                          int kpad, hipStream_t st) {
+                          int kpad, hipStream_t st, int terms) {
+  if (terms != 2 && terms != kTerms) return Status::err(kInvalid, "split: terms must be 2 or 3");
   if (n <= 0 || !jobs) return Status::err(kInvalid, "split group: no members");
   if (kpad % 128 != 0) return Status::err(kInvalid, "split: kpad must be a multiple of 128");
   const int mpad = (int)round_up(M, mxg_block_m(M));
   const int64_t waves = (int64_t)(mpad / 16) * (kpad / 128);
   const dim3 grid((unsigned)((waves + kThreads / 64 - 1) / (kThreads / 64)), (unsigned)n);
-  if (vec) k_split<true><<<grid, kThreads, 0, st>>>(nullptr, x_stride, M, cols, mpad, kpad, nullptr, nullptr, jobs);
-  else k_split<false><<<grid, kThreads, 0, st>>>(nullptr, x_stride, M, cols, mpad, kpad, nullptr, nullptr, jobs);
+  if (terms == 2) {
+    if (vec) k_split<true, 2><<<grid, kThreads, 0, st>>>(nullptr, x_stride, M, cols, mpad, kpad, nullptr, nullptr, jobs);
+    else k_split<false, 2><<<grid, kThreads, 0, st>>>(nullptr, x_stride, M, cols, mpad, kpad, nullptr, nullptr, jobs);
+  } else {
+    if (vec) k_split<true, kTerms><<<grid, kThreads, 0, st>>>(nullptr, x_stride, M, cols, mpad, kpad, nullptr, nullptr, jobs);
+    else k_split<false, kTerms><<<grid, kThreads, 0, st>>>(nullptr, x_stride, M, cols, mpad, kpad, nullptr, nullptr, jobs);
+  }
   return hip_status(hipGetLastError(), "split group launch");
 }
 
 template <int DT, bool BLK, int MATS>
 Status launch_group_t(const MxgArgs* tab, const MxgArgs& p, int n, hipStream_t st) {
   const int tiles_m = p.mpad / kBM;
-  if (mxg_wide(n, tiles_m, p.N, MATS)) {
-    const int tiles_n = (p.N + 256 / MATS - 1) / (256 / MATS);
-    k_mxg<DT, BLK, MATS, true, kMxgWaves, 256><<<(unsigned)(n * tiles_m * tiles_n), 64 * kMxgWaves, 0, st>>>(
-        p, tab, tiles_m, tiles_n);
-  } else {
-    const int tiles_n = (p.N + 128 / MATS - 1) / (128 / MATS);
-    k_mxg<DT, BLK, MATS, true, kMxgWaves, 128><<<(unsigned)(n * tiles_m * tiles_n), 64 * kMxgWaves, 0, st>>>(
-        p, tab, tiles_m, tiles_n);
+  const bool wide = mxg_wide(n, tiles_m, p.N, MATS);
+  const int tiles_n = wide ? (p.N + 256 / MATS - 1) / (256 / MATS) : (p.N + 128 / MATS - 1) / (128 / MATS);
+  const unsigned grid = (unsigned)(n * tiles_m * tiles_n);
+  if constexpr (MATS == 1) {
+    if (p.terms == 2) {
+      if (wide)
+        k_mxg<DT, BLK, 1, true, kMxgWaves, 256, false, 2><<<grid, 64 * kMxgWaves, 0, st>>>(
+            p, tab, tiles_m, tiles_n);
+      else
+        k_mxg<DT, BLK, 1, true, kMxgWaves, 128, false, 2><<<grid, 64 * kMxgWaves, 0, st>>>(
+            p, tab, tiles_m, tiles_n);
+      return hip_status(hipGetLastError(), "mxg group launch");
+    }
   }
+  if (wide)
+    k_mxg<DT, BLK, MATS, true, kMxgWaves, 256><<<grid, 64 * kMxgWaves, 0, st>>>(p, tab, tiles_m,
+                                                                               tiles_n);
+  else
+    k_mxg<DT, BLK, MATS, true, kMxgWaves, 128><<<grid, 64 * kMxgWaves, 0, st>>>(p, tab, tiles_m,
+                                                                               tiles_n);
   return hip_status(hipGetLastError(), "mxg group launch");
 }
 
 Status launch_mxg_group(const MxgArgs* tab, const MxgArgs& p, int n, int dtype, bool blk,
                         hipStream_t st) {
   if (n <= 0 || !tab) return Status::err(kInvalid, "mxg group: no members");
+  if (p.terms != 2 && p.terms != kTerms) return Status::err(kInvalid, "mxg: terms must be 2 or 3");
+  if (p.mats == 2 && p.terms != kTerms)
+    return Status::err(kUnsupported, "mxg: two activation terms are for one-matrix products");
   if (mxg_block_m(p.M) != kBM || p.mpad % kBM != 0 || p.kpad % 256 != 0)
     return Status::err(kInvalid, "mxg group: needs the large-tile layout");
   if ((size_t)kTerms * p.mpad * p.kpad >= (1ull << 31) ||
