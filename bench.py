@@ -56,6 +56,7 @@ C2_BYTES = 16826368
 # rocprof summaries (kernel stats + FETCH_SIZE/WRITE_SIZE scaled by a copy of
 # known size) per workload; `traffic_bytes:` is the measured HBM bytes per launch.
 PROFILES = {"c2": "gemv_fp8e4m3_rowscale_4096x4096_b1.txt",
+            "read_floor": "read_floor_16826368B.txt",
             "c2bwd": "dense_backward_4096x4096_fp8e4m3_rowscale_b1.txt"}
 
 
@@ -678,7 +679,7 @@ def main():
         value, unit = gbs, "GB/s"
         roof = {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(gbs / HBM_PEAK_GBS, 4),
-                "traffic": None if args.read_floor else measured_traffic(args.config)}
+                "traffic": measured_traffic("read_floor" if args.read_floor else args.config)}
     else:
         value, unit = tflops, "TFLOP/s"
         roof = {"bound": "mfma", "achieved": round(tflops, 3), "peak": MFMA_FP8_PEAK_TFLOPS,
