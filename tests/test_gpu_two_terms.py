@@ -25,7 +25,7 @@ TOL_TWO = 1e-3
 
 @pytest.mark.parametrize("dt,scheme", [(4, 2), (16, 3), (5, 1)])
 @pytest.mark.parametrize("rows,K,N", [(20, 1024, 2048), (64, 1024, 1024), (300, 700, 513),
-                                      (1024, 4096, 1024)])
+                                      (1024, 4096, 1024), (2048, 256, 4096)])
 def test_two_terms_dense_within_contract(gpu, oracle, dt, scheme, rows, K, N):
     rng = np.random.default_rng(rows + K + N + dt)
     W = (rng.standard_normal((N, K)) / np.sqrt(K)).astype(np.float32)
@@ -58,11 +58,12 @@ def test_two_terms_batch_up_to_four_and_one_unchanged(gpu):
         b.close()
 
 
-def test_two_terms_grouped_chain(gpu, oracle):
-    """16 cells x 3 layers (E4M3 row, FP4 E8M0, E4M3 row) at 256 rows, grouped
-    and chained through the epilogue split, every layer within the bound on
-    the GPU's own input."""
-    cells, batch, d = 16, 256, 1024
+@pytest.mark.parametrize("batch", [256, 512])
+def test_two_terms_grouped_chain(gpu, oracle, batch):
+    """16 cells x 3 layers (E4M3 row, FP4 E8M0, E4M3 row) at 256 and 512
+    rows (128-row and 256-row tiles), grouped and chained through the epilogue
+    split, every layer within the bound on the GPU's own input."""
+    cells, d = 16, 1024
     kinds = [(4, 2), (16, 3), (4, 2)]
     hip = gpu.Hip()
     sessions, bufs, Ws, xs = [], [], [], []
