@@ -139,6 +139,28 @@ void or_sgd(int64_t n, const float* w, const float* dW, double lr, float* next);
 void or_swiglu_bwd_product(const float* g, const float* u, const float* gh, float* d_up,
                            float* d_gate, int64_t n);
 
+/* --- packed block formats (QuantFormat): oracle/formats.c -----------------
+ * The reference reserves the enum (include/welvet/weights.hpp:12-15) and lists
+ * the formats (README.md:361-383) without implementing them; restated from
+ * ggml's published block layouts and rules (ggml-common.h, ggml-quants.c).
+ * Pinned by: IEEE half conversions against numpy's float16; closed-form blocks
+ * (grid values reproduced exactly, known scales, the nibble and high-bit
+ * positions of single set codes); the quantizers' error bounds and
+ * idempotence on their own grids. Parity against ggml itself: unpinned (no
+ * ggml output is in the image). */
+enum { OR_FMT_Q8_0 = 1, OR_FMT_Q4_0 = 2, OR_FMT_Q4_1 = 3, OR_FMT_Q5_0 = 4, OR_FMT_Q5_1 = 5,
+       OR_FMT_Q4_K = 8, OR_FMT_Q5_K = 9, OR_FMT_Q6_K = 10 };
+float or_f16_to_f32(uint16_t h);
+uint16_t or_f32_to_f16(float f);
+/* elements per block (32 or 256) and packed bytes per block; 0 unsupported */
+int or_fmt_block_elems(int fmt);
+int or_fmt_block_bytes(int fmt);
+/* n elements (a multiple of 32) of row-major x -> n / 32 packed blocks.
+ * Q8_0, Q4_0, Q4_1, Q5_0, Q5_1 only (the reference quantizers); -1 otherwise. */
+int or_fmt_quantize(int fmt, int64_t n, const float* x, uint8_t* out);
+/* n elements (a multiple of the block) of packed blocks -> f32; -1 on error. */
+int or_fmt_dequant(int fmt, int64_t n, const uint8_t* in, float* out);
+
 /* --- CPU baseline timing (reported beside the GPU) ---------------------------
  * Mount: decode codes to an f64 row-major W (src/layers/dense/dense.cpp:28-39).
  * Execute: or_dense semantics with f64 W, rows split over nthreads.

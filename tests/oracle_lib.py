@@ -57,6 +57,18 @@ class Oracle:
         L.or_cpu_dense_bench.restype = ctypes.c_double
         L.or_cpu_dense_bench.argtypes = [_i, _i, _i, _i, _i, _u8p, _fp, _u8p, _fp, _fp, _i, _i, _i,
                                          _dp]
+        L.or_f16_to_f32.restype = ctypes.c_float
+        L.or_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.or_f32_to_f16.restype = ctypes.c_uint16
+        L.or_f32_to_f16.argtypes = [ctypes.c_float]
+        L.or_fmt_block_elems.restype = _i
+        L.or_fmt_block_elems.argtypes = [_i]
+        L.or_fmt_block_bytes.restype = _i
+        L.or_fmt_block_bytes.argtypes = [_i]
+        L.or_fmt_quantize.restype = _i
+        L.or_fmt_quantize.argtypes = [_i, ctypes.c_int64, _fp, _u8p]
+        L.or_fmt_dequant.restype = _i
+        L.or_fmt_dequant.argtypes = [_i, ctypes.c_int64, _u8p, _fp]
         self.L = L
 
     def encode(self, dtype, x):
@@ -174,3 +186,28 @@ class Oracle:
         d_up, d_gate = np.zeros_like(g), np.zeros_like(g)
         self.L.or_swiglu_bwd_product(_f(g), _f(u), _f(gh), _f(d_up), _f(d_gate), g.size)
         return d_up, d_gate
+
+    # --- packed block formats (oracle/formats.c) ---
+    def f32_to_f16(self, x):
+        return np.array([self.L.or_f32_to_f16(float(v)) for v in np.asarray(x, np.float32).ravel()],
+                        np.uint16)
+
+    def f16_to_f32(self, h):
+        return np.array([self.L.or_f16_to_f32(int(v)) for v in np.asarray(h, np.uint16).ravel()],
+                        np.float32)
+
+    def fmt_block(self, fmt):
+        return self.L.or_fmt_block_elems(fmt), self.L.or_fmt_block_bytes(fmt)
+
+    def fmt_quantize(self, fmt, W):
+        W = np.ascontiguousarray(W, np.float32)
+        qk, bb = self.fmt_block(fmt)
+        out = np.zeros(W.size // qk * bb, np.uint8)
+        assert self.L.or_fmt_quantize(fmt, W.size, _f(W), _u8(out)) == 0
+        return out
+
+    def fmt_dequant(self, fmt, blocks, shape):
+        blocks = np.ascontiguousarray(blocks, np.uint8)
+        out = np.zeros(shape, np.float32)
+        assert self.L.or_fmt_dequant(fmt, out.size, _u8(blocks), _f(out)) == 0
+        return out
