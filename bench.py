@@ -25,6 +25,8 @@ Other workloads (--config), each its own line:
   c5     64 cells x (Dense 1024^2 E4M3 row -> FP4 block-32 -> E4M3 row), batch 256
   c5chain  the same cells as the reference's volume: one 192-layer serial chain (model session)
   c2bwd  Dense backward at the GEMV shape: d_pre, dX = W^T d_pre, dW (4096^2 E4M3 per-row, batch 1)
+  gemv_<fmt>  the c2 GEMV shape over a packed block format (q8_0, q4_0, q4_1, q5_0, q5_1,
+         q4_k, q5_k, q6_k; bytes = packed blocks + x + y)
 --read-floor BYTES instead times one streaming read of BYTES (default: the c2
 step's 16,826,368) over 64 rotated buffers, the same way: the floor for any
 kernel that reads those bytes once.
@@ -190,6 +192,68 @@ def dense_workload(pw, hip, name, cfg_id, dtype, scheme, batch, K, N, copies, bo
             "config": {"workload": name, "in": K, "out": N, "batch": batch, "scale": sname,
                        "weight_copies_rotated": copies},
             "cpu": cpu, "close": close}
+
+
+FORMATS = {"q8_0": (1, 32, 34), "q4_0": (2, 32, 18), "q4_1": (3, 32, 20), "q5_0": (4, 32, 22),
+           "q5_1": (5, 32, 24), "q4_k": (8, 256, 144), "q5_k": (9, 256, 176),
+           "q6_k": (10, 256, 210)}
+
+
+def format_blocks(fmt, qk, bb, N, K, seed):
+    """Valid packed blocks of random codes with f16 scales near 1/sqrt(K)/8
+    (the K formats: mounted from blocks, the reference quantizers of those
+    formats being a search that is not built here)."""
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    nb = N * K // qk
+    raw = rng.integers(0, 256, size=(nb, bb), dtype=np.uint8)
+    d = (rng.uniform(0.5, 1.5, nb) / np.sqrt(K) / 8).astype(np.float32)
+    if fmt in (8, 9):
+        raw[:, 0:2] = (d / 32).astype(np.float16).view(np.uint8).reshape(nb, 2)
+        raw[:, 2:4] = (d / 64).astype(np.float16).view(np.uint8).reshape(nb, 2)
+    else:
+        raw[:, 208:210] = (d / 64).astype(np.float16).view(np.uint8).reshape(nb, 2)
+    return raw.reshape(-1)
+
+
+def format_workload(pw, hip, name, fmt_name, batch, K, N, copies):
+    """GEMV over a packed block format (welvet_dense_mount_format): the
+    32-element formats quantized on the device from N(0, 1/sqrt(K)) weights,
+    the K formats mounted from valid packed blocks of random codes."""
+    import numpy as np
+
+    fmt, qk, bb = FORMATS[fmt_name]
+    seed = pw.seed_for(2)
+    x = pw.normal(seed + 500, batch * K).reshape(batch, K)
+    if qk == 32:
+        W = pw.normal(seed, N * K, 1 / np.sqrt(K)).reshape(N, K)
+        sessions = [pw.FormatDenseSession(batch, K, N, -1, fmt, W=W) for _ in range(copies)]
+    else:
+        blocks = format_blocks(fmt, qk, bb, N, K, seed)
+        sessions = [pw.FormatDenseSession(batch, K, N, -1, fmt, blocks=blocks)
+                    for _ in range(copies)]
+    dx = hip.upload(x)
+    dy = hip.malloc(batch * N * 4)
+    nbytes = N * K // qk * bb + 4 * batch * K + 4 * batch * N
+
+    def enqueue(i, stream):
+        sessions[i % copies].execute_device(dx, dy, dy, stream)
+
+    def close():
+        for s in sessions:
+            s.close()
+        hip.free(dx)
+        hip.free(dy)
+
+    return {"desc": name, "enqueue": enqueue, "per_graph": copies, "bytes": nbytes,
+            "flops": 2 * batch * N * K, "bound": "hbm", "dtype": fmt_name,
+            "config": {"workload": name, "in": K, "out": N, "batch": batch,
+                       "format": fmt_name.upper(), "packed_bytes": N * K // qk * bb,
+                       "weight_copies_rotated": copies,
+                       "cpu_baseline": "none: the reference has no implementation of this "
+                                       "format (README.md:361-383)"},
+            "cpu": None, "close": close}
 
 
 def swiglu_workload(pw, hip, name, batch, copies):
@@ -493,6 +557,9 @@ def make_workload(pw, hip, config, copies, terms=3):
     if config == "c5chain":
         return chain_workload(pw, hip, "volume_grid_4x4x4_stack3_dense_1024_b256_serial"
                               + ("_2terms" if two else ""), two)
+    if config.startswith("gemv_"):
+        f = config[len("gemv_"):]
+        return format_workload(pw, hip, f"dense_gemv_4096x4096_{f}_b1", f, 1, 4096, 4096, copies)
     if config == "c5":
         return cells_workload(pw, hip, "volume_64_cells_3x_dense_1024_b256"
                               + ("_2terms" if two else ""), two)
@@ -544,7 +611,8 @@ def read_floor_workload(pw, hip, nbytes, copies):
             "cpu": None, "close": close}
 
 
-CONFIGS = ["c1", "c2", "c3", "c3b16", "c4", "c4mha", "c5", "c5chain", "c2bwd"]
+CONFIGS = ["c1", "c2", "c3", "c3b16", "c4", "c4mha", "c5", "c5chain", "c2bwd"] + [
+    "gemv_" + f for f in FORMATS]
 
 
 class Runner:

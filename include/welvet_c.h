@@ -142,6 +142,31 @@ WELVET_API welvet_status welvet_dense_export_store(welvet_dense_session* sess, u
                                                    float* row_scale, uint8_t* blk_exp,
                                                    float* tensor_scale);
 
+/* Dense session over a packed block format (QuantFormat). The reference
+ * reserves the enum (include/welvet/weights.hpp:12-15) and lists the formats
+ * (README.md:361-383) without implementing any; this is the mount that a
+ * binding of those values would call. format: 1 Q8_0, 2 Q4_0, 3 Q4_1,
+ * 4 Q5_0, 5 Q5_1, 8 Q4_K, 9 Q5_K, 10 Q6_K (ggml's block layouts); the other
+ * values of the table (6, 7, 11-20) return code 3. Exactly one of W_init
+ * (fp32 [out*in], quantized on the device; the five 32-element formats) and
+ * blocks (the packed row-major blocks, blocks_len bytes; every built format)
+ * is given; in must be a multiple of the block (32, or 256 for Q4_K, Q5_K,
+ * Q6_K). Execute, execute_device, execute_noalloc and release are those of
+ * welvet_dense_session; backward and the grouped calls return an error. */
+WELVET_API welvet_status welvet_dense_mount_format(int32_t batch, int32_t in, int32_t out,
+                                                   int32_t act, int32_t format,
+                                                   const float* W_init, const uint8_t* blocks,
+                                                   size_t blocks_len, const double* bias,
+                                                   size_t bias_len,
+                                                   welvet_dense_session** sess_out);
+/* The packed blocks of a format session (cap bytes available; *len set). */
+WELVET_API welvet_status welvet_dense_export_blocks(welvet_dense_session* sess, uint8_t* blocks,
+                                                    size_t cap, size_t* len);
+/* A Dense session's weights dequantized to fp32 [out*in] host memory (the
+ * role of WeightStore::export_f32, reference src/weights/store.cpp:42-71):
+ * codes times row scales and E8M0 factors, or the format's dequantization. */
+WELVET_API welvet_status welvet_dense_export_f32(welvet_dense_session* sess, float* W);
+
 /* Grouped execution of Dense sessions of one shape (no counterpart in the
  * reference; for the independent cells of a volume): every session must have
  * the same batch, in, out, activation, dtype and scheme. x[i], pre[i],

@@ -151,6 +151,59 @@ welvet_status welvet_dense_mount_q(int32_t batch, int32_t in, int32_t out, int32
   return dense_mount(batch, in, out, act, dtype, backend, W_init, bias, bias_len, sess_out);
 }
 
+welvet_status welvet_dense_mount_format(int32_t batch, int32_t in, int32_t out, int32_t act,
+                                        int32_t format, const float* W_init,
+                                        const uint8_t* blocks, size_t blocks_len,
+                                        const double* bias, size_t bias_len,
+                                        welvet_dense_session** sess_out) {
+  if (!sess_out) return invalid("null mount args");
+  *sess_out = nullptr;
+  if (batch <= 0 || in <= 0 || out <= 0) return invalid("bad dims");
+  return guarded([&]() -> Status {
+    WV_TRY(wv::init_device());
+    auto* s = new welvet_dense_session();
+    Status st = s->stream.create();
+    if (st) st = wv::dense_build_format(in, out, act, format, W_init, blocks, blocks_len, bias,
+                                        bias_len, &s->layer, s->stream.s);
+    if (st) st = s->x.alloc((size_t)batch * in * sizeof(float));
+    if (st) st = s->pre.alloc((size_t)batch * out * sizeof(float));
+    if (st) st = s->post.alloc((size_t)batch * out * sizeof(float));
+    if (!st) {
+      delete s;
+      return st;
+    }
+    s->batch = batch;
+    *sess_out = s;
+    return Status::ok();
+  });
+}
+
+welvet_status welvet_dense_export_blocks(welvet_dense_session* s, uint8_t* blocks, size_t cap,
+                                         size_t* len) {
+  if (!s) return invalid("null session");
+  if (!s->layer.format) return to_c(Status::err(wv::kUnsupported, "not a packed block format session"));
+  const std::vector<uint8_t>& b = s->layer.fw.blocks;
+  if (len) *len = b.size();
+  if (blocks) {
+    if (cap < b.size()) return invalid("block buffer too small");
+    std::memcpy(blocks, b.data(), b.size());
+  }
+  return to_c(Status::ok());
+}
+
+welvet_status welvet_dense_export_f32(welvet_dense_session* s, float* W) {
+  if (!s || !W) return invalid("null export args");
+  return guarded([&]() -> Status {
+    const size_t n = (size_t)s->layer.in * s->layer.out;
+    wv::DevBuf w;
+    WV_TRY(w.alloc(n * sizeof(float)));
+    WV_TRY(wv::dense_export_f32(s->layer, w.as<float>(), s->stream.s));
+    WV_TRY(wv::copy_d2h(W, w.p, n * sizeof(float), s->stream.s));
+    WV_HIP(hipStreamSynchronize(s->stream.s));
+    return Status::ok();
+  });
+}
+
 welvet_status welvet_dense_execute(welvet_dense_session* s, const float* x, float* pre,
                                    float* post) {
   if (!s || !x || !pre || !post) return invalid("null execute args");
@@ -312,6 +365,9 @@ welvet_status welvet_dense_export_store(welvet_dense_session* s, uint8_t* native
                                         size_t native_cap, size_t* native_len, float* row_scale,
                                         uint8_t* blk_exp, float* tensor_scale) {
   if (!s) return invalid("null session");
+  if (s->layer.format)
+    return to_c(Status::err(wv::kUnsupported, "packed block format session: use "
+                                              "welvet_dense_export_blocks"));
   const wv::WeightStore& w = s->layer.store;
   if (native_len) *native_len = w.native.size();
   if (native) {

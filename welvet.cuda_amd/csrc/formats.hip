@@ -1,0 +1,593 @@
+// Packed block weight formats (QuantFormat): mount-time quantize and
+// relayout, dequantization, and the batch-row GEMV over the resident layout.
+//
+// The reference reserves the QuantFormat enum (include/welvet/weights.hpp:
+// 12-15) and lists the formats (README.md:361-383) without implementing any.
+// The packed blocks here are ggml's published layouts (block_q8_0 ..
+// block_q6_K of ggml-common.h; quantize_row_*_ref and dequantize_row_* of
+// ggml-quants.c), the interchange format a caller mounts and exports.
+//
+// Resident layout. The packed blocks are split at mount into per-row arrays
+// of 32-element sub-blocks, so that a lane's share of one sub-block is one
+// aligned 16-byte code load plus small aligned side loads:
+//   q  codes: 16 bytes per sub-block, byte l holding element l in the low
+//      nibble and element l + 16 in the high one (Q8_0: 32 int8, in order);
+//   h  high bits: Q5_0/Q5_1/Q5_K one dword (bit e = bit 4 of element e),
+//      Q6_K 8 bytes (bits 2e, 2e + 1 = bits 4-5 of element e);
+//   s  scales: Q8_0/Q4_0/Q5_0 f16 d; Q4_1/Q5_1 f16 d then f16 m; Q4_K/Q5_K
+//      the super-block's 16-byte header (f16 d, f16 dmin, 12 scale bytes),
+//      2 bytes per sub-block; Q6_K the sub-block's two int8 scales;
+//   e  Q6_K only: the super-block's f16 d.
+// Every array holds exactly the packed bytes of its part, so a GEMV reads
+// the packed size (plus x and y). Rows are padded to a multiple of 16 with
+// zero bytes (zero scales: padding rows read as 0).
+#include "common.h"
+#include "kernels.h"
+
+namespace wv {
+
+namespace {
+
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ uint16_t ld16(const uint8_t* p) {
+  return (uint16_t)(p[0] | (p[1] << 8));
+}
+__device__ __forceinline__ void st16(uint8_t* p, uint16_t v) {
+  p[0] = (uint8_t)v;
+  p[1] = (uint8_t)(v >> 8);
+}
+__device__ __forceinline__ float f16f(uint16_t h) {
+  return (float)__builtin_bit_cast(_Float16, h);
+}
+// binary32 -> binary16 bits, round to nearest even, overflow to infinity,
+// NaN to the quiet NaN 0x7E00, in integer operations on the bit pattern.
+// (A plain (_Float16) conversion of d = max * -0.125 is folded by the
+// compiler into v_fma_mix with a +0 addend, which turns d = -0 into +0.)
+__device__ __forceinline__ uint16_t f16b(float f) {
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t s = (u >> 16) & 0x8000u;
+  const uint32_t a = u & 0x7FFFFFFFu;
+  if (a > 0x7F800000u) return (uint16_t)(s | 0x7E00u);
+  if (a >= 0x47800000u) return (uint16_t)(s | 0x7C00u);
+  const int e = (int)(a >> 23) - 127;
+  if (e < -14) {
+    if (e < -25) return (uint16_t)s;
+    const uint32_t m = (a & 0x7FFFFFu) | 0x800000u;
+    const int shift = -e - 1;  // to units of 2^-24
+    const uint32_t q = m >> shift, rem = m & ((1u << shift) - 1), half = 1u << (shift - 1);
+    return (uint16_t)(s | (q + (rem > half || (rem == half && (q & 1u)))));
+  }
+  uint32_t q = ((uint32_t)(e + 15) << 10) | ((a & 0x7FFFFFu) >> 13);
+  const uint32_t rem = a & 0x1FFFu;
+  if (rem > 0x1000u || (rem == 0x1000u && (q & 1u))) ++q;
+  return (uint16_t)(s | q);
+}
+
+// ---- quantizers (ggml-quants.c quantize_row_*_ref), one thread per block.
+// Plain f32 arithmetic, no contraction, in the order written: the bytes
+// equal those of the C restatement.
+template <int FMT>
+__device__ void quantize_block(const float* __restrict__ x, uint8_t* __restrict__ y) {
+#pragma clang fp contract(off)
+  if constexpr (FMT == kQ8_0) {
+    float amax = 0.0f;
+    for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(x[j]));
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    st16(y, f16b(d));
+    for (int j = 0; j < 32; ++j) y[2 + j] = (uint8_t)(int8_t)roundf(x[j] * id);
+  } else if constexpr (FMT == kQ4_0 || FMT == kQ5_0) {
+    // d = max / -2^(bits - 1), max the element of largest magnitude
+    float amax = 0.0f, mx = 0.0f;
+    for (int j = 0; j < 32; ++j) {
+      if (amax < fabsf(x[j])) {
+        amax = fabsf(x[j]);
+        mx = x[j];
+      }
+    }
+    constexpr float kDiv = FMT == kQ4_0 ? -8.0f : -16.0f;
+    constexpr float kOff = FMT == kQ4_0 ? 8.5f : 16.5f;
+    constexpr int kTop = FMT == kQ4_0 ? 15 : 31;
+    const float d = mx / kDiv;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    st16(y, f16b(d));
+    uint32_t qh = 0;
+    uint8_t* qs = y + (FMT == kQ4_0 ? 2 : 6);
+    for (int j = 0; j < 16; ++j) {
+      int q0 = (int8_t)(x[j] * id + kOff);
+      int q1 = (int8_t)(x[16 + j] * id + kOff);
+      q0 = q0 < kTop ? q0 : kTop;
+      q1 = q1 < kTop ? q1 : kTop;
+      qs[j] = (uint8_t)((q0 & 15) | ((q1 & 15) << 4));
+      qh |= (uint32_t)((q0 >> 4) & 1) << j;
+      qh |= (uint32_t)((q1 >> 4) & 1) << (j + 16);
+    }
+    if constexpr (FMT == kQ5_0) {
+      for (int b = 0; b < 4; ++b) y[2 + b] = (uint8_t)(qh >> (8 * b));
+    }
+  } else {
+    // Q4_1 / Q5_1: d = (max - min) / (2^bits - 1), m = min
+    float mn = 3.402823466e38f, mx = -3.402823466e38f;
+    for (int j = 0; j < 32; ++j) {
+      if (x[j] < mn) mn = x[j];
+      if (x[j] > mx) mx = x[j];
+    }
+    const float d = (mx - mn) / (FMT == kQ4_1 ? 15.0f : 31.0f);
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    st16(y, f16b(d));
+    st16(y + 2, f16b(mn));
+    uint32_t qh = 0;
+    uint8_t* qs = y + (FMT == kQ4_1 ? 4 : 8);
+    for (int j = 0; j < 16; ++j) {
+      int q0, q1;
+      if constexpr (FMT == kQ4_1) {
+        q0 = (int8_t)((x[j] - mn) * id + 0.5f);
+        q1 = (int8_t)((x[16 + j] - mn) * id + 0.5f);
+        q0 = q0 < 15 ? q0 : 15;
+        q1 = q1 < 15 ? q1 : 15;
+      } else {
+        q0 = (uint8_t)((x[j] - mn) * id + 0.5f);
+        q1 = (uint8_t)((x[16 + j] - mn) * id + 0.5f);
+      }
+      qs[j] = (uint8_t)((q0 & 15) | ((q1 & 15) << 4));
+      qh |= (uint32_t)((q0 >> 4) & 1) << j;
+      qh |= (uint32_t)((q1 >> 4) & 1) << (j + 16);
+    }
+    if constexpr (FMT == kQ5_1) {
+      for (int b = 0; b < 4; ++b) y[4 + b] = (uint8_t)(qh >> (8 * b));
+    }
+  }
+}
+
+template <int FMT>
+__global__ __launch_bounds__(kThreads) void k_fmt_quantize(const float* __restrict__ W,
+                                                           int64_t nblocks,
+                                                           uint8_t* __restrict__ out) {
+  constexpr FmtGeom G = fmt_geom(FMT);
+  const int64_t b = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (b >= nblocks) return;
+  float x[32];
+  for (int j = 0; j < 32; ++j) x[j] = W[b * 32 + j];
+  quantize_block<FMT>(x, out + b * G.bb);
+}
+
+// ---- relayout: one thread per (row, 32-element sub-block) ----------------
+template <int FMT>
+__global__ __launch_bounds__(kThreads) void k_fmt_relayout(FmtArgs a, const uint8_t* __restrict__ blocks,
+                                                           int rows) {
+  constexpr FmtGeom G = fmt_geom(FMT);
+  constexpr int SPB = G.qk / 32;  // sub-blocks per block
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= (int64_t)rows * a.nsub) return;
+  const int row = (int)(i / a.nsub), t = (int)(i % a.nsub);
+  const int sb = t % SPB;
+  const uint8_t* B = blocks + ((size_t)row * (a.nsub / SPB) + t / SPB) * G.bb;
+  uint8_t* q = const_cast<uint8_t*>(a.q) + ((size_t)row * a.nsub + t) * G.qb;
+  uint8_t* s = const_cast<uint8_t*>(a.s) + ((size_t)row * a.nsub + t) * G.sb;
+  uint8_t* h = G.hb ? const_cast<uint8_t*>(a.h) + ((size_t)row * a.nsub + t) * G.hb : nullptr;
+  if constexpr (FMT == kQ8_0) {
+    for (int j = 0; j < 32; ++j) q[j] = B[2 + j];
+    s[0] = B[0], s[1] = B[1];
+  } else if constexpr (FMT == kQ4_0 || FMT == kQ4_1 || FMT == kQ5_0 || FMT == kQ5_1) {
+    constexpr int QS = FMT == kQ4_0 ? 2 : FMT == kQ4_1 ? 4 : FMT == kQ5_0 ? 6 : 8;
+    for (int j = 0; j < 16; ++j) q[j] = B[QS + j];
+    for (int j = 0; j < G.sb; ++j) s[j] = B[j];
+    if constexpr (G.hb) {
+      constexpr int QH = FMT == kQ5_0 ? 2 : 4;
+      for (int j = 0; j < 4; ++j) h[j] = B[QH + j];
+    }
+  } else if constexpr (FMT == kQ4_K || FMT == kQ5_K) {
+    // sub-block sb = 2i + n: nibble n of qs[32 i + e]; Q5_K: bit sb of qh[e]
+    constexpr int QS = FMT == kQ5_K ? 48 : 16;
+    const int i4 = sb / 2, n = sb % 2;
+    for (int l = 0; l < 16; ++l) {
+      const int lo = (B[QS + 32 * i4 + l] >> (4 * n)) & 15;
+      const int hi = (B[QS + 32 * i4 + l + 16] >> (4 * n)) & 15;
+      q[l] = (uint8_t)(lo | (hi << 4));
+    }
+    s[0] = B[2 * sb], s[1] = B[2 * sb + 1];  // this sub-block's two header bytes
+    if constexpr (FMT == kQ5_K) {
+      uint32_t bits = 0;
+      for (int e = 0; e < 32; ++e) bits |= (uint32_t)((B[16 + e] >> sb) & 1) << e;
+      for (int j = 0; j < 4; ++j) h[j] = (uint8_t)(bits >> (8 * j));
+    }
+  } else {
+    // Q6_K: sub-block sb = 4 n + t of half n: low 4 bits from nibble t >> 1
+    // of ql[64 n + 32 (t & 1) + e], bits 4-5 from bits 2t, 2t + 1 of
+    // qh[32 n + e]; scales sc[2 sb], sc[2 sb + 1]
+    const int n = sb / 4, tt = sb % 4;
+    for (int l = 0; l < 16; ++l) {
+      const int lo = (B[64 * n + 32 * (tt & 1) + l] >> (4 * (tt >> 1))) & 15;
+      const int hi = (B[64 * n + 32 * (tt & 1) + l + 16] >> (4 * (tt >> 1))) & 15;
+      q[l] = (uint8_t)(lo | (hi << 4));
+    }
+    for (int j = 0; j < 8; ++j) {
+      uint8_t v = 0;
+      for (int k = 0; k < 4; ++k) v |= (uint8_t)(((B[128 + 32 * n + 4 * j + k] >> (2 * tt)) & 3) << (2 * k));
+      h[j] = v;
+    }
+    s[0] = B[192 + 2 * sb], s[1] = B[192 + 2 * sb + 1];
+    if (sb == 0) {
+      uint8_t* e = const_cast<uint8_t*>(a.e) + ((size_t)row * (a.nsub / SPB) + t / SPB) * 2;
+      e[0] = B[208], e[1] = B[209];
+    }
+  }
+}
+
+// ---- decode of one lane's sub-block into 32 f32 code values ---------------
+// c[e] = the integer the format multiplies by its scale for element e (the
+// offset of the symmetric formats already removed).
+template <int FMT>
+__device__ __forceinline__ void decode_codes(const uint4 w0, const uint4 w1, uint32_t hb0,
+                                             uint32_t hb1, float* c) {
+  const uint32_t w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+  if constexpr (FMT == kQ8_0) {
+#pragma unroll
+    for (int d = 0; d < 8; ++d)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) c[4 * d + b] = (float)(int8_t)(w[d] >> (8 * b));
+  } else {
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int e = 4 * d + b;
+        int lo = (int)((w[d] >> (8 * b)) & 15), hi = (int)((w[d] >> (8 * b + 4)) & 15);
+        if constexpr (FMT == kQ5_0 || FMT == kQ5_1 || FMT == kQ5_K) {
+          lo |= (int)((hb0 >> e) & 1) << 4;
+          hi |= (int)((hb0 >> (e + 16)) & 1) << 4;
+        }
+        if constexpr (FMT == kQ6_K) {
+          lo |= (int)((e < 16 ? (hb0 >> (2 * e)) : 0) & 3) << 4;
+          hi |= (int)((hb1 >> (2 * e)) & 3) << 4;
+        }
+        constexpr int off = FMT == kQ4_0 ? 8 : FMT == kQ5_0 ? 16 : FMT == kQ6_K ? 32 : 0;
+        c[e] = (float)(lo - off);
+        c[e + 16] = (float)(hi - off);
+      }
+  }
+}
+
+// the element-16+ high bits of Q6_K start at bit 32 of the sub-block's 8 bytes
+// (hb1 = the second dword); elements 0..15 use the first dword
+
+// scale and min of Q4_K/Q5_K sub-block j from the 12 packed scale bytes
+// (get_scale_min_k4)
+__device__ __forceinline__ void scale_min_k4(int j, const uint8_t* q, int* sc, int* m) {
+  if (j < 4) {
+    *sc = q[j] & 63;
+    *m = q[j + 4] & 63;
+  } else {
+    *sc = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+    *m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+  }
+}
+
+// The same from the header's dwords 1-3 (scale bytes 0-11 at header bytes
+// 4-15) with selects only, no indexed register array: byte k + 4 of the
+// header is byte k of the scales.
+__device__ __forceinline__ void scale_min_k4_regs(int j, uint32_t h1, uint32_t h2, uint32_t h3,
+                                                  int* sc, int* m) {
+  const int sh = 8 * (j & 3);
+  const int b1 = (int)((h1 >> sh) & 0xFF);  // scales[j & 3]
+  const int b2 = (int)((h2 >> sh) & 0xFF);  // scales[4 + (j & 3)]
+  const int b3 = (int)((h3 >> sh) & 0xFF);  // scales[8 + (j & 3)]
+  if (j < 4) {
+    *sc = b1 & 63;
+    *m = b2 & 63;
+  } else {
+    *sc = (b3 & 0xF) | ((b1 >> 6) << 4);
+    *m = (b3 >> 4) | ((b2 >> 6) << 4);
+  }
+}
+
+// ---- dequantization of the resident layout (WeightStore::export_f32's
+// role): one thread per (row, sub-block), the oracle's arithmetic ---------
+template <int FMT>
+__global__ __launch_bounds__(kThreads) void k_fmt_dequant(FmtArgs a, int rows, float* __restrict__ out) {
+#pragma clang fp contract(off)
+  constexpr FmtGeom G = fmt_geom(FMT);
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= (int64_t)rows * a.nsub) return;
+  const int row = (int)(i / a.nsub), t = (int)(i % a.nsub);
+  const uint8_t* q = a.q + ((size_t)row * a.nsub + t) * G.qb;
+  const uint8_t* s = a.s + ((size_t)row * a.nsub + t) * G.sb;
+  uint4 w0 = *reinterpret_cast<const uint4*>(q), w1 = make_uint4(0, 0, 0, 0);
+  if constexpr (FMT == kQ8_0) w1 = *reinterpret_cast<const uint4*>(q + 16);
+  uint32_t hb0 = 0, hb1 = 0;
+  if constexpr (G.hb >= 4) hb0 = *reinterpret_cast<const uint32_t*>(a.h + ((size_t)row * a.nsub + t) * G.hb);
+  if constexpr (G.hb == 8) hb1 = *reinterpret_cast<const uint32_t*>(a.h + ((size_t)row * a.nsub + t) * G.hb + 4);
+  float c[32];
+  decode_codes<FMT>(w0, w1, hb0, hb1, c);
+  float* y = out + (size_t)row * a.cols + 32 * (size_t)t;
+  if constexpr (FMT == kQ8_0 || FMT == kQ4_0 || FMT == kQ5_0) {
+    const float d = f16f(ld16(s));
+    for (int e = 0; e < 32; ++e) y[e] = c[e] * d;
+  } else if constexpr (FMT == kQ4_1 || FMT == kQ5_1) {
+    const float d = f16f(ld16(s)), m = f16f(ld16(s + 2));
+    for (int e = 0; e < 32; ++e) y[e] = c[e] * d + m;
+  } else if constexpr (FMT == kQ4_K || FMT == kQ5_K) {
+    const uint8_t* hd = a.s + ((size_t)row * a.nsub + (t & ~7)) * G.sb;  // super-block header
+    int sc, m;
+    scale_min_k4(t & 7, hd + 4, &sc, &m);
+    const float d1 = f16f(ld16(hd)) * (float)sc, m1 = f16f(ld16(hd + 2)) * (float)m;
+    for (int e = 0; e < 32; ++e) y[e] = d1 * c[e] - m1;
+  } else {
+    const float d = f16f(ld16(a.e + ((size_t)row * (a.nsub / 8) + t / 8) * 2));
+    const float s0 = d * (float)(int8_t)s[0], s1 = d * (float)(int8_t)s[1];
+    for (int e = 0; e < 16; ++e) y[e] = s0 * c[e];
+    for (int e = 16; e < 32; ++e) y[e] = s1 * c[e];
+  }
+}
+
+__device__ __forceinline__ double act_f64(int act, double x) {
+  switch (act) {
+  case kReLU: return x < 0.0 ? 0.0 : x;
+  case kSilu: return x / (1.0 + exp(-x));
+  case kGELU: {
+    const double k = 0.7978845608028654;
+    return 0.5 * x * (1.0 + tanh(k * (x + 0.044715 * x * x * x)));
+  }
+  case kTanh: return tanh(x);
+  case kSigmoid: return 1.0 / (1.0 + exp(-x));
+  case kLeaky: return x < 0.0 ? 0.01 * x : x;
+  case kReLU2: return x < 0.0 ? 0.0 : x * x;
+  default: return x;
+  }
+}
+
+__device__ __forceinline__ uint4 load_stream(const uint8_t* p) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// ---- GEMV: one workgroup of WAVES waves owns R rows; lane l of wave w takes
+// sub-block 64 c + l of every row for chunks c = w, w + WAVES, ..; its 32 x
+// values are loaded once per chunk and applied to all R rows. Per row it
+// loads the 16-byte code (32 for Q8_0) and the small side arrays, decodes to
+// integers, forms the dot product with x in f32 and applies the sub-block's
+// scale (and min) once: d * sum(c x) (+ m * sum(x)). The R per-lane partial
+// sums are reduced across the wave and then across the waves in LDS; the
+// epilogue is the Dense one (kernels.cu:147-161: bias and activation in f64).
+template <int FMT, int R, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void k_fmt_gemv(FmtArgs a) {
+  constexpr FmtGeom G = fmt_geom(FMT);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r0 = blockIdx.x * R;
+  const int nsub = a.nsub;
+  const float* __restrict__ x = a.x + (size_t)blockIdx.y * a.x_stride;
+  const int nchunks = (nsub + 63) / 64;
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+
+  for (int ch = wave; ch < nchunks; ch += WAVES) {
+    const int t = ch * 64 + lane;
+    if (t < nsub) {
+      float xv[32];
+#pragma unroll
+      for (int i = 0; i < 32; i += 4) {
+        const float4 v = *reinterpret_cast<const float4*>(x + 32 * (size_t)t + i);
+        xv[i] = v.x, xv[i + 1] = v.y, xv[i + 2] = v.z, xv[i + 3] = v.w;
+      }
+      uint4 w0[R], w1[R];
+      uint32_t h0[R], h1[R], sv[R], hd[R][4];
+      uint16_t ev[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const size_t sub = (size_t)(r0 + r) * nsub + t;
+        w0[r] = load_stream(a.q + sub * G.qb);
+        w1[r] = make_uint4(0, 0, 0, 0);
+        if constexpr (FMT == kQ8_0) w1[r] = load_stream(a.q + sub * G.qb + 16);
+        h0[r] = h1[r] = 0;
+        if constexpr (G.hb >= 4) h0[r] = *reinterpret_cast<const uint32_t*>(a.h + sub * G.hb);
+        if constexpr (G.hb == 8) h1[r] = *reinterpret_cast<const uint32_t*>(a.h + sub * G.hb + 4);
+        if constexpr (FMT == kQ4_K || FMT == kQ5_K) {
+          const uint4 v = *reinterpret_cast<const uint4*>(a.s + ((size_t)(r0 + r) * nsub + (t & ~7)) * G.sb);
+          hd[r][0] = v.x, hd[r][1] = v.y, hd[r][2] = v.z, hd[r][3] = v.w;
+          sv[r] = 0;
+        } else if constexpr (G.sb == 4) {
+          sv[r] = *reinterpret_cast<const uint32_t*>(a.s + sub * 4);
+        } else {
+          sv[r] = *reinterpret_cast<const uint16_t*>(a.s + sub * 2);
+        }
+        ev[r] = 0;
+        if constexpr (FMT == kQ6_K)
+          ev[r] = *reinterpret_cast<const uint16_t*>(a.e + ((size_t)(r0 + r) * (nsub / 8) + t / 8) * 2);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      float sx_lo = 0.0f, sx_hi = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sx_lo += xv[e];
+#pragma unroll
+      for (int e = 16; e < 32; ++e) sx_hi += xv[e];
+      const float sx = sx_lo + sx_hi;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float c[32];
+        if constexpr (FMT == kQ6_K) {
+          // element e < 16: bits 2e of dword 0 (e < 16 covers 32 bits);
+          // e + 16: dword 1
+          decode_codes<FMT>(w0[r], w1[r], h0[r], h1[r], c);
+        } else {
+          decode_codes<FMT>(w0[r], w1[r], h0[r], 0u, c);
+        }
+        float plo = 0.0f, phi = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) plo = fmaf(c[e], xv[e], plo);
+#pragma unroll
+        for (int e = 16; e < 32; ++e) phi = fmaf(c[e], xv[e], phi);
+        float v;
+        if constexpr (FMT == kQ8_0 || FMT == kQ4_0 || FMT == kQ5_0) {
+          v = f16f((uint16_t)sv[r]) * (plo + phi);
+        } else if constexpr (FMT == kQ4_1 || FMT == kQ5_1) {
+          v = fmaf(f16f((uint16_t)(sv[r] >> 16)), sx, f16f((uint16_t)sv[r]) * (plo + phi));
+        } else if constexpr (FMT == kQ4_K || FMT == kQ5_K) {
+          int sc, m;
+          scale_min_k4_regs(t & 7, hd[r][1], hd[r][2], hd[r][3], &sc, &m);
+          const float d1 = f16f((uint16_t)hd[r][0]) * (float)sc;
+          const float m1 = f16f((uint16_t)(hd[r][0] >> 16)) * (float)m;
+          v = fmaf(d1, plo + phi, -m1 * sx);
+        } else {
+          const float d = f16f(ev[r]);
+          v = d * fmaf((float)(int8_t)(sv[r] >> 8), phi, (float)(int8_t)sv[r] * plo);
+        }
+        acc[r] += v;
+      }
+    }
+  }
+
+  // reduce each row over the wave, then over the waves
+  __shared__ float part[WAVES][R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    float v = acc[r];
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    if (lane == 0) part[wave][r] = v;
+  }
+  __syncthreads();
+  const int tr = threadIdx.x;
+  const int o = r0 + tr;
+  if (tr >= R || o >= a.rows) return;
+  float y = 0.0f;
+#pragma unroll
+  for (int w = 0; w < WAVES; ++w) y += part[w][tr];
+  const size_t oi = (size_t)blockIdx.y * a.out_stride + o;
+  if (a.need_epi) {
+    double v = (double)y;
+    if (a.bias && o < a.bias_len) {
+      v += a.bias[o];
+      y = (float)v;
+    }
+    a.pre[oi] = y;
+    a.post[oi] = (float)act_f64(a.act, v);
+  } else {
+    a.pre[oi] = y;
+    if (a.post && a.post != a.pre) a.post[oi] = y;
+  }
+}
+
+template <int FMT, int R>
+Status gemv_w(const FmtArgs& a, int batch, int waves, hipStream_t st) {
+  const dim3 grid((unsigned)((a.rows + R - 1) / R), (unsigned)batch);
+  switch (waves) {
+  case 1: k_fmt_gemv<FMT, R, 1><<<grid, 64, 0, st>>>(a); break;
+  case 2: k_fmt_gemv<FMT, R, 2><<<grid, 128, 0, st>>>(a); break;
+  default: k_fmt_gemv<FMT, R, 4><<<grid, 256, 0, st>>>(a); break;
+  }
+  return hip_status(hipGetLastError(), "format gemv launch");
+}
+
+template <int FMT>
+Status gemv_f(const FmtArgs& a, int batch, hipStream_t st) {
+  // one wave per 64-sub-block chunk up to 4; then rows per group so that the
+  // grid has >= 8 waves per CU when it can
+  const int chunks = (a.nsub + 63) / 64;
+  const int waves = chunks <= 1 ? 1 : chunks == 2 ? 2 : 4;
+  const long groups8 = ((long)a.rows + 7) / 8 * batch;
+  if (groups8 * waves >= 8L * 256) return gemv_w<FMT, 8>(a, batch, waves, st);
+  return gemv_w<FMT, 4>(a, batch, waves, st);
+}
+
+template <int FMT>
+Status quantize_f(const float* W, int64_t n, uint8_t* out, hipStream_t st) {
+  const int64_t nb = n / 32;
+  if (nb == 0) return Status::ok();
+  k_fmt_quantize<FMT><<<(unsigned)((nb + kThreads - 1) / kThreads), kThreads, 0, st>>>(W, nb, out);
+  return hip_status(hipGetLastError(), "format quantize launch");
+}
+
+template <int FMT>
+Status relayout_f(const FmtArgs& a, const uint8_t* blocks, int rows, hipStream_t st) {
+  const int64_t n = (int64_t)rows * a.nsub;
+  if (n == 0) return Status::ok();
+  k_fmt_relayout<FMT><<<(unsigned)((n + kThreads - 1) / kThreads), kThreads, 0, st>>>(a, blocks, rows);
+  return hip_status(hipGetLastError(), "format relayout launch");
+}
+
+template <int FMT>
+Status dequant_f(const FmtArgs& a, int rows, float* out, hipStream_t st) {
+  const int64_t n = (int64_t)rows * a.nsub;
+  if (n == 0) return Status::ok();
+  k_fmt_dequant<FMT><<<(unsigned)((n + kThreads - 1) / kThreads), kThreads, 0, st>>>(a, rows, out);
+  return hip_status(hipGetLastError(), "format dequant launch");
+}
+
+}  // namespace
+
+#define WV_FMT_DISPATCH(fmt, call)                             \
+  switch (fmt) {                                               \
+  case kQ8_0: return call<kQ8_0>;                              \
+  case kQ4_0: return call<kQ4_0>;                              \
+  case kQ4_1: return call<kQ4_1>;                              \
+  case kQ5_0: return call<kQ5_0>;                              \
+  case kQ5_1: return call<kQ5_1>;                              \
+  case kQ4_K: return call<kQ4_K>;                              \
+  case kQ5_K: return call<kQ5_K>;                              \
+  case kQ6_K: return call<kQ6_K>;                              \
+  default: return Status::err(kGap, "gap? quant format not implemented"); \
+  }
+
+Status format_quantize(int fmt, const float* W, int64_t n, uint8_t* out, hipStream_t st) {
+  if (n % 32) return Status::err(kInvalid, "format quantize: element count");
+  switch (fmt) {
+  case kQ8_0: return quantize_f<kQ8_0>(W, n, out, st);
+  case kQ4_0: return quantize_f<kQ4_0>(W, n, out, st);
+  case kQ4_1: return quantize_f<kQ4_1>(W, n, out, st);
+  case kQ5_0: return quantize_f<kQ5_0>(W, n, out, st);
+  case kQ5_1: return quantize_f<kQ5_1>(W, n, out, st);
+  default:
+    return Status::err(kUnsupported, "format quantize: only Q8_0, Q4_0, Q4_1, Q5_0 and Q5_1 "
+                                     "quantize fp32 weights; mount K formats from packed blocks");
+  }
+}
+
+Status format_relayout(int fmt, const FmtArgs& a, const uint8_t* blocks, int rows, hipStream_t st) {
+  switch (fmt) {
+  case kQ8_0: return relayout_f<kQ8_0>(a, blocks, rows, st);
+  case kQ4_0: return relayout_f<kQ4_0>(a, blocks, rows, st);
+  case kQ4_1: return relayout_f<kQ4_1>(a, blocks, rows, st);
+  case kQ5_0: return relayout_f<kQ5_0>(a, blocks, rows, st);
+  case kQ5_1: return relayout_f<kQ5_1>(a, blocks, rows, st);
+  case kQ4_K: return relayout_f<kQ4_K>(a, blocks, rows, st);
+  case kQ5_K: return relayout_f<kQ5_K>(a, blocks, rows, st);
+  case kQ6_K: return relayout_f<kQ6_K>(a, blocks, rows, st);
+  default: return Status::err(kGap, "gap? quant format not implemented");
+  }
+}
+
+Status format_dequant(int fmt, const FmtArgs& a, int rows, float* out, hipStream_t st) {
+  switch (fmt) {
+  case kQ8_0: return dequant_f<kQ8_0>(a, rows, out, st);
+  case kQ4_0: return dequant_f<kQ4_0>(a, rows, out, st);
+  case kQ4_1: return dequant_f<kQ4_1>(a, rows, out, st);
+  case kQ5_0: return dequant_f<kQ5_0>(a, rows, out, st);
+  case kQ5_1: return dequant_f<kQ5_1>(a, rows, out, st);
+  case kQ4_K: return dequant_f<kQ4_K>(a, rows, out, st);
+  case kQ5_K: return dequant_f<kQ5_K>(a, rows, out, st);
+  case kQ6_K: return dequant_f<kQ6_K>(a, rows, out, st);
+  default: return Status::err(kGap, "gap? quant format not implemented");
+  }
+}
+
+Status launch_format_gemv(int fmt, const FmtArgs& a, int batch, hipStream_t st) {
+  if (a.nsub <= 0 || a.rows <= 0 || batch <= 0) return Status::err(kInvalid, "format gemv: shape");
+  if ((reinterpret_cast<uintptr_t>(a.x) & 15u) || (a.x_stride % 4))
+    return Status::err(kInvalid, "format gemv: x must be 16-byte aligned with a stride of 4k");
+  switch (fmt) {
+  case kQ8_0: return gemv_f<kQ8_0>(a, batch, st);
+  case kQ4_0: return gemv_f<kQ4_0>(a, batch, st);
+  case kQ4_1: return gemv_f<kQ4_1>(a, batch, st);
+  case kQ5_0: return gemv_f<kQ5_0>(a, batch, st);
+  case kQ5_1: return gemv_f<kQ5_1>(a, batch, st);
+  case kQ4_K: return gemv_f<kQ4_K>(a, batch, st);
+  case kQ5_K: return gemv_f<kQ5_K>(a, batch, st);
+  case kQ6_K: return gemv_f<kQ6_K>(a, batch, st);
+  default: return Status::err(kGap, "gap? quant format not implemented");
+  }
+}
+
+}  // namespace wv

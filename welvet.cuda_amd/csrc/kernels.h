@@ -229,4 +229,54 @@ Status launch_sgd(const DeviceWeights& d, const float* dw, double lr, float* w_n
 // W as f32 [rows][cols]: decode times the scales.
 Status launch_dequant(const DeviceWeights& d, float* w, hipStream_t st);
 
+// ---- packed block formats (formats.hip) ----
+// QuantFormat ids: the reference's enum (include/welvet/weights.hpp:12-15)
+// holds only None; the other values follow the order of its format table
+// (README.md:361-383).
+enum QuantFormat : int32_t {
+  kFmtNone = 0, kQ8_0 = 1, kQ4_0 = 2, kQ4_1 = 3, kQ5_0 = 4, kQ5_1 = 5, kQ2_K = 6, kQ3_K = 7,
+  kQ4_K = 8, kQ5_K = 9, kQ6_K = 10, kFmtLast = 20
+};
+// Elements and packed bytes per block; bytes per 32-element sub-block of the
+// resident code (q), high-bit (h) and scale (s) arrays, and of the per-256
+// array e (Q6_K's d).
+struct FmtGeom {
+  int qk, bb, qb, hb, sb, eb;
+};
+constexpr FmtGeom fmt_geom(int fmt) {
+  return fmt == kQ8_0   ? FmtGeom{32, 34, 32, 0, 2, 0}
+         : fmt == kQ4_0 ? FmtGeom{32, 18, 16, 0, 2, 0}
+         : fmt == kQ4_1 ? FmtGeom{32, 20, 16, 0, 4, 0}
+         : fmt == kQ5_0 ? FmtGeom{32, 22, 16, 4, 2, 0}
+         : fmt == kQ5_1 ? FmtGeom{32, 24, 16, 4, 4, 0}
+         : fmt == kQ4_K ? FmtGeom{256, 144, 16, 0, 2, 0}
+         : fmt == kQ5_K ? FmtGeom{256, 176, 16, 4, 2, 0}
+         : fmt == kQ6_K ? FmtGeom{256, 210, 16, 8, 2, 2}
+                        : FmtGeom{0, 0, 0, 0, 0, 0};
+}
+struct FmtArgs {
+  const uint8_t* q = nullptr;  // [rpad][nsub][qb]
+  const uint8_t* h = nullptr;  // [rpad][nsub][hb]
+  const uint8_t* s = nullptr;  // [rpad][nsub][sb]
+  const uint8_t* e = nullptr;  // [rpad][nsub / 8][eb]
+  int rows = 0, cols = 0, nsub = 0;  // nsub = cols / 32
+  const float* x = nullptr;
+  int x_stride = 0;
+  float* pre = nullptr;
+  float* post = nullptr;
+  int out_stride = 0, act = -1, bias_len = 0;
+  bool need_epi = false;
+  const double* bias = nullptr;
+};
+// Packed blocks of n row-major elements (a multiple of 32) from fp32 W
+// (device): Q8_0, Q4_0, Q4_1, Q5_0 and Q5_1 (ggml's reference quantizers).
+Status format_quantize(int fmt, const float* W, int64_t n, uint8_t* out, hipStream_t st);
+// Packed blocks of rows x cols -> the resident arrays of a (q, h, s, e set).
+Status format_relayout(int fmt, const FmtArgs& a, const uint8_t* blocks, int rows, hipStream_t st);
+// The resident arrays -> f32 [rows][cols] (the format's dequantization).
+Status format_dequant(int fmt, const FmtArgs& a, int rows, float* out, hipStream_t st);
+// y = W x for every one of `batch` rows of x (a.x, a.x_stride), with the Dense
+// epilogue into a.pre / a.post.
+Status launch_format_gemv(int fmt, const FmtArgs& a, int batch, hipStream_t st);
+
 }  // namespace wv

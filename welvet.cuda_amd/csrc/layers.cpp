@@ -130,6 +130,95 @@ Status dense_build_from_store(int in, int out, int act, const WeightStore& store
   return upload_bias(L, store.bias.data(), store.bias.size(), st);
 }
 
+static FmtArgs format_args(const DenseLayer& L) {
+  FmtArgs a;
+  a.q = L.fw.q.as<const uint8_t>();
+  a.h = L.fw.h.as<const uint8_t>();
+  a.s = L.fw.s.as<const uint8_t>();
+  a.e = L.fw.e.as<const uint8_t>();
+  a.rows = L.out;
+  a.cols = L.in;
+  a.nsub = L.fw.nsub;
+  return a;
+}
+
+Status dense_build_format(int in, int out, int act, int format, const float* W_host,
+                          const uint8_t* blocks, size_t blocks_len, const double* bias,
+                          size_t bias_len, DenseLayer* L, hipStream_t st) {
+  if (!L) return Status::err(kInvalid, "dense: null layer");
+  if (in <= 0 || out <= 0) return Status::err(kInvalid, "dense: bad dims");
+  if (!act_valid(act)) return Status::err(kInvalid, "dense: bad activation");
+  const FmtGeom G = fmt_geom(format);
+  if (G.qk == 0) {
+    if (format > kFmtNone && format <= kFmtLast)
+      return Status::err(kGap, "gap? quant format " + std::to_string(format) + " not implemented");
+    return Status::err(kInvalid, "dense: quant format out of range");
+  }
+  if (in % G.qk) return Status::err(kInvalid, "dense: in must be a multiple of the format's block");
+  if ((W_host == nullptr) == (blocks == nullptr))
+    return Status::err(kInvalid, "dense: give either fp32 weights or packed blocks");
+  const int64_t n = (int64_t)in * out;
+  const size_t nbytes = (size_t)(n / G.qk) * G.bb;
+  if (blocks && blocks_len != nbytes) return Status::err(kInvalid, "dense: packed block length");
+  L->in = in, L->out = out, L->act = act, L->format = format;
+  FormatWeights& f = L->fw;
+  f.format = format, f.rows = out, f.cols = in, f.rpad = (int)round_up(out, 16), f.nsub = in / 32;
+  DevBuf packed;
+  WV_TRY(packed.alloc(nbytes));
+  if (W_host) {
+    DevBuf dW;
+    WV_TRY(dW.alloc((size_t)n * sizeof(float)));
+    WV_TRY(copy_h2d(dW.p, W_host, (size_t)n * sizeof(float), st));
+    WV_TRY(format_quantize(format, dW.as<float>(), n, packed.as<uint8_t>(), st));
+    WV_HIP(hipStreamSynchronize(st));
+  } else {
+    WV_TRY(copy_h2d(packed.p, blocks, nbytes, st));
+  }
+  const size_t subs = (size_t)f.rpad * f.nsub;
+  WV_TRY(f.q.alloc(subs * G.qb));
+  WV_HIP(hipMemsetAsync(f.q.p, 0, f.q.bytes, st));
+  WV_TRY(f.s.alloc(subs * G.sb));
+  WV_HIP(hipMemsetAsync(f.s.p, 0, f.s.bytes, st));
+  f.h.reset();
+  f.e.reset();
+  if (G.hb) {
+    WV_TRY(f.h.alloc(subs * G.hb));
+    WV_HIP(hipMemsetAsync(f.h.p, 0, f.h.bytes, st));
+  }
+  if (G.eb) {
+    WV_TRY(f.e.alloc(subs / 8 * G.eb));
+    WV_HIP(hipMemsetAsync(f.e.p, 0, f.e.bytes, st));
+  }
+  WV_TRY(format_relayout(format, format_args(*L), packed.as<uint8_t>(), out, st));
+  f.blocks.resize(nbytes);
+  WV_TRY(copy_d2h(f.blocks.data(), packed.p, nbytes, st));
+  WV_HIP(hipStreamSynchronize(st));
+  L->store = WeightStore{};
+  L->store.rows = out, L->store.cols = in;
+  return upload_bias(L, bias, bias_len, st);
+}
+
+Status dense_export_f32(const DenseLayer& L, float* w, hipStream_t st) {
+  if (!w) return Status::err(kInvalid, "dense export: null buffer");
+  if (L.format) return format_dequant(L.format, format_args(L), L.out, w, st);
+  return launch_dequant(L.dev, w, st);
+}
+
+static Status format_forward(const DenseLayer& L, int batch, const float* x, float* pre,
+                             float* post, hipStream_t st) {
+  FmtArgs a = format_args(L);
+  a.x = x;
+  a.x_stride = L.in;
+  a.pre = pre;
+  a.post = post;
+  a.out_stride = L.out;
+  a.act = L.act;
+  a.need_epi = L.need_epi();
+  a.bias = L.bias_dev.as<const double>();
+  a.bias_len = L.bias_len;
+  return launch_format_gemv(L.format, a, batch, st);
+}
+
 int gemv_batch_limit() { return 1 << 30; }
 
 static GemvTile tile_for(const DeviceWeights& d, int mats) {
@@ -180,7 +269,7 @@ static MxvArgs mxv_args(const DenseLayer& L, const float* x, int x_stride, int b
 bool uses_split(int batch) { return batch > kMxvMaxBatch; }
 
 Status dense_prepare_rows(DenseLayer* L, int batch, hipStream_t st) {
-  if (!uses_split(batch) || mxg_block_m(batch) != 16 || L->dev.codes_frag.p)
+  if (L->format || !uses_split(batch) || mxg_block_m(batch) != 16 || L->dev.codes_frag.p)
     return Status::ok();
   WV_TRY(build_codes_frag(&L->dev, st));
   return hip_status(hipStreamSynchronize(st), "codes_frag");
@@ -198,6 +287,7 @@ static size_t gemm_ws_bytes(const DenseLayer& L, int batch, int mats) {
 }
 
 size_t dense_workspace_bytes(const DenseLayer& L, int batch) {
+  if (L.format) return 0;
   return uses_split(batch) ? gemm_ws_bytes(L, batch, 1) : 0;
 }
 
@@ -291,6 +381,8 @@ Status dense_forward(const DenseLayer& L, int batch, const float* x, float* pre,
                      Workspace* ws, hipStream_t st) {
   if (batch <= 0 || !x || !pre) return Status::err(kInvalid, "dense forward: bad args");
   if (L.need_epi() && !post) return Status::err(kInvalid, "dense forward: post needed");
+  // packed block formats: the GEMV over every batch row
+  if (L.format) return format_forward(L, batch, x, pre, post, st);
   if (uses_split(batch)) {
     WV_TRY(ensure_split(ws, gemm_ws_bytes(L, batch, 1)));
     return dense_forward_split(L, batch, x, false, ws, pre, post, st);
@@ -316,6 +408,7 @@ Status dense_backward(const DenseLayer& L, int batch, const float* x, const floa
                       bool linear_act) {
   if (batch <= 0 || !x || !pre || !g || !dpre || !dx || !dw || !ws || (use_target && !post))
     return Status::err(kInvalid, "dense backward: bad args");
+  if (L.format) return Status::err(kGap, "gap? dense backward over packed block formats");
   const int64_t n = (int64_t)batch * L.out;
   WV_TRY(launch_dpre(g, post, pre, linear_act ? kLinear : L.act, use_target ? 1 : 0, n, dpre,
                      loss_part, st));
@@ -337,6 +430,7 @@ Status dense_backward(const DenseLayer& L, int batch, const float* x, const floa
 
 Status dense_apply_sgd(DenseLayer* L, const float* dw, double lr, hipStream_t st) {
   if (!L || !dw) return Status::err(kInvalid, "dense sgd: bad args");
+  if (L->format) return Status::err(kGap, "gap? SGD on packed block formats");
   const int64_t n = (int64_t)L->in * L->out;
   DevBuf next, raw;
   WV_TRY(next.alloc((size_t)n * sizeof(float)));
@@ -357,6 +451,9 @@ Status dense_group_build(const DenseLayer* const* layers, int n, int batch,
                          DenseGroup* g) {
   if (n <= 0 || !layers || !x || !pre || !g) return Status::err(kInvalid, "dense group: bad args");
   if (!dense_group_fused(batch)) return Status::err(kInvalid, "dense group: batch too small");
+  for (int i = 0; i < n; ++i)
+    if (layers[i]->format)
+      return Status::err(kUnsupported, "dense group: packed block formats run one by one");
   const DenseLayer& L0 = *layers[0];
   g->layers.clear();
   std::vector<SplitJob> jobs(n);

@@ -44,9 +44,20 @@ struct Workspace {
   double rope_theta = 0.0;
 };
 
+// Resident weights of a packed block format (formats.hip): the arrays that
+// FmtArgs points at, and the packed blocks as mounted (a host copy, for
+// export).
+struct FormatWeights {
+  int format = 0, rows = 0, cols = 0, rpad = 0, nsub = 0;
+  DevBuf q, h, s, e;
+  std::vector<uint8_t> blocks;
+};
+
 struct DenseLayer {
   int in = 0, out = 0, act = kLinear;
   int terms = kTerms;  // activation terms of the matrix-core paths (2 or 3)
+  int format = kFmtNone;  // a packed block format: the weights are in fw, not dev
+  FormatWeights fw;
   WeightStore store;
   DeviceWeights dev;
   DevBuf bias_dev;
@@ -60,6 +71,17 @@ Status dense_build(int in, int out, int act, int dtype, int scheme, const float*
 // Builds L from a stored payload (reference FormatNone bytes + scales).
 Status dense_build_from_store(int in, int out, int act, const WeightStore& store, DenseLayer* L,
                               hipStream_t st);
+
+// A Dense layer over a packed block format (QuantFormat): from fp32 W_host
+// (quantized on the device; Q8_0, Q4_0, Q4_1, Q5_0, Q5_1) or from the
+// format's packed row-major blocks (blocks_len bytes); exactly one is given.
+// in must be a multiple of the format's block (32, or 256 for the K formats).
+Status dense_build_format(int in, int out, int act, int format, const float* W_host,
+                          const uint8_t* blocks, size_t blocks_len, const double* bias,
+                          size_t bias_len, DenseLayer* L, hipStream_t st);
+// The layer's weights dequantized to f32 [out][in] in device memory w (the
+// role of WeightStore::export_f32, src/weights/store.cpp:42-71).
+Status dense_export_f32(const DenseLayer& L, float* w, hipStream_t st);
 
 // Batch rows at or below this go to the GEMV kernels.
 int gemv_batch_limit();

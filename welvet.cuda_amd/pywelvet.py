@@ -102,6 +102,10 @@ def lib():
     _sig(L, "welvet_dense_export_store", Status,
          [_vp, _u8p, _sz, ctypes.POINTER(_sz), _fp, _u8p, _fp])
     _sig(L, "welvet_dense_release", None, [_vp])
+    _sig(L, "welvet_dense_mount_format", Status,
+         [_i32, _i32, _i32, _i32, _i32, _fp, _u8p, _sz, _dp, _sz, ctypes.POINTER(_vp)])
+    _sig(L, "welvet_dense_export_blocks", Status, [_vp, _u8p, _sz, ctypes.POINTER(_sz)])
+    _sig(L, "welvet_dense_export_f32", Status, [_vp, _fp])
     _sig(L, "welvet_dense_group_mount", Status,
          [ctypes.POINTER(_vp), _i32, ctypes.POINTER(_vp), ctypes.POINTER(_vp),
           ctypes.POINTER(_vp), ctypes.POINTER(_vp)])
@@ -434,6 +438,11 @@ class DenseSession:
                                               blk.ctypes.data_as(_u8p), ctypes.byref(ts)))
         return native[: nlen.value], rs, blk, ts.value
 
+    def export_f32(self):
+        W = np.zeros((self.out_dim, self.in_dim), np.float32)
+        check(lib().welvet_dense_export_f32(self.h, fptr(W)))
+        return W
+
     def close(self):
         if self.h:
             lib().welvet_dense_release(self.h)
@@ -444,6 +453,37 @@ class DenseSession:
             self.close()
         except Exception:
             pass
+
+
+# packed block formats (QuantFormat ids of welvet_dense_mount_format)
+Q8_0, Q4_0, Q4_1, Q5_0, Q5_1, Q4_K, Q5_K, Q6_K = 1, 2, 3, 4, 5, 8, 9, 10
+
+
+class FormatDenseSession(DenseSession):
+    """welvet_dense_mount_format: a Dense session over a packed block format,
+    from fp32 weights W (quantized on the device) or from packed blocks."""
+
+    def __init__(self, batch, in_dim, out_dim, act, fmt, W=None, blocks=None, bias=None):
+        L = lib()
+        self.batch, self.in_dim, self.out_dim, self.fmt = batch, in_dim, out_dim, fmt
+        self.h = None
+        Wc = None if W is None else np.ascontiguousarray(W, dtype=np.float32)
+        bc = None if blocks is None else np.ascontiguousarray(blocks, dtype=np.uint8)
+        b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float64)
+        h = _vp()
+        check(L.welvet_dense_mount_format(
+            batch, in_dim, out_dim, act, fmt, fptr(Wc) if Wc is not None else None,
+            bc.ctypes.data_as(_u8p) if bc is not None else None, 0 if bc is None else bc.size,
+            dptr(b), 0 if b is None else b.size, ctypes.byref(h)))
+        self.h = h
+
+    def export_blocks(self):
+        n = _sz()
+        check(lib().welvet_dense_export_blocks(self.h, None, 0, ctypes.byref(n)))
+        out = np.zeros(n.value, np.uint8)
+        check(lib().welvet_dense_export_blocks(self.h, out.ctypes.data_as(_u8p), out.size,
+                                               ctypes.byref(n)))
+        return out
 
 
 class SwiGLUSession:
