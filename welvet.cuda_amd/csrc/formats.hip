@@ -23,6 +23,7 @@
 // zero bytes (zero scales: padding rows read as 0).
 #include "common.h"
 #include "kernels.h"
+#include "wave.h"
 
 namespace wv {
 
@@ -249,9 +250,6 @@ __device__ __forceinline__ void decode_codes(const uint4 w0, const uint4 w1, uin
   }
 }
 
-// the element-16+ high bits of Q6_K start at bit 32 of the sub-block's 8 bytes
-// (hb1 = the second dword); elements 0..15 use the first dword
-
 // scale and min of Q4_K/Q5_K sub-block j from the 12 packed scale bytes
 // (get_scale_min_k4)
 __device__ __forceinline__ void scale_min_k4(int j, const uint8_t* q, int* sc, int* m) {
@@ -346,14 +344,73 @@ __device__ __forceinline__ uint4 load_stream(const uint8_t* p) {
 // ---- GEMV: one workgroup of WAVES waves owns R rows; lane l of wave w takes
 // sub-block 64 c + l of every row for chunks c = w, w + WAVES, ..; its 32 x
 // values are loaded once per chunk and applied to all R rows. Per row it
-// loads the 16-byte code (32 for Q8_0) and the small side arrays, decodes to
-// integers, forms the dot product with x in f32 and applies the sub-block's
-// scale (and min) once: d * sum(c x) (+ m * sum(x)). The R per-lane partial
-// sums are reduced across the wave and then across the waves in LDS; the
-// epilogue is the Dense one (kernels.cu:147-161: bias and activation in f64).
+// loads the 16-byte code (32 for Q8_0) and the small side arrays, forms the
+// dot product of the unsigned codes with x in f32 and applies the
+// sub-block's scale once: d * (sum(c x) - off * sum(x)) for the symmetric
+// formats, d * sum(c x) + m * sum(x) for the affine ones. Codes become floats
+// by byte conversions of masked dwords (v_cvt_f32_ubyte), about 2.4 VALU
+// operations per 4-bit element with the FMA; the high bits of the 5- and
+// 6-bit formats are spread into bits 4-5 of each byte first. The R per-lane
+// partial sums are reduced across the wave with the transposing butterfly
+// and then across the waves in LDS; the epilogue is the Dense one
+// (kernels.cu:147-161: bias and activation in f64).
+
+// byte b of v as a float
+__device__ __forceinline__ float ub(uint32_t v, int b) { return (float)((v >> (8 * b)) & 0xFFu); }
+// bits 0-3 of x to bit 0 of bytes 0-3 (x * (1 + 2^7 + 2^14 + 2^21) puts bit
+// k at 8k with no other term on those bits)
+__device__ __forceinline__ uint32_t spread1(uint32_t x) { return (x * 0x00204081u) & 0x01010101u; }
+// 2-bit fields 0-3 of x to bits 0-1 of bytes 0-3
+__device__ __forceinline__ uint32_t spread2(uint32_t x) {
+  x = (x | (x << 12)) & 0x000F000Fu;
+  return (x | (x << 6)) & 0x03030303u;
+}
+
+// sum over the low-nibble elements (0..15) and the high-nibble ones (16..31)
+// of code * x; HB high bits per element from h0 (elements 0-15 for HB = 2)
+// and h1 (elements 16-31, HB = 2)
+template <int HB>
+__device__ __forceinline__ void dot_sub(const uint4 w, uint32_t h0, uint32_t h1,
+                                        const float* xv, float& plo, float& phi) {
+  const uint32_t W[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    uint32_t lo = W[d] & 0x0F0F0F0Fu, hi = (W[d] >> 4) & 0x0F0F0F0Fu;
+    if constexpr (HB == 1) {
+      lo |= spread1((h0 >> (4 * d)) & 0xFu) << 4;
+      hi |= spread1((h0 >> (16 + 4 * d)) & 0xFu) << 4;
+    } else if constexpr (HB == 2) {
+      lo |= spread2((h0 >> (8 * d)) & 0xFFu) << 4;
+      hi |= spread2((h1 >> (8 * d)) & 0xFFu) << 4;
+    }
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      plo = fmaf(ub(lo, b), xv[4 * d + b], plo);
+      phi = fmaf(ub(hi, b), xv[16 + 4 * d + b], phi);
+    }
+  }
+}
+
+// Q8_0: int8 codes q; (q + 128) as unsigned bytes, the 128 taken off with
+// sum(x) by the caller
+__device__ __forceinline__ float dot_q8(const uint4 w0, const uint4 w1, const float* xv) {
+  const uint32_t W[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+  float p0 = 0.0f, p1 = 0.0f;
+#pragma unroll
+  for (int d = 0; d < 8; ++d) {
+    const uint32_t u = W[d] ^ 0x80808080u;
+    p0 = fmaf(ub(u, 0), xv[4 * d], p0);
+    p1 = fmaf(ub(u, 1), xv[4 * d + 1], p1);
+    p0 = fmaf(ub(u, 2), xv[4 * d + 2], p0);
+    p1 = fmaf(ub(u, 3), xv[4 * d + 3], p1);
+  }
+  return p0 + p1;
+}
+
 template <int FMT, int R, int WAVES>
 __global__ __launch_bounds__(64 * WAVES) void k_fmt_gemv(FmtArgs a) {
   constexpr FmtGeom G = fmt_geom(FMT);
+  constexpr int HB = FMT == kQ6_K ? 2 : G.hb ? 1 : 0;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r0 = blockIdx.x * R;
   const int nsub = a.nsub;
@@ -400,61 +457,52 @@ __global__ __launch_bounds__(64 * WAVES) void k_fmt_gemv(FmtArgs a) {
       __builtin_amdgcn_sched_barrier(0);
       float sx_lo = 0.0f, sx_hi = 0.0f;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) sx_lo += xv[e];
-#pragma unroll
-      for (int e = 16; e < 32; ++e) sx_hi += xv[e];
+      for (int e = 0; e < 16; e += 2) {
+        sx_lo += xv[e] + xv[e + 1];
+        sx_hi += xv[16 + e] + xv[17 + e];
+      }
       const float sx = sx_lo + sx_hi;
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        float c[32];
-        if constexpr (FMT == kQ6_K) {
-          // element e < 16: bits 2e of dword 0 (e < 16 covers 32 bits);
-          // e + 16: dword 1
-          decode_codes<FMT>(w0[r], w1[r], h0[r], h1[r], c);
-        } else {
-          decode_codes<FMT>(w0[r], w1[r], h0[r], 0u, c);
-        }
-        float plo = 0.0f, phi = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) plo = fmaf(c[e], xv[e], plo);
-#pragma unroll
-        for (int e = 16; e < 32; ++e) phi = fmaf(c[e], xv[e], phi);
         float v;
-        if constexpr (FMT == kQ8_0 || FMT == kQ4_0 || FMT == kQ5_0) {
-          v = f16f((uint16_t)sv[r]) * (plo + phi);
-        } else if constexpr (FMT == kQ4_1 || FMT == kQ5_1) {
-          v = fmaf(f16f((uint16_t)(sv[r] >> 16)), sx, f16f((uint16_t)sv[r]) * (plo + phi));
-        } else if constexpr (FMT == kQ4_K || FMT == kQ5_K) {
-          int sc, m;
-          scale_min_k4_regs(t & 7, hd[r][1], hd[r][2], hd[r][3], &sc, &m);
-          const float d1 = f16f((uint16_t)hd[r][0]) * (float)sc;
-          const float m1 = f16f((uint16_t)(hd[r][0] >> 16)) * (float)m;
-          v = fmaf(d1, plo + phi, -m1 * sx);
+        if constexpr (FMT == kQ8_0) {
+          v = f16f((uint16_t)sv[r]) * fmaf(-128.0f, sx, dot_q8(w0[r], w1[r], xv));
         } else {
-          const float d = f16f(ev[r]);
-          v = d * fmaf((float)(int8_t)(sv[r] >> 8), phi, (float)(int8_t)sv[r] * plo);
+          float plo = 0.0f, phi = 0.0f;
+          dot_sub<HB>(w0[r], h0[r], h1[r], xv, plo, phi);
+          if constexpr (FMT == kQ4_0 || FMT == kQ5_0) {
+            constexpr float off = FMT == kQ4_0 ? -8.0f : -16.0f;
+            v = f16f((uint16_t)sv[r]) * fmaf(off, sx, plo + phi);
+          } else if constexpr (FMT == kQ4_1 || FMT == kQ5_1) {
+            v = fmaf(f16f((uint16_t)(sv[r] >> 16)), sx, f16f((uint16_t)sv[r]) * (plo + phi));
+          } else if constexpr (FMT == kQ4_K || FMT == kQ5_K) {
+            int sc, m;
+            scale_min_k4_regs(t & 7, hd[r][1], hd[r][2], hd[r][3], &sc, &m);
+            const float d1 = f16f((uint16_t)hd[r][0]) * (float)sc;
+            const float m1 = f16f((uint16_t)(hd[r][0] >> 16)) * (float)m;
+            v = fmaf(d1, plo + phi, -m1 * sx);
+          } else {
+            // Q6_K: codes 0..63, offset 32, one int8 scale per 16 elements
+            const float lo = fmaf(-32.0f, sx_lo, plo), hi = fmaf(-32.0f, sx_hi, phi);
+            v = f16f(ev[r]) * fmaf((float)(int8_t)(sv[r] >> 8), hi, (float)(int8_t)sv[r] * lo);
+          }
         }
         acc[r] += v;
       }
     }
   }
 
-  // reduce each row over the wave, then over the waves
+  // every lane is active here (the DPP moves need that)
   __shared__ float part[WAVES][R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    float v = acc[r];
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-    if (lane == 0) part[wave][r] = v;
-  }
+  wave_reduce_rows<R>(acc, lane);
+  if (lane < R) part[wave][reduced_row<R>(lane)] = acc[0];
   __syncthreads();
   const int tr = threadIdx.x;
   const int o = r0 + tr;
   if (tr >= R || o >= a.rows) return;
-  float y = 0.0f;
+  float y = part[0][tr];
 #pragma unroll
-  for (int w = 0; w < WAVES; ++w) y += part[w][tr];
+  for (int w = 1; w < WAVES; ++w) y += part[w][tr];
   const size_t oi = (size_t)blockIdx.y * a.out_stride + o;
   if (a.need_epi) {
     double v = (double)y;
