@@ -59,7 +59,8 @@ C2_BYTES = 16826368
 # known size) per workload; `traffic_bytes:` is the measured HBM bytes per launch.
 PROFILES = {"c2": "gemv_fp8e4m3_rowscale_4096x4096_b1.txt",
             "read_floor": "read_floor_16826368B.txt",
-            "c2bwd": "dense_backward_4096x4096_fp8e4m3_rowscale_b1.txt"}
+            "c2bwd": "dense_backward_4096x4096_fp8e4m3_rowscale_b1.txt",
+            "gemv_q4_k": "gemv_q4_k_4096x4096_b1.txt"}
 
 
 def measured_traffic(config):
