@@ -31,7 +31,6 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kFragBytes = 2048;                  // one 16 x 128 E4M3 operand
-constexpr int kChunkBytes = kTerms * kFragBytes;  // the terms of one (rb, kc)
 constexpr int kChunkScaleBytes = 256;             // one exponent dword per lane
 
 typedef int v8i __attribute__((ext_vector_type(8)));
