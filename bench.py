@@ -26,7 +26,7 @@ Other workloads (--config), each its own line:
   c5chain  the same cells as the reference's volume: one 192-layer serial chain (model session)
   c2bwd  Dense backward at the GEMV shape: d_pre, dX = W^T d_pre, dW (4096^2 E4M3 per-row, batch 1)
   gemv_<fmt>  the c2 GEMV shape over a packed block format (q8_0, q4_0, q4_1, q5_0, q5_1,
-         q4_k, q5_k, q6_k; bytes = packed blocks + x + y)
+         q2_k, q3_k, q4_k, q5_k, q6_k; bytes = packed blocks + x + y)
 --read-floor BYTES instead times one streaming read of BYTES (default: the c2
 step's 16,826,368) over 64 rotated buffers, the same way: the floor for any
 kernel that reads those bytes once.
@@ -196,8 +196,8 @@ def dense_workload(pw, hip, name, cfg_id, dtype, scheme, batch, K, N, copies, bo
 
 
 FORMATS = {"q8_0": (1, 32, 34), "q4_0": (2, 32, 18), "q4_1": (3, 32, 20), "q5_0": (4, 32, 22),
-           "q5_1": (5, 32, 24), "q4_k": (8, 256, 144), "q5_k": (9, 256, 176),
-           "q6_k": (10, 256, 210)}
+           "q5_1": (5, 32, 24), "q2_k": (6, 256, 84), "q3_k": (7, 256, 110),
+           "q4_k": (8, 256, 144), "q5_k": (9, 256, 176), "q6_k": (10, 256, 210)}
 
 
 def format_blocks(fmt, qk, bb, N, K, seed):
@@ -213,6 +213,11 @@ def format_blocks(fmt, qk, bb, N, K, seed):
     if fmt in (8, 9):
         raw[:, 0:2] = (d / 32).astype(np.float16).view(np.uint8).reshape(nb, 2)
         raw[:, 2:4] = (d / 64).astype(np.float16).view(np.uint8).reshape(nb, 2)
+    elif fmt == 6:
+        raw[:, 80:82] = (d / 8).astype(np.float16).view(np.uint8).reshape(nb, 2)
+        raw[:, 82:84] = (d / 16).astype(np.float16).view(np.uint8).reshape(nb, 2)
+    elif fmt == 7:
+        raw[:, 108:110] = (d / 16).astype(np.float16).view(np.uint8).reshape(nb, 2)
     else:
         raw[:, 208:210] = (d / 64).astype(np.float16).view(np.uint8).reshape(nb, 2)
     return raw.reshape(-1)

@@ -15,7 +15,7 @@
  * -ffp-contract=off), left to right as written below.
  *
  * Format ids follow the README's table order: 1 Q8_0, 2 Q4_0, 3 Q4_1,
- * 4 Q5_0, 5 Q5_1, 8 Q4_K, 9 Q5_K, 10 Q6_K.
+ * 4 Q5_0, 5 Q5_1, 6 Q2_K, 7 Q3_K, 8 Q4_K, 9 Q5_K, 10 Q6_K.
  */
 #include <float.h>
 #include <math.h>
@@ -83,7 +83,7 @@ int or_fmt_block_elems(int fmt) {
   switch (fmt) {
   case OR_FMT_Q8_0: case OR_FMT_Q4_0: case OR_FMT_Q4_1: case OR_FMT_Q5_0: case OR_FMT_Q5_1:
     return 32;
-  case OR_FMT_Q4_K: case OR_FMT_Q5_K: case OR_FMT_Q6_K:
+  case OR_FMT_Q2_K: case OR_FMT_Q3_K: case OR_FMT_Q4_K: case OR_FMT_Q5_K: case OR_FMT_Q6_K:
     return 256;
   default:
     return 0;
@@ -97,6 +97,8 @@ int or_fmt_block_bytes(int fmt) {
   case OR_FMT_Q4_1: return 20;  /* f16 d, f16 m, qs[16] */
   case OR_FMT_Q5_0: return 22;  /* f16 d, qh[4], qs[16] */
   case OR_FMT_Q5_1: return 24;  /* f16 d, f16 m, qh[4], qs[16] */
+  case OR_FMT_Q2_K: return 84;  /* scales[16], qs[64], f16 d, f16 dmin */
+  case OR_FMT_Q3_K: return 110; /* hmask[32], qs[64], scales[12], f16 d */
   case OR_FMT_Q4_K: return 144; /* f16 d, f16 dmin, scales[12], qs[128] */
   case OR_FMT_Q5_K: return 176; /* f16 d, f16 dmin, scales[12], qh[32], qs[128] */
   case OR_FMT_Q6_K: return 210; /* ql[128], qh[64], int8 scales[16], f16 d */
@@ -235,6 +237,17 @@ static void scale_min_k4(int j, const uint8_t* q, int* sc, int* m) {
   }
 }
 
+/* The 16 6-bit scales of a Q3_K super-block from its 12 packed bytes, as
+ * signed values (scale - 32): scale s = 4 g + i takes the low (g = 0, 1) or
+ * high (g = 2, 3) nibble of byte i (g even) or byte 4 + i (g odd), and bits
+ * 4-5 from bits 2g, 2g + 1 of byte 8 + i. */
+static int scale_q3k(int s, const uint8_t* q) {
+  const int g = s >> 2, i = s & 3;
+  const int lo = (q[(g & 1) * 4 + i] >> ((g >> 1) * 4)) & 0xF;
+  const int hi = (q[8 + i] >> (2 * g)) & 3;
+  return (lo | (hi << 4)) - 32;
+}
+
 static void dequant_block(int fmt, const uint8_t* b, float* y) {
   switch (fmt) {
   case OR_FMT_Q8_0: { /* y = q * d */
@@ -302,6 +315,41 @@ static void dequant_block(int fmt, const uint8_t* b, float* y) {
         y[64 * i + 32 + l] = d2 * (float)((qs[32 * i + l] >> 4) + hi1) - mm2;
       }
     }
+    break;
+  }
+  case OR_FMT_Q2_K: {
+    /* element 128 n + 32 j + l: 2-bit code j of qs[32 n + l] (bits 2j, 2j+1),
+     * scale byte sc = scales[8 n + 2 j + l / 16]:
+     * y = (d * (sc & 15)) * q - (dmin * (sc >> 4)) */
+    const uint8_t* sc = b;
+    const uint8_t* qs = b + 16;
+    const float d = or_f16_to_f32(get16(b + 80)), dmin = or_f16_to_f32(get16(b + 82));
+    for (int n = 0; n < 2; ++n)
+      for (int j = 0; j < 4; ++j)
+        for (int l = 0; l < 32; ++l) {
+          const int s = sc[8 * n + 2 * j + l / 16];
+          const float dl = d * (float)(s & 15), ml = dmin * (float)(s >> 4);
+          const int q = (qs[32 * n + l] >> (2 * j)) & 3;
+          y[128 * n + 32 * j + l] = dl * (float)q - ml;
+        }
+    break;
+  }
+  case OR_FMT_Q3_K: {
+    /* element 128 n + 32 j + l: low bits from bits 2j, 2j+1 of qs[32 n + l],
+     * minus 4 unless bit 4n + j of hmask[l] is set; scale 8 n + 2 j + l / 16:
+     * y = (d * scale) * q */
+    const uint8_t* hm = b;
+    const uint8_t* qs = b + 32;
+    const uint8_t* sc = b + 96;
+    const float d = or_f16_to_f32(get16(b + 108));
+    for (int n = 0; n < 2; ++n)
+      for (int j = 0; j < 4; ++j)
+        for (int l = 0; l < 32; ++l) {
+          const float dl = d * (float)scale_q3k(8 * n + 2 * j + l / 16, sc);
+          const int lo = (qs[32 * n + l] >> (2 * j)) & 3;
+          const int q = lo - (((hm[l] >> (4 * n + j)) & 1) ? 0 : 4);
+          y[128 * n + 32 * j + l] = dl * (float)q;
+        }
     break;
   }
   case OR_FMT_Q6_K: {

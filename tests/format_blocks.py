@@ -2,15 +2,15 @@
 valid packed blocks (ggml block layouts, restated in oracle/formats.c)."""
 import numpy as np
 
-Q8_0, Q4_0, Q4_1, Q5_0, Q5_1, Q4_K, Q5_K, Q6_K = 1, 2, 3, 4, 5, 8, 9, 10
+Q8_0, Q4_0, Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K = 1, 2, 3, 4, 5, 6, 7, 8, 9, 10
 LEGACY = [Q8_0, Q4_0, Q4_1, Q5_0, Q5_1]
-KQUANT = [Q4_K, Q5_K, Q6_K]
+KQUANT = [Q2_K, Q3_K, Q4_K, Q5_K, Q6_K]
 ALL = LEGACY + KQUANT
-NAMES = {Q8_0: "Q8_0", Q4_0: "Q4_0", Q4_1: "Q4_1", Q5_0: "Q5_0", Q5_1: "Q5_1", Q4_K: "Q4_K",
-         Q5_K: "Q5_K", Q6_K: "Q6_K"}
+NAMES = {Q8_0: "Q8_0", Q4_0: "Q4_0", Q4_1: "Q4_1", Q5_0: "Q5_0", Q5_1: "Q5_1", Q2_K: "Q2_K",
+         Q3_K: "Q3_K", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K"}
 # elements and bytes per block
 GEOM = {Q8_0: (32, 34), Q4_0: (32, 18), Q4_1: (32, 20), Q5_0: (32, 22), Q5_1: (32, 24),
-        Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210)}
+        Q2_K: (256, 84), Q3_K: (256, 110), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210)}
 
 
 def f16_bytes(v):
@@ -36,6 +36,11 @@ def random_blocks(fmt, rows, cols, rng, scale=None):
         raw[:, 0:2] = dk.view(np.uint8).reshape(nb, 2)
         mk = (np.abs(m.astype(np.float32)) / 32).astype(np.float16)
         raw[:, 2:4] = mk.view(np.uint8).reshape(nb, 2)
+    elif fmt == Q2_K:  # 4-bit sub-block scales and mins, f16 d, dmin at the end
+        raw[:, 80:82] = (d.astype(np.float32) / 8).astype(np.float16).view(np.uint8).reshape(nb, 2)
+        raw[:, 82:84] = (np.abs(m.astype(np.float32)) / 16).astype(np.float16).view(np.uint8).reshape(nb, 2)
+    elif fmt == Q3_K:  # signed 6-bit scales (-32..31), f16 d at the end
+        raw[:, 108:110] = (d.astype(np.float32) / 16).astype(np.float16).view(np.uint8).reshape(nb, 2)
     elif fmt == Q6_K:
         dk = (d.astype(np.float32) / 64).astype(np.float16)  # int8 sub-block scales
         raw[:, 208:210] = dk.view(np.uint8).reshape(nb, 2)

@@ -11,8 +11,8 @@ its header."""
 import numpy as np
 import pytest
 
-from format_blocks import GEOM, KQUANT, LEGACY, Q4_0, Q4_1, Q4_K, Q5_0, Q5_1, Q5_K, Q6_K, Q8_0, \
-    random_blocks
+from format_blocks import GEOM, KQUANT, LEGACY, Q2_K, Q3_K, Q4_0, Q4_1, Q4_K, Q5_0, Q5_1, Q5_K, \
+    Q6_K, Q8_0, random_blocks
 from oracle_lib import Oracle
 
 
@@ -202,6 +202,66 @@ def test_q6_k_scales_and_positions(orc):
                     want[128 * n + 32 * t + l] = 0.5 * sc[8 * n + 2 * t + l // 16] * ((lo | hi << 4) - 32)
         got = orc.fmt_dequant(Q6_K, blk, (256,))
         assert np.array_equal(got, want.astype(np.float32))
+
+
+def test_q2_k_scales_and_positions(orc):
+    """d = 0.5, dmin = 0.25, scale bytes sc[16] (scale in the low nibble, min
+    in the high one): element 128 n + 32 j + l = (d * (sc & 15)) * q -
+    (dmin * (sc >> 4)), q = bits 2j, 2j+1 of qs[32 n + l], sc = sc[8 n + 2 j +
+    l // 16]."""
+    rng = np.random.default_rng(2)
+    for _ in range(10):
+        blk = np.zeros(84, np.uint8)
+        sc = rng.integers(0, 256, 16, dtype=np.uint8)
+        qs = rng.integers(0, 256, 64, dtype=np.uint8)
+        blk[:16], blk[16:80] = sc, qs
+        blk[80:82] = np.array([0.5], np.float16).view(np.uint8)
+        blk[82:84] = np.array([0.25], np.float16).view(np.uint8)
+        want = np.zeros(256)
+        for n in range(2):
+            for j in range(4):
+                for l in range(32):
+                    s_ = int(sc[8 * n + 2 * j + l // 16])
+                    q = (int(qs[32 * n + l]) >> (2 * j)) & 3
+                    want[128 * n + 32 * j + l] = 0.5 * (s_ & 15) * q - 0.25 * (s_ >> 4)
+        assert np.array_equal(orc.fmt_dequant(Q2_K, blk, (256,)), want.astype(np.float32))
+
+
+def _pack_q3k_scales(sc):
+    """The 12 scale bytes of a Q3_K super-block holding 6-bit sc[0..15]
+    (stored as scale + 32): scale 4g + i keeps its low nibble in the low (g =
+    0, 1) or high (g = 2, 3) half of byte i (g even) or 4 + i (g odd), and its
+    top two bits in bits 2g, 2g + 1 of byte 8 + i."""
+    q = np.zeros(12, np.uint8)
+    for s_ in range(16):
+        g, i = divmod(s_, 4)
+        v = int(sc[s_])
+        q[(g & 1) * 4 + i] |= (v & 15) << (4 * (g >> 1))
+        q[8 + i] |= (v >> 4) << (2 * g)
+    return q
+
+
+def test_q3_k_scales_and_positions(orc):
+    """d = 0.25, scales (6-bit, minus 32) chosen: element 128 n + 32 j + l =
+    (d * (sc - 32)) * (q - 4 unless bit 4n + j of hmask[l] is set), q = bits
+    2j, 2j+1 of qs[32 n + l], scale 8 n + 2 j + l // 16."""
+    rng = np.random.default_rng(3)
+    for _ in range(10):
+        sc = rng.integers(0, 64, 16)
+        blk = np.zeros(110, np.uint8)
+        hm = rng.integers(0, 256, 32, dtype=np.uint8)
+        qs = rng.integers(0, 256, 64, dtype=np.uint8)
+        blk[:32], blk[32:96] = hm, qs
+        blk[96:108] = _pack_q3k_scales(sc)
+        blk[108:110] = np.array([0.25], np.float16).view(np.uint8)
+        want = np.zeros(256)
+        for n in range(2):
+            for j in range(4):
+                for l in range(32):
+                    q = (int(qs[32 * n + l]) >> (2 * j)) & 3
+                    q -= 0 if (int(hm[l]) >> (4 * n + j)) & 1 else 4
+                    want[128 * n + 32 * j + l] = 0.25 * (int(sc[8 * n + 2 * j + l // 16]) - 32) * q
+        assert np.array_equal(orc.fmt_dequant(Q3_K, blk, (256,)), want.astype(np.float32))
 
 
 @pytest.mark.parametrize("fmt", KQUANT)

@@ -12,15 +12,19 @@
 // aligned 16-byte code load plus small aligned side loads:
 //   q  codes: 16 bytes per sub-block, byte l holding element l in the low
 //      nibble and element l + 16 in the high one (Q8_0: 32 int8, in order);
-//   h  high bits: Q5_0/Q5_1/Q5_K one dword (bit e = bit 4 of element e),
-//      Q6_K 8 bytes (bits 2e, 2e + 1 = bits 4-5 of element e);
+//      Q2_K/Q3_K 8 bytes, byte b holding elements b, b + 8, b + 16, b + 24
+//      in bits 0-1, 2-3, 4-5, 6-7;
+//   h  high bits: Q5_0/Q5_1/Q5_K/Q3_K one dword (bit e = the top bit of
+//      element e), Q6_K 8 bytes (bits 2e, 2e + 1 = bits 4-5 of element e);
 //   s  scales: Q8_0/Q4_0/Q5_0 f16 d; Q4_1/Q5_1 f16 d then f16 m; Q4_K/Q5_K
 //      the super-block's 16-byte header (f16 d, f16 dmin, 12 scale bytes),
-//      2 bytes per sub-block; Q6_K the sub-block's two int8 scales;
-//   e  Q6_K only: the super-block's f16 d.
-// Every array holds exactly the packed bytes of its part, so a GEMV reads
-// the packed size (plus x and y). Rows are padded to a multiple of 16 with
-// zero bytes (zero scales: padding rows read as 0).
+//      2 bytes per sub-block; Q3_K likewise (12 scale bytes, f16 d, 2 zero
+//      bytes); Q2_K and Q6_K the sub-block's two scale bytes;
+//   e  per super-block: Q2_K f16 d and dmin, Q6_K f16 d.
+// Every array holds exactly the packed bytes of its part (Q3_K: 2 bytes of
+// padding per 110), so a GEMV reads the packed size (plus x and y). Rows are
+// padded to a multiple of 16 with zero bytes (zero scales: padding rows read
+// as 0).
 #include "common.h"
 #include "kernels.h"
 #include "wave.h"
@@ -193,6 +197,29 @@ __global__ __launch_bounds__(kThreads) void k_fmt_relayout(FmtArgs a, const uint
       for (int e = 0; e < 32; ++e) bits |= (uint32_t)((B[16 + e] >> sb) & 1) << e;
       for (int j = 0; j < 4; ++j) h[j] = (uint8_t)(bits >> (8 * j));
     }
+  } else if constexpr (FMT == kQ2_K || FMT == kQ3_K) {
+    // sub-block sb = 4 n + j: bits 2j, 2j + 1 of qs[32 n + l] (Q3_K: minus 4
+    // unless bit sb of hmask[l] is set); scales 2 sb, 2 sb + 1
+    constexpr int QS = FMT == kQ2_K ? 16 : 32;
+    const int n = sb / 4, j = sb % 4;
+    for (int b = 0; b < 8; ++b) {
+      uint8_t v = 0;
+      for (int f = 0; f < 4; ++f) v |= (uint8_t)(((B[QS + 32 * n + b + 8 * f] >> (2 * j)) & 3) << (2 * f));
+      q[b] = v;
+    }
+    if constexpr (FMT == kQ2_K) {
+      s[0] = B[2 * sb], s[1] = B[2 * sb + 1];
+      if (sb == 0) {
+        uint8_t* e = const_cast<uint8_t*>(a.e) + ((size_t)row * (a.nsub / SPB) + t / SPB) * 4;
+        for (int k = 0; k < 4; ++k) e[k] = B[80 + k];
+      }
+    } else {
+      uint32_t bits = 0;
+      for (int l = 0; l < 32; ++l) bits |= (uint32_t)((B[l] >> sb) & 1) << l;
+      for (int k = 0; k < 4; ++k) h[k] = (uint8_t)(bits >> (8 * k));
+      // header byte k: scales[k] (k < 12), d (12, 13), zero (14, 15)
+      for (int k = 2 * sb; k < 2 * sb + 2; ++k) s[k - 2 * sb] = k < 12 ? B[96 + k] : k < 14 ? B[108 + k - 12] : 0;
+    }
   } else {
     // Q6_K: sub-block sb = 4 n + t of half n: low 4 bits from nibble t >> 1
     // of ql[64 n + 32 (t & 1) + e], bits 4-5 from bits 2t, 2t + 1 of
@@ -228,6 +255,13 @@ __device__ __forceinline__ void decode_codes(const uint4 w0, const uint4 w1, uin
     for (int d = 0; d < 8; ++d)
 #pragma unroll
       for (int b = 0; b < 4; ++b) c[4 * d + b] = (float)(int8_t)(w[d] >> (8 * b));
+  } else if constexpr (FMT == kQ2_K || FMT == kQ3_K) {
+#pragma unroll
+    for (int e = 0; e < 32; ++e) {
+      int v = (int)((w[(e & 7) >> 2] >> (8 * (e & 3) + 2 * (e >> 3))) & 3);
+      if constexpr (FMT == kQ3_K) v += 4 * (int)((hb0 >> e) & 1) - 4;
+      c[e] = (float)v;
+    }
   } else {
 #pragma unroll
     for (int d = 0; d < 4; ++d)
@@ -262,7 +296,26 @@ __device__ __forceinline__ void scale_min_k4(int j, const uint8_t* q, int* sc, i
   }
 }
 
-// The same from the header's dwords 1-3 (scale bytes 0-11 at header bytes
+// Q3_K scale s (0..15) minus 32 from the 12 packed scale bytes: the low
+// (groups 0, 1) or high (2, 3) nibble of byte i (even group) or 4 + i (odd
+// group), and bits 2g, 2g + 1 of byte 8 + i for bits 4-5 (g = s / 4,
+// i = s % 4)
+__device__ __forceinline__ int scale_q3k(int s, const uint8_t* q) {
+  const int g = s >> 2, i = s & 3;
+  const int lo = (q[(g & 1) * 4 + i] >> ((g >> 1) * 4)) & 0xF;
+  const int hi = (q[8 + i] >> (2 * g)) & 3;
+  return (lo | (hi << 4)) - 32;
+}
+// the same from the header dwords a0 (scale bytes 0-3), a1 (4-7), tw (8-11)
+__device__ __forceinline__ int scale_q3k_regs(int s, uint32_t a0, uint32_t a1, uint32_t tw) {
+  const int g = s >> 2, i = s & 3;
+  const uint32_t src = (g & 1) ? a1 : a0;
+  const int lo = (int)((src >> (8 * i + 4 * (g >> 1))) & 0xFu);
+  const int hi = (int)((tw >> (8 * i + 2 * g)) & 3u);
+  return (lo | (hi << 4)) - 32;
+}
+
+// scale_min_k4 from the header's dwords 1-3 (scale bytes 0-11 at header bytes
 // 4-15) with selects only, no indexed register array: byte k + 4 of the
 // header is byte k of the scales.
 __device__ __forceinline__ void scale_min_k4_regs(int j, uint32_t h1, uint32_t h2, uint32_t h3,
@@ -291,7 +344,13 @@ __global__ __launch_bounds__(kThreads) void k_fmt_dequant(FmtArgs a, int rows, f
   const int row = (int)(i / a.nsub), t = (int)(i % a.nsub);
   const uint8_t* q = a.q + ((size_t)row * a.nsub + t) * G.qb;
   const uint8_t* s = a.s + ((size_t)row * a.nsub + t) * G.sb;
-  uint4 w0 = *reinterpret_cast<const uint4*>(q), w1 = make_uint4(0, 0, 0, 0);
+  uint4 w0 = make_uint4(0, 0, 0, 0), w1 = make_uint4(0, 0, 0, 0);
+  if constexpr (G.qb == 8) {
+    const uint2 v = *reinterpret_cast<const uint2*>(q);
+    w0.x = v.x, w0.y = v.y;
+  } else {
+    w0 = *reinterpret_cast<const uint4*>(q);
+  }
   if constexpr (FMT == kQ8_0) w1 = *reinterpret_cast<const uint4*>(q + 16);
   uint32_t hb0 = 0, hb1 = 0;
   if constexpr (G.hb >= 4) hb0 = *reinterpret_cast<const uint32_t*>(a.h + ((size_t)row * a.nsub + t) * G.hb);
@@ -311,6 +370,20 @@ __global__ __launch_bounds__(kThreads) void k_fmt_dequant(FmtArgs a, int rows, f
     scale_min_k4(t & 7, hd + 4, &sc, &m);
     const float d1 = f16f(ld16(hd)) * (float)sc, m1 = f16f(ld16(hd + 2)) * (float)m;
     for (int e = 0; e < 32; ++e) y[e] = d1 * c[e] - m1;
+  } else if constexpr (FMT == kQ2_K) {
+    const uint8_t* e = a.e + ((size_t)row * (a.nsub / 8) + t / 8) * 4;
+    const float d = f16f(ld16(e)), dmin = f16f(ld16(e + 2));
+    for (int h = 0; h < 2; ++h) {
+      const float dl = d * (float)(s[h] & 15), ml = dmin * (float)(s[h] >> 4);
+      for (int k = 16 * h; k < 16 * h + 16; ++k) y[k] = dl * c[k] - ml;
+    }
+  } else if constexpr (FMT == kQ3_K) {
+    const uint8_t* hd = a.s + ((size_t)row * a.nsub + (t & ~7)) * G.sb;  // super-block header
+    const float d = f16f(ld16(hd + 12));
+    for (int h = 0; h < 2; ++h) {
+      const float dl = d * (float)scale_q3k(2 * (t & 7) + h, hd);
+      for (int k = 16 * h; k < 16 * h + 16; ++k) y[k] = dl * c[k];
+    }
   } else {
     const float d = f16f(ld16(a.e + ((size_t)row * (a.nsub / 8) + t / 8) * 2));
     const float s0 = d * (float)(int8_t)s[0], s1 = d * (float)(int8_t)s[1];
@@ -391,6 +464,27 @@ __device__ __forceinline__ void dot_sub(const uint4 w, uint32_t h0, uint32_t h1,
   }
 }
 
+// Q2_K / Q3_K: 8 code bytes (byte b: elements b + 8f in bits 2f, 2f + 1);
+// Q3_K adds the high bit of element e (bit e of h) as bit 2 of its code
+template <bool Q3>
+__device__ __forceinline__ void dot_sub2(uint32_t w0, uint32_t w1, uint32_t h, const float* xv,
+                                         float& plo, float& phi) {
+#pragma unroll
+  for (int f = 0; f < 4; ++f) {
+    uint32_t u0 = (w0 >> (2 * f)) & 0x03030303u, u1 = (w1 >> (2 * f)) & 0x03030303u;
+    if constexpr (Q3) {
+      u0 |= spread1((h >> (8 * f)) & 0xFu) << 2;
+      u1 |= spread1((h >> (8 * f + 4)) & 0xFu) << 2;
+    }
+    float& p = f < 2 ? plo : phi;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      p = fmaf(ub(u0, b), xv[8 * f + b], p);
+      p = fmaf(ub(u1, b), xv[8 * f + 4 + b], p);
+    }
+  }
+}
+
 // Q8_0: int8 codes q; (q + 128) as unsigned bytes, the 128 taken off with
 // sum(x) by the caller
 __device__ __forceinline__ float dot_q8(const uint4 w0, const uint4 w1, const float* xv) {
@@ -410,7 +504,7 @@ __device__ __forceinline__ float dot_q8(const uint4 w0, const uint4 w1, const fl
 template <int FMT, int R, int WAVES>
 __global__ __launch_bounds__(64 * WAVES) void k_fmt_gemv(FmtArgs a) {
   constexpr FmtGeom G = fmt_geom(FMT);
-  constexpr int HB = FMT == kQ6_K ? 2 : G.hb ? 1 : 0;
+  constexpr int HB = FMT == kQ6_K ? 2 : G.hb ? 1 : 0;  // nibble formats
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r0 = blockIdx.x * R;
   const int nsub = a.nsub;
@@ -431,17 +525,23 @@ __global__ __launch_bounds__(64 * WAVES) void k_fmt_gemv(FmtArgs a) {
       }
       uint4 w0[R], w1[R];
       uint32_t h0[R], h1[R], sv[R], hd[R][4];
-      uint16_t ev[R];
+      uint32_t ev[R];
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const size_t sub = (size_t)(r0 + r) * nsub + t;
-        w0[r] = load_stream(a.q + sub * G.qb);
         w1[r] = make_uint4(0, 0, 0, 0);
+        if constexpr (G.qb == 8) {
+          typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+          const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(a.q + sub * 8));
+          w0[r] = make_uint4(v.x, v.y, 0u, 0u);
+        } else {
+          w0[r] = load_stream(a.q + sub * G.qb);
+        }
         if constexpr (FMT == kQ8_0) w1[r] = load_stream(a.q + sub * G.qb + 16);
         h0[r] = h1[r] = 0;
         if constexpr (G.hb >= 4) h0[r] = *reinterpret_cast<const uint32_t*>(a.h + sub * G.hb);
         if constexpr (G.hb == 8) h1[r] = *reinterpret_cast<const uint32_t*>(a.h + sub * G.hb + 4);
-        if constexpr (FMT == kQ4_K || FMT == kQ5_K) {
+        if constexpr (FMT == kQ4_K || FMT == kQ5_K || FMT == kQ3_K) {
           const uint4 v = *reinterpret_cast<const uint4*>(a.s + ((size_t)(r0 + r) * nsub + (t & ~7)) * G.sb);
           hd[r][0] = v.x, hd[r][1] = v.y, hd[r][2] = v.z, hd[r][3] = v.w;
           sv[r] = 0;
@@ -453,6 +553,8 @@ __global__ __launch_bounds__(64 * WAVES) void k_fmt_gemv(FmtArgs a) {
         ev[r] = 0;
         if constexpr (FMT == kQ6_K)
           ev[r] = *reinterpret_cast<const uint16_t*>(a.e + ((size_t)(r0 + r) * (nsub / 8) + t / 8) * 2);
+        if constexpr (FMT == kQ2_K)
+          ev[r] = *reinterpret_cast<const uint32_t*>(a.e + ((size_t)(r0 + r) * (nsub / 8) + t / 8) * 4);
       }
       __builtin_amdgcn_sched_barrier(0);
       float sx_lo = 0.0f, sx_hi = 0.0f;
@@ -467,6 +569,23 @@ __global__ __launch_bounds__(64 * WAVES) void k_fmt_gemv(FmtArgs a) {
         float v;
         if constexpr (FMT == kQ8_0) {
           v = f16f((uint16_t)sv[r]) * fmaf(-128.0f, sx, dot_q8(w0[r], w1[r], xv));
+        } else if constexpr (FMT == kQ2_K || FMT == kQ3_K) {
+          float plo = 0.0f, phi = 0.0f;
+          dot_sub2<FMT == kQ3_K>(w0[r].x, w0[r].y, h0[r], xv, plo, phi);
+          if constexpr (FMT == kQ2_K) {
+            // (d * sc) * sum(q x) - (dmin * m) * sum(x) per 16-element half
+            const float d = f16f((uint16_t)ev[r]), dmin = f16f((uint16_t)(ev[r] >> 16));
+            const float s0 = (float)(sv[r] & 15u), s1 = (float)((sv[r] >> 8) & 15u);
+            const float m0 = (float)((sv[r] >> 4) & 15u), m1 = (float)((sv[r] >> 12) & 15u);
+            v = fmaf(d, fmaf(s1, phi, s0 * plo), -dmin * fmaf(m1, sx_hi, m0 * sx_lo));
+          } else {
+            // codes 0..7 with offset 4, signed 6-bit scale per 16-element half
+            const int j = t & 7;
+            const float s0 = (float)scale_q3k_regs(2 * j, hd[r][0], hd[r][1], hd[r][2]);
+            const float s1 = (float)scale_q3k_regs(2 * j + 1, hd[r][0], hd[r][1], hd[r][2]);
+            const float lo = fmaf(-4.0f, sx_lo, plo), hi = fmaf(-4.0f, sx_hi, phi);
+            v = f16f((uint16_t)hd[r][3]) * fmaf(s1, hi, s0 * lo);
+          }
         } else {
           float plo = 0.0f, phi = 0.0f;
           dot_sub<HB>(w0[r], h0[r], h1[r], xv, plo, phi);
@@ -566,19 +685,6 @@ Status dequant_f(const FmtArgs& a, int rows, float* out, hipStream_t st) {
 
 }  // namespace
 
-#define WV_FMT_DISPATCH(fmt, call)                             \
-  switch (fmt) {                                               \
-  case kQ8_0: return call<kQ8_0>;                              \
-  case kQ4_0: return call<kQ4_0>;                              \
-  case kQ4_1: return call<kQ4_1>;                              \
-  case kQ5_0: return call<kQ5_0>;                              \
-  case kQ5_1: return call<kQ5_1>;                              \
-  case kQ4_K: return call<kQ4_K>;                              \
-  case kQ5_K: return call<kQ5_K>;                              \
-  case kQ6_K: return call<kQ6_K>;                              \
-  default: return Status::err(kGap, "gap? quant format not implemented"); \
-  }
-
 Status format_quantize(int fmt, const float* W, int64_t n, uint8_t* out, hipStream_t st) {
   if (n % 32) return Status::err(kInvalid, "format quantize: element count");
   switch (fmt) {
@@ -600,6 +706,8 @@ Status format_relayout(int fmt, const FmtArgs& a, const uint8_t* blocks, int row
   case kQ4_1: return relayout_f<kQ4_1>(a, blocks, rows, st);
   case kQ5_0: return relayout_f<kQ5_0>(a, blocks, rows, st);
   case kQ5_1: return relayout_f<kQ5_1>(a, blocks, rows, st);
+  case kQ2_K: return relayout_f<kQ2_K>(a, blocks, rows, st);
+  case kQ3_K: return relayout_f<kQ3_K>(a, blocks, rows, st);
   case kQ4_K: return relayout_f<kQ4_K>(a, blocks, rows, st);
   case kQ5_K: return relayout_f<kQ5_K>(a, blocks, rows, st);
   case kQ6_K: return relayout_f<kQ6_K>(a, blocks, rows, st);
@@ -614,6 +722,8 @@ Status format_dequant(int fmt, const FmtArgs& a, int rows, float* out, hipStream
   case kQ4_1: return dequant_f<kQ4_1>(a, rows, out, st);
   case kQ5_0: return dequant_f<kQ5_0>(a, rows, out, st);
   case kQ5_1: return dequant_f<kQ5_1>(a, rows, out, st);
+  case kQ2_K: return dequant_f<kQ2_K>(a, rows, out, st);
+  case kQ3_K: return dequant_f<kQ3_K>(a, rows, out, st);
   case kQ4_K: return dequant_f<kQ4_K>(a, rows, out, st);
   case kQ5_K: return dequant_f<kQ5_K>(a, rows, out, st);
   case kQ6_K: return dequant_f<kQ6_K>(a, rows, out, st);
@@ -631,6 +741,8 @@ Status launch_format_gemv(int fmt, const FmtArgs& a, int batch, hipStream_t st) 
   case kQ4_1: return gemv_f<kQ4_1>(a, batch, st);
   case kQ5_0: return gemv_f<kQ5_0>(a, batch, st);
   case kQ5_1: return gemv_f<kQ5_1>(a, batch, st);
+  case kQ2_K: return gemv_f<kQ2_K>(a, batch, st);
+  case kQ3_K: return gemv_f<kQ3_K>(a, batch, st);
   case kQ4_K: return gemv_f<kQ4_K>(a, batch, st);
   case kQ5_K: return gemv_f<kQ5_K>(a, batch, st);
   case kQ6_K: return gemv_f<kQ6_K>(a, batch, st);

@@ -249,6 +249,8 @@ constexpr FmtGeom fmt_geom(int fmt) {
          : fmt == kQ4_1 ? FmtGeom{32, 20, 16, 0, 4, 0}
          : fmt == kQ5_0 ? FmtGeom{32, 22, 16, 4, 2, 0}
          : fmt == kQ5_1 ? FmtGeom{32, 24, 16, 4, 4, 0}
+         : fmt == kQ2_K ? FmtGeom{256, 84, 8, 0, 2, 4}
+         : fmt == kQ3_K ? FmtGeom{256, 110, 8, 4, 2, 0}
          : fmt == kQ4_K ? FmtGeom{256, 144, 16, 0, 2, 0}
          : fmt == kQ5_K ? FmtGeom{256, 176, 16, 4, 2, 0}
          : fmt == kQ6_K ? FmtGeom{256, 210, 16, 8, 2, 2}
@@ -258,7 +260,7 @@ struct FmtArgs {
   const uint8_t* q = nullptr;  // [rpad][nsub][qb]
   const uint8_t* h = nullptr;  // [rpad][nsub][hb]
   const uint8_t* s = nullptr;  // [rpad][nsub][sb]
-  const uint8_t* e = nullptr;  // [rpad][nsub / 8][eb]
+  const uint8_t* e = nullptr;  // [rpad][nsub / 8][eb] (Q2_K d, dmin; Q6_K d)
   int rows = 0, cols = 0, nsub = 0;  // nsub = cols / 32
   const float* x = nullptr;
   int x_stride = 0;
