@@ -22,6 +22,19 @@ namespace {
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+
+// x as three bf16 terms hi + mid + lo, each rounding the remainder of the
+// previous ones (to nearest even): x - hi - mid - lo is below 2^-24 |x|
+// (three 8-bit significands)
+__device__ __forceinline__ void split3(float x, __bf16 (&t)[3]) {
+  const __bf16 hi = (__bf16)x;
+  const float r1 = x - (float)hi;
+  const __bf16 mid = (__bf16)r1;
+  t[0] = hi;
+  t[1] = mid;
+  t[2] = (__bf16)(r1 - (float)mid);
+}
 
 __device__ __forceinline__ bool allow(int qp, int kp, const AttnArgs& a) {
   if (a.mask == 2) return true;
@@ -185,12 +198,16 @@ __global__ __launch_bounds__(64) void k_attention(AttnArgs a) {
 // summation order differs from the per-position loop.
 //
 // A workgroup of 8 waves takes 128 queries (16 per wave) of one (batch,
-// head) and walks the distinct rows in tiles of 64 keys staged in LDS (rows
-// padded to hd + 4 floats: conflict-free reads below), double-buffered
-// through registers, one barrier per tile. Per 16-key
-// block a wave runs
-//   S^T = K Q^T  (v_mfma_f32_16x16x4f32, hd/4 steps): lane l holds the
-//                scores of query l%16 for keys 4*(l/16) + i, i = 0..3;
+// head) and walks the distinct rows in tiles of 64 keys staged in LDS in
+// matrix-core operand order, double-buffered through registers, one barrier
+// per tile. Per 16-key block a wave runs
+//   S^T = K Q^T  on the bf16 matrix cores (v_mfma_f32_16x16x32_bf16, hd/32
+//                steps), K and Q each split into three bf16 terms hi + mid +
+//                lo (x - hi - mid - lo ~ 2^-24 |x|) and the six products
+//                down to 2^-18 relative kept (hh, hm, mh, hl, lh, mm): the
+//                dropped ones are below 2^-26, so the scores carry fp32
+//                accuracy. Lane l holds the scores of query l%16 for keys
+//                4*(l/16) + i, i = 0..3;
 //   O^T += V^T P^T: the same 4 values per lane are the B operand (MFMA k
 //                index l/16 <-> key 4*(l/16) + j at step j), V^T the A
 //                operand, so no transpose is needed.
@@ -207,11 +224,13 @@ constexpr int kKT = 64;               // keys per LDS tile
 template <int HD, bool SIG>
 __global__ __launch_bounds__(64 * kAttnWaves) __attribute__((amdgpu_waves_per_eu(HD <= 64 ? 4 : 2, 8)))
 void k_attn_mfma(AttnArgs a, int qblocks) {
-  constexpr int ST = HD / 4;                            // QK MFMA steps
+  constexpr int KS = HD / 32;                           // QK MFMA steps (32 head dims)
   constexpr int DT = HD / 16;                           // 16-wide head-dim tiles of O
-  constexpr int ROW = HD + 4;                           // padded LDS row (floats)
   constexpr int NT = 64 * kAttnWaves;                   // threads
-  __shared__ float ks[2][kKT * ROW];
+  // K in bf16 operand order: [16-key block kb][step ks][hi, mid, lo][lane][8]:
+  // lane 16 g + c16 holds key 16 kb + c16, head dims 32 ks + 8 g + j
+  constexpr int KBYTES = 4 * KS * 3 * 1024;
+  __shared__ __attribute__((aligned(16))) uint8_t ksb[2][KBYTES];
   // V in bf16 operand order: [32-key group q][head-dim tile dt][hi, lo][lane][8]
   constexpr int VBYTES = 2 * DT * 2 * 1024;
   __shared__ __attribute__((aligned(16))) uint8_t vsb[2][VBYTES];
@@ -232,11 +251,22 @@ void k_attn_mfma(AttnArgs a, int qblocks) {
   const float scale_log2 = (float)(a.scale * 1.4426950408889634);
   const float scale_nat = (float)a.scale;
 
-  float qr[ST];
+  // Q operand: lane (query c16, group g), head dims 32 ks + 8 g + j, as
+  // three bf16 terms
+  bf16x8 qop[KS][3];
   {
     const float* qrow = a.q + (size_t)qp * qd + (size_t)h * HD;
 #pragma unroll
-    for (int st = 0; st < ST; ++st) qr[st] = qrow[4 * st + g];
+    for (int ks = 0; ks < KS; ++ks) {
+      const v4f q0 = *reinterpret_cast<const v4f*>(qrow + 32 * ks + 8 * g);
+      const v4f q1 = *reinterpret_cast<const v4f*>(qrow + 32 * ks + 8 * g + 4);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        __bf16 t3[3];
+        split3(j < 4 ? q0[j] : q1[j - 4], t3);
+        qop[ks][0][j] = t3[0], qop[ks][1][j] = t3[1], qop[ks][2][j] = t3[2];
+      }
+    }
   }
   v4f o[DT];
 #pragma unroll
@@ -279,14 +309,33 @@ void k_attn_mfma(AttnArgs a, int qblocks) {
       vreg[2 * u + 1] = p <= last ? v1 : z;
     }
   };
+  // K row r, head dims d..d+3 (d = c4 or c4 + HD/2, a multiple of 4) go to
+  // block r / 16, step d / 32, lane 16 ((d / 8) % 4) + r % 16, elements
+  // d % 8 .. + 3: one 8-byte store per term
   auto store_k = [&](int buf) {
 #pragma unroll
     for (int u = 0; u < PU; ++u) {
       const int i = tid + NT * u;
       if (UNITS % NT != 0 && i >= UNITS) break;
       const int r = i / (HD / 8), c4 = (i % (HD / 8)) * 4;
-      *reinterpret_cast<v4f*>(&ks[buf][r * ROW + c4]) = kreg[2 * u];
-      *reinterpret_cast<v4f*>(&ks[buf][r * ROW + c4 + HD / 2]) = kreg[2 * u + 1];
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const int d = c4 + half * (HD / 2);
+        __bf16 t[3][4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          __bf16 t3[3];
+          split3(kreg[2 * u + half][e], t3);
+          t[0][e] = t3[0], t[1][e] = t3[1], t[2][e] = t3[2];
+        }
+        uint8_t* dst = ksb[buf] + (size_t)(((r >> 4) * KS + (d >> 5)) * 3) * 1024 +
+                       (((d >> 3) & 3) * 16 + (r & 15)) * 16 + (d & 7) * 2;
+#pragma unroll
+        for (int term = 0; term < 3; ++term) {
+          bf16x4 v = {t[term][0], t[term][1], t[term][2], t[term][3]};
+          *reinterpret_cast<bf16x4*>(dst + term * 1024) = v;
+        }
+      }
     }
   };
   // V row r (key) and head dim d go to the bf16 A operand of the P V
@@ -315,15 +364,24 @@ void k_attn_mfma(AttnArgs a, int qblocks) {
         }
     }
   };
-  // S^T of a tile: 4 blocks of 16 keys
-  auto scores = [&](const float* kt, v4f (&sc)[4]) {
+  // S^T of a tile: 4 blocks of 16 keys; the small products first
+  auto scores = [&](const uint8_t* kt, v4f (&sc)[4]) {
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
       sc[kb] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int st = 0; st < ST; ++st)
-        sc[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kt[(16 * kb + c16) * ROW + 4 * st + g], qr[st],
-                                                      sc[kb], 0, 0, 0);
+      for (int ks = 0; ks < KS; ++ks) {
+        const uint8_t* kp = kt + (size_t)((kb * KS + ks) * 3) * 1024 + lane * 16;
+        const bf16x8 kh = *reinterpret_cast<const bf16x8*>(kp);
+        const bf16x8 km = *reinterpret_cast<const bf16x8*>(kp + 1024);
+        const bf16x8 kl = *reinterpret_cast<const bf16x8*>(kp + 2048);
+        sc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(km, qop[ks][1], sc[kb], 0, 0, 0);
+        sc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, qop[ks][2], sc[kb], 0, 0, 0);
+        sc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl, qop[ks][0], sc[kb], 0, 0, 0);
+        sc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, qop[ks][1], sc[kb], 0, 0, 0);
+        sc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(km, qop[ks][0], sc[kb], 0, 0, 0);
+        sc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, qop[ks][0], sc[kb], 0, 0, 0);
+      }
     }
   };
 
@@ -342,7 +400,7 @@ void k_attn_mfma(AttnArgs a, int qblocks) {
     load_k(t0 + kKT);
     load_v(t0 + kKT);
     v4f sc[4];
-    scores(ks[cur], sc);
+    scores(ksb[cur], sc);
     const uint8_t* vt = vsb[cur];
     // multiplicity base of the tile start: floor(t0 / msl) + 1 (msl >= 64, so
     // the tile crosses at most one multiple of msl)
