@@ -399,8 +399,6 @@ void k_attn_mfma(AttnArgs a, int qblocks) {
   for (int t0 = p_lo, cur = 0; t0 <= last; t0 += kKT, cur ^= 1) {
     load_k(t0 + kKT);
     load_v(t0 + kKT);
-    v4f sc[4];
-    scores(ksb[cur], sc);
     const uint8_t* vt = vsb[cur];
     // multiplicity base of the tile start: floor(t0 / msl) + 1 (msl >= 64, so
     // the tile crosses at most one multiple of msl)
@@ -413,27 +411,53 @@ void k_attn_mfma(AttnArgs a, int qblocks) {
       const float c = p <= last ? base0f + (p >= next_mult ? 1.0f : 0.0f) : 0.0f;
       return c - (causal && p > qp ? 1.0f : 0.0f);
     };
+    // Most tiles give every key of the wave the same multiplicity: wholly
+    // inside [p_lo, last], not crossing a multiple of msl, and wholly at or
+    // below (c = base) or wholly above (c = base - 1, causal) the wave's 16
+    // queries. cu is that value (wave-uniform), or -1 for per-key values; a
+    // tile with cu == 0 adds nothing to this wave's queries.
+    const int kmax = t0 + kKT - 1;
+    const int qw0 = b * a.seq + qb * kQB + __builtin_amdgcn_readfirstlane(wave) * 16;
+    int cu = -1;
+    if (kmax <= last && next_mult > kmax) {
+      if (!causal || kmax <= qw0) cu = base0;
+      else if (t0 > qw0 + 15) cu = base0 - 1;
+    }
+    if (cu != 0) {  // wave-uniform
+    v4f sc[4];
+    scores(ksb[cur], sc);
     float w[16];
     if constexpr (SIG) {
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float c = mult(kb, i);
+          const float c = cu > 0 ? (float)cu : mult(kb, i);
           w[4 * kb + i] = c > 0.0f ? c / (1.0f + expf(-sc[kb][i] * scale_nat)) : 0.0f;
         }
     } else {
       // base-2 scores with the multiplicity folded into the exponent
       // (c 2^x = 2^(x + log2 c)); masked keys at -inf
       float smax = -INFINITY;
+      if (cu > 0) {
+        const float lc = __builtin_amdgcn_logf((float)cu);
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
+        for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float c = mult(kb, i);
-          w[4 * kb + i] = c > 0.0f ? sc[kb][i] * scale_log2 + __builtin_amdgcn_logf(c) : -INFINITY;
-          smax = fmaxf(smax, w[4 * kb + i]);
-        }
+          for (int i = 0; i < 4; ++i) {
+            w[4 * kb + i] = sc[kb][i] * scale_log2 + lc;
+            smax = fmaxf(smax, w[4 * kb + i]);
+          }
+      } else {
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float c = mult(kb, i);
+            w[4 * kb + i] = c > 0.0f ? sc[kb][i] * scale_log2 + __builtin_amdgcn_logf(c) : -INFINITY;
+            smax = fmaxf(smax, w[4 * kb + i]);
+          }
+      }
       smax = fmaxf(smax, __shfl_xor(smax, 16, 64));
       smax = fmaxf(smax, __shfl_xor(smax, 32, 64));
       const float nm = fmaxf(m, smax);
@@ -476,6 +500,7 @@ void k_attn_mfma(AttnArgs a, int qblocks) {
         o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, pl, o[d], 0, 0, 0);
         o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vl, ph, o[d], 0, 0, 0);
       }
+    }
     }
     store_k(cur ^ 1);
     store_v(cur ^ 1);
