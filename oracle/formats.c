@@ -15,7 +15,8 @@
  * -ffp-contract=off), left to right as written below.
  *
  * Format ids follow the README's table order: 1 Q8_0, 2 Q4_0, 3 Q4_1,
- * 4 Q5_0, 5 Q5_1, 6 Q2_K, 7 Q3_K, 8 Q4_K, 9 Q5_K, 10 Q6_K.
+ * 4 Q5_0, 5 Q5_1, 6 Q2_K, 7 Q3_K, 8 Q4_K, 9 Q5_K, 10 Q6_K, 16 IQ4_NL,
+ * 17 IQ4_XS.
  */
 #include <float.h>
 #include <math.h>
@@ -82,8 +83,10 @@ uint16_t or_f32_to_f16(float f) {
 int or_fmt_block_elems(int fmt) {
   switch (fmt) {
   case OR_FMT_Q8_0: case OR_FMT_Q4_0: case OR_FMT_Q4_1: case OR_FMT_Q5_0: case OR_FMT_Q5_1:
+  case OR_FMT_IQ4_NL:
     return 32;
   case OR_FMT_Q2_K: case OR_FMT_Q3_K: case OR_FMT_Q4_K: case OR_FMT_Q5_K: case OR_FMT_Q6_K:
+  case OR_FMT_IQ4_XS:
     return 256;
   default:
     return 0;
@@ -102,6 +105,8 @@ int or_fmt_block_bytes(int fmt) {
   case OR_FMT_Q4_K: return 144; /* f16 d, f16 dmin, scales[12], qs[128] */
   case OR_FMT_Q5_K: return 176; /* f16 d, f16 dmin, scales[12], qh[32], qs[128] */
   case OR_FMT_Q6_K: return 210; /* ql[128], qh[64], int8 scales[16], f16 d */
+  case OR_FMT_IQ4_NL: return 18; /* f16 d, qs[16] (indices into the 16-value table) */
+  case OR_FMT_IQ4_XS: return 136; /* f16 d, u16 scales_h, scales_l[4], qs[128] */
   default: return 0;
   }
 }
@@ -248,6 +253,10 @@ static int scale_q3k(int s, const uint8_t* q) {
   return (lo | (hi << 4)) - 32;
 }
 
+/* ggml's non-linear 4-bit code book of IQ4_NL and IQ4_XS (kvalues_iq4nl). */
+static const int8_t kIq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
+                                  1,    13,   25,  38,  53,  69,  89,  113};
+
 static void dequant_block(int fmt, const uint8_t* b, float* y) {
   switch (fmt) {
   case OR_FMT_Q8_0: { /* y = q * d */
@@ -350,6 +359,31 @@ static void dequant_block(int fmt, const uint8_t* b, float* y) {
           const int q = lo - (((hm[l] >> (4 * n + j)) & 1) ? 0 : 4);
           y[128 * n + 32 * j + l] = dl * (float)q;
         }
+    break;
+  }
+  case OR_FMT_IQ4_NL: { /* y = d * table[index]; element j low nibble of qs[j], j + 16 high */
+    const float d = or_f16_to_f32(get16(b));
+    for (int j = 0; j < 16; ++j) {
+      y[j] = d * (float)kIq4nl[b[2 + j] & 15];
+      y[j + 16] = d * (float)kIq4nl[b[2 + j] >> 4];
+    }
+    break;
+  }
+  case OR_FMT_IQ4_XS: {
+    /* 8 sub-blocks of 32: 6-bit scale ls = nibble (ib & 1) of scales_l[ib / 2]
+     * | bits 2ib, 2ib+1 of scales_h << 4; y = (d * (ls - 32)) * table[index],
+     * indices of sub-block ib in qs[16 ib ..] as IQ4_NL */
+    const float d = or_f16_to_f32(get16(b));
+    const int sh = get16(b + 2);
+    for (int ib = 0; ib < 8; ++ib) {
+      const int ls = ((b[4 + ib / 2] >> (4 * (ib & 1))) & 15) | (((sh >> (2 * ib)) & 3) << 4);
+      const float dl = d * (float)(ls - 32);
+      const uint8_t* qs = b + 8 + 16 * ib;
+      for (int j = 0; j < 16; ++j) {
+        y[32 * ib + j] = dl * (float)kIq4nl[qs[j] & 15];
+        y[32 * ib + j + 16] = dl * (float)kIq4nl[qs[j] >> 4];
+      }
+    }
     break;
   }
   case OR_FMT_Q6_K: {

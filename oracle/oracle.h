@@ -149,7 +149,8 @@ void or_swiglu_bwd_product(const float* g, const float* u, const float* gh, floa
  * idempotence on their own grids. Parity against ggml itself: unpinned (no
  * ggml output is in the image). */
 enum { OR_FMT_Q8_0 = 1, OR_FMT_Q4_0 = 2, OR_FMT_Q4_1 = 3, OR_FMT_Q5_0 = 4, OR_FMT_Q5_1 = 5,
-       OR_FMT_Q2_K = 6, OR_FMT_Q3_K = 7, OR_FMT_Q4_K = 8, OR_FMT_Q5_K = 9, OR_FMT_Q6_K = 10 };
+       OR_FMT_Q2_K = 6, OR_FMT_Q3_K = 7, OR_FMT_Q4_K = 8, OR_FMT_Q5_K = 9, OR_FMT_Q6_K = 10,
+       OR_FMT_IQ4_NL = 16, OR_FMT_IQ4_XS = 17 };
 float or_f16_to_f32(uint16_t h);
 uint16_t or_f32_to_f16(float f);
 /* elements per block (32 or 256) and packed bytes per block; 0 unsupported */

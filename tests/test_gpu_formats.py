@@ -191,7 +191,7 @@ def test_errors_and_gaps(gpu):
         return gpu.FormatDenseSession(args["batch"], args["in_dim"], args["out_dim"], args["act"],
                                       args["fmt"], W=args["W"], blocks=args["blocks"])
 
-    for fmt in (11, 12, 15, 17, 18, 20):  # listed by the reference, not built here
+    for fmt in (11, 12, 13, 14, 15, 18, 19, 20):  # listed by the reference, not built here
         with pytest.raises(gpu.WelvetError) as e:
             mount(fmt=fmt, W=W)
         assert e.value.code == 3

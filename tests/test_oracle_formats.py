@@ -11,8 +11,8 @@ its header."""
 import numpy as np
 import pytest
 
-from format_blocks import GEOM, KQUANT, LEGACY, Q2_K, Q3_K, Q4_0, Q4_1, Q4_K, Q5_0, Q5_1, Q5_K, \
-    Q6_K, Q8_0, random_blocks
+from format_blocks import GEOM, IQ, IQ4_NL, IQ4_XS, IQ4NL_TABLE, KQUANT, LEGACY, Q2_K, Q3_K, Q4_0, \
+    Q4_1, Q4_K, Q5_0, Q5_1, Q5_K, Q6_K, Q8_0, random_blocks
 from oracle_lib import Oracle
 
 
@@ -264,7 +264,47 @@ def test_q3_k_scales_and_positions(orc):
         assert np.array_equal(orc.fmt_dequant(Q3_K, blk, (256,)), want.astype(np.float32))
 
 
-@pytest.mark.parametrize("fmt", KQUANT)
+def test_iq4_nl_codebook_and_positions(orc):
+    """d = 1: element j takes the table value of the low nibble of qs[j],
+    element j + 16 that of its high nibble; every code appears."""
+    table = np.array(IQ4NL_TABLE, np.float32)
+    rng = np.random.default_rng(16)
+    for _ in range(5):
+        blk = np.zeros(18, np.uint8)
+        blk[:2] = np.array([1.0], np.float16).view(np.uint8)
+        lo, hi = rng.permutation(16), rng.integers(0, 16, 16)
+        blk[2:] = lo | (hi << 4)
+        want = np.concatenate([table[lo], table[hi]])
+        assert np.array_equal(orc.fmt_dequant(IQ4_NL, blk, (32,)), want)
+
+
+def test_iq4_xs_scales_and_positions(orc):
+    """d = 0.5, 6-bit scales ls[8] chosen (low nibble of sub-block ib in nibble
+    ib & 1 of scales_l[ib / 2], top two bits in bits 2ib, 2ib + 1 of
+    scales_h): element 32 ib + e = (d * (ls - 32)) * table[code]."""
+    table = np.array(IQ4NL_TABLE, np.float64)
+    rng = np.random.default_rng(17)
+    for _ in range(10):
+        ls = rng.integers(0, 64, 8)
+        blk = np.zeros(136, np.uint8)
+        blk[:2] = np.array([0.5], np.float16).view(np.uint8)
+        sh = 0
+        for ib in range(8):
+            blk[4 + ib // 2] |= (int(ls[ib]) & 15) << (4 * (ib & 1))
+            sh |= (int(ls[ib]) >> 4) << (2 * ib)
+        blk[2:4] = np.array([sh], np.uint16).view(np.uint8)
+        qs = rng.integers(0, 256, 128, dtype=np.uint8)
+        blk[8:] = qs
+        want = np.zeros(256)
+        for ib in range(8):
+            for e in range(32):
+                byte = int(qs[16 * ib + (e % 16)])
+                code = byte & 15 if e < 16 else byte >> 4
+                want[32 * ib + e] = 0.5 * (int(ls[ib]) - 32) * table[code]
+        assert np.array_equal(orc.fmt_dequant(IQ4_XS, blk, (256,)), want.astype(np.float32))
+
+
+@pytest.mark.parametrize("fmt", KQUANT + IQ)
 def test_k_formats_have_no_quantizer(orc, fmt):
     x = np.zeros(256, np.float32)
     out = np.zeros(GEOM[fmt][1], np.uint8)
@@ -272,7 +312,7 @@ def test_k_formats_have_no_quantizer(orc, fmt):
     assert orc.L.or_fmt_quantize(fmt, 256, _f(x), _u8(out)) == -1
 
 
-@pytest.mark.parametrize("fmt", KQUANT + LEGACY)
+@pytest.mark.parametrize("fmt", KQUANT + LEGACY + IQ)
 def test_random_blocks_decode_finite(orc, fmt):
     rng = np.random.default_rng(fmt + 50)
     b = random_blocks(fmt, 8, 512, rng)

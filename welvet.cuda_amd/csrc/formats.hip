@@ -19,7 +19,9 @@
 //   s  scales: Q8_0/Q4_0/Q5_0 f16 d; Q4_1/Q5_1 f16 d then f16 m; Q4_K/Q5_K
 //      the super-block's 16-byte header (f16 d, f16 dmin, 12 scale bytes),
 //      2 bytes per sub-block; Q3_K likewise (12 scale bytes, f16 d, 2 zero
-//      bytes); Q2_K and Q6_K the sub-block's two scale bytes;
+//      bytes); Q2_K and Q6_K the sub-block's two scale bytes; IQ4_NL f16 d;
+//      IQ4_XS the super-block's 8-byte header (f16 d, scales_h, scales_l),
+//      1 byte per sub-block;
 //   e  per super-block: Q2_K f16 d and dmin, Q6_K f16 d.
 // Every array holds exactly the packed bytes of its part (Q3_K: 2 bytes of
 // padding per 110), so a GEMV reads the packed size (plus x and y). Rows are
@@ -197,6 +199,12 @@ __global__ __launch_bounds__(kThreads) void k_fmt_relayout(FmtArgs a, const uint
       for (int e = 0; e < 32; ++e) bits |= (uint32_t)((B[16 + e] >> sb) & 1) << e;
       for (int j = 0; j < 4; ++j) h[j] = (uint8_t)(bits >> (8 * j));
     }
+  } else if constexpr (FMT == kIQ4_NL || FMT == kIQ4_XS) {
+    // table indices in Q4_0's nibble order; IQ4_XS sub-block sb at qs[16 sb]
+    constexpr int QS = FMT == kIQ4_NL ? 2 : 8;
+    for (int j = 0; j < 16; ++j) q[j] = B[QS + 16 * sb + j];
+    if constexpr (FMT == kIQ4_NL) s[0] = B[0], s[1] = B[1];
+    else s[0] = B[sb];  // header byte sb
   } else if constexpr (FMT == kQ2_K || FMT == kQ3_K) {
     // sub-block sb = 4 n + j: bits 2j, 2j + 1 of qs[32 n + l] (Q3_K: minus 4
     // unless bit sb of hmask[l] is set); scales 2 sb, 2 sb + 1
@@ -243,6 +251,19 @@ __global__ __launch_bounds__(kThreads) void k_fmt_relayout(FmtArgs a, const uint
   }
 }
 
+// IQ4_NL / IQ4_XS code book (ggml's kvalues_iq4nl) plus 128, as bytes:
+// {1, 24, 45, 63, 79, 93, 106, 118, 129, 141, 153, 166, 181, 197, 217, 241}
+constexpr uint32_t kIqT0 = 0x3F2D1801u, kIqT1 = 0x766A5D4Fu, kIqT2 = 0xA6998D81u, kIqT3 = 0xF1D9C5B5u;
+// the table entries (value + 128) of the four indices (0..15) in the bytes of
+// idx: two byte permutes and a blend on bit 3 of each index
+__device__ __forceinline__ uint32_t iq4_lookup(uint32_t idx) {
+  const uint32_t sel = idx & 0x07070707u;
+  const uint32_t lo = __builtin_amdgcn_perm(kIqT1, kIqT0, sel);
+  const uint32_t hi = __builtin_amdgcn_perm(kIqT3, kIqT2, sel);
+  const uint32_t mask = ((idx >> 3) & 0x01010101u) * 0xFFu;
+  return (hi & mask) | (lo & ~mask);
+}
+
 // ---- decode of one lane's sub-block into 32 f32 code values ---------------
 // c[e] = the integer the format multiplies by its scale for element e (the
 // offset of the symmetric formats already removed).
@@ -255,6 +276,16 @@ __device__ __forceinline__ void decode_codes(const uint4 w0, const uint4 w1, uin
     for (int d = 0; d < 8; ++d)
 #pragma unroll
       for (int b = 0; b < 4; ++b) c[4 * d + b] = (float)(int8_t)(w[d] >> (8 * b));
+  } else if constexpr (FMT == kIQ4_NL || FMT == kIQ4_XS) {
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      const uint32_t lo = iq4_lookup(w[d] & 0x0F0F0F0Fu), hi = iq4_lookup((w[d] >> 4) & 0x0F0F0F0Fu);
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        c[4 * d + b] = (float)((int)((lo >> (8 * b)) & 0xFFu) - 128);
+        c[4 * d + b + 16] = (float)((int)((hi >> (8 * b)) & 0xFFu) - 128);
+      }
+    }
   } else if constexpr (FMT == kQ2_K || FMT == kQ3_K) {
 #pragma unroll
     for (int e = 0; e < 32; ++e) {
@@ -370,6 +401,15 @@ __global__ __launch_bounds__(kThreads) void k_fmt_dequant(FmtArgs a, int rows, f
     scale_min_k4(t & 7, hd + 4, &sc, &m);
     const float d1 = f16f(ld16(hd)) * (float)sc, m1 = f16f(ld16(hd + 2)) * (float)m;
     for (int e = 0; e < 32; ++e) y[e] = d1 * c[e] - m1;
+  } else if constexpr (FMT == kIQ4_NL) {
+    const float d = f16f(ld16(s));
+    for (int e = 0; e < 32; ++e) y[e] = d * c[e];
+  } else if constexpr (FMT == kIQ4_XS) {
+    const uint8_t* hd = a.s + ((size_t)row * a.nsub + (t & ~7));  // super-block header
+    const int ib = t & 7, sh = ld16(hd + 2);
+    const int ls = ((hd[4 + ib / 2] >> (4 * (ib & 1))) & 15) | (((sh >> (2 * ib)) & 3) << 4);
+    const float dl = f16f(ld16(hd)) * (float)(ls - 32);
+    for (int e = 0; e < 32; ++e) y[e] = dl * c[e];
   } else if constexpr (FMT == kQ2_K) {
     const uint8_t* e = a.e + ((size_t)row * (a.nsub / 8) + t / 8) * 4;
     const float d = f16f(ld16(e)), dmin = f16f(ld16(e + 2));
@@ -485,6 +525,22 @@ __device__ __forceinline__ void dot_sub2(uint32_t w0, uint32_t w1, uint32_t h, c
   }
 }
 
+// IQ4_NL / IQ4_XS: sum over the 32 elements of (table value + 128) * x
+__device__ __forceinline__ float dot_iq4(const uint4 w, const float* xv) {
+  const uint32_t W[4] = {w.x, w.y, w.z, w.w};
+  float p0 = 0.0f, p1 = 0.0f;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const uint32_t lo = iq4_lookup(W[d] & 0x0F0F0F0Fu), hi = iq4_lookup((W[d] >> 4) & 0x0F0F0F0Fu);
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      p0 = fmaf(ub(lo, b), xv[4 * d + b], p0);
+      p1 = fmaf(ub(hi, b), xv[16 + 4 * d + b], p1);
+    }
+  }
+  return p0 + p1;
+}
+
 // Q8_0: int8 codes q; (q + 128) as unsigned bytes, the 128 taken off with
 // sum(x) by the caller
 __device__ __forceinline__ float dot_q8(const uint4 w0, const uint4 w1, const float* xv) {
@@ -541,7 +597,11 @@ __global__ __launch_bounds__(64 * WAVES) void k_fmt_gemv(FmtArgs a) {
         h0[r] = h1[r] = 0;
         if constexpr (G.hb >= 4) h0[r] = *reinterpret_cast<const uint32_t*>(a.h + sub * G.hb);
         if constexpr (G.hb == 8) h1[r] = *reinterpret_cast<const uint32_t*>(a.h + sub * G.hb + 4);
-        if constexpr (FMT == kQ4_K || FMT == kQ5_K || FMT == kQ3_K) {
+        if constexpr (FMT == kIQ4_XS) {
+          const uint2 v = *reinterpret_cast<const uint2*>(a.s + ((size_t)(r0 + r) * nsub + (t & ~7)));
+          hd[r][0] = v.x, hd[r][1] = v.y, hd[r][2] = hd[r][3] = 0;
+          sv[r] = 0;
+        } else if constexpr (FMT == kQ4_K || FMT == kQ5_K || FMT == kQ3_K) {
           const uint4 v = *reinterpret_cast<const uint4*>(a.s + ((size_t)(r0 + r) * nsub + (t & ~7)) * G.sb);
           hd[r][0] = v.x, hd[r][1] = v.y, hd[r][2] = v.z, hd[r][3] = v.w;
           sv[r] = 0;
@@ -569,6 +629,13 @@ __global__ __launch_bounds__(64 * WAVES) void k_fmt_gemv(FmtArgs a) {
         float v;
         if constexpr (FMT == kQ8_0) {
           v = f16f((uint16_t)sv[r]) * fmaf(-128.0f, sx, dot_q8(w0[r], w1[r], xv));
+        } else if constexpr (FMT == kIQ4_NL) {
+          v = f16f((uint16_t)sv[r]) * fmaf(-128.0f, sx, dot_iq4(w0[r], xv));
+        } else if constexpr (FMT == kIQ4_XS) {
+          const int ib = t & 7;
+          const uint32_t sh = hd[r][0] >> 16;
+          const int ls = (int)(((hd[r][1] >> (8 * (ib >> 1) + 4 * (ib & 1))) & 15u) | (((sh >> (2 * ib)) & 3u) << 4));
+          v = f16f((uint16_t)hd[r][0]) * (float)(ls - 32) * fmaf(-128.0f, sx, dot_iq4(w0[r], xv));
         } else if constexpr (FMT == kQ2_K || FMT == kQ3_K) {
           float plo = 0.0f, phi = 0.0f;
           dot_sub2<FMT == kQ3_K>(w0[r].x, w0[r].y, h0[r], xv, plo, phi);
@@ -711,6 +778,8 @@ Status format_relayout(int fmt, const FmtArgs& a, const uint8_t* blocks, int row
   case kQ4_K: return relayout_f<kQ4_K>(a, blocks, rows, st);
   case kQ5_K: return relayout_f<kQ5_K>(a, blocks, rows, st);
   case kQ6_K: return relayout_f<kQ6_K>(a, blocks, rows, st);
+  case kIQ4_NL: return relayout_f<kIQ4_NL>(a, blocks, rows, st);
+  case kIQ4_XS: return relayout_f<kIQ4_XS>(a, blocks, rows, st);
   default: return Status::err(kGap, "gap? quant format not implemented");
   }
 }
@@ -727,6 +796,8 @@ Status format_dequant(int fmt, const FmtArgs& a, int rows, float* out, hipStream
   case kQ4_K: return dequant_f<kQ4_K>(a, rows, out, st);
   case kQ5_K: return dequant_f<kQ5_K>(a, rows, out, st);
   case kQ6_K: return dequant_f<kQ6_K>(a, rows, out, st);
+  case kIQ4_NL: return dequant_f<kIQ4_NL>(a, rows, out, st);
+  case kIQ4_XS: return dequant_f<kIQ4_XS>(a, rows, out, st);
   default: return Status::err(kGap, "gap? quant format not implemented");
   }
 }
@@ -746,6 +817,8 @@ Status launch_format_gemv(int fmt, const FmtArgs& a, int batch, hipStream_t st) 
   case kQ4_K: return gemv_f<kQ4_K>(a, batch, st);
   case kQ5_K: return gemv_f<kQ5_K>(a, batch, st);
   case kQ6_K: return gemv_f<kQ6_K>(a, batch, st);
+  case kIQ4_NL: return gemv_f<kIQ4_NL>(a, batch, st);
+  case kIQ4_XS: return gemv_f<kIQ4_XS>(a, batch, st);
   default: return Status::err(kGap, "gap? quant format not implemented");
   }
 }

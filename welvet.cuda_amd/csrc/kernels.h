@@ -235,7 +235,7 @@ Status launch_dequant(const DeviceWeights& d, float* w, hipStream_t st);
 // (README.md:361-383).
 enum QuantFormat : int32_t {
   kFmtNone = 0, kQ8_0 = 1, kQ4_0 = 2, kQ4_1 = 3, kQ5_0 = 4, kQ5_1 = 5, kQ2_K = 6, kQ3_K = 7,
-  kQ4_K = 8, kQ5_K = 9, kQ6_K = 10, kFmtLast = 20
+  kQ4_K = 8, kQ5_K = 9, kQ6_K = 10, kIQ4_NL = 16, kIQ4_XS = 17, kFmtLast = 20
 };
 // Elements and packed bytes per block; bytes per 32-element sub-block of the
 // resident code (q), high-bit (h) and scale (s) arrays, and of the per-256
@@ -254,6 +254,8 @@ constexpr FmtGeom fmt_geom(int fmt) {
          : fmt == kQ4_K ? FmtGeom{256, 144, 16, 0, 2, 0}
          : fmt == kQ5_K ? FmtGeom{256, 176, 16, 4, 2, 0}
          : fmt == kQ6_K ? FmtGeom{256, 210, 16, 8, 2, 2}
+         : fmt == kIQ4_NL ? FmtGeom{32, 18, 16, 0, 2, 0}
+         : fmt == kIQ4_XS ? FmtGeom{256, 136, 16, 0, 1, 0}
                         : FmtGeom{0, 0, 0, 0, 0, 0};
 }
 struct FmtArgs {

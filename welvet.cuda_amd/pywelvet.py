@@ -457,6 +457,7 @@ class DenseSession:
 
 # packed block formats (QuantFormat ids of welvet_dense_mount_format)
 Q8_0, Q4_0, Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K = 1, 2, 3, 4, 5, 6, 7, 8, 9, 10
+IQ4_NL, IQ4_XS = 16, 17
 
 
 class FormatDenseSession(DenseSession):
