@@ -221,3 +221,20 @@ def test_errors_and_gaps(gpu):
         assert e.value.code == 2
     finally:
         s.close()
+
+
+@pytest.mark.parametrize("dt,scheme", [(4, 0), (4, 2), (5, 1), (16, 3), (16, 2)])
+def test_export_f32_of_fp8_fp4_sessions(gpu, oracle, dt, scheme):
+    """welvet_dense_export_f32 on an FP8/FP4 session: codes times row scales
+    and E8M0 factors, bit for bit the oracle's dequantization."""
+    rng = np.random.default_rng(dt * 10 + scheme)
+    rows, cols = 77, 300
+    W = (rng.standard_normal((rows, cols)) * 3).astype(np.float32)
+    s = gpu.DenseSession(1, cols, rows, -1, dt, scheme, W)
+    try:
+        got = s.export_f32()
+    finally:
+        s.close()
+    native, rs, blk = oracle.quantize(dt, scheme, rows, cols, W)
+    want = oracle.dequant(dt, scheme, rows, cols, native, rs, blk)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
