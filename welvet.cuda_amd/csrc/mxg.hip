@@ -87,7 +87,7 @@ constexpr int waitcnt_imm(int vm, int lgkm) {
 // gathered to the lanes that pass them to the instruction (row l % 16, block
 // l / 16) and stored as one dword per lane at scales + 4 l (byte t: term t).
 // AS: the address space of the destination (1 global, 3 LDS).
-template <int AS, int NT = kTerms>
+template <int AS, int NT = kTerms, bool STREAM = false>
 __device__ __forceinline__ void split_terms(float (&v)[2][16],
                                             __attribute__((address_space(AS))) uint8_t* chunk,
                                             __attribute__((address_space(AS))) uint8_t* scales,
@@ -124,12 +124,19 @@ __device__ __forceinline__ void split_terms(float (&v)[2][16],
           v[h][4 * q + 2] -= q1.x * sc, v[h][4 * q + 3] -= q1.y * sc;
         }
       }
-      *reinterpret_cast<I4*>(dst + t * kFragBytes + h * 1024) = i32x4{wq[0], wq[1], wq[2], wq[3]};
+      const i32x4 codes = i32x4{wq[0], wq[1], wq[2], wq[3]};
+      if constexpr (AS == 1 && STREAM)  // read by a later launch: streaming store
+        __builtin_nontemporal_store(codes, reinterpret_cast<I4*>(dst + t * kFragBytes + h * 1024));
+      else
+        *reinterpret_cast<I4*>(dst + t * kFragBytes + h * 1024) = codes;
     }
     const int e0 = __shfl(e[0], src, 64), e1 = __shfl(e[1], src, 64);
     sword |= (uint32_t)(((lane >> 5) ? e1 : e0) + 127) << (8 * t);
   }
-  *reinterpret_cast<U32*>(scales + lane * 4) = sword;
+  if constexpr (AS == 1 && STREAM)
+    __builtin_nontemporal_store(sword, reinterpret_cast<U32*>(scales + lane * 4));
+  else
+    *reinterpret_cast<U32*>(scales + lane * 4) = sword;
 }
 
 // The activation split, written in operand order. One wave per (16-row block
@@ -137,13 +144,14 @@ __device__ __forceinline__ void split_terms(float (&v)[2][16],
 // row-contiguous loads; then lane l (row i16 = l % 16, group g = l / 16)
 // takes the 32 values of its operand, k = 64h + 16g + j (h = 0, 1; j < 16),
 // and split_terms writes them. Rows >= M and columns >= cols give zero codes.
-// VEC: x 16-byte aligned, cols and x_stride multiples of 4.
+// VEC: x 16-byte aligned, cols and x_stride multiples of 4. stream: the
+// split is larger than the L2s hold, so its stores are non-temporal.
 template <bool VEC, int NT>
 __global__ __launch_bounds__(kThreads) void k_split(const float* __restrict__ x, int x_stride,
                                                     int M, int cols, int mpad, int kpad,
                                                     uint8_t* __restrict__ a,
                                                     uint8_t* __restrict__ as,
-                                                    const SplitJob* __restrict__ jobs) {
+                                                    const SplitJob* __restrict__ jobs, int stream) {
   if (jobs) {  // grouped: member blockIdx.y
     const SplitJob j = jobs[blockIdx.y];
     x = j.x;
@@ -202,8 +210,12 @@ __global__ __launch_bounds__(kThreads) void k_split(const float* __restrict__ x,
       v[h][4 * q] = t.x, v[h][4 * q + 1] = t.y, v[h][4 * q + 2] = t.z, v[h][4 * q + 3] = t.w;
     }
 
-  split_terms<1, NT>(v, (GlobalU8)(a + (size_t)(rb * KC + kc) * NT * kFragBytes),
-                     (GlobalU8)(as + (size_t)(rb * KC + kc) * kChunkScaleBytes), lane);
+  const GlobalU8 chunk = (GlobalU8)(a + (size_t)(rb * KC + kc) * NT * kFragBytes);
+  const GlobalU8 scales = (GlobalU8)(as + (size_t)(rb * KC + kc) * kChunkScaleBytes);
+  if (stream)
+    split_terms<1, NT, true>(v, chunk, scales, lane);
+  else
+    split_terms<1, NT, false>(v, chunk, scales, lane);
 }
 
 // Large-M tile (M > 32): 128 activation rows x 128 staged weight rows (64 per
@@ -675,7 +687,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
               v[h][4 * q] = live ? t.x : 0.0f, v[h][4 * q + 1] = live ? t.y : 0.0f;
               v[h][4 * q + 2] = live ? t.z : 0.0f, v[h][4 * q + 3] = live ? t.w : 0.0f;
             }
-          split_terms<1, NT>(v, (GlobalU8)(p.next + (size_t)(rb * kcn + kc) * CB),
+          split_terms<1, NT, true>(v, (GlobalU8)(p.next + (size_t)(rb * kcn + kc) * CB),
                              (GlobalU8)(nscale + (size_t)(rb * kcn + kc) * kChunkScaleBytes), lane);
         }
         __builtin_amdgcn_wave_barrier();
@@ -1171,6 +1183,10 @@ size_t split_bytes(int M, int kpad) {
   return (size_t)kTerms * mpad * kpad + mpad * (size_t)kpad / 8;
 }
 
+// Splits of at least this many code bytes per launch are written with
+// streaming stores (the eight XCD L2s hold 32 MB together).
+constexpr size_t kStreamSplitBytes = 8u << 20;
+
 Status launch_split(const float* x, int x_stride, int M, int cols, int kpad, uint8_t* buf,
                     hipStream_t st, int terms) {
   if (terms != 2 && terms != kTerms) return Status::err(kInvalid, "split: terms must be 2 or 3");
@@ -1181,12 +1197,13 @@ Status launch_split(const float* x, int x_stride, int M, int cols, int kpad, uin
   const int64_t waves = (int64_t)(mpad / 16) * (kpad / 128);
   const unsigned grid = (unsigned)((waves + kThreads / 64 - 1) / (kThreads / 64));
   const bool vec = x_stride % 4 == 0 && cols % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+  const int stream = (size_t)terms * mpad * kpad >= kStreamSplitBytes;
   if (terms == 2) {
-    if (vec) k_split<true, 2><<<grid, kThreads, 0, st>>>(x, x_stride, M, cols, mpad, kpad, a, as, nullptr);
-    else k_split<false, 2><<<grid, kThreads, 0, st>>>(x, x_stride, M, cols, mpad, kpad, a, as, nullptr);
+    if (vec) k_split<true, 2><<<grid, kThreads, 0, st>>>(x, x_stride, M, cols, mpad, kpad, a, as, nullptr, stream);
+    else k_split<false, 2><<<grid, kThreads, 0, st>>>(x, x_stride, M, cols, mpad, kpad, a, as, nullptr, stream);
   } else {
-    if (vec) k_split<true, kTerms><<<grid, kThreads, 0, st>>>(x, x_stride, M, cols, mpad, kpad, a, as, nullptr);
-    else k_split<false, kTerms><<<grid, kThreads, 0, st>>>(x, x_stride, M, cols, mpad, kpad, a, as, nullptr);
+    if (vec) k_split<true, kTerms><<<grid, kThreads, 0, st>>>(x, x_stride, M, cols, mpad, kpad, a, as, nullptr, stream);
+    else k_split<false, kTerms><<<grid, kThreads, 0, st>>>(x, x_stride, M, cols, mpad, kpad, a, as, nullptr, stream);
   }
   return hip_status(hipGetLastError(), "split launch");
 }
@@ -1199,12 +1216,13 @@ Status launch_split_group(const SplitJob* jobs, int n, bool vec, int x_stride, i
   const int mpad = (int)round_up(M, mxg_block_m(M));
   const int64_t waves = (int64_t)(mpad / 16) * (kpad / 128);
   const dim3 grid((unsigned)((waves + kThreads / 64 - 1) / (kThreads / 64)), (unsigned)n);
+  const int stream = (size_t)terms * mpad * kpad * n >= kStreamSplitBytes;
   if (terms == 2) {
-    if (vec) k_split<true, 2><<<grid, kThreads, 0, st>>>(nullptr, x_stride, M, cols, mpad, kpad, nullptr, nullptr, jobs);
-    else k_split<false, 2><<<grid, kThreads, 0, st>>>(nullptr, x_stride, M, cols, mpad, kpad, nullptr, nullptr, jobs);
+    if (vec) k_split<true, 2><<<grid, kThreads, 0, st>>>(nullptr, x_stride, M, cols, mpad, kpad, nullptr, nullptr, jobs, stream);
+    else k_split<false, 2><<<grid, kThreads, 0, st>>>(nullptr, x_stride, M, cols, mpad, kpad, nullptr, nullptr, jobs, stream);
   } else {
-    if (vec) k_split<true, kTerms><<<grid, kThreads, 0, st>>>(nullptr, x_stride, M, cols, mpad, kpad, nullptr, nullptr, jobs);
-    else k_split<false, kTerms><<<grid, kThreads, 0, st>>>(nullptr, x_stride, M, cols, mpad, kpad, nullptr, nullptr, jobs);
+    if (vec) k_split<true, kTerms><<<grid, kThreads, 0, st>>>(nullptr, x_stride, M, cols, mpad, kpad, nullptr, nullptr, jobs, stream);
+    else k_split<false, kTerms><<<grid, kThreads, 0, st>>>(nullptr, x_stride, M, cols, mpad, kpad, nullptr, nullptr, jobs, stream);
   }
   return hip_status(hipGetLastError(), "split group launch");
 }
