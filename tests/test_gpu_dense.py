@@ -64,8 +64,12 @@ def test_release_smoke_known_answer(gpu):
 ])
 def test_integer_exact_bit_for_bit(gpu, oracle, dt, values):
     rng = np.random.default_rng(dt)
+    # 12588 and 24876 columns: 13 chunks of 1 KiB per wave for FP8 and FP4,
+    # so the waves take chunks two at a time and the ragged last chunk is
+    # the second of a pair
     for rows, cols, batch in [(129, 1000, 1), (64, 4096, 1), (5, 77, 3), (9, 300, 9), (24, 9300, 1),
-                              (40, 301, 9), (130, 4096, 40)]:
+                              (40, 301, 9), (130, 4096, 40), (24, 12588, 1), (16, 24876, 2),
+                              (8, 16384, 1)]:
         W = rng.choice(np.array(values, np.float32), (rows, cols))
         x = rng.integers(-4, 5, (batch, cols)).astype(np.float32)
         pre, post = run(gpu, dt, 0, W, x)
@@ -76,10 +80,12 @@ def test_integer_exact_bit_for_bit(gpu, oracle, dt, values):
 
 @pytest.mark.parametrize("dt", [4, 16])
 @pytest.mark.parametrize("scheme", [2, 3])
-@pytest.mark.parametrize("rows,cols", [(70, 3000), (40, 5000), (24, 8000), (16, 9300)])
+@pytest.mark.parametrize("rows,cols", [(70, 3000), (40, 5000), (24, 8000), (16, 9300),
+                                       (24, 12588), (16, 24876)])
 def test_gemv_k_split_over_waves(gpu, oracle, dt, scheme, rows, cols):
-    """Batch-1 GEMV whose K axis spans 2-10 chunks of 1 KiB per wave (FP8: 3, 5,
-    8, 10; FP4: 2, 3, 4, 5), so groups of 2, 3, 4, 6 and 8 waves split it."""
+    """Batch-1 GEMV whose K axis spans 2-25 chunks of 1 KiB per wave (FP8: 3, 5,
+    8, 10, 13, 25; FP4: 2, 3, 4, 5, 7, 13), so groups of 2, 3, 4, 6 and 8 waves
+    split it, and waves with more than one chunk take them in pairs."""
     rng = np.random.default_rng(rows * cols + dt + scheme)
     W = rng.standard_normal((rows, cols)).astype(np.float32) / np.sqrt(cols)
     x = rng.standard_normal((1, cols)).astype(np.float32)
