@@ -68,25 +68,46 @@ __global__ __launch_bounds__(kThreads) void k_row_scales(const float* __restrict
   }
 }
 
-// One thread per (row, 32-column block) of the padded layout: E8M0 byte.
+// E8M0 byte per (row, 32-column block) of the padded layout. Lane per 4
+// consecutive columns (16-byte loads when cols % 4 == 0, so a wave reads
+// 1 KiB contiguous), the block's 8 lanes combine their maxima with xor
+// shuffles. The max keeps the larger value and never takes a NaN
+// ((a > m) ? a : m from m = 0), so the combining order does not change it.
 __global__ __launch_bounds__(kThreads) void k_block_exp(const float* __restrict__ W, int rows,
                                                         int cols, int rpad, int nblk, float maxrep,
                                                         uint8_t* __restrict__ blk) {
   const int64_t t = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  if (t >= (int64_t)rpad * nblk) return;
-  const int r = (int)(t / nblk), b = (int)(t % nblk);
-  int e = 0;
-  if (r < rows && b * 32 < cols) {
-    const float* wb = W + (size_t)r * cols + b * 32;
-    const int len = min(32, cols - b * 32);
-    float m = 0.0f;
-    for (int i = 0; i < len; ++i) {
-      const float a = fabsf(wb[i]);
-      m = (a > m) ? a : m;
+  const int64_t nq = (int64_t)rpad * nblk * 8;  // a multiple of 8: groups stay whole
+  const bool live = t < nq;
+  const int64_t tq = live ? t : nq - 1;
+  const int r = (int)(tq / ((int64_t)nblk * 8)), q = (int)(tq % ((int64_t)nblk * 8));
+  const int c0 = q * 4;
+  float m = 0.0f;
+  if (live && r < rows && c0 < cols) {
+    const float* w = W + (size_t)r * cols + c0;
+    if ((cols & 3) == 0) {
+      const float4 v = *reinterpret_cast<const float4*>(w);
+      const float a[4] = {fabsf(v.x), fabsf(v.y), fabsf(v.z), fabsf(v.w)};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) m = (a[i] > m) ? a[i] : m;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (c0 + i < cols) {
+          const float a = fabsf(w[i]);
+          m = (a > m) ? a : m;
+        }
     }
-    e = e8m0_exponent(m, maxrep);
   }
-  blk[t] = (uint8_t)(e + 127);
+#pragma unroll
+  for (int o = 1; o < 8; o <<= 1) {
+    const float v = __shfl_xor(m, o, 64);
+    m = (v > m) ? v : m;
+  }
+  if (live && (q & 7) == 0) {
+    const int e = r < rows && c0 < cols ? e8m0_exponent(m, maxrep) : 0;
+    blk[(size_t)r * nblk + q / 8] = (uint8_t)(e + 127);
+  }
 }
 
 // Value handed to the element encoder for W[r][c] under the scheme.
@@ -320,7 +341,7 @@ Status quantize_to_device(const float* dW, int dtype, int scheme, int rows, int 
   if (scheme == kSchemeBlock32) {
     WV_TRY(dw->blk.alloc((size_t)dw->rpad * dw->nblk));
     blk = dw->blk.as<uint8_t>();
-    k_block_exp<<<grid_for((int64_t)dw->rpad * dw->nblk), kThreads, 0, st>>>(
+    k_block_exp<<<grid_for((int64_t)dw->rpad * dw->nblk * 8), kThreads, 0, st>>>(
         dW, rows, cols, dw->rpad, dw->nblk, maxrep, blk);
     WV_HIP(hipGetLastError());
     WV_TRY(build_blk_frag(dw, st));
