@@ -154,6 +154,10 @@ struct MxgArgs {
   uint8_t* next = nullptr;
   // activation terms: kTerms, or 2 for one-matrix products
   int terms = kTerms;
+  // large tiles: 1 when the next launch reads the output (the MHA Q, K, V
+  // and SwiGLU gate+up products): plain stores, which leave it in the
+  // caches; 0: streaming stores
+  int keep_out = 0;
 };
 int mxg_block_m(int M);
 // Bytes of the K-split partial buffer the product of M rows with N outputs

@@ -361,10 +361,11 @@ static Status fix_nonfinite(const DenseLayer& L, int batch, const float* x, int 
 
 Status dense_forward_split(const DenseLayer& L, int batch, const float* x, bool split_ready,
                            Workspace* ws, float* pre, float* post, hipStream_t st,
-                           const double* rope_tab, int rope_hd) {
+                           const double* rope_tab, int rope_hd, bool keep_out) {
   MxgArgs p = mxg_args(L, batch, split_buf(ws));
   p.pre = pre;
   p.post = post;
+  p.keep_out = keep_out ? 1 : 0;
   p.rope_tab = rope_tab;
   p.rope_hd = rope_hd;
   if (mxg_block_m(batch) > 16) {
@@ -649,6 +650,7 @@ Status swiglu_forward(const SwiGLULayer& L, int rows, const float* x, float* h, 
     p.codesf[1] = L.up.dev.d_codesf();
     p.pre = h;
     p.need_epi = 0;
+    p.keep_out = 1;  // h is split by the down projection next
     WV_TRY(launch_mxg(p, L.gate.dev.dtype, L.gate.dev.scheme == kSchemeBlock32, st));
     WV_TRY(swiglu_fix(L, rows, x, h, st));
     return dense_forward_split(L.down, rows, h, false, ws, y, nullptr, st);
@@ -819,9 +821,10 @@ Status mha_forward(const MHALayer& L, int batch, int seq, const float* x, float*
     const int rhd = rope_epi ? c.head_dim : 0;
     if (once)
       WV_TRY(launch_split(x, c.d_model, T, c.d_model, L.q.dev.kpad, split_buf(ws), st, L.q.terms));
-    WV_TRY(dense_forward_split(L.q, T, x, once, ws, qb, nullptr, st, tab, rhd));
-    WV_TRY(dense_forward_split(L.k, T, x, once, ws, kb, nullptr, st, tab, rhd));
-    WV_TRY(dense_forward_split(L.v, T, x, once, ws, vb, nullptr, st));
+    // (Q, K and V are read by the attention kernel next: kept in the caches)
+    WV_TRY(dense_forward_split(L.q, T, x, once, ws, qb, nullptr, st, tab, rhd, true));
+    WV_TRY(dense_forward_split(L.k, T, x, once, ws, kb, nullptr, st, tab, rhd, true));
+    WV_TRY(dense_forward_split(L.v, T, x, once, ws, vb, nullptr, st, nullptr, 0, true));
   } else {
     WV_TRY(dense_forward(L.q, T, x, qb, nullptr, ws, st));
     WV_TRY(dense_forward(L.k, T, x, kb, nullptr, ws, st));

@@ -122,10 +122,12 @@ inline uint8_t* split_buf(Workspace* ws) { return ws->b.as<uint8_t>(); }
 // Batched path (batch > 4 rows) on x [batch][L.in]. Above 32 rows the GEMM
 // reads the split terms of x from split_buf(ws), made here unless
 // `split_ready` (launch_split of x with L.dev.kpad already ran); up to 32
-// rows the GEMM kernel splits x itself.
+// rows the GEMM kernel splits x itself. keep_out: the next launch reads the
+// output (MxgArgs::keep_out).
 Status dense_forward_split(const DenseLayer& L, int batch, const float* x, bool split_ready,
                            Workspace* ws, float* pre, float* post, hipStream_t st,
-                           const double* rope_tab = nullptr, int rope_hd = 0);
+                           const double* rope_tab = nullptr, int rope_hd = 0,
+                           bool keep_out = false);
 // Grows ws->b to at least n bytes (mount time; a forward that finds it too
 // small allocates, which a captured graph cannot do).
 Status ensure_split(Workspace* ws, size_t n);

@@ -286,6 +286,7 @@ __device__ __forceinline__ MxgArgs load_args(ConstArgs t) {
   p.rope_tab = t->rope_tab;
   p.rope_hd = t->rope_hd;
   p.terms = t->terms;
+  p.keep_out = t->keep_out;
   return p;
 }
 
@@ -622,11 +623,14 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
         }
         if (rbase + r >= p.M || n >= p.N) continue;
         const size_t oi = (size_t)(rbase + r) * p.out_stride + n;
-        if (vec_out && n + 3 < p.N) {
-          // streaming stores: the output is not read again by this launch
+        if (vec_out && n + 3 < p.N && !p.keep_out) {
+          // streaming stores: no workgroup of this launch reads the output
           const f32x4 yv = f32x4{y.x, y.y, y.z, y.w};
           __builtin_nontemporal_store(yv, reinterpret_cast<f32x4*>(p.pre + oi));
           if (post) __builtin_nontemporal_store(yv, reinterpret_cast<f32x4*>(post + oi));
+        } else if (vec_out && n + 3 < p.N) {
+          *reinterpret_cast<float4*>(p.pre + oi) = y;
+          if (post) *reinterpret_cast<float4*>(post + oi) = y;
         } else {
           const float yv[4] = {y.x, y.y, y.z, y.w};
 #pragma unroll
