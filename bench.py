@@ -544,7 +544,7 @@ def backward_workload(pw, hip, name, copies):
             "cpu": cpu, "close": close}
 
 
-def make_workload(pw, hip, config, copies, terms=3):
+def make_workload(pw, hip, config, copies, terms=3, batch=1):
     two = 16 if terms == 2 else 0  # backend bit for two activation terms
     if config == "c2":
         return dense_workload(pw, hip, "dense_gemv_4096x4096_fp8e4m3_rowscale_b1", 2, 4, 2, 1,
@@ -570,7 +570,8 @@ def make_workload(pw, hip, config, copies, terms=3):
                               + ("_2terms" if two else ""), two)
     if config.startswith("gemv_"):
         f = config[len("gemv_"):]
-        return format_workload(pw, hip, f"dense_gemv_4096x4096_{f}_b1", f, 1, 4096, 4096, copies)
+        b = max(1, batch)
+        return format_workload(pw, hip, f"dense_gemv_4096x4096_{f}_b{b}", f, b, 4096, 4096, copies)
     if config == "c5":
         return cells_workload(pw, hip, "volume_64_cells_3x_dense_1024_b256"
                               + ("_2terms" if two else ""), two)
@@ -687,6 +688,8 @@ def main():
                     help="untimed warmup steps; the warmup also lasts at least WARMUP_S seconds")
     ap.add_argument("--config", default="c2", choices=CONFIGS)
     ap.add_argument("--copies", type=int, default=64)
+    ap.add_argument("--batch", type=int, default=1,
+                    help="batch rows of the packed-format GEMV configs (gemv_<fmt>)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--terms", type=int, default=3, choices=(2, 3),
                     help="activation terms of the matrix-core GEMMs (c4, c4mha, c5, c5chain): "
@@ -716,7 +719,7 @@ def main():
         wl = read_floor_workload(pw, hip, args.read_floor, max(1, args.copies))
         gemv = True
     else:
-        wl = make_workload(pw, hip, args.config, max(1, args.copies), args.terms)
+        wl = make_workload(pw, hip, args.config, max(1, args.copies), args.terms, args.batch)
         gemv = args.config in ("c1", "c2", "c3", "c3b16")
     steps = args.steps if args.steps is not None else (1280 if gemv else 64)
     steps = max(1, steps)

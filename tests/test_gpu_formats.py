@@ -97,8 +97,10 @@ def test_mount_from_blocks_dequant_and_export(gpu, oracle, fmt, rows, cols):
 
 
 @pytest.mark.parametrize("fmt", ALL, ids=lambda f: NAMES[f])
-@pytest.mark.parametrize("batch", [1, 3, 16])
+@pytest.mark.parametrize("batch", [1, 3, 8, 16, 37])
 def test_gemv_against_oracle(gpu, oracle, fmt, batch):
+    """Batches below 8 run the per-row kernel, from 8 the matrix-core one
+    (37: three groups of 16 batch rows, the last ragged)."""
     rng = np.random.default_rng(fmt * 31 + batch)
     rows, cols = 333, 2048
     blocks = random_blocks(fmt, rows, cols, rng)
@@ -141,9 +143,10 @@ def test_gemv_full_size_4096(gpu, oracle, fmt):
 
 
 @pytest.mark.parametrize("act", [-1, 0, 1, 3, 6])
-def test_epilogue_bias_and_activation(gpu, oracle, act):
+@pytest.mark.parametrize("batch", [2, 9])
+def test_epilogue_bias_and_activation(gpu, oracle, act, batch):
     rng = np.random.default_rng(act + 10)
-    rows, cols, batch = 100, 512, 2
+    rows, cols = 100, 512
     W = rng.standard_normal((rows, cols)).astype(np.float32) / 20
     bias = rng.standard_normal(rows)
     x = rng.standard_normal((batch, cols)).astype(np.float32)
@@ -155,6 +158,24 @@ def test_epilogue_bias_and_activation(gpu, oracle, act):
     Wd = oracle.fmt_dequant(3, oracle.fmt_quantize(3, W), (rows, cols))
     wpre, wpost = want_dense(oracle, Wd, x, act, bias)
     assert rel_l2(pre, wpre) <= TOL and rel_l2(post, wpost) <= TOL
+
+
+@pytest.mark.parametrize("fmt", LEGACY, ids=lambda f: NAMES[f])
+@pytest.mark.parametrize("batch", [1, 8])
+def test_gemv_ragged_columns(gpu, oracle, fmt, batch):
+    """45 sub-blocks of 32 columns: the matrix-core kernel's last group of 4
+    holds one."""
+    rng = np.random.default_rng(fmt * 7 + batch)
+    rows, cols = 70, 32 * 45
+    blocks = random_blocks(fmt, rows, cols, rng)
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    s = gpu.FormatDenseSession(batch, cols, rows, -1, fmt, blocks=blocks)
+    try:
+        pre, _ = s.execute(x)
+    finally:
+        s.close()
+    want, _ = want_dense(oracle, oracle.fmt_dequant(fmt, blocks, (rows, cols)), x)
+    assert rel_l2(pre, want) <= TOL
 
 
 def test_device_execute_and_noalloc_match_host_execute(gpu):
