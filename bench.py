@@ -353,7 +353,7 @@ def mha_workload(pw, hip, name, two=0):
             "cpu": None, "close": close}
 
 
-def cells_workload(pw, hip, name, two=0):
+def cells_workload(pw, hip, name, two=0, keep_inner=False):
     import numpy as np
 
     cells, batch, d = 64, 256, 1024
@@ -372,12 +372,14 @@ def cells_workload(pw, hip, name, two=0):
     # the 64 cells are independent: layer li of every cell runs as one group
     # (one matrix-core launch per layer position); the groups form a chain,
     # so each layer's epilogue also writes the next layer's activation split
-    # and only the first layer runs the split kernel
+    # and only the first layer runs the split kernel. A cell returns its last
+    # layer's output: unless keep_inner, the first two layers write only the
+    # next layer's split (WELVET_CHAIN_INNER_NOT_KEPT)
     groups = [pw.DenseGroup([sessions[c][li] for c in range(cells)],
                             [bufs[c][li] for c in range(cells)],
                             [bufs[c][li + 1] for c in range(cells)],
                             [bufs[c][li + 1] for c in range(cells)]) for li in range(len(kinds))]
-    chain = pw.DenseChain(groups)
+    chain = pw.DenseChain(groups, keep_inner=keep_inner)
 
     def enqueue(i, stream):
         chain.execute(stream)
@@ -410,7 +412,10 @@ def cells_workload(pw, hip, name, two=0):
             "config": {"workload": name, "cells": cells, "layers_per_cell": 3, "batch": batch,
                        "width": d, "layer_kinds": "E4M3 per-row, FP4 E8M0/32, E4M3 per-row",
                        "execution": ("independent cells, one grouped launch per layer position, "
-                                     "chained: each epilogue writes the next layer's split")},
+                                     "chained: each epilogue writes the next layer's split"),
+                       "inner_outputs": ("written (fp32 pre/post of layers 1 and 2)" if keep_inner
+                                         else "not written: each cell returns its last layer's "
+                                         "output; layers 1 and 2 write only the next split")},
             "cpu": cpu, "close": close}
 
 
@@ -544,7 +549,7 @@ def backward_workload(pw, hip, name, copies):
             "cpu": cpu, "close": close}
 
 
-def make_workload(pw, hip, config, copies, terms=3, batch=1):
+def make_workload(pw, hip, config, copies, terms=3, batch=1, keep_inner=False):
     two = 16 if terms == 2 else 0  # backend bit for two activation terms
     if config == "c2":
         return dense_workload(pw, hip, "dense_gemv_4096x4096_fp8e4m3_rowscale_b1", 2, 4, 2, 1,
@@ -574,7 +579,8 @@ def make_workload(pw, hip, config, copies, terms=3, batch=1):
         return format_workload(pw, hip, f"dense_gemv_4096x4096_{f}_b{b}", f, b, 4096, 4096, copies)
     if config == "c5":
         return cells_workload(pw, hip, "volume_64_cells_3x_dense_1024_b256"
-                              + ("_2terms" if two else ""), two)
+                              + ("_2terms" if two else "") + ("_inner_kept" if keep_inner else ""),
+                              two, keep_inner)
     raise SystemExit(f"unknown config {config}")
 
 
@@ -694,6 +700,8 @@ def main():
     ap.add_argument("--terms", type=int, default=3, choices=(2, 3),
                     help="activation terms of the matrix-core GEMMs (c4, c4mha, c5, c5chain): "
                          "3 (default) or 2 (backend bit 16)")
+    ap.add_argument("--keep-inner", action="store_true",
+                    help="c5: also write the fp32 outputs of each cell's first two layers")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run device-to-device copies of MIB MiB (the known-size copy "
                          "that scales the FETCH_SIZE/WRITE_SIZE counters) and exit")
@@ -719,7 +727,8 @@ def main():
         wl = read_floor_workload(pw, hip, args.read_floor, max(1, args.copies))
         gemv = True
     else:
-        wl = make_workload(pw, hip, args.config, max(1, args.copies), args.terms, args.batch)
+        wl = make_workload(pw, hip, args.config, max(1, args.copies), args.terms, args.batch,
+                           args.keep_inner)
         gemv = args.config in ("c1", "c2", "c3", "c3b16")
     steps = args.steps if args.steps is not None else (1280 if gemv else 64)
     steps = max(1, steps)

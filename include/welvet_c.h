@@ -195,6 +195,17 @@ WELVET_API void welvet_dense_group_release(welvet_dense_group* g);
 typedef struct welvet_dense_chain welvet_dense_chain;
 WELVET_API welvet_status welvet_dense_chain_mount(welvet_dense_group* const* groups, int32_t n,
                                                   welvet_dense_chain** out);
+/* As welvet_dense_chain_mount, with flags (no counterpart in the reference).
+ * WELVET_CHAIN_INNER_NOT_KEPT: a group whose epilogue writes the next
+ * group's split (above 32 rows, out a multiple of 256) writes only that
+ * split, not its own pre and post, whose contents after execute are then
+ * unspecified; the last group's outputs, and those of every group that the
+ * next one reads from memory, are written as before. For callers that need
+ * only the last layer's output, as a volume's cells return it. Other bits:
+ * code 1. */
+#define WELVET_CHAIN_INNER_NOT_KEPT 1
+WELVET_API welvet_status welvet_dense_chain_mount_ex(welvet_dense_group* const* groups, int32_t n,
+                                                     int32_t flags, welvet_dense_chain** out);
 WELVET_API welvet_status welvet_dense_chain_execute(welvet_dense_chain* c, void* stream);
 WELVET_API void welvet_dense_chain_release(welvet_dense_chain* c);
 

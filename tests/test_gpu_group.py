@@ -156,3 +156,62 @@ def test_chain_rejects_unlinked_groups(gpu):
         hip.free(p)
     a.close()
     b.close()
+
+
+@pytest.mark.parametrize("batch,n,widths,layers", [
+    (256, 16, [1024, 1024, 1024, 1024], [(4, 2, -1, False), (16, 3, -1, False), (4, 2, -1, False)]),
+    (200, 3, [256, 512, 256, 384], [(5, 1, -1, False), (4, 3, 1, True), (16, 3, 2, True)]),
+    (130, 2, [128, 384, 256, 128], [(4, 2, 0, False), (16, 3, -1, False), (4, 2, -1, True)]),
+])
+def test_chain_inner_not_kept(gpu, batch, n, widths, layers):
+    """WELVET_CHAIN_INNER_NOT_KEPT: the last group's outputs equal those of the
+    chain that keeps every output, bit for bit; a group whose epilogue writes
+    the next split leaves its own pre / post untouched; a group that the next
+    one reads from memory (width not a multiple of 256) still writes them."""
+    import pywelvet as pw
+    hip = pw.Hip()
+    rng = np.random.default_rng(batch * 11 + n)
+    Ws, bs, sessions, x0, bufs, groups = _chain_setup(hip, pw, rng, batch, n, widths, layers)
+    full = pw.DenseChain(groups)
+    lean = pw.DenseChain(groups, keep_inner=False)
+    L = len(layers)
+    xa = [rng.standard_normal((batch, widths[0])).astype(np.float32) for _ in range(n)]
+    for i in range(n):
+        hip.copy_in(x0[i], xa[i])
+    full.execute()
+    hip.sync()
+    want = [(hip.download(bufs[L - 1][0][i], (batch, widths[L])),
+             hip.download(bufs[L - 1][1][i], (batch, widths[L]))) for i in range(n)]
+    kept = [[hip.download(bufs[k][1][i], (batch, widths[k + 1])) for i in range(n)] for k in range(L)]
+    for k in range(L):  # poison every output buffer (0xFF bytes: NaN)
+        for i in range(n):
+            for p in {bufs[k][0][i], bufs[k][1][i]}:
+                hip.memset(p, 0xFF, batch * widths[k + 1] * 4)
+    hip.sync()
+    for _ in range(2):  # twice: the second run starts from the first's state
+        lean.execute()
+    hip.sync()
+    for i in range(n):
+        pre = hip.download(bufs[L - 1][0][i], (batch, widths[L]))
+        post = hip.download(bufs[L - 1][1][i], (batch, widths[L]))
+        assert np.array_equal(pre, want[i][0]) and np.array_equal(post, want[i][1]), i
+    for k in range(L - 1):
+        fused = batch > 32 and widths[k + 1] % 256 == 0
+        for i in range(n):
+            post = hip.download(bufs[k][1][i], (batch, widths[k + 1]))
+            if fused:
+                assert np.isnan(post).all(), (k, i)
+            else:
+                assert np.array_equal(post, kept[k][i]), (k, i)
+    lean.close()
+    full.close()
+    for g in groups:
+        g.close()
+    seen = set()
+    for p in x0 + [q for pre, post in bufs for q in pre + post]:
+        if p not in seen:
+            seen.add(p)
+            hip.free(p)
+    for sk in sessions:
+        for s in sk:
+            s.close()

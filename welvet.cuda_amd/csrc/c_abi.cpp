@@ -312,9 +312,15 @@ struct welvet_dense_chain {
 
 welvet_status welvet_dense_chain_mount(welvet_dense_group* const* groups, int32_t n,
                                        welvet_dense_chain** out) {
+  return welvet_dense_chain_mount_ex(groups, n, 0, out);
+}
+
+welvet_status welvet_dense_chain_mount_ex(welvet_dense_group* const* groups, int32_t n,
+                                          int32_t flags, welvet_dense_chain** out) {
   if (!out) return invalid("null chain out");
   *out = nullptr;
   if (n <= 0 || !groups) return invalid("chain: null or empty arguments");
+  if (flags & ~WELVET_CHAIN_INNER_NOT_KEPT) return invalid("chain: unknown flags");
   return guarded([&]() -> Status {
     auto ch = std::make_unique<welvet_dense_chain>();
     bool fused = true;
@@ -341,7 +347,8 @@ welvet_status welvet_dense_chain_mount(welvet_dense_group* const* groups, int32_
     if (fused) {
       std::vector<const wv::DenseGroup*> gs;
       for (auto* g : ch->groups) gs.push_back(&g->g);
-      WV_TRY(wv::dense_chain_build(gs.data(), n, &ch->c));
+      WV_TRY(wv::dense_chain_build(gs.data(), n, &ch->c,
+                                   (flags & WELVET_CHAIN_INNER_NOT_KEPT) == 0));
     }
     *out = ch.release();
     return Status::ok();

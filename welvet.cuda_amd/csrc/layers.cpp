@@ -520,7 +520,8 @@ Status dense_group_forward(const DenseGroup& g, hipStream_t st) {
   return group_fix(g, st);
 }
 
-Status dense_chain_build(const DenseGroup* const* groups, int count, DenseChain* c) {
+Status dense_chain_build(const DenseGroup* const* groups, int count, DenseChain* c,
+                         bool keep_inner) {
   if (count <= 0 || !groups || !c) return Status::err(kInvalid, "dense chain: bad args");
   for (int k = 0; k < count; ++k)
     if (!groups[k] || groups[k]->n <= 0) return Status::err(kInvalid, "dense chain: null group");
@@ -548,7 +549,11 @@ Status dense_chain_build(const DenseGroup* const* groups, int count, DenseChain*
         group_has_nonfinite(P) || P.terms != C.terms)
       continue;
     std::vector<MxgArgs> tab = P.htab;
-    for (int i = 0; i < P.n; ++i) tab[i].next = C.hjobs[i].buf;
+    for (int i = 0; i < P.n; ++i) {
+      tab[i].next = C.hjobs[i].buf;
+      // the consumer reads the split only: the output need not be written
+      if (!keep_inner) tab[i].pre = tab[i].post = nullptr;
+    }
     WV_TRY(c->tabs[k].alloc(sizeof(MxgArgs) * P.n));
     WV_TRY(copy_h2d(c->tabs[k].p, tab.data(), sizeof(MxgArgs) * P.n, nullptr));
     WV_HIP(hipStreamSynchronize(nullptr));

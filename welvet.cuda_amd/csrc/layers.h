@@ -159,13 +159,16 @@ Status dense_group_forward(const DenseGroup& g, hipStream_t st);
 // x is member i's post, or its pre when the two are one buffer): the layers
 // of a volume's cells. Where group k's out is a multiple of 256 (then the
 // consumer's kpad equals it), group k's GEMM epilogue writes group k + 1's
-// split buffer as well and group k + 1 runs no split kernel.
+// split buffer as well and group k + 1 runs no split kernel. Without
+// keep_inner, such a group k writes only that split, not its own pre / post
+// (the cells of a volume return their last layer's output only).
 struct DenseChain {
   std::vector<const DenseGroup*> groups;
   std::vector<DevBuf> tabs;  // per link k -> k + 1: group k's MxgArgs[n] with `next` set
   std::vector<char> fused;   // per link: the epilogue writes the next split
 };
-Status dense_chain_build(const DenseGroup* const* groups, int count, DenseChain* c);
+Status dense_chain_build(const DenseGroup* const* groups, int count, DenseChain* c,
+                         bool keep_inner = true);
 Status dense_chain_forward(const DenseChain& c, hipStream_t st);
 
 struct SwiGLULayer {

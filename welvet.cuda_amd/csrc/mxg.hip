@@ -594,10 +594,11 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
       }
     } else if (MATS == 2 || !p.need_epi) {
       // post = pre here; a caller that passes one buffer for both gets it
-      // written once
+      // written once. No pre: an inner layer of a chain whose output is not
+      // kept (only the next layer's split below is written).
       float* post = MATS == 1 && p.post != p.pre ? p.post : nullptr;
 #pragma unroll
-      for (int rr = 0; rr < SM * 16 / RPI; ++rr) {
+      for (int rr = 0; rr < (p.pre ? SM * 16 / RPI : 0); ++rr) {
         const int r = rr * RPI + lane / LPR;
         float4 y = *reinterpret_cast<const float4*>(&stage[wave][r][cl]);
         if constexpr (MATS == 1 && CH == 128) {
@@ -660,9 +661,11 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
             v += p.bias[n + i];
             y = (float)v;
           }
-          p.pre[oi + i] = y;
           yv[i] = (float)act_f64(p.act, v);
-          p.post[oi + i] = yv[i];
+          if (p.pre) {
+            p.pre[oi + i] = y;
+            p.post[oi + i] = yv[i];
+          }
         }
         // post stays in the stage for the split below (same lane, same place)
         *reinterpret_cast<float4*>(&stage[wave][r][cl]) = make_float4(yv[0], yv[1], yv[2], yv[3]);

@@ -112,6 +112,7 @@ def lib():
     _sig(L, "welvet_dense_group_execute", Status, [_vp, _vp])
     _sig(L, "welvet_dense_group_release", None, [_vp])
     _sig(L, "welvet_dense_chain_mount", Status, [_vp, ctypes.c_int32, _vp])
+    _sig(L, "welvet_dense_chain_mount_ex", Status, [_vp, ctypes.c_int32, ctypes.c_int32, _vp])
     _sig(L, "welvet_dense_chain_execute", Status, [_vp, _vp])
     _sig(L, "welvet_dense_chain_release", None, [_vp])
     _sig(L, "welvet_swiglu_forward_f32", Status,
@@ -338,14 +339,23 @@ class Hip:
 
 
 # --------------------------------------------------------------------------
-class DenseChain:
-    """Groups run in order, each reading the previous group's outputs."""
+CHAIN_INNER_NOT_KEPT = 1
 
-    def __init__(self, groups):
+
+class DenseChain:
+    """Groups run in order, each reading the previous group's outputs.
+    keep_inner=False: groups whose epilogue writes the next group's split do
+    not write their own outputs (WELVET_CHAIN_INNER_NOT_KEPT)."""
+
+    def __init__(self, groups, keep_inner=True):
         n = len(groups)
         self._groups = list(groups)  # the groups must outlive the chain
         h = _vp()
-        check(lib().welvet_dense_chain_mount((_vp * n)(*[g.h for g in groups]), n, ctypes.byref(h)))
+        arr = (_vp * n)(*[g.h for g in groups])
+        if keep_inner:
+            check(lib().welvet_dense_chain_mount(arr, n, ctypes.byref(h)))
+        else:
+            check(lib().welvet_dense_chain_mount_ex(arr, n, CHAIN_INNER_NOT_KEPT, ctypes.byref(h)))
         self.h = h
 
     def execute(self, stream=None):
