@@ -550,7 +550,8 @@ def backward_workload(pw, hip, name, copies):
 
 
 def make_workload(pw, hip, config, copies, terms=3, batch=1, keep_inner=False):
-    two = 16 if terms == 2 else 0  # backend bit for two activation terms
+    two = {1: 32, 2: 16}.get(terms, 0)  # backend bit for two (16) or one (32) activation terms
+    tname = {1: "_1term", 2: "_2terms"}.get(terms, "")
     if config == "c2":
         return dense_workload(pw, hip, "dense_gemv_4096x4096_fp8e4m3_rowscale_b1", 2, 4, 2, 1,
                               4096, 4096, copies, "hbm")
@@ -563,23 +564,23 @@ def make_workload(pw, hip, config, copies, terms=3, batch=1, keep_inner=False):
         return swiglu_workload(pw, hip, "swiglu_4096x11008_fp4_e8m0_b16", 16, min(copies, 8))
     if config == "c4":
         return dense_workload(pw, hip, "mha_projection_gemm_4096x1024x1024_fp8e5m2_rowscale"
-                              + ("_2terms" if two else ""), 4, 5, 2 | two, 4096, 1024, 1024,
+                              + tname, 4, 5, 2 | two, 4096, 1024, 1024,
                               min(copies, 4), "mfma")
     if config == "c4mha":
         return mha_workload(pw, hip, "mha_layer_b8_s512_d1024_h16_fp8e5m2_rowscale"
-                            + ("_2terms" if two else ""), two)
+                            + tname, two)
     if config == "c2bwd":
         return backward_workload(pw, hip, "dense_backward_4096x4096_fp8e4m3_rowscale_b1", 16)
     if config == "c5chain":
         return chain_workload(pw, hip, "volume_grid_4x4x4_stack3_dense_1024_b256_serial"
-                              + ("_2terms" if two else ""), two)
+                              + tname, two)
     if config.startswith("gemv_"):
         f = config[len("gemv_"):]
         b = max(1, batch)
         return format_workload(pw, hip, f"dense_gemv_4096x4096_{f}_b{b}", f, b, 4096, 4096, copies)
     if config == "c5":
         return cells_workload(pw, hip, "volume_64_cells_3x_dense_1024_b256"
-                              + ("_2terms" if two else "") + ("_inner_kept" if keep_inner else ""),
+                              + tname + ("_inner_kept" if keep_inner else ""),
                               two, keep_inner)
     raise SystemExit(f"unknown config {config}")
 
@@ -697,9 +698,10 @@ def main():
     ap.add_argument("--batch", type=int, default=1,
                     help="batch rows of the packed-format GEMV configs (gemv_<fmt>)")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--terms", type=int, default=3, choices=(2, 3),
+    ap.add_argument("--terms", type=int, default=3, choices=(1, 2, 3),
                     help="activation terms of the matrix-core GEMMs (c4, c4mha, c5, c5chain): "
-                         "3 (default) or 2 (backend bit 16)")
+                         "3 (default), 2 (backend bit 16) or 1 (backend bit 32: the throughput mode, "
+                         "outside the 1e-3 bound)")
     ap.add_argument("--keep-inner", action="store_true",
                     help="c5: also write the fp32 outputs of each cell's first two layers")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",

@@ -126,6 +126,8 @@ static welvet_status dense_mount(int32_t batch, int32_t in, int32_t out, int32_t
     if (st) st = wv::dense_build(in, out, act, dtype, scheme, W_init, bias, bias_len, &s->layer,
                                  s->stream.s);
     s->layer.terms = terms;
+    if (st && terms == 1 && batch > wv::kMxvMaxBatch && batch <= 32)
+      st = Status::err(wv::kUnsupported, "one activation term needs a batch above 32 rows (or 1-4)");
     if (st) st = wv::dense_prepare_rows(&s->layer, batch, s->stream.s);
     if (st) st = wv::ensure_split(&s->ws, wv::dense_workspace_bytes(s->layer, batch));
     if (st) st = s->x.alloc((size_t)batch * in * sizeof(float));

@@ -152,7 +152,8 @@ struct MxgArgs {
   // with the same rows (mpad) and kpad = N (the next layer of a chain, which
   // uses the same number of terms)
   uint8_t* next = nullptr;
-  // activation terms: kTerms, or 2 for one-matrix products
+  // activation terms: kTerms, or 1 or 2 for one-matrix products (1: above
+  // 32 rows only)
   int terms = kTerms;
   // large tiles: 1 when the next launch reads the output (the MHA Q, K, V
   // and SwiGLU gate+up products): plain stores, which leave it in the

@@ -27,10 +27,13 @@ Status check_dtype_scheme(int dtype, int scheme) {
 }
 
 Status decode_backend(int backend, int* scheme, int* terms) {
-  if (backend < 0 || (backend & ~(kBackendTwoTerms | 0xF)) != 0 || (backend & 0xF) > kSchemeBlock32)
-    return Status::err(kInvalid, "backend: scale scheme 0..3, plus 16 for two activation terms");
+  if (backend < 0 || (backend & ~(kBackendTwoTerms | kBackendOneTerm | 0xF)) != 0 ||
+      (backend & 0xF) > kSchemeBlock32 ||
+      (backend & (kBackendTwoTerms | kBackendOneTerm)) == (kBackendTwoTerms | kBackendOneTerm))
+    return Status::err(kInvalid, "backend: scale scheme 0..3, plus 16 for two activation terms "
+                                 "or 32 for one");
   *scheme = backend & 0xF;
-  *terms = (backend & kBackendTwoTerms) ? 2 : kTerms;
+  *terms = (backend & kBackendOneTerm) ? 1 : (backend & kBackendTwoTerms) ? 2 : kTerms;
   return Status::ok();
 }
 

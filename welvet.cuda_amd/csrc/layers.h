@@ -32,6 +32,9 @@ Status check_dtype_scheme(int dtype, int scheme);
 // 1e-3 layer bound. SwiGLU and MHA layers refuse it (their chained products
 // and the softmax take the error past the bound). Other bits are invalid.
 constexpr int kBackendTwoTerms = 0x10;
+// bit 5: one activation term (the throughput mode: about 2.7e-2 relative L2,
+// outside the 1e-3 layer bound); Dense layers above 32 rows only
+constexpr int kBackendOneTerm = 0x20;
 Status decode_backend(int backend, int* scheme, int* terms);
 
 // Scratch owned by a session and reused across calls (grown at mount).

@@ -22,12 +22,24 @@
 // a wave fetches an operand with two fully coalesced 1 KiB loads and needs no
 // LDS for it; the kTerms E8M0 exponents a lane passes to the instruction sit
 // in one dword (byte t), also at 4 l.
+#include <type_traits>
+
 #include "codec.h"
 #include "common.h"
 #include "kernels.h"
 
 namespace wv {
 namespace {
+
+// Calls f(std::integral_constant<int, i>) for i = I .. N - 1: straight-line
+// code with compile-time indices.
+template <int I, int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
+}
 
 constexpr int kThreads = 256;
 constexpr int kFragBytes = 2048;                  // one 16 x 128 E4M3 operand
@@ -422,6 +434,10 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
   // indices and no condition around any load: the compiler then knows
   // exactly which loads are outstanding and waits only for the ones a step
   // uses (a conditional load makes it wait for all of them).
+  // 128-row tiles of a single launch with exactly 8 K steps (K = 1024: the
+  // MHA projections) take the two-step-ahead form below
+  constexpr bool PF2 = BR == 128 && !GROUP && !KS;
+  if (!PF2 || ke - kb != 8) {
   AFrag fr[2];
   {
     uint4 q0, q1, q2, q3;
@@ -469,17 +485,19 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
           }
         };
         auto mfma_half = [&](int c0) {
-          static_assert(NT == 2 || NT == 3, "two or three activation terms");
+          static_assert(NT >= 1 && NT <= 3, "one to three activation terms");
 #pragma unroll
           for (int a = 0; a < SM; ++a)
 #pragma unroll
             for (int c = 0; c < HB; ++c)
               acc[a][c0 + c] = mfma_term<DT, 0>(bf[c], fr[cur].x[0][a], acc[a][c0 + c], bsc[c], fr[cur].xs[a]);
+          if constexpr (NT >= 2) {
 #pragma unroll
-          for (int a = 0; a < SM; ++a)
+            for (int a = 0; a < SM; ++a)
 #pragma unroll
-            for (int c = 0; c < HB; ++c)
-              acc[a][c0 + c] = mfma_term<DT, 1>(bf[c], fr[cur].x[1][a], acc[a][c0 + c], bsc[c], fr[cur].xs[a]);
+              for (int c = 0; c < HB; ++c)
+                acc[a][c0 + c] = mfma_term<DT, 1>(bf[c], fr[cur].x[1][a], acc[a][c0 + c], bsc[c], fr[cur].xs[a]);
+          }
           if constexpr (NT == 3) {
 #pragma unroll
             for (int a = 0; a < SM; ++a)
@@ -525,6 +543,125 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
         __builtin_amdgcn_sched_barrier(0);
       }
     }
+  }
+
+  } else if constexpr (PF2) {
+    // The 8 steps as straight-line code, with loads two steps ahead: step j
+    // computes from LDS buffer j & 1 and activation set j % 3, loads step
+    // j + 2's weights into register set j & 1 (stored to LDS at the end of
+    // step j + 1) and its activations into set (j + 2) % 3. Without a loop
+    // back-edge the compiler waits for exactly the loads each step uses.
+    // Measured at 4096 x 1024 x 1024: 22.97 -> 22.37 us (three terms), 20.1
+    // -> 18.9 us (two terms). Wide tiles do not take it: their weight and
+    // activation sets do not fit the register budget (spills).
+#define WV_LOAD_BX(s, Q0, Q1, Q2, Q3, BE)                                       \
+  do {                                                                          \
+    Q0 = *WV_BSRC(0, s);                                                        \
+    if constexpr (B_CPW >= 2) Q1 = *WV_BSRC(1, s);                              \
+    if constexpr (B_CPW == 4) {                                                 \
+      Q2 = *WV_BSRC(2, s);                                                      \
+      Q3 = *WV_BSRC(3, s);                                                      \
+    }                                                                           \
+    if constexpr (BLK) BE = *reinterpret_cast<const uint32_t*>(bsrc + (s) * 4); \
+  } while (0)
+#define WV_STORE_BX(buf, Q0, Q1, Q2, Q3, BE)                   \
+  do {                                                         \
+    *WV_BDST(0, buf) = Q0;                                     \
+    if constexpr (B_CPW >= 2) *WV_BDST(1, buf) = Q1;           \
+    if constexpr (B_CPW == 4) {                                \
+      *WV_BDST(2, buf) = Q2;                                   \
+      *WV_BDST(3, buf) = Q3;                                   \
+    }                                                          \
+    if constexpr (BLK) ssb[buf][(wave % EC) * 64 + lane] = BE; \
+  } while (0)
+    AFrag f3[3];
+    uint4 qa0, qa1, qa2, qa3, qb0, qb1, qb2, qb3;
+    uint32_t bea = 0, beb = 0;
+    WV_LOAD_BX(kb, qa0, qa1, qa2, qa3, bea);
+    WV_STORE_BX(0, qa0, qa1, qa2, qa3, bea);
+    WV_LOAD_BX(kb + 1, qb0, qb1, qb2, qb3, beb);
+    load_a(kb, f3[0]);
+    load_a(kb + 1, f3[1]);
+    if constexpr (!BLK) {
+      for (int i = tid; i < 2 * BR; i += 64 * W) (&ssb[0][0])[i] = 0x7F7F7F7Fu;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 0));
+    asm volatile("s_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    static_for<0, 8>([&](auto J) {
+      constexpr int j = decltype(J)::value;
+      constexpr int cur = j & 1;
+      const int s = kb + j;
+      const AFrag& fa = f3[j % 3];
+      constexpr int HB = SN < 4 ? SN : 4;
+      v8i bf[HB];
+      int bsc[HB];
+      auto read_b = [&](int c0) {
+#pragma unroll
+        for (int c = 0; c < HB; ++c) {
+          const int row = (c0 + c) * 16 + i16;
+          int4 lo, hi = make_int4(0, 0, 0, 0);
+          if constexpr (FP4) {
+            lo = *reinterpret_cast<const int4*>(&sb[cur][row * 64 + ((g ^ ((row >> 2) & 3)) * 16)]);
+          } else {
+            const int sw = (row >> 1) & 7;
+            lo = *reinterpret_cast<const int4*>(&sb[cur][row * 128 + ((g ^ sw) * 16)]);
+            hi = *reinterpret_cast<const int4*>(&sb[cur][row * 128 + (((4 + g) ^ sw) * 16)]);
+          }
+          bf[c] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+          bsc[c] = (int)((ssb[cur][row] >> (8 * g)) & 0xFFu);
+        }
+      };
+      auto mfma_half = [&](int c0) {
+#pragma unroll
+        for (int a = 0; a < SM; ++a)
+#pragma unroll
+          for (int c = 0; c < HB; ++c)
+            acc[a][c0 + c] = mfma_term<DT, 0>(bf[c], fa.x[0][a], acc[a][c0 + c], bsc[c], fa.xs[a]);
+        if constexpr (NT >= 2) {
+#pragma unroll
+          for (int a = 0; a < SM; ++a)
+#pragma unroll
+            for (int c = 0; c < HB; ++c)
+              acc[a][c0 + c] = mfma_term<DT, 1>(bf[c], fa.x[1][a], acc[a][c0 + c], bsc[c], fa.xs[a]);
+        }
+        if constexpr (NT == 3) {
+#pragma unroll
+          for (int a = 0; a < SM; ++a)
+#pragma unroll
+            for (int c = 0; c < HB; ++c)
+              acc[a][c0 + c] = mfma_term<DT, 2>(bf[c], fa.x[NT - 1][a], acc[a][c0 + c], bsc[c], fa.xs[a]);
+        }
+      };
+      read_b(0);
+      __builtin_amdgcn_sched_barrier(0);
+      // register set j & 1 held step j's weights, stored to LDS at the end of
+      // step j - 1; activation set (j + 2) % 3 was last read by step j - 1.
+      // Past the last step the loads repeat it (nothing reads them).
+      const int nx = s + 2 < ke ? s + 2 : ke - 1;
+      if constexpr ((j & 1) == 0) WV_LOAD_BX(nx, qa0, qa1, qa2, qa3, bea);
+      else WV_LOAD_BX(nx, qb0, qb1, qb2, qb3, beb);
+      load_a(nx, f3[(j + 2) % 3]);
+      __builtin_amdgcn_sched_barrier(0);
+      mfma_half(0);
+#pragma unroll
+      for (int h = 1; h < SN / HB; ++h) {
+        __builtin_amdgcn_sched_barrier(0);
+        read_b(h * HB);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_half(h * HB);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      // step j + 1's weights (loaded during step j - 1) into the other buffer
+      if constexpr (((j + 1) & 1) == 0) WV_STORE_BX(cur ^ 1, qa0, qa1, qa2, qa3, bea);
+      else WV_STORE_BX(cur ^ 1, qb0, qb1, qb2, qb3, beb);
+      __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 0));
+      asm volatile("s_barrier" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+    });
+#undef WV_LOAD_BX
+#undef WV_STORE_BX
   }
 
 #undef WV_BSRC
@@ -1118,7 +1255,10 @@ Status launch_t(const MxgArgs& p, int bm, hipStream_t st) {
         if (!p.part) return Status::err(kInvalid, "mxg: K-split partial buffer missing");
         const int tiles_n = (p.N + 127) / 128;
         const dim3 grid((unsigned)(tiles_m * tiles_n), (unsigned)ks);
-        if (p.terms == 2)
+        if (p.terms == 1)
+          k_mxg<DT, BLK, 1, false, kMxgWaves, 128, true, 1><<<grid, 64 * kMxgWaves, 0, st>>>(
+              p, nullptr, tiles_m, tiles_n);
+        else if (p.terms == 2)
           k_mxg<DT, BLK, 1, false, kMxgWaves, 128, true, 2><<<grid, 64 * kMxgWaves, 0, st>>>(
               p, nullptr, tiles_m, tiles_n);
         else
@@ -1134,6 +1274,15 @@ Status launch_t(const MxgArgs& p, int bm, hipStream_t st) {
     const int tiles_n = wide ? (p.N + 256 / MATS - 1) / (256 / MATS) : (p.N + 128 / MATS - 1) / (128 / MATS);
     const unsigned grid = (unsigned)(tiles_m * tiles_n);
     if constexpr (MATS == 1) {
+      if (p.terms == 1) {
+        if (wide)
+          k_mxg<DT, BLK, 1, false, kMxgWaves, 256, false, 1><<<grid, 64 * kMxgWaves, 0, st>>>(
+              p, nullptr, tiles_m, tiles_n);
+        else
+          k_mxg<DT, BLK, 1, false, kMxgWaves, 128, false, 1><<<grid, 64 * kMxgWaves, 0, st>>>(
+              p, nullptr, tiles_m, tiles_n);
+        return hip_status(hipGetLastError(), "mxg launch");
+      }
       if (p.terms == 2) {
         if (wide)
           k_mxg<DT, BLK, 1, false, kMxgWaves, 256, false, 2><<<grid, 64 * kMxgWaves, 0, st>>>(
@@ -1158,9 +1307,11 @@ Status launch_t(const MxgArgs& p, int bm, hipStream_t st) {
 
 template <int MATS>
 Status launch_m(const MxgArgs& p, int dtype, bool blk, int bm, hipStream_t st) {
-  if (p.terms != 2 && p.terms != kTerms) return Status::err(kInvalid, "mxg: terms must be 2 or 3");
+  if (p.terms < 1 || p.terms > kTerms) return Status::err(kInvalid, "mxg: terms must be 1, 2 or 3");
   if (MATS == 2 && p.terms != kTerms)
-    return Status::err(kUnsupported, "mxg: two activation terms are for one-matrix products");
+    return Status::err(kUnsupported, "mxg: fewer activation terms are for one-matrix products");
+  if (p.terms == 1 && bm != kBM)
+    return Status::err(kUnsupported, "mxg: one activation term needs more than 32 rows");
   switch (dtype) {
   case kE4M3: return blk ? launch_t<kE4M3, true, MATS>(p, bm, st) : launch_t<kE4M3, false, MATS>(p, bm, st);
   case kE5M2: return blk ? launch_t<kE5M2, true, MATS>(p, bm, st) : launch_t<kE5M2, false, MATS>(p, bm, st);
@@ -1196,7 +1347,7 @@ constexpr size_t kStreamSplitBytes = 8u << 20;
 
 Status launch_split(const float* x, int x_stride, int M, int cols, int kpad, uint8_t* buf,
                     hipStream_t st, int terms) {
-  if (terms != 2 && terms != kTerms) return Status::err(kInvalid, "split: terms must be 2 or 3");
+  if (terms < 1 || terms > kTerms) return Status::err(kInvalid, "split: terms must be 1, 2 or 3");
   if (kpad % 128 != 0) return Status::err(kInvalid, "split: kpad must be a multiple of 128");
   const int mpad = (int)round_up(M, mxg_block_m(M));
   uint8_t* a = buf;
@@ -1205,7 +1356,10 @@ Status launch_split(const float* x, int x_stride, int M, int cols, int kpad, uin
   const unsigned grid = (unsigned)((waves + kThreads / 64 - 1) / (kThreads / 64));
   const bool vec = x_stride % 4 == 0 && cols % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
   const int stream = (size_t)terms * mpad * kpad >= kStreamSplitBytes;
-  if (terms == 2) {
+  if (terms == 1) {
+    if (vec) k_split<true, 1><<<grid, kThreads, 0, st>>>(x, x_stride, M, cols, mpad, kpad, a, as, nullptr, stream);
+    else k_split<false, 1><<<grid, kThreads, 0, st>>>(x, x_stride, M, cols, mpad, kpad, a, as, nullptr, stream);
+  } else if (terms == 2) {
     if (vec) k_split<true, 2><<<grid, kThreads, 0, st>>>(x, x_stride, M, cols, mpad, kpad, a, as, nullptr, stream);
     else k_split<false, 2><<<grid, kThreads, 0, st>>>(x, x_stride, M, cols, mpad, kpad, a, as, nullptr, stream);
   } else {
@@ -1217,14 +1371,17 @@ Status launch_split(const float* x, int x_stride, int M, int cols, int kpad, uin
 
 Status launch_split_group(const SplitJob* jobs, int n, bool vec, int x_stride, int M, int cols,
                           int kpad, hipStream_t st, int terms) {
-  if (terms != 2 && terms != kTerms) return Status::err(kInvalid, "split: terms must be 2 or 3");
+  if (terms < 1 || terms > kTerms) return Status::err(kInvalid, "split: terms must be 1, 2 or 3");
   if (n <= 0 || !jobs) return Status::err(kInvalid, "split group: no members");
   if (kpad % 128 != 0) return Status::err(kInvalid, "split: kpad must be a multiple of 128");
   const int mpad = (int)round_up(M, mxg_block_m(M));
   const int64_t waves = (int64_t)(mpad / 16) * (kpad / 128);
   const dim3 grid((unsigned)((waves + kThreads / 64 - 1) / (kThreads / 64)), (unsigned)n);
   const int stream = (size_t)terms * mpad * kpad * n >= kStreamSplitBytes;
-  if (terms == 2) {
+  if (terms == 1) {
+    if (vec) k_split<true, 1><<<grid, kThreads, 0, st>>>(nullptr, x_stride, M, cols, mpad, kpad, nullptr, nullptr, jobs, stream);
+    else k_split<false, 1><<<grid, kThreads, 0, st>>>(nullptr, x_stride, M, cols, mpad, kpad, nullptr, nullptr, jobs, stream);
+  } else if (terms == 2) {
     if (vec) k_split<true, 2><<<grid, kThreads, 0, st>>>(nullptr, x_stride, M, cols, mpad, kpad, nullptr, nullptr, jobs, stream);
     else k_split<false, 2><<<grid, kThreads, 0, st>>>(nullptr, x_stride, M, cols, mpad, kpad, nullptr, nullptr, jobs, stream);
   } else {
@@ -1241,6 +1398,15 @@ Status launch_group_t(const MxgArgs* tab, const MxgArgs& p, int n, hipStream_t s
   const int tiles_n = wide ? (p.N + 256 / MATS - 1) / (256 / MATS) : (p.N + 128 / MATS - 1) / (128 / MATS);
   const unsigned grid = (unsigned)(n * tiles_m * tiles_n);
   if constexpr (MATS == 1) {
+    if (p.terms == 1) {
+      if (wide)
+        k_mxg<DT, BLK, 1, true, kMxgWaves, 256, false, 1><<<grid, 64 * kMxgWaves, 0, st>>>(
+            p, tab, tiles_m, tiles_n);
+      else
+        k_mxg<DT, BLK, 1, true, kMxgWaves, 128, false, 1><<<grid, 64 * kMxgWaves, 0, st>>>(
+            p, tab, tiles_m, tiles_n);
+      return hip_status(hipGetLastError(), "mxg group launch");
+    }
     if (p.terms == 2) {
       if (wide)
         k_mxg<DT, BLK, 1, true, kMxgWaves, 256, false, 2><<<grid, 64 * kMxgWaves, 0, st>>>(
@@ -1263,9 +1429,9 @@ Status launch_group_t(const MxgArgs* tab, const MxgArgs& p, int n, hipStream_t s
 Status launch_mxg_group(const MxgArgs* tab, const MxgArgs& p, int n, int dtype, bool blk,
                         hipStream_t st) {
   if (n <= 0 || !tab) return Status::err(kInvalid, "mxg group: no members");
-  if (p.terms != 2 && p.terms != kTerms) return Status::err(kInvalid, "mxg: terms must be 2 or 3");
+  if (p.terms < 1 || p.terms > kTerms) return Status::err(kInvalid, "mxg: terms must be 1, 2 or 3");
   if (p.mats == 2 && p.terms != kTerms)
-    return Status::err(kUnsupported, "mxg: two activation terms are for one-matrix products");
+    return Status::err(kUnsupported, "mxg: fewer activation terms are for one-matrix products");
   if (mxg_block_m(p.M) != kBM || p.mpad % kBM != 0 || p.kpad % 256 != 0)
     return Status::err(kInvalid, "mxg group: needs the large-tile layout");
   if ((size_t)kTerms * p.mpad * p.kpad >= (1ull << 31) ||
