@@ -43,6 +43,7 @@ __device__ __forceinline__ void static_for(F&& f) {
 
 constexpr int kThreads = 256;
 constexpr int kFragBytes = 2048;                  // one 16 x 128 E4M3 operand
+constexpr int kFrag6Bytes = 1536;                 // one 16 x 128 FP6 (E2M3) operand
 constexpr int kChunkScaleBytes = 256;             // one exponent dword per lane
 
 typedef int v8i __attribute__((ext_vector_type(8)));
@@ -51,6 +52,8 @@ typedef float v2f __attribute__((ext_vector_type(2)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
 // fp32 input rows in the global address space (global, not flat, loads)
 typedef const __attribute__((address_space(1))) float* GlobalF;
 typedef __attribute__((address_space(1))) uint8_t* GlobalU8;
@@ -80,9 +83,20 @@ constexpr int wfmt() {
 // One scaled MFMA with the weights as first operand and activation term T
 // as second: `xs` holds the exponents of all terms (byte t = term t) and the
 // instruction's op_sel picks byte T, so no per-term extraction is needed.
-template <int DT, int T>
+// X6: the activation terms are FP6 E2M3 (format 2) instead of E4M3 (0).
+template <int DT, int T, bool X6 = false>
 __device__ __forceinline__ v4f mfma_term(v8i w, v8i x, v4f c, int wsc, uint32_t xs) {
-  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(w, x, c, wfmt<DT>(), 0, 0, wsc, T, (int)xs);
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(w, x, c, wfmt<DT>(), X6 ? 2 : 0, 0, wsc, T,
+                                                          (int)xs);
+}
+
+// Three-term splits for one-matrix products on the large tiles hold FP6
+// (E2M3) terms: 0.75 byte per term and element instead of 1, and FP4 weights
+// times FP6 terms run at the FP4/FP6 rate of the matrix cores. The other
+// splits (two or one term, two-matrix products) hold E4M3 terms.
+template <int MATS, int NT>
+constexpr bool act_fp6() {
+  return MATS == 1 && NT == kTerms;
 }
 
 // s_waitcnt immediate (gfx9 encoding) waiting for at most `vm` outstanding
@@ -151,14 +165,72 @@ __device__ __forceinline__ void split_terms(float (&v)[2][16],
     *reinterpret_cast<U32*>(scales + lane * 4) = sword;
 }
 
+// FP6 terms of one (16-row block, 128-wide K chunk) operand slice. The
+// f8f6f4 instruction's FP6 operand gives lane l (row l % 16, g = l / 16) the
+// 32 values k = 32 g + p of one 32-element block, packed element p of the
+// lane's six dwords; the converter packs its two 16-value inputs interleaved
+// (element 2i from the first, 2i + 1 from the second). So the block's amax is
+// the lane's own. Per term: e, the smallest exponent with amax <= 7.5 * 2^e
+// (at least -126, so that 2^-e and 2^e are normal floats); the E2M3 codes of
+// v * 2^-e, rounded to nearest-even by the converter (scale 1); the residual
+// v - dec(code) * 2^e for the next term. The lane stores dwords 0-3 of its
+// operand at chunk + t * kFrag6Bytes + 16 l, dwords 4-5 at chunk + t *
+// kFrag6Bytes + 1024 + 8 l (both planes fully coalesced), and its exponents
+// as one dword at scales + 4 l (byte t: term t).
+template <int AS, int NT = kTerms, bool STREAM = false>
+__device__ __forceinline__ void split_terms6(float (&v)[32],
+                                             __attribute__((address_space(AS))) uint8_t* chunk,
+                                             __attribute__((address_space(AS))) uint8_t* scales,
+                                             int lane) {
+  typedef __attribute__((address_space(AS))) i32x4 I4;
+  typedef __attribute__((address_space(AS))) i32x2 I2;
+  typedef __attribute__((address_space(AS))) uint32_t U32;
+  uint32_t sword = 0x7F7F7F7Fu;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    float am = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) am = fmaxf(am, fabsf(v[j]));
+    int e = e8m0_exponent(am, 7.5f);
+    e = e < -126 ? -126 : e;
+    const float inv = pow2f(-e), sc = pow2f(e);
+    v16f lo, hi;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) lo[i] = v[2 * i] * inv, hi[i] = v[2 * i + 1] * inv;
+    const auto code = __builtin_amdgcn_cvt_scalef32_2xpk16_fp6_f32(lo, hi, 1.0f);
+    if (t + 1 < NT) {
+      const auto d = __builtin_amdgcn_cvt_scalef32_pk32_f32_fp6(code, 1.0f);
+#pragma unroll
+      for (int j = 0; j < 32; ++j) v[j] = fmaf(-d[j], sc, v[j]);
+    }
+    const i32x4 c0 = i32x4{(int)code[0], (int)code[1], (int)code[2], (int)code[3]};
+    const i32x2 c1 = i32x2{(int)code[4], (int)code[5]};
+    I4* d0 = reinterpret_cast<I4*>(chunk + t * kFrag6Bytes + lane * 16);
+    I2* d1 = reinterpret_cast<I2*>(chunk + t * kFrag6Bytes + 1024 + lane * 8);
+    if constexpr (AS == 1 && STREAM) {
+      __builtin_nontemporal_store(c0, d0);
+      __builtin_nontemporal_store(c1, d1);
+    } else {
+      *d0 = c0;
+      *d1 = c1;
+    }
+    sword = (sword & ~(0xFFu << (8 * t))) | ((uint32_t)(e + 127) << (8 * t));
+  }
+  if constexpr (AS == 1 && STREAM)
+    __builtin_nontemporal_store(sword, reinterpret_cast<U32*>(scales + lane * 4));
+  else
+    *reinterpret_cast<U32*>(scales + lane * 4) = sword;
+}
+
 // The activation split, written in operand order. One wave per (16-row block
 // rb, 128-wide K chunk kc): the 16 x 128 fp32 slice is staged in LDS with
 // row-contiguous loads; then lane l (row i16 = l % 16, group g = l / 16)
 // takes the 32 values of its operand, k = 64h + 16g + j (h = 0, 1; j < 16),
 // and split_terms writes them. Rows >= M and columns >= cols give zero codes.
 // VEC: x 16-byte aligned, cols and x_stride multiples of 4. stream: the
-// split is larger than the L2s hold, so its stores are non-temporal.
-template <bool VEC, int NT>
+// split is larger than the L2s hold, so its stores are non-temporal. F6:
+// FP6 terms (split_terms6; lane l takes k = 32 g + p of its row instead).
+template <bool VEC, int NT, bool F6 = false>
 __global__ __launch_bounds__(kThreads) void k_split(const float* __restrict__ x, int x_stride,
                                                     int M, int cols, int mpad, int kpad,
                                                     uint8_t* __restrict__ a,
@@ -213,21 +285,34 @@ __global__ __launch_bounds__(kThreads) void k_split(const float* __restrict__ x,
   // The LDS operations of one wave execute in order, so the reads below see
   // this wave's writes.
   const int i16 = lane & 15, g = lane >> 4;
-  float v[2][16];
-#pragma unroll
-  for (int h = 0; h < 2; ++h)
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const float4 t = *reinterpret_cast<const float4*>(&sl[i16][64 * h + 16 * g + 4 * q]);
-      v[h][4 * q] = t.x, v[h][4 * q + 1] = t.y, v[h][4 * q + 2] = t.z, v[h][4 * q + 3] = t.w;
-    }
-
-  const GlobalU8 chunk = (GlobalU8)(a + (size_t)(rb * KC + kc) * NT * kFragBytes);
   const GlobalU8 scales = (GlobalU8)(as + (size_t)(rb * KC + kc) * kChunkScaleBytes);
-  if (stream)
-    split_terms<1, NT, true>(v, chunk, scales, lane);
-  else
-    split_terms<1, NT, false>(v, chunk, scales, lane);
+  if constexpr (F6) {
+    float v[32];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const float4 t = *reinterpret_cast<const float4*>(&sl[i16][32 * g + 4 * q]);
+      v[4 * q] = t.x, v[4 * q + 1] = t.y, v[4 * q + 2] = t.z, v[4 * q + 3] = t.w;
+    }
+    const GlobalU8 chunk = (GlobalU8)(a + (size_t)(rb * KC + kc) * NT * kFrag6Bytes);
+    if (stream)
+      split_terms6<1, NT, true>(v, chunk, scales, lane);
+    else
+      split_terms6<1, NT, false>(v, chunk, scales, lane);
+  } else {
+    float v[2][16];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float4 t = *reinterpret_cast<const float4*>(&sl[i16][64 * h + 16 * g + 4 * q]);
+        v[h][4 * q] = t.x, v[h][4 * q + 1] = t.y, v[h][4 * q + 2] = t.z, v[h][4 * q + 3] = t.w;
+      }
+    const GlobalU8 chunk = (GlobalU8)(a + (size_t)(rb * KC + kc) * NT * kFragBytes);
+    if (stream)
+      split_terms<1, NT, true>(v, chunk, scales, lane);
+    else
+      split_terms<1, NT, false>(v, chunk, scales, lane);
+  }
 }
 
 // Large-M tile (M > 32): 128 activation rows x 128 staged weight rows (64 per
@@ -344,7 +429,10 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
 
   // activation fragments of this wave (step s adds s * CB / s * 256): the
   // NT terms of a (16-row block, K chunk) are contiguous, CB bytes
-  constexpr int CB = NT * kFragBytes;
+  // FP6 terms (act_fp6): NT fragments of kFrag6Bytes, dwords 0-3 of lane l at
+  // 16 l, dwords 4-5 at 1024 + 8 l
+  constexpr bool X6 = act_fp6<MATS, NT>();
+  constexpr int CB = NT * (X6 ? kFrag6Bytes : kFragBytes);
   const uint8_t* abase[SM];
   const uint32_t* sbase[SM];
 #pragma unroll
@@ -385,9 +473,15 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
       const uint8_t* src = abase[a] + (size_t)s * CB;
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
-        const int4 lo = *reinterpret_cast<const int4*>(src + t * kFragBytes);
-        const int4 hi = *reinterpret_cast<const int4*>(src + t * kFragBytes + 1024);
-        fr.x[t][a] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+        if constexpr (X6) {
+          const int4 lo = *reinterpret_cast<const int4*>(src + t * kFrag6Bytes);
+          const int2 hi = *reinterpret_cast<const int2*>(src + t * kFrag6Bytes + 1024 - lane * 8);
+          fr.x[t][a] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, 0, 0};
+        } else {
+          const int4 lo = *reinterpret_cast<const int4*>(src + t * kFragBytes);
+          const int4 hi = *reinterpret_cast<const int4*>(src + t * kFragBytes + 1024);
+          fr.x[t][a] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+        }
       }
       fr.xs[a] = sbase[a][s * (kChunkScaleBytes / 4)];
     }
@@ -490,20 +584,20 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
           for (int a = 0; a < SM; ++a)
 #pragma unroll
             for (int c = 0; c < HB; ++c)
-              acc[a][c0 + c] = mfma_term<DT, 0>(bf[c], fr[cur].x[0][a], acc[a][c0 + c], bsc[c], fr[cur].xs[a]);
+              acc[a][c0 + c] = mfma_term<DT, 0, X6>(bf[c], fr[cur].x[0][a], acc[a][c0 + c], bsc[c], fr[cur].xs[a]);
           if constexpr (NT >= 2) {
 #pragma unroll
             for (int a = 0; a < SM; ++a)
 #pragma unroll
               for (int c = 0; c < HB; ++c)
-                acc[a][c0 + c] = mfma_term<DT, 1>(bf[c], fr[cur].x[1][a], acc[a][c0 + c], bsc[c], fr[cur].xs[a]);
+                acc[a][c0 + c] = mfma_term<DT, 1, X6>(bf[c], fr[cur].x[1][a], acc[a][c0 + c], bsc[c], fr[cur].xs[a]);
           }
           if constexpr (NT == 3) {
 #pragma unroll
             for (int a = 0; a < SM; ++a)
 #pragma unroll
               for (int c = 0; c < HB; ++c)
-                acc[a][c0 + c] = mfma_term<DT, 2>(bf[c], fr[cur].x[NT - 1][a], acc[a][c0 + c], bsc[c], fr[cur].xs[a]);
+                acc[a][c0 + c] = mfma_term<DT, 2, X6>(bf[c], fr[cur].x[NT - 1][a], acc[a][c0 + c], bsc[c], fr[cur].xs[a]);
           }
         };
         read_b(0);
@@ -618,20 +712,20 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
         for (int a = 0; a < SM; ++a)
 #pragma unroll
           for (int c = 0; c < HB; ++c)
-            acc[a][c0 + c] = mfma_term<DT, 0>(bf[c], fa.x[0][a], acc[a][c0 + c], bsc[c], fa.xs[a]);
+            acc[a][c0 + c] = mfma_term<DT, 0, X6>(bf[c], fa.x[0][a], acc[a][c0 + c], bsc[c], fa.xs[a]);
         if constexpr (NT >= 2) {
 #pragma unroll
           for (int a = 0; a < SM; ++a)
 #pragma unroll
             for (int c = 0; c < HB; ++c)
-              acc[a][c0 + c] = mfma_term<DT, 1>(bf[c], fa.x[1][a], acc[a][c0 + c], bsc[c], fa.xs[a]);
+              acc[a][c0 + c] = mfma_term<DT, 1, X6>(bf[c], fa.x[1][a], acc[a][c0 + c], bsc[c], fa.xs[a]);
         }
         if constexpr (NT == 3) {
 #pragma unroll
           for (int a = 0; a < SM; ++a)
 #pragma unroll
             for (int c = 0; c < HB; ++c)
-              acc[a][c0 + c] = mfma_term<DT, 2>(bf[c], fa.x[NT - 1][a], acc[a][c0 + c], bsc[c], fa.xs[a]);
+              acc[a][c0 + c] = mfma_term<DT, 2, X6>(bf[c], fa.x[NT - 1][a], acc[a][c0 + c], bsc[c], fa.xs[a]);
         }
       };
       read_b(0);
@@ -822,17 +916,29 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
         for (int a = 0; a < SM; ++a) {
           const int rb = rbase / 16 + a;
           const bool live = rb * 16 + i16 < p.M;
-          float v[2][16];
+          const GlobalU8 nchunk = (GlobalU8)(p.next + (size_t)(rb * kcn + kc) * CB);
+          const GlobalU8 nsc = (GlobalU8)(nscale + (size_t)(rb * kcn + kc) * kChunkScaleBytes);
+          if constexpr (X6) {
+            float v[32];
 #pragma unroll
-          for (int h = 0; h < 2; ++h)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const float4 t = *reinterpret_cast<const float4*>(&stage[wave][a * 16 + i16][64 * h + 16 * g + 4 * q]);
-              v[h][4 * q] = live ? t.x : 0.0f, v[h][4 * q + 1] = live ? t.y : 0.0f;
-              v[h][4 * q + 2] = live ? t.z : 0.0f, v[h][4 * q + 3] = live ? t.w : 0.0f;
+            for (int q = 0; q < 8; ++q) {
+              const float4 t = *reinterpret_cast<const float4*>(&stage[wave][a * 16 + i16][32 * g + 4 * q]);
+              v[4 * q] = live ? t.x : 0.0f, v[4 * q + 1] = live ? t.y : 0.0f;
+              v[4 * q + 2] = live ? t.z : 0.0f, v[4 * q + 3] = live ? t.w : 0.0f;
             }
-          split_terms<1, NT, true>(v, (GlobalU8)(p.next + (size_t)(rb * kcn + kc) * CB),
-                             (GlobalU8)(nscale + (size_t)(rb * kcn + kc) * kChunkScaleBytes), lane);
+            split_terms6<1, NT, true>(v, nchunk, nsc, lane);
+          } else {
+            float v[2][16];
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                const float4 t = *reinterpret_cast<const float4*>(&stage[wave][a * 16 + i16][64 * h + 16 * g + 4 * q]);
+                v[h][4 * q] = live ? t.x : 0.0f, v[h][4 * q + 1] = live ? t.y : 0.0f;
+                v[h][4 * q + 2] = live ? t.z : 0.0f, v[h][4 * q + 3] = live ? t.w : 0.0f;
+              }
+            split_terms<1, NT, true>(v, nchunk, nsc, lane);
+          }
         }
         __builtin_amdgcn_wave_barrier();
       }
@@ -1346,7 +1452,7 @@ size_t split_bytes(int M, int kpad) {
 constexpr size_t kStreamSplitBytes = 8u << 20;
 
 Status launch_split(const float* x, int x_stride, int M, int cols, int kpad, uint8_t* buf,
-                    hipStream_t st, int terms) {
+                    hipStream_t st, int terms, int mats) {
   if (terms < 1 || terms > kTerms) return Status::err(kInvalid, "split: terms must be 1, 2 or 3");
   if (kpad % 128 != 0) return Status::err(kInvalid, "split: kpad must be a multiple of 128");
   const int mpad = (int)round_up(M, mxg_block_m(M));
@@ -1363,8 +1469,14 @@ Status launch_split(const float* x, int x_stride, int M, int cols, int kpad, uin
     if (vec) k_split<true, 2><<<grid, kThreads, 0, st>>>(x, x_stride, M, cols, mpad, kpad, a, as, nullptr, stream);
     else k_split<false, 2><<<grid, kThreads, 0, st>>>(x, x_stride, M, cols, mpad, kpad, a, as, nullptr, stream);
   } else {
-    if (vec) k_split<true, kTerms><<<grid, kThreads, 0, st>>>(x, x_stride, M, cols, mpad, kpad, a, as, nullptr, stream);
-    else k_split<false, kTerms><<<grid, kThreads, 0, st>>>(x, x_stride, M, cols, mpad, kpad, a, as, nullptr, stream);
+    // the consumer's activation format (act_fp6)
+    if (mats == 1) {
+      if (vec) k_split<true, kTerms, true><<<grid, kThreads, 0, st>>>(x, x_stride, M, cols, mpad, kpad, a, as, nullptr, stream);
+      else k_split<false, kTerms, true><<<grid, kThreads, 0, st>>>(x, x_stride, M, cols, mpad, kpad, a, as, nullptr, stream);
+    } else {
+      if (vec) k_split<true, kTerms><<<grid, kThreads, 0, st>>>(x, x_stride, M, cols, mpad, kpad, a, as, nullptr, stream);
+      else k_split<false, kTerms><<<grid, kThreads, 0, st>>>(x, x_stride, M, cols, mpad, kpad, a, as, nullptr, stream);
+    }
   }
   return hip_status(hipGetLastError(), "split launch");
 }
@@ -1385,8 +1497,9 @@ Status launch_split_group(const SplitJob* jobs, int n, bool vec, int x_stride, i
     if (vec) k_split<true, 2><<<grid, kThreads, 0, st>>>(nullptr, x_stride, M, cols, mpad, kpad, nullptr, nullptr, jobs, stream);
     else k_split<false, 2><<<grid, kThreads, 0, st>>>(nullptr, x_stride, M, cols, mpad, kpad, nullptr, nullptr, jobs, stream);
   } else {
-    if (vec) k_split<true, kTerms><<<grid, kThreads, 0, st>>>(nullptr, x_stride, M, cols, mpad, kpad, nullptr, nullptr, jobs, stream);
-    else k_split<false, kTerms><<<grid, kThreads, 0, st>>>(nullptr, x_stride, M, cols, mpad, kpad, nullptr, nullptr, jobs, stream);
+    // grouped members are one-matrix (Dense) products: FP6 terms (act_fp6)
+    if (vec) k_split<true, kTerms, true><<<grid, kThreads, 0, st>>>(nullptr, x_stride, M, cols, mpad, kpad, nullptr, nullptr, jobs, stream);
+    else k_split<false, kTerms, true><<<grid, kThreads, 0, st>>>(nullptr, x_stride, M, cols, mpad, kpad, nullptr, nullptr, jobs, stream);
   }
   return hip_status(hipGetLastError(), "split group launch");
 }
