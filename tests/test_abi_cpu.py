@@ -171,11 +171,13 @@ def test_scaled_store_payload_parse(scheme, f, ok):
         assert st.code == 1, st.message
 
 
-@pytest.mark.parametrize("backend,ok", [(0, True), (3, True), (16, True), (19, True), (4, False),
-                                        (32, False), (-1, False)])
+@pytest.mark.parametrize("backend,ok", [(0, True), (3, True), (16, True), (19, True), (32, True),
+                                        (34, True), (4, False), (48, False), (64, False),
+                                        (-1, False)])
 def test_model_backend_bits(backend, ok):
     """backend: scale scheme 0-3 in bits 0-3, bit 4 (16) asks for two
-    activation terms; anything else is code 1, found before device work."""
+    activation terms, bit 5 (32) for one; both bits together, or anything
+    else, is code 1, found before device work."""
     L = pw.lib()
     buf = _one_dense(0, [])
     h = ctypes.c_void_p()
