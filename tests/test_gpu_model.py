@@ -444,3 +444,55 @@ def test_requantized_model_export_mounts_back_identically(gpu, oracle, scheme):
     m2.close()
     for a, b in zip(snap, snap2):
         assert a[:5] == b[:5] and all(np.array_equal(u, v) for u, v in zip(a[5:], b[5:]))
+
+
+def mha_child(w, seq, d, heads, kv_heads, head_dim, msl, mask, pos, dtype, Q, K, V, O):
+    """MHA child (child_wire.hpp:153-192): dims, kinds, dtype, then Q, K, V, O."""
+    w.i32(7, seq, d, heads, kv_heads, head_dim, msl, mask, pos, dtype)
+    w.f32(np.concatenate([np.ravel(Q), np.ravel(K), np.ravel(V), np.ravel(O)]))
+
+
+@pytest.mark.parametrize("B,S,d,H,KVH,msl,mask,pos,lead", [
+    (2, 48, 128, 4, 2, 64, 1, 1, False),   # causal, RoPE, GQA, [B, S, d] input
+    (1, 40, 64, 4, 4, 40, 2, 0, True),     # bidirectional, no positions, after a Dense child
+])
+def test_mha_child_matches_sessions(gpu, oracle, B, S, d, H, KVH, msl, mask, pos, lead):
+    """A Stack whose ops are (a Dense child and) an MHA child, E5M2 stores as
+    the reference's FormatNone payloads, against the same layers run as a
+    Dense session and an MHA session (each tested against the oracle on its
+    own): the model wires the child's dims, kinds, weights and stores to the
+    same kernels, so the outputs agree bit for bit."""
+    rng = np.random.default_rng(B * 100 + S)
+    hd = d // H
+    Q = (rng.standard_normal((H * hd, d)) / np.sqrt(d)).astype(np.float32)
+    K = (rng.standard_normal((KVH * hd, d)) / np.sqrt(d)).astype(np.float32)
+    V = (rng.standard_normal((KVH * hd, d)) / np.sqrt(d)).astype(np.float32)
+    O = (rng.standard_normal((d, H * hd)) / np.sqrt(H * hd)).astype(np.float32)
+    W1 = (rng.standard_normal((d, d)) / np.sqrt(d)).astype(np.float32)
+    w = pw.Wire()
+    w.u32(0x314E4D57)
+    w.i32(0, 1, 1, 1, 1, 1)
+    w.i32(19, 2 if lead else 1)
+    if lead:
+        pw.dense_child(w, d, d, 0, 4, W1)
+    mha_child(w, S, d, H, KVH, 0, msl, mask, pos, 5, Q, K, V, O)
+    for _ in range(3 + (1 if lead else 0)):  # the stack, its child and its ops
+        pw.empty_controls(w)
+    stores = ([(4, W1)] if lead else []) + [(5, Q), (5, K), (5, V), (5, O)]
+    w.i32(len(stores))
+    for dt, Wm in stores:
+        pw.store_payload(w, dt, Wm.shape[0], Wm.shape[1], oracle.pack(dt, Wm))
+    m = pw.ModelSession(w.bytes())
+    x = rng.standard_normal((B, S, d) if not lead else (S, d)).astype(np.float32)
+    y = m.forward(x)
+    m.close()
+    cur = x.reshape(B * S, d)
+    if lead:
+        s = pw.DenseSession(B * S, d, d, 0, 4, 0, W1)
+        _, cur = s.execute(cur)
+        s.close()
+    sess = pw.MHASession(B, S, d, H, KVH, 0, msl, mask, pos, 5, 0, Q, K, V, O)
+    _, want = sess.execute(cur)
+    sess.close()
+    assert y.shape == ((B, S, d) if not lead else (1, S, d))
+    assert np.array_equal(y.reshape(B * S, d), want)
