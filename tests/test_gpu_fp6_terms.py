@@ -1,12 +1,14 @@
 """FP6 (E2M3) activation terms: the three-term split read by one-matrix
-products on the large tiles (Dense layers and MHA projections above 32 rows).
+products on the large tiles (Dense layers and MHA projections above 32
+rows), and the split that the 5-32-row kernel makes in its prologue.
 
 Each 32-element block of x is split into three E2M3 terms: per term, the
 block exponent e is the smallest with amax <= 7.5 * 2^e (at least -126), the
 term is RNE_E2M3(v / 2^e) * 2^e, and v keeps the residual. The f8f6f4 matrix
 cores multiply the stored FP8/FP4 weight codes by the three terms; FP4
-weights times FP6 terms run at the FP4/FP6 rate. Two-term, one-term and
-two-matrix (SwiGLU gate+up) splits keep E4M3 terms.
+weights times FP6 terms run at the FP4/FP6 rate. Two-term and one-term
+splits, and the large-tile two-matrix (SwiGLU gate+up) split, keep E4M3
+terms.
 
 Pinned by a numpy model of the three-term product (the block rule restated,
 E2M3 rounding to nearest-even on the grid 0.125 * {0..15}, 0.25 * {8..15},
@@ -90,7 +92,8 @@ def test_fp6_model_known_values():
 
 @pytest.mark.parametrize("dt,scheme", [(4, 2), (16, 3), (5, 1)])
 @pytest.mark.parametrize("rows,K,N", [(4096, 1024, 1024), (64, 1024, 1024), (300, 700, 513),
-                                      (1024, 4096, 1024), (2048, 256, 4096)])
+                                      (1024, 4096, 1024), (2048, 256, 4096), (16, 4096, 2048),
+                                      (5, 700, 513), (32, 11008, 512)])
 def test_three_term_dense_matches_fp6_model(gpu, oracle, dt, scheme, rows, K, N):
     rng = np.random.default_rng(rows * 3 + K + N + dt)
     W = (rng.standard_normal((N, K)) / np.sqrt(K)).astype(np.float32)

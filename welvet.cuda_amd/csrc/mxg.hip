@@ -988,7 +988,10 @@ __global__ __launch_bounds__(64 * kSmallWaves) __attribute__((amdgpu_waves_per_e
   constexpr int ROWS = 16 * kSmallWaves * RB;  // weight rows per workgroup
   constexpr bool FP4 = DT == kFP4;
   constexpr int WB = FP4 ? 64 : 128;  // code bytes per weight row per chunk
-  constexpr int CB = NT * kFragBytes;  // the NT terms of one split unit
+  // three terms: FP6 (E2M3) terms, as the large tiles use them for one-matrix
+  // products (split_terms6); fewer terms: E4M3
+  constexpr bool X6 = NT == kTerms;
+  constexpr int CB = NT * (X6 ? kFrag6Bytes : kFragBytes);  // the NT terms of one split unit
   __shared__ __attribute__((aligned(16))) uint8_t sA[MB * KRT * CB];
   __shared__ __attribute__((aligned(16))) uint32_t sS[MB * KRT * 64];
 
@@ -1047,7 +1050,8 @@ __global__ __launch_bounds__(64 * kSmallWaves) __attribute__((amdgpu_waves_per_e
   // The activation terms of the K range, made here from the fp32 input with
   // the code k_split uses and kept in LDS: split unit j = (row block b,
   // chunk r), j = b * KR + r, goes to wave j % 8. Each lane loads the 32
-  // values of its operand (row b * 16 + i16, k = 64h + 16g + ..), with
+  // values of its operand (row b * 16 + i16, k = 64h + 16g + .. for E4M3
+  // terms, k = 32g + .. for FP6 terms), with
   // unconditional loads clamped to the last unit, row and column (16-byte
   // loads when XV: x aligned, cols and stride multiples of 4). The first
   // unit's loads are issued before the first D - 1 chunks of weights, so its
@@ -1060,17 +1064,17 @@ __global__ __launch_bounds__(64 * kSmallWaves) __attribute__((amdgpu_waves_per_e
     const int j = wave + kSmallWaves * u < units ? wave + kSmallWaves * u : units - 1;
     const int row = (j / KR) * 16 + i16;
     const float* src = p.x + (size_t)(row < p.M ? row : p.M - 1) * p.x_stride;
-    const int kb = (k0 + j % KR) * 128 + 16 * g;
+    const int kb = (k0 + j % KR) * 128 + (X6 ? 32 : 16) * g;
     if constexpr (XV) {
 #pragma unroll
       for (int q = 0; q < 8; ++q) {
-        const int k = kb + 64 * (q >> 2) + 4 * (q & 3);
+        const int k = X6 ? kb + 4 * q : kb + 64 * (q >> 2) + 4 * (q & 3);
         xin[q] = *reinterpret_cast<const float4*>(src + (k < p.cols ? k : 0));
       }
     } else {
 #pragma unroll
       for (int q = 0; q < 8; ++q) {
-        const int k = kb + 64 * (q >> 2) + 4 * (q & 3);
+        const int k = X6 ? kb + 4 * q : kb + 64 * (q >> 2) + 4 * (q & 3);
         xin[q].x = src[k < p.cols ? k : p.cols - 1];
         xin[q].y = src[k + 1 < p.cols ? k + 1 : p.cols - 1];
         xin[q].z = src[k + 2 < p.cols ? k + 2 : p.cols - 1];
@@ -1089,19 +1093,23 @@ __global__ __launch_bounds__(64 * kSmallWaves) __attribute__((amdgpu_waves_per_e
     const int j = wave + kSmallWaves * u;
     if (j < units) {  // uniform
       const bool rowok = (j / KR) * 16 + i16 < p.M;
-      const int kb = (k0 + j % KR) * 128 + 16 * g;
+      const int kb = (k0 + j % KR) * 128 + (X6 ? 32 : 16) * g;
       float v[2][16];
 #pragma unroll
       for (int q = 0; q < 8; ++q) {
-        const int k = kb + 64 * (q >> 2) + 4 * (q & 3);
+        const int k = X6 ? kb + 4 * q : kb + 64 * (q >> 2) + 4 * (q & 3);
         const float4 t = xin[q];
-        float* d = &v[q >> 2][4 * (q & 3)];
+        float* d = &v[q >> 2][4 * (q & 3)];  // FP6: v viewed as 32 values in k order
         d[0] = rowok && k < p.cols ? t.x : 0.0f;
         d[1] = rowok && k + 1 < p.cols ? t.y : 0.0f;
         d[2] = rowok && k + 2 < p.cols ? t.z : 0.0f;
         d[3] = rowok && k + 3 < p.cols ? t.w : 0.0f;
       }
-      split_terms<3, NT>(v, (LdsU8)(sA + (size_t)j * CB), (LdsU8)(sS + j * 64), lane);
+      if constexpr (X6)
+        split_terms6<3, NT>(reinterpret_cast<float(&)[32]>(v), (LdsU8)(sA + (size_t)j * CB),
+                            (LdsU8)(sS + j * 64), lane);
+      else
+        split_terms<3, NT>(v, (LdsU8)(sA + (size_t)j * CB), (LdsU8)(sS + j * 64), lane);
     }
     if (u + 1 < U) load_unit(u + 1);
   }
@@ -1131,9 +1139,15 @@ __global__ __launch_bounds__(64 * kSmallWaves) __attribute__((amdgpu_waves_per_e
       const uint8_t* src = sA + (size_t)(b * KR + rr) * CB + lane * 16;
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
-        const int4 lo = *reinterpret_cast<const int4*>(src + t * kFragBytes);
-        const int4 hi = *reinterpret_cast<const int4*>(src + t * kFragBytes + 1024);
-        x[t][b] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+        if constexpr (X6) {
+          const int4 lo = *reinterpret_cast<const int4*>(src + t * kFrag6Bytes);
+          const int2 hi = *reinterpret_cast<const int2*>(src + t * kFrag6Bytes + 1024 - lane * 8);
+          x[t][b] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, 0, 0};
+        } else {
+          const int4 lo = *reinterpret_cast<const int4*>(src + t * kFragBytes);
+          const int4 hi = *reinterpret_cast<const int4*>(src + t * kFragBytes + 1024);
+          x[t][b] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+        }
       }
       xs[b] = sS[(b * KR + rr) * 64 + lane];
     }
@@ -1163,14 +1177,14 @@ __global__ __launch_bounds__(64 * kSmallWaves) __attribute__((amdgpu_waves_per_e
       for (int j = 0; j < RB; ++j)
 #pragma unroll
         for (int b = 0; b < MB; ++b)
-          acc[m][j][b] = mfma_term<DT, 0>(w[m][j], x[0][b], acc[m][j][b], we[m][j], xs[b]);
+          acc[m][j][b] = mfma_term<DT, 0, X6>(w[m][j], x[0][b], acc[m][j][b], we[m][j], xs[b]);
 #pragma unroll
     for (int m = 0; m < MATS; ++m)
 #pragma unroll
       for (int j = 0; j < RB; ++j)
 #pragma unroll
         for (int b = 0; b < MB; ++b)
-          acc[m][j][b] = mfma_term<DT, 1>(w[m][j], x[1][b], acc[m][j][b], we[m][j], xs[b]);
+          acc[m][j][b] = mfma_term<DT, 1, X6>(w[m][j], x[1][b], acc[m][j][b], we[m][j], xs[b]);
     if constexpr (NT == 3) {
 #pragma unroll
       for (int m = 0; m < MATS; ++m)
@@ -1178,7 +1192,7 @@ __global__ __launch_bounds__(64 * kSmallWaves) __attribute__((amdgpu_waves_per_e
         for (int j = 0; j < RB; ++j)
 #pragma unroll
           for (int b = 0; b < MB; ++b)
-            acc[m][j][b] = mfma_term<DT, 2>(w[m][j], x[NT - 1][b], acc[m][j][b], we[m][j], xs[b]);
+            acc[m][j][b] = mfma_term<DT, 2, X6>(w[m][j], x[NT - 1][b], acc[m][j][b], we[m][j], xs[b]);
     }
     __builtin_amdgcn_sched_barrier(0);
   }
