@@ -21,7 +21,6 @@ split. 5..32-row batches refuse the option at mount.
 import numpy as np
 import pytest
 
-import pywelvet as pw
 from test_gpu_dense import rel_l2
 
 pytestmark = pytest.mark.gpu
