@@ -1,14 +1,13 @@
-"""FP6 (E2M3) activation terms: the three-term split read by one-matrix
-products on the large tiles (Dense layers and MHA projections above 32
-rows), and the split that the 5-32-row kernel makes in its prologue.
+"""FP6 (E2M3) activation terms: every three-term split (the default), on the
+large tiles (above 32 rows: Dense, SwiGLU and MHA projections) and in the
+prologue of the 5-32-row kernel.
 
 Each 32-element block of x is split into three E2M3 terms: per term, the
 block exponent e is the smallest with amax <= 7.5 * 2^e (at least -126), the
 term is RNE_E2M3(v / 2^e) * 2^e, and v keeps the residual. The f8f6f4 matrix
 cores multiply the stored FP8/FP4 weight codes by the three terms; FP4
 weights times FP6 terms run at the FP4/FP6 rate. Two-term and one-term
-splits, and the large-tile two-matrix (SwiGLU gate+up) split, keep E4M3
-terms.
+splits keep E4M3 terms.
 
 Pinned by a numpy model of the three-term product (the block rule restated,
 E2M3 rounding to nearest-even on the grid 0.125 * {0..15}, 0.25 * {8..15},

@@ -202,11 +202,12 @@ __global__ __launch_bounds__(64) void k_attention(AttnArgs a) {
 // matrix-core operand order, double-buffered through registers, one barrier
 // per tile. Per 16-key block a wave runs
 //   S^T = K Q^T  on the bf16 matrix cores (v_mfma_f32_16x16x32_bf16, hd/32
-//                steps), K and Q each split into three bf16 terms hi + mid +
-//                lo (x - hi - mid - lo ~ 2^-24 |x|) and the six products
-//                down to 2^-18 relative kept (hh, hm, mh, hl, lh, mm): the
-//                dropped ones are below 2^-26, so the scores carry fp32
-//                accuracy. Lane l holds the scores of query l%16 for keys
+//                steps), Q split into three bf16 terms hi + mid + lo
+//                (x - hi - mid - lo ~ 2^-24 |x|) and K into two, hi + lo
+//                (k - hi - lo ~ 2^-17 |k|), and the five products down to
+//                2^-16 relative kept (hh, hm, lh, hl, lm): the scores carry
+//                ~2^-17 relative accuracy, and K costs two thirds of the
+//                LDS bytes of three terms. Lane l holds the scores of query l%16 for keys
 //                4*(l/16) + i, i = 0..3;
 //   O^T += V^T P^T: the same 4 values per lane are the B operand (MFMA k
 //                index l/16 <-> key 4*(l/16) + j at step j), V^T the A
@@ -227,9 +228,9 @@ void k_attn_mfma(AttnArgs a, int qblocks) {
   constexpr int KS = HD / 32;                           // QK MFMA steps (32 head dims)
   constexpr int DT = HD / 16;                           // 16-wide head-dim tiles of O
   constexpr int NT = 64 * kAttnWaves;                   // threads
-  // K in bf16 operand order: [16-key block kb][step ks][hi, mid, lo][lane][8]:
+  // K in bf16 operand order: [16-key block kb][step ks][hi, lo][lane][8]:
   // lane 16 g + c16 holds key 16 kb + c16, head dims 32 ks + 8 g + j
-  constexpr int KBYTES = 4 * KS * 3 * 1024;
+  constexpr int KBYTES = 4 * KS * 2 * 1024;
   __shared__ __attribute__((aligned(16))) uint8_t ksb[2][KBYTES];
   // V in bf16 operand order: [32-key group q][head-dim tile dt][hi, lo][lane][8]
   constexpr int VBYTES = 2 * DT * 2 * 1024;
@@ -311,7 +312,8 @@ void k_attn_mfma(AttnArgs a, int qblocks) {
   };
   // K row r, head dims d..d+3 (d = c4 or c4 + HD/2, a multiple of 4) go to
   // block r / 16, step d / 32, lane 16 ((d / 8) % 4) + r % 16, elements
-  // d % 8 .. + 3: one 8-byte store per term
+  // d % 8 .. + 3: one 8-byte store per term. K takes two bf16 terms, hi and
+  // lo = bf16(k - hi) (k - hi is exact): k to ~2^-17 relative.
   auto store_k = [&](int buf) {
 #pragma unroll
     for (int u = 0; u < PU; ++u) {
@@ -321,17 +323,18 @@ void k_attn_mfma(AttnArgs a, int qblocks) {
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
         const int d = c4 + half * (HD / 2);
-        __bf16 t[3][4];
+        __bf16 t[2][4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          __bf16 t3[3];
-          split3(kreg[2 * u + half][e], t3);
-          t[0][e] = t3[0], t[1][e] = t3[1], t[2][e] = t3[2];
+          const float k = kreg[2 * u + half][e];
+          const __bf16 hi = (__bf16)k;
+          t[0][e] = hi;
+          t[1][e] = (__bf16)(k - (float)hi);
         }
-        uint8_t* dst = ksb[buf] + (size_t)(((r >> 4) * KS + (d >> 5)) * 3) * 1024 +
+        uint8_t* dst = ksb[buf] + (size_t)(((r >> 4) * KS + (d >> 5)) * 2) * 1024 +
                        (((d >> 3) & 3) * 16 + (r & 15)) * 16 + (d & 7) * 2;
 #pragma unroll
-        for (int term = 0; term < 3; ++term) {
+        for (int term = 0; term < 2; ++term) {
           bf16x4 v = {t[term][0], t[term][1], t[term][2], t[term][3]};
           *reinterpret_cast<bf16x4*>(dst + term * 1024) = v;
         }
@@ -364,22 +367,21 @@ void k_attn_mfma(AttnArgs a, int qblocks) {
         }
     }
   };
-  // S^T of a tile: 4 blocks of 16 keys; the small products first
+  // S^T of a tile: 4 blocks of 16 keys; K (hi, lo) times Q (hi, mid, lo):
+  // the five products down to 2^-16 relative, the small ones first
   auto scores = [&](const uint8_t* kt, v4f (&sc)[4]) {
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
       sc[kb] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        const uint8_t* kp = kt + (size_t)((kb * KS + ks) * 3) * 1024 + lane * 16;
+        const uint8_t* kp = kt + (size_t)((kb * KS + ks) * 2) * 1024 + lane * 16;
         const bf16x8 kh = *reinterpret_cast<const bf16x8*>(kp);
-        const bf16x8 km = *reinterpret_cast<const bf16x8*>(kp + 1024);
-        const bf16x8 kl = *reinterpret_cast<const bf16x8*>(kp + 2048);
-        sc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(km, qop[ks][1], sc[kb], 0, 0, 0);
+        const bf16x8 kl = *reinterpret_cast<const bf16x8*>(kp + 1024);
+        sc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl, qop[ks][1], sc[kb], 0, 0, 0);
         sc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, qop[ks][2], sc[kb], 0, 0, 0);
         sc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl, qop[ks][0], sc[kb], 0, 0, 0);
         sc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, qop[ks][1], sc[kb], 0, 0, 0);
-        sc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(km, qop[ks][0], sc[kb], 0, 0, 0);
         sc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, qop[ks][0], sc[kb], 0, 0, 0);
       }
     }

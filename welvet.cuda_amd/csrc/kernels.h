@@ -106,9 +106,9 @@ Status launch_mxv(const MxvArgs& a, int dtype, bool blk, hipStream_t st);
 // ---- batched GEMM on the scaled MFMA (mxg.hip) ----
 // Activations are split into kTerms terms with per-32 E8M0 scales (two or one
 // for one-matrix products that ask for them: less residual precision, less
-// matrix-core work and fewer activation bytes). Three-term splits read by a
-// one-matrix product hold FP6 E2M3 terms ((block, chunk) slices of 3 x 1.5
-// KiB), the others E4M3 terms (NT x 2 KiB). The split buffer is always sized
+// matrix-core work and fewer activation bytes). Three-term splits hold FP6
+// E2M3 terms ((block, chunk) slices of 3 x 1.5 KiB), the others E4M3 terms
+// (NT x 2 KiB). The split buffer is always sized
 // for kTerms E4M3 terms; the exponents sit at the same offset in every
 // format.
 constexpr int kTerms = 3;
@@ -171,12 +171,10 @@ size_t mxg_part_bytes(int M, int kpad, int N, int mats);
 // Bytes of the split buffer for M rows of kpad columns.
 size_t split_bytes(int M, int kpad);
 // x [M][cols] (row stride x_stride) -> split terms in buf.
-// mats: the matrices of the product that reads the split (1: Dense, MHA
-// projections; 2: SwiGLU gate+up). Three-term splits for one-matrix products
-// hold FP6 (E2M3) terms, the others E4M3 terms; the product's kernel reads
-// the same format.
+// Three-term splits hold FP6 (E2M3) terms, two- and one-term splits E4M3
+// terms; the product's kernel reads the same format.
 Status launch_split(const float* x, int x_stride, int M, int cols, int kpad, uint8_t* buf,
-                    hipStream_t st, int terms = kTerms, int mats = 1);
+                    hipStream_t st, int terms = kTerms);
 Status launch_mxg(const MxgArgs& p, int dtype, bool blk, hipStream_t st);
 // Grouped forms over n members that share every shape field: `jobs` / `tab`
 // are device arrays of n entries (one split input and buffer / one GEMM

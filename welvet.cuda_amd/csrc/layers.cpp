@@ -648,8 +648,7 @@ Status swiglu_forward(const SwiGLULayer& L, int rows, const float* x, float* h, 
     WV_TRY(ensure_split(ws, swiglu_workspace_bytes(L, rows)));
     uint8_t* buf = split_buf(ws);
     MxgArgs p = mxg_args(L.gate, rows, buf);
-    if (mxg_block_m(rows) > 16)
-      WV_TRY(launch_split(x, L.in, rows, L.in, L.gate.dev.kpad, buf, st, kTerms, 2));
+    if (mxg_block_m(rows) > 16) WV_TRY(launch_split(x, L.in, rows, L.in, L.gate.dev.kpad, buf, st));
     else set_input(p, x, L.in, L.in);
     p.mats = 2;
     p.codes[1] = L.up.dev.d_codes();

@@ -90,13 +90,13 @@ __device__ __forceinline__ v4f mfma_term(v8i w, v8i x, v4f c, int wsc, uint32_t 
                                                           (int)xs);
 }
 
-// Three-term splits for one-matrix products on the large tiles hold FP6
-// (E2M3) terms: 0.75 byte per term and element instead of 1, and FP4 weights
-// times FP6 terms run at the FP4/FP6 rate of the matrix cores. The other
-// splits (two or one term, two-matrix products) hold E4M3 terms.
-template <int MATS, int NT>
+// Three-term splits hold FP6 (E2M3) terms: 0.75 byte per term and element
+// instead of 1, and FP4 weights times FP6 terms run at the FP4/FP6 rate of
+// the matrix cores. Two- and one-term splits hold E4M3 terms (two FP6 terms
+// would sit at 7.8e-4 of the 1e-3 bound).
+template <int NT>
 constexpr bool act_fp6() {
-  return MATS == 1 && NT == kTerms;
+  return NT == kTerms;
 }
 
 // s_waitcnt immediate (gfx9 encoding) waiting for at most `vm` outstanding
@@ -431,7 +431,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W
   // NT terms of a (16-row block, K chunk) are contiguous, CB bytes
   // FP6 terms (act_fp6): NT fragments of kFrag6Bytes, dwords 0-3 of lane l at
   // 16 l, dwords 4-5 at 1024 + 8 l
-  constexpr bool X6 = act_fp6<MATS, NT>();
+  constexpr bool X6 = act_fp6<NT>();
   constexpr int CB = NT * (X6 ? kFrag6Bytes : kFragBytes);
   const uint8_t* abase[SM];
   const uint32_t* sbase[SM];
@@ -988,9 +988,9 @@ __global__ __launch_bounds__(64 * kSmallWaves) __attribute__((amdgpu_waves_per_e
   constexpr int ROWS = 16 * kSmallWaves * RB;  // weight rows per workgroup
   constexpr bool FP4 = DT == kFP4;
   constexpr int WB = FP4 ? 64 : 128;  // code bytes per weight row per chunk
-  // three terms: FP6 (E2M3) terms, as the large tiles use them for one-matrix
-  // products (split_terms6); fewer terms: E4M3
-  constexpr bool X6 = NT == kTerms;
+  // three terms: FP6 (E2M3) terms (split_terms6), as on the large tiles;
+  // fewer terms: E4M3
+  constexpr bool X6 = act_fp6<NT>();
   constexpr int CB = NT * (X6 ? kFrag6Bytes : kFragBytes);  // the NT terms of one split unit
   __shared__ __attribute__((aligned(16))) uint8_t sA[MB * KRT * CB];
   __shared__ __attribute__((aligned(16))) uint32_t sS[MB * KRT * 64];
@@ -1466,7 +1466,7 @@ size_t split_bytes(int M, int kpad) {
 constexpr size_t kStreamSplitBytes = 8u << 20;
 
 Status launch_split(const float* x, int x_stride, int M, int cols, int kpad, uint8_t* buf,
-                    hipStream_t st, int terms, int mats) {
+                    hipStream_t st, int terms) {
   if (terms < 1 || terms > kTerms) return Status::err(kInvalid, "split: terms must be 1, 2 or 3");
   if (kpad % 128 != 0) return Status::err(kInvalid, "split: kpad must be a multiple of 128");
   const int mpad = (int)round_up(M, mxg_block_m(M));
@@ -1483,14 +1483,9 @@ Status launch_split(const float* x, int x_stride, int M, int cols, int kpad, uin
     if (vec) k_split<true, 2><<<grid, kThreads, 0, st>>>(x, x_stride, M, cols, mpad, kpad, a, as, nullptr, stream);
     else k_split<false, 2><<<grid, kThreads, 0, st>>>(x, x_stride, M, cols, mpad, kpad, a, as, nullptr, stream);
   } else {
-    // the consumer's activation format (act_fp6)
-    if (mats == 1) {
-      if (vec) k_split<true, kTerms, true><<<grid, kThreads, 0, st>>>(x, x_stride, M, cols, mpad, kpad, a, as, nullptr, stream);
-      else k_split<false, kTerms, true><<<grid, kThreads, 0, st>>>(x, x_stride, M, cols, mpad, kpad, a, as, nullptr, stream);
-    } else {
-      if (vec) k_split<true, kTerms><<<grid, kThreads, 0, st>>>(x, x_stride, M, cols, mpad, kpad, a, as, nullptr, stream);
-      else k_split<false, kTerms><<<grid, kThreads, 0, st>>>(x, x_stride, M, cols, mpad, kpad, a, as, nullptr, stream);
-    }
+    // three terms: FP6 (act_fp6)
+    if (vec) k_split<true, kTerms, true><<<grid, kThreads, 0, st>>>(x, x_stride, M, cols, mpad, kpad, a, as, nullptr, stream);
+    else k_split<false, kTerms, true><<<grid, kThreads, 0, st>>>(x, x_stride, M, cols, mpad, kpad, a, as, nullptr, stream);
   }
   return hip_status(hipGetLastError(), "split launch");
 }
@@ -1511,7 +1506,7 @@ Status launch_split_group(const SplitJob* jobs, int n, bool vec, int x_stride, i
     if (vec) k_split<true, 2><<<grid, kThreads, 0, st>>>(nullptr, x_stride, M, cols, mpad, kpad, nullptr, nullptr, jobs, stream);
     else k_split<false, 2><<<grid, kThreads, 0, st>>>(nullptr, x_stride, M, cols, mpad, kpad, nullptr, nullptr, jobs, stream);
   } else {
-    // grouped members are one-matrix (Dense) products: FP6 terms (act_fp6)
+    // three terms: FP6 (act_fp6)
     if (vec) k_split<true, kTerms, true><<<grid, kThreads, 0, st>>>(nullptr, x_stride, M, cols, mpad, kpad, nullptr, nullptr, jobs, stream);
     else k_split<false, kTerms, true><<<grid, kThreads, 0, st>>>(nullptr, x_stride, M, cols, mpad, kpad, nullptr, nullptr, jobs, stream);
   }
