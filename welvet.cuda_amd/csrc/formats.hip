@@ -27,6 +27,7 @@
 // padding per 110), so a GEMV reads the packed size (plus x and y). Rows are
 // padded to a multiple of 16 with zero bytes (zero scales: padding rows read
 // as 0).
+#include "act.h"
 #include "common.h"
 #include "kernels.h"
 #include "wave.h"
@@ -455,21 +456,6 @@ __global__ __launch_bounds__(kThreads) void k_fmt_dequant(FmtArgs a, int rows, f
   for (int e = 0; e < 32; ++e) o[e] = y[e];
 }
 
-__device__ __forceinline__ double act_f64(int act, double x) {
-  switch (act) {
-  case kReLU: return x < 0.0 ? 0.0 : x;
-  case kSilu: return x / (1.0 + exp(-x));
-  case kGELU: {
-    const double k = 0.7978845608028654;
-    return 0.5 * x * (1.0 + tanh(k * (x + 0.044715 * x * x * x)));
-  }
-  case kTanh: return tanh(x);
-  case kSigmoid: return 1.0 / (1.0 + exp(-x));
-  case kLeaky: return x < 0.0 ? 0.01 * x : x;
-  case kReLU2: return x < 0.0 ? 0.0 : x * x;
-  default: return x;
-  }
-}
 
 __device__ __forceinline__ uint4 load_stream(const uint8_t* p) {
   typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));

@@ -13,6 +13,7 @@
 // bias/activation rule (src/cuda/kernels.cu:147-161) or the SwiGLU product
 // (kernels.cu:296-304).
 #include "codec.h"
+#include "act.h"
 #include "common.h"
 #include "kernels.h"
 #include "wave.h"
@@ -34,21 +35,6 @@ typedef float v2f __attribute__((ext_vector_type(2)));
 // lifetime): uniform loads through it compile to scalar loads.
 typedef const float __attribute__((address_space(4)))* ConstF32;
 
-__device__ __forceinline__ double act_f64(int act, double x) {
-  switch (act) {
-  case kReLU: return x < 0.0 ? 0.0 : x;
-  case kSilu: return x / (1.0 + exp(-x));
-  case kGELU: {
-    const double k = 0.7978845608028654;
-    return 0.5 * x * (1.0 + tanh(k * (x + 0.044715 * x * x * x)));
-  }
-  case kTanh: return tanh(x);
-  case kSigmoid: return 1.0 / (1.0 + exp(-x));
-  case kLeaky: return x < 0.0 ? 0.01 * x : x;
-  case kReLU2: return x < 0.0 ? 0.0 : x * x;
-  default: return x;
-  }
-}
 
 // Elements per lane per 16-byte chunk.
 template <int DT>

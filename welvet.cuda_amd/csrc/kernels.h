@@ -176,6 +176,11 @@ size_t split_bytes(int M, int kpad);
 Status launch_split(const float* x, int x_stride, int M, int cols, int kpad, uint8_t* buf,
                     hipStream_t st, int terms = kTerms);
 Status launch_mxg(const MxgArgs& p, int dtype, bool blk, hipStream_t st);
+// Adds the ksplit partial planes of a split product (rows: the product's
+// weight rows per workgroup, which pad the planes) and applies the epilogue
+// (reduce.hip); mats 2: the SwiGLU gate+up pair. Launch errors are left for
+// the caller's hipGetLastError.
+void launch_mxs_reduce(const MxgArgs& p, int ksplit, int rows, int mats, hipStream_t st);
 // Grouped forms over n members that share every shape field: `jobs` / `tab`
 // are device arrays of n entries (one split input and buffer / one GEMM
 // argument block per member). One launch covers all members.

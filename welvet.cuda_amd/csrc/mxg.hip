@@ -25,6 +25,7 @@
 #include <type_traits>
 
 #include "codec.h"
+#include "act.h"
 #include "common.h"
 #include "kernels.h"
 
@@ -59,21 +60,6 @@ typedef const __attribute__((address_space(1))) float* GlobalF;
 typedef __attribute__((address_space(1))) uint8_t* GlobalU8;
 typedef __attribute__((address_space(3))) uint8_t* LdsU8;
 
-__device__ __forceinline__ double act_f64(int act, double x) {
-  switch (act) {
-  case kReLU: return x < 0.0 ? 0.0 : x;
-  case kSilu: return x / (1.0 + exp(-x));
-  case kGELU: {
-    const double k = 0.7978845608028654;
-    return 0.5 * x * (1.0 + tanh(k * (x + 0.044715 * x * x * x)));
-  }
-  case kTanh: return tanh(x);
-  case kSigmoid: return 1.0 / (1.0 + exp(-x));
-  case kLeaky: return x < 0.0 ? 0.01 * x : x;
-  case kReLU2: return x < 0.0 ? 0.0 : x * x;
-  default: return x;
-  }
-}
 
 template <int DT>
 constexpr int wfmt() {
@@ -1245,55 +1231,6 @@ __global__ __launch_bounds__(64 * kSmallWaves) __attribute__((amdgpu_waves_per_e
   }
 }
 
-// Adds the K-split partial sums of k_mxs (in split order) and applies the
-// epilogue; one thread per output, the partial loads of up to 16 splits in
-// flight at a time (consecutive threads read consecutive floats of a plane).
-template <int MATS>
-__global__ __launch_bounds__(kThreads) void k_mxs_reduce(MxgArgs p, int ksplit, int rows) {
-  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  if (i >= (int64_t)p.M * p.N) return;
-  const int mrow = (int)(i / p.N), n = (int)(i % p.N);
-  const size_t npad = ((size_t)p.N + rows - 1) / rows * rows;
-  const size_t plane = (size_t)p.mpad * npad;  // one (split, matrix) plane
-  const float* src = p.part + (size_t)mrow * npad + n;
-  float tot[MATS];
-#pragma unroll
-  for (int m = 0; m < MATS; ++m) tot[m] = 0.0f;
-#pragma unroll 1
-  for (int k0 = 0; k0 < ksplit; k0 += 16) {
-    float t[MATS][16];
-#pragma unroll
-    for (int u = 0; u < 16; ++u) {
-      const int kk = k0 + u < ksplit ? k0 + u : ksplit - 1;
-#pragma unroll
-      for (int m = 0; m < MATS; ++m) t[m][u] = src[((size_t)kk * MATS + m) * plane];
-    }
-#pragma unroll
-    for (int u = 0; u < 16; ++u)
-#pragma unroll
-      for (int m = 0; m < MATS; ++m) tot[m] += k0 + u < ksplit ? t[m][u] : 0.0f;
-  }
-  const size_t oi = (size_t)mrow * p.out_stride + n;
-  if constexpr (MATS == 2) {
-    const float gs = (float)act_f64(kSilu, (double)(tot[0] * p.scale[0][n]));
-    p.pre[oi] = (float)((double)gs * (double)(tot[1] * p.scale[1][n]));
-  } else {
-    float y = tot[0] * p.scale[0][n];
-    if (p.need_epi) {
-      double v = (double)y;
-      if (p.bias && n < p.bias_len) {
-        v += p.bias[n];
-        y = (float)v;
-      }
-      p.pre[oi] = y;
-      p.post[oi] = (float)act_f64(p.act, v);
-    } else {
-      p.pre[oi] = y;
-      if (p.post && p.post != p.pre) p.post[oi] = y;
-    }
-  }
-}
-
 template <int DT, bool BLK, int MATS, int MB, int RB, int KRT, bool XV = true>
 void launch_small_krt(const MxgArgs& p, int ksplit, hipStream_t st) {
   constexpr int NT3 = kTerms;
@@ -1339,9 +1276,7 @@ Status launch_small(const MxgArgs& p, hipStream_t st) {
   if (ksplit > 1) {
     // the kernel boundary makes every split's partial sums visible (the
     // XCDs' L2 caches are not coherent with each other)
-    const int64_t n = (int64_t)p.M * p.N;
-    k_mxs_reduce<MATS><<<(unsigned)((n + kThreads - 1) / kThreads), kThreads, 0, st>>>(
-        p, ksplit, 16 * kSmallWaves * rb);
+    launch_mxs_reduce(p, ksplit, 16 * kSmallWaves * rb, MATS, st);
   }
   return hip_status(hipGetLastError(), "mxs launch");
 }
@@ -1385,8 +1320,7 @@ Status launch_t(const MxgArgs& p, int bm, hipStream_t st) {
           k_mxg<DT, BLK, 1, false, kMxgWaves, 128, true><<<grid, 64 * kMxgWaves, 0, st>>>(
               p, nullptr, tiles_m, tiles_n);
         // the kernel boundary makes every split's partial sums visible
-        const int64_t n = (int64_t)p.M * p.N;
-        k_mxs_reduce<1><<<(unsigned)((n + kThreads - 1) / kThreads), kThreads, 0, st>>>(p, ks, 256);
+        launch_mxs_reduce(p, ks, 256, 1, st);
         return hip_status(hipGetLastError(), "mxg K-split launch");
       }
     }

@@ -20,6 +20,7 @@
 // sums of the 8 waves meet in LDS for the epilogue (row scale, bias,
 // activation, or the SwiGLU product).
 #include "codec.h"
+#include "act.h"
 #include "common.h"
 #include "kernels.h"
 
@@ -40,21 +41,6 @@ __device__ __forceinline__ u32x4 load_stream(const uint8_t* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }
 
-__device__ __forceinline__ double act_f64(int act, double x) {
-  switch (act) {
-  case kReLU: return x < 0.0 ? 0.0 : x;
-  case kSilu: return x / (1.0 + exp(-x));
-  case kGELU: {
-    const double k = 0.7978845608028654;
-    return 0.5 * x * (1.0 + tanh(k * (x + 0.044715 * x * x * x)));
-  }
-  case kTanh: return tanh(x);
-  case kSigmoid: return 1.0 / (1.0 + exp(-x));
-  case kLeaky: return x < 0.0 ? 0.01 * x : x;
-  case kReLU2: return x < 0.0 ? 0.0 : x * x;
-  default: return x;
-  }
-}
 
 __device__ __forceinline__ float quad_max(float v) {
   int o = __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false);

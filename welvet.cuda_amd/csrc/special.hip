@@ -15,6 +15,7 @@
 // rows (all batch rows) with decoded weights and an f64 sum, and applies the
 // layer's epilogue (bias / activation, or the SwiGLU product).
 #include "codec.h"
+#include "act.h"
 #include "common.h"
 #include "kernels.h"
 #include "runtime.h"
@@ -24,21 +25,6 @@ namespace {
 
 constexpr int kThreads = 256;
 
-__device__ __forceinline__ double act_f64(int act, double x) {
-  switch (act) {
-  case kReLU: return x < 0.0 ? 0.0 : x;
-  case kSilu: return x / (1.0 + exp(-x));
-  case kGELU: {
-    const double k = 0.7978845608028654;
-    return 0.5 * x * (1.0 + tanh(k * (x + 0.044715 * x * x * x)));
-  }
-  case kTanh: return tanh(x);
-  case kSigmoid: return 1.0 / (1.0 + exp(-x));
-  case kLeaky: return x < 0.0 ? 0.01 * x : x;
-  case kReLU2: return x < 0.0 ? 0.0 : x * x;
-  default: return x;
-  }
-}
 
 // flags[r] = 1 when row r of the canonical codes holds a non-finite E5M2
 // code (the exponent field all ones). One workgroup per row.
