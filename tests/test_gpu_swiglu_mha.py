@@ -49,6 +49,26 @@ def test_swiglu_matches_oracle(gpu, oracle, dt, scheme, batch, seq, d, inter):
     assert rel_l2(y, oy) <= tol(batch * seq, chain=2)
 
 
+@pytest.mark.parametrize("scheme", [3, 0])
+@pytest.mark.parametrize("rows,d,inter", [(5, 700, 8200), (16, 1024, 8300), (12, 4096, 8192),
+                                          (17, 700, 8200)])
+def test_swiglu_fp4_small_batch_ragged(gpu, oracle, scheme, rows, d, inter):
+    """FP4 SwiGLU at 5-17 rows on the K-split matrix-core path (256-row
+    workgroups): ragged K, output counts that are no multiple of 256 (the
+    grid's last rows clamped), one and two activation row blocks."""
+    rng = np.random.default_rng(rows + d + inter + scheme)
+    G = (rng.standard_normal((inter, d)) / np.sqrt(d)).astype(np.float32)
+    U = (rng.standard_normal((inter, d)) / np.sqrt(d)).astype(np.float32)
+    D = (rng.standard_normal((d, inter)) / np.sqrt(inter)).astype(np.float32)
+    x = rng.standard_normal((rows, d)).astype(np.float32)
+    s = gpu.SwiGLUSession(rows, 1, d, inter, 16, scheme, G, U, D)
+    h, y = s.execute(x)
+    s.close()
+    oh, oy = oracle_swiglu(oracle, 16, scheme, G, U, D, x)
+    assert rel_l2(h, oh) <= tol(rows)
+    assert rel_l2(y, oy) <= tol(rows, chain=2)
+
+
 def test_c3_swiglu_fp4_block32_batch1(gpu, oracle):
     """SwiGLU d_model 4096, d_ff 11008, FP4 E2M1 + E8M0 per 32 along K, batch 1."""
     import pywelvet as pw
