@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 
 import pywelvet as pw
-from test_gpu_dense import rel_l2, tol
+from test_gpu_dense import TOL_CONTRACT, rel_l2, tol
 
 pytestmark = pytest.mark.gpu
 
@@ -118,12 +118,15 @@ def test_repeated_forwards_reuse_device_buffers(gpu, oracle):
     m.close()
 
 
-@pytest.mark.parametrize("scheme", [2, 3])
+@pytest.mark.parametrize("scheme", [2, 3, 2 | 16, 3 | 32])
 def test_grid_chain_matches_layer_by_layer(gpu, oracle, scheme):
     """A grid of two Stack cells run as one chain gives the bits of running
-    each layer as its own session (same kernels: split-K products at 200
-    rows, 56 padding rows). Layers: 1024 -> 1024 (SiLU) -> 1024 -> 512 |
-    512 -> 768 -> 256."""
+    each layer as its own session (split-K products at 200 rows, 56 padding
+    rows). Within a cell the chain fuses the next layer's activation split
+    into each K-split reduce (no split launch between the products), which
+    must not change a bit. Layers: 1024 -> 1024 (SiLU) -> 1024 -> 512 |
+    512 -> 768 -> 256; three activation terms (FP6), two (bit 16) and one
+    (bit 32)."""
     rng = np.random.default_rng(10 + scheme)
     widths = [1024, 1024, 1024, 512, 768, 256]
     kinds = [(4, 1), (16, -1), (5, -1), (4, 0), (16, -1)]
@@ -140,7 +143,13 @@ def test_grid_chain_matches_layer_by_layer(gpu, oracle, scheme):
         _, cur = s.execute(cur)
         s.close()
     assert np.array_equal(y, cur)
-    assert rel_l2(y, oracle_chain(oracle, seq, x, scheme)) <= tol(200, chain=5)
+    err = rel_l2(y, oracle_chain(oracle, seq, x, scheme & 15))
+    if scheme & 32:  # one E4M3 term: ~2.7e-2 per product, outside the contract bound
+        assert err <= 0.15
+    elif scheme & 16:  # two E4M3 terms: ~6.3e-4 per product
+        assert err <= 5 * TOL_CONTRACT
+    else:
+        assert err <= tol(200, chain=5)
     y2 = m.forward(x)  # a second pass over the same buffers
     assert np.array_equal(y2, y)
     m.close()

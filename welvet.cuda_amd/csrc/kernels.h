@@ -181,6 +181,11 @@ Status launch_mxg(const MxgArgs& p, int dtype, bool blk, hipStream_t st);
 // (reduce.hip); mats 2: the SwiGLU gate+up pair. Launch errors are left for
 // the caller's hipGetLastError.
 void launch_mxs_reduce(const MxgArgs& p, int ksplit, int rows, int mats, hipStream_t st);
+// The reduce of a split large-tile product of one matrix (N a multiple of
+// 256, pre and post 16-byte aligned, out_stride a multiple of 4) that also
+// writes the split of post to p.next for the next layer of a chain
+// (reduce.hip).
+void launch_reduce_split(const MxgArgs& p, int ksplit, hipStream_t st);
 // Grouped forms over n members that share every shape field: `jobs` / `tab`
 // are device arrays of n entries (one split input and buffer / one GEMM
 // argument block per member). One launch covers all members.

@@ -364,10 +364,12 @@ static Status fix_nonfinite(const DenseLayer& L, int batch, const float* x, int 
 
 Status dense_forward_split(const DenseLayer& L, int batch, const float* x, bool split_ready,
                            Workspace* ws, float* pre, float* post, hipStream_t st,
-                           const double* rope_tab, int rope_hd, bool keep_out) {
+                           const double* rope_tab, int rope_hd, bool keep_out,
+                           uint8_t* next_split) {
   MxgArgs p = mxg_args(L, batch, split_buf(ws));
   p.pre = pre;
   p.post = post;
+  p.next = next_split;
   p.keep_out = keep_out ? 1 : 0;
   p.rope_tab = rope_tab;
   p.rope_hd = rope_hd;
@@ -379,6 +381,12 @@ Status dense_forward_split(const DenseLayer& L, int batch, const float* x, bool 
   }
   WV_TRY(launch_mxg(p, L.dev.dtype, L.dev.scheme == kSchemeBlock32, st));
   return fix_nonfinite(L, batch, x, L.in, pre, post, st);
+}
+
+bool dense_fuses_next(const DenseLayer& L, const DenseLayer& next, int batch) {
+  return !L.format && !next.format && mxg_block_m(batch) > 16 && L.dev.nf_count() == 0 &&
+         L.out % 256 == 0 && next.in == L.out && next.dev.kpad == L.out &&
+         next.terms == L.terms && mxg_part_bytes(batch, L.dev.kpad, L.out, 1) > 0;
 }
 
 Status dense_forward(const DenseLayer& L, int batch, const float* x, float* pre, float* post,

@@ -43,6 +43,9 @@ struct Workspace {
   DevBuf b;
   DevBuf c;  // MHA: RoPE (cos, sin) table for rope_tokens tokens of rope_hd, rope_theta
   DevBuf d;
+  // a serial chain of Dense layers: the next layer's split terms (and its
+  // partial sums), written by this layer's K-split reduce; swapped with b
+  DevBuf e;
   int rope_tokens = 0, rope_hd = 0;
   double rope_theta = 0.0;
 };
@@ -127,10 +130,19 @@ inline uint8_t* split_buf(Workspace* ws) { return ws->b.as<uint8_t>(); }
 // `split_ready` (launch_split of x with L.dev.kpad already ran); up to 32
 // rows the GEMM kernel splits x itself. keep_out: the next launch reads the
 // output (MxgArgs::keep_out).
+// next_split: the reduce of this layer's K-split product also writes the
+// split of post there, for `next` (dense_fuses_next must hold).
 Status dense_forward_split(const DenseLayer& L, int batch, const float* x, bool split_ready,
                            Workspace* ws, float* pre, float* post, hipStream_t st,
                            const double* rope_tab = nullptr, int rope_hd = 0,
-                           bool keep_out = false);
+                           bool keep_out = false, uint8_t* next_split = nullptr);
+// True when `batch` rows of L and then `next` (whose input is L's post) can
+// run with L's K-split reduce writing next's split terms: both on the
+// split matrix-core path above 32 rows, L's product split along K, N a
+// multiple of 256 equal to next's kpad, the same activation terms, and no
+// weight rows of L with non-finite codes (whose recomputation follows the
+// product).
+bool dense_fuses_next(const DenseLayer& L, const DenseLayer& next, int batch);
 // Grows ws->b to at least n bytes (mount time; a forward that finds it too
 // small allocates, which a captured graph cannot do).
 Status ensure_split(Workspace* ws, size_t n);

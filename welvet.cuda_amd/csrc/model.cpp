@@ -18,6 +18,7 @@
 #include <map>
 #include <stdexcept>
 #include <tuple>
+#include <utility>
 
 #include "codec.h"
 
@@ -408,12 +409,55 @@ Tensor op_forward(ModelNode& c, const Tensor& in, Arena& ar, Workspace* ws, hipS
   return out;
 }
 
+// A Dense op of a serial chain on the split matrix-core path: `ready` when
+// the previous op's reduce already wrote the split of `in` to split_buf(ws);
+// with `next`, this op's reduce writes next's split to ws->e, and the two
+// split buffers are swapped afterwards (ws->e sized for next beforehand, so
+// that nothing reallocates a buffer that holds a split).
+Tensor dense_chain_op(ModelNode& c, const Tensor& in, Arena& ar, Workspace* ws, hipStream_t st,
+                      bool ready, const DenseLayer* next) {
+  require(in.shape.size() == 2, "dense: input shape need [batch,in]");
+  require(in.shape[1] == c.in, "dense: input width mismatch");
+  const int b = in.shape[0];
+  const DenseLayer& L = *c.dense;
+  Tensor out;
+  out.shape = {b, c.out};
+  out.data = ar.get(out.numel());
+  float* pre = L.need_epi() ? ar.get(out.numel()) : nullptr;
+  good(ensure_split(ws, dense_workspace_bytes(L, b)));
+  uint8_t* nsplit = nullptr;
+  if (next) {
+    const size_t need = dense_workspace_bytes(*next, b);
+    if (ws->e.bytes < need) good(ws->e.alloc(need));
+    nsplit = ws->e.as<uint8_t>();
+  }
+  if (pre) good(dense_forward_split(L, b, in.data, ready, ws, pre, out.data, st, nullptr, 0, false, nsplit));
+  else good(dense_forward_split(L, b, in.data, ready, ws, out.data, nullptr, st, nullptr, 0, false, nsplit));
+  if (next) std::swap(ws->b, ws->e);
+  return out;
+}
+
 Tensor stack_forward(std::vector<ModelNode>& children, const Tensor& in, Arena& ar, Workspace* ws,
                      hipStream_t st) {
   std::vector<ModelNode*> ops;
   for (auto& c : children) flatten(c, &ops);
   Tensor cur = in;
-  for (ModelNode* op : ops) cur = op_forward(*op, cur, ar, ws, st);
+  // consecutive Dense ops that dense_fuses_next admits skip the split launch
+  // of the second (stack.cpp:470-494 runs them in this order)
+  bool ready = false;
+  for (size_t i = 0; i < ops.size(); ++i) {
+    ModelNode* op = ops[i];
+    ModelNode* nx = i + 1 < ops.size() ? ops[i + 1] : nullptr;
+    const bool dense2 = op->kind == 1 && cur.shape.size() == 2;
+    const bool fuse = dense2 && nx && nx->kind == 1 &&
+                      dense_fuses_next(*op->dense, *nx->dense, cur.shape[0]);
+    if (fuse || ready) {
+      cur = dense_chain_op(*op, cur, ar, ws, st, ready, fuse ? nx->dense.get() : nullptr);
+      ready = fuse;
+    } else {
+      cur = op_forward(*op, cur, ar, ws, st);
+    }
+  }
   return cur;
 }
 

@@ -28,6 +28,7 @@
 #include "act.h"
 #include "common.h"
 #include "kernels.h"
+#include "split.h"
 
 namespace wv {
 namespace {
@@ -43,23 +44,6 @@ __device__ __forceinline__ void static_for(F&& f) {
 }
 
 constexpr int kThreads = 256;
-constexpr int kFragBytes = 2048;                  // one 16 x 128 E4M3 operand
-constexpr int kFrag6Bytes = 1536;                 // one 16 x 128 FP6 (E2M3) operand
-constexpr int kChunkScaleBytes = 256;             // one exponent dword per lane
-
-typedef int v8i __attribute__((ext_vector_type(8)));
-typedef float v4f __attribute__((ext_vector_type(4)));
-typedef float v2f __attribute__((ext_vector_type(2)));
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-typedef int i32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef float v16f __attribute__((ext_vector_type(16)));
-typedef int i32x2 __attribute__((ext_vector_type(2)));
-// fp32 input rows in the global address space (global, not flat, loads)
-typedef const __attribute__((address_space(1))) float* GlobalF;
-typedef __attribute__((address_space(1))) uint8_t* GlobalU8;
-typedef __attribute__((address_space(3))) uint8_t* LdsU8;
-
 
 template <int DT>
 constexpr int wfmt() {
@@ -76,136 +60,10 @@ __device__ __forceinline__ v4f mfma_term(v8i w, v8i x, v4f c, int wsc, uint32_t 
                                                           (int)xs);
 }
 
-// Three-term splits hold FP6 (E2M3) terms: 0.75 byte per term and element
-// instead of 1, and FP4 weights times FP6 terms run at the FP4/FP6 rate of
-// the matrix cores. Two- and one-term splits hold E4M3 terms (two FP6 terms
-// would sit at 7.8e-4 of the 1e-3 bound).
-template <int NT>
-constexpr bool act_fp6() {
-  return NT == kTerms;
-}
-
 // s_waitcnt immediate (gfx9 encoding) waiting for at most `vm` outstanding
 // vector-memory operations and `lgkm` LDS/scalar operations.
 constexpr int waitcnt_imm(int vm, int lgkm) {
   return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | ((lgkm & 15) << 8);
-}
-
-// The terms of one (16-row block, 128-wide K chunk) operand slice: lane l
-// (row l % 16, group g = l / 16) holds its 32 values v[h][j], k = 64h + 16g +
-// j. A 32-element block is held by lanes l and l ^ 16, which exchange their
-// amax. Per term and half the lane stores its 16 codes with one 16-byte
-// store at chunk + t * kFragBytes + h * 1024 + 16 l; the block exponents are
-// gathered to the lanes that pass them to the instruction (row l % 16, block
-// l / 16) and stored as one dword per lane at scales + 4 l (byte t: term t).
-// AS: the address space of the destination (1 global, 3 LDS).
-template <int AS, int NT = kTerms, bool STREAM = false>
-__device__ __forceinline__ void split_terms(float (&v)[2][16],
-                                            __attribute__((address_space(AS))) uint8_t* chunk,
-                                            __attribute__((address_space(AS))) uint8_t* scales,
-                                            int lane) {
-  typedef __attribute__((address_space(AS))) i32x4 I4;
-  typedef __attribute__((address_space(AS))) uint32_t U32;
-  __attribute__((address_space(AS))) uint8_t* dst = chunk + lane * 16;
-  const int i16 = lane & 15;
-  // exponent of block b = l / 16 for row i16 comes from lane 32 (b & 1) + i16,
-  // half b >> 1
-  const int src = ((lane >> 4) & 1) * 32 + i16;
-  uint32_t sword = 0x7F000000u;  // byte 3 unused
-#pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    int e[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      float am = 0.0f;
-#pragma unroll
-      for (int j = 0; j < 16; ++j) am = fmaxf(am, fabsf(v[h][j]));
-      am = fmaxf(am, __shfl_xor(am, 16, 64));
-      e[h] = e8m0_exponent(am, 448.0f);
-      const float inv = pow2f(-e[h]), sc = pow2f(e[h]);
-      int wq[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        int w4 = __builtin_amdgcn_cvt_pk_fp8_f32(v[h][4 * q] * inv, v[h][4 * q + 1] * inv, 0, false);
-        w4 = __builtin_amdgcn_cvt_pk_fp8_f32(v[h][4 * q + 2] * inv, v[h][4 * q + 3] * inv, w4, true);
-        wq[q] = w4;
-        if (t + 1 < NT) {
-          const v2f q0 = __builtin_amdgcn_cvt_pk_f32_fp8(w4, false);
-          const v2f q1 = __builtin_amdgcn_cvt_pk_f32_fp8(w4, true);
-          v[h][4 * q] -= q0.x * sc, v[h][4 * q + 1] -= q0.y * sc;
-          v[h][4 * q + 2] -= q1.x * sc, v[h][4 * q + 3] -= q1.y * sc;
-        }
-      }
-      const i32x4 codes = i32x4{wq[0], wq[1], wq[2], wq[3]};
-      if constexpr (AS == 1 && STREAM)  // read by a later launch: streaming store
-        __builtin_nontemporal_store(codes, reinterpret_cast<I4*>(dst + t * kFragBytes + h * 1024));
-      else
-        *reinterpret_cast<I4*>(dst + t * kFragBytes + h * 1024) = codes;
-    }
-    const int e0 = __shfl(e[0], src, 64), e1 = __shfl(e[1], src, 64);
-    sword |= (uint32_t)(((lane >> 5) ? e1 : e0) + 127) << (8 * t);
-  }
-  if constexpr (AS == 1 && STREAM)
-    __builtin_nontemporal_store(sword, reinterpret_cast<U32*>(scales + lane * 4));
-  else
-    *reinterpret_cast<U32*>(scales + lane * 4) = sword;
-}
-
-// FP6 terms of one (16-row block, 128-wide K chunk) operand slice. The
-// f8f6f4 instruction's FP6 operand gives lane l (row l % 16, g = l / 16) the
-// 32 values k = 32 g + p of one 32-element block, packed element p of the
-// lane's six dwords; the converter packs its two 16-value inputs interleaved
-// (element 2i from the first, 2i + 1 from the second). So the block's amax is
-// the lane's own. Per term: e, the smallest exponent with amax <= 7.5 * 2^e
-// (at least -126, so that 2^-e and 2^e are normal floats); the E2M3 codes of
-// v * 2^-e, rounded to nearest-even by the converter (scale 1); the residual
-// v - dec(code) * 2^e for the next term. The lane stores dwords 0-3 of its
-// operand at chunk + t * kFrag6Bytes + 16 l, dwords 4-5 at chunk + t *
-// kFrag6Bytes + 1024 + 8 l (both planes fully coalesced), and its exponents
-// as one dword at scales + 4 l (byte t: term t).
-template <int AS, int NT = kTerms, bool STREAM = false>
-__device__ __forceinline__ void split_terms6(float (&v)[32],
-                                             __attribute__((address_space(AS))) uint8_t* chunk,
-                                             __attribute__((address_space(AS))) uint8_t* scales,
-                                             int lane) {
-  typedef __attribute__((address_space(AS))) i32x4 I4;
-  typedef __attribute__((address_space(AS))) i32x2 I2;
-  typedef __attribute__((address_space(AS))) uint32_t U32;
-  uint32_t sword = 0x7F7F7F7Fu;
-#pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    float am = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 32; ++j) am = fmaxf(am, fabsf(v[j]));
-    int e = e8m0_exponent(am, 7.5f);
-    e = e < -126 ? -126 : e;
-    const float inv = pow2f(-e), sc = pow2f(e);
-    v16f lo, hi;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) lo[i] = v[2 * i] * inv, hi[i] = v[2 * i + 1] * inv;
-    const auto code = __builtin_amdgcn_cvt_scalef32_2xpk16_fp6_f32(lo, hi, 1.0f);
-    if (t + 1 < NT) {
-      const auto d = __builtin_amdgcn_cvt_scalef32_pk32_f32_fp6(code, 1.0f);
-#pragma unroll
-      for (int j = 0; j < 32; ++j) v[j] = fmaf(-d[j], sc, v[j]);
-    }
-    const i32x4 c0 = i32x4{(int)code[0], (int)code[1], (int)code[2], (int)code[3]};
-    const i32x2 c1 = i32x2{(int)code[4], (int)code[5]};
-    I4* d0 = reinterpret_cast<I4*>(chunk + t * kFrag6Bytes + lane * 16);
-    I2* d1 = reinterpret_cast<I2*>(chunk + t * kFrag6Bytes + 1024 + lane * 8);
-    if constexpr (AS == 1 && STREAM) {
-      __builtin_nontemporal_store(c0, d0);
-      __builtin_nontemporal_store(c1, d1);
-    } else {
-      *d0 = c0;
-      *d1 = c1;
-    }
-    sword = (sword & ~(0xFFu << (8 * t))) | ((uint32_t)(e + 127) << (8 * t));
-  }
-  if constexpr (AS == 1 && STREAM)
-    __builtin_nontemporal_store(sword, reinterpret_cast<U32*>(scales + lane * 4));
-  else
-    *reinterpret_cast<U32*>(scales + lane * 4) = sword;
 }
 
 // The activation split, written in operand order. One wave per (16-row block
@@ -1283,8 +1141,8 @@ Status launch_small(const MxgArgs& p, hipStream_t st) {
 
 // Split along K for a large-tile product of one matrix with few tiles (fewer
 // than 128 of 128 columns): whole step pairs per split, about 256 workgroups
-// in all. Used when nothing else is fused into the epilogue (no RoPE, no
-// chained split): the reduce kernel applies the scale and epilogue.
+// in all. Used when no RoPE is fused into the epilogue: the reduce kernel
+// applies the scale and epilogue (and writes a chained split).
 int mxg_ksplit(int M, int kpad, int N, int mats) {
   if (M <= 32 || mats != 1) return 1;
   const int64_t tiles = round_up(M, kBM) / kBM * ((N + 127) / 128);
@@ -1304,7 +1162,16 @@ Status launch_t(const MxgArgs& p, int bm, hipStream_t st) {
         (size_t)round_up(p.N, 256) * p.pitch >= (1ull << 31))
       return Status::err(kUnsupported, "mxg: operands above 2 GiB");
     const int tiles_m = p.mpad / kBM;
-    const int ks = p.rope_tab || p.next ? 1 : mxg_ksplit(p.M, p.kpad, p.N, MATS);
+    // with p.next set, a K split ends in the reduce that also writes the
+    // next layer's split (launch_reduce_split); unsplit, the epilogue does
+    const int ks = p.rope_tab ? 1 : mxg_ksplit(p.M, p.kpad, p.N, MATS);
+    if (p.next && (MATS != 1 || p.N % 256 != 0 || (ks == 1 && p.need_epi)))
+      return Status::err(kInvalid, "mxg: a chained split needs one matrix, N % 256 == 0 and, "
+                                   "unsplit, no epilogue");
+    // the split reduce stores 16-byte vectors of pre and post
+    if (p.next && ks > 1 &&
+        (p.out_stride % 4 != 0 || ((reinterpret_cast<uintptr_t>(p.pre) | reinterpret_cast<uintptr_t>(p.post)) & 15)))
+      return Status::err(kInvalid, "mxg: a chained split reduce needs 16-byte aligned outputs");
     if constexpr (MATS == 1) {
       if (ks > 1) {
         if (!p.part) return Status::err(kInvalid, "mxg: K-split partial buffer missing");
@@ -1320,7 +1187,11 @@ Status launch_t(const MxgArgs& p, int bm, hipStream_t st) {
           k_mxg<DT, BLK, 1, false, kMxgWaves, 128, true><<<grid, 64 * kMxgWaves, 0, st>>>(
               p, nullptr, tiles_m, tiles_n);
         // the kernel boundary makes every split's partial sums visible
-        launch_mxs_reduce(p, ks, 256, 1, st);
+        if (p.next) {
+          launch_reduce_split(p, ks, st);
+        } else {
+          launch_mxs_reduce(p, ks, 256, 1, st);
+        }
         return hip_status(hipGetLastError(), "mxg K-split launch");
       }
     }
