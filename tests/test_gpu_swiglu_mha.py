@@ -122,6 +122,35 @@ def test_mha_matches_oracle(gpu, oracle, B, S, d, H, KVH, msl, mask, pos):
 
 
 @pytest.mark.parametrize("B,S,d,H,KVH,msl,mask", [
+    (2, 64, 256, 4, 4, 64, 1),     # hd 64: two heads per 128-column slice
+    (2, 48, 256, 8, 2, 64, 2),     # hd 32, GQA, 96 tokens (32 padding rows)
+    (1, 96, 256, 2, 2, 96, 1),     # hd 128: one head per slice
+    (4, 512, 1024, 16, 16, 512, 1),  # the benchmark layer at half the batch
+    (3, 70, 128, 2, 2, 80, 1),     # seq % 16 != 0: the O projection splits its input itself
+])
+def test_mha_output_split_matches_o_session(gpu, B, S, d, H, KVH, msl, mask):
+    """When the matrix-core attention also writes the O projection's FP6
+    split of its output (heads * hd % 256 == 0, seq % 16 == 0), the layer's
+    output equals an O-projection session run over the returned attention
+    output, bit for bit: the split is the one k_split makes from it."""
+    dt, scheme = 5, 2
+    hd = d // H
+    rng = np.random.default_rng(B * 7 + S + d + H)
+    Q = (rng.standard_normal((H * hd, d)) / np.sqrt(d)).astype(np.float32)
+    K = (rng.standard_normal((KVH * hd, d)) / np.sqrt(d)).astype(np.float32)
+    V = (rng.standard_normal((KVH * hd, d)) / np.sqrt(d)).astype(np.float32)
+    O = (rng.standard_normal((d, H * hd)) / np.sqrt(H * hd)).astype(np.float32)
+    x = rng.standard_normal((B * S, d)).astype(np.float32)
+    s = gpu.MHASession(B, S, d, H, KVH, 0, msl, mask, 0, dt, scheme, Q, K, V, O)
+    attn, y = s.execute(x)
+    s.close()
+    o = gpu.DenseSession(B * S, H * hd, d, -1, dt, scheme, O)
+    yo, _ = o.execute(attn.reshape(B * S, H * hd))
+    o.close()
+    assert np.array_equal(y.reshape(B * S, d), yo)
+
+
+@pytest.mark.parametrize("B,S,d,H,KVH,msl,mask", [
     (3, 70, 128, 2, 2, 80, 1),     # ring of 80 rows < 210 positions: multiplicities 1..3
     (2, 64, 128, 4, 2, 64, 2),     # bidirectional, GQA, hd 32
     (2, 40, 128, 1, 1, 100, 1),    # hd 128, ragged query block

@@ -16,11 +16,11 @@
 // k_rope before either kernel.
 #include "common.h"
 #include "kernels.h"
+#include "split.h"
 
 namespace wv {
 namespace {
 
-typedef float v4f __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 
@@ -517,10 +517,36 @@ void k_attn_mfma(AttnArgs a, int qblocks) {
   // o[d]: lane holds query c16, head dims d*16 + 4g + i
   const float inv = SIG ? 1.0f : (l > 0.0f ? 1.0f / l : 0.0f);
   float* out = a.out + (size_t)qp * qd + (size_t)h * HD;
+  // with a.split (seq % 16 == 0: the wave's 16 queries are rows 16 rb ..
+  // 16 rb + 15, all valid), the outputs are also staged in LDS, which the
+  // K/V tiles no longer use after the loop's last barrier: 64 HD bytes per
+  // wave, waves 0-7 in ksb and 8-15 in vsb
+  float* stg = reinterpret_cast<float*>(wave < 8 ? &ksb[0][0] + wave * 64 * HD
+                                                 : &vsb[0][0] + (wave - 8) * 64 * HD);
 #pragma unroll
   for (int d = 0; d < DT; ++d) {
     const float4 v = make_float4(o[d][0] * inv, o[d][1] * inv, o[d][2] * inv, o[d][3] * inv);
     *reinterpret_cast<float4*>(out + d * 16 + 4 * g) = v;
+    if (a.split) *reinterpret_cast<float4*>(stg + c16 * HD + d * 16 + 4 * g) = v;
+  }
+  if (a.split && lane < 16 * (HD / 32)) {  // (the LDS operations of a wave run in order)
+    // the head's 32-element blocks of row i16: operand lane i16 + 16 gq of
+    // the O projection's 16 x 128 slice (rb, kc), gq = (h HD % 128) / 32 + gg,
+    // split exactly as k_split splits the stored outputs
+    const int i16 = lane & 15, gg = lane >> 4;
+    float v[32];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const float4 t = *reinterpret_cast<const float4*>(stg + i16 * HD + 32 * gg + 4 * q);
+      v[4 * q] = t.x, v[4 * q + 1] = t.y, v[4 * q + 2] = t.z, v[4 * q + 3] = t.w;
+    }
+    const int col0 = h * HD, kc = col0 / 128, KC = qd / 128;
+    const int rb = (qp - c16) / 16;
+    const int vlane = i16 + 16 * ((col0 % 128) / 32 + gg);
+    const GlobalU8 chunk = (GlobalU8)(a.split + (size_t)(rb * KC + kc) * kTerms * kFrag6Bytes);
+    const GlobalU8 scales = (GlobalU8)(a.split + (size_t)kTerms * a.split_mpad * qd +
+                                       (size_t)(rb * KC + kc) * kChunkScaleBytes);
+    split_terms6<1, kTerms, false>(v, chunk, scales, vlane);
   }
 }
 
@@ -533,14 +559,25 @@ Status build_rope_table(double* tab, int tokens, int hd, double theta, hipStream
   return hip_status(hipGetLastError(), "rope table launch");
 }
 
+// the matrix-core kernel's conditions (launch_attention)
+static bool attention_fast(const AttnArgs& a) {
+  return (a.mask == 1 || a.mask == 2) && !a.alibi && a.msl >= kKT && a.msl >= a.seq &&
+         (a.hd == 32 || a.hd == 64 || a.hd == 128) && a.seq > 0 && a.tokens % a.seq == 0;
+}
+
+bool attention_writes_split(const AttnArgs& a) {
+  return attention_fast(a) && (a.heads * a.hd) % 256 == 0 && a.seq % 16 == 0;
+}
+
 Status launch_attention(const AttnArgs& a, hipStream_t st) {
   if (a.hd > 64 * kMaxHdPerLane || a.hd % 4 != 0)
     return Status::err(kUnsupported, "attention: head_dim must be a multiple of 4 and <= 256");
   // the tile multiplicity update assumes at most one multiple of msl per
   // 64-key tile, hence msl >= 64
-  const bool fast = (a.mask == 1 || a.mask == 2) && !a.alibi && a.msl >= kKT &&
-                    a.msl >= a.seq && (a.hd == 32 || a.hd == 64 || a.hd == 128) &&
-                    a.seq > 0 && a.tokens % a.seq == 0;
+  const bool fast = attention_fast(a);
+  if (a.split && (!attention_writes_split(a) || a.split_mpad < a.tokens || a.split_mpad % 16 != 0))
+    return Status::err(kInvalid, "attention: the output split needs the matrix-core path, "
+                                 "heads * hd % 256 == 0 and seq % 16 == 0");
   if (a.rope) {
     k_rope<<<a.tokens, 256, 0, st>>>(const_cast<float*>(a.q), const_cast<float*>(a.k), a.tokens,
                                      a.heads, a.kv_heads, a.hd, a.rope_theta, a.rope_tab);

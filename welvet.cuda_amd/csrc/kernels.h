@@ -212,8 +212,17 @@ struct AttnArgs {
   // optional (cos, sin) per [token][pair] in f64 (build_rope_table); without
   // it the rotation angles are computed per call
   const double* rope_tab = nullptr;
+  // optional (attention_writes_split): the kernel also writes the
+  // three-term FP6 split of out, laid out as the split buffer of a layer
+  // with split_mpad rows and kpad = heads * hd (the O projection's input)
+  uint8_t* split = nullptr;
+  int split_mpad = 0;
 };
 Status launch_attention(const AttnArgs& a, hipStream_t st);
+// True when the matrix-core attention runs for `a` and can write the split
+// of its output: head_dim 32, 64 or 128, heads * hd a multiple of 256, seq
+// a multiple of 16 (each wave's 16 queries are one aligned row block).
+bool attention_writes_split(const AttnArgs& a);
 // (cos, sin) of t / theta^(2d/hd) for tokens t < tokens and pairs d < hd/2,
 // in f64: tab[2 * (t * (hd/2) + d) + {0, 1}].
 Status build_rope_table(double* tab, int tokens, int hd, double theta, hipStream_t st);

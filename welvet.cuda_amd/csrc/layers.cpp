@@ -858,6 +858,19 @@ Status mha_forward(const MHALayer& L, int batch, int seq, const float* x, float*
   a.sigmoid = c.softmax == 1 ? 1 : 0;
   a.rope_theta = c.rope_theta;
   a.scale = c.scale_override > 0 ? c.scale_override : 1.0 / std::sqrt((double)c.head_dim);
+  // The matrix-core attention can also write the O projection's split of
+  // its output (three FP6 terms; the QKV split is no longer needed): no
+  // split launch between the two.
+  const bool fuse_o = uses_split(T) && mxg_block_m(T) > 16 && !L.o.format &&
+                      L.o.terms == kTerms && L.o.dev.kpad == c.q_dim() &&
+                      attention_writes_split(a);
+  if (fuse_o) {
+    WV_TRY(ensure_split(ws, dense_workspace_bytes(L.o, T)));
+    a.split = split_buf(ws);
+    a.split_mpad = (int)round_up(T, mxg_block_m(T));
+    WV_TRY(launch_attention(a, st));
+    return dense_forward_split(L.o, T, attn, true, ws, y, nullptr, st);
+  }
   WV_TRY(launch_attention(a, st));
   return dense_forward(L.o, T, attn, y, nullptr, ws, st);
 }
