@@ -102,7 +102,7 @@ def oracle_mha(oracle, dt, scheme, Q, K, V, O, x, B, S, H, KVH, hd, msl, mask, p
     (2, 6, 48, 3, 3, 6, 3, 2),     # sliding window (msl), ALiBi
     (1, 9, 64, 4, 1, 9, 4, 3),     # prefix LM (prefix 0), RoPE + ALiBi, MQA
     (4, 12, 64, 4, 4, 12, 1, 0),   # 48 tokens: projections on the large-tile GEMM
-    (2, 40, 64, 2, 2, 40, 2, 1),   # 80 tokens, no positions: Q/K/V as one grouped product
+    (2, 40, 64, 2, 2, 40, 2, 1),   # 80 tokens, no positions, ring below one 64-key tile: VALU attention
 ])
 def test_mha_matches_oracle(gpu, oracle, B, S, d, H, KVH, msl, mask, pos):
     dt, scheme = 5, 2
