@@ -437,10 +437,9 @@ Tensor dense_chain_op(ModelNode& c, const Tensor& in, Arena& ar, Workspace* ws, 
   return out;
 }
 
-Tensor stack_forward(std::vector<ModelNode>& children, const Tensor& in, Arena& ar, Workspace* ws,
-                     hipStream_t st) {
-  std::vector<ModelNode*> ops;
-  for (auto& c : children) flatten(c, &ops);
+// Runs flattened ops in order, each reading the previous one's post.
+Tensor ops_forward(const std::vector<ModelNode*>& ops, const Tensor& in, Arena& ar, Workspace* ws,
+                   hipStream_t st) {
   Tensor cur = in;
   // consecutive Dense ops that dense_fuses_next admits skip the split launch
   // of the second (stack.cpp:470-494 runs them in this order)
@@ -459,6 +458,13 @@ Tensor stack_forward(std::vector<ModelNode>& children, const Tensor& in, Arena& 
     }
   }
   return cur;
+}
+
+Tensor stack_forward(std::vector<ModelNode>& children, const Tensor& in, Arena& ar, Workspace* ws,
+                     hipStream_t st) {
+  std::vector<ModelNode*> ops;
+  for (auto& c : children) flatten(c, &ops);
+  return ops_forward(ops, in, ar, ws, st);
 }
 
 }  // namespace
@@ -546,10 +552,25 @@ Status model_forward_view(Model& m, const std::vector<int>& in_shape, const floa
       // (z, y, x, l), disabled cells skipped, a remote link reads the post of
       // its target cell recorded earlier in this pass.
       const int L = m.dims[3], C = m.dims[2], R = m.dims[1];
+      // per cell when a cell reads a remote link (or holds no op kind,
+      // which op_forward rejects)
+      bool any = false, remote = false;
+      for (size_t i = 0; i < m.children.size(); ++i)
+        if (m.cells[i].enabled)
+          any = true, remote = remote || m.cells[i].remote || m.children[i].kind == 0;
+      require(any, "runtime.forward: grid has no enabled cells with ops");
       std::map<int, Tensor> posts;
       Tensor cur = in;
-      bool any = false;
-      for (size_t i = 0; i < m.children.size(); ++i) {
+      if (!remote) {
+        // no remote links: every enabled cell reads the previous one's post,
+        // so the cells' ops form one chain (fused across cell boundaries
+        // like the ops of one stack)
+        std::vector<ModelNode*> ops;
+        for (size_t i = 0; i < m.children.size(); ++i)
+          if (m.cells[i].enabled) flatten(m.children[i], &ops);
+        cur = ops_forward(ops, in, ar, &ws, st);
+      }
+      for (size_t i = 0; remote && i < m.children.size(); ++i) {
         const GridCell& g = m.cells[i];
         if (!g.enabled) continue;
         Tensor src = cur;
@@ -566,9 +587,7 @@ Status model_forward_view(Model& m, const std::vector<int>& in_shape, const floa
         else post = op_forward(c, src, ar, &ws, st);
         posts[(int)i] = post;
         cur = post;
-        any = true;
       }
-      require(any, "runtime.forward: grid has no enabled cells with ops");
       out = cur;
     }
     *out_shape = out.shape;
