@@ -197,17 +197,15 @@ __global__ __launch_bounds__(64) void k_attention(AttnArgs a) {
 // Scores and sums are the same function of the same values; only the fp32
 // summation order differs from the per-position loop.
 //
-// A workgroup of 8 waves takes 128 queries (16 per wave) of one (batch,
-// head) and walks the distinct rows in tiles of 64 keys staged in LDS in
+// A workgroup of 16 waves (8 at hd 128) takes 16 queries per wave of one
+// (batch, head) and walks the distinct rows in tiles of 64 keys staged in LDS in
 // matrix-core operand order, double-buffered through registers, one barrier
 // per tile. Per 16-key block a wave runs
 //   S^T = K Q^T  on the bf16 matrix cores (v_mfma_f32_16x16x32_bf16, hd/32
-//                steps), Q split into three bf16 terms hi + mid + lo
-//                (x - hi - mid - lo ~ 2^-24 |x|) and K into two, hi + lo
-//                (k - hi - lo ~ 2^-17 |k|), and the five products down to
-//                2^-16 relative kept (hh, hm, lh, hl, lm): the scores carry
-//                ~2^-17 relative accuracy, and K costs two thirds of the
-//                LDS bytes of three terms. Lane l holds the scores of query l%16 for keys
+//                steps), Q and K each split into two bf16 terms hi + lo
+//                (x - hi - lo ~ 2^-17 |x|), and the three products down to
+//                2^-16 relative kept (hh, hl, lh): the scores carry ~2^-16
+//                relative accuracy. Lane l holds the scores of query l%16 for keys
 //                4*(l/16) + i, i = 0..3;
 //   O^T += V^T P^T: the same 4 values per lane are the B operand (MFMA k
 //                index l/16 <-> key 4*(l/16) + j at step j), V^T the A
@@ -258,8 +256,8 @@ void k_attn_mfma(AttnArgs a, int qblocks) {
   const float scale_nat = (float)a.scale;
 
   // Q operand: lane (query c16, group g), head dims 32 ks + 8 g + j, as
-  // three bf16 terms
-  bf16x8 qop[KS][3];
+  // two bf16 terms (hi and the rounded remainder: 16 significand bits, as K)
+  bf16x8 qop[KS][2];
   {
     const float* qrow = a.q + (size_t)qp * qd + (size_t)h * HD;
 #pragma unroll
@@ -270,7 +268,7 @@ void k_attn_mfma(AttnArgs a, int qblocks) {
       for (int j = 0; j < 8; ++j) {
         __bf16 t3[3];
         split3(j < 4 ? q0[j] : q1[j - 4], t3);
-        qop[ks][0][j] = t3[0], qop[ks][1][j] = t3[1], qop[ks][2][j] = t3[2];
+        qop[ks][0][j] = t3[0], qop[ks][1][j] = t3[1];
       }
     }
   }
@@ -372,8 +370,8 @@ void k_attn_mfma(AttnArgs a, int qblocks) {
         }
     }
   };
-  // S^T of a tile: 4 blocks of 16 keys; K (hi, lo) times Q (hi, mid, lo):
-  // the five products down to 2^-16 relative, the small ones first
+  // S^T of a tile: 4 blocks of 16 keys; K (hi, lo) times Q (hi, lo): the
+  // three products down to 2^-16 relative, the small ones first
   auto scores = [&](const uint8_t* kt, v4f (&sc)[4]) {
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
@@ -383,8 +381,6 @@ void k_attn_mfma(AttnArgs a, int qblocks) {
         const uint8_t* kp = kt + (size_t)((kb * KS + ks) * 2) * 1024 + lane * 16;
         const bf16x8 kh = *reinterpret_cast<const bf16x8*>(kp);
         const bf16x8 kl = *reinterpret_cast<const bf16x8*>(kp + 1024);
-        sc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl, qop[ks][1], sc[kb], 0, 0, 0);
-        sc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, qop[ks][2], sc[kb], 0, 0, 0);
         sc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl, qop[ks][0], sc[kb], 0, 0, 0);
         sc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, qop[ks][1], sc[kb], 0, 0, 0);
         sc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, qop[ks][0], sc[kb], 0, 0, 0);
