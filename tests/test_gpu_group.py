@@ -215,3 +215,53 @@ def test_chain_inner_not_kept(gpu, batch, n, widths, layers):
     for sk in sessions:
         for s in sk:
             s.close()
+
+
+def test_chain_inner_not_kept_nonfinite_consumer(gpu):
+    """A consumer whose E5M2 codes hold inf and NaN (scheme 0: weights past
+    the E5M2 range encode to 0x7C / 0xFC, NaN to 0x7E) recomputes those rows
+    from its fp32 input after its product. In a chain that leaves out the
+    inner outputs, the producer feeding such a consumer still writes that
+    input, so the lean chain's last outputs equal the kept chain's bit for
+    bit."""
+    import pywelvet as pw
+    hip = pw.Hip()
+    rng = np.random.default_rng(77)
+    batch, n, d = 64, 3, 256
+    W0 = [(rng.standard_normal((d, d)) / 16).astype(np.float32) for _ in range(n)]
+    W1 = [(rng.standard_normal((d, d)) / 16).astype(np.float32) for _ in range(n)]
+    for i, W in enumerate(W1):
+        W[3 + i, 5] = 7.0e4     # -> 0x7C (+inf)
+        W[40, 7 + i] = -7.0e4   # -> 0xFC (-inf)
+        W[100 + i, 0] = np.nan  # -> 0x7E (NaN)
+    s0 = [pw.DenseSession(batch, d, d, -1, 4, 2, W) for W in W0]
+    s1 = [pw.DenseSession(batch, d, d, -1, 5, 0, W) for W in W1]
+    x0 = [hip.malloc(batch * d * 4) for _ in range(n)]
+    y0 = [hip.malloc(batch * d * 4) for _ in range(n)]
+    y1 = [hip.malloc(batch * d * 4) for _ in range(n)]
+    g0 = pw.DenseGroup(s0, x0, y0, y0)
+    g1 = pw.DenseGroup(s1, y0, y1, y1)
+    full = pw.DenseChain([g0, g1])
+    lean = pw.DenseChain([g0, g1], keep_inner=False)
+    for i in range(n):
+        hip.copy_in(x0[i], rng.standard_normal((batch, d)).astype(np.float32))
+    full.execute()
+    hip.sync()
+    want = [hip.download(y1[i], (batch, d)) for i in range(n)]
+    for i in range(n):
+        assert np.isposinf(want[i][:, 3 + i]).any() or np.isneginf(want[i][:, 3 + i]).any()
+        assert np.isnan(want[i][:, 100 + i]).all()
+        for p in (y0[i], y1[i]):
+            hip.memset(p, 0xFF, batch * d * 4)
+    hip.sync()
+    lean.execute()
+    hip.sync()
+    for i in range(n):
+        got = hip.download(y1[i], (batch, d))
+        assert np.array_equal(got.view(np.uint32), want[i].view(np.uint32)), i
+    for c in (lean, full, g1, g0):
+        c.close()
+    for p in x0 + y0 + y1:
+        hip.free(p)
+    for s in s0 + s1:
+        s.close()

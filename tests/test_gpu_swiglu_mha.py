@@ -216,3 +216,41 @@ def test_runtime_identity_names_the_device(gpu):
     ident = gpu.lib().welvet_runtime_identity().decode()
     parts = ident.split(":")
     assert parts[0] == "hip" and parts[1] != "" and parts[2] == "idx=0", ident
+
+
+@pytest.mark.parametrize("score_std", [10.0, 20.0, 30.0])
+@pytest.mark.parametrize("pos", [0, 1])
+def test_mha_peaked_attention(gpu, oracle, score_std, pos):
+    """Peaked softmax: Q and K scaled so the scores have a standard deviation
+    of 10-30 (the other tests' scores are about N(0, 1)). exp() turns an
+    absolute score error into a relative weight error, so this is where the
+    precision of the matrix-core score products shows. The inputs are small
+    integers, which the FP6 activation split holds exactly, so the GPU's
+    projections differ from the oracle's f64 ones by fp32 summation only and
+    the comparison measures the attention core itself (bound 1e-4)."""
+    B, S, d, H, KVH, msl, mask = 2, 128, 128, 2, 2, 128, 1
+    dt, scheme = 5, 2
+    hd = d // H
+    rng = np.random.default_rng(int(score_std) * 10 + pos)
+    x = rng.integers(-7, 8, size=(B * S, d)).astype(np.float32)
+    Q = (rng.standard_normal((H * hd, d)) / np.sqrt(d)).astype(np.float32)
+    K = (rng.standard_normal((KVH * hd, d)) / np.sqrt(d)).astype(np.float32)
+    V = (rng.standard_normal((KVH * hd, d)) / np.sqrt(d)).astype(np.float32)
+    O = (rng.standard_normal((d, H * hd)) / np.sqrt(H * hd)).astype(np.float32)
+    # unscaled scores: q, k entries have std ~ 4.3 (x std), q.k / sqrt(hd)
+    # std ~ 4.3^2; scale K to reach the target
+    xs = float(np.std(x))
+    K *= np.float32(score_std / (xs * xs))
+    s = gpu.MHASession(B, S, d, H, KVH, 0, msl, mask, pos, dt, scheme, Q, K, V, O)
+    attn, y = s.execute(x)
+    s.close()
+    q, _ = oracle.dense(oracle_dequant(oracle, dt, scheme, Q), x)
+    k, _ = oracle.dense(oracle_dequant(oracle, dt, scheme, K), x)
+    v, _ = oracle.dense(oracle_dequant(oracle, dt, scheme, V), x)
+    scores = np.einsum("thd,thd->th", q.reshape(-1, H, hd)[:S], k.reshape(-1, H, hd)[::-1][:S])
+    got_std = float(np.std(scores / np.sqrt(hd)))
+    assert 0.5 * score_std <= got_std <= 2.0 * score_std, got_std
+    oattn = oracle.mha_attention(q, k, v, B, S, H, KVH, hd, msl, mask, pos)
+    err = rel_l2(attn, oattn)
+    print(f"peaked attention score std {got_std:.1f} pos {pos}: rel-L2 {err:.2e}")
+    assert err <= 1e-4

@@ -357,10 +357,13 @@ __device__ __forceinline__ float dequant_at(const DequantView& d, const uint8_t*
   return v * scale[o];
 }
 
+// G: the gradient's element type (f32 from the backward kernels, f64 from a
+// caller of WeightStore::apply_sgd); either is widened to f64 exactly.
+template <class G>
 __global__ __launch_bounds__(kThreads) void k_sgd(DequantView v, const uint8_t* __restrict__ codes,
                                                   const float* __restrict__ scale,
                                                   const uint8_t* __restrict__ blk,
-                                                  const float* __restrict__ dw, double lr,
+                                                  const G* __restrict__ dw, double lr,
                                                   float* __restrict__ w_next) {
   const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
   if (i >= (int64_t)v.rows * v.cols) return;
@@ -472,12 +475,23 @@ Status launch_add_f64(const float* a, const float* b, float* out, int64_t n, hip
   return hip_status(hipGetLastError(), "add launch");
 }
 
+template <class G>
+static Status sgd_launch(const DeviceWeights& d, const G* dw, double lr, float* w_next,
+                         hipStream_t st) {
+  if (!dw || !w_next) return Status::err(kInvalid, "sgd: bad args");
+  k_sgd<G><<<grid_for((int64_t)d.rows * d.cols), kThreads, 0, st>>>(
+      view_of(d), d.d_codes(), d.d_scale(), d.d_blk(), dw, lr, w_next);
+  return hip_status(hipGetLastError(), "sgd launch");
+}
+
 Status launch_sgd(const DeviceWeights& d, const float* dw, double lr, float* w_next,
                   hipStream_t st) {
-  if (!dw || !w_next) return Status::err(kInvalid, "sgd: bad args");
-  k_sgd<<<grid_for((int64_t)d.rows * d.cols), kThreads, 0, st>>>(view_of(d), d.d_codes(), d.d_scale(),
-                                                                  d.d_blk(), dw, lr, w_next);
-  return hip_status(hipGetLastError(), "sgd launch");
+  return sgd_launch(d, dw, lr, w_next, st);
+}
+
+Status launch_sgd(const DeviceWeights& d, const double* dw, double lr, float* w_next,
+                  hipStream_t st) {
+  return sgd_launch(d, dw, lr, w_next, st);
 }
 
 Status launch_dequant(const DeviceWeights& d, float* w, hipStream_t st) {

@@ -25,6 +25,15 @@ Status codec_sweep(int dtype, uint32_t first_chunk, uint32_t n_chunks, int64_t* 
 // ---- weight rows with non-finite codes (special.hip) ----
 // Fills dw->nf_rows / nf_host with the rows holding E5M2 inf/NaN codes.
 Status find_nonfinite_rows(DeviceWeights* dw, hipStream_t st);
+// Dequantized f32 of elements [e0, e0 + n) of a row-major rows x cols
+// FormatNone payload (FP4: element i in byte i / 2, odd i in the high
+// nibble): decode times the row scale, or times 2^e of the element's
+// 32-column block. `bytes` starts at the byte of element e0 (e0 / 2 for
+// FP4); row_scale (or null: 1) and blk ([row][nb] E8M0 bytes, or null) start
+// at row e0 / cols.
+Status launch_decode_store(const uint8_t* bytes, int dtype, int64_t e0, int64_t n, int cols,
+                           const float* row_scale, const uint8_t* blk, int nb, float* out,
+                           hipStream_t st);
 // Device copy of a row list (out is reset; left empty for an empty list).
 Status upload_rows(const std::vector<int>& rows, DevBuf* out, hipStream_t st);
 // Recomputes the listed output rows of a product (decoded weights, f64 sum)
@@ -54,6 +63,8 @@ Status launch_nf_fix(const NfArgs& a, hipStream_t st);
 // Words of `out` a read of `bytes` writes (one per workgroup).
 size_t read_probe_words(size_t bytes);
 Status launch_read_probe(const uint8_t* buf, size_t bytes, uint32_t* out, hipStream_t st);
+// the device wall clock into *out (one lane of one workgroup)
+Status launch_clock_stamp(uint64_t* out, hipStream_t st);
 
 // ---- small-batch GEMV (gemv.hip) ----
 struct GemvArgs {
@@ -255,6 +266,8 @@ Status launch_swiglu_bwd(const float* gate_pre, const float* up_post, const floa
 Status launch_add_f64(const float* a, const float* b, float* out, int64_t n, hipStream_t st);
 // w_next [rows][cols] = f32(f64(dequant(W)) - lr * f64(dW)).
 Status launch_sgd(const DeviceWeights& d, const float* dw, double lr, float* w_next,
+                  hipStream_t st);
+Status launch_sgd(const DeviceWeights& d, const double* dw, double lr, float* w_next,
                   hipStream_t st);
 // W as f32 [rows][cols]: decode times the scales.
 Status launch_dequant(const DeviceWeights& d, float* w, hipStream_t st);

@@ -322,7 +322,10 @@ static MxgArgs mxg_args(const DenseLayer& L, int batch, const uint8_t* split) {
   p.bias_len = L.bias_len;
   // the partial sums follow the split terms (gemm_ws_bytes)
   p.part = reinterpret_cast<float*>(const_cast<uint8_t*>(split) + split_bytes(batch, L.dev.kpad));
-  p.terms = L.terms;
+  // one activation term is built for the large-tile kernels only (more
+  // than 32 rows); 5..32 rows of such a layer (a model forward, the
+  // allocation-free execute) take the default terms
+  p.terms = (L.terms == 1 && mxg_block_m(batch) == 16) ? kTerms : L.terms;
   return p;
 }
 
@@ -440,7 +443,8 @@ Status dense_backward(const DenseLayer& L, int batch, const float* x, const floa
                                   ws->d.as<double>(), dx, st);
 }
 
-Status dense_apply_sgd(DenseLayer* L, const float* dw, double lr, hipStream_t st) {
+template <class G>
+static Status apply_sgd_impl(DenseLayer* L, const G* dw, double lr, hipStream_t st) {
   if (!L || !dw) return Status::err(kInvalid, "dense sgd: bad args");
   if (L->format) return Status::err(kGap, "gap? SGD on packed block formats");
   const int64_t n = (int64_t)L->in * L->out;
@@ -454,6 +458,83 @@ Status dense_apply_sgd(DenseLayer* L, const float* dw, double lr, hipStream_t st
   if (L->dev.codes_frag.p) WV_TRY(build_codes_frag(&fresh, st));
   L->dev = std::move(fresh);
   return download_store(L, raw.as<uint8_t>(), st);
+}
+
+Status dense_apply_sgd(DenseLayer* L, const float* dw, double lr, hipStream_t st) {
+  return apply_sgd_impl(L, dw, lr, st);
+}
+
+Status dense_apply_sgd(DenseLayer* L, const double* dw, double lr, hipStream_t st) {
+  return apply_sgd_impl(L, dw, lr, st);
+}
+
+std::vector<float> remap_len(const float* src, size_t sn, size_t need) {
+  std::vector<float> out(need, 0.0f);
+  if (sn == 0 || need == 0) return out;
+  if (sn == need) {
+    std::memcpy(out.data(), src, need * sizeof(float));
+    return out;
+  }
+  for (size_t i = 0; i < need; ++i) {
+    size_t lo = i * sn / need, hi = (i + 1) * sn / need;
+    if (hi <= lo) hi = lo + 1;
+    if (hi > sn) hi = sn;
+    double sum = 0.0;
+    for (size_t j = lo; j < hi; ++j) sum += (double)src[j];
+    out[i] = (float)(sum / (double)(hi - lo));
+  }
+  return out;
+}
+
+Status store_quantize(int rows, int cols, int dtype, int scheme, const float* W_host,
+                      WeightStore* out, hipStream_t st) {
+  if (!out) return Status::err(kInvalid, "weights: null store");
+  DenseLayer L;
+  WV_TRY(dense_build(cols, rows, kLinear, dtype, scheme, W_host, nullptr, 0, &L, st));
+  *out = std::move(L.store);
+  out->bias.clear();
+  return Status::ok();
+}
+
+Status store_decode_rows(const StoreView& s, int row0, int nrows, float* host_out,
+                         hipStream_t st) {
+  if (!host_out || row0 < 0 || nrows < 0 || row0 + nrows > s.rows || s.cols <= 0)
+    return Status::err(kInvalid, "weights: decode rows out of range");
+  WV_TRY(check_dtype_scheme(s.dtype, s.scheme));
+  if (nrows == 0) return Status::ok();
+  const int64_t e0 = (int64_t)row0 * s.cols, n = (int64_t)nrows * s.cols;
+  const int64_t total = (int64_t)s.rows * s.cols;
+  const bool fp4 = s.dtype == kFP4;
+  const size_t need = fp4 ? (size_t)((total + 1) / 2) : (size_t)total;
+  if (!s.native || s.native_len != need)
+    return Status::err(kInvalid, "weights: native payload length");
+  const size_t b0 = fp4 ? (size_t)(e0 / 2) : (size_t)e0;
+  const size_t b1 = fp4 ? (size_t)((e0 + n + 1) / 2) : (size_t)(e0 + n);
+  const int nb = (s.cols + 31) / 32;
+  const bool blk = s.scheme == kSchemeBlock32;
+  const bool scaled = s.scheme == kSchemeTensor || s.scheme == kSchemeRow;
+  if (blk && (!s.blk_exp || s.blk_exp_len != (size_t)s.rows * nb))
+    return Status::err(kInvalid, "weights: block scale length");
+  if (scaled && (!s.row_scale || s.row_scale_len != (size_t)s.rows))
+    return Status::err(kInvalid, "weights: row scale length");
+  DevBuf bytes, sc, ex, out;
+  WV_TRY(bytes.alloc(b1 - b0));
+  WV_TRY(copy_h2d(bytes.p, s.native + b0, b1 - b0, st));
+  if (scaled) {
+    WV_TRY(sc.alloc((size_t)nrows * sizeof(float)));
+    WV_TRY(copy_h2d(sc.p, s.row_scale + row0, (size_t)nrows * sizeof(float), st));
+  }
+  if (blk) {
+    WV_TRY(ex.alloc((size_t)nrows * nb));
+    WV_TRY(copy_h2d(ex.p, s.blk_exp + (size_t)row0 * nb, (size_t)nrows * nb, st));
+  }
+  WV_TRY(out.alloc((size_t)n * sizeof(float)));
+  WV_TRY(launch_decode_store(bytes.as<uint8_t>(), s.dtype, e0, n, s.cols,
+                             scaled ? sc.as<float>() : nullptr, blk ? ex.as<uint8_t>() : nullptr,
+                             nb, out.as<float>(), st));
+  WV_TRY(copy_d2h(host_out, out.p, (size_t)n * sizeof(float), st));
+  WV_HIP(hipStreamSynchronize(st));
+  return Status::ok();
 }
 
 bool dense_group_fused(int batch) { return uses_split(batch) && mxg_block_m(batch) > 16; }
@@ -559,11 +640,15 @@ Status dense_chain_build(const DenseGroup* const* groups, int count, DenseChain*
     if (P.shape.N % 256 != 0 || C.kpad != P.shape.N || P.shape.mats != 1 ||
         group_has_nonfinite(P) || P.terms != C.terms)
       continue;
+    // The consumer's GEMM reads the split only, so the producer's fp32 output
+    // may be left out, unless the consumer has rows with non-finite codes:
+    // their recomputation after the consumer's product (group_fix) reads the
+    // consumer's fp32 input, which is this output.
+    const bool drop_out = !keep_inner && !group_has_nonfinite(C);
     std::vector<MxgArgs> tab = P.htab;
     for (int i = 0; i < P.n; ++i) {
       tab[i].next = C.hjobs[i].buf;
-      // the consumer reads the split only: the output need not be written
-      if (!keep_inner) tab[i].pre = tab[i].post = nullptr;
+      if (drop_out) tab[i].pre = tab[i].post = nullptr;
     }
     WV_TRY(c->tabs[k].alloc(sizeof(MxgArgs) * P.n));
     WV_TRY(copy_h2d(c->tabs[k].p, tab.data(), sizeof(MxgArgs) * P.n, nullptr));

@@ -115,6 +115,33 @@ Status dense_backward(const DenseLayer& L, int batch, const float* x, const floa
 // f32(f64(dequant(W)) - lr * f64(dW))) with the layer's scheme; the device
 // copy and the host store are replaced.
 Status dense_apply_sgd(DenseLayer* L, const float* dw, double lr, hipStream_t st);
+// The same with an f64 gradient (WeightStore::apply_sgd takes f64 dW).
+Status dense_apply_sgd(DenseLayer* L, const double* dw, double lr, hipStream_t st);
+
+// A weight store quantized on the device from host fp32 W [rows][cols] (null:
+// zeros) with `scheme` (WeightStore::make: native codes, scales; no bias).
+Status store_quantize(int rows, int cols, int dtype, int scheme, const float* W_host,
+                      WeightStore* out, hipStream_t st);
+// A store's payload in host memory, not owned (the C++ API's WeightStore
+// and this library's share the layout).
+struct StoreView {
+  int dtype = 0, scheme = 0, rows = 0, cols = 0;
+  const uint8_t* native = nullptr;
+  size_t native_len = 0;
+  const float* row_scale = nullptr;  // [rows], schemes 1 and 2
+  size_t row_scale_len = 0;
+  const uint8_t* blk_exp = nullptr;  // [rows][ceil(cols / 32)], scheme 3
+  size_t blk_exp_len = 0;
+};
+// Rows [row0, row0 + nrows) of a store, dequantized on the device (decode
+// times the row scale or block scale) into host_out [nrows][cols]. Only
+// those rows' bytes are uploaded.
+Status store_decode_rows(const StoreView& s, int row0, int nrows, float* host_out,
+                         hipStream_t st);
+// ABI remap_gap_len (reference src/layers/dense/dense.cpp:121-139): src
+// resized to `need` values, a different length averaging ranges of src in
+// f64.
+std::vector<float> remap_len(const float* src, size_t sn, size_t need);
 // True when `batch` rows take the split + batched-MFMA path.
 bool uses_split(int batch);
 // Builds the operand-order code copy when `batch` rows run the 5..32-row

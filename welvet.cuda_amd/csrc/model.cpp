@@ -25,33 +25,57 @@
 namespace wv {
 namespace {
 
-struct Reader {
-  const uint8_t* p;
-  size_t left;
-  int depth = 0;
+// Little-endian cursor over the descriptor bytes. Callers name the part of
+// the descriptor they are in (`part`), so a descriptor that ends early or
+// carries an impossible element count is reported with where it happened.
+// Every failure is std::invalid_argument (status code 1).
+class WireIn {
+ public:
+  WireIn(const uint8_t* data, size_t size) : at_(data), end_(data + size) {}
+
+  size_t remaining() const { return static_cast<size_t>(end_ - at_); }
+  const char* part = "header";
+  int nesting = 0;
+
+  int32_t i32() { return scalar<int32_t>(); }
+  uint32_t u32() { return scalar<uint32_t>(); }
+  float f32() { return scalar<float>(); }
+  double f64() { return scalar<double>(); }
+
+  // n values of T into dst
   template <class T>
-  bool read(T* out, size_t n) {
-    if (n > left / sizeof(T)) return false;
-    const size_t bytes = n * sizeof(T);
-    if (bytes) std::memcpy(out, p, bytes);
-    p += bytes;
-    left -= bytes;
-    return true;
+  void fill(T* dst, size_t n) {
+    if (n > remaining() / sizeof(T)) ended();
+    take(dst, n * sizeof(T));
   }
+  // an i32 element count, then that many values of T
   template <class T>
-  T one() {
-    T v{};
-    if (!read(&v, 1)) throw std::invalid_argument("truncated descriptor");
+  std::vector<T> counted() {
+    const int32_t n = i32();
+    if (n < 0 || static_cast<size_t>(n) > remaining() / sizeof(T))
+      throw std::invalid_argument(std::string("model descriptor: bad element count in ") + part);
+    std::vector<T> out(static_cast<size_t>(n));
+    take(out.data(), out.size() * sizeof(T));
+    return out;
+  }
+
+ private:
+  template <class T>
+  T scalar() {
+    T v;
+    take(&v, sizeof(T));
     return v;
   }
-  template <class T>
-  std::vector<T> vec() {
-    const int32_t n = one<int32_t>();
-    if (n < 0 || (size_t)n > left / sizeof(T)) throw std::invalid_argument("invalid vector length");
-    std::vector<T> v((size_t)n);
-    if (!read(v.data(), v.size())) throw std::invalid_argument("short vector");
-    return v;
+  void take(void* dst, size_t bytes) {
+    if (bytes > remaining()) ended();
+    if (bytes) std::memcpy(dst, at_, bytes);
+    at_ += bytes;
   }
+  [[noreturn]] void ended() const {
+    throw std::invalid_argument(std::string("model descriptor ends inside ") + part);
+  }
+  const uint8_t* at_;
+  const uint8_t* end_;
 };
 
 void require(bool ok, const char* why) {
@@ -66,46 +90,49 @@ void good(const Status& s) {
   if (!s) throw StatusError(s);
 }
 
-size_t count_of(Reader& r, int64_t n, bool allow_empty) {
+// Element counts implied by a child's dimensions: at most 2^26, and no more
+// 4-byte values than the bytes left could hold.
+size_t payload_count(const WireIn& r, int64_t n, bool allow_empty) {
   require(n >= 0 && (allow_empty || n > 0) && n <= (int64_t(1) << 26) &&
-              (size_t)n <= r.left / 4,
+              static_cast<size_t>(n) <= r.remaining() / 4,
           "invalid model payload size");
-  return (size_t)n;
+  return static_cast<size_t>(n);
 }
 
-std::vector<float> floats(Reader& r, int64_t n) {
-  std::vector<float> v(count_of(r, n, false));
-  require(r.read(v.data(), v.size()), "short weights");
+std::vector<float> weights_f32(WireIn& r, int64_t n) {
+  std::vector<float> v(payload_count(r, n, false));
+  r.fill(v.data(), v.size());
   return v;
 }
 
-void read_child(Reader& r, ModelNode* c) {
-  require(++r.depth <= 64, "model nesting exceeds 64");
-  c->kind = r.one<int32_t>();
+void read_child(WireIn& r, ModelNode* c) {
+  require(++r.nesting <= 64, "model nesting exceeds 64");
+  r.part = "a child operation";
+  c->kind = r.i32();
   switch (c->kind) {
   case 0: break;
   case 1: {  // Dense: child_wire.hpp:29-55
-    c->in = r.one<int32_t>();
-    c->out = r.one<int32_t>();
-    c->act = r.one<int32_t>();
-    c->dtype = r.one<int32_t>();
+    c->in = r.i32();
+    c->out = r.i32();
+    c->act = r.i32();
+    c->dtype = r.i32();
     require(c->in > 0 && c->out > 0, "invalid Dense dims");
-    c->W = floats(r, (int64_t)c->out * c->in);
-    const uint32_t bl = r.one<uint32_t>();
-    std::vector<double> bias(count_of(r, bl, true));
-    require(r.read(bias.data(), bias.size()), "short bias");
+    c->W = weights_f32(r, (int64_t)c->out * c->in);
+    const uint32_t bl = r.u32();
+    std::vector<double> bias(payload_count(r, bl, true));
+    r.fill(bias.data(), bias.size());
     WeightStore s;
     s.rows = c->out, s.cols = c->in, s.bias = std::move(bias);
     c->stores.push_back(std::move(s));
     break;
   }
   case 4: {  // SwiGLU: child_wire.hpp:95-118
-    c->in = r.one<int32_t>();
-    c->inter = r.one<int32_t>();
-    c->dtype = r.one<int32_t>();
+    c->in = r.i32();
+    c->inter = r.i32();
+    c->dtype = r.i32();
     require(c->in > 0 && c->inter > 0, "invalid SwiGLU dims");
     const int64_t n = (int64_t)c->in * c->inter;
-    std::vector<float> packed = floats(r, 3 * n);
+    std::vector<float> packed = weights_f32(r, 3 * n);
     c->W.assign(packed.begin(), packed.begin() + n);
     c->W2.assign(packed.begin() + n, packed.begin() + 2 * n);
     c->W3.assign(packed.begin() + 2 * n, packed.end());
@@ -118,26 +145,26 @@ void read_child(Reader& r, ModelNode* c) {
     break;
   }
   case 7: {  // MHA: child_wire.hpp:153-192
-    const int seq = r.one<int32_t>();
+    const int seq = r.i32();
     MHAConfig& g = c->mha_cfg;
-    g.d_model = r.one<int32_t>();
-    g.num_heads = r.one<int32_t>();
-    g.num_kv_heads = r.one<int32_t>();
-    g.head_dim = r.one<int32_t>();
-    const int msl = r.one<int32_t>();
-    g.mask = r.one<int32_t>();
-    g.pos = r.one<int32_t>();
-    c->dtype = r.one<int32_t>();
+    g.d_model = r.i32();
+    g.num_heads = r.i32();
+    g.num_kv_heads = r.i32();
+    g.head_dim = r.i32();
+    const int msl = r.i32();
+    g.mask = r.i32();
+    g.pos = r.i32();
+    c->dtype = r.i32();
     require(g.num_heads > 0 && g.d_model > 0 && g.num_kv_heads >= 0 && g.head_dim >= 0,
             "invalid MHA dims");
     const int hd = g.head_dim > 0 ? g.head_dim : g.d_model / g.num_heads;
     const int kvh = g.num_kv_heads > 0 ? g.num_kv_heads : g.num_heads;
     g.max_seq_len = msl > 0 ? msl : seq;
     const int qd = g.num_heads * hd, kvd = kvh * hd;
-    c->W = floats(r, (int64_t)qd * g.d_model);
-    c->W2 = floats(r, (int64_t)kvd * g.d_model);
-    c->W3 = floats(r, (int64_t)kvd * g.d_model);
-    c->W4 = floats(r, (int64_t)g.d_model * qd);
+    c->W = weights_f32(r, (int64_t)qd * g.d_model);
+    c->W2 = weights_f32(r, (int64_t)kvd * g.d_model);
+    c->W3 = weights_f32(r, (int64_t)kvd * g.d_model);
+    c->W4 = weights_f32(r, (int64_t)g.d_model * qd);
     good(mha_validate(&g));
     const int rows[4] = {qd, kvd, kvd, g.d_model}, cols[4] = {g.d_model, g.d_model, g.d_model, qd};
     for (int i = 0; i < 4; ++i) {
@@ -148,55 +175,56 @@ void read_child(Reader& r, ModelNode* c) {
     break;
   }
   case 19: {  // NestedStack: child_wire.hpp:409-421
-    const int32_t n = r.one<int32_t>();
+    const int32_t n = r.i32();
     require(n > 0 && n <= 4096, "invalid nested count");
     c->nested.resize((size_t)n);
     for (auto& ch : c->nested) read_child(r, &ch);
     break;
   }
   default:
-    --r.depth;
+    --r.nesting;
     throw StatusError(Status::err(kGap, "gap? model child kind " + std::to_string(c->kind) +
                                             " is outside the quantized Dense path"));
   }
-  --r.depth;
+  --r.nesting;
 }
 
 // Cameral training controls (model_wire.hpp:195-253): parsed for framing and
 // validation; they carry no forward semantics.
-void skip_controls(Reader& r) {
-  int32_t n = r.one<int32_t>();
+void skip_controls(WireIn& r) {
+  r.part = "the training controls";
+  int32_t n = r.i32();
   require(n >= 0 && n <= 4096, "invalid controls");
   for (int i = 0; i < n; ++i) {
-    const int32_t m = r.one<int32_t>();
+    const int32_t m = r.i32();
     require(m >= 0 && m <= 33, "invalid train mode");
   }
-  n = r.one<int32_t>();
+  n = r.i32();
   require(n >= 0 && n <= 4096, "invalid controls");
-  for (int i = 0; i < n; ++i) (void)r.one<double>();
-  (void)r.one<double>(), (void)r.one<double>(), (void)r.one<double>();
-  const int32_t present = r.one<int32_t>();
+  for (int i = 0; i < n; ++i) (void)r.f64();
+  (void)r.f64(), (void)r.f64(), (void)r.f64();
+  const int32_t present = r.i32();
   if (!present) return;
-  (void)r.one<int32_t>();
-  (void)r.one<double>();
-  const int32_t when = r.one<int32_t>();
+  (void)r.i32();
+  (void)r.f64();
+  const int32_t when = r.i32();
   require(when >= 0 && when <= 3, "invalid sync timing");
-  n = r.one<int32_t>();
+  n = r.i32();
   require(n >= 0 && n <= 4096, "invalid controls");
-  for (int i = 0; i < n; ++i) (void)r.one<double>();
-  n = r.one<int32_t>();
+  for (int i = 0; i < n; ++i) (void)r.f64();
+  n = r.i32();
   require(n >= 0 && n <= 4096, "invalid controls");
   for (int g = 0; g < n; ++g) {
-    const int32_t cnt = r.one<int32_t>();
+    const int32_t cnt = r.i32();
     require(cnt >= 0 && cnt <= 4096, "invalid controls");
-    for (int i = 0; i < cnt; ++i) (void)r.one<int32_t>();
+    for (int i = 0; i < cnt; ++i) (void)r.i32();
   }
-  n = r.one<int32_t>();
+  n = r.i32();
   require(n >= 0 && n <= 4096, "invalid controls");
-  for (int i = 0; i < 6 * n; ++i) (void)r.one<int32_t>();
+  for (int i = 0; i < 6 * n; ++i) (void)r.i32();
 }
 
-void skip_control_tree(Reader& r, const ModelNode& c) {
+void skip_control_tree(WireIn& r, const ModelNode& c) {
   skip_controls(r);
   for (const auto& ch : c.nested) skip_control_tree(r, ch);
 }
@@ -229,45 +257,76 @@ int e8m0_of_pow2(float v) {
   return (int)ex - 127;
 }
 
-void read_store(Reader& r, WeightStore* s) {
-  const int32_t tag = r.one<int32_t>(), rows = r.one<int32_t>(), cols = r.one<int32_t>();
-  const float scale = r.one<float>();
-  const int32_t dt = tag & 0xFF, scheme = (tag >> kSchemeShift) & 0xFF;
-  require(tag >= 0 && (tag >> 16) == 0 && dt <= 33 && scheme <= 3 && rows == s->rows &&
-              cols == s->cols && std::isfinite(scale),
-          "native store metadata mismatch");
-  auto f = r.vec<float>();
-  auto raw = r.vec<uint8_t>();
-  auto bias = r.vec<double>();
+// One store payload as it sits on the wire, before it is checked against
+// the child that owns it.
+struct StoreWire {
+  int32_t tag = 0, rows = 0, cols = 0;
+  float scale = 0.0f;
+  std::vector<float> f32;
+  std::vector<uint8_t> native;
+  std::vector<double> bias;
+  int dtype() const { return tag & 0xFF; }
+  int scheme() const { return (tag >> kSchemeShift) & 0xFF; }
+};
+
+StoreWire take_store(WireIn& r) {
+  r.part = "a weight store";
+  StoreWire w;
+  w.tag = r.i32();
+  w.rows = r.i32();
+  w.cols = r.i32();
+  w.scale = r.f32();
+  w.f32 = r.counted<float>();
+  w.native = r.counted<uint8_t>();
+  w.bias = r.counted<double>();
+  return w;
+}
+
+// Number of f32 scale values each scheme carries in the store's f32 field.
+size_t scales_carried(int scheme, int rows, int cols) {
+  if (scheme == kSchemeRow) return static_cast<size_t>(rows);
+  if (scheme == kSchemeBlock32) return static_cast<size_t>(rows) * ((cols + 31) / 32);
+  return 0;
+}
+
+void install_store(StoreWire&& w, WeightStore* s) {
+  const int dt = w.dtype(), scheme = w.scheme();
+  require(w.tag >= 0 && (w.tag >> 16) == 0 && dt <= 33 && scheme <= kSchemeBlock32,
+          "store header: unknown dtype or scale scheme");
+  require(w.rows == s->rows && w.cols == s->cols, "store shape differs from its operation");
+  require(std::isfinite(w.scale), "store scale is not finite");
   if (dt != kE4M3 && dt != kE5M2 && dt != kFP4)
     throw StatusError(Status::err(kUnsupported, "model store dtype " + std::to_string(dt) +
                                                     " is outside the FP8/FP4 path"));
-  const int64_t n = (int64_t)rows * cols;
-  const size_t nb = (size_t)(cols + 31) / 32;
-  require(raw.size() == (dt == kFP4 ? (size_t)((n + 1) / 2) : (size_t)n),
-          "native store payload length mismatch");
-  const size_t want_f = scheme == kSchemeRow ? (size_t)rows
-                        : scheme == kSchemeBlock32 ? (size_t)rows * nb : 0;
-  require(f.size() == want_f, "store scale payload length mismatch");
+  const int64_t elems = static_cast<int64_t>(w.rows) * w.cols;
+  const size_t code_bytes = dt == kFP4 ? static_cast<size_t>((elems + 1) / 2)
+                                       : static_cast<size_t>(elems);
+  require(w.native.size() == code_bytes, "store code bytes do not match its shape");
+  require(w.f32.size() == scales_carried(scheme, w.rows, w.cols),
+          "store scale count does not match its scheme");
   s->dtype = dt;
   s->scheme = scheme;
-  s->scale = scale;
-  s->native = std::move(raw);
+  s->scale = w.scale;
+  s->native = std::move(w.native);
+  s->bias = std::move(w.bias);
   s->blk_exp.clear();
-  if (scheme == kSchemeTensor) {
-    require(scale > 0.0f, "tensor scale must be positive");
-    s->row_scale.assign((size_t)rows, scale);
-  } else if (scheme == kSchemeRow) {
-    for (float v : f) require(std::isfinite(v), "row scale is not finite");
-    s->row_scale = std::move(f);
-  } else {
-    s->row_scale.assign((size_t)rows, 1.0f);
+  switch (scheme) {
+  case kSchemeTensor:
+    require(w.scale > 0.0f, "tensor scale must be positive");
+    s->row_scale.assign(static_cast<size_t>(w.rows), w.scale);
+    break;
+  case kSchemeRow:
+    for (float v : w.f32) require(std::isfinite(v), "row scale is not finite");
+    s->row_scale = std::move(w.f32);
+    break;
+  default:  // reference stores (scale unused) and E8M0 blocks: unit row scales
+    s->row_scale.assign(static_cast<size_t>(w.rows), 1.0f);
     if (scheme == kSchemeBlock32) {
-      s->blk_exp.resize(f.size());
-      for (size_t i = 0; i < f.size(); ++i) s->blk_exp[i] = (uint8_t)(e8m0_of_pow2(f[i]) + 127);
+      s->blk_exp.reserve(w.f32.size());
+      for (float v : w.f32) s->blk_exp.push_back(static_cast<uint8_t>(e8m0_of_pow2(v) + 127));
     }
+    break;
   }
-  s->bias = std::move(bias);
 }
 
 void build(ModelNode& c, int scheme, int terms, hipStream_t st) {
@@ -474,21 +533,22 @@ Status model_parse(const uint8_t* data, size_t size, int backend, Model* m) {
     require(data && size >= 28 && size <= (1ull << 32), "invalid mount arguments");
     int scheme = 0, terms = kTerms;
     WV_TRY(decode_backend(backend, &scheme, &terms));
-    Reader r{data, size};
-    require(r.one<uint32_t>() == 0x314e4d57u, "unsupported model descriptor version");
-    m->root = r.one<int32_t>();
-    const int count = r.one<int32_t>();
+    WireIn r(data, size);
+    require(r.u32() == 0x314e4d57u, "unsupported model descriptor version");
+    m->root = r.i32();
+    const int count = r.i32();
     require(m->root >= 0 && m->root <= 2 && count > 0 && count <= 4096, "invalid model root/count");
     if (m->root == 1) return Status::err(kGap, "gap? Parallel model root is outside the quantized Dense path");
-    for (int& d : m->dims) d = r.one<int32_t>();
+    for (int& d : m->dims) d = r.i32();
     m->children.resize((size_t)count);
     for (auto& c : m->children) read_child(r, &c);
     skip_controls(r);
     for (auto& c : m->children) skip_control_tree(r, c);
     std::vector<WeightStore*> stores;
     for (auto& c : m->children) collect(c, &stores);
-    require(r.one<int32_t>() == (int)stores.size(), "store count mismatch");
-    for (WeightStore* s : stores) read_store(r, s);
+    r.part = "the store list";
+    require(r.i32() == (int)stores.size(), "store count mismatch");
+    for (WeightStore* s : stores) install_store(take_store(r), s);
     if (m->root == 2) {
       int64_t n = 1;
       for (int d : m->dims) {
@@ -497,19 +557,20 @@ Status model_parse(const uint8_t* data, size_t size, int backend, Model* m) {
       }
       require(n == count, "grid cell count mismatch");
       m->cells.resize((size_t)count);
+      r.part = "the grid cells";
       for (int i = 0; i < count; ++i) {
         GridCell& g = m->cells[(size_t)i];
-        g.enabled = r.one<int32_t>();
+        g.enabled = r.i32();
         require(!g.enabled || m->children[(size_t)i].kind != 0, "enabled grid cell has no operation");
-        g.remote = r.one<int32_t>() != 0;
-        g.tz = r.one<int32_t>(), g.ty = r.one<int32_t>(), g.tx = r.one<int32_t>(), g.tl = r.one<int32_t>();
+        g.remote = r.i32() != 0;
+        g.tz = r.i32(), g.ty = r.i32(), g.tx = r.i32(), g.tl = r.i32();
         if (g.remote)
           require(g.tz >= 0 && g.tz < m->dims[0] && g.ty >= 0 && g.ty < m->dims[1] && g.tx >= 0 &&
                       g.tx < m->dims[2] && g.tl >= 0 && g.tl < m->dims[3],
                   "invalid remote link");
       }
     }
-    require(r.left == 0, "trailing descriptor bytes");
+    require(r.remaining() == 0, "trailing descriptor bytes");
     m->scheme = scheme;
     m->terms = terms;
     return Status::ok();

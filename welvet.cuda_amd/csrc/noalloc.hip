@@ -56,6 +56,23 @@ wv::Status scratch_on_current_device(void** out) {
   return wv::Status::ok();
 }
 
+// Lends the scratch array to a Workspace's split buffer for one call. The
+// buffer is handed back (pointer cleared) when the guard leaves scope, on
+// every path including unwinding, so ~DevBuf never frees the array.
+struct ScratchLoan {
+  wv::DevBuf* buf;
+  ScratchLoan(wv::DevBuf* b, void* p, size_t bytes) : buf(b) {
+    buf->p = p;
+    buf->bytes = bytes;
+  }
+  ~ScratchLoan() {
+    buf->p = nullptr;
+    buf->bytes = 0;
+  }
+  ScratchLoan(const ScratchLoan&) = delete;
+  ScratchLoan& operator=(const ScratchLoan&) = delete;
+};
+
 welvet_status status_out(const wv::Status& st) {
   welvet_status out{};
   out.code = st.code;
@@ -84,19 +101,15 @@ extern "C" welvet_status welvet_dense_execute_noalloc(welvet_dense_session* s, i
                             std::to_string(s->layer.in) + " inputs need " + std::to_string(need) +
                             " bytes of scratch; the fixed scratch holds " +
                             std::to_string(kScratchBytes)));
-    wv::Workspace ws;  // borrows the scratch array for its split buffer
+    void* p = nullptr;
     if (need > 0) {
-      void* p = nullptr;
       wv::Status st = scratch_on_current_device(&p);
       if (!st) return status_out(st);
-      ws.b.p = p;
-      ws.b.bytes = kScratchBytes;
     }
+    wv::Workspace ws;  // its split buffer is the scratch array, on loan
+    ScratchLoan loan(&ws.b, p, p ? kScratchBytes : 0);
     hipStream_t st = stream ? static_cast<hipStream_t>(stream) : s->stream.s;
-    const wv::Status r = wv::dense_forward(s->layer, rows, x, pre, post, &ws, st);
-    ws.b.p = nullptr;  // not owned: never freed
-    ws.b.bytes = 0;
-    return status_out(r);
+    return status_out(wv::dense_forward(s->layer, rows, x, pre, post, &ws, st));
   } catch (const std::bad_alloc&) {
     return status_out(wv::Status::err(wv::kInternal, "out of host memory"));
   } catch (...) {

@@ -408,6 +408,42 @@ Status relayout_to_device(const uint8_t* d_raw, int dtype, int scheme, int rows,
   return Status::ok();
 }
 
+namespace {
+__global__ __launch_bounds__(kThreads) void k_decode_store(const uint8_t* __restrict__ bytes,
+                                                           int dtype, int64_t e0, int64_t n,
+                                                           int cols,
+                                                           const float* __restrict__ row_scale,
+                                                           const uint8_t* __restrict__ blk, int nb,
+                                                           float* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= n) return;
+  const int64_t e = e0 + i;
+  uint8_t q;
+  if (dtype == kFP4) {
+    const uint8_t b = bytes[e / 2 - e0 / 2];
+    q = (e & 1) ? (uint8_t)(b >> 4) : (uint8_t)(b & 15u);
+  } else {
+    q = bytes[i];
+  }
+  const int64_t r = e / cols - e0 / cols;
+  const int c = (int)(e % cols);
+  const float v = decode(dtype, q);
+  if (blk) out[i] = v * pow2f((int)blk[r * nb + c / 32] - 127);
+  else out[i] = row_scale ? v * row_scale[r] : v;
+}
+}  // namespace
+
+Status launch_decode_store(const uint8_t* bytes, int dtype, int64_t e0, int64_t n, int cols,
+                           const float* row_scale, const uint8_t* blk, int nb, float* out,
+                           hipStream_t st) {
+  if (n <= 0) return Status::ok();
+  if (!bytes || !out || cols <= 0 || e0 < 0 || (blk && nb != (cols + 31) / 32))
+    return Status::err(kInvalid, "decode store: bad args");
+  k_decode_store<<<grid_for(n), kThreads, 0, st>>>(bytes, dtype, e0, n, cols, row_scale, blk, nb,
+                                                   out);
+  return hip_status(hipGetLastError(), "decode store launch");
+}
+
 Status codec_sweep(int dtype, uint32_t first_chunk, uint32_t n_chunks, int64_t* host_out,
                    hipStream_t st) {
   DevBuf out;

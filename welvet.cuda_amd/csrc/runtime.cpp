@@ -93,20 +93,36 @@ Status copy_h2d(void* dst, const void* src, size_t n, hipStream_t st) {
   std::lock_guard<std::mutex> lock(g_stage_mu);
   WV_TRY(stage_ready());
   bool used[2] = {false, false};
+  // The next caller refills the buffers, so every DMA queued here must have
+  // read its buffer before this returns, on the error paths too. A failed
+  // copy or record leaves an earlier event that may still be pending; the
+  // whole stream is drained then, since that event no longer marks the last
+  // use of its buffer.
+  auto fail = [&](Status s) {
+    if (hipStreamSynchronize(st) != hipSuccess) (void)hipGetLastError();
+    return s;
+  };
   int i = 0;
   for (size_t off = 0; off < n; off += kStageBytes, i ^= 1) {
     const size_t len = n - off < kStageBytes ? n - off : kStageBytes;
     // the DMA that last read this buffer must be done before it is refilled
-    if (used[i]) WV_HIP(hipEventSynchronize(g_stage_ev[i]));
+    if (used[i]) {
+      Status s = hip_status(hipEventSynchronize(g_stage_ev[i]), "copy_h2d: stage wait");
+      if (!s) return fail(s);
+    }
     std::memcpy(g_stage[i], static_cast<const char*>(src) + off, len);
-    WV_HIP(hipMemcpyAsync(static_cast<char*>(dst) + off, g_stage[i], len, hipMemcpyHostToDevice,
-                          st));
-    WV_HIP(hipEventRecord(g_stage_ev[i], st));
     used[i] = true;
+    Status s = hip_status(hipMemcpyAsync(static_cast<char*>(dst) + off, g_stage[i], len,
+                                         hipMemcpyHostToDevice, st),
+                          "copy_h2d: hipMemcpyAsync");
+    if (s) s = hip_status(hipEventRecord(g_stage_ev[i], st), "copy_h2d: hipEventRecord");
+    if (!s) return fail(s);
   }
-  // the next caller refills the buffers: their DMAs must have read them
   for (int k = 0; k < 2; ++k)
-    if (used[k]) WV_HIP(hipEventSynchronize(g_stage_ev[k]));
+    if (used[k]) {
+      Status s = hip_status(hipEventSynchronize(g_stage_ev[k]), "copy_h2d: stage wait");
+      if (!s) return fail(s);
+    }
   return Status::ok();
 }
 
@@ -117,6 +133,12 @@ Status copy_d2h(void* dst, const void* src, size_t n, hipStream_t st) {
   WV_TRY(stage_ready());
   bool pend[2] = {false, false};
   size_t pend_off[2] = {0, 0}, pend_len[2] = {0, 0};
+  // as in copy_h2d: no DMA into a staging buffer may still be running when
+  // this returns, on the error paths too
+  auto fail = [&](Status s) {
+    if (hipStreamSynchronize(st) != hipSuccess) (void)hipGetLastError();
+    return s;
+  };
   auto drain = [&](int k) -> Status {
     WV_HIP(hipEventSynchronize(g_stage_ev[k]));
     std::memcpy(static_cast<char*>(dst) + pend_off[k], g_stage[k], pend_len[k]);
@@ -126,14 +148,22 @@ Status copy_d2h(void* dst, const void* src, size_t n, hipStream_t st) {
   int i = 0;
   for (size_t off = 0; off < n; off += kStageBytes, i ^= 1) {
     const size_t len = n - off < kStageBytes ? n - off : kStageBytes;
-    if (pend[i]) WV_TRY(drain(i));
-    WV_HIP(hipMemcpyAsync(g_stage[i], static_cast<const char*>(src) + off, len,
-                          hipMemcpyDeviceToHost, st));
-    WV_HIP(hipEventRecord(g_stage_ev[i], st));
+    if (pend[i]) {
+      Status s = drain(i);
+      if (!s) return fail(s);
+    }
+    Status s = hip_status(hipMemcpyAsync(g_stage[i], static_cast<const char*>(src) + off, len,
+                                         hipMemcpyDeviceToHost, st),
+                          "copy_d2h: hipMemcpyAsync");
+    if (s) s = hip_status(hipEventRecord(g_stage_ev[i], st), "copy_d2h: hipEventRecord");
+    if (!s) return fail(s);
     pend[i] = true, pend_off[i] = off, pend_len[i] = len;
   }
   for (int k = 0; k < 2; ++k)
-    if (pend[i ^ k]) WV_TRY(drain(i ^ k));
+    if (pend[i ^ k]) {
+      Status s = drain(i ^ k);
+      if (!s) return fail(s);
+    }
   return Status::ok();
 }
 
