@@ -277,6 +277,14 @@ WELVET_API welvet_status welvet_read_probe(const void* buf, size_t bytes, uint32
                                            size_t out_cap, void* stream);
 WELVET_API size_t welvet_read_probe_words(size_t bytes);
 
+/* Measurement extension, no reference counterpart: a one-lane kernel queued
+ * on `stream` (null: the default stream) writes the device's constant-rate
+ * wall clock to *out (device memory). Two stamps captured into one graph
+ * around a run of kernels time that run with no graph launch inside it;
+ * welvet_clock_rate_khz gives the clock's rate (0 without a device). */
+WELVET_API welvet_status welvet_clock_stamp(uint64_t* out, void* stream);
+WELVET_API int64_t welvet_clock_rate_khz(void);
+
 /* Segment backward of a Stack model of Dense / SwiGLU children (replaces reference
  * include/welvet_c.h:55, src/interop/model_session.cpp:435-455): the input
  * blob holds the tensors x and gy (model wire: rank, dims, float32 data);

@@ -18,6 +18,11 @@ def pytest_sessionstart(session):
     if not os.path.exists(os.path.join(ROOT, "oracle", "liboracle.so")):
         subprocess.check_call(["make", "-s", "-f", os.path.join(ROOT, "oracle", "Makefile"),
                                os.path.join(ROOT, "oracle", "liboracle.so")])
+    # The C++ API probe links libwelvet.so (built by __graft_entry__.build).
+    probe = os.path.join(ROOT, "tests", "cpp", "libapi_probe.so")
+    if not os.path.exists(probe) and os.path.exists(
+            os.path.join(ROOT, "welvet.cuda_amd", "libwelvet.so")):
+        subprocess.check_call(["make", "-s", "-f", os.path.join(ROOT, "tests", "cpp", "Makefile")])
 
 
 @pytest.fixture(scope="session")

@@ -104,6 +104,24 @@ welvet_status welvet_read_probe(const void* buf, size_t bytes, uint32_t* out_wor
 
 size_t welvet_read_probe_words(size_t bytes) { return wv::read_probe_words(bytes); }
 
+welvet_status welvet_clock_stamp(uint64_t* out, void* stream) {
+  if (!out) return invalid("clock stamp: null output");
+  return guarded([&]() -> Status {
+    WV_TRY(wv::init_device());
+    return wv::launch_clock_stamp(out, static_cast<hipStream_t>(stream));
+  });
+}
+
+int64_t welvet_clock_rate_khz(void) {
+  if (!wv::init_device()) return 0;
+  int khz = 0;
+  if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, 0) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  return khz;
+}
+
 // ---------------------------------------------------------------- Dense ----
 static welvet_status dense_mount(int32_t batch, int32_t in, int32_t out, int32_t act,
                                  int32_t dtype, int32_t backend, const float* W_init,
@@ -1006,26 +1024,6 @@ welvet_status welvet_model_forward_pair(welvet_model_session* s, const uint8_t* 
   });
 }
 
-// remap_gap_len (reference src/layers/dense/dense.cpp:121-139): src resized
-// to `need` values; a different length averages ranges of src in f64.
-static std::vector<float> remap_len(const float* src, size_t sn, size_t need) {
-  std::vector<float> out(need, 0.0f);
-  if (sn == 0 || need == 0) return out;
-  if (sn == need) {
-    std::memcpy(out.data(), src, need * sizeof(float));
-    return out;
-  }
-  for (size_t i = 0; i < need; ++i) {
-    size_t lo = i * sn / need, hi = (i + 1) * sn / need;
-    if (hi <= lo) hi = lo + 1;
-    if (hi > sn) hi = sn;
-    double sum = 0.0;
-    for (size_t j = lo; j < hi; ++j) sum += (double)src[j];
-    out[i] = (float)(sum / (double)(hi - lo));
-  }
-  return out;
-}
-
 // Dense proxy (reference model_session.cpp:475-493) of a Stack holding one
 // Dense: x, gy, an int32 flag and (flag 1) pre in; kind 0 the linear input
 // gradient [batch, in], kind 1 dW [out, in] out.
@@ -1055,7 +1053,7 @@ welvet_status welvet_model_dense_proxy(welvet_model_session* s, int32_t kind, co
     if (xs.size() != 2 || xs[0] <= 0 || ng == 0 || (size_t)xs[0] * L.in != nx)
       return Status::err(wv::kInvalid, kind == 0 ? "dense: LinearGradIn shape" : "dense: GradWOnly shape");
     const size_t b = (size_t)xs[0], ny = b * L.out;
-    const std::vector<float> g = remap_len(hg, ng, ny);
+    const std::vector<float> g = wv::remap_len(hg, ng, ny);
     // kind 1 uses pre only when it is 2-D and long enough (dense.cpp:183-187)
     const bool use_pre = kind == 1 && present && ps.size() == 2 && np >= ny;
     hipStream_t st = s->stream.s;

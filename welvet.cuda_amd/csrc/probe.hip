@@ -38,7 +38,20 @@ __global__ __launch_bounds__(kThreads) void k_read(const uint8_t* __restrict__ b
   if (threadIdx.x == 0) out[blockIdx.x] = part[0] ^ part[1] ^ part[2] ^ part[3];
 }
 
+// One lane writes the device's constant-rate wall clock (wall_clock64) to
+// *out: placed before and after a run of kernels in one stream or graph, two
+// stamps time that run on the device.
+__global__ __launch_bounds__(64) void k_clock_stamp(unsigned long long* __restrict__ out) {
+  if (threadIdx.x == 0) *out = wall_clock64();
+}
+
 }  // namespace
+
+Status launch_clock_stamp(uint64_t* out, hipStream_t st) {
+  if (!out) return Status::err(kInvalid, "clock stamp: null output");
+  k_clock_stamp<<<1, 64, 0, st>>>(reinterpret_cast<unsigned long long*>(out));
+  return hip_status(hipGetLastError(), "clock stamp");
+}
 
 size_t read_probe_words(size_t bytes) { return (bytes + kRun - 1) / kRun; }
 
