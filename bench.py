@@ -46,9 +46,20 @@ sys.path.insert(0, os.path.join(ROOT, "welvet.cuda_amd"))
 HBM_PEAK_GBS = 8000.0
 REPEATS = 3  # timed regions per run; the median is reported
 WARMUP_S = 0.2  # warmup lasts at least this long (clocks leave their idle level)
-# dense MFMA peak of the f8f6f4 instruction with an FP8 operand (the activation
-# terms are E4M3, so FP4 weights run at the FP8 rate)
+# Untimed steps queued right before every timed region, with no host wait in
+# between, lasting about this long: the device runs at its sustained-load
+# clock when timing starts (a region that starts after an idle gap of even
+# tens of microseconds runs ~4% slower at first).
+LEAD_S = 0.01
+# dense matrix-core peaks of MI355X (TFLOP/s). The f8f6f4 instruction runs at
+# the FP8 rate when either operand is FP8, at the FP4/FP6 rate when both are
+# FP4 or FP6: FP8 weights (any activation terms) and FP4 weights with E4M3
+# terms (two- and one-term modes) use the FP8 peak; FP4 weights with the
+# default three FP6 (E2M3) terms the FP4/FP6 peak. The attention core's
+# products run on the bf16 matrix cores.
 MFMA_FP8_PEAK_TFLOPS = 5000.0
+MFMA_FP4_PEAK_TFLOPS = 10070.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 METRIC = "FP8/FP4 Dense GEMV GB/s + GEMM TFLOPS (% roofline), 1 MI355X vs host CPU"
 # CPU threads for the baseline: the job's CPU share (the affinity mask),
 # capped at the 16 threads a one-GPU job is given on the GPU hosts
@@ -137,6 +148,14 @@ def cpu_record(value_n, value_1, unit, th, per_n, per_1, mount, sample):
             "host_threads_visible": os.cpu_count(), "sample": sample}
 
 
+def step_peak(parts):
+    """Peak for a step made of products at different matrix-core rates:
+    parts = [(flops, peak_tflops)]; the step's useful FLOPs over the time
+    they take when each product runs at its own peak."""
+    total = sum(f for f, _ in parts)
+    return total / sum(f / p for f, p in parts)
+
+
 # --------------------------------------------------------------------------
 # workloads: each builds its sessions and returns a dict with
 #   desc, enqueue(i, stream), per_graph, bytes, flops, bound, dtype, config,
@@ -188,8 +207,10 @@ def dense_workload(pw, hip, name, cfg_id, dtype, scheme, batch, K, N, copies, bo
         hip.free(dx)
         hip.free(dy)
 
+    fp6_terms = (scheme & 0x30) == 0  # three FP6 terms unless bit 16 or 32 asks for E4M3 ones
+    peak = MFMA_FP4_PEAK_TFLOPS if (dtype == 16 and fp6_terms) else MFMA_FP8_PEAK_TFLOPS
     return {"desc": name, "enqueue": enqueue, "per_graph": copies, "bytes": nbytes,
-            "flops": flops, "bound": bound, "dtype": dname,
+            "flops": flops, "bound": bound, "dtype": dname, "peak_tflops": peak,
             "config": {"workload": name, "in": K, "out": N, "batch": batch, "scale": sname,
                        "weight_copies_rotated": copies},
             "cpu": cpu, "close": close}
@@ -343,13 +364,20 @@ def mha_workload(pw, hip, name, two=0):
             hip.free(p)
 
     return {"desc": name, "enqueue": enqueue, "per_graph": 4, "bytes": nbytes,
-            "flops": proj + att, "bound": "mfma", "dtype": "fp8e5m2",
+            "flops": proj + att_computed, "bound": "mfma", "dtype": "fp8e5m2",
+            "peak_tflops": step_peak([(proj, MFMA_FP8_PEAK_TFLOPS),
+                                      (att_computed, MFMA_BF16_PEAK_TFLOPS)]),
             "config": {"workload": name, "batch": B, "seq": S, "d_model": d, "heads": H,
                        "head_dim": hd, "mask": "causal", "pos": "rope",
                        "projection_flops": proj,
-                       "attention_flops_reference_semantics": att,
                        "attention_flops_computed": att_computed,
-                       "flops_basis": "value counts the reference's per-key-position attention"},
+                       "attention_flops_reference_semantics": att,
+                       "flops_basis": ("value counts the FLOPs computed: the projections plus "
+                                       "the attention over distinct KV-ring rows; the "
+                                       "reference's per-key-position count is "
+                                       "attention_flops_reference_semantics"),
+                       "tflops_reference_semantics": None},
+            "flops_ref": proj + att,
             "cpu": None, "close": close}
 
 
@@ -407,8 +435,12 @@ def cells_workload(pw, hip, name, two=0, keep_inner=False):
             for p in b:
                 hip.free(p)
 
+    per_layer = flops // len(kinds)
+    fp4_peak = MFMA_FP4_PEAK_TFLOPS if two == 0 else MFMA_FP8_PEAK_TFLOPS
+    peak = step_peak([(per_layer, fp4_peak if dt == 16 else MFMA_FP8_PEAK_TFLOPS)
+                      for dt, _ in kinds])
     return {"desc": name, "enqueue": enqueue, "per_graph": 1, "bytes": None, "flops": flops,
-            "bound": "mfma", "dtype": "fp8e4m3+fp4e2m1",
+            "bound": "mfma", "dtype": "fp8e4m3+fp4e2m1", "peak_tflops": peak,
             "config": {"workload": name, "cells": cells, "layers_per_cell": 3, "batch": batch,
                        "width": d, "layer_kinds": "E4M3 per-row, FP4 E8M0/32, E4M3 per-row",
                        "execution": ("independent cells, one grouped launch per layer position, "
@@ -466,8 +498,12 @@ def chain_workload(pw, hip, name, two=0):
         hip.free(x)
         hip.free(y)
 
+    per_layer = flops // len(kinds)
+    fp4_peak = MFMA_FP4_PEAK_TFLOPS if two == 0 else MFMA_FP8_PEAK_TFLOPS
+    peak = step_peak([(per_layer, fp4_peak if dt == 16 else MFMA_FP8_PEAK_TFLOPS)
+                      for dt, _ in kinds])
     return {"desc": name, "enqueue": enqueue, "per_graph": 1, "bytes": None, "flops": flops,
-            "bound": "mfma", "dtype": "fp8e4m3+fp4e2m1", "direct": True,
+            "bound": "mfma", "dtype": "fp8e4m3+fp4e2m1", "direct": True, "peak_tflops": peak,
             "config": {"workload": name, "cells": cells, "layers_per_cell": 3, "batch": batch,
                        "width": d, "layer_kinds": "E4M3 per-row, FP4 E8M0/32, E4M3 per-row "
                                                "(scaled WMN1 store payloads)",
@@ -640,8 +676,8 @@ class Runner:
     next, so every step reads the copy least recently used. A graph of n
     steps from rotation offset o is captured once and kept."""
 
-    def __init__(self, hip, wl, stream):
-        self.hip, self.wl, self.stream = hip, wl, stream
+    def __init__(self, pw, hip, wl, stream):
+        self.pw, self.hip, self.wl, self.stream = pw, hip, wl, stream
         self.per = max(1, wl["per_graph"])
         self.direct = wl.get("direct", False)  # synchronous calls: no capture
         self.offset = 0
@@ -679,6 +715,32 @@ class Runner:
         if rem:
             self.hip.launch(self._graph(self.offset, rem), self.stream)
             self.offset = (self.offset + rem) % self.per
+
+    def timed(self, steps, stamps):
+        """The graph of one timed region: an untimed rotation, a device clock
+        stamp into stamps[0], `steps` steps, a stamp into stamps[1], all
+        captured as one graph (kept per rotation offset and length). No graph
+        launch falls inside the timed steps, whatever `steps` is."""
+        key = ("timed", self.offset % self.per, steps)
+        if key not in self.graphs:
+            start = self.offset
+            L = self.pw.lib()
+
+            def go():
+                for i in range(start, start + self.per):
+                    self.wl["enqueue"](i, self.stream)
+                self.pw.check(L.welvet_clock_stamp(ctypes.c_void_p(stamps), ctypes.c_void_p(self.stream)))
+                for i in range(start + self.per, start + self.per + steps):
+                    self.wl["enqueue"](i, self.stream)
+                self.pw.check(L.welvet_clock_stamp(ctypes.c_void_p(stamps + 8),
+                                                   ctypes.c_void_p(self.stream)))
+            g = self.hip.capture(self.stream, go)
+            # one untimed launch: a graph's first launch also uploads its
+            # nodes' kernel arguments, which later launches reuse
+            self.hip.launch(g, self.stream)
+            self.hip.sync()
+            self.graphs[key] = g
+        return self.graphs[key]
 
     def close(self):
         for g in self.graphs.values():
@@ -735,7 +797,7 @@ def main():
     steps = args.steps if args.steps is not None else (1280 if gemv else 64)
     steps = max(1, steps)
     stream = hip.stream()
-    runner = Runner(hip, wl, stream)
+    runner = Runner(pw, hip, wl, stream)
 
     # warmup: at least the requested steps and at least WARMUP_S seconds, in
     # whole rotations (the clocks start from their idle level)
@@ -746,22 +808,63 @@ def main():
         runner.run(runner.per)
         hip.sync()
         warmup += runner.per
+    # lead-in before each timed region: whole rotations, about LEAD_S long
+    per_step_est = (time.perf_counter() - t0) / max(1, warmup)
+    lead = runner.per * max(1, int(LEAD_S / (per_step_est * runner.per) + 0.999))
     # The timed region (exactly `steps` steps between device synchronizations)
     # runs REPEATS times; the median is reported, so one disturbed run does not
     # become the result (the three times are in config.ms_runs).
     e0, e1 = hip.event(), hip.event()
     runs = []
     t_wall = 0.0
-    for _ in range(REPEATS):
-        runner.prepare(steps)
+    # Graph-replayed workloads: each region is one captured graph holding an
+    # untimed rotation, a device clock stamp, the `steps` timed steps and a
+    # second stamp (Runner.timed), so the steps run back to back with no
+    # graph launch among them at any `steps`; the region's time is the
+    # difference of the two stamps. Direct workloads (synchronous calls) are
+    # timed between events recorded around the calls.
+    stamps = hip.malloc(16)
+    khz = pw.lib().welvet_clock_rate_khz()
+
+    def stamped(n):
+        """ms between the two stamps of one region of n steps."""
+        import numpy as np
+        g = runner.timed(n, stamps)
         hip.sync()
-        t1 = time.perf_counter()
-        hip.record(e0, stream)
-        runner.run(steps)
-        hip.record(e1, stream)
+        runner.run(lead)
+        hip.launch(g, stream)
+        runner.offset = (runner.offset + n) % runner.per
+        hip.sync()
+        t = hip.download(stamps, (2,), np.uint64)
+        return float(int(t[1]) - int(t[0])) / khz
+
+    # The stamps' own cost (the first stamp's run and the second's dispatch,
+    # the same in every region) is the median time of regions with no steps;
+    # it is subtracted from every timed region.
+    stamp_ms = 0.0 if runner.direct else sorted(stamped(0) for _ in range(5))[2]
+    for _ in range(REPEATS):
+        if runner.direct:
+            hip.sync()
+            t1 = time.perf_counter()
+            hip.record(e0, stream)
+            runner.run(steps)
+            hip.record(e1, stream)
+        else:
+            g = runner.timed(steps, stamps)
+            hip.sync()
+            t1 = time.perf_counter()
+            runner.run(lead)
+            hip.launch(g, stream)
+            runner.offset = (runner.offset + steps) % runner.per
         hip.sync()
         t_wall += time.perf_counter() - t1
-        runs.append(hip.elapsed_ms(e0, e1))
+        if runner.direct:
+            runs.append(hip.elapsed_ms(e0, e1))
+        else:
+            import numpy as np
+            t = hip.download(stamps, (2,), np.uint64)
+            runs.append(float(int(t[1]) - int(t[0])) / khz - stamp_ms)
+    hip.free(stamps)
     t_wall /= REPEATS
     ms = sorted(runs)[len(runs) // 2]
     per_step_s = ms * 1e-3 / steps
@@ -775,18 +878,26 @@ def main():
                 "traffic": measured_traffic("read_floor" if args.read_floor else args.config)}
     else:
         value, unit = tflops, "TFLOP/s"
-        roof = {"bound": "mfma", "achieved": round(tflops, 3), "peak": MFMA_FP8_PEAK_TFLOPS,
-                "unit": "TFLOP/s", "frac": round(tflops / MFMA_FP8_PEAK_TFLOPS, 4),
+        peak = wl.get("peak_tflops", MFMA_FP8_PEAK_TFLOPS)
+        roof = {"bound": "mfma", "achieved": round(tflops, 3), "peak": round(peak, 1),
+                "unit": "TFLOP/s", "frac": round(tflops / peak, 4),
                 "traffic": measured_traffic(args.config)}
     cpu = None if (args.no_cpu or wl["cpu"] is None) else wl["cpu"](16.0)
     config = dict(wl["config"])
     rotated = min(runner.per, steps) if runner.direct else runner.per
+    config.update({"timer": ("HIP events around the synchronous calls" if runner.direct else
+                             "device wall-clock stamps captured in the region's graph, "
+                             f"less the stamps' own cost ({stamp_ms * 1e3:.3f} us, the median "
+                             "of empty regions)"),
+                   "lead_in_steps": 0 if runner.direct else lead})
     config.update({"tflops": round(tflops, 4), "wall_s": round(t_wall, 4),
                    "ms_runs": [round(r, 4) for r in runs], "timed_regions": REPEATS,
                    "copies_rotated": rotated,
                    "rotation": ("one rotation over the copies continuing across warmup and "
                                 "timed regions: each step reads the least recently used copy")})
     config.pop("weight_copies_rotated", None)
+    if "tflops_reference_semantics" in config:
+        config["tflops_reference_semantics"] = round(wl["flops_ref"] / per_step_s / 1e12, 4)
     if wl["bound"] == "mfma":
         config["activation_terms"] = args.terms
     if wl["bytes"]:
