@@ -26,7 +26,8 @@ Other workloads (--config), each its own line:
   c5chain  the same cells as the reference's volume: one 192-layer serial chain (model session)
   c2bwd  Dense backward at the GEMV shape: d_pre, dX = W^T d_pre, dW (4096^2 E4M3 per-row, batch 1)
   gemv_<fmt>  the c2 GEMV shape over a packed block format (q8_0, q4_0, q4_1, q5_0, q5_1,
-         q2_k, q3_k, q4_k, q5_k, q6_k, iq4_nl, iq4_xs; bytes = packed blocks + x + y)
+         q2_k, q3_k, q4_k, q5_k, q6_k, iq4_nl, iq4_xs; quantized on the device from the
+         same weights; bytes = packed blocks + x + y)
 --read-floor BYTES instead times one streaming read of BYTES (default: the c2
 step's 16,826,368) over 64 rotated buffers, the same way: the floor for any
 kernel that reads those bytes once.
@@ -222,49 +223,16 @@ FORMATS = {"q8_0": (1, 32, 34), "q4_0": (2, 32, 18), "q4_1": (3, 32, 20), "q5_0"
            "iq4_nl": (16, 32, 18), "iq4_xs": (17, 256, 136)}
 
 
-def format_blocks(fmt, qk, bb, N, K, seed):
-    """Valid packed blocks of random codes with f16 scales near 1/sqrt(K)/8
-    (the K and IQ4 formats: mounted from blocks, their reference quantizers
-    being a search that is not built here)."""
-    import numpy as np
-
-    rng = np.random.default_rng(seed)
-    nb = N * K // qk
-    raw = rng.integers(0, 256, size=(nb, bb), dtype=np.uint8)
-    d = (rng.uniform(0.5, 1.5, nb) / np.sqrt(K) / 8).astype(np.float32)
-    if fmt in (8, 9):
-        raw[:, 0:2] = (d / 32).astype(np.float16).view(np.uint8).reshape(nb, 2)
-        raw[:, 2:4] = (d / 64).astype(np.float16).view(np.uint8).reshape(nb, 2)
-    elif fmt == 6:
-        raw[:, 80:82] = (d / 8).astype(np.float16).view(np.uint8).reshape(nb, 2)
-        raw[:, 82:84] = (d / 16).astype(np.float16).view(np.uint8).reshape(nb, 2)
-    elif fmt == 7:
-        raw[:, 108:110] = (d / 16).astype(np.float16).view(np.uint8).reshape(nb, 2)
-    elif fmt == 16:
-        raw[:, 0:2] = (d / 16).astype(np.float16).view(np.uint8).reshape(nb, 2)
-    elif fmt == 17:
-        raw[:, 0:2] = (d / 256).astype(np.float16).view(np.uint8).reshape(nb, 2)
-    else:
-        raw[:, 208:210] = (d / 64).astype(np.float16).view(np.uint8).reshape(nb, 2)
-    return raw.reshape(-1)
-
-
 def format_workload(pw, hip, name, fmt_name, batch, K, N, copies):
-    """GEMV over a packed block format (welvet_dense_mount_format): Q8_0 ..
-    Q5_1 quantized on the device from N(0, 1/sqrt(K)) weights, the K and IQ4
-    formats mounted from valid packed blocks of random codes."""
+    """GEMV over a packed block format (welvet_dense_mount_format), every
+    format quantized on the device from N(0, 1/sqrt(K)) weights."""
     import numpy as np
 
     fmt, qk, bb = FORMATS[fmt_name]
     seed = pw.seed_for(2)
     x = pw.normal(seed + 500, batch * K).reshape(batch, K)
-    if fmt <= 5:
-        W = pw.normal(seed, N * K, 1 / np.sqrt(K)).reshape(N, K)
-        sessions = [pw.FormatDenseSession(batch, K, N, -1, fmt, W=W) for _ in range(copies)]
-    else:
-        blocks = format_blocks(fmt, qk, bb, N, K, seed)
-        sessions = [pw.FormatDenseSession(batch, K, N, -1, fmt, blocks=blocks)
-                    for _ in range(copies)]
+    W = pw.normal(seed, N * K, 1 / np.sqrt(K)).reshape(N, K)
+    sessions = [pw.FormatDenseSession(batch, K, N, -1, fmt, W=W) for _ in range(copies)]
     dx = hip.upload(x)
     dy = hip.malloc(batch * N * 4)
     nbytes = N * K // qk * bb + 4 * batch * K + 4 * batch * N

@@ -149,8 +149,10 @@ WELVET_API welvet_status welvet_dense_export_store(welvet_dense_session* sess, u
  * 4 Q5_0, 5 Q5_1, 6 Q2_K, 7 Q3_K, 8 Q4_K, 9 Q5_K, 10 Q6_K, 16 IQ4_NL,
  * 17 IQ4_XS (ggml's block layouts); the other values of the table (11-15,
  * 18-20) return code 3. Exactly one of W_init (fp32 [out*in], quantized on
- * the device: Q8_0 .. Q5_1) and blocks (the packed row-major blocks,
- * blocks_len bytes: every built format) is given; in must be a multiple of
+ * the device: Q8_0 .. Q5_1 with ggml's reference quantizers, the K formats
+ * and IQ4_NL / IQ4_XS with the library's one-pass quantizers) and blocks
+ * (the packed row-major blocks, blocks_len bytes) is given; in must be a
+ * multiple of
  * the block (32, or 256 for the K formats and IQ4_XS). Execute,
  * execute_device, execute_noalloc and release are those of
  * welvet_dense_session (device x must be 16-byte aligned); backward and the

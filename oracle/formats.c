@@ -214,6 +214,233 @@ static void q5_1_block(const float* x, uint8_t* y) {
   memcpy(y + 4, &qh, 4);
 }
 
+/* ggml's non-linear 4-bit code book of IQ4_NL and IQ4_XS (kvalues_iq4nl). */
+static const int8_t kIq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
+                                  1,    13,   25,  38,  53,  69,  89,  113};
+
+/* ---- The library's quantizers of the K and IQ4 formats.
+ * ggml's own (make_qkx2_quants, make_q3_quants, make_qx_quants and the IQ4
+ * scale search) refine the scales with a weighted least-squares search;
+ * ggml is not in this image, so these are the library's own one-pass
+ * quantizers into the same block layouts (the restatement of the device
+ * code in formats.hip, which must give the same bytes):
+ *  - affine formats (Q2_K, Q4_K, Q5_K): per sub-block, scale = (max - mn) /
+ *    qmax and offset = -mn with mn = min(0, min); the super-block's scales
+ *    and offsets are quantized to lmax levels of d = max scale / lmax and
+ *    dmin = max offset / lmax; codes q = round((x + dmin * lm) / (d * ls));
+ *  - signed formats (Q3_K, Q6_K): per sub-block s = m / qdiv with m the
+ *    element of largest magnitude (so m takes the code qdiv exactly); the
+ *    super-block's scales are integers of d = ms / ldiv, ms the s of largest
+ *    magnitude; q = round(x / (d * l));
+ *  - IQ4_NL / IQ4_XS: the scale maps the element of largest magnitude to
+ *    the code book's -127 (IQ4_XS: per sub-block, with the 6-bit integer
+ *    scales of d = ms / -32); each element takes the nearest code-book entry
+ *    (the first on ties).
+ * d and dmin are rounded to f16 before the codes are chosen, so the codes fit
+ * the stored scales. Plain f32 arithmetic in the order written, no
+ * contraction. */
+static int clampi(int v, int lo, int hi) { return v < lo ? lo : v > hi ? hi : v; }
+static float f16r(float v) { return or_f16_to_f32(or_f32_to_f16(v)); }
+/* nearest integer of v clamped to [lo, hi] (half away from zero) */
+static int qround(float v, int lo, int hi) {
+  return clampi((int)roundf(fminf(fmaxf(v, (float)lo), (float)hi)), lo, hi);
+}
+static float signed_amax_n(const float* x, int n) {
+  float amax = 0.0f, max = 0.0f;
+  for (int j = 0; j < n; ++j) {
+    if (amax < fabsf(x[j])) {
+      amax = fabsf(x[j]);
+      max = x[j];
+    }
+  }
+  return max;
+}
+
+/* Affine super-block: nsub sub-blocks of sub elements; qmax code levels,
+ * lmax scale / offset levels. ls, lm: integer scales and offsets; q: codes;
+ * d, dmin: the f32 super-block scales (stored as f16). */
+static void affine_k(const float* x, int nsub, int sub, int qmax, int lmax, int* ls, int* lm,
+                     int* q, float* d, float* dmin) {
+  float scale[16], off[16];
+  float max_scale = 0.0f, max_off = 0.0f;
+  for (int j = 0; j < nsub; ++j) {
+    const float* v = x + sub * j;
+    float mn = v[0], mx = v[0];
+    for (int i = 1; i < sub; ++i) {
+      mn = v[i] < mn ? v[i] : mn;
+      mx = v[i] > mx ? v[i] : mx;
+    }
+    /* the offset is -min(min, 0); comparisons, not fmaxf, so that an all-zero
+     * or constant sub-block gives +0 (fmaxf may return either signed zero) */
+    off[j] = mn < 0.0f ? -mn : 0.0f;
+    scale[j] = (mx + off[j]) / (float)qmax;
+    if (scale[j] > max_scale) max_scale = scale[j];
+    if (off[j] > max_off) max_off = off[j];
+  }
+  const float inv_s = max_scale > 0.0f ? (float)lmax / max_scale : 0.0f;
+  const float inv_m = max_off > 0.0f ? (float)lmax / max_off : 0.0f;
+  *d = max_scale / (float)lmax;
+  *dmin = max_off / (float)lmax;
+  const float dd = f16r(*d), dm = f16r(*dmin);
+  for (int j = 0; j < nsub; ++j) {
+    ls[j] = qround(inv_s * scale[j], 0, lmax);
+    lm[j] = qround(inv_m * off[j], 0, lmax);
+    const float ds = dd * (float)ls[j];
+    const float dmn = dm * (float)lm[j];
+    const float id = ds > 0.0f ? 1.0f / ds : 0.0f;
+    for (int i = 0; i < sub; ++i) q[sub * j + i] = qround((x[sub * j + i] + dmn) * id, 0, qmax);
+  }
+}
+
+/* Signed super-block: sub-block scales m / qdiv as integers of d = ms / ldiv
+ * in [lmin, lmax]; codes in [qlo, qhi]. */
+static void signed_k(const float* x, int nsub, int sub, float qdiv, int qlo, int qhi, float ldiv,
+                     int lmin, int lmax, int* l, int* q, float* d) {
+  float s[16];
+  for (int j = 0; j < nsub; ++j) s[j] = signed_amax_n(x + sub * j, sub) / qdiv;
+  const float ms = signed_amax_n(s, nsub);
+  *d = ms / ldiv;
+  const float id = *d != 0.0f ? 1.0f / *d : 0.0f;
+  const float dd = f16r(*d);
+  for (int j = 0; j < nsub; ++j) {
+    l[j] = qround(s[j] * id, lmin, lmax);
+    const float ds = dd * (float)l[j];
+    const float is = ds != 0.0f ? 1.0f / ds : 0.0f;
+    for (int i = 0; i < sub; ++i) q[sub * j + i] = qround(x[sub * j + i] * is, qlo, qhi);
+  }
+}
+
+/* index of the code-book entry nearest t (the first on ties) */
+static int iq4_index(float t) {
+  int best = 0;
+  float err = fabsf(t - (float)kIq4nl[0]);
+  for (int k = 1; k < 16; ++k) {
+    const float e = fabsf(t - (float)kIq4nl[k]);
+    if (e < err) {
+      err = e;
+      best = k;
+    }
+  }
+  return best;
+}
+
+static void q4k_block(const float* x, uint8_t* y, int k5) {
+  int ls[8], lm[8], q[256];
+  float d, dmin;
+  affine_k(x, 8, 32, k5 ? 31 : 15, 63, ls, lm, q, &d, &dmin);
+  memset(y, 0, k5 ? 176 : 144);
+  put16(y, or_f32_to_f16(d));
+  put16(y + 2, or_f32_to_f16(dmin));
+  uint8_t* sc = y + 4;
+  for (int j = 0; j < 8; ++j) {
+    if (j < 4) {
+      sc[j] |= (uint8_t)(ls[j] & 63);
+      sc[j + 4] |= (uint8_t)(lm[j] & 63);
+    } else {
+      sc[j + 4] = (uint8_t)((ls[j] & 15) | ((lm[j] & 15) << 4));
+      sc[j - 4] |= (uint8_t)((ls[j] >> 4) << 6);
+      sc[j] |= (uint8_t)((lm[j] >> 4) << 6);
+    }
+  }
+  uint8_t* qh = y + 16;
+  uint8_t* qs = y + (k5 ? 48 : 16);
+  for (int i = 0; i < 4; ++i)
+    for (int l = 0; l < 32; ++l) {
+      const int a = q[64 * i + l], b = q[64 * i + 32 + l];
+      qs[32 * i + l] = (uint8_t)((a & 15) | ((b & 15) << 4));
+      if (k5) qh[l] |= (uint8_t)(((a >> 4) << (2 * i)) | ((b >> 4) << (2 * i + 1)));
+    }
+}
+static void q4_k_block(const float* x, uint8_t* y) { q4k_block(x, y, 0); }
+static void q5_k_block(const float* x, uint8_t* y) { q4k_block(x, y, 1); }
+
+static void q2_k_block(const float* x, uint8_t* y) {
+  int ls[16], lm[16], q[256];
+  float d, dmin;
+  affine_k(x, 16, 16, 3, 15, ls, lm, q, &d, &dmin);
+  memset(y, 0, 84);
+  for (int j = 0; j < 16; ++j) y[j] = (uint8_t)(ls[j] | (lm[j] << 4));
+  for (int n = 0; n < 2; ++n)
+    for (int j = 0; j < 4; ++j)
+      for (int l = 0; l < 32; ++l) y[16 + 32 * n + l] |= (uint8_t)(q[128 * n + 32 * j + l] << (2 * j));
+  put16(y + 80, or_f32_to_f16(d));
+  put16(y + 82, or_f32_to_f16(dmin));
+}
+
+static void q3_k_block(const float* x, uint8_t* y) {
+  int l[16], q[256];
+  float d;
+  signed_k(x, 16, 16, -4.0f, -4, 3, -32.0f, -32, 31, l, q, &d);
+  memset(y, 0, 110);
+  uint8_t* hm = y;
+  uint8_t* qs = y + 32;
+  uint8_t* sc = y + 96;
+  for (int n = 0; n < 2; ++n)
+    for (int j = 0; j < 4; ++j)
+      for (int i = 0; i < 32; ++i) {
+        const int v = q[128 * n + 32 * j + i] + 4;
+        qs[32 * n + i] |= (uint8_t)((v & 3) << (2 * j));
+        hm[i] |= (uint8_t)((v >> 2) << (4 * n + j));
+      }
+  for (int s = 0; s < 16; ++s) {
+    const int v = l[s] + 32, g = s >> 2, i = s & 3;
+    sc[(g & 1) * 4 + i] |= (uint8_t)((v & 15) << ((g >> 1) * 4));
+    sc[8 + i] |= (uint8_t)((v >> 4) << (2 * g));
+  }
+  put16(y + 108, or_f32_to_f16(d));
+}
+
+static void q6_k_block(const float* x, uint8_t* y) {
+  int l[16], q[256];
+  float d;
+  signed_k(x, 16, 16, -32.0f, -32, 31, -128.0f, -128, 127, l, q, &d);
+  memset(y, 0, 210);
+  uint8_t* ql = y;
+  uint8_t* qh = y + 128;
+  for (int n = 0; n < 2; ++n)
+    for (int t = 0; t < 4; ++t)
+      for (int i = 0; i < 32; ++i) {
+        const int v = q[128 * n + 32 * t + i] + 32;
+        ql[64 * n + 32 * (t & 1) + i] |= (uint8_t)((v & 15) << (4 * (t >> 1)));
+        qh[32 * n + i] |= (uint8_t)((v >> 4) << (2 * t));
+      }
+  for (int s = 0; s < 16; ++s) y[192 + s] = (uint8_t)(int8_t)l[s];
+  put16(y + 208, or_f32_to_f16(d));
+}
+
+/* the 32 code-book indices of one sub-block at scale ds into qs[16] */
+static void iq4_sub(const float* x, float ds, uint8_t* qs) {
+  const float id = ds != 0.0f ? 1.0f / ds : 0.0f;
+  for (int j = 0; j < 16; ++j)
+    qs[j] = (uint8_t)(iq4_index(x[j] * id) | (iq4_index(x[16 + j] * id) << 4));
+}
+
+static void iq4_nl_block(const float* x, uint8_t* y) {
+  const float d = signed_amax_n(x, 32) / -127.0f;
+  put16(y, or_f32_to_f16(d));
+  iq4_sub(x, f16r(d), y + 2);
+}
+
+static void iq4_xs_block(const float* x, uint8_t* y) {
+  float s[8];
+  for (int j = 0; j < 8; ++j) s[j] = signed_amax_n(x + 32 * j, 32) / -127.0f;
+  const float ms = signed_amax_n(s, 8);
+  const float d = ms / -32.0f;
+  const float id = d != 0.0f ? 1.0f / d : 0.0f;
+  const float dd = f16r(d);
+  memset(y, 0, 136);
+  put16(y, or_f32_to_f16(d));
+  int sh = 0;
+  for (int j = 0; j < 8; ++j) {
+    const int l = qround(s[j] * id, -32, 31);
+    const int ls = l + 32;
+    y[4 + j / 2] |= (uint8_t)((ls & 15) << (4 * (j & 1)));
+    sh |= (ls >> 4) << (2 * j);
+    iq4_sub(x + 32 * j, dd * (float)l, y + 8 + 16 * j);
+  }
+  put16(y + 2, (uint16_t)sh);
+}
+
 int or_fmt_quantize(int fmt, int64_t n, const float* x, uint8_t* out) {
   void (*blk)(const float*, uint8_t*) = NULL;
   switch (fmt) {
@@ -222,11 +449,19 @@ int or_fmt_quantize(int fmt, int64_t n, const float* x, uint8_t* out) {
   case OR_FMT_Q4_1: blk = q4_1_block; break;
   case OR_FMT_Q5_0: blk = q5_0_block; break;
   case OR_FMT_Q5_1: blk = q5_1_block; break;
-  default: return -1; /* the K formats' quantizers (an rmse search) are not restated */
+  case OR_FMT_Q2_K: blk = q2_k_block; break;
+  case OR_FMT_Q3_K: blk = q3_k_block; break;
+  case OR_FMT_Q4_K: blk = q4_k_block; break;
+  case OR_FMT_Q5_K: blk = q5_k_block; break;
+  case OR_FMT_Q6_K: blk = q6_k_block; break;
+  case OR_FMT_IQ4_NL: blk = iq4_nl_block; break;
+  case OR_FMT_IQ4_XS: blk = iq4_xs_block; break;
+  default: return -1;
   }
-  if (n % 32) return -1;
+  const int qk = or_fmt_block_elems(fmt);
+  if (n % qk) return -1;
   const int bb = or_fmt_block_bytes(fmt);
-  for (int64_t b = 0; b < n / 32; ++b) blk(x + 32 * b, out + bb * b);
+  for (int64_t b = 0; b < n / qk; ++b) blk(x + qk * b, out + bb * b);
   return 0;
 }
 
@@ -253,9 +488,6 @@ static int scale_q3k(int s, const uint8_t* q) {
   return (lo | (hi << 4)) - 32;
 }
 
-/* ggml's non-linear 4-bit code book of IQ4_NL and IQ4_XS (kvalues_iq4nl). */
-static const int8_t kIq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
-                                  1,    13,   25,  38,  53,  69,  89,  113};
 
 static void dequant_block(int fmt, const uint8_t* b, float* y) {
   switch (fmt) {

@@ -1,6 +1,8 @@
 """Packed block formats on the GPU (welvet_dense_mount_format), against the
 oracle (oracle/formats.c):
-- the device quantizers give the oracle's packed blocks byte for byte;
+- the device quantizers give the oracle's packed blocks byte for byte (ggml's
+  reference quantizers for Q8_0 .. Q5_1, the library's one-pass quantizers
+  for the K and IQ4 formats);
 - the resident layout dequantizes to the oracle's f32 bit for bit (export);
 - the GEMV matches the oracle's dequantize-then-f64 Dense at rel-L2 <= 1e-5
   (f32 accumulation on the VALU, as the FP8/FP4 GEMV);
@@ -49,7 +51,31 @@ def test_quantize_blocks_and_dequant_bit_exact(gpu, oracle, fmt, rows, cols):
         s.close()
 
 
-@pytest.mark.parametrize("fmt", LEGACY, ids=lambda f: NAMES[f])
+NEW_Q = [f for f in ALL if f not in LEGACY]
+
+
+@pytest.mark.parametrize("fmt", NEW_Q, ids=lambda f: NAMES[f])
+@pytest.mark.parametrize("rows,cols", [(1, 256), (7, 512), (300, 1024), (129, 4096)])
+def test_k_quantize_blocks_and_dequant_bit_exact(gpu, oracle, fmt, rows, cols):
+    """The K and IQ4 formats quantized from fp32 on the device (the library's
+    one-pass quantizers): the oracle's blocks byte for byte, and the resident
+    layout dequantizes to the oracle's f32 bit for bit."""
+    rng = np.random.default_rng(fmt * 1000 + rows + cols + 5)
+    W = (rng.standard_normal((rows, cols)) * rng.uniform(1e-3, 10.0, (rows, 1))).astype(np.float32)
+    s = gpu.FormatDenseSession(1, cols, rows, -1, fmt, W=W)
+    try:
+        got = s.export_blocks()
+        want = oracle.fmt_quantize(fmt, W)
+        assert got.size == want.size
+        bad = np.flatnonzero(got != want)
+        assert bad.size == 0, f"{NAMES[fmt]}: {bad.size} bytes differ, first at {bad[:4]}"
+        Wd = oracle.fmt_dequant(fmt, want, (rows, cols))
+        assert np.array_equal(s.export_f32().view(np.uint32), Wd.view(np.uint32))
+    finally:
+        s.close()
+
+
+@pytest.mark.parametrize("fmt", ALL, ids=lambda f: NAMES[f])
 def test_quantize_extreme_blocks(gpu, oracle, fmt):
     """Blocks whose scale is an f16 subnormal or near the f16 maximum, all-zero
     blocks, constant blocks and one-hot blocks."""
@@ -69,12 +95,12 @@ def test_quantize_extreme_blocks(gpu, oracle, fmt):
     try:
         got = s.export_blocks()
         want = oracle.fmt_quantize(fmt, W)
-        bb = GEOM[fmt][1]
+        qk, bb = GEOM[fmt]
         bad = np.flatnonzero(got != want)
         for i in bad[:8]:
             blk = i // bb
-            print(f"block {blk} (row {blk // (cols // 32)}) byte {i % bb}: got {got[i]:#04x} "
-                  f"want {want[i]:#04x}; x = {W.reshape(-1, 32)[blk][:4]}")
+            print(f"block {blk} (row {blk // (cols // qk)}) byte {i % bb}: got {got[i]:#04x} "
+                  f"want {want[i]:#04x}; x = {W.reshape(-1, qk)[blk][:4]}")
         assert bad.size == 0
         Wd = oracle.fmt_dequant(fmt, want, (rows, cols))
         assert np.array_equal(s.export_f32().view(np.uint32), Wd.view(np.uint32))
@@ -118,14 +144,15 @@ def test_gemv_against_oracle(gpu, oracle, fmt, batch):
     assert np.array_equal(pre, post)
 
 
-@pytest.mark.parametrize("fmt", [2, 8, 10], ids=lambda f: NAMES[f])
-def test_gemv_full_size_4096(gpu, oracle, fmt):
-    """The benchmark shape: 4096 x 4096 at batch 1 (Q4_0 quantized from fp32 on
-    the device; Q4_K and Q6_K from packed blocks)."""
+@pytest.mark.parametrize("fmt,from_fp32", [(2, True), (8, False), (10, False), (8, True),
+                                           (17, True)], ids=lambda v: str(v))
+def test_gemv_full_size_4096(gpu, oracle, fmt, from_fp32):
+    """The benchmark shape: 4096 x 4096 at batch 1, quantized from fp32 on
+    the device or mounted from packed blocks."""
     rng = np.random.default_rng(4096 + fmt)
     n = 4096
     x = rng.standard_normal((1, n)).astype(np.float32)
-    if fmt in LEGACY:
+    if from_fp32:
         W = (rng.standard_normal((n, n)) / np.sqrt(n)).astype(np.float32)
         s = gpu.FormatDenseSession(1, n, n, -1, fmt, W=W)
         blocks = oracle.fmt_quantize(fmt, W)
@@ -229,9 +256,11 @@ def test_errors_and_gaps(gpu):
     with pytest.raises(gpu.WelvetError) as e:  # in not a multiple of the block
         mount(in_dim=48, W=np.zeros((16, 48), np.float32))
     assert e.value.code == 1
-    with pytest.raises(gpu.WelvetError) as e:  # K formats need 256 and blocks
-        mount(fmt=8, W=np.zeros((16, 256), np.float32), in_dim=256)
-    assert e.value.code == 2
+    with pytest.raises(gpu.WelvetError) as e:  # K formats: in a multiple of 256
+        mount(fmt=8, W=np.zeros((16, 128), np.float32), in_dim=128)
+    assert e.value.code == 1
+    s = mount(fmt=8, W=np.zeros((16, 256), np.float32), in_dim=256)  # quantized from fp32
+    s.close()
     with pytest.raises(gpu.WelvetError) as e:  # wrong packed length
         mount(blocks=blocks[:-1])
     assert e.value.code == 1

@@ -304,12 +304,198 @@ def test_iq4_xs_scales_and_positions(orc):
         assert np.array_equal(orc.fmt_dequant(IQ4_XS, blk, (256,)), want.astype(np.float32))
 
 
+# ---- the library's quantizers of the K and IQ4 formats (one pass: scales
+# from each sub-block's range or extreme element, integer super-block scales,
+# codes for the f16-rounded scales). Pinned by closed-form blocks that must
+# come back exactly (grid values with power-of-two scales) and by per-element
+# error bounds computed from the block's own stored scales.
+
+def _closed_form_affine(fmt, rng):
+    """x on the grid of an affine K format: y = d*ls*q - dmin*lm, with d and
+    dmin powers of two, one sub-block at ls = lm = lmax, every sub-block
+    holding the codes 0 and qmax."""
+    nsub, sub, qmax, lmax = {Q4_K: (8, 32, 15, 63), Q5_K: (8, 32, 31, 63),
+                             Q2_K: (16, 16, 3, 15)}[fmt]
+    d, dmin = 2.0 ** -6, 2.0 ** -7
+    ls = rng.integers(1, lmax + 1, nsub)
+    lm = rng.integers(0, lmax + 1, nsub)
+    j = rng.integers(0, nsub)
+    ls[j] = lm[rng.integers(0, nsub)] = lmax
+    q = rng.integers(0, qmax + 1, (nsub, sub))
+    q[:, 0], q[:, 1] = 0, qmax
+    for r in range(nsub):
+        rng.shuffle(q[r])
+    x = (d * ls[:, None] * q - dmin * lm[:, None]).astype(np.float32).ravel()
+    return x
+
+
+def _closed_form_signed(fmt, rng):
+    """x on the grid of Q3_K / Q6_K: y = d*l*q, d a power of two, one
+    sub-block at l = lmin, no l = 0, every sub-block holding the code qlo."""
+    qlo, qhi, lmin, lmax = {Q3_K: (-4, 3, -32, 31), Q6_K: (-32, 31, -128, 127)}[fmt]
+    d = 2.0 ** -9
+    l = rng.integers(lmin + 1, lmax + 1, 16)
+    l[l == 0] = 1
+    l[rng.integers(0, 16)] = lmin
+    q = rng.integers(qlo + 1, qhi + 1, (16, 16))
+    q[:, 0] = qlo
+    for r in range(16):
+        rng.shuffle(q[r])
+    return (d * l[:, None] * q).astype(np.float32).ravel()
+
+
+def _closed_form_iq4(fmt, rng):
+    table = np.array(IQ4NL_TABLE, np.float64)
+    d = 2.0 ** -10
+    if fmt == IQ4_NL:
+        idx = rng.integers(0, 16, 32)
+        idx[rng.integers(0, 32)] = 0
+        return (d * table[idx]).astype(np.float32)
+    l = rng.integers(-31, 32, 8)
+    l[l == 0] = 1
+    l[rng.integers(0, 8)] = -32
+    idx = rng.integers(0, 16, (8, 32))
+    idx[:, 0] = 0
+    for r in range(8):
+        rng.shuffle(idx[r])
+    return (d * l[:, None] * table[idx]).astype(np.float32).ravel()
+
+
 @pytest.mark.parametrize("fmt", KQUANT + IQ)
-def test_k_formats_have_no_quantizer(orc, fmt):
-    x = np.zeros(256, np.float32)
-    out = np.zeros(GEOM[fmt][1], np.uint8)
-    from oracle_lib import _f, _u8
-    assert orc.L.or_fmt_quantize(fmt, 256, _f(x), _u8(out)) == -1
+def test_k_quantizers_closed_form(orc, fmt):
+    """Values on a format's grid come back exactly, and quantizing the
+    decoded block again gives the same bytes."""
+    rng = np.random.default_rng(fmt + 900)
+    for _ in range(20):
+        if fmt in (Q2_K, Q4_K, Q5_K):
+            x = _closed_form_affine(fmt, rng)
+        elif fmt in (Q3_K, Q6_K):
+            x = _closed_form_signed(fmt, rng)
+        else:
+            x = _closed_form_iq4(fmt, rng)
+        b = orc.fmt_quantize(fmt, x)
+        y = orc.fmt_dequant(fmt, b, x.shape)
+        assert np.array_equal(y, x)
+        assert np.array_equal(orc.fmt_quantize(fmt, y), b)
+
+
+def _k_bound(fmt, x, b):
+    """Per-element error bound of one block from its stored scales: half a
+    step of the sub-block's scale (a full step on the short side of the
+    signed formats' code range), plus what the integer super-block scales
+    lose against the sub-block's exact range (the codes that clip)."""
+    f16 = lambda v: float(np.array([v], np.uint16).view(np.float16)[0])
+    g16 = lambda off: f16(int(b[off]) | (int(b[off + 1]) << 8))
+    table = np.array(IQ4NL_TABLE, np.float64)
+    x = x.astype(np.float64)
+    if fmt in (Q4_K, Q5_K, Q2_K):
+        if fmt == Q2_K:
+            nsub, sub, qmax = 16, 16, 3
+            d, dm = g16(80), g16(82)
+            ls = [int(b[j]) & 15 for j in range(16)]
+            lm = [int(b[j]) >> 4 for j in range(16)]
+        else:
+            nsub, sub, qmax = 8, 32, 15 if fmt == Q4_K else 31
+            d, dm = g16(0), g16(2)
+            sc = b[4:16]
+            ls, lm = [], []
+            for j in range(8):
+                if j < 4:
+                    ls.append(int(sc[j]) & 63), lm.append(int(sc[j + 4]) & 63)
+                else:
+                    ls.append((int(sc[j + 4]) & 15) | ((int(sc[j - 4]) >> 6) << 4))
+                    lm.append((int(sc[j + 4]) >> 4) | ((int(sc[j]) >> 6) << 4))
+        out = np.zeros(x.size)
+        for j in range(nsub):
+            v = x[sub * j:sub * (j + 1)]
+            mn = min(0.0, float(v.min()))
+            scale, off = (float(v.max()) - mn) / qmax, -mn
+            ds, dmn = d * ls[j], dm * lm[j]
+            out[sub * j:sub * (j + 1)] = 0.5 * ds + qmax * abs(scale - ds) + abs(off - dmn)
+        return out
+    if fmt in (Q3_K, Q6_K):
+        qdiv = 4.0 if fmt == Q3_K else 32.0
+        if fmt == Q3_K:
+            d = g16(108)
+            sc = b[96:108]
+            l = []
+            for s in range(16):
+                g, i = s >> 2, s & 3
+                lo = (int(sc[(g & 1) * 4 + i]) >> ((g >> 1) * 4)) & 15
+                hi = (int(sc[8 + i]) >> (2 * g)) & 3
+                l.append((lo | (hi << 4)) - 32)
+        else:
+            d = g16(208)
+            l = [int(np.int8(b[192 + s])) for s in range(16)]
+        out = np.zeros(x.size)
+        for j in range(16):
+            v = x[16 * j:16 * (j + 1)]
+            m = float(v[np.argmax(np.abs(v))])
+            s, ds = m / qdiv, d * l[j]
+            # the code range is one step shorter on the side opposite the
+            # extreme element (Q3_K: -4..3): values there may lose a full step
+            out[16 * j:16 * (j + 1)] = abs(ds) + qdiv * abs(abs(s) - abs(ds))
+        return out
+    # IQ4: the code book's largest half gap is 12 steps of the scale, and its
+    # top entry (113) is 14 steps short of the extreme (-127) on the other side
+    if fmt == IQ4_NL:
+        d = g16(0)
+        m = float(x[np.argmax(np.abs(x))])
+        return np.full(x.size, 14 * abs(d) + 127 * abs(abs(m) / 127 - abs(d)))
+    d, sh = g16(0), int(b[2]) | (int(b[3]) << 8)
+    out = np.zeros(x.size)
+    for ib in range(8):
+        ls = ((int(b[4 + ib // 2]) >> (4 * (ib & 1))) & 15) | (((sh >> (2 * ib)) & 3) << 4)
+        dl = d * (ls - 32)
+        v = x[32 * ib:32 * (ib + 1)]
+        m = float(v[np.argmax(np.abs(v))])
+        out[32 * ib:32 * (ib + 1)] = 14 * abs(dl) + 127 * abs(abs(m) / 127 - abs(dl))
+    return out
+
+
+@pytest.mark.parametrize("fmt", [Q2_K, Q4_K, Q5_K])
+def test_affine_zero_and_constant_blocks(orc, fmt):
+    """An all-zero super-block is all zero bytes (d = dmin = +0, not -0: the
+    sign bit of a stored zero is not left to how fmax orders signed zeros);
+    a constant positive block has dmin = +0 and decodes to within d of x."""
+    qk, bb = GEOM[fmt]
+    zero = np.zeros(qk, np.float32)
+    b = orc.fmt_quantize(fmt, zero)
+    assert not b.any()
+    assert not orc.fmt_dequant(fmt, b, zero.shape).view(np.uint32).any()
+    const = np.full(qk, 0.37, np.float32)
+    b = orc.fmt_quantize(fmt, const)
+    dmin = b[bb - 2:bb] if fmt == Q2_K else b[2:4]
+    assert not dmin.any()
+    y = orc.fmt_dequant(fmt, b, const.shape)
+    assert np.all(np.abs(y - const) <= 0.37 / 15)
+
+
+@pytest.mark.parametrize("fmt", KQUANT + IQ)
+def test_k_quantizer_error_bound(orc, fmt):
+    """Random rows over six orders of magnitude, constant and all-zero blocks:
+    every element within the bound of its block's stored scales."""
+    rng = np.random.default_rng(fmt + 400)
+    x = (rng.standard_normal((16, 512)) * rng.uniform(1e-3, 1e3, (16, 1))).astype(np.float32)
+    x[3] = 0.0
+    x[4] = -0.75
+    x[5, :256] = 2.5
+    x[6] = np.abs(x[6])
+    x[7] = -np.abs(x[7])
+    b = orc.fmt_quantize(fmt, x)
+    y = orc.fmt_dequant(fmt, b, x.shape).astype(np.float64)
+    qk, bb = GEOM[fmt][0], GEOM[fmt][1]
+    xb, yb, bl = x.reshape(-1, qk), y.reshape(-1, qk), b.reshape(-1, bb)
+    for i in range(xb.shape[0]):
+        bound = _k_bound(fmt, xb[i], bl[i])
+        err = np.abs(xb[i].astype(np.float64) - yb[i])
+        tol = bound * (1 + 1e-6) + 1e-30 + np.abs(xb[i]) * 2e-7
+        bad = np.flatnonzero(err > tol)
+        assert bad.size == 0, (i, bad[:4], err[bad[:4]], bound[bad[:4]])
+    # the rows' overall error stays small against their size
+    rel = np.linalg.norm(x - y) / np.linalg.norm(x)
+    assert rel < {Q2_K: 0.4, Q3_K: 0.2, Q4_K: 0.1, Q5_K: 0.05, Q6_K: 0.025, IQ4_NL: 0.1,
+                  IQ4_XS: 0.1}[fmt], rel
 
 
 @pytest.mark.parametrize("fmt", KQUANT + LEGACY + IQ)

@@ -161,6 +161,228 @@ __global__ __launch_bounds__(kThreads) void k_fmt_quantize(const float* __restri
   quantize_block<FMT>(x, out + b * G.bb);
 }
 
+// ---- the library's quantizers of the K and IQ4 formats, one thread per
+// block, reading x from memory as it goes (a super-block is 256 values).
+// One pass, as stated in oracle/formats.c (same arithmetic in the same
+// order, no contraction, so the bytes are equal):
+//  - affine (Q2_K, Q4_K, Q5_K): per sub-block scale = (max - mn) / qmax and
+//    offset = -mn, mn = min(0, min); integer scales / offsets of d = max
+//    scale / lmax and dmin = max offset / lmax; q = round((x + dmin lm) /
+//    (d ls)) with the f16-rounded d, dmin;
+//  - signed (Q3_K, Q6_K): per sub-block s = m / qdiv, m the element of largest
+//    magnitude; integer scales l = round(s / d), d = ms / ldiv; q = round(x /
+//    (d l));
+//  - IQ4_NL / IQ4_XS: the scale maps the largest-magnitude element to the code
+//    book's -127 (IQ4_XS: 6-bit integer sub-block scales of d = ms / -32); each
+//    element takes the nearest entry (the first on ties).
+__device__ __forceinline__ int clampi(int v, int lo, int hi) { return v < lo ? lo : v > hi ? hi : v; }
+__device__ __forceinline__ float f16r(float v) { return f16f(f16b(v)); }
+__device__ __forceinline__ int qround(float v, int lo, int hi) {
+#pragma clang fp contract(off)
+  return clampi((int)roundf(fminf(fmaxf(v, (float)lo), (float)hi)), lo, hi);
+}
+__device__ float signed_amax_n(const float* x, int n) {
+  float amax = 0.0f, max = 0.0f;
+  for (int j = 0; j < n; ++j) {
+    if (amax < fabsf(x[j])) {
+      amax = fabsf(x[j]);
+      max = x[j];
+    }
+  }
+  return max;
+}
+__device__ __forceinline__ void or8(uint8_t* p, int v) { *p = (uint8_t)(*p | (uint8_t)v); }
+
+__constant__ int8_t kIq4Book[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
+                                    1,    13,   25,  38,  53,  69,  89,  113};
+
+__device__ int iq4_index(float t) {
+#pragma clang fp contract(off)
+  int best = 0;
+  float err = fabsf(t - (float)kIq4Book[0]);
+  for (int k = 1; k < 16; ++k) {
+    const float e = fabsf(t - (float)kIq4Book[k]);
+    if (e < err) {
+      err = e;
+      best = k;
+    }
+  }
+  return best;
+}
+
+// Affine super-block scales: per sub-block the effective scale ds, offset dmn
+// and 1/ds; the integer scales ls, lm; d, dmin before f16 rounding.
+template <int NSUB, int SUB, int QMAX, int LMAX>
+__device__ void affine_scales(const float* x, int (&ls)[NSUB], int (&lm)[NSUB],
+                              float (&dmn)[NSUB], float (&id)[NSUB], float* d, float* dmin) {
+#pragma clang fp contract(off)
+  float scale[NSUB], off[NSUB];
+  float max_scale = 0.0f, max_off = 0.0f;
+  for (int j = 0; j < NSUB; ++j) {
+    const float* v = x + SUB * j;
+    float mn = v[0], mx = v[0];
+    for (int i = 1; i < SUB; ++i) {
+      mn = v[i] < mn ? v[i] : mn;
+      mx = v[i] > mx ? v[i] : mx;
+    }
+    // the offset is -min(min, 0); comparisons, not fmaxf, so that an all-zero
+    // or constant sub-block gives +0 (fmaxf may return either signed zero)
+    off[j] = mn < 0.0f ? -mn : 0.0f;
+    scale[j] = (mx + off[j]) / (float)QMAX;
+    if (scale[j] > max_scale) max_scale = scale[j];
+    if (off[j] > max_off) max_off = off[j];
+  }
+  const float inv_s = max_scale > 0.0f ? (float)LMAX / max_scale : 0.0f;
+  const float inv_m = max_off > 0.0f ? (float)LMAX / max_off : 0.0f;
+  *d = max_scale / (float)LMAX;
+  *dmin = max_off / (float)LMAX;
+  const float dd = f16r(*d), dm = f16r(*dmin);
+  for (int j = 0; j < NSUB; ++j) {
+    ls[j] = qround(inv_s * scale[j], 0, LMAX);
+    lm[j] = qround(inv_m * off[j], 0, LMAX);
+    const float ds = dd * (float)ls[j];
+    dmn[j] = dm * (float)lm[j];
+    id[j] = ds > 0.0f ? 1.0f / ds : 0.0f;
+  }
+}
+
+// Signed super-block scales: integer l and 1/(d l) per sub-block, d.
+template <int SUB, int LMIN, int LMAX>
+__device__ void signed_scales(const float* x, float qdiv, float ldiv, int (&l)[16],
+                              float (&is)[16], float* d) {
+#pragma clang fp contract(off)
+  float s[16];
+  for (int j = 0; j < 16; ++j) s[j] = signed_amax_n(x + SUB * j, SUB) / qdiv;
+  const float ms = signed_amax_n(s, 16);
+  *d = ms / ldiv;
+  const float idd = *d != 0.0f ? 1.0f / *d : 0.0f;
+  const float dd = f16r(*d);
+  for (int j = 0; j < 16; ++j) {
+    l[j] = qround(s[j] * idd, LMIN, LMAX);
+    const float ds = dd * (float)l[j];
+    is[j] = ds != 0.0f ? 1.0f / ds : 0.0f;
+  }
+}
+
+// 32 code-book indices of one sub-block at scale ds into qs[16]
+__device__ void iq4_sub(const float* x, float ds, uint8_t* qs) {
+#pragma clang fp contract(off)
+  const float id = ds != 0.0f ? 1.0f / ds : 0.0f;
+  for (int j = 0; j < 16; ++j)
+    qs[j] = (uint8_t)(iq4_index(x[j] * id) | (iq4_index(x[16 + j] * id) << 4));
+}
+
+template <int FMT>
+__device__ void quantize_kblock(const float* __restrict__ x, uint8_t* __restrict__ y) {
+#pragma clang fp contract(off)
+  constexpr FmtGeom G = fmt_geom(FMT);
+  for (int i = 0; i < G.bb; ++i) y[i] = 0;
+  if constexpr (FMT == kQ4_K || FMT == kQ5_K) {
+    constexpr bool K5 = FMT == kQ5_K;
+    int ls[8], lm[8];
+    float dmn[8], id[8], d, dmin;
+    affine_scales<8, 32, K5 ? 31 : 15, 63>(x, ls, lm, dmn, id, &d, &dmin);
+    st16(y, f16b(d));
+    st16(y + 2, f16b(dmin));
+    uint8_t* sc = y + 4;
+    for (int j = 0; j < 8; ++j) {
+      if (j < 4) {
+        or8(sc + j, ls[j] & 63);
+        or8(sc + j + 4, lm[j] & 63);
+      } else {
+        sc[j + 4] = (uint8_t)((ls[j] & 15) | ((lm[j] & 15) << 4));
+        or8(sc + j - 4, (ls[j] >> 4) << 6);
+        or8(sc + j, (lm[j] >> 4) << 6);
+      }
+    }
+    uint8_t* qh = y + 16;
+    uint8_t* qs = y + (K5 ? 48 : 16);
+    for (int i = 0; i < 4; ++i)
+      for (int l = 0; l < 32; ++l) {
+        const int ja = 2 * i, jb = 2 * i + 1;
+        const int a = qround((x[64 * i + l] + dmn[ja]) * id[ja], 0, K5 ? 31 : 15);
+        const int b = qround((x[64 * i + 32 + l] + dmn[jb]) * id[jb], 0, K5 ? 31 : 15);
+        qs[32 * i + l] = (uint8_t)((a & 15) | ((b & 15) << 4));
+        if constexpr (K5) or8(qh + l, ((a >> 4) << (2 * i)) | ((b >> 4) << (2 * i + 1)));
+      }
+  } else if constexpr (FMT == kQ2_K) {
+    int ls[16], lm[16];
+    float dmn[16], id[16], d, dmin;
+    affine_scales<16, 16, 3, 15>(x, ls, lm, dmn, id, &d, &dmin);
+    for (int j = 0; j < 16; ++j) y[j] = (uint8_t)(ls[j] | (lm[j] << 4));
+    for (int n = 0; n < 2; ++n)
+      for (int j = 0; j < 4; ++j)
+        for (int l = 0; l < 32; ++l) {
+          const int e = 128 * n + 32 * j + l, sb = e / 16;
+          or8(y + 16 + 32 * n + l, qround((x[e] + dmn[sb]) * id[sb], 0, 3) << (2 * j));
+        }
+    st16(y + 80, f16b(d));
+    st16(y + 82, f16b(dmin));
+  } else if constexpr (FMT == kQ3_K || FMT == kQ6_K) {
+    constexpr bool K3 = FMT == kQ3_K;
+    int l[16];
+    float is[16], d;
+    if constexpr (K3) signed_scales<16, -32, 31>(x, -4.0f, -32.0f, l, is, &d);
+    else signed_scales<16, -128, 127>(x, -32.0f, -128.0f, l, is, &d);
+    for (int n = 0; n < 2; ++n)
+      for (int t = 0; t < 4; ++t)
+        for (int i = 0; i < 32; ++i) {
+          const int e = 128 * n + 32 * t + i, sb = e / 16;
+          if constexpr (K3) {
+            const int v = qround(x[e] * is[sb], -4, 3) + 4;
+            or8(y + 32 + 32 * n + i, (v & 3) << (2 * t));
+            or8(y + i, (v >> 2) << (4 * n + t));
+          } else {
+            const int v = qround(x[e] * is[sb], -32, 31) + 32;
+            or8(y + 64 * n + 32 * (t & 1) + i, (v & 15) << (4 * (t >> 1)));
+            or8(y + 128 + 32 * n + i, (v >> 4) << (2 * t));
+          }
+        }
+    if constexpr (K3) {
+      for (int sidx = 0; sidx < 16; ++sidx) {
+        const int v = l[sidx] + 32, g = sidx >> 2, i = sidx & 3;
+        or8(y + 96 + (g & 1) * 4 + i, (v & 15) << ((g >> 1) * 4));
+        or8(y + 96 + 8 + i, (v >> 4) << (2 * g));
+      }
+      st16(y + 108, f16b(d));
+    } else {
+      for (int sidx = 0; sidx < 16; ++sidx) y[192 + sidx] = (uint8_t)(int8_t)l[sidx];
+      st16(y + 208, f16b(d));
+    }
+  } else if constexpr (FMT == kIQ4_NL) {
+    const float d = signed_amax_n(x, 32) / -127.0f;
+    st16(y, f16b(d));
+    iq4_sub(x, f16r(d), y + 2);
+  } else if constexpr (FMT == kIQ4_XS) {
+    float s[8];
+    for (int j = 0; j < 8; ++j) s[j] = signed_amax_n(x + 32 * j, 32) / -127.0f;
+    const float ms = signed_amax_n(s, 8);
+    const float d = ms / -32.0f;
+    const float idd = d != 0.0f ? 1.0f / d : 0.0f;
+    const float dd = f16r(d);
+    st16(y, f16b(d));
+    int sh = 0;
+    for (int j = 0; j < 8; ++j) {
+      const int l = qround(s[j] * idd, -32, 31);
+      const int ls = l + 32;
+      or8(y + 4 + j / 2, (ls & 15) << (4 * (j & 1)));
+      sh |= (ls >> 4) << (2 * j);
+      iq4_sub(x + 32 * j, dd * (float)l, y + 8 + 16 * j);
+    }
+    st16(y + 2, (uint16_t)sh);
+  }
+}
+
+template <int FMT>
+__global__ __launch_bounds__(kThreads) void k_fmt_quantize_k(const float* __restrict__ W,
+                                                             int64_t nblocks,
+                                                             uint8_t* __restrict__ out) {
+  constexpr FmtGeom G = fmt_geom(FMT);
+  const int64_t b = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (b >= nblocks) return;
+  quantize_kblock<FMT>(W + b * G.qk, out + b * G.bb);
+}
+
 // ---- relayout: one thread per (row, 32-element sub-block) ----------------
 template <int FMT>
 __global__ __launch_bounds__(kThreads) void k_fmt_relayout(FmtArgs a, const uint8_t* __restrict__ blocks,
@@ -825,9 +1047,14 @@ Status gemv_f(const FmtArgs& a, int batch, hipStream_t st) {
 
 template <int FMT>
 Status quantize_f(const float* W, int64_t n, uint8_t* out, hipStream_t st) {
-  const int64_t nb = n / 32;
+  constexpr FmtGeom G = fmt_geom(FMT);
+  const int64_t nb = n / G.qk;
   if (nb == 0) return Status::ok();
-  k_fmt_quantize<FMT><<<(unsigned)((nb + kThreads - 1) / kThreads), kThreads, 0, st>>>(W, nb, out);
+  const unsigned grid = (unsigned)((nb + kThreads - 1) / kThreads);
+  if constexpr (FMT == kQ8_0 || FMT == kQ4_0 || FMT == kQ4_1 || FMT == kQ5_0 || FMT == kQ5_1)
+    k_fmt_quantize<FMT><<<grid, kThreads, 0, st>>>(W, nb, out);
+  else
+    k_fmt_quantize_k<FMT><<<grid, kThreads, 0, st>>>(W, nb, out);
   return hip_status(hipGetLastError(), "format quantize launch");
 }
 
@@ -850,16 +1077,22 @@ Status dequant_f(const FmtArgs& a, int rows, float* out, hipStream_t st) {
 }  // namespace
 
 Status format_quantize(int fmt, const float* W, int64_t n, uint8_t* out, hipStream_t st) {
-  if (n % 32) return Status::err(kInvalid, "format quantize: element count");
+  const FmtGeom G = fmt_geom(fmt);
+  if (G.qk == 0 || n % G.qk) return Status::err(kInvalid, "format quantize: element count");
   switch (fmt) {
   case kQ8_0: return quantize_f<kQ8_0>(W, n, out, st);
   case kQ4_0: return quantize_f<kQ4_0>(W, n, out, st);
   case kQ4_1: return quantize_f<kQ4_1>(W, n, out, st);
   case kQ5_0: return quantize_f<kQ5_0>(W, n, out, st);
   case kQ5_1: return quantize_f<kQ5_1>(W, n, out, st);
-  default:
-    return Status::err(kUnsupported, "format quantize: only Q8_0, Q4_0, Q4_1, Q5_0 and Q5_1 "
-                                     "quantize fp32 weights; mount K formats from packed blocks");
+  case kQ2_K: return quantize_f<kQ2_K>(W, n, out, st);
+  case kQ3_K: return quantize_f<kQ3_K>(W, n, out, st);
+  case kQ4_K: return quantize_f<kQ4_K>(W, n, out, st);
+  case kQ5_K: return quantize_f<kQ5_K>(W, n, out, st);
+  case kQ6_K: return quantize_f<kQ6_K>(W, n, out, st);
+  case kIQ4_NL: return quantize_f<kIQ4_NL>(W, n, out, st);
+  case kIQ4_XS: return quantize_f<kIQ4_XS>(W, n, out, st);
+  default: return Status::err(kUnsupported, "format quantize: no quantizer for this format");
   }
 }
 

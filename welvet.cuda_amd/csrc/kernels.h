@@ -315,8 +315,10 @@ struct FmtArgs {
   bool need_epi = false;
   const double* bias = nullptr;
 };
-// Packed blocks of n row-major elements (a multiple of 32) from fp32 W
-// (device): Q8_0, Q4_0, Q4_1, Q5_0 and Q5_1 (ggml's reference quantizers).
+// Packed blocks of n row-major elements (a multiple of the format's block)
+// from fp32 W (device): Q8_0, Q4_0, Q4_1, Q5_0 and Q5_1 with ggml's
+// reference quantizers; the K and IQ4 formats with the library's one-pass
+// quantizers (formats.hip).
 Status format_quantize(int fmt, const float* W, int64_t n, uint8_t* out, hipStream_t st);
 // Packed blocks of rows x cols -> the resident arrays of a (q, h, s, e set).
 Status format_relayout(int fmt, const FmtArgs& a, const uint8_t* blocks, int rows, hipStream_t st);

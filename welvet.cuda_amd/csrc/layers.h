@@ -79,7 +79,7 @@ Status dense_build_from_store(int in, int out, int act, const WeightStore& store
                               hipStream_t st);
 
 // A Dense layer over a packed block format (QuantFormat): from fp32 W_host
-// (quantized on the device; Q8_0, Q4_0, Q4_1, Q5_0, Q5_1) or from the
+// (quantized on the device, every built format: format_quantize) or from the
 // format's packed row-major blocks (blocks_len bytes); exactly one is given.
 // in must be a multiple of the format's block (32, or 256 for the K formats).
 Status dense_build_format(int in, int out, int act, int format, const float* W_host,
