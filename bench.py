@@ -31,6 +31,9 @@ Other workloads (--config), each its own line:
 --read-floor BYTES instead times one streaming read of BYTES (default: the c2
 step's 16,826,368) over 64 rotated buffers, the same way: the floor for any
 kernel that reads those bytes once.
+--probe mfma times the scaled matrix-core instruction alone (issue rate per
+operand-format pair, 16x16x128 and 32x32x64); --probe fetch the bytes per
+cycle one CU takes from L2 (a 2 MiB region) and from HBM (4 GiB).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2]
 """
@@ -52,12 +55,14 @@ WARMUP_S = 0.2  # warmup lasts at least this long (clocks leave their idle level
 # clock when timing starts (a region that starts after an idle gap of even
 # tens of microseconds runs ~4% slower at first).
 LEAD_S = 0.01
-# dense matrix-core peaks of MI355X (TFLOP/s). The f8f6f4 instruction runs at
-# the FP8 rate when either operand is FP8, at the FP4/FP6 rate when both are
-# FP4 or FP6: FP8 weights (any activation terms) and FP4 weights with E4M3
-# terms (two- and one-term modes) use the FP8 peak; FP4 weights with the
-# default three FP6 (E2M3) terms the FP4/FP6 peak. The attention core's
-# products run on the bf16 matrix cores.
+# dense matrix-core peaks of MI355X (TFLOP/s), the published figures: FP8
+# weights (any activation terms) and FP4 weights with E4M3 terms (two- and
+# one-term modes) are rated against the FP8 peak; FP4 weights with the
+# default three FP6 (E2M3) terms against the FP4/FP6 peak. Measured issue
+# rates (--probe mfma): the 16x16x128 f8f6f4 form reaches ~4.1 PFLOP/s with
+# an FP8 operand and ~4.6 with FP4/FP6 operands only, the 32x32x64 form ~8.5
+# with FP4/FP6 operands. The attention core's products run on the bf16
+# matrix cores.
 MFMA_FP8_PEAK_TFLOPS = 5000.0
 MFMA_FP4_PEAK_TFLOPS = 10070.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
@@ -610,6 +615,77 @@ def copy_calibration(pw, nbytes, steps):
     hip.free(dst)
 
 
+MFMA_FORMATS = {0: "E4M3", 1: "E5M2", 2: "FP6 E2M3", 4: "FP4 E2M1"}
+CLOCK_GHZ = 2.4  # MI355X peak engine clock: cycles below are at this clock
+
+
+def best_ms(hip, stream, launch, reps=3):
+    """Shortest of `reps` event-timed launches, after one untimed launch."""
+    e0, e1 = hip.event(), hip.event()
+    launch()
+    hip.sync()
+    best = None
+    for _ in range(reps):
+        hip.record(e0, stream)
+        launch()
+        hip.record(e1, stream)
+        ms = hip.elapsed_ms(e0, e1)
+        best = ms if best is None else min(best, ms)
+    return best
+
+
+def probe_mfma(pw, hip):
+    """Issue rate of the scaled f8f6f4 matrix-core instruction: 2048
+    workgroups of 4 waves, each wave 1000 rounds of 8 independent 16x16x128
+    MFMAs (or 4 of 32x32x64: the same multiply-adds)."""
+    wgs, iters, simds = 2048, 1000, 1024
+    out = hip.malloc(4 * 256 * wgs)
+    stream = hip.stream()
+    rows = []
+    for fa, fb in ((0, 0), (2, 0), (2, 1), (2, 4), (4, 4)):
+        for shape in (16, 32):
+            def launch():
+                pw.check(pw.lib().welvet_mfma_probe(fa, fb, shape, iters, wgs, ctypes.c_void_p(out),
+                                                    256 * wgs, ctypes.c_void_p(stream)))
+            ms = best_ms(hip, stream, launch)
+            macs = wgs * 4 * iters * 8 * 32768
+            per_simd = wgs * 4 * iters * 8 / simds  # 16x16x128-equivalent MFMAs per SIMD
+            rows.append({"a": MFMA_FORMATS[fa], "b": MFMA_FORMATS[fb],
+                         "shape": "16x16x128" if shape == 16 else "32x32x64",
+                         "ms": round(ms, 4), "tflops": round(2 * macs / ms / 1e9, 1),
+                         "cycles_per_16x16x128": round(ms * 1e-3 * CLOCK_GHZ * 1e9 / per_simd, 1)})
+    hip.free(out)
+    print(json.dumps({"probe": "mfma_issue_rate", "clock_ghz": CLOCK_GHZ, "workgroups": wgs,
+                      "waves_per_workgroup": 4, "rows": rows}), flush=True)
+
+
+def probe_fetch(pw, hip):
+    """Bytes per cycle per CU read from an L2-resident region (2 MiB) and
+    from HBM (a 4 GiB buffer, every 64 KiB region read once per launch)."""
+    big, small, cus = 4 << 30, 2 << 20, 256
+    buf = hip.malloc(big)
+    hip.memset(buf, 1, big)
+    stream = hip.stream()
+    rows = []
+    for per_cu in (1, 4):
+        wgs = cus * per_cu
+        out = hip.malloc(4 * wgs)
+        for name, region, iters in (("l2", small, 64), ("hbm", big, (big >> 16) // wgs)):
+            def launch():
+                pw.check(pw.lib().welvet_fetch_probe(ctypes.c_void_p(buf), region, iters, wgs,
+                                                     ctypes.c_void_p(out), wgs, ctypes.c_void_p(stream)))
+            ms = best_ms(hip, stream, launch)
+            nbytes = wgs * iters * 65536
+            rows.append({"source": name, "region_bytes": region, "workgroups": wgs,
+                         "bytes": nbytes, "ms": round(ms, 4), "GB/s": round(nbytes / ms / 1e6, 1),
+                         "bytes_per_cycle_per_cu": round(nbytes / (ms * 1e-3) / cus / (CLOCK_GHZ * 1e9), 2)})
+        hip.free(out)
+    hip.free(buf)
+    print(json.dumps({"probe": "fetch_rate", "clock_ghz": CLOCK_GHZ, "cus": cus,
+                      "loads": "16-byte, 4 per lane in flight, 256-lane workgroups", "rows": rows}),
+          flush=True)
+
+
 def read_floor_workload(pw, hip, nbytes, copies):
     """One streaming read of nbytes per step over `copies` rotated buffers."""
     bufs = [hip.malloc(nbytes) for _ in range(copies)]
@@ -741,6 +817,9 @@ def main():
                     metavar="BYTES",
                     help="time a plain streaming read of BYTES (default: the c2 step's bytes) "
                          "instead of a workload")
+    ap.add_argument("--probe", choices=("mfma", "fetch"), default=None,
+                    help="only run a hardware probe: the scaled MFMA issue rate or the per-CU "
+                         "fetch rate from L2 and HBM")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU; --gpus above 1 is not part of it",
@@ -755,6 +834,9 @@ def main():
 
     pw.check(pw.lib().welvet_cuda_init())
     hip = pw.Hip()
+    if args.probe:
+        (probe_mfma if args.probe == "mfma" else probe_fetch)(pw, hip)
+        return
     if args.read_floor:
         wl = read_floor_workload(pw, hip, args.read_floor, max(1, args.copies))
         gemv = True

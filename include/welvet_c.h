@@ -279,6 +279,27 @@ WELVET_API welvet_status welvet_read_probe(const void* buf, size_t bytes, uint32
                                            size_t out_cap, void* stream);
 WELVET_API size_t welvet_read_probe_words(size_t bytes);
 
+/* Measurement extension, no reference counterpart: `workgroups` workgroups
+ * of 256 lanes each read `iters` 64 KiB regions of buf[0, region_bytes)
+ * (region_bytes a positive multiple of 65536) with 16-byte loads, queued on
+ * `stream`; out_words (device, out_cap >= workgroups) receives one digest
+ * per workgroup. A region of a few MiB stays in L2 and one of GiB streams
+ * from HBM: bytes / time / CUs is the fetch rate of one CU from either. */
+WELVET_API welvet_status welvet_fetch_probe(const void* buf, size_t region_bytes, int32_t iters,
+                                            int32_t workgroups, uint32_t* out_words,
+                                            size_t out_cap, void* stream);
+
+/* Measurement extension, no reference counterpart: `workgroups` workgroups
+ * of 4 waves each issue iters x 8 (shape 16: v_mfma_scale_f32_16x16x128_f8f6f4)
+ * or iters x 4 (shape 32: the 32x32x64 form) independent scaled MFMAs with
+ * operand formats fmt_a x fmt_b (0 E4M3, 1 E5M2, 2 FP6 E2M3, 4 FP4; built
+ * pairs: 0x0, 2x0, 2x1, 2x4, 4x4, others code 2), queued on `stream`; out
+ * (device, out_cap >= 256 * workgroups floats) receives the sums. The time
+ * gives the instruction's issue rate per SIMD. */
+WELVET_API welvet_status welvet_mfma_probe(int32_t fmt_a, int32_t fmt_b, int32_t shape,
+                                           int32_t iters, int32_t workgroups, float* out,
+                                           size_t out_cap, void* stream);
+
 /* Measurement extension, no reference counterpart: a one-lane kernel queued
  * on `stream` (null: the default stream) writes the device's constant-rate
  * wall clock to *out (device memory). Two stamps captured into one graph

@@ -104,6 +104,29 @@ welvet_status welvet_read_probe(const void* buf, size_t bytes, uint32_t* out_wor
 
 size_t welvet_read_probe_words(size_t bytes) { return wv::read_probe_words(bytes); }
 
+welvet_status welvet_fetch_probe(const void* buf, size_t region_bytes, int32_t iters,
+                                 int32_t workgroups, uint32_t* out_words, size_t out_cap,
+                                 void* stream) {
+  if (!buf || !out_words) return invalid("fetch probe: null buffer");
+  if (workgroups > 0 && out_cap < (size_t)workgroups) return invalid("fetch probe: output too small");
+  return guarded([&]() -> Status {
+    WV_TRY(wv::init_device());
+    return wv::launch_fetch_probe(static_cast<const uint8_t*>(buf), region_bytes, iters, workgroups,
+                                  out_words, static_cast<hipStream_t>(stream));
+  });
+}
+
+welvet_status welvet_mfma_probe(int32_t fmt_a, int32_t fmt_b, int32_t shape, int32_t iters,
+                                int32_t workgroups, float* out, size_t out_cap, void* stream) {
+  if (!out) return invalid("mfma probe: null output");
+  if (workgroups > 0 && out_cap < (size_t)workgroups * 256) return invalid("mfma probe: output too small");
+  return guarded([&]() -> Status {
+    WV_TRY(wv::init_device());
+    return wv::launch_mfma_probe(fmt_a, fmt_b, shape, iters, workgroups, out,
+                                 static_cast<hipStream_t>(stream));
+  });
+}
+
 welvet_status welvet_clock_stamp(uint64_t* out, void* stream) {
   if (!out) return invalid("clock stamp: null output");
   return guarded([&]() -> Status {

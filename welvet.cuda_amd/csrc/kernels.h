@@ -65,6 +65,15 @@ size_t read_probe_words(size_t bytes);
 Status launch_read_probe(const uint8_t* buf, size_t bytes, uint32_t* out, hipStream_t st);
 // the device wall clock into *out (one lane of one workgroup)
 Status launch_clock_stamp(uint64_t* out, hipStream_t st);
+// `workgroups` workgroups of 256 lanes each read `iters` 64 KiB regions of
+// buf[0, region_bytes); out: one word per workgroup
+Status launch_fetch_probe(const uint8_t* buf, size_t region_bytes, int iters, int workgroups,
+                          uint32_t* out, hipStream_t st);
+// `workgroups` workgroups of 4 waves each issue iters x 8 (shape 16) or x 4
+// (shape 32) scaled MFMAs with operand formats fmt_a / fmt_b (0 E4M3, 1
+// E5M2, 2 FP6 E2M3, 4 FP4); out: workgroups x 256 floats
+Status launch_mfma_probe(int fmt_a, int fmt_b, int shape, int iters, int workgroups, float* out,
+                         hipStream_t st);
 
 // ---- small-batch GEMV (gemv.hip) ----
 struct GemvArgs {

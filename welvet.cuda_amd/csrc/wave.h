@@ -48,25 +48,28 @@ __device__ __forceinline__ void fold(float* v, int lane) {
 
 template <int R>
 constexpr int log2c() {
-  return R >= 16 ? 4 : R >= 8 ? 3 : R >= 4 ? 2 : R >= 2 ? 1 : 0;
+  return R >= 32 ? 5 : R >= 16 ? 4 : R >= 8 ? 3 : R >= 4 ? 2 : R >= 2 ? 1 : 0;
 }
 
-// Reduces v[0..R) over the 64 lanes with a transposing butterfly (R/2 + R/4
+// Reduces v[0..R) (R <= 32) over the 64 lanes with a transposing butterfly (R/2 + R/4
 // + ... exchanges instead of 6 per row), folding the low lane bits first so
 // the multi-value steps are DPP moves. Afterwards lanes 0..R-1 hold in v[0]
 // the totals of rows reduced_row<R>(lane).
 template <int R>
 __device__ __forceinline__ void wave_reduce_rows(float* v, int lane) {
   constexpr int L = log2c<R>();
-  if constexpr (L >= 4) fold<16, 1>(v, lane);
-  if constexpr (L >= 3) fold<8, (L >= 4 ? 2 : 1)>(v, lane);
+  // fold j halves the values over lane bit j: 2^L values -> 1
+  if constexpr (L >= 5) fold<32, 1>(v, lane);
+  if constexpr (L >= 4) fold<16, (1 << (L - 4))>(v, lane);
+  if constexpr (L >= 3) fold<8, (1 << (L - 3))>(v, lane);
   if constexpr (L >= 2) fold<4, (1 << (L - 2))>(v, lane);
   if constexpr (L >= 1) fold<2, (1 << (L - 1))>(v, lane);
+  // the lane bits above the folded ones: plain sums
   if constexpr (L < 1) v[0] += xor_lane<1>(v[0], lane);
   if constexpr (L < 2) v[0] += xor_lane<2>(v[0], lane);
   if constexpr (L < 3) v[0] += xor_lane<4>(v[0], lane);
   if constexpr (L < 4) v[0] += xor_lane<8>(v[0], lane);
-  v[0] += xor_lane<16>(v[0], lane);
+  if constexpr (L < 5) v[0] += xor_lane<16>(v[0], lane);
   v[0] += xor_lane<32>(v[0], lane);
 }
 

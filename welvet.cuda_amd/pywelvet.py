@@ -143,6 +143,8 @@ def lib():
     _sig(L, "welvet_codec_sweep", Status, [_i32, _u32, _u32, _i64p])
     _sig(L, "welvet_read_probe", Status, [_vp, _sz, _vp, _sz, _vp])
     _sig(L, "welvet_read_probe_words", _sz, [_sz])
+    _sig(L, "welvet_fetch_probe", Status, [_vp, _sz, _i32, _i32, _vp, _sz, _vp])
+    _sig(L, "welvet_mfma_probe", Status, [_i32, _i32, _i32, _i32, _i32, _vp, _sz, _vp])
     _sig(L, "welvet_clock_stamp", Status, [_vp, _vp])
     _sig(L, "welvet_clock_rate_khz", ctypes.c_int64, [])
     _sig(L, "welvet_seqmix_kind_name", Status, [_i32, ctypes.c_char_p, _i32])
