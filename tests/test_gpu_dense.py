@@ -64,9 +64,9 @@ def test_release_smoke_known_answer(gpu):
 ])
 def test_integer_exact_bit_for_bit(gpu, oracle, dt, values):
     rng = np.random.default_rng(dt)
-    # 12588 and 24876 columns: 13 chunks of 1 KiB per wave for FP8 and FP4,
-    # so the waves take chunks two at a time and the ragged last chunk is
-    # the second of a pair
+    # 12588 and 24876 columns: 25 chunks (512 FP8 or 1024 FP4 elements each)
+    # over 4 waves, so every wave takes several and the ragged last chunk is
+    # the seventh of wave 0
     for rows, cols, batch in [(129, 1000, 1), (64, 4096, 1), (5, 77, 3), (9, 300, 9), (24, 9300, 1),
                               (40, 301, 9), (130, 4096, 40), (24, 12588, 1), (16, 24876, 2),
                               (8, 16384, 1)]:
@@ -80,12 +80,14 @@ def test_integer_exact_bit_for_bit(gpu, oracle, dt, values):
 
 @pytest.mark.parametrize("dt", [4, 16])
 @pytest.mark.parametrize("scheme", [2, 3])
-@pytest.mark.parametrize("rows,cols", [(70, 3000), (40, 5000), (24, 8000), (16, 9300),
-                                       (24, 12588), (16, 24876)])
+@pytest.mark.parametrize("rows,cols", [(70, 1000), (70, 2000), (70, 3000), (40, 4000),
+                                       (40, 5000), (24, 8000), (16, 9300), (24, 12588),
+                                       (16, 24876)])
 def test_gemv_k_split_over_waves(gpu, oracle, dt, scheme, rows, cols):
-    """Batch-1 GEMV whose K axis spans 2-25 chunks of 1 KiB per wave (FP8: 3, 5,
-    8, 10, 13, 25; FP4: 2, 3, 4, 5, 7, 13), so groups of 2, 3, 4, 6 and 8 waves
-    split it, and waves with more than one chunk take them in pairs."""
+    """Batch-1 GEMV whose K axis spans 1-49 chunks of 64 lanes x 8 bytes (FP8:
+    2, 4, 6, 8, 10, 16, 19, 25, 49; FP4: 1, 2, 3, 4, 5, 8, 10, 13, 25), so groups
+    of 1, 2, 3, 4, 6 and 8 waves split it, and waves of 4-wave groups take
+    several chunks, the last one ragged where cols is not a multiple of it."""
     rng = np.random.default_rng(rows * cols + dt + scheme)
     W = rng.standard_normal((rows, cols)).astype(np.float32) / np.sqrt(cols)
     x = rng.standard_normal((1, cols)).astype(np.float32)

@@ -1,10 +1,13 @@
 // Quantized-weight GEMV for small batches (the HBM-streaming path).
 //
-// One workgroup = 4 waves owns R consecutive weight rows. The K axis is cut
-// into 1 KiB-per-wave chunks (64 lanes x 16 bytes: 16 FP8 or 32 FP4 codes per
-// lane); waves take chunks round-robin. Each lane keeps its slice of x in
-// registers and applies it to all R rows, so x is read once per R rows while
-// the weights stream with one 128-bit load per lane per row. Codes are
+// One workgroup of W waves owns R consecutive weight rows. The K axis is cut
+// into chunks of 64 lanes x KB bytes per row (KB 16: 16 FP8 or 32 FP4 codes
+// per lane, 1 KiB per wave and row; KB 8: half that); waves take chunks
+// round-robin. Each lane keeps its slice of x in registers and applies it to
+// all R rows, so x is read once per R rows while the weights stream with one
+// KB-byte load per lane per row. All of a chunk's loads are in flight before
+// any is used, so the decode and FMAs of a wave's last chunk run after its
+// last bytes arrive: half-width chunks (twice the waves) halve that tail. Codes are
 // decoded in registers by the gfx950 conversion instructions (valid because
 // the device copy is canonical, see codec.h) and accumulated in fp32. The R
 // partial sums per lane are folded across the wave with a transposing
@@ -25,9 +28,25 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 // Streaming weight load: non-temporal, so the 16-byte lines do not displace
 // x and other reused data from the caches.
-__device__ __forceinline__ uint4 load_stream(const uint8_t* p) {
-  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
-  return make_uint4(v.x, v.y, v.z, v.w);
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+// KB bytes of codes per lane: KB / 4 words
+template <int KB>
+struct Words {
+  uint32_t w[KB / 4];
+};
+template <int KB>
+__device__ __forceinline__ Words<KB> load_stream(const uint8_t* p) {
+  Words<KB> r;
+  if constexpr (KB == 16) {
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    r.w[0] = v.x, r.w[1] = v.y, r.w[2] = v.z, r.w[3] = v.w;
+  } else {
+    static_assert(KB == 8, "8 or 16 bytes per lane");
+    const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+    r.w[0] = v.x, r.w[1] = v.y;
+  }
+  return r;
 }
 
 typedef float v2f __attribute__((ext_vector_type(2)));
@@ -36,20 +55,20 @@ typedef float v2f __attribute__((ext_vector_type(2)));
 typedef const float __attribute__((address_space(4)))* ConstF32;
 
 
-// Elements per lane per 16-byte chunk.
-template <int DT>
+// Elements per lane per chunk of KB bytes.
+template <int DT, int KB>
 struct Codec {
-  static constexpr int KS = DT == kFP4 ? 32 : 16;
+  static constexpr int KS = DT == kFP4 ? 2 * KB : KB;
 };
 
-// Decodes the 16 bytes of q and accumulates sum(dec * xv) into acc.
-template <int DT>
-__device__ __forceinline__ float dot_chunk(const uint4 q, const float* xv) {
-  const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+// Decodes the KB bytes of q and returns sum(dec * xv).
+template <int DT, int KB>
+__device__ __forceinline__ float dot_chunk(const Words<KB>& q, const float* xv) {
+  const uint32_t* w = q.w;
   float s0 = 0.0f, s1 = 0.0f;
   if constexpr (DT == kFP4) {
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
+    for (int d = 0; d < KB / 4; ++d) {
       const v2f v0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[d], 1.0f, 0);
       const v2f v1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[d], 1.0f, 1);
       const v2f v2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[d], 1.0f, 2);
@@ -65,7 +84,7 @@ __device__ __forceinline__ float dot_chunk(const uint4 q, const float* xv) {
     }
   } else {
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
+    for (int d = 0; d < KB / 4; ++d) {
       v2f lo, hi;
       if constexpr (DT == kE4M3) {
         lo = __builtin_amdgcn_cvt_pk_f32_fp8(w[d], false);
@@ -83,18 +102,19 @@ __device__ __forceinline__ float dot_chunk(const uint4 q, const float* xv) {
   return s0 + s1;
 }
 
-// One 1 KiB-per-wave chunk c of K: loads first (x slice, then the weight rows
-// and block exponents), all in flight before any of them is used, then the
-// decode and FMAs into acc. With CLAMP, x reads past cols are clamped to the
-// last element and zeroed after the loads (the codes there are zero).
-template <int DT, bool BLK, int R, int MATS, bool VECX, bool CLAMP>
+// One chunk c of K (64 lanes x KB bytes per row): loads first (x slice, then
+// the weight rows and block exponents), all in flight before any of them is
+// used, then the decode and FMAs into acc. With CLAMP, x reads past cols are
+// clamped to the last element and zeroed after the loads (the codes there
+// are zero).
+template <int DT, bool BLK, int R, int MATS, bool VECX, bool CLAMP, int KB>
 __device__ __forceinline__ void gemv_chunk(int c, int lane, int cols, const float* __restrict__ x,
                                            const uint8_t* __restrict__ w0,
                                            const uint8_t* __restrict__ w1,
                                            const uint8_t* __restrict__ e0,
                                            const uint8_t* __restrict__ e1, uint32_t pitch,
                                            uint32_t nblk, float (&acc)[MATS][R]) {
-  constexpr int KS = Codec<DT>::KS;
+  constexpr int KS = Codec<DT, KB>::KS;
   const int k0 = c * 64 * KS + lane * KS;
   float xr[KS];
   if constexpr (VECX) {
@@ -110,14 +130,14 @@ __device__ __forceinline__ void gemv_chunk(int c, int lane, int cols, const floa
   }
   // 32-bit offsets from the wave-uniform row-group bases: one add per row
   // and loads addressed as scalar base + vector offset
-  const uint32_t boff = (uint32_t)c * 1024u + (uint32_t)lane * 16u;
+  const uint32_t boff = (uint32_t)c * (64u * KB) + (uint32_t)lane * KB;
   const uint32_t eoff = (uint32_t)k0 >> 5;
-  uint4 q[MATS][R];
+  Words<KB> q[MATS][R];
   uint8_t e[MATS][R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    q[0][r] = load_stream(w0 + (r * pitch + boff));
-    if constexpr (MATS == 2) q[1][r] = load_stream(w1 + (r * pitch + boff));
+    q[0][r] = load_stream<KB>(w0 + (r * pitch + boff));
+    if constexpr (MATS == 2) q[1][r] = load_stream<KB>(w1 + (r * pitch + boff));
     if constexpr (BLK) {
       e[0][r] = e0[r * nblk + eoff];
       if constexpr (MATS == 2) e[1][r] = e1[r * nblk + eoff];
@@ -131,7 +151,7 @@ __device__ __forceinline__ void gemv_chunk(int c, int lane, int cols, const floa
   for (int m = 0; m < MATS; ++m) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const float p = dot_chunk<DT>(q[m][r], xv);
+      const float p = dot_chunk<DT, KB>(q[m][r], xv);
       if constexpr (BLK) acc[m][r] = fmaf(p, pow2f((int)e[m][r] - 127), acc[m][r]);
       else acc[m][r] += p;
     }
@@ -140,9 +160,9 @@ __device__ __forceinline__ void gemv_chunk(int c, int lane, int cols, const floa
 
 // MATS = 1: y = W x with the Dense epilogue into pre/post.
 // MATS = 2: g = Wg x, u = Wu x, pre = h = f32(f64(f32(SiLU(g))) * f64(u)).
-template <int DT, bool BLK, int R, int MATS, bool VECX, int WAVES>
+template <int DT, bool BLK, int R, int MATS, bool VECX, int WAVES, int KB>
 __global__ __launch_bounds__(64 * WAVES) void k_gemv(GemvArgs a) {
-  constexpr int KS = Codec<DT>::KS;
+  constexpr int KS = Codec<DT, KB>::KS;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int r0 = blockIdx.x * R;
@@ -183,9 +203,9 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemv(GemvArgs a) {
     // Chunks wholly inside cols (all but a ragged last one) read x without
     // clamps or selects; the test is wave-uniform.
     if ((c + 1) * 64 * KS <= cols) {
-      gemv_chunk<DT, BLK, R, MATS, VECX, false>(c, lane, cols, x, w0, w1, e0, e1, pitch, nblk, acc);
+      gemv_chunk<DT, BLK, R, MATS, VECX, false, KB>(c, lane, cols, x, w0, w1, e0, e1, pitch, nblk, acc);
     } else if (c * 64 * KS + lane * KS < kpad) {
-      gemv_chunk<DT, BLK, R, MATS, VECX, true>(c, lane, cols, x, w0, w1, e0, e1, pitch, nblk, acc);
+      gemv_chunk<DT, BLK, R, MATS, VECX, true, KB>(c, lane, cols, x, w0, w1, e0, e1, pitch, nblk, acc);
     }
   }
 
@@ -231,13 +251,19 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemv(GemvArgs a) {
   }
 }
 
+// Bytes per lane per row and chunk. Measured against 16 (1 KiB per wave and
+// row): 4096 x 4096 E4M3 5.04 -> 4.88 us, the 11008 x 4096 FP4 gate+up pair
+// 12.2 -> 11.7 us, 4096 x 11008 FP4 8.08 -> 7.53 us.
+constexpr int kChunkLaneBytes = 8;
+
 template <int DT, bool BLK, int R, int MATS, int WAVES>
 Status launch_t(const GemvArgs& a, int batch, hipStream_t st) {
   const bool vecx = (a.cols % 4 == 0) && (a.x_stride % 4 == 0) &&
                     ((reinterpret_cast<uintptr_t>(a.x) & 15u) == 0);
   dim3 grid((a.rows + R - 1) / R, batch);
-  if (vecx) k_gemv<DT, BLK, R, MATS, true, WAVES><<<grid, 64 * WAVES, 0, st>>>(a);
-  else k_gemv<DT, BLK, R, MATS, false, WAVES><<<grid, 64 * WAVES, 0, st>>>(a);
+  constexpr int KB = kChunkLaneBytes;
+  if (vecx) k_gemv<DT, BLK, R, MATS, true, WAVES, KB><<<grid, 64 * WAVES, 0, st>>>(a);
+  else k_gemv<DT, BLK, R, MATS, false, WAVES, KB><<<grid, 64 * WAVES, 0, st>>>(a);
   return hip_status(hipGetLastError(), "gemv launch");
 }
 
@@ -277,17 +303,14 @@ Status launch_m(const GemvArgs& a, int dtype, bool blk, int batch, GemvTile t, h
 }  // namespace
 
 GemvTile gemv_tile(int dtype, int kpad, int rows, int mats, int cus) {
-  // K chunks of 1 KiB per wave. Waves per group: one per chunk up to 8
-  // chunks (5 -> 6, 7 -> 8), so no wave streams two chunks while another
-  // idles; 4 beyond that. Then rows per group so that the grid has >= 8
-  // waves per CU when it can (8 rows with 3, 6 or 8 waves).
-  const int ks = dtype == kFP4 ? 32 : 16;
+  // K chunks of 64 lanes x kChunkLaneBytes. Waves per group: one per chunk up
+  // to 8 chunks (5 -> 6, 7 -> 8), so no wave streams two chunks while
+  // another idles; 4 beyond that. Then rows per group so that the grid has
+  // >= 8 waves per CU when it can (8 rows with 3, 6 or 8 waves).
+  const int ks = dtype == kFP4 ? 2 * kChunkLaneBytes : kChunkLaneBytes;
   const int chunks = (kpad + 64 * ks - 1) / (64 * ks);
   GemvTile t;
   t.waves = chunks <= 4 ? chunks : chunks <= 6 ? 6 : chunks <= 8 ? 8 : 4;
-  // FP4 with 5-6 chunks (the 11008-wide SwiGLU down projection): 3 waves of
-  // two chunks each measured 7.8 us against 8.5 us for 6 waves of one
-  if (dtype == kFP4 && (chunks == 5 || chunks == 6)) t.waves = 3;
   if (t.waves == 3 || t.waves >= 6) {
     t.rows = 8;
     return t;
