@@ -69,6 +69,27 @@ def test_swiglu_fp4_small_batch_ragged(gpu, oracle, scheme, rows, d, inter):
     assert rel_l2(y, oy) <= tol(rows, chain=2)
 
 
+@pytest.mark.parametrize("dt,scheme", [(16, 3), (4, 2), (5, 1)])
+@pytest.mark.parametrize("rows,d,inter", [(16, 1024, 4100), (24, 1024, 4100), (32, 2000, 8200),
+                                          (9, 4096, 4096)])
+def test_swiglu_gate_up_whole_k_workgroups(gpu, oracle, dt, scheme, rows, d, inter):
+    """The 5-32-row gate+up pair on the path without a K split (16 weight rows
+    per workgroup over all of K, at least 256 workgroups: inter > 4080 and
+    d >= 1024): one and two activation row blocks, a ragged row count of the
+    grid's last block (4100, 8200), ragged K (2000), FP4 and FP8 weights."""
+    rng = np.random.default_rng(rows + d + inter + dt)
+    G = (rng.standard_normal((inter, d)) / np.sqrt(d)).astype(np.float32)
+    U = (rng.standard_normal((inter, d)) / np.sqrt(d)).astype(np.float32)
+    D = (rng.standard_normal((d, inter)) / np.sqrt(inter)).astype(np.float32)
+    x = rng.standard_normal((rows, d)).astype(np.float32)
+    s = gpu.SwiGLUSession(rows, 1, d, inter, dt, scheme, G, U, D)
+    h, y = s.execute(x)
+    s.close()
+    oh, oy = oracle_swiglu(oracle, dt, scheme, G, U, D, x)
+    assert rel_l2(h, oh) <= tol(rows)
+    assert rel_l2(y, oy) <= tol(rows, chain=2)
+
+
 def test_c3_swiglu_fp4_block32_batch1(gpu, oracle):
     """SwiGLU d_model 4096, d_ff 11008, FP4 E2M1 + E8M0 per 32 along K, batch 1."""
     import pywelvet as pw
