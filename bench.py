@@ -35,6 +35,10 @@ kernel that reads those bytes once.
 operand-format pair, 16x16x128 and 32x32x64); --probe fetch the bytes per
 cycle one CU takes from L2 (a 2 MiB region) and from HBM (4 GiB).
 
+The default line (c2) also carries "gemm": the c4 and c5 GEMM workloads timed
+the same way in the same run (64 steps each, three FP6 activation terms), with
+their useful TFLOP/s against the matrix-core peak (--no-gemm leaves them out).
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2]
 """
 import argparse
@@ -792,66 +796,15 @@ class Runner:
         self.graphs = {}
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=None,
-                    help="timed steps (default: 1280 for the GEMV workloads, 64 for the rest)")
-    ap.add_argument("--warmup", type=int, default=None,
-                    help="untimed warmup steps; the warmup also lasts at least WARMUP_S seconds")
-    ap.add_argument("--config", default="c2", choices=CONFIGS)
-    ap.add_argument("--copies", type=int, default=64)
-    ap.add_argument("--batch", type=int, default=1,
-                    help="batch rows of the packed-format GEMV configs (gemv_<fmt>)")
-    ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--terms", type=int, default=3, choices=(1, 2, 3),
-                    help="activation terms of the matrix-core GEMMs (c4, c4mha, c5, c5chain): "
-                         "3 (default), 2 (backend bit 16) or 1 (backend bit 32: the throughput mode, "
-                         "outside the 1e-3 bound)")
-    ap.add_argument("--keep-inner", action="store_true",
-                    help="c5: also write the fp32 outputs of each cell's first two layers")
-    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
-                    help="only run device-to-device copies of MIB MiB (the known-size copy "
-                         "that scales the FETCH_SIZE/WRITE_SIZE counters) and exit")
-    ap.add_argument("--read-floor", type=int, nargs="?", const=C2_BYTES, default=0,
-                    metavar="BYTES",
-                    help="time a plain streaming read of BYTES (default: the c2 step's bytes) "
-                         "instead of a workload")
-    ap.add_argument("--probe", choices=("mfma", "fetch"), default=None,
-                    help="only run a hardware probe: the scaled MFMA issue rate or the per-CU "
-                         "fetch rate from L2 and HBM")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print("bench.py: this build measures one GPU; --gpus above 1 is not part of it",
-              file=sys.stderr)
-        sys.exit(2)
-
-    import pywelvet as pw
-
-    if args.copy_calibration:
-        copy_calibration(pw, args.copy_calibration << 20, args.steps or 10)
-        return
-
-    pw.check(pw.lib().welvet_cuda_init())
-    hip = pw.Hip()
-    if args.probe:
-        (probe_mfma if args.probe == "mfma" else probe_fetch)(pw, hip)
-        return
-    if args.read_floor:
-        wl = read_floor_workload(pw, hip, args.read_floor, max(1, args.copies))
-        gemv = True
-    else:
-        wl = make_workload(pw, hip, args.config, max(1, args.copies), args.terms, args.batch,
-                           args.keep_inner)
-        gemv = args.config in ("c1", "c2", "c3", "c3b16")
-    steps = args.steps if args.steps is not None else (1280 if gemv else 64)
-    steps = max(1, steps)
+def measure(pw, hip, wl, steps, want):
+    """Warmup, then REPEATS timed regions of exactly `steps` steps of wl; the
+    median region time in ms (less the clock stamps' own cost), all regions,
+    the warmup steps run and the Runner (still holding the graphs)."""
     stream = hip.stream()
     runner = Runner(pw, hip, wl, stream)
 
     # warmup: at least the requested steps and at least WARMUP_S seconds, in
     # whole rotations (the clocks start from their idle level)
-    want = args.warmup if args.warmup is not None else 0
     runner.prepare(runner.per)
     warmup, t0 = 0, time.perf_counter()
     while warmup < want or time.perf_counter() - t0 < WARMUP_S:
@@ -915,8 +868,93 @@ def main():
             t = hip.download(stamps, (2,), np.uint64)
             runs.append(float(int(t[1]) - int(t[0])) / khz - stamp_ms)
     hip.free(stamps)
-    t_wall /= REPEATS
-    ms = sorted(runs)[len(runs) // 2]
+    return {"runner": runner, "warmup": warmup, "runs": runs, "ms": sorted(runs)[len(runs) // 2],
+            "stamp_ms": stamp_ms, "lead": lead, "t_wall": t_wall / REPEATS}
+
+
+# The GEMM half of the metric, measured in the same run as the default GEMV
+# line: the MHA projection GEMM and the 64-cell volume, three FP6 activation
+# terms (the defaults).
+GEMM_LINE = ("c4", "c5")
+
+
+def gemm_summary(pw, hip, config, copies):
+    wl = make_workload(pw, hip, config, copies)
+    try:
+        steps = 64
+        m = measure(pw, hip, wl, steps, 0)
+        m["runner"].close()
+    finally:
+        wl["close"]()
+    per_step_s = m["ms"] * 1e-3 / steps
+    tflops = wl["flops"] / per_step_s / 1e12
+    peak = wl.get("peak_tflops", MFMA_FP8_PEAK_TFLOPS)
+    return {"workload": wl["config"]["workload"], "ms_per_step": round(m["ms"] / steps, 6),
+            "tflops": round(tflops, 2), "peak_tflops": round(peak, 1),
+            "frac": round(tflops / peak, 4), "dtype": wl["dtype"], "activation_terms": 3,
+            "steps": steps, "ms_runs": [round(r, 4) for r in m["runs"]]}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=None,
+                    help="timed steps (default: 1280 for the GEMV workloads, 64 for the rest)")
+    ap.add_argument("--warmup", type=int, default=None,
+                    help="untimed warmup steps; the warmup also lasts at least WARMUP_S seconds")
+    ap.add_argument("--config", default="c2", choices=CONFIGS)
+    ap.add_argument("--copies", type=int, default=64)
+    ap.add_argument("--batch", type=int, default=1,
+                    help="batch rows of the packed-format GEMV configs (gemv_<fmt>)")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--terms", type=int, default=3, choices=(1, 2, 3),
+                    help="activation terms of the matrix-core GEMMs (c4, c4mha, c5, c5chain): "
+                         "3 (default), 2 (backend bit 16) or 1 (backend bit 32: the throughput mode, "
+                         "outside the 1e-3 bound)")
+    ap.add_argument("--keep-inner", action="store_true",
+                    help="c5: also write the fp32 outputs of each cell's first two layers")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run device-to-device copies of MIB MiB (the known-size copy "
+                         "that scales the FETCH_SIZE/WRITE_SIZE counters) and exit")
+    ap.add_argument("--read-floor", type=int, nargs="?", const=C2_BYTES, default=0,
+                    metavar="BYTES",
+                    help="time a plain streaming read of BYTES (default: the c2 step's bytes) "
+                         "instead of a workload")
+    ap.add_argument("--no-gemm", action="store_true",
+                    help="c2: leave out the GEMM workloads (c4, c5) that the default line also times")
+    ap.add_argument("--probe", choices=("mfma", "fetch"), default=None,
+                    help="only run a hardware probe: the scaled MFMA issue rate or the per-CU "
+                         "fetch rate from L2 and HBM")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this build measures one GPU; --gpus above 1 is not part of it",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import pywelvet as pw
+
+    if args.copy_calibration:
+        copy_calibration(pw, args.copy_calibration << 20, args.steps or 10)
+        return
+
+    pw.check(pw.lib().welvet_cuda_init())
+    hip = pw.Hip()
+    if args.probe:
+        (probe_mfma if args.probe == "mfma" else probe_fetch)(pw, hip)
+        return
+    if args.read_floor:
+        wl = read_floor_workload(pw, hip, args.read_floor, max(1, args.copies))
+        gemv = True
+    else:
+        wl = make_workload(pw, hip, args.config, max(1, args.copies), args.terms, args.batch,
+                           args.keep_inner)
+        gemv = args.config in ("c1", "c2", "c3", "c3b16")
+    steps = args.steps if args.steps is not None else (1280 if gemv else 64)
+    steps = max(1, steps)
+    want = args.warmup if args.warmup is not None else 0
+    m = measure(pw, hip, wl, steps, want)
+    runner, warmup, runs, ms = m["runner"], m["warmup"], m["runs"], m["ms"]
+    stamp_ms, lead, t_wall = m["stamp_ms"], m["lead"], m["t_wall"]
     per_step_s = ms * 1e-3 / steps
 
     tflops = wl["flops"] / per_step_s / 1e12
@@ -969,9 +1007,13 @@ def main():
         "roofline": roof,
         "cpu_baseline": cpu,
     }
-    print(json.dumps(line), flush=True)
     runner.close()
     wl["close"]()
+    if args.config == "c2" and not args.read_floor and not args.no_gemm:
+        # the GEMM half of the metric, same process and device (after the
+        # GEMV's buffers are freed)
+        line["gemm"] = [gemm_summary(pw, hip, c, max(1, args.copies)) for c in GEMM_LINE]
+    print(json.dumps(line), flush=True)
 
 
 if __name__ == "__main__":
