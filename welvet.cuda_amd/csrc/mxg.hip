@@ -1121,6 +1121,7 @@ __global__ __launch_bounds__(64 * W) void k_mxr(MxgArgs p) {
   const int S = p.kpad / 128;
   const int k0 = S * wave / W, KR = S * (wave + 1) / W - k0;  // 0 .. NS
   const int rb16 = blockIdx.x, n0 = 16 * rb16;
+  const int ab0 = MB * (int)blockIdx.y;  // first activation row block of this workgroup
   const int egroups = (S + 3) / 4;
   // weights: the operand-order copy (a wave's operand is the 1 KiB at
   // lane * 16 of its (row block, chunk, half) slot) or row-major rows
@@ -1143,8 +1144,8 @@ __global__ __launch_bounds__(64 * W) void k_mxr(MxgArgs p) {
   const uint8_t* sbase[MB];
 #pragma unroll
   for (int b = 0; b < MB; ++b) {
-    abase[b] = p.a + (size_t)b * S * CB + lane * 16;
-    sbase[b] = p.as + (size_t)b * S * kChunkScaleBytes + lane * 4;
+    abase[b] = p.a + (size_t)(ab0 + b) * S * CB + lane * 16;
+    sbase[b] = p.as + (size_t)(ab0 + b) * S * kChunkScaleBytes + lane * 4;
   }
   struct Frag {
     u32x4 lo[MATS], hi[MATS];
@@ -1237,7 +1238,7 @@ __global__ __launch_bounds__(64 * W) void k_mxr(MxgArgs p) {
   if (tid >= MB * 256) return;
   const int b = tid >> 8, m16 = (tid >> 4) & 15, n16 = tid & 15;
   const int src = m16 + 16 * (n16 >> 2), r = n16 & 3;
-  const int mrow = 16 * b + m16, n = n0 + n16;
+  const int mrow = 16 * (ab0 + b) + m16, n = n0 + n16;
   if (mrow >= p.M || n >= p.N) return;
   float tot[MATS];
 #pragma unroll
@@ -1275,6 +1276,38 @@ bool mxr_fits(const MxgArgs& p) {
   const int S = p.kpad / 128;
   return p.mats == 2 && p.terms == kTerms && p.a != nullptr && (p.N + 15) / 16 >= 256 &&
          S >= kRowWaves && (S + kRowWaves - 1) / kRowWaves <= 16;
+}
+
+template <int DT, bool BLK, int MATS, int MB, int NS, int W, bool ROT>
+void launch_mxr_grid(const MxgArgs& p, dim3 grid, hipStream_t st) {
+  constexpr int D = NS < 3 ? NS : 3;
+  k_mxr<DT, BLK, MATS, MB, NS, D, W, ROT><<<grid, 64 * W, 0, st>>>(p);
+}
+
+// The large-tile products split along K (mxg_ksplit > 1: fewer than 128
+// tiles of 128 x 128, such as the 256 x 1024 x 1024 layers of a serial volume
+// chain) take k_mxr instead when they have one matrix, three activation
+// terms and 2..128 K chunks: 16 weight rows x 32 activation rows per
+// workgroup (grid.y over the row pairs of blocks), 8 waves over K, no partial
+// sums and no reduce launch. Not for chained products (the K-split reduce
+// writes their next split) or a fused RoPE.
+int mxg_ksplit(int M, int kpad, int N, int mats);
+bool replaces_ksplit(int M, int kpad, int N, int mats, int terms) {
+  const int S = kpad / 128;
+  return mats == 1 && terms == kTerms && M > 32 && mxg_ksplit(M, kpad, N, mats) > 1 &&
+         S >= 2 && S <= 16 * kRowWaves;
+}
+
+template <int DT, bool BLK>
+Status launch_mxr_large(const MxgArgs& p, hipStream_t st) {
+  const int ns = (p.kpad / 128 + kRowWaves - 1) / kRowWaves;
+  const dim3 grid((unsigned)((p.N + 15) / 16), (unsigned)(p.mpad / 32));
+  if (ns <= 1) launch_mxr_grid<DT, BLK, 1, 2, 1, kRowWaves, false>(p, grid, st);
+  else if (ns <= 2) launch_mxr_grid<DT, BLK, 1, 2, 2, kRowWaves, false>(p, grid, st);
+  else if (ns <= 4) launch_mxr_grid<DT, BLK, 1, 2, 4, kRowWaves, false>(p, grid, st);
+  else if (ns <= 8) launch_mxr_grid<DT, BLK, 1, 2, 8, kRowWaves, false>(p, grid, st);
+  else launch_mxr_grid<DT, BLK, 1, 2, 16, kRowWaves, false>(p, grid, st);
+  return hip_status(hipGetLastError(), "mxr launch");
 }
 
 template <int DT, bool BLK, int MATS, int MB>
@@ -1379,6 +1412,8 @@ Status launch_t(const MxgArgs& p, int bm, hipStream_t st) {
         (p.out_stride % 4 != 0 || ((reinterpret_cast<uintptr_t>(p.pre) | reinterpret_cast<uintptr_t>(p.post)) & 15)))
       return Status::err(kInvalid, "mxg: a chained split reduce needs 16-byte aligned outputs");
     if constexpr (MATS == 1) {
+      if (ks > 1 && !p.next && replaces_ksplit(p.M, p.kpad, p.N, MATS, p.terms))
+        return launch_mxr_large<DT, BLK>(p, st);
       if (ks > 1) {
         if (!p.part) return Status::err(kInvalid, "mxg: K-split partial buffer missing");
         const int tiles_n = (p.N + 127) / 128;
@@ -1454,6 +1489,10 @@ Status launch_m(const MxgArgs& p, int dtype, bool blk, int bm, hipStream_t st) {
 }  // namespace
 
 int mxg_block_m(int M) { return M <= 32 ? 16 : kBM; }
+
+bool mxr_replaces_ksplit(int M, int kpad, int N, int mats, int terms) {
+  return replaces_ksplit(M, kpad, N, mats, terms);
+}
 
 size_t mxg_part_bytes(int M, int kpad, int N, int mats) {
   if (mxg_block_m(M) != 16) {
