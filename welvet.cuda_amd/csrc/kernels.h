@@ -188,10 +188,6 @@ int mxg_block_m(int M);
 // Bytes of the K-split partial buffer the product of M rows with N outputs
 // (per matrix) needs; 0 when it takes no split.
 size_t mxg_part_bytes(int M, int kpad, int N, int mats);
-// Whether a large-tile product that mxg_ksplit would split along K runs
-// whole-K workgroups instead (one matrix, three terms): no partial sums and
-// no reduce launch, so no reduce that could write a chained split either.
-bool mxr_replaces_ksplit(int M, int kpad, int N, int mats, int terms);
 // Bytes of the split buffer for M rows of kpad columns.
 size_t split_bytes(int M, int kpad);
 // x [M][cols] (row stride x_stride) -> split terms in buf.

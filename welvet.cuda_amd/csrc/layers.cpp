@@ -389,8 +389,7 @@ Status dense_forward_split(const DenseLayer& L, int batch, const float* x, bool 
 bool dense_fuses_next(const DenseLayer& L, const DenseLayer& next, int batch) {
   return !L.format && !next.format && mxg_block_m(batch) > 16 && L.dev.nf_count() == 0 &&
          L.out % 256 == 0 && next.in == L.out && next.dev.kpad == L.out &&
-         next.terms == L.terms && mxg_part_bytes(batch, L.dev.kpad, L.out, 1) > 0 &&
-         !mxr_replaces_ksplit(batch, L.dev.kpad, L.out, 1, L.terms);
+         next.terms == L.terms && mxg_part_bytes(batch, L.dev.kpad, L.out, 1) > 0;
 }
 
 Status dense_forward(const DenseLayer& L, int batch, const float* x, float* pre, float* post,

@@ -1110,7 +1110,8 @@ __global__ __launch_bounds__(64 * kSmallWaves) __attribute__((amdgpu_waves_per_e
 // 88 KB of weights), so only the two-matrix product takes it.
 constexpr int kRowWaves = 8;
 
-template <int DT, bool BLK, int MATS, int MB, int NS, int D, int W = kRowWaves, bool ROT = false>
+template <int DT, bool BLK, int MATS, int MB, int NS, int D, int W = kRowWaves, bool ROT = false,
+          int RB = 1>
 __global__ __launch_bounds__(64 * W) void k_mxr(MxgArgs p) {
   constexpr bool FP4 = DT == kFP4;
   constexpr int NT = kTerms;  // FP6 terms (act_fp6)
@@ -1120,8 +1121,8 @@ __global__ __launch_bounds__(64 * W) void k_mxr(MxgArgs p) {
   const int i16 = lane & 15, g = lane >> 4;
   const int S = p.kpad / 128;
   const int k0 = S * wave / W, KR = S * (wave + 1) / W - k0;  // 0 .. NS
-  const int rb16 = blockIdx.x, n0 = 16 * rb16;
-  const int ab0 = MB * (int)blockIdx.y;  // first activation row block of this workgroup
+  const int n0 = 16 * RB * (int)blockIdx.x;  // RB blocks of 16 weight rows
+  const int ab0 = MB * (int)blockIdx.y;      // first activation row block of this workgroup
   const int egroups = (S + 3) / 4;
   // weights: the operand-order copy (a wave's operand is the 1 KiB at
   // lane * 16 of its (row block, chunk, half) slot) or row-major rows
@@ -1129,14 +1130,17 @@ __global__ __launch_bounds__(64 * W) void k_mxr(MxgArgs p) {
   // grid covers whole 16-row blocks of the rows, which are padded to 128
   const bool frag = p.codesf[0] != nullptr && (MATS == 1 || p.codesf[MATS - 1] != nullptr);
   const uint32_t cstride = frag ? WB * 16 : WB, hstride = frag ? 1024 : 64;
-  const uint8_t* wrow[MATS];
-  const uint8_t* erow[MATS];
+  const uint8_t* wrow[MATS][RB];
+  const uint8_t* erow[MATS][RB];
 #pragma unroll
-  for (int m = 0; m < MATS; ++m) {
-    wrow[m] = frag ? p.codesf[m] + (size_t)rb16 * S * (WB * 16) + lane * 16
-                   : p.codes[m] + (size_t)(n0 + i16) * p.pitch + 16 * g;
-    erow[m] = BLK ? p.blkf[m] + (size_t)rb16 * egroups * 256 + lane * 4 : nullptr;
-  }
+  for (int m = 0; m < MATS; ++m)
+#pragma unroll
+    for (int j = 0; j < RB; ++j) {
+      const int rb16 = n0 / 16 + j;
+      wrow[m][j] = frag ? p.codesf[m] + (size_t)rb16 * S * (WB * 16) + lane * 16
+                        : p.codes[m] + (size_t)(16 * rb16 + i16) * p.pitch + 16 * g;
+      erow[m][j] = BLK ? p.blkf[m] + (size_t)rb16 * egroups * 256 + lane * 4 : nullptr;
+    }
   // activation terms of row block b, chunk c: term t's 16 bytes of lane l at
   // ((b S + c) NT + t) 1536 + 16 l, its 8 more at + 1024 + 8 l; the
   // exponent dword (byte t: term t) at (b S + c) 256 + 4 l
@@ -1148,8 +1152,8 @@ __global__ __launch_bounds__(64 * W) void k_mxr(MxgArgs p) {
     sbase[b] = p.as + (size_t)(ab0 + b) * S * kChunkScaleBytes + lane * 4;
   }
   struct Frag {
-    u32x4 lo[MATS], hi[MATS];
-    uint32_t e[MATS];
+    u32x4 lo[MATS][RB], hi[MATS][RB];
+    uint32_t e[MATS][RB];
     int4 xl[NT][MB];
     int2 xh[NT][MB];
     uint32_t xs[MB];
@@ -1162,12 +1166,15 @@ __global__ __launch_bounds__(64 * W) void k_mxr(MxgArgs p) {
   auto load = [&](int r, Frag& f) {  // chunk k0 + r, clamped to the range
     const int c = chunk(r);
 #pragma unroll
-    for (int m = 0; m < MATS; ++m) {
-      const uint8_t* src = wrow[m] + (size_t)c * cstride;
-      f.lo[m] = *reinterpret_cast<const u32x4*>(src);
-      if constexpr (!FP4) f.hi[m] = *reinterpret_cast<const u32x4*>(src + hstride);
-      f.e[m] = BLK ? *reinterpret_cast<const uint32_t*>(erow[m] + (size_t)(c >> 2) * 256) : 0x7F7F7F7Fu;
-    }
+    for (int m = 0; m < MATS; ++m)
+#pragma unroll
+      for (int j = 0; j < RB; ++j) {
+        const uint8_t* src = wrow[m][j] + (size_t)c * cstride;
+        f.lo[m][j] = *reinterpret_cast<const u32x4*>(src);
+        if constexpr (!FP4) f.hi[m][j] = *reinterpret_cast<const u32x4*>(src + hstride);
+        f.e[m][j] = BLK ? *reinterpret_cast<const uint32_t*>(erow[m][j] + (size_t)(c >> 2) * 256)
+                        : 0x7F7F7F7Fu;
+      }
 #pragma unroll
     for (int b = 0; b < MB; ++b) {
       const uint8_t* src = abase[b] + (size_t)c * CB;
@@ -1180,11 +1187,13 @@ __global__ __launch_bounds__(64 * W) void k_mxr(MxgArgs p) {
     }
   };
 
-  v4f acc[MATS][MB];
+  v4f acc[MATS][RB][MB];
 #pragma unroll
   for (int m = 0; m < MATS; ++m)
 #pragma unroll
-    for (int b = 0; b < MB; ++b) acc[m][b] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < RB; ++j)
+#pragma unroll
+      for (int b = 0; b < MB; ++b) acc[m][j][b] = v4f{0.f, 0.f, 0.f, 0.f};
   Frag f[D];
 #pragma unroll
   for (int i = 0; i < D - 1; ++i) load(i, f[i]);
@@ -1196,75 +1205,115 @@ __global__ __launch_bounds__(64 * W) void k_mxr(MxgArgs p) {
     const bool live = r < KR;  // uniform
     const int c = chunk(r);
     const int eb = 8 * (c & 3);  // byte of this chunk in the exponent dwords
-    v8i w[MATS];
-    int we[MATS];
+    v8i w[MATS][RB];
+    int we[MATS][RB];
 #pragma unroll
-    for (int m = 0; m < MATS; ++m) {
-      const u32x4 lo = fr.lo[m];
-      const u32x4 hi = FP4 ? u32x4{0u, 0u, 0u, 0u} : fr.hi[m];
-      w[m] = live ? v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z,
-                        (int)hi.w}
-                  : v8i{0, 0, 0, 0, 0, 0, 0, 0};
-      we[m] = (int)((fr.e[m] >> eb) & 0xFFu);
-    }
+    for (int m = 0; m < MATS; ++m)
+#pragma unroll
+      for (int j = 0; j < RB; ++j) {
+        const u32x4 lo = fr.lo[m][j];
+        const u32x4 hi = FP4 ? u32x4{0u, 0u, 0u, 0u} : fr.hi[m][j];
+        w[m][j] = live ? v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y,
+                             (int)hi.z, (int)hi.w}
+                       : v8i{0, 0, 0, 0, 0, 0, 0, 0};
+        we[m][j] = (int)((fr.e[m][j] >> eb) & 0xFFu);
+      }
     static_for<0, NT>([&](auto T) {
       constexpr int t = decltype(T)::value;
 #pragma unroll
       for (int m = 0; m < MATS; ++m)
 #pragma unroll
-        for (int b = 0; b < MB; ++b) {
-          const int4 xl = fr.xl[t][b];
-          const int2 xh = fr.xh[t][b];
-          const v8i x = v8i{xl.x, xl.y, xl.z, xl.w, xh.x, xh.y, 0, 0};
-          acc[m][b] = mfma_term<DT, t, true>(w[m], x, acc[m][b], we[m], fr.xs[b]);
-        }
+        for (int j = 0; j < RB; ++j)
+#pragma unroll
+          for (int b = 0; b < MB; ++b) {
+            const int4 xl = fr.xl[t][b];
+            const int2 xh = fr.xh[t][b];
+            const v8i x = v8i{xl.x, xl.y, xl.z, xl.w, xh.x, xh.y, 0, 0};
+            acc[m][j][b] = mfma_term<DT, t, true>(w[m][j], x, acc[m][j][b], we[m][j], fr.xs[b]);
+          }
     });
     __builtin_amdgcn_sched_barrier(0);
   }
 
-  // acc[m][b]: lane holds activation row 16 b + i16 and weight rows
-  // n0 + 4g + r (r = 0..3); the waves' sums meet in LDS
-  __shared__ float red[W][MATS][MB][4][64];
+  // acc[m][j][b]: lane holds activation row 16 b + i16 and weight rows
+  // n0 + 16 j + 4g + r (r = 0..3); the waves' sums meet in LDS
+  __shared__ float red[W][MATS][RB][MB][4][64];
 #pragma unroll
   for (int m = 0; m < MATS; ++m)
 #pragma unroll
-    for (int b = 0; b < MB; ++b)
+    for (int j = 0; j < RB; ++j)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) red[wave][m][b][r][lane] = acc[m][b][r];
+      for (int b = 0; b < MB; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[wave][m][j][b][r][lane] = acc[m][j][b][r];
+  // chained products (RB = 2, one matrix): post of the 16 rows x 32 columns
+  // of each row block, for the next layer's split
+  constexpr bool CAN_NEXT = MATS == 1 && RB == 2;
+  __shared__ float nstage[CAN_NEXT ? MB : 1][16][33];
   __syncthreads();
-  // thread e: row block e / 256, activation row (e / 16) % 16, weight row
-  // n0 + e % 16 (16 consecutive outputs per 16 threads)
-  static_assert(64 * W >= MB * 256, "one thread per output of the workgroup");
-  if (tid >= MB * 256) return;
-  const int b = tid >> 8, m16 = (tid >> 4) & 15, n16 = tid & 15;
-  const int src = m16 + 16 * (n16 >> 2), r = n16 & 3;
-  const int mrow = 16 * (ab0 + b) + m16, n = n0 + n16;
-  if (mrow >= p.M || n >= p.N) return;
-  float tot[MATS];
+  // output e: row block e / (256 RB), activation row (e / 16 RB) % 16,
+  // column n0 + e % 16 RB (16 RB consecutive outputs per 16 RB threads)
+  constexpr int NOUT = RB * MB * 256;
+  for (int e = tid; e < NOUT; e += 64 * W) {
+    const int b = e / (256 * RB), m16 = (e / (16 * RB)) % 16, nc = e % (16 * RB);
+    const int j = nc >> 4, n16 = nc & 15;
+    const int src = m16 + 16 * (n16 >> 2), r = n16 & 3;
+    const int mrow = 16 * (ab0 + b) + m16, n = n0 + nc;
+    const bool live = mrow < p.M && n < p.N;
+    float tot[MATS];
 #pragma unroll
-  for (int m = 0; m < MATS; ++m) {
-    float v = red[0][m][b][r][src];
+    for (int m = 0; m < MATS; ++m) {
+      float v = red[0][m][j][b][r][src];
 #pragma unroll
-    for (int w = 1; w < W; ++w) v += red[w][m][b][r][src];
-    tot[m] = v;
-  }
-  const size_t oi = (size_t)mrow * p.out_stride + n;
-  if constexpr (MATS == 2) {
-    const float gs = (float)act_f64(kSilu, (double)(tot[0] * p.scale[0][n]));
-    p.pre[oi] = (float)((double)gs * (double)(tot[1] * p.scale[1][n]));
-  } else {
-    float y = tot[0] * p.scale[0][n];
-    if (p.need_epi) {
-      double v = (double)y;
-      if (p.bias && n < p.bias_len) {
-        v += p.bias[n];
-        y = (float)v;
+      for (int w = 1; w < W; ++w) v += red[w][m][j][b][r][src];
+      tot[m] = v;
+    }
+    const size_t oi = (size_t)mrow * p.out_stride + n;
+    if constexpr (MATS == 2) {
+      if (live) {
+        const float gs = (float)act_f64(kSilu, (double)(tot[0] * p.scale[0][n]));
+        p.pre[oi] = (float)((double)gs * (double)(tot[1] * p.scale[1][n]));
       }
-      p.pre[oi] = y;
-      p.post[oi] = (float)act_f64(p.act, v);
     } else {
-      p.pre[oi] = y;
-      if (p.post && p.post != p.pre) p.post[oi] = y;
+      float y = 0.0f, out = 0.0f;
+      if (live) {
+        y = tot[0] * p.scale[0][n];
+        out = y;
+        if (p.need_epi) {
+          double v = (double)y;
+          if (p.bias && n < p.bias_len) {
+            v += p.bias[n];
+            y = (float)v;
+          }
+          out = (float)act_f64(p.act, v);
+          if (p.pre) p.pre[oi] = y;
+          if (p.post) p.post[oi] = out;
+        } else {
+          if (p.pre) p.pre[oi] = y;
+          if (p.post && p.post != p.pre) p.post[oi] = y;
+        }
+      }
+      if constexpr (CAN_NEXT) nstage[b][m16][nc] = out;  // zero outside [0, M) x [0, N)
+    }
+  }
+  if constexpr (CAN_NEXT) {
+    // The next layer's split of post (the terms k_split makes from post in
+    // memory; same rows mpad, kpad = N): this workgroup's 32 columns are one
+    // block of a 128-wide chunk, held in operand order by lanes i + 16 g of
+    // each (row block, chunk) slot, one lane per activation row.
+    if (p.next) {
+      __syncthreads();
+      if (tid < 16 * MB) {
+        const int b = tid >> 4, i = tid & 15, rb = ab0 + b;
+        const int kcn = p.N / 128, kc = n0 / 128, gb = (n0 % 128) / 32;
+        float v[32];
+#pragma unroll
+        for (int q = 0; q < 32; ++q) v[q] = nstage[b][i][q];
+        const GlobalU8 nchunk = (GlobalU8)(p.next + (size_t)(rb * kcn + kc) * CB);
+        const GlobalU8 nsc = (GlobalU8)(p.next + (size_t)kTerms * p.mpad * p.N +
+                                        (size_t)(rb * kcn + kc) * kChunkScaleBytes);
+        split_terms6<1, NT, true>(v, nchunk, nsc, i + 16 * gb);
+      }
     }
   }
 }
@@ -1278,19 +1327,18 @@ bool mxr_fits(const MxgArgs& p) {
          S >= kRowWaves && (S + kRowWaves - 1) / kRowWaves <= 16;
 }
 
-template <int DT, bool BLK, int MATS, int MB, int NS, int W, bool ROT>
+template <int DT, bool BLK, int MATS, int MB, int NS, int W, bool ROT, int RB = 1>
 void launch_mxr_grid(const MxgArgs& p, dim3 grid, hipStream_t st) {
   constexpr int D = NS < 3 ? NS : 3;
-  k_mxr<DT, BLK, MATS, MB, NS, D, W, ROT><<<grid, 64 * W, 0, st>>>(p);
+  k_mxr<DT, BLK, MATS, MB, NS, D, W, ROT, RB><<<grid, 64 * W, 0, st>>>(p);
 }
 
 // The large-tile products split along K (mxg_ksplit > 1: fewer than 128
 // tiles of 128 x 128, such as the 256 x 1024 x 1024 layers of a serial volume
 // chain) take k_mxr instead when they have one matrix, three activation
-// terms and 2..128 K chunks: 16 weight rows x 32 activation rows per
-// workgroup (grid.y over the row pairs of blocks), 8 waves over K, no partial
-// sums and no reduce launch. Not for chained products (the K-split reduce
-// writes their next split) or a fused RoPE.
+// terms and 2..128 K chunks: 16 (chained: 32) weight rows x 32 activation
+// rows per workgroup (grid.y over the pairs of row blocks), 8 waves over K,
+// no partial sums and no reduce launch. (A fused RoPE takes no K split.)
 int mxg_ksplit(int M, int kpad, int N, int mats);
 bool replaces_ksplit(int M, int kpad, int N, int mats, int terms) {
   const int S = kpad / 128;
@@ -1298,15 +1346,28 @@ bool replaces_ksplit(int M, int kpad, int N, int mats, int terms) {
          S >= 2 && S <= 16 * kRowWaves;
 }
 
+template <int DT, bool BLK, int RB>
+void launch_mxr_large_rb(const MxgArgs& p, hipStream_t st) {
+  const int ns = (p.kpad / 128 + kRowWaves - 1) / kRowWaves;
+  const dim3 grid((unsigned)((p.N + 16 * RB - 1) / (16 * RB)), (unsigned)(p.mpad / 32));
+  if (ns <= 1) launch_mxr_grid<DT, BLK, 1, 2, 1, kRowWaves, false, RB>(p, grid, st);
+  else if (ns <= 2) launch_mxr_grid<DT, BLK, 1, 2, 2, kRowWaves, false, RB>(p, grid, st);
+  else if (ns <= 4) launch_mxr_grid<DT, BLK, 1, 2, 4, kRowWaves, false, RB>(p, grid, st);
+  else if (ns <= 8) launch_mxr_grid<DT, BLK, 1, 2, 8, kRowWaves, false, RB>(p, grid, st);
+  else launch_mxr_grid<DT, BLK, 1, 2, 16, kRowWaves, false, RB>(p, grid, st);
+}
+
+// 16 weight rows per workgroup; 32 for a chained product, whose epilogue
+// then holds whole 32-column blocks of post and writes the next layer's split
+// (the K ranges of the waves, and so every sum, are the same for both).
 template <int DT, bool BLK>
 Status launch_mxr_large(const MxgArgs& p, hipStream_t st) {
-  const int ns = (p.kpad / 128 + kRowWaves - 1) / kRowWaves;
-  const dim3 grid((unsigned)((p.N + 15) / 16), (unsigned)(p.mpad / 32));
-  if (ns <= 1) launch_mxr_grid<DT, BLK, 1, 2, 1, kRowWaves, false>(p, grid, st);
-  else if (ns <= 2) launch_mxr_grid<DT, BLK, 1, 2, 2, kRowWaves, false>(p, grid, st);
-  else if (ns <= 4) launch_mxr_grid<DT, BLK, 1, 2, 4, kRowWaves, false>(p, grid, st);
-  else if (ns <= 8) launch_mxr_grid<DT, BLK, 1, 2, 8, kRowWaves, false>(p, grid, st);
-  else launch_mxr_grid<DT, BLK, 1, 2, 16, kRowWaves, false>(p, grid, st);
+  if (p.next) {
+    if (p.N % 128 != 0) return Status::err(kInvalid, "mxr: a chained split needs N % 128 == 0");
+    launch_mxr_large_rb<DT, BLK, 2>(p, st);
+  } else {
+    launch_mxr_large_rb<DT, BLK, 1>(p, st);
+  }
   return hip_status(hipGetLastError(), "mxr launch");
 }
 
@@ -1412,7 +1473,7 @@ Status launch_t(const MxgArgs& p, int bm, hipStream_t st) {
         (p.out_stride % 4 != 0 || ((reinterpret_cast<uintptr_t>(p.pre) | reinterpret_cast<uintptr_t>(p.post)) & 15)))
       return Status::err(kInvalid, "mxg: a chained split reduce needs 16-byte aligned outputs");
     if constexpr (MATS == 1) {
-      if (ks > 1 && !p.next && replaces_ksplit(p.M, p.kpad, p.N, MATS, p.terms))
+      if (ks > 1 && replaces_ksplit(p.M, p.kpad, p.N, MATS, p.terms))
         return launch_mxr_large<DT, BLK>(p, st);
       if (ks > 1) {
         if (!p.part) return Status::err(kInvalid, "mxg: K-split partial buffer missing");
@@ -1489,10 +1550,6 @@ Status launch_m(const MxgArgs& p, int dtype, bool blk, int bm, hipStream_t st) {
 }  // namespace
 
 int mxg_block_m(int M) { return M <= 32 ? 16 : kBM; }
-
-bool mxr_replaces_ksplit(int M, int kpad, int N, int mats, int terms) {
-  return replaces_ksplit(M, kpad, N, mats, terms);
-}
 
 size_t mxg_part_bytes(int M, int kpad, int N, int mats) {
   if (mxg_block_m(M) != 16) {
