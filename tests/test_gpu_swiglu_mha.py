@@ -5,7 +5,8 @@ with the reference's f32/f64 rounding; post = Down h.
 MHA (mha.cpp:123-183, kernels.cu:470-631): Q/K/V projections, attention core
 with the reference's global positions and KV ring, O projection.
 Tolerance: relative L2 <= 1e-5 for one row (VALU GEMV, fp32), <= 5e-5 where
-rows go through the scaled matrix cores (see test_gpu_dense), <= 1e-4 after
+rows go through the scaled matrix cores (see test_gpu_dense; batch-1 layers
+of 4081 rows and more do too), <= 1e-4 after
 the attention core (fp32 exp/sin/cos against f64 libm). The layer contract
 bound is 1e-3.
 """
@@ -91,7 +92,9 @@ def test_swiglu_gate_up_whole_k_workgroups(gpu, oracle, dt, scheme, rows, d, int
 
 
 def test_c3_swiglu_fp4_block32_batch1(gpu, oracle):
-    """SwiGLU d_model 4096, d_ff 11008, FP4 E2M1 + E8M0 per 32 along K, batch 1."""
+    """SwiGLU d_model 4096, d_ff 11008, FP4 E2M1 + E8M0 per 32 along K, batch 1:
+    both products on the matrix cores over the operand-order weights, the
+    down projection on the split of h that the gate+up launch writes."""
     import pywelvet as pw
     d, f = 4096, 11008
     seed = pw.seed_for(3)
@@ -103,8 +106,10 @@ def test_c3_swiglu_fp4_block32_batch1(gpu, oracle):
     h, y = s.execute(x)
     s.close()
     oh, oy = oracle_swiglu(oracle, 16, 3, G, U, D, x)
-    assert rel_l2(h, oh) <= 1e-5
-    assert rel_l2(y, oy) <= 1e-5
+    assert rel_l2(h, oh) <= tol(16)
+    oy_own, _ = oracle.dense(oracle_dequant(oracle, 16, 3, D), h)
+    assert rel_l2(y, oy_own) <= tol(16)
+    assert rel_l2(y, oy) <= tol(16, chain=2)
 
 
 def oracle_mha(oracle, dt, scheme, Q, K, V, O, x, B, S, H, KVH, hd, msl, mask, pos):

@@ -714,6 +714,7 @@ Status forward(Layer& layer, const TensorF32& input, TensorF32* pre, TensorF32* 
       CX_WV(fit(&d->x, xb));
       CX_WV(fit(&d->pre, hb));
       CX_WV(fit(&d->post, xb));
+      CX_WV(wv::ensure_split(&d->ws, wv::swiglu_workspace_bytes(f, rows)));
       CX_WV(wv::copy_h2d(d->x.p, input.data.data(), xb, st));
       CX_WV(wv::swiglu_forward(f, rows, d->x.as<float>(), d->pre.as<float>(), d->post.as<float>(),
                                &d->ws, st));

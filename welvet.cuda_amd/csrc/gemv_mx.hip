@@ -1,0 +1,556 @@
+// Batch-1 quantized GEMV on the CDNA4 scaled matrix cores, over the weights
+// in matrix-core operand order (DeviceWeights::codes_frag).
+//
+//   y[n] = rowscale[n] * sum_k x[k] * dec(W[n][k]) * blockscale[n][k/32]
+//
+// Weights. Per 16-row block and K chunk of 128 the operand a wave passes to
+// v_mfma_scale_f32_16x16x128_f8f6f4 is stored contiguously (1 KiB for FP4,
+// 2 x 1 KiB for FP8), so every weight load of a wave reads 1 KiB in one
+// piece and a workgroup's 16 rows are one contiguous run. The matrix core
+// takes the stored codes and their E8M0 block scales directly: nothing is
+// decoded on the VALU.
+//
+// Activations. x is split into three E4M3 terms per 16-element piece: term t
+// quantizes the residual of terms 0..t-1 with its own E8M0 exponent (the
+// smallest with the piece's amax <= 448 * 2^e). The terms sit in the rows of
+// the A operand, so one MFMA applies all three to a weight fragment. A lane's
+// scale covers one 32-element block of one row, so the two 16-element halves
+// of a block go to different rows, each with its own exponent: row 3h + t
+// holds term t of the pieces that are half h of their block. Piece p of a
+// chunk (k = 16p .. 16p + 15) is held by lane group p & 3 at byte 16 (p >> 2)
+// (the FP8 operand layout: bytes 0-15 -> k = 16g + j, 16-31 -> k = 64 + 16g
+// + j), so row 3h + t carries data only in lane groups g with g & 1 == h; its
+// scale for block b is the exponent of piece 2b + h. The six accumulator
+// rows (lanes g = 0: rows 0-3, g = 1: rows 4-5) add up to the product.
+//
+// Work split. One workgroup per 16 weight rows (per matrix); its W waves cut
+// K into ranges of at most NSW chunks. A wave issues the loads of its input
+// first, then every weight load of its range; it splits its slice of x into
+// its own LDS region while the weights arrive (or, with a pre-split input,
+// loads the terms a producer wrote), runs one MFMA per chunk and matrix, and
+// the partial sums of the waves meet in LDS for the epilogue (row scale,
+// bias, activation, or the SwiGLU product). The SwiGLU gate+up launch can
+// also write the three-term split of its output h for the down projection:
+// each workgroup's 16 outputs are exactly one piece.
+//
+// Non-finite inputs. A wave whose slice of x holds inf or NaN (or whose
+// pre-split pieces carry the 0xFF exponent that marks a non-finite piece)
+// computes its partial sums on the VALU instead, from the same weight
+// registers decoded exactly, so such inputs give the IEEE result of the
+// fp32 GEMV.
+#include <type_traits>
+
+#include "codec.h"
+#include "act.h"
+#include "common.h"
+#include "kernels.h"
+#include "wave.h"
+
+namespace wv {
+namespace {
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v2f __attribute__((ext_vector_type(2)));
+typedef short v2s __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kTermsMx = 3;
+constexpr int kChunkCodeBytes = kTermsMx * 4 * 32;  // codes of one chunk's terms
+constexpr int kChunkExpBytes = kTermsMx * 8;       // exponents: term x piece
+constexpr uint8_t kNonFinite = 0xFF;               // exponent byte of a non-finite piece
+
+template <int I, int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
+}
+
+template <int DT>
+constexpr int wfmt() {
+  return DT == kE4M3 ? 0 : DT == kE5M2 ? 1 : 4;
+}
+
+__device__ __forceinline__ u32x4 load_stream(const uint8_t* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+
+__device__ __forceinline__ float pair_max(float v) {  // lanes l, l ^ 1
+  const int o = __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false);
+  return fmaxf(v, __builtin_bit_cast(float, o));
+}
+
+__device__ __forceinline__ bool finite_amax(float am) {
+  return am <= 3.40282347e38f;  // false for inf and NaN
+}
+
+// Term t of 8 values with scale 2^e: the E4M3 codes of v / 2^e (two words)
+// and v - dec(codes) * 2^e left in v. The scaled converters divide by and
+// multiply with the scale exactly (same bits as an explicit multiply by the
+// power of two, then the plain converter).
+__device__ __forceinline__ int2 term8(float (&v)[8], float sc, bool residual) {
+  v2s w0 = {0, 0}, w1 = {0, 0};
+  w0 = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(w0, v[0], v[1], sc, false);
+  w0 = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(w0, v[2], v[3], sc, true);
+  w1 = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(w1, v[4], v[5], sc, false);
+  w1 = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(w1, v[6], v[7], sc, true);
+  const int c0 = __builtin_bit_cast(int, w0), c1 = __builtin_bit_cast(int, w1);
+  if (residual) {
+    const v2f d0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(c0, sc, false);
+    const v2f d1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(c0, sc, true);
+    const v2f d2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(c1, sc, false);
+    const v2f d3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(c1, sc, true);
+    v[0] -= d0.x, v[1] -= d0.y, v[2] -= d1.x, v[3] -= d1.y;
+    v[4] -= d2.x, v[5] -= d2.y, v[6] -= d3.x, v[7] -= d3.y;
+  }
+  return make_int2(c0, c1);
+}
+
+// Exact partial sum of one lane's operand slice (row n of the fragment,
+// its K positions) against x, for the non-finite fallback: FP4 nibble j ->
+// k = 32 g + j; FP8 byte j -> k = 16 g + j (j < 16), 64 + 16 g + j - 16.
+// Exact sum of one lane's operand slice against x for the non-finite
+// fallback, one 4-byte word at a time (a rolled loop: this path must not add
+// register pressure to the matrix-core path). FP4 word d holds nibbles 8d ..
+// 8d + 7 (k = 32 g + 8d + j); FP8 word d < 4 holds k = 16 g + 4d + j, word
+// d >= 4 k = 64 + 16 g + 4 (d - 4) + j. Each word is scaled by the exponent
+// of its block (lanes e_lo for FP4 and FP8 words 0-3, e_hi for FP8 words 4-7).
+template <int DT>
+__device__ float exact_slice(const uint8_t* w, const float* x, int k0, int g, int cols,
+                             float s_lo, float s_hi) {
+  constexpr int WORDS = DT == kFP4 ? 4 : 8;
+  float s = 0.0f;
+#pragma unroll 1
+  for (int d = 0; d < WORDS; ++d) {
+    const uint32_t v = *reinterpret_cast<const uint32_t*>(w + (d < 4 ? 4 * d : 1024 + 4 * (d - 4)));
+    float p = 0.0f;
+    if constexpr (DT == kFP4) {
+      const int k = k0 + 32 * g + 8 * d;
+      float q[8];
+      const v2f a0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(v, 1.0f, 0);
+      const v2f a1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(v, 1.0f, 1);
+      const v2f a2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(v, 1.0f, 2);
+      const v2f a3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(v, 1.0f, 3);
+      q[0] = a0[0], q[1] = a0[1], q[2] = a1[0], q[3] = a1[1];
+      q[4] = a2[0], q[5] = a2[1], q[6] = a3[0], q[7] = a3[1];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) p = fmaf(q[j], k + j < cols ? x[k + j] : 0.0f, p);
+      s = fmaf(p, s_lo, s);
+    } else {
+      const int k = k0 + (d < 4 ? 16 * g + 4 * d : 64 + 16 * g + 4 * (d - 4));
+      const v2f a0 = DT == kE4M3 ? __builtin_amdgcn_cvt_pk_f32_fp8(v, false)
+                                 : __builtin_amdgcn_cvt_pk_f32_bf8(v, false);
+      const v2f a1 = DT == kE4M3 ? __builtin_amdgcn_cvt_pk_f32_fp8(v, true)
+                                 : __builtin_amdgcn_cvt_pk_f32_bf8(v, true);
+      const float q[4] = {a0[0], a0[1], a1[0], a1[1]};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) p = fmaf(q[j], k + j < cols ? x[k + j] : 0.0f, p);
+      s = fmaf(p, d < 4 ? s_lo : s_hi, s);
+    }
+  }
+  return s;
+}
+
+// PRE: the input is a pre-split image (a.asplit); otherwise the waves split
+// a.x themselves. NEXT (MATS == 2): write the split of h to a.next.
+template <int DT, bool BLK, int MATS, int W, int NSW, bool PRE, bool NEXT>
+__global__ __launch_bounds__(64 * W) void k_gemv_mx(GemvMxArgs a) {
+  constexpr bool FP4 = DT == kFP4;
+  constexpr int XR = (NSW * 16 + 63) / 64;  // split rounds of 64 items (8 values each)
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n = lane & 15, g = lane >> 4;
+  const int S = a.kpad / 128;
+  const int s0 = wave * S / W, s1 = (wave + 1) * S / W, ns = s1 - s0;
+  const int rb = blockIdx.x, n0 = 16 * rb;
+  // A-operand row of this lane: term t of half h; rows 6..15 are zero
+  const int ah = n >= 3 ? 1 : 0, at = n - 3 * ah;
+  const bool arow = n < 6, adata = arow && (g & 1) == ah;
+
+  __shared__ __attribute__((aligned(16))) uint8_t lds_c[W][NSW][kChunkCodeBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_e[W][NSW][kChunkExpBytes];
+  __shared__ float part[W][MATS][16][2];
+
+  // 1. the input: this wave's chunks of the pre-split image (16-byte pieces:
+  // 24 per chunk of codes, then the exponents), or x for the split below
+  constexpr int PR = (NSW * (kChunkCodeBytes / 16) + 63) / 64;
+  u32x4 pc[PRE ? PR : 1];
+  uint32_t pe[PRE ? (NSW * kChunkExpBytes / 4 + 63) / 64 : 1];
+  float4 xv[PRE ? 1 : XR][2];
+  if constexpr (PRE) {
+    const int SA = a.asplit_steps;
+    const int valid = (a.cols + 15) / 16;  // pieces ever written
+#pragma unroll
+    for (int r = 0; r < PR; ++r) {
+      const int u = r * 64 + lane, i = u / 24, v = u % 24;  // chunk, 16-byte piece of its codes
+      // v = 2 (4 t + g) + hi: piece 8 s + g + 4 hi of term t
+      const int s = s0 + (i < ns ? i : 0), pc_piece = 8 * s + ((v >> 1) & 3) + 4 * (v & 1);
+      // every load unconditional (from a clamped address, then selected):
+      // a branch around a load makes the compiler wait for all loads at the join
+      const u32x4 t = *reinterpret_cast<const u32x4*>(a.asplit + (size_t)s * kChunkCodeBytes + 16 * v);
+      const bool live = i < ns && pc_piece < valid;
+      pc[r] = live ? t : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int r = 0; r < (int)(sizeof(pe) / 4); ++r) {
+      const int u = r * 64 + lane, i = u / (kChunkExpBytes / 4), v = u % (kChunkExpBytes / 4);
+      const uint32_t t = *reinterpret_cast<const uint32_t*>(
+          a.asplit + (size_t)SA * kChunkCodeBytes + (size_t)(s0 + (i < ns ? i : 0)) * kChunkExpBytes + 4 * v);
+      pe[r] = i < ns ? t : 0x7F7F7F7Fu;
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < XR; ++r) {
+      const int it = r * 64 + lane, i = it >> 4, q = it & 15;
+      const int k = (s0 + i) * 128 + 8 * q;
+      // x 16-byte aligned and cols % 4 == 0 (launch_gemv_mx checks): the
+      // two float4 of an item are wholly inside or outside [0, cols)
+      const bool live0 = i < ns && k < a.cols, live1 = i < ns && k + 4 < a.cols;
+      const float4 t0 = *reinterpret_cast<const float4*>(a.x + (live0 ? k : 0));
+      const float4 t1 = *reinterpret_cast<const float4*>(a.x + (live1 ? k + 4 : 0));
+      const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+      xv[r][0] = live0 ? t0 : z;
+      xv[r][1] = live1 ? t1 : z;
+    }
+  }
+
+  // the epilogue's row scales (and bias) early, so the epilogue waits for no
+  // global load (wave 0 computes it: lane l for row n0 + l % 16)
+  float rs[MATS];
+#pragma unroll
+  for (int m = 0; m < MATS; ++m) rs[m] = wave == 0 ? a.scale[m][n0 + n] : 1.0f;
+  const int ob = n0 + n;
+  const double bias = wave == 0 && MATS == 1 && a.bias && ob < a.bias_len ? a.bias[ob] : 0.0;
+
+  // 2. every weight load of this wave's range in flight
+  constexpr int H = FP4 ? 1 : 2;
+  constexpr int EG = NSW / 4 + 2;  // exponent dwords a range of NSW chunks touches
+  u32x4 wl[MATS][NSW], wh[MATS][FP4 ? 1 : NSW];
+  uint32_t we[MATS][BLK ? EG : 1];
+#pragma unroll
+  for (int m = 0; m < MATS; ++m) {
+    const uint8_t* f = a.codesf[m] + (size_t)rb * S * (H * 1024) + lane * 16;
+#pragma unroll
+    for (int i = 0; i < NSW; ++i) {
+      // chunks past the range load the range's last one again (cache hits;
+      // no MFMA uses them)
+      const int s = s0 + i < s1 ? s0 + i : s1 - 1;
+      wl[m][i] = load_stream(f + (size_t)s * (H * 1024));
+      if constexpr (!FP4) wh[m][i] = load_stream(f + (size_t)s * (H * 1024) + 1024);
+    }
+    if constexpr (BLK) {
+      const int groups = (S + 3) / 4;
+#pragma unroll
+      for (int j = 0; j < EG; ++j) {
+        const int grp = s0 / 4 + j, gc = grp < groups ? grp : groups - 1;
+        const uint32_t t = *reinterpret_cast<const uint32_t*>(a.blkf[m] + (((size_t)rb * groups + gc) * 64 + lane) * 4);
+        we[m][j] = grp < groups ? t : 0x7F7F7F7Fu;
+      }
+    }
+  }
+
+  // 3. the split of this wave's slice of x (three E4M3 terms per piece)
+  bool bad = false;
+  if constexpr (!PRE) {
+    bool nonfinite = false;
+#pragma unroll
+    for (int r = 0; r < XR; ++r) {
+      const int it = r * 64 + lane, i = it >> 4, q = it & 15, p = q >> 1;
+      float v[8] = {xv[r][0].x, xv[r][0].y, xv[r][0].z, xv[r][0].w,
+                    xv[r][1].x, xv[r][1].y, xv[r][1].z, xv[r][1].w};
+      const int cb = (p & 3) * 32 + 16 * (p >> 2) + 8 * (q & 1);
+      uint32_t eb = 0;
+      // fmaxf passes over NaN, so inf and NaN are caught by the plain sum
+      // (a finite sum that overflows only sends the wave to the exact path)
+      float sum = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sum += v[j];
+      nonfinite |= !finite_amax(fabsf(sum));
+#pragma unroll
+      for (int t = 0; t < kTermsMx; ++t) {
+        float am = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) am = fmaxf(am, fabsf(v[j]));
+        am = pair_max(am);
+        const int e = e8m0_exponent(am, 448.0f);
+        const int2 c = term8(v, pow2f(e), t + 1 < kTermsMx);
+        if (i < NSW) *reinterpret_cast<int2*>(&lds_c[wave][i][t * 128 + cb]) = c;
+        eb |= (uint32_t)(e + 127) << (8 * t);
+      }
+      if ((q & 1) == 0 && i < NSW) {
+#pragma unroll
+        for (int t = 0; t < kTermsMx; ++t) lds_e[wave][i][t * 8 + p] = (uint8_t)(eb >> (8 * t));
+      }
+    }
+    bad = __ballot(nonfinite) != 0;
+    // LDS writes of this wave complete before its lanes read them
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  } else {
+    // the pre-split chunks into this wave's LDS; exponent bytes of pieces
+    // that were never written read as 127 (their codes as zero)
+    const int valid = (a.cols + 15) / 16;
+    bool marked = false;
+#pragma unroll
+    for (int r = 0; r < PR; ++r) {
+      const int u = r * 64 + lane, i = u / 24, v = u % 24;
+      if (i < NSW) *reinterpret_cast<u32x4*>(&lds_c[wave][i][16 * v]) = pc[r];
+    }
+#pragma unroll
+    for (int r = 0; r < (int)(sizeof(pe) / 4); ++r) {
+      const int u = r * 64 + lane, i = u / (kChunkExpBytes / 4), v = u % (kChunkExpBytes / 4);
+      uint32_t w = pe[r];
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int piece = 8 * (s0 + i) + ((4 * v + b) & 7);
+        const uint32_t e = (w >> (8 * b)) & 0xFFu;
+        if (piece >= valid) w = (w & ~(0xFFu << (8 * b))) | (127u << (8 * b));
+        else marked |= i < ns && e == kNonFinite;
+      }
+      if (i < NSW) *reinterpret_cast<uint32_t*>(&lds_e[wave][i][4 * v]) = w;
+    }
+    bad = __ballot(marked) != 0;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+
+  // 4. one MFMA per chunk and matrix, or the exact VALU sums
+  float p0[MATS], p1[MATS];
+  if (!bad) {
+    // A fragments from LDS (lanes of rows 0-5 only), read one chunk ahead of
+    // their MFMA
+    auto read_a = [&](int i, v8i& A, int& asc) {
+      A = v8i{0, 0, 0, 0, 0, 0, 0, 0};
+      asc = 127;
+      if (arow) {
+        if (adata) {
+          const int4 lo = *reinterpret_cast<const int4*>(&lds_c[wave][i][at * 128 + g * 32]);
+          const int4 hi = *reinterpret_cast<const int4*>(&lds_c[wave][i][at * 128 + g * 32 + 16]);
+          A = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+        }
+        asc = lds_e[wave][i][at * 8 + 2 * g + ah];
+      }
+    };
+    v8i A[2];
+    int asc[2];
+    read_a(0, A[0], asc[0]);
+    v4f acc[MATS];
+#pragma unroll
+    for (int m = 0; m < MATS; ++m) acc[m] = v4f{0.f, 0.f, 0.f, 0.f};
+    static_for<0, NSW>([&](auto I) {
+      constexpr int i = decltype(I)::value;
+      if (i < ns) {
+        if constexpr (i + 1 < NSW) read_a(i + 1, A[(i + 1) & 1], asc[(i + 1) & 1]);
+        const int s = s0 + i;
+#pragma unroll
+        for (int m = 0; m < MATS; ++m) {
+          v8i B;
+          if constexpr (FP4) B = v8i{(int)wl[m][i].x, (int)wl[m][i].y, (int)wl[m][i].z, (int)wl[m][i].w, 0, 0, 0, 0};
+          else B = v8i{(int)wl[m][i].x, (int)wl[m][i].y, (int)wl[m][i].z, (int)wl[m][i].w,
+                       (int)wh[m][i].x, (int)wh[m][i].y, (int)wh[m][i].z, (int)wh[m][i].w};
+          int wsc = 127;
+          if constexpr (BLK) wsc = (int)((we[m][(s >> 2) - (s0 >> 2)] >> (8 * (s & 3))) & 0xFFu);
+          acc[m] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[i & 1], B, acc[m], 0, wfmt<DT>(), 0,
+                                                                   asc[i & 1], 0, wsc);
+        }
+      }
+    });
+#pragma unroll
+    for (int m = 0; m < MATS; ++m) {
+      p0[m] = (acc[m][0] + acc[m][1]) + (acc[m][2] + acc[m][3]);  // g = 0: rows 0-3
+      p1[m] = acc[m][0] + acc[m][1];                                // g = 1: rows 4-5
+    }
+  } else {
+    // the weights are read again here, so the registers above are dead on
+    // this path
+#pragma unroll
+    for (int m = 0; m < MATS; ++m) {
+      const uint8_t* f = a.codesf[m] + (size_t)rb * S * (H * 1024) + lane * 16;
+      float s_ = 0.0f;
+#pragma unroll 1
+      for (int s = s0; s < s1; ++s) {
+        float s_lo = 1.0f, s_hi = 1.0f;
+        if constexpr (BLK) {
+          // lane (n, g) takes the exponent of block g of chunk s; its FP4
+          // nibbles are block g, its FP8 bytes blocks g / 2 (bytes 0-15) and
+          // 2 + g / 2 (bytes 16-31), whose exponents other lanes take
+          const int groups = (S + 3) / 4;
+          const int e = a.blkf[m][(((size_t)rb * groups + (s >> 2)) * 64 + lane) * 4 + (s & 3)];
+          if constexpr (FP4) {
+            s_lo = pow2f(e - 127);
+          } else {
+            s_lo = pow2f(__shfl(e, n + 16 * (g >> 1), 64) - 127);
+            s_hi = pow2f(__shfl(e, n + 16 * (2 + (g >> 1)), 64) - 127);
+          }
+        }
+        s_ += exact_slice<DT>(f + (size_t)s * (H * 1024), a.x, 128 * s, g, a.cols, s_lo, s_hi);
+      }
+      // the four lane groups of row n
+      s_ += __shfl_xor(s_, 16, 64);
+      s_ += __shfl_xor(s_, 32, 64);
+      p0[m] = s_;
+      p1[m] = 0.0f;
+    }
+  }
+  if (g < 2) {
+#pragma unroll
+    for (int m = 0; m < MATS; ++m) part[wave][m][n][g] = g == 0 ? p0[m] : p1[m];
+  }
+  __syncthreads();
+
+  // 5. epilogue in wave 0: lane l computes row n0 + l % 16 (the four lane
+  // groups alike, so that the 16-lane DPP maxima below run with every lane
+  // active); lanes 0-15 store
+  if (wave != 0) return;
+  const int o = n0 + n;
+  const bool store = g == 0;
+  float tot[MATS];
+#pragma unroll
+  for (int m = 0; m < MATS; ++m) {
+    float sum = part[0][m][n][0] + part[0][m][n][1];
+#pragma unroll
+    for (int w = 1; w < W; ++w) sum += part[w][m][n][0] + part[w][m][n][1];
+    tot[m] = sum * rs[m];
+  }
+  if constexpr (MATS == 2) {
+    const float gt = (float)act_f64(kSilu, (double)tot[0]);
+    const float h = (float)((double)gt * (double)tot[1]);
+    if (store && o < a.rows) a.pre[o] = h;
+    if constexpr (NEXT) {
+      // the three-term split of this piece (outputs n0 .. n0 + 15) for the
+      // next product
+      float v = o < a.rows ? h : 0.0f;
+      auto piece_max = [&](float t) {
+        t = fmaxf(t, xor_lane<1>(t, lane));
+        t = fmaxf(t, xor_lane<2>(t, lane));
+        t = fmaxf(t, xor_lane<4>(t, lane));
+        return fmaxf(t, xor_lane<8>(t, lane));
+      };
+      const float am0 = piece_max(finite_amax(fabsf(v)) ? fabsf(v) : __builtin_inff());  // NaN as inf
+      const int s = rb >> 3, p = rb & 7;
+      uint8_t* codes = a.next + (size_t)s * kChunkCodeBytes + (p & 3) * 32 + 16 * (p >> 2);
+      uint8_t* exps = a.next + (size_t)a.next_steps * kChunkCodeBytes + (size_t)s * kChunkExpBytes + p;
+      // the terms' 16 code bytes each meet in LDS (the reduction's buffer,
+      // read above by this wave only), then lanes 0-2 store 16 bytes each
+      uint8_t* gather = reinterpret_cast<uint8_t*>(&part[0][0][0][0]);
+      if (!finite_amax(am0)) {
+        if (lane == 0) {
+#pragma unroll
+          for (int t = 0; t < kTermsMx; ++t) exps[t * 8] = kNonFinite;
+        }
+      } else {
+        float am = am0;
+#pragma unroll
+        for (int t = 0; t < kTermsMx; ++t) {
+          if (t > 0) am = piece_max(fabsf(v));
+          const int e = e8m0_exponent(am, 448.0f);
+          const float sc = pow2f(e);
+          v2s w = {0, 0};
+          w = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(w, v, 0.0f, sc, false);
+          const int code = __builtin_bit_cast(int, w) & 0xFF;
+          if (store) gather[t * 16 + n] = (uint8_t)code;
+          if (t + 1 < kTermsMx) v -= __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(code, sc, false)[0];
+          if (lane == 0) exps[t * 8] = (uint8_t)(e + 127);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (lane < kTermsMx)
+          *reinterpret_cast<int4*>(codes + lane * 128) = *reinterpret_cast<const int4*>(gather + lane * 16);
+      }
+    }
+  } else {
+    if (!store || o >= a.rows) return;
+    float y = tot[0];
+    if (a.need_epi) {
+      double v = (double)y;
+      if (a.bias && o < a.bias_len) {
+        v += bias;
+        y = (float)v;
+      }
+      a.pre[o] = y;
+      a.post[o] = (float)act_f64(a.act, v);
+    } else {
+      a.pre[o] = y;
+      if (a.post && a.post != a.pre) a.post[o] = y;
+    }
+  }
+}
+
+// Waves per workgroup and chunks per wave for kpad / 128 = S chunks (chunks
+// past a wave's range are loaded again and not used, so the step count
+// tracks S / W closely). A wave holds all its weight operands in registers,
+// so 16 waves (128 VGPRs each) take 8 chunks only of one FP4 matrix, 4 of
+// one FP8 matrix or of two FP4 matrices; two FP8 matrices run 8 waves
+// (S <= 32) only.
+constexpr int max_chunks(int dtype, int mats) {
+  return dtype == kFP4 ? (mats == 1 ? 128 : 64) : (mats == 1 ? 64 : 32);
+}
+
+template <int DT, bool BLK, int MATS, int W, int NSW, bool PRE, bool NEXT>
+Status launch_t(const GemvMxArgs& a, hipStream_t st) {
+  const unsigned grid = (unsigned)((a.rows + 15) / 16);
+  k_gemv_mx<DT, BLK, MATS, W, NSW, PRE, NEXT><<<grid, 64 * W, 0, st>>>(a);
+  return hip_status(hipGetLastError(), "gemv_mx launch");
+}
+
+template <int DT, bool BLK, int MATS, bool PRE, bool NEXT>
+Status launch_shape(const GemvMxArgs& a, hipStream_t st) {
+  const int S = a.kpad / 128;
+  if (S <= 32) return launch_t<DT, BLK, MATS, 8, 4, PRE, NEXT>(a, st);
+  if constexpr (DT == kFP4 || MATS == 1)
+    if (S <= 64) return launch_t<DT, BLK, MATS, 16, 4, PRE, NEXT>(a, st);
+  if constexpr (DT == kFP4 && MATS == 1) {
+    if (S <= 96) return launch_t<DT, BLK, MATS, 16, 6, PRE, NEXT>(a, st);
+    return launch_t<DT, BLK, MATS, 16, 8, PRE, NEXT>(a, st);
+  }
+  return Status::err(kUnsupported, "gemv_mx: K");
+}
+
+template <int DT, bool BLK>
+Status launch_dt(const GemvMxArgs& a, hipStream_t st) {
+  if (a.mats == 2) {
+    return a.next ? launch_shape<DT, BLK, 2, false, true>(a, st)
+                  : launch_shape<DT, BLK, 2, false, false>(a, st);
+  }
+  return a.asplit ? launch_shape<DT, BLK, 1, true, false>(a, st)
+                  : launch_shape<DT, BLK, 1, false, false>(a, st);
+}
+
+}  // namespace
+
+bool gemv_mx_fits(int dtype, int rows, int kpad, int mats) {
+  if (dtype != kE4M3 && dtype != kE5M2 && dtype != kFP4) return false;
+  const int S = kpad / 128;
+  // whole-GPU grids only (one workgroup per 16 rows per CU or more), and K
+  // ranges that the instantiated shapes cover
+  return mats >= 1 && mats <= 2 && (rows + 15) / 16 >= 256 && S >= 16 &&
+         S <= max_chunks(dtype, mats) && kpad % 128 == 0;
+}
+
+size_t gemv_mx_split_bytes(int kpad) {
+  const size_t S = (size_t)kpad / 128;
+  return S * (kChunkCodeBytes + kChunkExpBytes);
+}
+
+Status launch_gemv_mx(const GemvMxArgs& a, int dtype, bool blk, hipStream_t st) {
+  if (!gemv_mx_fits(dtype, a.rows, a.kpad, a.mats) || !a.codesf[0] || !a.scale[0] || !a.pre ||
+      (a.mats == 2 && (!a.codesf[1] || !a.scale[1])) || (blk && (!a.blkf[0] || (a.mats == 2 && !a.blkf[1]))) ||
+      !a.x || (a.asplit && (a.mats != 1 || a.asplit_steps < a.kpad / 128)) ||
+      // the split of x reads 16-byte vectors
+      (!a.asplit && (a.cols % 4 != 0 || (reinterpret_cast<uintptr_t>(a.x) & 15u) != 0)) ||
+      (a.next && (a.mats != 2 || a.next_steps < (a.rows + 127) / 128)) ||
+      (a.mats == 1 && a.need_epi && !a.post))
+    return Status::err(kInvalid, "gemv_mx: arguments");
+  switch (dtype) {
+  case kE4M3: return blk ? launch_dt<kE4M3, true>(a, st) : launch_dt<kE4M3, false>(a, st);
+  case kE5M2: return blk ? launch_dt<kE5M2, true>(a, st) : launch_dt<kE5M2, false>(a, st);
+  case kFP4: return blk ? launch_dt<kFP4, true>(a, st) : launch_dt<kFP4, false>(a, st);
+  }
+  return Status::err(kUnsupported, "gemv_mx: dtype");
+}
+
+}  // namespace wv

@@ -123,6 +123,40 @@ struct MxvArgs {
 };
 Status launch_mxv(const MxvArgs& a, int dtype, bool blk, hipStream_t st);
 
+// ---- batch-1 GEMV on the scaled MFMA over operand-order weights (gemv_mx.hip) ----
+// x as three E4M3 terms per 16-element piece in the rows of the A operand;
+// the weights from DeviceWeights::codes_frag (and blk_frag). The pre-split
+// input image (asplit / next) holds, per K chunk of 128, the term codes
+// [3][4 lane groups][32 B] (piece p of the chunk at lane group p & 3, byte
+// 16 (p >> 2)), and after all `steps` chunks the exponents [steps][3][8]
+// (E8M0 + 127 per term and piece; 0xFF marks a non-finite piece).
+struct GemvMxArgs {
+  const uint8_t* codesf[2] = {nullptr, nullptr};
+  const uint8_t* blkf[2] = {nullptr, nullptr};
+  const float* scale[2] = {nullptr, nullptr};
+  int mats = 1;
+  int kpad = 0, cols = 0, rows = 0;
+  // fp32 input [cols], 16-byte aligned with cols % 4 == 0 unless asplit is
+  // given (then read only by the non-finite fallback)
+  const float* x = nullptr;
+  const uint8_t* asplit = nullptr;  // pre-split x (one matrix), or null
+  int asplit_steps = 0;
+  uint8_t* next = nullptr;   // two matrices: the split of h written here, or null
+  int next_steps = 0;
+  float* pre = nullptr;
+  float* post = nullptr;
+  int act = kLinear;
+  int need_epi = 0;
+  const double* bias = nullptr;
+  int bias_len = 0;
+};
+// Shapes the kernel runs: FP8/FP4, at least 256 row blocks of 16, 16..128
+// K chunks of 128.
+bool gemv_mx_fits(int dtype, int rows, int kpad, int mats);
+// Bytes of a pre-split input image over kpad columns.
+size_t gemv_mx_split_bytes(int kpad);
+Status launch_gemv_mx(const GemvMxArgs& a, int dtype, bool blk, hipStream_t st);
+
 // ---- batched GEMM on the scaled MFMA (mxg.hip) ----
 // Activations are split into kTerms terms with per-32 E8M0 scales (two or one
 // for one-matrix products that ask for them: less residual precision, less
