@@ -566,7 +566,8 @@ def make_workload(pw, hip, config, copies, terms=3, batch=1, keep_inner=False):
     two = {1: 32, 2: 16}.get(terms, 0)  # backend bit for two (16) or one (32) activation terms
     tname = {1: "_1term", 2: "_2terms"}.get(terms, "")
     if config == "c2":
-        return dense_workload(pw, hip, "dense_gemv_4096x4096_fp8e4m3_rowscale_b1", 2, 4, 2, 1,
+        b = max(1, batch)
+        return dense_workload(pw, hip, f"dense_gemv_4096x4096_fp8e4m3_rowscale_b{b}", 2, 4, 2, b,
                               4096, 4096, copies, "hbm")
     if config == "c1":
         return dense_workload(pw, hip, "dense_512x512_fp8e4m3_tensorscale_b1", 1, 4, 1, 1,
@@ -905,7 +906,7 @@ def main():
     ap.add_argument("--config", default="c2", choices=CONFIGS)
     ap.add_argument("--copies", type=int, default=64)
     ap.add_argument("--batch", type=int, default=1,
-                    help="batch rows of the packed-format GEMV configs (gemv_<fmt>)")
+                    help="batch rows of c2 and of the packed-format GEMV configs (gemv_<fmt>)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--terms", type=int, default=3, choices=(1, 2, 3),
                     help="activation terms of the matrix-core GEMMs (c4, c4mha, c5, c5chain): "

@@ -56,6 +56,8 @@ def assert_ieee_match(got, want, tol):
     (16, 0, 4200, 2048, 0, False),    # 16 chunks (the fewest), ReLU
     (4, 3, 4096, 8192, -1, False),    # E4M3 with E8M0 blocks, 64 chunks
     (16, 3, 4096, 16384, -1, False),  # 128 chunks (the most)
+    (16, 3, 4096, 13000, -1, False),  # 102 chunks: 16 waves of 6 or 7 in ranges of 8
+    (5, 3, 4096, 5000, 2, True),      # E5M2 with E8M0 blocks, 40 chunks; bias + GELU
     (5, 2, 4096, 2050, 3, False),     # cols % 4 != 0: stays on the VALU GEMV (x read as vectors); tanh
 ])
 def test_dense_batch1_matches_oracle(gpu, oracle, dt, scheme, rows, cols, act, with_bias):
