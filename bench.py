@@ -573,7 +573,8 @@ def make_workload(pw, hip, config, copies, terms=3, batch=1, keep_inner=False):
         return dense_workload(pw, hip, "dense_512x512_fp8e4m3_tensorscale_b1", 1, 4, 1, 1,
                               512, 512, copies, "hbm")
     if config == "c3":
-        return swiglu_workload(pw, hip, "swiglu_4096x11008_fp4_e8m0_b1", 1, min(copies, 8))
+        b = max(1, batch)
+        return swiglu_workload(pw, hip, f"swiglu_4096x11008_fp4_e8m0_b{b}", b, min(copies, 8))
     if config == "c3b16":
         return swiglu_workload(pw, hip, "swiglu_4096x11008_fp4_e8m0_b16", 16, min(copies, 8))
     if config == "c4":
@@ -906,7 +907,7 @@ def main():
     ap.add_argument("--config", default="c2", choices=CONFIGS)
     ap.add_argument("--copies", type=int, default=64)
     ap.add_argument("--batch", type=int, default=1,
-                    help="batch rows of c2 and of the packed-format GEMV configs (gemv_<fmt>)")
+                    help="batch rows of c2, c3 and of the packed-format GEMV configs (gemv_<fmt>)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--terms", type=int, default=3, choices=(1, 2, 3),
                     help="activation terms of the matrix-core GEMMs (c4, c4mha, c5, c5chain): "

@@ -158,3 +158,102 @@ def test_swiglu_batch1_nonfinite_x(gpu, oracle):
     assert_ieee_match(h, oh, TOL_MFMA)
     oy_own, _ = oracle.dense(Dd, h)
     assert_ieee_match(y, oy_own, TOL_MFMA)
+
+
+# 2-4 batch rows: six A rows per batch row (two halves x three terms), one
+# MFMA per weight fragment for 2 rows, two for 3-4
+@pytest.mark.parametrize("batch", [2, 3, 4])
+@pytest.mark.parametrize("dt,scheme,rows,cols,act,with_bias", [
+    (4, 2, 4096, 4096, -1, False),    # 32 chunks, 8 waves of 4
+    (5, 1, 4100, 3000, 1, True),      # ragged rows and K; bias + SiLU
+    (16, 3, 4096, 11008, -1, False),  # SwiGLU down shape: 16 waves of <= 6
+    (4, 3, 4096, 8192, -1, False),    # E4M3 with E8M0 blocks, 16 waves of 4
+    (16, 3, 4096, 16384, 0, False),   # 128 chunks: 16 waves of 8 (4 rows: stays on the VALU kernel); ReLU
+])
+def test_dense_rows_matches_oracle(gpu, oracle, batch, dt, scheme, rows, cols, act, with_bias):
+    rng = np.random.default_rng(rows + cols + dt + scheme + batch)
+    W = (rng.standard_normal((rows, cols)) / np.sqrt(cols)).astype(np.float32)
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    x[-1] *= 1e3  # batch rows of different magnitudes
+    bias = rng.standard_normal(rows) * 0.1 if with_bias else None
+    pre, post = run_dense(gpu, dt, scheme, W, x, act, bias)
+    o_pre, o_post = oracle.dense(dequant(oracle, dt, scheme, W), x, act, bias, threads=8)
+    for b in range(batch):
+        assert rel_l2(pre[b], o_pre[b]) <= TOL_MFMA, (b, rel_l2(pre[b], o_pre[b]))
+        assert rel_l2(post[b], o_post[b]) <= TOL_MFMA, b
+
+
+@pytest.mark.parametrize("batch", [2, 3, 4])
+def test_dense_rows_integer_exact(gpu, oracle, batch):
+    rng = np.random.default_rng(batch)
+    rows, cols = 4100, 3000
+    W = rng.choice(np.array([-6, -4, -3, -1.5, -0.5, 0, 0.5, 1, 2, 6], np.float32), (rows, cols))
+    x = rng.integers(-4, 5, (batch, cols)).astype(np.float32)
+    pre, _ = run_dense(gpu, 16, 0, W, x)
+    o_pre, _ = oracle.dense(dequant(oracle, 16, 0, W), x)
+    assert np.array_equal(pre, o_pre)
+
+
+@pytest.mark.parametrize("batch", [2, 4])
+def test_dense_rows_nonfinite_x(gpu, oracle, batch):
+    """inf in one batch row only: the waves whose K range holds it sum all
+    batch rows on the VALU, the other batch rows keep finite results."""
+    rows, cols = 4096, 4096
+    rng = np.random.default_rng(batch + 100)
+    W = (rng.standard_normal((rows, cols)) / np.sqrt(cols)).astype(np.float32)
+    Wd = dequant(oracle, 4, 2, W)
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    x[1, 700] = np.inf
+    x[batch - 1, 3000] = np.nan
+    pre, _ = run_dense(gpu, 4, 2, W, x)
+    o_pre, _ = oracle.dense(Wd, x)
+    for b in range(batch):
+        assert_ieee_match(pre[b], o_pre[b], TOL_MFMA)
+
+
+@pytest.mark.parametrize("rows", [2, 3, 4])
+@pytest.mark.parametrize("dt,scheme,d,inter", [
+    (16, 3, 4096, 11008),  # the C3 shapes: the down reads the pair's split over 86 chunks
+    (4, 2, 4096, 4196),    # FP8 pair; last piece ragged
+])
+def test_swiglu_rows_matrix_core(gpu, oracle, rows, dt, scheme, d, inter):
+    rng = np.random.default_rng(d + inter + dt + rows)
+    G = (rng.standard_normal((inter, d)) / np.sqrt(d)).astype(np.float32)
+    U = (rng.standard_normal((inter, d)) / np.sqrt(d)).astype(np.float32)
+    D = (rng.standard_normal((d, inter)) / np.sqrt(inter)).astype(np.float32)
+    s = gpu.SwiGLUSession(rows, 1, d, inter, dt, scheme, G, U, D)
+    try:
+        for rep in range(2):
+            x = rng.standard_normal((rows, d)).astype(np.float32)
+            x[0] *= 1e-3
+            h, y = s.execute(x)
+            oh, oy, Dd = oracle_swiglu(oracle, dt, scheme, G, U, D, x)
+            oy_own, _ = oracle.dense(Dd, h, threads=8)
+            for b in range(rows):
+                assert rel_l2(h[b], oh[b]) <= TOL_MFMA, (rep, b, rel_l2(h[b], oh[b]))
+                assert rel_l2(y[b], oy_own[b]) <= TOL_MFMA, (rep, b, rel_l2(y[b], oy_own[b]))
+                assert rel_l2(y[b], oy[b]) <= 2 * TOL_MFMA
+    finally:
+        s.close()
+
+
+def test_swiglu_rows_nonfinite_x(gpu, oracle):
+    """inf in the second of three batch rows: its pieces of h carry the
+    non-finite mark, the other rows' pieces are split as usual."""
+    d, inter, rows = 4096, 4196, 3
+    rng = np.random.default_rng(12)
+    G = (rng.standard_normal((inter, d)) / np.sqrt(d)).astype(np.float32)
+    U = (rng.standard_normal((inter, d)) / np.sqrt(d)).astype(np.float32)
+    D = (rng.standard_normal((d, inter)) / np.sqrt(inter)).astype(np.float32)
+    x = rng.standard_normal((rows, d)).astype(np.float32)
+    x[1, 1000] = np.inf
+    s = gpu.SwiGLUSession(rows, 1, d, inter, 4, 2, G, U, D)
+    try:
+        h, y = s.execute(x)
+    finally:
+        s.close()
+    oh, _, Dd = oracle_swiglu(oracle, 4, 2, G, U, D, x)
+    oy_own, _ = oracle.dense(Dd, h)
+    for b in range(rows):
+        assert_ieee_match(h[b], oh[b], TOL_MFMA)
+        assert_ieee_match(y[b], oy_own[b], TOL_MFMA)

@@ -153,62 +153,83 @@ __device__ float exact_slice(const uint8_t* w, const float* x, int k0, int g, in
   return s;
 }
 
-// PRE: the input is a pre-split image (a.asplit); otherwise the waves split
-// a.x themselves. NEXT (MATS == 2): write the split of h to a.next.
-template <int DT, bool BLK, int MATS, int W, int NSW, bool PRE, bool NEXT>
+// NB batch rows (1..4). Row r = 6 b + 3 h + t of the A operand rows of all
+// MFMAs (MFMA j takes rows 16 j .. 16 j + 15) holds term t of half h of
+// batch row b, so NMF = ceil(6 NB / 16) MFMAs per weight fragment: one for
+// 1-2 rows, two for 3-4. Accumulator lane (n, g) of MFMA j holds rows
+// 16 j + 4 g .. + 3 of column n, of one batch row or (when 16 j + 4 g is
+// 2 mod 6 ... rows 2-3 past a multiple of 6) split two and two between
+// consecutive batch rows.
+// PRE: the input is a pre-split image per batch row (a.asplit); otherwise the
+// waves split a.x themselves. NEXT (MATS == 2): write the split of h to
+// a.next.
+template <int DT, bool BLK, int MATS, int NB, int W, int NSW, bool PRE, bool NEXT>
 __global__ __launch_bounds__(64 * W) void k_gemv_mx(GemvMxArgs a) {
   constexpr bool FP4 = DT == kFP4;
-  constexpr int XR = (NSW * 16 + 63) / 64;  // split rounds of 64 items (8 values each)
+  constexpr int NMF = (6 * NB + 15) / 16;  // MFMAs per weight fragment
+  constexpr int XI = NSW * 16;             // split items (8 values) per batch row
+  constexpr int XR = (NB * XI + 63) / 64;  // split rounds of 64 items
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 15, g = lane >> 4;
   const int S = a.kpad / 128;
   const int s0 = wave * S / W, s1 = (wave + 1) * S / W, ns = s1 - s0;
   const int rb = blockIdx.x, n0 = 16 * rb;
-  // A-operand row of this lane: term t of half h; rows 6..15 are zero
-  const int ah = n >= 3 ? 1 : 0, at = n - 3 * ah;
-  const bool arow = n < 6, adata = arow && (g & 1) == ah;
+  // bytes of one batch row's pre-split image
+  const size_t img = (size_t)(PRE ? a.asplit_steps : a.next_steps) * (kChunkCodeBytes + kChunkExpBytes);
 
-  __shared__ __attribute__((aligned(16))) uint8_t lds_c[W][NSW][kChunkCodeBytes];
-  __shared__ __attribute__((aligned(16))) uint8_t lds_e[W][NSW][kChunkExpBytes];
-  __shared__ float part[W][MATS][16][2];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_c[W][NSW][NB][kChunkCodeBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_e[W][NSW][NB][kChunkExpBytes];
+  // the waves' partial sums: one batch row in a buffer of their own; more
+  // rows in each wave's staging region, dead once its MFMAs are issued
+  constexpr int PARTF = MATS * NMF * 4 * 16 * 2;  // floats per wave (NB > 1)
+  static_assert(NB == 1 || PARTF * 4 + NB * 48 <= NSW * NB * kChunkCodeBytes, "partials fit the staging");
+  __shared__ float part[NB == 1 ? W : 1][MATS][16][2];
+  auto part_w = [&](int w) { return reinterpret_cast<float*>(&lds_c[w][0][0][0]); };
 
-  // 1. the input: this wave's chunks of the pre-split image (16-byte pieces:
+  // 1. the input: this wave's chunks of the pre-split images (16-byte pieces:
   // 24 per chunk of codes, then the exponents), or x for the split below
-  constexpr int PR = (NSW * (kChunkCodeBytes / 16) + 63) / 64;
+  constexpr int PU = NSW * (kChunkCodeBytes / 16);  // code pieces per batch row
+  constexpr int EU = NSW * (kChunkExpBytes / 4);    // exponent dwords per batch row
+  constexpr int PR = (NB * PU + 63) / 64;
   u32x4 pc[PRE ? PR : 1];
-  uint32_t pe[PRE ? (NSW * kChunkExpBytes / 4 + 63) / 64 : 1];
+  uint32_t pe[PRE ? (NB * EU + 63) / 64 : 1];
   float4 xv[PRE ? 1 : XR][2];
   if constexpr (PRE) {
     const int SA = a.asplit_steps;
     const int valid = (a.cols + 15) / 16;  // pieces ever written
 #pragma unroll
     for (int r = 0; r < PR; ++r) {
-      const int u = r * 64 + lane, i = u / 24, v = u % 24;  // chunk, 16-byte piece of its codes
+      // batch row b, chunk i, 16-byte piece v of its codes
+      const int u = r * 64 + lane, b = NB == 1 ? 0 : u / PU, i = (u - b * PU) / 24, v = (u - b * PU) % 24;
       // v = 2 (4 t + g) + hi: piece 8 s + g + 4 hi of term t
       const int s = s0 + (i < ns ? i : 0), pc_piece = 8 * s + ((v >> 1) & 3) + 4 * (v & 1);
       // every load unconditional (from a clamped address, then selected):
       // a branch around a load makes the compiler wait for all loads at the join
-      const u32x4 t = *reinterpret_cast<const u32x4*>(a.asplit + (size_t)s * kChunkCodeBytes + 16 * v);
-      const bool live = i < ns && pc_piece < valid;
+      const u32x4 t = *reinterpret_cast<const u32x4*>(a.asplit + (b < NB ? b : 0) * img +
+                                                      (size_t)s * kChunkCodeBytes + 16 * v);
+      const bool live = b < NB && i < ns && pc_piece < valid;  // NB == 1: i < ns covers the tail
       pc[r] = live ? t : u32x4{0u, 0u, 0u, 0u};
     }
 #pragma unroll
     for (int r = 0; r < (int)(sizeof(pe) / 4); ++r) {
-      const int u = r * 64 + lane, i = u / (kChunkExpBytes / 4), v = u % (kChunkExpBytes / 4);
+      const int u = r * 64 + lane, b = NB == 1 ? 0 : u / EU, i = (u - b * EU) / (kChunkExpBytes / 4),
+                v = (u - b * EU) % (kChunkExpBytes / 4);
       const uint32_t t = *reinterpret_cast<const uint32_t*>(
-          a.asplit + (size_t)SA * kChunkCodeBytes + (size_t)(s0 + (i < ns ? i : 0)) * kChunkExpBytes + 4 * v);
-      pe[r] = i < ns ? t : 0x7F7F7F7Fu;
+          a.asplit + (b < NB ? b : 0) * img + (size_t)SA * kChunkCodeBytes +
+          (size_t)(s0 + (i < ns ? i : 0)) * kChunkExpBytes + 4 * v);
+      pe[r] = b < NB && i < ns ? t : 0x7F7F7F7Fu;
     }
   } else {
 #pragma unroll
     for (int r = 0; r < XR; ++r) {
-      const int it = r * 64 + lane, i = it >> 4, q = it & 15;
+      const int it = r * 64 + lane, b = NB == 1 ? 0 : it / XI, i = (it - b * XI) >> 4, q = it & 15;
       const int k = (s0 + i) * 128 + 8 * q;
       // x 16-byte aligned and cols % 4 == 0 (launch_gemv_mx checks): the
       // two float4 of an item are wholly inside or outside [0, cols)
-      const bool live0 = i < ns && k < a.cols, live1 = i < ns && k + 4 < a.cols;
-      const float4 t0 = *reinterpret_cast<const float4*>(a.x + (live0 ? k : 0));
-      const float4 t1 = *reinterpret_cast<const float4*>(a.x + (live1 ? k + 4 : 0));
+      const bool live0 = b < NB && i < ns && k < a.cols, live1 = b < NB && i < ns && k + 4 < a.cols;
+      const float* xb = a.x + (size_t)(b < NB ? b : 0) * a.cols;
+      const float4 t0 = *reinterpret_cast<const float4*>(xb + (live0 ? k : 0));
+      const float4 t1 = *reinterpret_cast<const float4*>(xb + (live1 ? k + 4 : 0));
       const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
       xv[r][0] = live0 ? t0 : z;
       xv[r][1] = live1 ? t1 : z;
@@ -256,7 +277,10 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mx(GemvMxArgs a) {
     bool nonfinite = false;
 #pragma unroll
     for (int r = 0; r < XR; ++r) {
-      const int it = r * 64 + lane, i = it >> 4, q = it & 15, p = q >> 1;
+      const int it = r * 64 + lane, b = NB == 1 ? 0 : it / XI, i = (it - b * XI) >> 4, q = it & 15, p = q >> 1;
+      // staged item: one batch row stages chunks i < NSW (the last round's
+      // tail is past them)
+      const bool staged = NB == 1 ? i < NSW : b < NB;
       float v[8] = {xv[r][0].x, xv[r][0].y, xv[r][0].z, xv[r][0].w,
                     xv[r][1].x, xv[r][1].y, xv[r][1].z, xv[r][1].w};
       const int cb = (p & 3) * 32 + 16 * (p >> 2) + 8 * (q & 1);
@@ -275,12 +299,12 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mx(GemvMxArgs a) {
         am = pair_max(am);
         const int e = e8m0_exponent(am, 448.0f);
         const int2 c = term8(v, pow2f(e), t + 1 < kTermsMx);
-        if (i < NSW) *reinterpret_cast<int2*>(&lds_c[wave][i][t * 128 + cb]) = c;
+        if (staged) *reinterpret_cast<int2*>(&lds_c[wave][i][b][t * 128 + cb]) = c;
         eb |= (uint32_t)(e + 127) << (8 * t);
       }
-      if ((q & 1) == 0 && i < NSW) {
+      if ((q & 1) == 0 && staged) {
 #pragma unroll
-        for (int t = 0; t < kTermsMx; ++t) lds_e[wave][i][t * 8 + p] = (uint8_t)(eb >> (8 * t));
+        for (int t = 0; t < kTermsMx; ++t) lds_e[wave][i][b][t * 8 + p] = (uint8_t)(eb >> (8 * t));
       }
     }
     bad = __ballot(nonfinite) != 0;
@@ -295,21 +319,22 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mx(GemvMxArgs a) {
     bool marked = false;
 #pragma unroll
     for (int r = 0; r < PR; ++r) {
-      const int u = r * 64 + lane, i = u / 24, v = u % 24;
-      if (i < NSW) *reinterpret_cast<u32x4*>(&lds_c[wave][i][16 * v]) = pc[r];
+      const int u = r * 64 + lane, b = NB == 1 ? 0 : u / PU, i = (u - b * PU) / 24, v = (u - b * PU) % 24;
+      if (NB == 1 ? i < NSW : b < NB) *reinterpret_cast<u32x4*>(&lds_c[wave][i][b][16 * v]) = pc[r];
     }
 #pragma unroll
     for (int r = 0; r < (int)(sizeof(pe) / 4); ++r) {
-      const int u = r * 64 + lane, i = u / (kChunkExpBytes / 4), v = u % (kChunkExpBytes / 4);
+      const int u = r * 64 + lane, b = NB == 1 ? 0 : u / EU, i = (u - b * EU) / (kChunkExpBytes / 4),
+                v = (u - b * EU) % (kChunkExpBytes / 4);
       uint32_t w = pe[r];
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const int piece = 8 * (s0 + i) + ((4 * v + b) & 7);
-        const uint32_t e = (w >> (8 * b)) & 0xFFu;
-        if (piece >= valid) w = (w & ~(0xFFu << (8 * b))) | (127u << (8 * b));
-        else marked |= i < ns && e == kNonFinite;
+      for (int c = 0; c < 4; ++c) {
+        const int piece = 8 * (s0 + i) + ((4 * v + c) & 7);
+        const uint32_t e = (w >> (8 * c)) & 0xFFu;
+        if (piece >= valid) w = (w & ~(0xFFu << (8 * c))) | (127u << (8 * c));
+        else marked |= b < NB && i < ns && e == kNonFinite;
       }
-      if (i < NSW) *reinterpret_cast<uint32_t*>(&lds_e[wave][i][4 * v]) = w;
+      if (NB == 1 ? i < NSW : b < NB) *reinterpret_cast<uint32_t*>(&lds_e[wave][i][b][4 * v]) = w;
     }
     bad = __ballot(marked) != 0;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -317,29 +342,47 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mx(GemvMxArgs a) {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
 
-  // 4. one MFMA per chunk and matrix, or the exact VALU sums
-  float p0[MATS], p1[MATS];
+  // 4. NMF MFMAs per chunk and matrix, or the exact VALU sums. Lane (n, g)
+  // of MFMA j sums into batch row bl[j] (its rows 0-3, or rows 0-1 when
+  // two[j]) and bl[j] + 1 (rows 2-3 when two[j]).
+  float plo[MATS][NMF], phi[MATS][NMF];
   if (!bad) {
-    // A fragments from LDS (lanes of rows 0-5 only), read one chunk ahead of
-    // their MFMA
-    auto read_a = [&](int i, v8i& A, int& asc) {
-      A = v8i{0, 0, 0, 0, 0, 0, 0, 0};
-      asc = 127;
-      if (arow) {
-        if (adata) {
-          const int4 lo = *reinterpret_cast<const int4*>(&lds_c[wave][i][at * 128 + g * 32]);
-          const int4 hi = *reinterpret_cast<const int4*>(&lds_c[wave][i][at * 128 + g * 32 + 16]);
-          A = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+    // A row 16 j + n: batch row ab[j], half ah[j], term at[j]; rows past
+    // 6 NB are zero
+    int ab[NMF], ah[NMF], at[NMF];
+    bool arow[NMF], adata[NMF];
+#pragma unroll
+    for (int j = 0; j < NMF; ++j) {
+      const int r = 16 * j + n;
+      ab[j] = r / 6, ah[j] = (r % 6) / 3, at[j] = r % 3;
+      arow[j] = ab[j] < NB, adata[j] = arow[j] && (g & 1) == ah[j];
+      if (NB == 1 || !arow[j]) ab[j] = 0;
+    }
+    // A fragments from LDS, read one chunk ahead of their MFMAs
+    auto read_a = [&](int i, v8i (&A)[NMF], int (&asc)[NMF]) {
+#pragma unroll
+      for (int j = 0; j < NMF; ++j) {
+        A[j] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
+        asc[j] = 127;
+        if (arow[j]) {
+          if (adata[j]) {
+            const uint8_t* c = &lds_c[wave][i][ab[j]][at[j] * 128 + g * 32];
+            const int4 lo = *reinterpret_cast<const int4*>(c);
+            const int4 hi = *reinterpret_cast<const int4*>(c + 16);
+            A[j] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+          }
+          asc[j] = lds_e[wave][i][ab[j]][at[j] * 8 + 2 * g + ah[j]];
         }
-        asc = lds_e[wave][i][at * 8 + 2 * g + ah];
       }
     };
-    v8i A[2];
-    int asc[2];
+    v8i A[2][NMF];
+    int asc[2][NMF];
     read_a(0, A[0], asc[0]);
-    v4f acc[MATS];
+    v4f acc[MATS][NMF];
 #pragma unroll
-    for (int m = 0; m < MATS; ++m) acc[m] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int m = 0; m < MATS; ++m)
+#pragma unroll
+      for (int j = 0; j < NMF; ++j) acc[m][j] = v4f{0.f, 0.f, 0.f, 0.f};
     static_for<0, NSW>([&](auto I) {
       constexpr int i = decltype(I)::value;
       if (i < ns) {
@@ -353,75 +396,123 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mx(GemvMxArgs a) {
                        (int)wh[m][i].x, (int)wh[m][i].y, (int)wh[m][i].z, (int)wh[m][i].w};
           int wsc = 127;
           if constexpr (BLK) wsc = (int)((we[m][(s >> 2) - (s0 >> 2)] >> (8 * (s & 3))) & 0xFFu);
-          acc[m] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[i & 1], B, acc[m], 0, wfmt<DT>(), 0,
-                                                                   asc[i & 1], 0, wsc);
+#pragma unroll
+          for (int j = 0; j < NMF; ++j)
+            acc[m][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[i & 1][j], B, acc[m][j], 0, wfmt<DT>(),
+                                                                         0, asc[i & 1][j], 0, wsc);
         }
       }
     });
 #pragma unroll
-    for (int m = 0; m < MATS; ++m) {
-      p0[m] = (acc[m][0] + acc[m][1]) + (acc[m][2] + acc[m][3]);  // g = 0: rows 0-3
-      p1[m] = acc[m][0] + acc[m][1];                                // g = 1: rows 4-5
-    }
+    for (int m = 0; m < MATS; ++m)
+#pragma unroll
+      for (int j = 0; j < NMF; ++j) {
+        const bool two = (16 * j + 4 * g) % 6 == 4;  // rows 2-3 start the next batch row
+        const float lo = acc[m][j][0] + acc[m][j][1], hi = acc[m][j][2] + acc[m][j][3];
+        plo[m][j] = two ? lo : lo + hi;
+        phi[m][j] = two ? hi : 0.0f;
+      }
   } else {
     // the weights are read again here, so the registers above are dead on
-    // this path
+    // this path; each batch row's exact sum lands in the slot the epilogue
+    // reads first for it
 #pragma unroll
     for (int m = 0; m < MATS; ++m) {
+#pragma unroll
+      for (int j = 0; j < NMF; ++j) plo[m][j] = phi[m][j] = 0.0f;
       const uint8_t* f = a.codesf[m] + (size_t)rb * S * (H * 1024) + lane * 16;
-      float s_ = 0.0f;
 #pragma unroll 1
-      for (int s = s0; s < s1; ++s) {
-        float s_lo = 1.0f, s_hi = 1.0f;
-        if constexpr (BLK) {
-          // lane (n, g) takes the exponent of block g of chunk s; its FP4
-          // nibbles are block g, its FP8 bytes blocks g / 2 (bytes 0-15) and
-          // 2 + g / 2 (bytes 16-31), whose exponents other lanes take
-          const int groups = (S + 3) / 4;
-          const int e = a.blkf[m][(((size_t)rb * groups + (s >> 2)) * 64 + lane) * 4 + (s & 3)];
-          if constexpr (FP4) {
-            s_lo = pow2f(e - 127);
-          } else {
-            s_lo = pow2f(__shfl(e, n + 16 * (g >> 1), 64) - 127);
-            s_hi = pow2f(__shfl(e, n + 16 * (2 + (g >> 1)), 64) - 127);
+      for (int b = 0; b < NB; ++b) {
+        float s_ = 0.0f;
+#pragma unroll 1
+        for (int s = s0; s < s1; ++s) {
+          float s_lo = 1.0f, s_hi = 1.0f;
+          if constexpr (BLK) {
+            // lane (n, g) takes the exponent of block g of chunk s; its FP4
+            // nibbles are block g, its FP8 bytes blocks g / 2 (bytes 0-15) and
+            // 2 + g / 2 (bytes 16-31), whose exponents other lanes take
+            const int groups = (S + 3) / 4;
+            const int e = a.blkf[m][(((size_t)rb * groups + (s >> 2)) * 64 + lane) * 4 + (s & 3)];
+            if constexpr (FP4) {
+              s_lo = pow2f(e - 127);
+            } else {
+              s_lo = pow2f(__shfl(e, n + 16 * (g >> 1), 64) - 127);
+              s_hi = pow2f(__shfl(e, n + 16 * (2 + (g >> 1)), 64) - 127);
+            }
+          }
+          s_ += exact_slice<DT>(f + (size_t)s * (H * 1024), a.x + (size_t)b * a.cols, 128 * s, g, a.cols,
+                                s_lo, s_hi);
+        }
+        // the four lane groups of row n
+        s_ += __shfl_xor(s_, 16, 64);
+        s_ += __shfl_xor(s_, 32, 64);
+        if constexpr (NB == 1) {
+          plo[m][0] = g == 0 ? s_ : 0.0f;  // the lanes of group 1 store a zero
+        } else {
+          // batch row b's first rows sit in group G = 6 b / 4 (MFMA G / 4,
+          // lane group G % 4), in its upper slot when 6 b % 4 == 2
+#pragma unroll
+          for (int j = 0; j < NMF; ++j) {
+            if (4 * j + g == 6 * b / 4) {
+              if ((6 * b) % 4 == 2) phi[m][j] = s_;
+              else plo[m][j] = s_;
+            }
           }
         }
-        s_ += exact_slice<DT>(f + (size_t)s * (H * 1024), a.x, 128 * s, g, a.cols, s_lo, s_hi);
       }
-      // the four lane groups of row n
-      s_ += __shfl_xor(s_, 16, 64);
-      s_ += __shfl_xor(s_, 32, 64);
-      p0[m] = s_;
-      p1[m] = 0.0f;
     }
   }
-  if (g < 2) {
+  if constexpr (NB == 1) {
+    if (g < 2) {
 #pragma unroll
-    for (int m = 0; m < MATS; ++m) part[wave][m][n][g] = g == 0 ? p0[m] : p1[m];
+      for (int m = 0; m < MATS; ++m) part[wave][m][n][g] = plo[m][0];
+    }
+  } else {
+    float* pw = part_w(wave);
+#pragma unroll
+    for (int m = 0; m < MATS; ++m)
+#pragma unroll
+      for (int j = 0; j < NMF; ++j)
+        *reinterpret_cast<float2*>(&pw[((m * NMF + j) * 4 + g) * 32 + 2 * n]) = make_float2(plo[m][j], phi[m][j]);
   }
   __syncthreads();
 
-  // 5. epilogue in wave 0: lane l computes row n0 + l % 16 (the four lane
-  // groups alike, so that the 16-lane DPP maxima below run with every lane
-  // active); lanes 0-15 store
+  // 5. epilogue in wave 0: lane (n, g) computes row n0 + n of batch row g
+  // (one batch row: the four lane groups alike, so that the 16-lane DPP
+  // maxima below run with every lane active); lanes of batch rows < NB store
   if (wave != 0) return;
   const int o = n0 + n;
-  const bool store = g == 0;
+  const int bq = NB == 1 ? 0 : (g < NB ? g : NB - 1);
+  const bool store = NB == 1 ? g == 0 : g < NB;
   float tot[MATS];
 #pragma unroll
   for (int m = 0; m < MATS; ++m) {
-    float sum = part[0][m][n][0] + part[0][m][n][1];
+    if constexpr (NB == 1) {
+      float sum = part[0][m][n][0] + part[0][m][n][1];
 #pragma unroll
-    for (int w = 1; w < W; ++w) sum += part[w][m][n][0] + part[w][m][n][1];
-    tot[m] = sum * rs[m];
+      for (int w = 1; w < W; ++w) sum += part[w][m][n][0] + part[w][m][n][1];
+      tot[m] = sum * rs[m];
+    } else {
+      // rows 6 bq .. 6 bq + 5: groups G1 = 6 bq / 4 (upper slot when it
+      // starts with the previous batch row) and G1 + 1 (lower slot)
+      const int G1 = 6 * bq / 4;
+      const int i1 = ((m * NMF + G1 / 4) * 4 + G1 % 4) * 32 + 2 * n + ((6 * bq) % 4 == 2 ? 1 : 0);
+      const int G2 = G1 + 1;
+      const int i2 = ((m * NMF + G2 / 4) * 4 + G2 % 4) * 32 + 2 * n;
+      float sum = part_w(0)[i1] + part_w(0)[i2];
+#pragma unroll
+      for (int w = 1; w < W; ++w) sum += part_w(w)[i1] + part_w(w)[i2];
+      tot[m] = sum * rs[m];
+    }
   }
+  const size_t ob_out = (size_t)bq * a.rows + o;
   if constexpr (MATS == 2) {
     const float gt = (float)act_f64(kSilu, (double)tot[0]);
     const float h = (float)((double)gt * (double)tot[1]);
-    if (store && o < a.rows) a.pre[o] = h;
+    if (store && o < a.rows) a.pre[ob_out] = h;
     if constexpr (NEXT) {
-      // the three-term split of this piece (outputs n0 .. n0 + 15) for the
-      // next product
+      // the three-term split of this piece (outputs n0 .. n0 + 15 of batch
+      // row bq) for the next product
       float v = o < a.rows ? h : 0.0f;
       auto piece_max = [&](float t) {
         t = fmaxf(t, xor_lane<1>(t, lane));
@@ -430,19 +521,26 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mx(GemvMxArgs a) {
         return fmaxf(t, xor_lane<8>(t, lane));
       };
       const float am0 = piece_max(finite_amax(fabsf(v)) ? fabsf(v) : __builtin_inff());  // NaN as inf
+      const bool fin = finite_amax(am0);
       const int s = rb >> 3, p = rb & 7;
-      uint8_t* codes = a.next + (size_t)s * kChunkCodeBytes + (p & 3) * 32 + 16 * (p >> 2);
-      uint8_t* exps = a.next + (size_t)a.next_steps * kChunkCodeBytes + (size_t)s * kChunkExpBytes + p;
-      // the terms' 16 code bytes each meet in LDS (the reduction's buffer,
-      // read above by this wave only), then lanes 0-2 store 16 bytes each
-      uint8_t* gather = reinterpret_cast<uint8_t*>(&part[0][0][0][0]);
-      if (!finite_amax(am0)) {
+      uint8_t* codes = a.next + bq * img + (size_t)s * kChunkCodeBytes + (p & 3) * 32 + 16 * (p >> 2);
+      uint8_t* exps = a.next + bq * img + (size_t)a.next_steps * kChunkCodeBytes + (size_t)s * kChunkExpBytes + p;
+      // the terms' 16 code bytes each meet in LDS (a region this wave alone
+      // uses now), then lanes 0-2 of the batch row store 16 bytes each
+      uint8_t* gather = (NB == 1 ? reinterpret_cast<uint8_t*>(&part[0][0][0][0])
+                                 : reinterpret_cast<uint8_t*>(part_w(0) + PARTF)) + bq * 48;
+      // one batch row: fin is the same in every lane, and the DPP maxima
+      // inside the branch run with every lane active. More rows: every lane
+      // runs the terms (of zeros where its piece is not finite), the stores
+      // are selected.
+      if (NB == 1 && !fin) {
         if (lane == 0) {
 #pragma unroll
           for (int t = 0; t < kTermsMx; ++t) exps[t * 8] = kNonFinite;
         }
       } else {
-        float am = am0;
+        if (!fin) v = 0.0f;
+        float am = fin ? am0 : 0.0f;
 #pragma unroll
         for (int t = 0; t < kTermsMx; ++t) {
           if (t > 0) am = piece_max(fabsf(v));
@@ -453,13 +551,15 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mx(GemvMxArgs a) {
           const int code = __builtin_bit_cast(int, w) & 0xFF;
           if (store) gather[t * 16 + n] = (uint8_t)code;
           if (t + 1 < kTermsMx) v -= __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(code, sc, false)[0];
-          if (lane == 0) exps[t * 8] = (uint8_t)(e + 127);
+          if (store && n == 0) exps[t * 8] = fin ? (uint8_t)(e + 127) : kNonFinite;
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_s_waitcnt(0xc07f);
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        if (lane < kTermsMx)
-          *reinterpret_cast<int4*>(codes + lane * 128) = *reinterpret_cast<const int4*>(gather + lane * 16);
+        // a non-finite piece keeps whatever codes it had: its 0xFF exponents
+        // send the reader to the exact path over h
+        if (store && fin && n < kTermsMx)
+          *reinterpret_cast<int4*>(codes + n * 128) = *reinterpret_cast<const int4*>(gather + n * 16);
       }
     }
   } else {
@@ -471,11 +571,11 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mx(GemvMxArgs a) {
         v += bias;
         y = (float)v;
       }
-      a.pre[o] = y;
-      a.post[o] = (float)act_f64(a.act, v);
+      a.pre[ob_out] = y;
+      a.post[ob_out] = (float)act_f64(a.act, v);
     } else {
-      a.pre[o] = y;
-      if (a.post && a.post != a.pre) a.post[o] = y;
+      a.pre[ob_out] = y;
+      if (a.post && a.post != a.pre) a.post[ob_out] = y;
     }
   }
 }
@@ -485,50 +585,64 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mx(GemvMxArgs a) {
 // tracks S / W closely). A wave holds all its weight operands in registers,
 // so 16 waves (128 VGPRs each) take 8 chunks only of one FP4 matrix, 4 of
 // one FP8 matrix or of two FP4 matrices; two FP8 matrices run 8 waves
-// (S <= 32) only.
-constexpr int max_chunks(int dtype, int mats) {
-  return dtype == kFP4 ? (mats == 1 ? 128 : 64) : (mats == 1 ? 64 : 32);
+// (S <= 32) only. The staged terms take W x NSW x NB x 408 bytes of LDS, so
+// 16 waves of 8 chunks run at most 3 batch rows.
+constexpr int max_chunks(int dtype, int mats, int nb) {
+  return dtype == kFP4 ? (mats == 1 ? (nb <= 3 ? 128 : 96) : 64) : (mats == 1 ? 64 : 32);
 }
 
-template <int DT, bool BLK, int MATS, int W, int NSW, bool PRE, bool NEXT>
+template <int DT, bool BLK, int MATS, int NB, int W, int NSW, bool PRE, bool NEXT>
 Status launch_t(const GemvMxArgs& a, hipStream_t st) {
+  static_assert(W * NSW * NB * (kChunkCodeBytes + kChunkExpBytes) + (NB == 1 ? W * MATS * 128 : 0) <= 160 * 1024,
+                "LDS of one workgroup");
   const unsigned grid = (unsigned)((a.rows + 15) / 16);
-  k_gemv_mx<DT, BLK, MATS, W, NSW, PRE, NEXT><<<grid, 64 * W, 0, st>>>(a);
+  k_gemv_mx<DT, BLK, MATS, NB, W, NSW, PRE, NEXT><<<grid, 64 * W, 0, st>>>(a);
   return hip_status(hipGetLastError(), "gemv_mx launch");
 }
 
-template <int DT, bool BLK, int MATS, bool PRE, bool NEXT>
+template <int DT, bool BLK, int MATS, int NB, bool PRE, bool NEXT>
 Status launch_shape(const GemvMxArgs& a, hipStream_t st) {
   const int S = a.kpad / 128;
-  if (S <= 32) return launch_t<DT, BLK, MATS, 8, 4, PRE, NEXT>(a, st);
+  if (S <= 32) return launch_t<DT, BLK, MATS, NB, 8, 4, PRE, NEXT>(a, st);
   if constexpr (DT == kFP4 || MATS == 1)
-    if (S <= 64) return launch_t<DT, BLK, MATS, 16, 4, PRE, NEXT>(a, st);
+    if (S <= 64) return launch_t<DT, BLK, MATS, NB, 16, 4, PRE, NEXT>(a, st);
   if constexpr (DT == kFP4 && MATS == 1) {
-    if (S <= 96) return launch_t<DT, BLK, MATS, 16, 6, PRE, NEXT>(a, st);
-    return launch_t<DT, BLK, MATS, 16, 8, PRE, NEXT>(a, st);
+    if (S <= 96) return launch_t<DT, BLK, MATS, NB, 16, 6, PRE, NEXT>(a, st);
+    if constexpr (NB <= 3) return launch_t<DT, BLK, MATS, NB, 16, 8, PRE, NEXT>(a, st);
   }
   return Status::err(kUnsupported, "gemv_mx: K");
 }
 
+template <int DT, bool BLK, int NB>
+Status launch_nb(const GemvMxArgs& a, hipStream_t st) {
+  if (a.mats == 2) {
+    return a.next ? launch_shape<DT, BLK, 2, NB, false, true>(a, st)
+                  : launch_shape<DT, BLK, 2, NB, false, false>(a, st);
+  }
+  return a.asplit ? launch_shape<DT, BLK, 1, NB, true, false>(a, st)
+                  : launch_shape<DT, BLK, 1, NB, false, false>(a, st);
+}
+
 template <int DT, bool BLK>
 Status launch_dt(const GemvMxArgs& a, hipStream_t st) {
-  if (a.mats == 2) {
-    return a.next ? launch_shape<DT, BLK, 2, false, true>(a, st)
-                  : launch_shape<DT, BLK, 2, false, false>(a, st);
+  switch (a.nb) {
+  case 1: return launch_nb<DT, BLK, 1>(a, st);
+  case 2: return launch_nb<DT, BLK, 2>(a, st);
+  case 3: return launch_nb<DT, BLK, 3>(a, st);
+  case 4: return launch_nb<DT, BLK, 4>(a, st);
   }
-  return a.asplit ? launch_shape<DT, BLK, 1, true, false>(a, st)
-                  : launch_shape<DT, BLK, 1, false, false>(a, st);
+  return Status::err(kUnsupported, "gemv_mx: batch rows");
 }
 
 }  // namespace
 
-bool gemv_mx_fits(int dtype, int rows, int kpad, int mats) {
+bool gemv_mx_fits(int dtype, int rows, int kpad, int mats, int nb) {
   if (dtype != kE4M3 && dtype != kE5M2 && dtype != kFP4) return false;
   const int S = kpad / 128;
   // whole-GPU grids only (one workgroup per 16 rows per CU or more), and K
   // ranges that the instantiated shapes cover
-  return mats >= 1 && mats <= 2 && (rows + 15) / 16 >= 256 && S >= 16 &&
-         S <= max_chunks(dtype, mats) && kpad % 128 == 0;
+  return mats >= 1 && mats <= 2 && nb >= 1 && nb <= kGemvMxMaxRows && (rows + 15) / 16 >= 256 &&
+         S >= 16 && S <= max_chunks(dtype, mats, nb) && kpad % 128 == 0;
 }
 
 size_t gemv_mx_split_bytes(int kpad) {
@@ -537,7 +651,7 @@ size_t gemv_mx_split_bytes(int kpad) {
 }
 
 Status launch_gemv_mx(const GemvMxArgs& a, int dtype, bool blk, hipStream_t st) {
-  if (!gemv_mx_fits(dtype, a.rows, a.kpad, a.mats) || !a.codesf[0] || !a.scale[0] || !a.pre ||
+  if (!gemv_mx_fits(dtype, a.rows, a.kpad, a.mats, a.nb) || !a.codesf[0] || !a.scale[0] || !a.pre ||
       (a.mats == 2 && (!a.codesf[1] || !a.scale[1])) || (blk && (!a.blkf[0] || (a.mats == 2 && !a.blkf[1]))) ||
       !a.x || (a.asplit && (a.mats != 1 || a.asplit_steps < a.kpad / 128)) ||
       // the split of x reads 16-byte vectors

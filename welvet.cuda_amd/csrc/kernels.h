@@ -123,7 +123,7 @@ struct MxvArgs {
 };
 Status launch_mxv(const MxvArgs& a, int dtype, bool blk, hipStream_t st);
 
-// ---- batch-1 GEMV on the scaled MFMA over operand-order weights (gemv_mx.hip) ----
+// ---- 1-4-row GEMV on the scaled MFMA over operand-order weights (gemv_mx.hip) ----
 // x as three E4M3 terms per 16-element piece in the rows of the A operand;
 // the weights from DeviceWeights::codes_frag (and blk_frag). The pre-split
 // input image (asplit / next) holds, per K chunk of 128, the term codes
@@ -136,24 +136,30 @@ struct GemvMxArgs {
   const float* scale[2] = {nullptr, nullptr};
   int mats = 1;
   int kpad = 0, cols = 0, rows = 0;
-  // fp32 input [cols], 16-byte aligned with cols % 4 == 0 unless asplit is
-  // given (then read only by the non-finite fallback)
+  int nb = 1;  // batch rows, 1..kGemvMxMaxRows
+  // fp32 input [nb][cols], 16-byte aligned with cols % 4 == 0 unless asplit
+  // is given (then read only by the non-finite fallback)
   const float* x = nullptr;
-  const uint8_t* asplit = nullptr;  // pre-split x (one matrix), or null
+  // pre-split x (one matrix): one image of asplit_steps chunks per batch
+  // row, back to back; or null
+  const uint8_t* asplit = nullptr;
   int asplit_steps = 0;
-  uint8_t* next = nullptr;   // two matrices: the split of h written here, or null
+  // two matrices: the split of h written here (one image of next_steps
+  // chunks per batch row), or null
+  uint8_t* next = nullptr;
   int next_steps = 0;
-  float* pre = nullptr;
-  float* post = nullptr;
+  float* pre = nullptr;   // [nb][rows]
+  float* post = nullptr;  // [nb][rows]
   int act = kLinear;
   int need_epi = 0;
   const double* bias = nullptr;
   int bias_len = 0;
 };
+constexpr int kGemvMxMaxRows = 4;
 // Shapes the kernel runs: FP8/FP4, at least 256 row blocks of 16, 16..128
-// K chunks of 128.
-bool gemv_mx_fits(int dtype, int rows, int kpad, int mats);
-// Bytes of a pre-split input image over kpad columns.
+// K chunks of 128 (96 for 4 batch rows), 1..4 batch rows.
+bool gemv_mx_fits(int dtype, int rows, int kpad, int mats, int nb);
+// Bytes of one batch row's pre-split input image over kpad columns.
 size_t gemv_mx_split_bytes(int kpad);
 Status launch_gemv_mx(const GemvMxArgs& a, int dtype, bool blk, hipStream_t st);
 

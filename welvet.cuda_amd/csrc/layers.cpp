@@ -271,18 +271,17 @@ static MxvArgs mxv_args(const DenseLayer& L, const float* x, int x_stride, int b
 
 bool uses_split(int batch) { return batch > kMxvMaxBatch; }
 
-// Batch-1 products on the matrix cores over operand-order weights
+// 1-4-row products on the matrix cores over operand-order weights
 // (gemv_mx.hip): large enough to fill the GPU with 16-row workgroups, and
 // without weight rows holding non-finite codes (whose products the matrix
 // cores would turn into NaN where the reference gives inf).
 static bool mx_dense(const DenseLayer& L, int batch) {
-  return batch == 1 && !L.format && L.dev.nf_count() == 0 &&
-         gemv_mx_fits(L.dev.dtype, L.out, L.dev.kpad, 1);
+  return !L.format && L.dev.nf_count() == 0 && gemv_mx_fits(L.dev.dtype, L.out, L.dev.kpad, 1, batch);
 }
 
 static bool mx_pair(const SwiGLULayer& L, int rows) {
-  return rows == 1 && !L.gate.format && !L.up.format && L.gate.dev.nf_count() == 0 &&
-         L.up.dev.nf_count() == 0 && gemv_mx_fits(L.gate.dev.dtype, L.inter, L.gate.dev.kpad, 2);
+  return !L.gate.format && !L.up.format && L.gate.dev.nf_count() == 0 && L.up.dev.nf_count() == 0 &&
+         gemv_mx_fits(L.gate.dev.dtype, L.inter, L.gate.dev.kpad, 2, rows);
 }
 
 static Status build_frag(DenseLayer* L, hipStream_t st) {
@@ -313,8 +312,9 @@ static bool mx_vec(const DenseLayer& L, const float* x) {
   return L.in % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
 }
 
-static GemvMxArgs mx_args(const DenseLayer& L, const float* x) {
+static GemvMxArgs mx_args(const DenseLayer& L, const float* x, int batch) {
   GemvMxArgs a;
+  a.nb = batch;
   a.codesf[0] = L.dev.d_codesf();
   a.blkf[0] = L.dev.d_blkf();
   a.scale[0] = L.dev.d_scale();
@@ -443,6 +443,12 @@ Status dense_forward(const DenseLayer& L, int batch, const float* x, float* pre,
   if (L.need_epi() && !post) return Status::err(kInvalid, "dense forward: post needed");
   // packed block formats: the GEMV over every batch row
   if (L.format) return format_forward(L, batch, x, pre, post, st);
+  if (mx_dense(L, batch) && L.dev.codes_frag.p && mx_vec(L, x)) {
+    GemvMxArgs m = mx_args(L, x, batch);
+    m.pre = pre;
+    m.post = post;
+    return launch_gemv_mx(m, L.dev.dtype, L.dev.scheme == kSchemeBlock32, st);
+  }
   if (uses_split(batch)) {
     WV_TRY(ensure_split(ws, gemm_ws_bytes(L, batch, 1)));
     return dense_forward_split(L, batch, x, false, ws, pre, post, st);
@@ -453,12 +459,6 @@ Status dense_forward(const DenseLayer& L, int batch, const float* x, float* pre,
     m.post = post;
     WV_TRY(launch_mxv(m, L.dev.dtype, L.dev.scheme == kSchemeBlock32, st));
     return fix_nonfinite(L, batch, x, L.in, pre, post, st);
-  }
-  if (mx_dense(L, batch) && L.dev.codes_frag.p && mx_vec(L, x)) {
-    GemvMxArgs m = mx_args(L, x);
-    m.pre = pre;
-    m.post = post;
-    return launch_gemv_mx(m, L.dev.dtype, L.dev.scheme == kSchemeBlock32, st);
   }
   GemvArgs a = gemv_args(L, x, L.in);
   a.pre = pre;
@@ -767,13 +767,13 @@ static Status swiglu_fix(const SwiGLULayer& L, int rows, const float* x, float* 
   return launch_nf_fix(a, st);
 }
 
-// The batch-1 gate+up launch writes the down projection's input split.
+// The 1-4-row gate+up launch writes the down projection's input split.
 static bool mx_fused(const SwiGLULayer& L, int rows) {
   return mx_pair(L, rows) && mx_dense(L.down, rows) && L.down.in == L.inter;
 }
 
 size_t swiglu_workspace_bytes(const SwiGLULayer& L, int rows) {
-  if (mx_fused(L, rows)) return gemv_mx_split_bytes(L.down.dev.kpad);
+  if (mx_fused(L, rows)) return (size_t)rows * gemv_mx_split_bytes(L.down.dev.kpad);
   if (!uses_split(rows)) return 0;
   const size_t a = gemm_ws_bytes(L.gate, rows, 2), b = gemm_ws_bytes(L.down, rows, 1);
   return a > b ? a : b;
@@ -782,6 +782,32 @@ size_t swiglu_workspace_bytes(const SwiGLULayer& L, int rows) {
 Status swiglu_forward(const SwiGLULayer& L, int rows, const float* x, float* h, float* y,
                       Workspace* ws, hipStream_t st) {
   if (rows <= 0 || !x || !h || !y) return Status::err(kInvalid, "swiglu forward: bad args");
+  if (mx_pair(L, rows) && L.gate.dev.codes_frag.p && L.up.dev.codes_frag.p && mx_vec(L.gate, x)) {
+    GemvMxArgs g = mx_args(L.gate, x, rows);
+    g.mats = 2;
+    g.codesf[1] = L.up.dev.d_codesf();
+    g.blkf[1] = L.up.dev.d_blkf();
+    g.scale[1] = L.up.dev.d_scale();
+    g.pre = h;
+    g.need_epi = 0;
+    // the split of h for the down projection, when the session's workspace
+    // holds it (never allocated here: this may run under graph capture)
+    const size_t nb = (size_t)rows * gemv_mx_split_bytes(L.down.dev.kpad);
+    const bool fuse = mx_fused(L, rows) && L.down.dev.codes_frag.p && ws && ws->b.bytes >= nb;
+    if (fuse) {
+      g.next = split_buf(ws);
+      g.next_steps = L.down.dev.kpad / 128;
+    }
+    const bool blk = L.gate.dev.scheme == kSchemeBlock32;
+    WV_TRY(launch_gemv_mx(g, L.gate.dev.dtype, blk, st));
+    if (!fuse) return dense_forward(L.down, rows, h, y, nullptr, ws, st);
+    GemvMxArgs d = mx_args(L.down, h, rows);
+    d.asplit = split_buf(ws);
+    d.asplit_steps = L.down.dev.kpad / 128;
+    d.pre = y;
+    d.post = nullptr;
+    return launch_gemv_mx(d, L.down.dev.dtype, L.down.dev.scheme == kSchemeBlock32, st);
+  }
   if (rows >= 2 && rows <= kMxvMaxBatch) {
     MxvArgs m = mxv_args(L.gate, x, L.in, rows);
     m.mats = 2;
@@ -812,32 +838,6 @@ Status swiglu_forward(const SwiGLULayer& L, int rows, const float* x, float* h, 
     WV_TRY(launch_mxg(p, L.gate.dev.dtype, L.gate.dev.scheme == kSchemeBlock32, st));
     WV_TRY(swiglu_fix(L, rows, x, h, st));
     return dense_forward_split(L.down, rows, h, false, ws, y, nullptr, st);
-  }
-  if (mx_pair(L, rows) && L.gate.dev.codes_frag.p && L.up.dev.codes_frag.p && mx_vec(L.gate, x)) {
-    GemvMxArgs g = mx_args(L.gate, x);
-    g.mats = 2;
-    g.codesf[1] = L.up.dev.d_codesf();
-    g.blkf[1] = L.up.dev.d_blkf();
-    g.scale[1] = L.up.dev.d_scale();
-    g.pre = h;
-    g.need_epi = 0;
-    // the split of h for the down projection, when the session's workspace
-    // holds it (never allocated here: this may run under graph capture)
-    const size_t nb = gemv_mx_split_bytes(L.down.dev.kpad);
-    const bool fuse = mx_fused(L, rows) && L.down.dev.codes_frag.p && ws && ws->b.bytes >= nb;
-    if (fuse) {
-      g.next = split_buf(ws);
-      g.next_steps = L.down.dev.kpad / 128;
-    }
-    const bool blk = L.gate.dev.scheme == kSchemeBlock32;
-    WV_TRY(launch_gemv_mx(g, L.gate.dev.dtype, blk, st));
-    if (!fuse) return dense_forward(L.down, rows, h, y, nullptr, ws, st);
-    GemvMxArgs d = mx_args(L.down, h);
-    d.asplit = split_buf(ws);
-    d.asplit_steps = L.down.dev.kpad / 128;
-    d.pre = y;
-    d.post = nullptr;
-    return launch_gemv_mx(d, L.down.dev.dtype, L.down.dev.scheme == kSchemeBlock32, st);
   }
   GemvArgs a = gemv_args(L.gate, x, L.in);
   a.mats = 2;
