@@ -1,7 +1,8 @@
-"""Batch-1 products on the scaled matrix cores over operand-order weights
+"""1-4-row products on the scaled matrix cores over operand-order weights
 (gemv_mx.hip): Dense layers with at least 4081 output rows and 16-128 K
-chunks of 128 (FP8: up to 64), and the batch-1 SwiGLU, whose gate+up launch
-writes the three-term split of h that the down projection reads.
+chunks of 128 (FP8: up to 64; four rows: up to 96), and the 1-4-row SwiGLU,
+whose gate+up launch writes the three-term split of h that the down
+projection reads.
 
 Parity reference: the oracle's contract (dequantize, f64 serial sums, bias in
 f64, activation; src/cuda/kernels.cu:130-161; SwiGLU swiglu.cpp:87-136,

@@ -1,7 +1,7 @@
-// Batch-1 quantized GEMV on the CDNA4 scaled matrix cores, over the weights
-// in matrix-core operand order (DeviceWeights::codes_frag).
+// Quantized GEMV for 1-4 batch rows on the CDNA4 scaled matrix cores, over
+// the weights in matrix-core operand order (DeviceWeights::codes_frag).
 //
-//   y[n] = rowscale[n] * sum_k x[k] * dec(W[n][k]) * blockscale[n][k/32]
+//   y[b][n] = rowscale[n] * sum_k x[b][k] * dec(W[n][k]) * blockscale[n][k/32]
 //
 // Weights. Per 16-row block and K chunk of 128 the operand a wave passes to
 // v_mfma_scale_f32_16x16x128_f8f6f4 is stored contiguously (1 KiB for FP4,
@@ -21,7 +21,9 @@
 // (the FP8 operand layout: bytes 0-15 -> k = 16g + j, 16-31 -> k = 64 + 16g
 // + j), so row 3h + t carries data only in lane groups g with g & 1 == h; its
 // scale for block b is the exponent of piece 2b + h. The six accumulator
-// rows (lanes g = 0: rows 0-3, g = 1: rows 4-5) add up to the product.
+// rows (lanes g = 0: rows 0-3, g = 1: rows 4-5) add up to the product. More
+// batch rows take six A rows each (rows 6b .. 6b + 5 for batch row b), so two
+// rows share one MFMA per weight fragment and three or four take two.
 //
 // Work split. One workgroup per 16 weight rows (per matrix); its W waves cut
 // K into ranges of at most NSW chunks. A wave issues the loads of its input
@@ -35,9 +37,9 @@
 //
 // Non-finite inputs. A wave whose slice of x holds inf or NaN (or whose
 // pre-split pieces carry the 0xFF exponent that marks a non-finite piece)
-// computes its partial sums on the VALU instead, from the same weight
-// registers decoded exactly, so such inputs give the IEEE result of the
-// fp32 GEMV.
+// computes its partial sums on the VALU instead, from the weight codes read
+// again and decoded exactly, so such inputs give the IEEE result of the fp32
+// GEMV.
 #include <type_traits>
 
 #include "codec.h"
@@ -157,9 +159,9 @@ __device__ float exact_slice(const uint8_t* w, const float* x, int k0, int g, in
 // MFMAs (MFMA j takes rows 16 j .. 16 j + 15) holds term t of half h of
 // batch row b, so NMF = ceil(6 NB / 16) MFMAs per weight fragment: one for
 // 1-2 rows, two for 3-4. Accumulator lane (n, g) of MFMA j holds rows
-// 16 j + 4 g .. + 3 of column n, of one batch row or (when 16 j + 4 g is
-// 2 mod 6 ... rows 2-3 past a multiple of 6) split two and two between
-// consecutive batch rows.
+// 16 j + 4 g .. + 3 of column n: all four of one batch row, or, when
+// 16 j + 4 g = 4 mod 6, two of batch row (16 j + 4 g) / 6 and two of the
+// next.
 // PRE: the input is a pre-split image per batch row (a.asplit); otherwise the
 // waves split a.x themselves. NEXT (MATS == 2): write the split of h to
 // a.next.
