@@ -248,7 +248,9 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mx(GemvMxArgs a) {
 
   // 2. every weight load of this wave's range in flight
   constexpr int H = FP4 ? 1 : 2;
-  constexpr int EG = NSW / 4 + 2;  // exponent dwords a range of NSW chunks touches
+  // exponent dwords (groups of 4 chunks) that NSW consecutive chunks from
+  // any start touch: (s0 + NSW - 1) / 4 - s0 / 4 <= (NSW + 2) / 4
+  constexpr int EG = (NSW + 2) / 4 + 1;
   u32x4 wl[MATS][NSW], wh[MATS][FP4 ? 1 : NSW];
   uint32_t we[MATS][BLK ? EG : 1];
 #pragma unroll
