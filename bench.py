@@ -79,6 +79,7 @@ C2_BYTES = 16826368
 # rocprof summaries (kernel stats + FETCH_SIZE/WRITE_SIZE scaled by a copy of
 # known size) per workload; `traffic_bytes:` is the measured HBM bytes per launch.
 PROFILES = {"c2": "gemv_fp8e4m3_rowscale_4096x4096_b1.txt",
+            "c2_b2": "gemv_fp8e4m3_rowscale_4096x4096_b2.txt",
             "read_floor": "read_floor_16826368B.txt",
             "c2bwd": "dense_backward_4096x4096_fp8e4m3_rowscale_b1.txt",
             "gemv_q4_k": "gemv_q4_k_4096x4096_b1.txt"}
@@ -889,6 +890,8 @@ def gemm_summary(pw, hip, config, copies):
     finally:
         wl["close"]()
     per_step_s = m["ms"] * 1e-3 / steps
+    # profiles are per workload: the batch rows of c2 and c3 are part of it
+    traffic_key = args.config + (f"_b{args.batch}" if args.batch > 1 and args.config in ("c2", "c3") else "")
     tflops = wl["flops"] / per_step_s / 1e12
     peak = wl.get("peak_tflops", MFMA_FP8_PEAK_TFLOPS)
     return {"workload": wl["config"]["workload"], "ms_per_step": round(m["ms"] / steps, 6),
@@ -959,19 +962,21 @@ def main():
     stamp_ms, lead, t_wall = m["stamp_ms"], m["lead"], m["t_wall"]
     per_step_s = ms * 1e-3 / steps
 
+    # profiles are per workload: the batch rows of c2 and c3 are part of it
+    traffic_key = args.config + (f"_b{args.batch}" if args.batch > 1 and args.config in ("c2", "c3") else "")
     tflops = wl["flops"] / per_step_s / 1e12
     gbs = wl["bytes"] / per_step_s / 1e9 if wl["bytes"] else None
     if wl["bound"] == "hbm":
         value, unit = gbs, "GB/s"
         roof = {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(gbs / HBM_PEAK_GBS, 4),
-                "traffic": measured_traffic("read_floor" if args.read_floor else args.config)}
+                "traffic": measured_traffic("read_floor" if args.read_floor else traffic_key)}
     else:
         value, unit = tflops, "TFLOP/s"
         peak = wl.get("peak_tflops", MFMA_FP8_PEAK_TFLOPS)
         roof = {"bound": "mfma", "achieved": round(tflops, 3), "peak": round(peak, 1),
                 "unit": "TFLOP/s", "frac": round(tflops / peak, 4),
-                "traffic": measured_traffic(args.config)}
+                "traffic": measured_traffic(traffic_key)}
     cpu = None if (args.no_cpu or wl["cpu"] is None) else wl["cpu"](16.0)
     config = dict(wl["config"])
     rotated = min(runner.per, steps) if runner.direct else runner.per
