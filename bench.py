@@ -890,8 +890,6 @@ def gemm_summary(pw, hip, config, copies):
     finally:
         wl["close"]()
     per_step_s = m["ms"] * 1e-3 / steps
-    # profiles are per workload: the batch rows of c2 and c3 are part of it
-    traffic_key = args.config + (f"_b{args.batch}" if args.batch > 1 and args.config in ("c2", "c3") else "")
     tflops = wl["flops"] / per_step_s / 1e12
     peak = wl.get("peak_tflops", MFMA_FP8_PEAK_TFLOPS)
     return {"workload": wl["config"]["workload"], "ms_per_step": round(m["ms"] / steps, 6),
