@@ -930,7 +930,7 @@ def main():
                          "fetch rate from L2 and HBM")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py: this build measures one GPU; --gpus above 1 is not part of it",
+        print("bench.py: measures one GPU; --gpus above 1 is not part of it",
               file=sys.stderr)
         sys.exit(2)
 

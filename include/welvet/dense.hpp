@@ -69,7 +69,7 @@ WELVET_API Status new_layer(int in_h, int out_h, Activation act, DType dt,
 WELVET_API Status new_layer_scaled(int in_h, int out_h, Activation act, DType dt,
                                    ScaleScheme scheme, const float* init_or_null, Layer* layer);
 
-// True for the dtypes this build's Dense forward runs (4, 5, 16).
+// True for the dtypes this library's Dense forward runs (4, 5, 16).
 WELVET_API bool dtype_supported_cuda_forward(DType dt);
 
 // input [batch, in] -> pre, post [batch, out].

@@ -1,5 +1,5 @@
 // Storage types (reference include/welvet/dtype.hpp:9-46): the ids the C ABI's
-// `dtype` argument and the WMN1 store payloads carry. This build serves the
+// `dtype` argument and the WMN1 store payloads carry. This library serves the
 // quantized path: FP8E4M3 (4), FP8E5M2 (5) and FP4 (16); every other id is
 // reported as Unsupported by the calls that take a dtype.
 #pragma once
@@ -52,7 +52,7 @@ constexpr int kNumDTypes = 34;
 
 // Lower-case name of a dtype ("fp8e4m3", "fp4", ...); "unknown" outside 0-33.
 WELVET_API std::string_view dtype_name(DType dt);
-// True for the dtypes whose Dense forward this build runs (4, 5 and 16).
+// True for the dtypes whose Dense forward this library runs (4, 5 and 16).
 WELVET_API bool dtype_implemented_forward(DType dt);
 
 }  // namespace welvet

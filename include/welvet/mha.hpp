@@ -92,7 +92,7 @@ WELVET_API Status forward(Layer& layer, const TensorF32& input, TensorF32* pre, 
 // Length of the concatenated Q | K | V | O weight gradient.
 WELVET_API int grad_w_size(const Layer& layer);
 
-// The attention backward is not part of this build: Gap.
+// The attention backward is not part of this library: Gap.
 WELVET_API Status backward_f32(const Layer& layer, const TensorF32& grad_out,
                                const TensorF32& input, const TensorF32& pre, TensorF32* grad_in,
                                TensorF32* grad_w);

@@ -11,7 +11,7 @@ namespace welvet {
 enum class StatusCode {
   Ok = 0,
   InvalidArgument = 1,  // a shape, pointer or argument the call cannot accept
-  Unsupported = 2,      // outside what this build serves (no device, another dtype)
+  Unsupported = 2,      // outside what this library serves (no device, another dtype)
   Gap = 3,              // an entry point of the reference that is not on this path
   Internal = 4,         // a runtime or device failure
 };

@@ -2,7 +2,7 @@
 // A WeightStore holds one [rows][cols] matrix (rows = outputs) as the
 // reference's FormatNone payload: `native` is the codes of W row-major, one
 // byte per FP8 code or two FP4 codes per byte (even element in the low
-// nibble). This build serves FP8E4M3, FP8E5M2 and FP4; quantizing and
+// nibble). This library serves FP8E4M3, FP8E5M2 and FP4; quantizing and
 // decoding run on the GPU (the calls return Unsupported without a device).
 //
 // Extension (no counterpart in the reference): a scale scheme. Reference
@@ -40,7 +40,7 @@ struct WELVET_API WeightStore {
   QuantFormat format = QuantFormat::None;
   int rows = 0;
   int cols = 0;
-  std::vector<float> f32;       // Float32 payload: not served by this build (empty)
+  std::vector<float> f32;       // Float32 payload: not served by this library (empty)
   std::vector<uint8_t> native;  // the FormatNone codes
   float scale = 1.0f;
   std::vector<double> bias;

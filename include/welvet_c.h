@@ -56,7 +56,7 @@ WELVET_API const char* welvet_runtime_identity(void);
 WELVET_API welvet_status welvet_cuda_init(void);
 /* Replaces welvet_c.h:37. */
 WELVET_API int32_t welvet_cuda_available(void);
-/* Replaces welvet_c.h:38-39 (gaps census): counts of this build's ledger. */
+/* Replaces welvet_c.h:38-39 (gaps census): counts of this library's ledger. */
 WELVET_API int32_t welvet_gaps_count(void);
 WELVET_API int32_t welvet_gaps_done(void);
 

@@ -1,7 +1,7 @@
 /*
  * CPU oracle for the packed block weight formats (QuantFormat).
  *
- * TEST INFRASTRUCTURE ONLY: the checker for the library's block-format
+ * TEST INFRASTRUCTURE ONLY: the reference for the library's block-format
  * kernels; the product never links or calls it.
  *
  * The reference reserves the QuantFormat enum (include/welvet/weights.hpp:

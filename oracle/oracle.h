@@ -2,7 +2,7 @@
  * CPU oracle for the quantized-weight Dense path.
  *
  * TEST INFRASTRUCTURE ONLY. This is a plain-C restatement of the reference
- * numerical contract (openfluke/welvet.cuda 0.79). It is the checker: only the
+ * numerical contract (openfluke/welvet.cuda 0.79). It is test infrastructure: only the
  * tests, the smoke check and the CPU-baseline leg of the benchmark load it.
  * The product library (welvet.cuda_amd) never links or calls it.
  *

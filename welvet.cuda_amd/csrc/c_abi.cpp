@@ -47,7 +47,7 @@ welvet_status guarded(F&& fn) {
 
 welvet_status gap(const char* what) {
   return to_c(Status::err(wv::kGap, std::string("gap? ") + what +
-                                        " is outside the quantized Dense path of this build"));
+                                        " is outside the quantized Dense path of this library"));
 }
 
 hipStream_t pick(void* stream, hipStream_t own) {
@@ -86,7 +86,7 @@ welvet_status welvet_cuda_init(void) { return to_c(wv::init_device()); }
 
 int32_t welvet_cuda_available(void) { return wv::device_available() ? 1 : 0; }
 
-// Ledger of this build: reference C entry points served on the GPU vs those
+// Ledger of this library: reference C entry points served on the GPU vs those
 // returning code 3.
 int32_t welvet_gaps_count(void) { return 41; }
 int32_t welvet_gaps_done(void) { return 18; }

@@ -80,7 +80,7 @@ bool served(DType dt) {
 Status unserved(const char* who, DType dt) {
   return Status::Err(StatusCode::Unsupported,
                      std::string(who) + ": dtype " + std::string(dtype_name(dt)) +
-                         " is outside the FP8/FP4 path of this build (fp8e4m3, fp8e5m2, fp4)");
+                         " is outside the FP8/FP4 path of this library (fp8e4m3, fp8e5m2, fp4)");
 }
 
 int64_t elems(const WeightStore& s) { return static_cast<int64_t>(s.rows) * s.cols; }

@@ -237,7 +237,7 @@ void collect(ModelNode& c, std::vector<WeightStore*>* out) {
 // Store payload (model_session.cpp:135-162): i32 dtype, rows, cols, f32
 // scale, vec<f32> f32, vec<u8> native, vec<f64> bias. The reference's FP8 /
 // FP4 stores are FormatNone: f32 empty, scale unused (native_codec.cpp:176,
-// 534-549). Scaled stores of this build are an additive extension keyed in
+// 534-549). Scaled stores of this library are an additive extension keyed in
 // the dtype word: bits 0-7 the DType id, bits 8-15 the scale scheme (0 is
 // the reference format, and the only one a reference reader accepts):
 //   1  per tensor: `scale` holds s (finite, > 0), f32 empty;
@@ -667,7 +667,7 @@ Status model_forward_view(Model& m, const std::vector<int>& in_shape, const floa
 namespace {
 
 // The ops of a Stack model for the segment training calls: Dense and SwiGLU
-// (the MHA backward is not part of this build).
+// (the MHA backward is not part of this library).
 std::vector<ModelNode*> train_ops(Model& m) {
   require(m.root == 0, "segment backward expects Stack or Parallel");
   std::vector<ModelNode*> ops;
@@ -675,7 +675,7 @@ std::vector<ModelNode*> train_ops(Model& m) {
   for (ModelNode* op : ops)
     if (op->kind != 1 && op->kind != 4)
       throw StatusError(Status::err(kGap, "gap? segment backward of MHA children is outside the "
-                                          "quantized Dense path of this build"));
+                                          "quantized Dense path of this library"));
   return ops;
 }
 
@@ -774,7 +774,7 @@ Status model_forward_pair(Model& m, const std::vector<int>& in_shape, const floa
     for (size_t i = 0; i < ops.size(); ++i) {
       if (i + 1 == ops.size() && ops[i]->kind != 1)
         throw StatusError(Status::err(kGap, "gap? segment forward ending in a SwiGLU / MHA child "
-                                            "is outside the quantized Dense path of this build"));
+                                            "is outside the quantized Dense path of this library"));
       cur = op_forward(*ops[i], cur, ar, &m.scratch.ws, st, i + 1 == ops.size() ? &last_pre : nullptr);
     }
     good(hip_status(hipStreamSynchronize(st), "segment forward"));
