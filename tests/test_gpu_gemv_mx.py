@@ -258,3 +258,30 @@ def test_swiglu_rows_nonfinite_x(gpu, oracle):
     for b in range(rows):
         assert_ieee_match(h[b], oh[b], TOL_MFMA)
         assert_ieee_match(y[b], oy_own[b], TOL_MFMA)
+
+
+def _sweep_cases():
+    """Seeded shapes across the launch shapes' boundaries (16/32/33/64/65/96/97/128
+    chunks of 128), every dtype and scale scheme, 1-4 batch rows."""
+    rng = np.random.default_rng(20261202)
+    cases = []
+    chunks = [16, 32, 33, 64, 65, 96, 97, 128]
+    for i, s in enumerate(chunks):
+        dt = [4, 5, 16][i % 3]
+        scheme = int(rng.integers(0, 4))
+        cols = 128 * (s - 1) + 4 * int(rng.integers(1, 32))  # s chunks, the last ragged
+        rows = int(rng.integers(4081, 4700))
+        batch = 1 + i % 4
+        cases.append((dt, scheme, rows, cols, batch))
+    return cases
+
+
+@pytest.mark.parametrize("dt,scheme,rows,cols,batch", _sweep_cases())
+def test_dense_rows_shape_sweep(gpu, oracle, dt, scheme, rows, cols, batch):
+    rng = np.random.default_rng(rows * 7 + cols)
+    W = (rng.standard_normal((rows, cols)) / np.sqrt(cols)).astype(np.float32)
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    pre, _ = run_dense(gpu, dt, scheme, W, x)
+    o_pre, _ = oracle.dense(dequant(oracle, dt, scheme, W), x, threads=8)
+    for b in range(batch):
+        assert rel_l2(pre[b], o_pre[b]) <= TOL_MFMA, (b, rel_l2(pre[b], o_pre[b]))
