@@ -25,6 +25,7 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef short v2s __attribute__((ext_vector_type(2)));
 // fp32 input rows in the global address space (global, not flat, loads)
 typedef const __attribute__((address_space(1))) float* GlobalF;
 typedef __attribute__((address_space(1))) uint8_t* GlobalU8;
@@ -70,18 +71,21 @@ __device__ __forceinline__ void split_terms(float (&v)[2][16],
       for (int j = 0; j < 16; ++j) am = fmaxf(am, fabsf(v[h][j]));
       am = fmaxf(am, __shfl_xor(am, 16, 64));
       e[h] = e8m0_exponent(am, 448.0f);
-      const float inv = pow2f(-e[h]), sc = pow2f(e[h]);
+      // scaled converters: divide by and multiply with 2^e exactly
+      const float sc = pow2f(e[h]);
       int wq[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        int w4 = __builtin_amdgcn_cvt_pk_fp8_f32(v[h][4 * q] * inv, v[h][4 * q + 1] * inv, 0, false);
-        w4 = __builtin_amdgcn_cvt_pk_fp8_f32(v[h][4 * q + 2] * inv, v[h][4 * q + 3] * inv, w4, true);
+        v2s w = {0, 0};
+        w = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(w, v[h][4 * q], v[h][4 * q + 1], sc, false);
+        w = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(w, v[h][4 * q + 2], v[h][4 * q + 3], sc, true);
+        const int w4 = __builtin_bit_cast(int, w);
         wq[q] = w4;
         if (t + 1 < NT) {
-          const v2f q0 = __builtin_amdgcn_cvt_pk_f32_fp8(w4, false);
-          const v2f q1 = __builtin_amdgcn_cvt_pk_f32_fp8(w4, true);
-          v[h][4 * q] -= q0.x * sc, v[h][4 * q + 1] -= q0.y * sc;
-          v[h][4 * q + 2] -= q1.x * sc, v[h][4 * q + 3] -= q1.y * sc;
+          const v2f q0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w4, sc, false);
+          const v2f q1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w4, sc, true);
+          v[h][4 * q] -= q0.x, v[h][4 * q + 1] -= q0.y;
+          v[h][4 * q + 2] -= q1.x, v[h][4 * q + 3] -= q1.y;
         }
       }
       const i32x4 codes = i32x4{wq[0], wq[1], wq[2], wq[3]};
@@ -106,8 +110,8 @@ __device__ __forceinline__ void split_terms(float (&v)[2][16],
 // (element 2i from the first, 2i + 1 from the second). So the block's amax is
 // the lane's own. Per term: e, the smallest exponent with amax <= 7.5 * 2^e
 // (at least -126, so that 2^-e and 2^e are normal floats); the E2M3 codes of
-// v * 2^-e, rounded to nearest-even by the converter (scale 1); the residual
-// v - dec(code) * 2^e for the next term. The lane stores dwords 0-3 of its
+// v * 2^-e, rounded to nearest-even by the converter (scale 2^e); the
+// residual v - dec(code) * 2^e for the next term. The lane stores dwords 0-3 of its
 // operand at chunk + t * kFrag6Bytes + 16 l, dwords 4-5 at chunk + t *
 // kFrag6Bytes + 1024 + 8 l (both planes fully coalesced), and its exponents
 // as one dword at scales + 4 l (byte t: term t).
@@ -127,15 +131,17 @@ __device__ __forceinline__ void split_terms6(float (&v)[32],
     for (int j = 0; j < 32; ++j) am = fmaxf(am, fabsf(v[j]));
     int e = e8m0_exponent(am, 7.5f);
     e = e < -126 ? -126 : e;
-    const float inv = pow2f(-e), sc = pow2f(e);
+    // the converters divide by and multiply with the power of two exactly
+    // (the same bits as an explicit multiply by 2^-e and an unscaled convert)
+    const float sc = pow2f(e);
     v16f lo, hi;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) lo[i] = v[2 * i] * inv, hi[i] = v[2 * i + 1] * inv;
-    const auto code = __builtin_amdgcn_cvt_scalef32_2xpk16_fp6_f32(lo, hi, 1.0f);
+    for (int i = 0; i < 16; ++i) lo[i] = v[2 * i], hi[i] = v[2 * i + 1];
+    const auto code = __builtin_amdgcn_cvt_scalef32_2xpk16_fp6_f32(lo, hi, sc);
     if (t + 1 < NT) {
-      const auto d = __builtin_amdgcn_cvt_scalef32_pk32_f32_fp6(code, 1.0f);
+      const auto d = __builtin_amdgcn_cvt_scalef32_pk32_f32_fp6(code, sc);
 #pragma unroll
-      for (int j = 0; j < 32; ++j) v[j] = fmaf(-d[j], sc, v[j]);
+      for (int j = 0; j < 32; ++j) v[j] -= d[j];
     }
     const i32x4 c0 = i32x4{(int)code[0], (int)code[1], (int)code[2], (int)code[3]};
     const i32x2 c1 = i32x2{(int)code[4], (int)code[5]};
