@@ -109,7 +109,7 @@ __device__ __forceinline__ void split_terms(float (&v)[2][16],
 // lane's six dwords; the converter packs its two 16-value inputs interleaved
 // (element 2i from the first, 2i + 1 from the second). So the block's amax is
 // the lane's own. Per term: e, the smallest exponent with amax <= 7.5 * 2^e
-// (at least -126, so that 2^-e and 2^e are normal floats); the E2M3 codes of
+// (at least -126, so that 2^e is a normal float); the E2M3 codes of
 // v * 2^-e, rounded to nearest-even by the converter (scale 2^e); the
 // residual v - dec(code) * 2^e for the next term. The lane stores dwords 0-3 of its
 // operand at chunk + t * kFrag6Bytes + 16 l, dwords 4-5 at chunk + t *
