@@ -165,7 +165,7 @@ __device__ float exact_slice(const uint8_t* w, const float* x, int k0, int g, in
 // PRE: the input is a pre-split image per batch row (a.asplit); otherwise the
 // waves split a.x themselves. NEXT (MATS == 2): write the split of h to
 // a.next.
-template <int DT, bool BLK, int MATS, int NB, int W, int NSW, bool PRE, bool NEXT>
+template <int DT, bool BLK, int MATS, int NB, int W, int NSW, bool PRE, bool NEXT, bool ALIGNED = false>
 __global__ __launch_bounds__(64 * W) void k_gemv_mx(GemvMxArgs a) {
   constexpr bool FP4 = DT == kFP4;
   constexpr int NMF = (6 * NB + 15) / 16;  // MFMAs per weight fragment
@@ -250,7 +250,8 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mx(GemvMxArgs a) {
   constexpr int H = FP4 ? 1 : 2;
   // exponent dwords (groups of 4 chunks) that NSW consecutive chunks from
   // any start touch: (s0 + NSW - 1) / 4 - s0 / 4 <= (NSW + 2) / 4
-  constexpr int EG = (NSW + 2) / 4 + 1;
+  // (ALIGNED: every range is NSW chunks from a multiple of 4, NSW / 4 groups)
+  constexpr int EG = ALIGNED ? NSW / 4 : (NSW + 2) / 4 + 1;
   u32x4 wl[MATS][NSW], wh[MATS][FP4 ? 1 : NSW];
   uint32_t we[MATS][BLK ? EG : 1];
 #pragma unroll
@@ -595,18 +596,21 @@ constexpr int max_chunks(int dtype, int mats, int nb) {
   return dtype == kFP4 ? (mats == 1 ? (nb <= 3 ? 128 : 96) : 64) : (mats == 1 ? 64 : 32);
 }
 
-template <int DT, bool BLK, int MATS, int NB, int W, int NSW, bool PRE, bool NEXT>
+template <int DT, bool BLK, int MATS, int NB, int W, int NSW, bool PRE, bool NEXT, bool ALIGNED = false>
 Status launch_t(const GemvMxArgs& a, hipStream_t st) {
   static_assert(W * NSW * NB * (kChunkCodeBytes + kChunkExpBytes) + (NB == 1 ? W * MATS * 128 : 0) <= 160 * 1024,
                 "LDS of one workgroup");
   const unsigned grid = (unsigned)((a.rows + 15) / 16);
-  k_gemv_mx<DT, BLK, MATS, NB, W, NSW, PRE, NEXT><<<grid, 64 * W, 0, st>>>(a);
+  k_gemv_mx<DT, BLK, MATS, NB, W, NSW, PRE, NEXT, ALIGNED><<<grid, 64 * W, 0, st>>>(a);
   return hip_status(hipGetLastError(), "gemv_mx launch");
 }
 
 template <int DT, bool BLK, int MATS, int NB, bool PRE, bool NEXT>
 Status launch_shape(const GemvMxArgs& a, hipStream_t st) {
   const int S = a.kpad / 128;
+  // 32 chunks over 8 waves: each range is one exponent group
+  if constexpr (BLK)
+    if (S == 32) return launch_t<DT, BLK, MATS, NB, 8, 4, PRE, NEXT, true>(a, st);
   if (S <= 32) return launch_t<DT, BLK, MATS, NB, 8, 4, PRE, NEXT>(a, st);
   if constexpr (DT == kFP4 || MATS == 1)
     if (S <= 64) return launch_t<DT, BLK, MATS, NB, 16, 4, PRE, NEXT>(a, st);
