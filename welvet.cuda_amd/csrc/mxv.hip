@@ -128,21 +128,24 @@ __global__ __launch_bounds__(64 * kW) void k_mxv(MxvArgs a) {
         for (int i = 0; i < 8; ++i) am = fmaxf(am, fabsf(r[i]));
         am = quad_max(am);
         const int e = e8m0_exponent(am, 448.0f);
-        const float inv = pow2f(-e), sc = pow2f(e);
-        int w0 = __builtin_amdgcn_cvt_pk_fp8_f32(r[0] * inv, r[1] * inv, 0, false);
-        w0 = __builtin_amdgcn_cvt_pk_fp8_f32(r[2] * inv, r[3] * inv, w0, true);
-        int w1 = __builtin_amdgcn_cvt_pk_fp8_f32(r[4] * inv, r[5] * inv, 0, false);
-        w1 = __builtin_amdgcn_cvt_pk_fp8_f32(r[6] * inv, r[7] * inv, w1, true);
+        // scaled converters: divide by and multiply with 2^e exactly
+        const float sc = pow2f(e);
+        v2s p0 = {0, 0}, p1 = {0, 0};
+        p0 = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(p0, r[0], r[1], sc, false);
+        p0 = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(p0, r[2], r[3], sc, true);
+        p1 = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(p1, r[4], r[5], sc, false);
+        p1 = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(p1, r[6], r[7], sc, true);
+        const int w0 = __builtin_bit_cast(int, p0), w1 = __builtin_bit_cast(int, p1);
         const int row = b * kT + t;
         *reinterpret_cast<int2*>(la + row * (kSB * 128) + kl) = make_int2(w0, w1);
         if ((lane & 3) == 0) ls[row * (kSB * 4) + kl / 32] = (uint8_t)(e + 127);
         if (t + 1 < kT) {
-          const v2f q0 = __builtin_amdgcn_cvt_pk_f32_fp8(w0, false);
-          const v2f q1 = __builtin_amdgcn_cvt_pk_f32_fp8(w0, true);
-          const v2f q2 = __builtin_amdgcn_cvt_pk_f32_fp8(w1, false);
-          const v2f q3 = __builtin_amdgcn_cvt_pk_f32_fp8(w1, true);
-          r[0] -= q0.x * sc, r[1] -= q0.y * sc, r[2] -= q1.x * sc, r[3] -= q1.y * sc;
-          r[4] -= q2.x * sc, r[5] -= q2.y * sc, r[6] -= q3.x * sc, r[7] -= q3.y * sc;
+          const v2f q0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w0, sc, false);
+          const v2f q1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w0, sc, true);
+          const v2f q2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w1, sc, false);
+          const v2f q3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w1, sc, true);
+          r[0] -= q0.x, r[1] -= q0.y, r[2] -= q1.x, r[3] -= q1.y;
+          r[4] -= q2.x, r[5] -= q2.y, r[6] -= q3.x, r[7] -= q3.y;
         }
       }
     }
