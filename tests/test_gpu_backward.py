@@ -121,17 +121,24 @@ def test_normalbp_rejects_bad_arguments(gpu):
     assert e.value.code == 2
 
 
-@pytest.mark.parametrize("dt,scheme,batch,act,use_target", [(4, 2, 1, -1, True), (16, 3, 6, 1, False),
-                                                            (5, 0, 40, 5, True)])
-def test_backward_device_matches_normalbp(gpu, dt, scheme, batch, act, use_target):
+@pytest.mark.parametrize("dt,scheme,batch,act,use_target,nonfinite", [
+    (4, 2, 1, -1, True, False), (16, 3, 6, 1, False, False), (5, 0, 40, 5, True, False),
+    (4, 2, 5, -1, False, False),   # Linear, no target: d_pre = gy from the products' launch
+    (16, 3, 1, -1, False, True),   # the same with inf and NaN in gy
+])
+def test_backward_device_matches_normalbp(gpu, oracle, dt, scheme, batch, act, use_target,
+                                          nonfinite):
     """welvet_dense_backward_device on a mounted session (device buffers, the
     session stream) gives the bits of welvet_dense_normalbp_f32, twice in a
-    row over the same buffers (the second call reuses the dX partials)."""
+    row over the same buffers (the second call reuses the dX partials), and
+    its d_pre output is the oracle's (kernels.cu:83-90)."""
     rng = np.random.default_rng(batch + dt)
     inn, out = 700, 300
     W = (rng.standard_normal((out, inn)) / np.sqrt(inn)).astype(np.float32)
     x = rng.standard_normal((batch, inn)).astype(np.float32)
     g = rng.standard_normal((batch, out)).astype(np.float32)
+    if nonfinite:
+        g[0, 3], g[0, 77], g[-1, -1] = np.inf, -np.inf, np.nan
     pre, post, dx, dw, _, loss = gpu.dense_normalbp(batch, inn, out, act, dt, scheme, W, x, g,
                                                     use_target)
     hip = gpu.Hip()
@@ -150,8 +157,15 @@ def test_backward_device_matches_normalbp(gpu, dt, scheme, batch, act, use_targe
                           bufs["dx"], bufs["dw"], lp)
         hip.sync()
         assert np.array_equal(hip.download(bufs["pre"], (batch, out)), pre)
-        assert np.array_equal(hip.download(bufs["dx"], (batch, inn)), dx)
-        assert np.array_equal(hip.download(bufs["dw"], (out, inn)), dw)
+        assert np.array_equal(hip.download(bufs["dx"], (batch, inn)), dx, equal_nan=True)
+        assert np.array_equal(hip.download(bufs["dw"], (out, inn)), dw, equal_nan=True)
+        gy = oracle.mse_grad(post, g) if use_target else g
+        dpre_o = oracle.backward(W, gy, pre, x, act)[0]  # d_pre does not depend on W
+        d = hip.download(bufs["d"], (batch, out))
+        if act in EXACT_ACTS:
+            assert np.array_equal(d, dpre_o, equal_nan=True)
+        else:
+            assert rel_l2(d, dpre_o) <= 1e-6
         if use_target:
             total = 0.0
             for v in hip.download(lp, (nparts,), np.float64):  # in order, as the library adds them

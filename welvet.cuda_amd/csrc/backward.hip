@@ -5,7 +5,9 @@
 //   k_dpre     d_pre = f32(f64(gy) * act'(f64 pre)) (src/cuda/kernels.cu:48-90).
 //              With a target, gy = f32(2/n * (f64 post - f64 target)) and the
 //              squared differences are summed per block for the MSE loss
-//              (src/runtime/training.cpp:44-69).
+//              (src/runtime/training.cpp:44-69). Not launched for a Linear
+//              layer without a target: there d_pre is gy, which k_bwd reads
+//              directly and stores as d_pre.
 //   k_bwd      both products, which read only d_pre, in one launch:
 //              * dX = W^T d_pre (kernels.cu:92-107) from the code rows the
 //                forward streams: a workgroup owns 1024 columns and a band of
@@ -147,6 +149,7 @@ __device__ __forceinline__ void decode16(const typename RowCodes<DT>::T q, float
 struct OuterArgs {
   const float* x = nullptr;  // [batch][in]
   float* dw = nullptr;       // [out][in]
+  float* dpre_out = nullptr;  // [batch][out]: d_pre written here when the products read gy
   int batch = 0, cb = 0, vec = 0;
 };
 
@@ -228,6 +231,13 @@ __device__ __forceinline__ void gemvt_tile(const GemvtArgs& a, int blk, int tile
 __device__ __forceinline__ void outer_rows(const float* __restrict__ dpre, const OuterArgs& oa,
                                            int g, int in, int out) {
   const int r0 = (g / oa.cb) * kOuterRows;
+  // Linear without a target: d_pre = f32(f64(gy) * 1), which is gy (a NaN
+  // stays a NaN), is not formed by a launch of its own; the first column
+  // block of each row group stores it.
+  if (oa.dpre_out && g % oa.cb == 0 && (int)threadIdx.x < kOuterRows && r0 + (int)threadIdx.x < out) {
+    const size_t r = (size_t)r0 + threadIdx.x;
+    for (int b = 0; b < oa.batch; ++b) oa.dpre_out[(size_t)b * out + r] = dpre[(size_t)b * out + r];
+  }
   const int c = ((g % oa.cb) * kThreads + (int)threadIdx.x) * 4;
   if (c >= in) return;
   const ConstF32 dp = (ConstF32)dpre;
@@ -427,7 +437,7 @@ size_t gemvt_part_bytes(int in, int out) {
 
 Status launch_backward_products(const GemvtArgs& a, int dtype, bool blk, int batch,
                                 const float* x, float* dw, double* part, float* dx,
-                                hipStream_t st) {
+                                float* dpre_out, hipStream_t st) {
   if (batch <= 0 || a.in <= 0 || a.out <= 0 || !a.codes || !a.scale || !a.dpre || !part || !dx ||
       !x || !dw || (blk && !a.blk) || a.in > a.kpad)
     return Status::err(kInvalid, "backward: bad args");
@@ -437,6 +447,7 @@ Status launch_backward_products(const GemvtArgs& a, int dtype, bool blk, int bat
   OuterArgs oa;
   oa.x = x;
   oa.dw = dw;
+  oa.dpre_out = dpre_out;
   oa.batch = batch;
   oa.cb = (a.in + 4 * kThreads - 1) / (4 * kThreads);
   oa.vec = a.in % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0 &&

@@ -305,9 +305,11 @@ struct GemvtArgs {
 size_t gemvt_part_bytes(int in, int out);
 // dX [batch][in] = W^T d_pre (f64 accumulation, rounded once to f32) and dW
 // [out][in] (the reference's per-batch-row f32 accumulation) from d_pre.
+// With dpre_out set, a.dpre is gy of a Linear layer without a target (d_pre
+// equals it) and the launch also stores it to dpre_out [batch][out].
 Status launch_backward_products(const GemvtArgs& a, int dtype, bool blk, int batch,
                                 const float* x, float* dw, double* part, float* dx,
-                                hipStream_t st);
+                                float* dpre_out, hipStream_t st);
 // SwiGLU backward product (d_up, d_gate from gate_pre, up_post, grad_h) and
 // the f64 sum of two gradients, rounded to f32.
 Status launch_swiglu_bwd(const float* gate_pre, const float* up_post, const float* grad_h,

@@ -476,8 +476,11 @@ Status dense_backward(const DenseLayer& L, int batch, const float* x, const floa
     return Status::err(kInvalid, "dense backward: bad args");
   if (L.format) return Status::err(kGap, "gap? dense backward over packed block formats");
   const int64_t n = (int64_t)batch * L.out;
-  WV_TRY(launch_dpre(g, post, pre, linear_act ? kLinear : L.act, use_target ? 1 : 0, n, dpre,
-                     loss_part, st));
+  // Linear without a target: d_pre = gy, stored by the products' launch
+  const bool direct = !use_target && (linear_act || L.act == kLinear);
+  if (!direct)
+    WV_TRY(launch_dpre(g, post, pre, linear_act ? kLinear : L.act, use_target ? 1 : 0, n, dpre,
+                       loss_part, st));
   const size_t pb = gemvt_part_bytes(L.in, L.out);
   if (ws->d.bytes < pb) WV_TRY(ws->d.alloc(pb));
   GemvtArgs a;
@@ -489,9 +492,11 @@ Status dense_backward(const DenseLayer& L, int batch, const float* x, const floa
   a.kpad = L.dev.kpad;
   a.in = L.in;
   a.out = L.out;
-  a.dpre = dpre;
+  a.dpre = direct ? g : dpre;
+  // (d_pre in gy's own buffer already holds it)
+  float* dpre_out = direct && dpre != g ? dpre : nullptr;
   return launch_backward_products(a, L.dev.dtype, L.dev.scheme == kSchemeBlock32, batch, x, dw,
-                                  ws->d.as<double>(), dx, st);
+                                  ws->d.as<double>(), dx, dpre_out, st);
 }
 
 template <class G>
