@@ -601,6 +601,34 @@ def make_workload(pw, hip, config, copies, terms=3, batch=1, keep_inner=False):
     raise SystemExit(f"unknown config {config}")
 
 
+def lib_layout(pw, hip):
+    """Prints the executable mappings of this process and the addresses of a
+    few runtime entry points after one small Dense mount and execute, so that
+    the frames of a native backtrace taken under a profiler can be assigned to
+    libraries (libraries loaded at start keep their relative offsets from run
+    to run)."""
+    import numpy as np
+
+    W = pw.normal(1, 256 * 256, 0.05).reshape(256, 256)
+    s = pw.DenseSession(1, 256, 256, -1, 4, 2, W)
+    s.execute(np.ones((1, 256), np.float32))
+
+    def addr(lib, name):
+        return hex(ctypes.cast(getattr(lib, name), ctypes.c_void_p).value)
+
+    libc = ctypes.CDLL("libc.so.6")
+    hl = ctypes.CDLL("libamdhip64.so.7")
+    print("libc memcpy", addr(libc, "memcpy"), "sigaction", addr(libc, "sigaction"))
+    print("hipMemcpyAsync", addr(hl, "hipMemcpyAsync"), "hipLaunchKernel", addr(hl, "hipLaunchKernel"))
+    print("welvet_dense_mount_q", addr(pw.lib(), "welvet_dense_mount_q"))
+    with open("/proc/self/maps") as f:
+        for line in f:
+            parts = line.split()
+            if len(parts) >= 6 and ".so" in parts[5] and "x" in parts[1]:
+                print(parts[0], parts[1], os.path.basename(parts[5]))
+    s.close()
+
+
 def copy_calibration(pw, nbytes, steps):
     """Times `steps` device-to-device copies of nbytes (read nbytes, write nbytes)."""
     pw.check(pw.lib().welvet_cuda_init())
@@ -925,6 +953,8 @@ def main():
                          "instead of a workload")
     ap.add_argument("--no-gemm", action="store_true",
                     help="c2: leave out the GEMM workloads (c4, c5) that the default line also times")
+    ap.add_argument("--lib-layout", action="store_true",
+                    help="only print the process's library mappings after a small mount")
     ap.add_argument("--probe", choices=("mfma", "fetch"), default=None,
                     help="only run a hardware probe: the scaled MFMA issue rate or the per-CU "
                          "fetch rate from L2 and HBM")
@@ -944,6 +974,9 @@ def main():
     hip = pw.Hip()
     if args.probe:
         (probe_mfma if args.probe == "mfma" else probe_fetch)(pw, hip)
+        return
+    if args.lib_layout:
+        lib_layout(pw, hip)
         return
     if args.read_floor:
         wl = read_floor_workload(pw, hip, args.read_floor, max(1, args.copies))
